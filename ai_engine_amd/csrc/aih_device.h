@@ -1,0 +1,127 @@
+// aih_device.h -- device-side helpers shared by the gfx950 conv kernels:
+// storage dtypes (f32 / f16 / bf16 with fp32 accumulation), 16-byte vector
+// types, the fused epilogue activation, and an XCD-aware workgroup remap.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/aih_conv.h"
+
+namespace aih {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Storage dtype tags (same values as enum aih_dtype).
+enum : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+
+template <int DT> struct Storage;
+template <> struct Storage<DT_F32> { using T = float; static constexpr int bytes = 4; };
+template <> struct Storage<DT_F16> { using T = uint16_t; static constexpr int bytes = 2; };
+template <> struct Storage<DT_BF16> { using T = uint16_t; static constexpr int bytes = 2; };
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// f32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+  _Float16 h;
+  uint16_t b = (uint16_t)bits16;
+  __builtin_memcpy(&h, &b, 2);
+  return (float)h;
+}
+
+// f32 -> f16 via the hardware conversion (round to nearest even).
+__device__ __forceinline__ uint32_t f32_to_f16(float f) {
+  _Float16 h = (_Float16)f;
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+// 4 consecutive channels (one vec4 of NHWC-C4) <-> fp32.
+template <int DT> struct Vec4IO;
+
+template <> struct Vec4IO<DT_F32> {
+  static __device__ __forceinline__ f32x4 load(const void *base, size_t vec_idx) {
+    return reinterpret_cast<const f32x4 *>(base)[vec_idx];
+  }
+  static __device__ __forceinline__ void store(void *base, size_t vec_idx, f32x4 v) {
+    reinterpret_cast<f32x4 *>(base)[vec_idx] = v;
+  }
+};
+
+template <> struct Vec4IO<DT_F16> {
+  static __device__ __forceinline__ f32x4 load(const void *base, size_t vec_idx) {
+    u32x2 r = reinterpret_cast<const u32x2 *>(base)[vec_idx];
+    return f32x4{f16_to_f32(r.x & 0xffffu), f16_to_f32(r.x >> 16), f16_to_f32(r.y & 0xffffu),
+                 f16_to_f32(r.y >> 16)};
+  }
+  static __device__ __forceinline__ void store(void *base, size_t vec_idx, f32x4 v) {
+    u32x2 r;
+    r.x = f32_to_f16(v.x) | (f32_to_f16(v.y) << 16);
+    r.y = f32_to_f16(v.z) | (f32_to_f16(v.w) << 16);
+    reinterpret_cast<u32x2 *>(base)[vec_idx] = r;
+  }
+};
+
+template <> struct Vec4IO<DT_BF16> {
+  static __device__ __forceinline__ f32x4 load(const void *base, size_t vec_idx) {
+    u32x2 r = reinterpret_cast<const u32x2 *>(base)[vec_idx];
+    return f32x4{bf16_to_f32(r.x & 0xffffu), bf16_to_f32(r.x >> 16), bf16_to_f32(r.y & 0xffffu),
+                 bf16_to_f32(r.y >> 16)};
+  }
+  static __device__ __forceinline__ void store(void *base, size_t vec_idx, f32x4 v) {
+    u32x2 r;
+    r.x = f32_to_bf16(v.x) | (f32_to_bf16(v.y) << 16);
+    r.y = f32_to_bf16(v.z) | (f32_to_bf16(v.w) << 16);
+    reinterpret_cast<u32x2 *>(base)[vec_idx] = r;
+  }
+};
+
+// Epilogue activation (ai-core Activation::apply, crates/ai-core/src/activation.rs:28-43).
+// `act` is uniform across the grid, so the switch does not diverge.
+__device__ __forceinline__ float act_apply(int act, float x) {
+  switch (act) {
+    case AIH_ACT_NONE: return x;
+    case AIH_ACT_RELU: return fmaxf(x, 0.0f);
+    case AIH_ACT_SIGMOID: return 1.0f / (1.0f + expf(-x));
+    case AIH_ACT_TANH: return tanhf(x);
+    case AIH_ACT_HARDSWISH: return x * fminf(fmaxf(x / 6.0f + 0.5f, 0.0f), 1.0f);
+    case AIH_ACT_HARDSIGMOID: return fminf(fmaxf(x / 6.0f + 0.5f, 0.0f), 1.0f);
+    case AIH_ACT_CLAMP01: return fminf(fmaxf(x, 0.0f), 1.0f);
+    case AIH_ACT_RELU6: return fminf(fmaxf(x, 0.0f), 6.0f);
+    case AIH_ACT_SQRT: return sqrtf(fmaxf(x, 0.0f));
+    case AIH_ACT_NEG: return -x;
+    case AIH_ACT_RECIP: return 1.0f / x;
+    default: return x;
+  }
+}
+
+__device__ __forceinline__ f32x4 act_apply4(int act, f32x4 v) {
+  return f32x4{act_apply(act, v.x), act_apply(act, v.y), act_apply(act, v.z), act_apply(act, v.w)};
+}
+
+// MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs,
+// each with a private L2. Remap so that every XCD walks a contiguous range of
+// logical tiles: neighbouring tiles (which share input rows / halos) then hit
+// the same L2. Bijective on [0, n).
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n) {
+  constexpr uint32_t XCD = 8;
+  uint32_t per = n / XCD;
+  if (bid >= per * XCD) return bid;
+  return (bid % XCD) * per + bid / XCD;
+}
+
+}  // namespace aih

@@ -1,0 +1,563 @@
+// capi.hip -- the extern "C" boundary of include/aih_conv.h.
+//
+// Every export validates its descriptor, never throws across the boundary
+// (the reference's FFI returns VbResult 0 / -1 behind catch_unwind,
+// crates/ai-ffi/src/lib.rs:45-52,130-133), and records a per-thread message
+// for aih_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <string>
+
+#include "../../include/aih_conv.h"
+#include "conv_dw.h"
+#include "conv_gemm_launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const std::string &msg) {
+  g_err = msg;
+  return AIH_ERR;
+}
+
+template <class F>
+int guarded(F &&f) {
+  try {
+    return f();
+  } catch (const std::exception &e) {
+    return fail(std::string("exception: ") + e.what());
+  } catch (...) {
+    return fail("unknown exception");
+  }
+}
+
+inline uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+bool dtype_ok(int32_t dt) { return dt == AIH_F32 || dt == AIH_F16 || dt == AIH_BF16; }
+
+// Activation storage dt with weight storage wdt: fp32 activations take any
+// weight dtype (converted to fp32 in LDS, fp32 MFMA); 16-bit activations need
+// weights of the same dtype (f16 / bf16 MFMA).
+bool dtype_pair_ok(int32_t dt, int32_t wdt) {
+  if (!dtype_ok(dt) || !dtype_ok(wdt)) return false;
+  return dt == AIH_F32 || dt == wdt;
+}
+
+size_t dsize(int32_t dt) { return dt == AIH_F32 ? 4 : 2; }
+
+// ---------------------------------------------------------------- policy
+//
+// The reference's policy (gemm_pw.rs:91-102, conv_igemm.rs:201-233) splits K
+// when the tile grid cannot fill its 19-core GPU and K is long enough to be
+// worth cutting. Re-tuned for MI355X: 256 CUs, one 128-pixel MFMA tile per
+// workgroup; split when the tile grid covers fewer than 256 CUs and K spans at
+// least two stages, aiming at two workgroups per CU, at most 8 chunks, and at
+// least one full stage per chunk.
+constexpr uint32_t kCUs = 256;
+
+int stage_kg(int32_t dt, int bn) { return dt == AIH_F32 ? (bn > 160 ? 4 : 8) : 16; }
+
+int pick_bn(uint32_t n4) {
+  int best = 32;
+  uint64_t best_cols = ~0ull;
+  for (int bn : aih::kGemmBN) {
+    const uint64_t cols = (uint64_t)div_ceil(n4, bn) * bn;
+    if (cols < best_cols || (cols == best_cols && bn > best)) {
+      best = bn;
+      best_cols = cols;
+    }
+  }
+  return best;
+}
+
+struct GemmPlan {
+  int bn;
+  uint32_t mtiles, ntiles, nsplit, kk_chunk;
+  size_t ws;
+};
+
+int plan_gemm(uint32_t M, uint32_t N4, uint32_t KK, int32_t dt, int32_t variant, int32_t splitk,
+              GemmPlan *p) {
+  if (variant != AIH_VAR_AUTO && variant != AIH_VAR_TILE && variant != AIH_VAR_SPLITK)
+    return fail("variant must be AIH_VAR_AUTO, AIH_VAR_TILE or AIH_VAR_SPLITK");
+  if (splitk < 0 || splitk > 64) return fail("splitk must be in [0, 64]");
+  p->bn = pick_bn(N4);
+  p->mtiles = div_ceil(M, aih::GEMM_BM);
+  p->ntiles = div_ceil(N4, p->bn);
+  const uint32_t bkg = (uint32_t)stage_kg(dt, p->bn);
+  const uint32_t tiles = p->mtiles * p->ntiles;
+  uint32_t s = 1;
+  if (splitk > 0) {
+    s = (uint32_t)splitk;
+  } else if (variant == AIH_VAR_SPLITK) {
+    s = 4;
+  } else if (variant == AIH_VAR_AUTO && tiles < kCUs && KK >= 2 * bkg) {
+    s = (2 * kCUs) / tiles;
+    if (s > 8) s = 8;
+    const uint32_t max_s = KK / bkg;
+    if (s > max_s) s = max_s;
+    if (s < 1) s = 1;
+  }
+  if (variant == AIH_VAR_TILE && splitk > 1) return fail("AIH_VAR_TILE with splitk > 1");
+  uint32_t chunk = div_ceil(KK, s);
+  chunk = div_ceil(chunk, bkg) * bkg;
+  p->kk_chunk = chunk;
+  p->nsplit = div_ceil(KK, chunk);
+  p->ws = p->nsplit > 1 ? (size_t)p->nsplit * M * N4 * sizeof(float) : 0;
+  const uint64_t grid = (uint64_t)p->mtiles * p->ntiles * p->nsplit;
+  if (grid > 0x7fffffffull) return fail("grid too large");
+  return AIH_OK;
+}
+
+void fill_plan(const GemmPlan &g, aih_plan *out) {
+  out->variant = g.nsplit > 1 ? AIH_VAR_SPLITK : AIH_VAR_TILE;
+  out->splitk = g.nsplit;
+  out->bm = aih::GEMM_BM;
+  out->bn = (uint32_t)g.bn;
+  out->grid = g.mtiles * g.ntiles * g.nsplit;
+  out->ws_bytes = g.ws;
+}
+
+int run_gemm(aih::GemmArgs &a, const GemmPlan &g, int32_t dt, int32_t wdt, bool igemm, void *ws,
+             size_t ws_bytes, hipStream_t st) {
+  a.mtiles = g.mtiles;
+  a.ntiles = g.ntiles;
+  a.nsplit = g.nsplit;
+  a.kk_chunk = g.kk_chunk;
+  a.partial = nullptr;
+  if (g.nsplit > 1) {
+    if (ws == nullptr || ws_bytes < g.ws)
+      return fail("split-K needs a workspace of " + std::to_string(g.ws) + " bytes");
+    if (reinterpret_cast<uintptr_t>(ws) % 16) return fail("workspace must be 16-byte aligned");
+    a.partial = static_cast<float *>(ws);
+  }
+  hipError_t e = aih::launch_conv_gemm(a, dt, wdt, g.bn, igemm, st);
+  if (e != hipSuccess) return fail(std::string("conv_gemm launch: ") + hipGetErrorString(e));
+  if (g.nsplit > 1) {
+    e = aih::launch_splitk_reduce(a, dt, st);
+    if (e != hipSuccess) return fail(std::string("splitk_reduce launch: ") + hipGetErrorString(e));
+  }
+  return AIH_OK;
+}
+
+bool aligned(const void *p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+// ---------------------------------------------------------------- pw
+
+int check_pw(const aih_pw_desc *d) {
+  if (!d) return fail("null descriptor");
+  if (d->n == 0 || d->m == 0) return fail("pw: n and m must be > 0");
+  if (d->kg == 0 || d->ng == 0) return fail("pw: kg and ng must be > 0");
+  if (d->kg_pad < d->kg) return fail("pw: kg_pad < kg");
+  if (d->act < AIH_ACT_NONE || d->act > AIH_ACT_RECIP) return fail("pw: unknown activation");
+  if (!dtype_pair_ok(d->dt, d->wdt)) return fail("pw: unsupported (dt, wdt) pair");
+  if ((uint64_t)d->n * d->m > 0xffffffffull / 4) return fail("pw: too many pixels");
+  if ((uint64_t)d->n * d->m * d->kg > 0xffffffffull) return fail("pw: input too large");
+  return AIH_OK;
+}
+
+int plan_pw(const aih_pw_desc *d, GemmPlan *g) {
+  return plan_gemm(d->n * d->m, d->ng * 4, d->kg, d->dt, d->variant, d->splitk, g);
+}
+
+// ---------------------------------------------------------------- igemm
+
+int igemm_out_hw(const aih_igemm_desc *d, uint32_t *oh, uint32_t *ow) {
+  const uint32_t ek = d->d * (d->k - 1) + 1;
+  if (d->ih + d->pad[0] + d->pad[2] < ek || d->iw + d->pad[1] + d->pad[3] < ek)
+    return fail("igemm: kernel larger than the padded input");
+  *oh = (d->ih + d->pad[0] + d->pad[2] - ek) / d->s + 1;
+  *ow = (d->iw + d->pad[1] + d->pad[3] - ek) / d->s + 1;
+  return AIH_OK;
+}
+
+int check_igemm(const aih_igemm_desc *d) {
+  if (!d) return fail("null descriptor");
+  if (d->n == 0 || d->ih == 0 || d->iw == 0 || d->cin == 0 || d->cout == 0)
+    return fail("igemm: zero-sized dimension");
+  if (d->k == 0 || d->k > 15 || d->s == 0 || d->d == 0) return fail("igemm: k must be in [1, 15], s and d > 0");
+  if (d->act < AIH_ACT_NONE || d->act > AIH_ACT_RECIP) return fail("igemm: unknown activation");
+  if (!dtype_pair_ok(d->dt, d->wdt)) return fail("igemm: unsupported (dt, wdt) pair");
+  if (d->nsrcs > 3) return fail("igemm: at most 3 input parts (lowering.rs:177-179)");
+  if (d->nsrcs > 0) {
+    uint32_t csum = 0, kgsum = 0;
+    for (uint32_t i = 0; i < d->nsrcs; ++i) {
+      const aih_src &s = d->srcs[i];
+      if (s.c == 0) return fail("igemm: empty input part");
+      if (s.stride_c % 4 || s.c_off % 4) return fail("igemm: part stride_c / c_off must be multiples of 4");
+      if (i + 1 < d->nsrcs && s.c % 4) return fail("igemm: only the last part may have c % 4 != 0");
+      if (s.c_off + div_ceil(s.c, 4) * 4 > s.stride_c) return fail("igemm: part exceeds its pixel stride");
+      csum += s.c;
+      kgsum += div_ceil(s.c, 4);
+    }
+    if (csum != d->cin || kgsum != div_ceil(d->cin, 4)) return fail("igemm: parts do not add up to cin");
+  }
+  uint32_t oh, ow;
+  if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
+  if ((uint64_t)d->n * oh * ow > 0xffffffffull / 4) return fail("igemm: too many output pixels");
+  if ((uint64_t)d->n * d->ih * d->iw * 64 > 0xffffffffull) return fail("igemm: input too large");
+  return AIH_OK;
+}
+
+int plan_igemm(const aih_igemm_desc *d, GemmPlan *g) {
+  uint32_t oh, ow;
+  if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
+  return plan_gemm(d->n * oh * ow, div_ceil(d->cout, 4) * 4, d->k * d->k * div_ceil(d->cin, 4), d->dt,
+                   d->variant, d->splitk, g);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *aih_last_error(void) { return g_err.c_str(); }
+
+const char *aih_version(void) { return "aih_conv 0.1 gfx950"; }
+
+int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out) {
+  return guarded([&] {
+    if (check_pw(d)) return AIH_ERR;
+    if (!out) return fail("null plan");
+    GemmPlan g;
+    if (plan_pw(d, &g)) return AIH_ERR;
+    fill_plan(g, out);
+    return AIH_OK;
+  });
+}
+
+int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *bias, const void *res, void *y,
+                void *ws, size_t ws_bytes, aih_stream stream) {
+  return guarded([&] {
+    if (check_pw(d)) return AIH_ERR;
+    if (!x || !w || !bias || !y) return fail("pw: null buffer");
+    if ((d->residual != 0) != (res != nullptr)) return fail("pw: res must be given iff residual");
+    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 8) || !aligned(bias, 8) || (res && !aligned(res, 8)))
+      return fail("pw: misaligned buffer");
+    GemmPlan g;
+    if (plan_pw(d, &g)) return AIH_ERR;
+    aih::GemmArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.src[0] = x;
+    a.nparts = 1;
+    a.stride_kg[0] = d->kg;
+    a.w = w;
+    a.bias = bias;
+    a.res = res;
+    a.y = y;
+    a.M = d->n * d->m;
+    a.OHW = d->m;
+    a.OW = d->m;
+    a.IH = 1;
+    a.IW = d->m;
+    a.K = 1;
+    a.S = 1;
+    a.D = 1;
+    a.KG = d->kg;
+    a.KGP = d->kg_pad;
+    a.KK = d->kg;
+    a.N4 = d->ng * 4;
+    a.act = d->act;
+    a.has_res = d->residual ? 1 : 0;
+    return run_gemm(a, g, d->dt, d->wdt, false, ws, ws_bytes, static_cast<hipStream_t>(stream));
+  });
+}
+
+int aih_conv_igemm_plan(const aih_igemm_desc *d, aih_plan *out) {
+  return guarded([&] {
+    if (check_igemm(d)) return AIH_ERR;
+    if (!out) return fail("null plan");
+    GemmPlan g;
+    if (plan_igemm(d, &g)) return AIH_ERR;
+    fill_plan(g, out);
+    return AIH_OK;
+  });
+}
+
+int aih_conv_igemm(const aih_igemm_desc *d, const void *const *inputs, const void *w, const void *bias,
+                   const void *res, void *y, void *ws, size_t ws_bytes, aih_stream stream) {
+  return guarded([&] {
+    if (check_igemm(d)) return AIH_ERR;
+    if (!inputs || !w || !bias || !y) return fail("igemm: null buffer");
+    const uint32_t nin = d->nsrcs ? d->nsrcs : 1;
+    for (uint32_t i = 0; i < nin; ++i) {
+      if (!inputs[i]) return fail("igemm: null input part");
+      if (!aligned(inputs[i], 8)) return fail("igemm: misaligned input");
+    }
+    if ((d->residual != 0) != (res != nullptr)) return fail("igemm: res must be given iff residual");
+    if (!aligned(w, 16) || !aligned(y, 8) || !aligned(bias, 8) || (res && !aligned(res, 8)))
+      return fail("igemm: misaligned buffer");
+    uint32_t oh, ow;
+    if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
+    GemmPlan g;
+    if (plan_igemm(d, &g)) return AIH_ERR;
+    aih::GemmArgs a;
+    std::memset(&a, 0, sizeof(a));
+    const uint32_t kg = div_ceil(d->cin, 4);
+    if (d->nsrcs == 0) {
+      a.src[0] = inputs[0];
+      a.nparts = 1;
+      a.stride_kg[0] = kg;
+    } else {
+      uint32_t kg0 = 0;
+      for (uint32_t i = 0; i < d->nsrcs; ++i) {
+        a.src[i] = inputs[i];
+        a.part_kg[i] = kg0;
+        a.stride_kg[i] = d->srcs[i].stride_c / 4;
+        a.off_kg[i] = d->srcs[i].c_off / 4;
+        kg0 += div_ceil(d->srcs[i].c, 4);
+      }
+      a.nparts = d->nsrcs;
+    }
+    a.w = w;
+    a.bias = bias;
+    a.res = res;
+    a.y = y;
+    a.M = d->n * oh * ow;
+    a.OHW = oh * ow;
+    a.OW = ow;
+    a.IH = d->ih;
+    a.IW = d->iw;
+    a.K = d->k;
+    a.S = d->s;
+    a.D = d->d;
+    a.PT = (int32_t)d->pad[0];
+    a.PL = (int32_t)d->pad[1];
+    a.KG = kg;
+    a.KGP = div_ceil(kg, 4) * 4;
+    a.KK = d->k * d->k * kg;
+    a.N4 = div_ceil(d->cout, 4) * 4;
+    a.act = d->act;
+    a.has_res = d->residual ? 1 : 0;
+    return run_gemm(a, g, d->dt, d->wdt, true, ws, ws_bytes, static_cast<hipStream_t>(stream));
+  });
+}
+
+int aih_conv_dw(const aih_dw_desc *d, const void *x, const void *w, const void *bias, const void *res, void *y,
+                aih_stream stream) {
+  return guarded([&] {
+    if (!d) return fail("null descriptor");
+    if (d->n == 0 || d->ih == 0 || d->iw == 0 || d->c == 0) return fail("dw: zero-sized dimension");
+    if (d->k == 0 || d->s == 0 || d->d == 0) return fail("dw: k, s, d must be > 0");
+    if (d->act < AIH_ACT_NONE || d->act > AIH_ACT_RECIP) return fail("dw: unknown activation");
+    if (!dtype_ok(d->dt)) return fail("dw: unknown dtype");
+    if (!x || !w || !bias || !y) return fail("dw: null buffer");
+    if ((d->residual != 0) != (res != nullptr)) return fail("dw: res must be given iff residual");
+    if (!aligned(x, 8) || !aligned(w, 8) || !aligned(y, 8) || !aligned(bias, 8) || (res && !aligned(res, 8)))
+      return fail("dw: misaligned buffer");
+    const uint32_t ek = d->d * (d->k - 1) + 1;
+    if (d->ih + d->pad[0] + d->pad[2] < ek || d->iw + d->pad[1] + d->pad[3] < ek)
+      return fail("dw: kernel larger than the padded input");
+    aih::DwArgs a;
+    a.x = x;
+    a.w = w;
+    a.bias = bias;
+    a.res = res;
+    a.y = y;
+    a.N = d->n;
+    a.IH = d->ih;
+    a.IW = d->iw;
+    a.OH = (d->ih + d->pad[0] + d->pad[2] - ek) / d->s + 1;
+    a.OW = (d->iw + d->pad[1] + d->pad[3] - ek) / d->s + 1;
+    a.CG = div_ceil(d->c, 4);
+    a.K = d->k;
+    a.S = d->s;
+    a.D = d->d;
+    a.PT = (int32_t)d->pad[0];
+    a.PL = (int32_t)d->pad[1];
+    a.act = d->act;
+    a.has_res = d->residual ? 1 : 0;
+    if ((uint64_t)a.N * a.IH * a.IW * a.CG > 0xffffffffull || (uint64_t)a.N * a.OH * a.OW * a.CG > 0xffffffffull)
+      return fail("dw: tensor too large");
+    hipError_t e = aih::launch_conv_dw(a, d->dt, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(std::string("conv_dw launch: ") + hipGetErrorString(e));
+    return AIH_OK;
+  });
+}
+
+// lower_op's Conv arm (crates/ai-gpu-runtime/src/lowering.rs:122-168).
+static int conv_route(const aih_conv_desc *d, aih_pw_desc *pw, aih_igemm_desc *ig, aih_dw_desc *dw) {
+  if (!d) return fail("null descriptor");
+  if (d->groups == 0) return fail("conv: groups must be > 0");
+  if (d->groups > 1) {
+    if (d->groups != d->cin || d->cin != d->cout) return fail("conv: grouped conv other than depthwise");
+    if (d->kh != d->kw || d->sh != d->sw) return fail("conv: depthwise needs square k and isotropic stride");
+    *dw = aih_dw_desc{d->n, d->ih, d->iw, d->cin, d->kh, d->sh, d->d, {d->pad[0], d->pad[1], d->pad[2], d->pad[3]},
+                      d->act, d->residual, d->dt};
+    return 2;
+  }
+  if (d->kh == 1 && d->kw == 1) {
+    if (d->sh != 1 || d->sw != 1 || d->pad[0] || d->pad[1] || d->pad[2] || d->pad[3])
+      return fail("conv: 1x1 conv with stride/pad is not supported (lowering.rs:136-140)");
+    *pw = aih_pw_desc{d->n, d->ih * d->iw, div_ceil(d->cin, 4), div_ceil(d->cout, 4), d->kg_pad, d->act,
+                      d->residual, d->dt, d->wdt, AIH_VAR_AUTO, 0};
+    return 0;
+  }
+  if (d->kh != d->kw) return fail("conv: square kernels only (conv_igemm.rs:81)");
+  if (d->sh != d->sw) return fail("conv: isotropic stride only (conv_igemm.rs:82)");
+  std::memset(ig, 0, sizeof(*ig));
+  *ig = aih_igemm_desc{d->n, d->ih, d->iw, d->cin, d->cout, d->kh, d->sh, d->d,
+                       {d->pad[0], d->pad[1], d->pad[2], d->pad[3]}, d->act, d->residual, d->dt, d->wdt,
+                       AIH_VAR_AUTO, 0, 0, {}};
+  if (d->kg_pad != div_ceil(div_ceil(d->cin, 4), 4) * 4) return fail("conv: kg_pad must be ceil(cin/4) rounded to 4");
+  return 1;
+}
+
+size_t aih_conv_workspace_size(const aih_conv_desc *d) {
+  aih_pw_desc pw;
+  aih_igemm_desc ig;
+  aih_dw_desc dw;
+  GemmPlan g;
+  const int r = conv_route(d, &pw, &ig, &dw);
+  if (r == 0 && !check_pw(&pw) && !plan_pw(&pw, &g)) return g.ws;
+  if (r == 1 && !check_igemm(&ig) && !plan_igemm(&ig, &g)) return g.ws;
+  return 0;
+}
+
+int aih_conv(const aih_conv_desc *d, const void *x, const void *w, const void *bias, const void *res, void *y,
+             void *ws, size_t ws_bytes, aih_stream stream) {
+  return guarded([&] {
+    aih_pw_desc pw;
+    aih_igemm_desc ig;
+    aih_dw_desc dw;
+    const int r = conv_route(d, &pw, &ig, &dw);
+    if (r < 0) return AIH_ERR;
+    if (r == 0) return aih_conv_pw(&pw, x, w, bias, res, y, ws, ws_bytes, stream);
+    if (r == 1) {
+      const void *ins[1] = {x};
+      return aih_conv_igemm(&ig, ins, w, bias, res, y, ws, ws_bytes, stream);
+    }
+    return aih_conv_dw(&dw, x, w, bias, res, y, stream);
+  });
+}
+
+// ---------------------------------------------------------------- host packing (ai-core pack.rs)
+
+static inline uint16_t host_f32_to_f16(float f) {
+  _Float16 h = (_Float16)f;
+  uint16_t b;
+  std::memcpy(&b, &h, 2);
+  return b;
+}
+
+static inline uint16_t host_f32_to_bf16(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static inline float host_load(const void *p, size_t i, int32_t dt) {
+  if (dt == AIH_F32) return static_cast<const float *>(p)[i];
+  const uint16_t b = static_cast<const uint16_t *>(p)[i];
+  if (dt == AIH_F16) {
+    _Float16 h;
+    std::memcpy(&h, &b, 2);
+    return (float)h;
+  }
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+static inline void host_store(void *p, size_t i, float v, int32_t dt) {
+  if (dt == AIH_F32) static_cast<float *>(p)[i] = v;
+  else if (dt == AIH_F16) static_cast<uint16_t *>(p)[i] = host_f32_to_f16(v);
+  else static_cast<uint16_t *>(p)[i] = host_f32_to_bf16(v);
+}
+
+size_t aih_nhwc_c4_bytes(uint32_t n, uint32_t h, uint32_t w, uint32_t c, int32_t dt) {
+  if (!dtype_ok(dt)) return 0;
+  return (size_t)n * h * w * div_ceil(c, 4) * 4 * dsize(dt);
+}
+
+// pack_nhwc (pack.rs:34-47) with the batch outermost.
+int aih_pack_nhwc(const float *data, uint32_t n, uint32_t h, uint32_t w, uint32_t c, int32_t dt, void *out) {
+  return guarded([&] {
+    if (!data || !out || !dtype_ok(dt)) return fail("pack_nhwc: bad argument");
+    const uint32_t c4 = div_ceil(c, 4) * 4;
+    const size_t px = (size_t)n * h * w;
+    for (size_t p = 0; p < px; ++p)
+      for (uint32_t ch = 0; ch < c4; ++ch) host_store(out, p * c4 + ch, ch < c ? data[p * c + ch] : 0.0f, dt);
+    return AIH_OK;
+  });
+}
+
+// unpack_nhwc (pack.rs:50-64).
+int aih_unpack_nhwc(const void *bytes, uint32_t n, uint32_t h, uint32_t w, uint32_t c, int32_t dt, float *out) {
+  return guarded([&] {
+    if (!bytes || !out || !dtype_ok(dt)) return fail("unpack_nhwc: bad argument");
+    const uint32_t c4 = div_ceil(c, 4) * 4;
+    const size_t px = (size_t)n * h * w;
+    for (size_t p = 0; p < px; ++p)
+      for (uint32_t ch = 0; ch < c; ++ch) out[p * c + ch] = host_load(bytes, p * c4 + ch, dt);
+    return AIH_OK;
+  });
+}
+
+// pack_weights_conv (pack.rs:68-102): OIHW -> [tap][kg_pad][ng][j][comp].
+uint32_t aih_pack_weights_conv(const float *wt, uint32_t cout, uint32_t cin, uint32_t kh, uint32_t kw,
+                               uint32_t kg_align, int32_t dt, void *out) {
+  if (!wt || !out || !dtype_ok(dt) || !cout || !cin || !kh || !kw) {
+    g_err = "pack_weights_conv: bad argument";
+    return 0;
+  }
+  const uint32_t al = kg_align ? kg_align : 1;
+  const uint32_t kg = div_ceil(div_ceil(cin, 4), al) * al;
+  const uint32_t ng = div_ceil(cout, 4);
+  for (uint32_t t = 0; t < kh * kw; ++t) {
+    const uint32_t ky = t / kw, kx = t % kw;
+    for (uint32_t g = 0; g < kg; ++g)
+      for (uint32_t o = 0; o < ng; ++o)
+        for (uint32_t j = 0; j < 4; ++j)
+          for (uint32_t comp = 0; comp < 4; ++comp) {
+            const uint32_t oc = o * 4 + j, ic = g * 4 + comp;
+            const float v = (oc < cout && ic < cin) ? wt[(((size_t)oc * cin + ic) * kh + ky) * kw + kx] : 0.0f;
+            host_store(out, ((((size_t)t * kg + g) * ng + o) * 4 + j) * 4 + comp, v, dt);
+          }
+  }
+  return kg;
+}
+
+// pack_weights_dw (pack.rs:105-122): [c][kh][kw] -> [tap][cg][comp].
+int aih_pack_weights_dw(const float *wt, uint32_t c, uint32_t kh, uint32_t kw, int32_t dt, void *out) {
+  return guarded([&] {
+    if (!wt || !out || !dtype_ok(dt)) return fail("pack_weights_dw: bad argument");
+    const uint32_t cg = div_ceil(c, 4), taps = kh * kw;
+    for (uint32_t g = 0; g < cg; ++g)
+      for (uint32_t t = 0; t < taps; ++t)
+        for (uint32_t comp = 0; comp < 4; ++comp) {
+          const uint32_t ch = g * 4 + comp;
+          host_store(out, ((size_t)t * cg + g) * 4 + comp, ch < c ? wt[(size_t)ch * taps + t] : 0.0f, dt);
+        }
+    return AIH_OK;
+  });
+}
+
+// pack_bias (pack.rs:178-184).
+int aih_pack_bias(const float *b, uint32_t cout, int32_t dt, void *out) {
+  return guarded([&] {
+    if (!b || !out || !dtype_ok(dt)) return fail("pack_bias: bad argument");
+    const uint32_t n4 = div_ceil(cout, 4) * 4;
+    for (uint32_t i = 0; i < n4; ++i) host_store(out, i, i < cout ? b[i] : 0.0f, dt);
+    return AIH_OK;
+  });
+}
+
+int aih_pack_nhwc_device(const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c, int32_t dt, void *y,
+                         aih_stream stream) {
+  return guarded([&] {
+    if (!x || !y || !dtype_ok(dt) || !n || !h || !w || !c) return fail("pack_nhwc_device: bad argument");
+    if (!aligned(y, 8) || !aligned(x, 4)) return fail("pack_nhwc_device: misaligned buffer");
+    hipError_t e = aih::launch_pack_nhwc(x, (uint64_t)n * h * w, c, dt, y, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(std::string("pack_nhwc launch: ") + hipGetErrorString(e));
+    return AIH_OK;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,344 @@
+"""Benchmark of the MI355X conv-as-GEMM backend (one GPU).
+
+Headline workload (value, frames/s): the MobileNetV4-small-width segmentation
+encoder at 160x288, batch 64, bf16 storage with fp32 accumulation -- 32 convs
+(stem 3x3 s2 3->32, ten inverted-residual blocks, 1x1 head 128->2) with
+random He-init weights and U[-1,1) synthetic input already resident in HBM.
+One step = pack the fp32 NHWC input to NHWC-C4 on the device + all 32 convs.
+
+Also measured in the same run (the "kernels" object), each with absolute
+TFLOP/s, GB/s and its roofline fraction (t_roof / t_measured,
+t_roof = max(flops / MFMA peak, bytes / 8 TB/s)):
+  pw_32to64_relu6_80x144            1x1 32->64 + ReLU6, [1,80,144,32] fp32
+  pw_960to160_10x18_b1_splitk{1,4,8} 1x1 960->160, [1,10,18,960] fp32, split-K forced
+  pw_960to160_10x18_b256            the same layer at batch 256 (policy: no split)
+  igemm3x3s2_16to32_relu_160x288_b32 3x3 s2 pad 1 16->32 + ReLU, [32,160,288,16] fp32
+  igemm3x3s1_32to64_relu_80x144_b32  3x3 s1 pad 1 32->64 + ReLU, [32,80,144,32] fp32
+  ir_block_chain_4x_64c_40x72_b64    4 inverted-residual blocks at [64,40,72,64] fp32
+  encoder_f16                        the headline workload with f16 storage
+Small configurations are timed over rotated buffer sets larger than the 256 MB
+Infinity Cache, so their GB/s are HBM figures.
+
+cpu_baseline: the oracle's C restatement of ai-cpu (the reference's CPU path:
+conv_std / im2row stem / conv_dw / pw_dot head, row-band threads) running the
+same encoder in fp32 on the host's cores, on a bounded sample of frames.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--dtype bf16|f16]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "conv-GEMM TFLOP/s + HBM GB/s (% roofline), frames/s at 160x288 batch 64"
+HBM_GBS = 8000.0
+PEAK_TF = {"f32": 157.3, "f16": 2516.6, "bf16": 2516.6}
+MALL_BYTES = 256 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def roof(flops: float, nbytes: float, secs: float, dtype: str) -> dict:
+    t_mfma = flops / (PEAK_TF[dtype] * 1e12)
+    t_hbm = nbytes / (HBM_GBS * 1e9)
+    bound = "mfma" if t_mfma >= t_hbm else "hbm"
+    return dict(
+        us=secs * 1e6, tflops=flops / secs / 1e12, gbs=nbytes / secs / 1e9, bound=bound,
+        frac=max(t_mfma, t_hbm) / secs, flops=flops, bytes=nbytes,
+    )
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "f16"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the per-config kernel table")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(batch sharding across GPUs needs no exchange and is not run here)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from ai_engine_amd import conv, workloads as W
+    from ai_engine_amd.model import Model
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    conv.lib()
+    torch.manual_seed(0)
+    DT = {"f32": conv.DType.F32, "f16": conv.DType.F16, "bf16": conv.DType.BF16}
+
+    # ------------------------------------------------------------ headline: encoder, batch 64
+    layers, meta = W.mnv4_small_encoder_160x288(64)
+    n, H, Wd = meta["n"], meta["h"], meta["w"]
+    wts = W.make_weights(layers, seed=0)
+    x = (torch.rand(n, H, Wd, 3, device=dev) * 2 - 1).contiguous()
+    model = Model(layers, wts, n, H, Wd, 3, dt=DT[args.dtype])
+    stream = torch.cuda.current_stream()
+
+    def step():
+        model.upload_input(x)
+        model.infer()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = e0.elapsed_time(e1) / args.steps
+    ms_per_step = wall * 1e3 / args.steps
+    fps = n / (ms_per_step / 1e3)
+    log(f"encoder {args.dtype} b{n}: {ms_per_step:.3f} ms/step wall, {gpu_ms:.3f} ms/step gpu, {fps:.0f} frames/s")
+
+    # per-op timing (HIP events on the launch stream), grouped by kernel instantiation
+    R = 5
+    nops = len(model.ops)
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nops)]
+           for _ in range(R)]
+    for r in range(R):
+        model.upload_input(x)
+        for i in range(nops):
+            evs[r][i][0].record(stream)
+            model.launch_op(i)
+            evs[r][i][1].record(stream)
+    torch.cuda.synchronize()
+    act_b = 2 if args.dtype != "f32" else 4
+    groups: dict[str, dict] = {}
+    layer_rows = []
+    for i, (Lr, op, _) in enumerate(model.ops):
+        t = sorted(evs[r][i][0].elapsed_time(evs[r][i][1]) for r in range(R))[R // 2] / 1e3
+        fl, by = Lr.flops(n), Lr.bytes(n, act_b, act_b)
+        if Lr.depthwise:
+            key = f"conv_dw_kernel<{args.dtype}>"
+        else:
+            if Lr.k == 1:
+                p = conv.GemmPwSpec(m=Lr.ih * Lr.iw, kg=-(-Lr.cin // 4), ng=-(-Lr.cout // 4), dt=DT[args.dtype],
+                                    n=n).plan()
+            else:
+                p = conv.ConvIgemmSpec(ih=Lr.ih, iw=Lr.iw, cin=Lr.cin, cout=Lr.cout, k=Lr.k, s=Lr.s,
+                                       pad=(Lr.pad,) * 4, dt=DT[args.dtype], n=n).plan()
+            key = f"conv_gemm_kernel<{args.dtype},{args.dtype},BN={p.bn},{'igemm' if Lr.k > 1 else 'pw'}>"
+            if p.splitk > 1:
+                key += "+splitk_reduce"
+        g = groups.setdefault(key, dict(launches=0, secs=0.0, flops=0, bytes=0))
+        g["launches"] += 1
+        g["secs"] += t
+        g["flops"] += fl
+        g["bytes"] += by
+        layer_rows.append(dict(layer=Lr.name, kernel=key, us=round(t * 1e6, 2),
+                               gbs=round(by / t / 1e9, 1), tflops=round(fl / t / 1e12, 2)))
+    step_secs = sum(g["secs"] for g in groups.values())
+    dom_key, dom = max(groups.items(), key=lambda kv: kv[1]["secs"])
+    dr = roof(dom["flops"] / dom["launches"], dom["bytes"] / dom["launches"], dom["secs"] / dom["launches"],
+              args.dtype)
+    if dr["bound"] == "hbm":
+        roofline = dict(bound="hbm", achieved=round(dr["gbs"], 1), peak=HBM_GBS, unit="GB/s",
+                        frac=round(dr["gbs"] / HBM_GBS, 4), traffic=None)
+    else:
+        roofline = dict(bound="mfma", achieved=round(dr["tflops"], 2), peak=PEAK_TF[args.dtype], unit="TFLOP/s",
+                        frac=round(dr["tflops"] / PEAK_TF[args.dtype], 4), traffic=None)
+    roofline.update(kernel=dom_key, launches_per_step=dom["launches"],
+                    avg_launch_us=round(dom["secs"] / dom["launches"] * 1e6, 2),
+                    algorithmic_bytes_per_launch=int(dom["bytes"] / dom["launches"]),
+                    algorithmic_flops_per_launch=int(dom["flops"] / dom["launches"]),
+                    share_of_step=round(dom["secs"] / step_secs, 3))
+    tot_fl, tot_by = W.totals(layers, n, act_b, act_b)
+    step_roof = roof(tot_fl, tot_by, gpu_ms / 1e3, args.dtype)
+    log(f"dominant kernel {dom_key}: {roofline}")
+
+    # ------------------------------------------------------------ per-config kernel table (fp32)
+    kernels = {}
+    if not args.no_kernels:
+        kernels = kernel_table(torch, conv, W, Model, dev, stream, DT)
+        kernels["encoder_f16" if args.dtype == "bf16" else "encoder_bf16"] = encoder_other(
+            torch, W, Model, layers, wts, x, n, H, Wd, "f16" if args.dtype == "bf16" else "bf16", DT, stream)
+    kernels["encoder_layers"] = layer_rows
+
+    # ------------------------------------------------------------ CPU baseline (oracle ai-cpu restatement)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(layers, wts, H, Wd, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC, "value": round(fps, 1), "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": args.dtype, "data": "synthetic",
+        "config": {"workload": meta["name"], "batch": n, "height": H, "width": Wd, "convs": len(layers),
+                   "storage": args.dtype, "accumulate": "f32", "step": "device pack + 32 convs"},
+        "gpu_ms_per_step": round(gpu_ms, 4),
+        "step_roofline": {"tflops": round(step_roof["tflops"], 2), "gbs": round(step_roof["gbs"], 1),
+                          "bound": step_roof["bound"], "frac": round(step_roof["frac"], 4),
+                          "algorithmic_flops": tot_fl, "algorithmic_bytes": tot_by},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def time_launches(torch, stream, fn, reps: int, warm: int = 3) -> float:
+    """Median seconds of fn() measured with HIP events on the launch stream."""
+    for _ in range(warm):
+        fn(0)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for r in range(reps):
+        ev[r][0].record(stream)
+        fn(r)
+        ev[r][1].record(stream)
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in ev)
+    return ts[len(ts) // 2] / 1e3
+
+
+def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
+    res = {}
+
+    def sets_for(footprint: int) -> int:
+        return max(1, math.ceil(2 * MALL_BYTES / footprint))
+
+    def rnd(nel, dtype=torch.float32, scale=1.0):
+        return (torch.rand(nel, device=dev, dtype=dtype) * 2 - 1) * scale
+
+    def pw_case(name, n, h, w, cin, cout, act, splitk=0, reps=60):
+        spec = conv.GemmPwSpec(m=h * w, kg=cin // 4, ng=cout // 4, act=act, n=n, splitk=splitk)
+        plan = spec.plan()
+        m = n * h * w
+        fl = 2 * m * cin * cout
+        by = 4 * (m * cin + cin * cout + cout + m * cout)
+        S = sets_for(4 * (m * cin + m * cout))
+        xs = [rnd(m * cin) for _ in range(S)]
+        ys = [torch.empty(m * cout, device=dev) for _ in range(S)]
+        wt = rnd(cin * cout, scale=0.05)
+        b = rnd(cout, scale=0.01)
+        ws = torch.empty(max(plan.ws_bytes // 4, 1), device=dev)
+        t = time_launches(torch, stream, lambda r: spec.run(xs[r % S], wt, b, None, ys[r % S], ws, stream), reps)
+        row = roof(fl, by, t, "f32")
+        row.update(splitk=plan.splitk, bn=plan.bn, grid=plan.grid, buffer_sets=S)
+        res[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
+        log(f"{name}: {row['us']:.2f} us {row['tflops']:.2f} TF {row['gbs']:.0f} GB/s frac {row['frac']:.3f}")
+
+    def ig_case(name, n, ih, iw, cin, cout, s, act, reps=30):
+        spec = conv.ConvIgemmSpec(ih=ih, iw=iw, cin=cin, cout=cout, k=3, s=s, pad=(1, 1, 1, 1), act=act, n=n)
+        plan = spec.plan()
+        oh, ow = spec.out_hw()
+        m = n * oh * ow
+        fl = 2 * m * 9 * cin * cout
+        by = 4 * (n * ih * iw * cin + 9 * cin * cout + cout + m * cout)
+        S = sets_for(4 * (n * ih * iw * cin + m * cout))
+        xs = [rnd(n * ih * iw * cin) for _ in range(S)]
+        ys = [torch.empty(m * cout, device=dev) for _ in range(S)]
+        wt = rnd(9 * cin * cout, scale=0.1)
+        b = rnd(cout, scale=0.01)
+        ws = torch.empty(max(plan.ws_bytes // 4, 1), device=dev)
+        t = time_launches(torch, stream, lambda r: spec.run([xs[r % S]], wt, b, None, ys[r % S], ws, stream), reps)
+        row = roof(fl, by, t, "f32")
+        row.update(splitk=plan.splitk, bn=plan.bn, grid=plan.grid, buffer_sets=S)
+        res[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
+        log(f"{name}: {row['us']:.2f} us {row['tflops']:.2f} TF {row['gbs']:.0f} GB/s frac {row['frac']:.3f}")
+
+    A = conv.Activation
+    pw_case("pw_32to64_relu6_80x144", 1, 80, 144, 32, 64, A.RELU6, reps=200)
+    for s in (1, 4, 8):
+        pw_case(f"pw_960to160_10x18_b1_splitk{s}", 1, 10, 18, 960, 160, A.NONE, splitk=s, reps=200)
+    pw_case("pw_960to160_10x18_b256", 256, 10, 18, 960, 160, A.NONE, reps=40)
+    ig_case("igemm3x3s2_16to32_relu_160x288_b32", 32, 160, 288, 16, 32, 2, A.RELU)
+    ig_case("igemm3x3s1_32to64_relu_80x144_b32", 32, 80, 144, 32, 64, 1, A.RELU)
+
+    # four inverted-residual blocks, fp32
+    layers, meta = W.ir_chain_40x72(64)
+    wts = W.make_weights(layers, seed=1)
+    m4 = Model(layers, wts, meta["n"], meta["h"], meta["w"], meta["c"], dt=DT["f32"])
+    m4.tensors["input"].uniform_(-1, 1)
+    t = time_launches(torch, stream, lambda r: m4.infer(stream), 10)
+    fl, by = W.totals(layers, meta["n"], 4, 4)
+    row = roof(fl, by, t, "f32")
+    row["per_layer_roofline_sum_us"] = sum(
+        max(L.flops(meta["n"]) / (PEAK_TF["f32"] * 1e12), L.bytes(meta["n"], 4, 4) / (HBM_GBS * 1e9))
+        for L in layers) * 1e6
+    res["ir_block_chain_4x_64c_40x72_b64"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
+    log(f"ir chain: {row['us']:.1f} us frac {row['frac']:.3f}")
+    del m4
+    return res
+
+
+def encoder_other(torch, W, Model, layers, wts, x, n, H, Wd, dtname, DT, stream) -> dict:
+    m = Model(layers, wts, n, H, Wd, 3, dt=DT[dtname])
+
+    def step(_):
+        m.upload_input(x)
+        m.infer()
+
+    t = time_launches(torch, stream, step, 10)
+    fl, by = W.totals(layers, n, 2, 2)
+    row = roof(fl, by, t, dtname)
+    row["frames_per_s"] = n / t
+    log(f"encoder {dtname}: {t * 1e3:.3f} ms {n / t:.0f} frames/s")
+    return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
+
+
+def cpu_baseline(layers, wts, H, Wd, budget_s: float) -> dict:
+    """The oracle's ai-cpu restatement on the same encoder (fp32, one frame at a
+    time as ai-cpu has no batch), T = all host cores, row-band threading."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    ops = []
+    for L in layers:
+        op = orc.conv2d(L.cin, L.cout, k=L.k, s=L.s, pad=L.pad, groups=L.groups, act=L.act)
+        ops.append((L, orc.CpuConv(op, L.ih, L.iw, wts.w[L.name], wts.b[L.name], has_res=L.res is not None)))
+    rng = np.random.default_rng(5)
+    x = rng.uniform(-1, 1, H * Wd * 3).astype(np.float32)
+
+    def frame():
+        bufs = {"input": x}
+        for L, cc in ops:
+            bufs[L.name] = cc.run(bufs[L.src], 1, bufs[L.res] if L.res else None, threads=cores)
+        return bufs[layers[-1].name]
+
+    frame()  # warm-up (also sizes the sample)
+    t0 = time.perf_counter()
+    frame()
+    t1 = time.perf_counter() - t0
+    frames = max(2, min(64, int(budget_s / max(t1, 1e-6))))
+    t0 = time.perf_counter()
+    for _ in range(frames):
+        frame()
+    secs = time.perf_counter() - t0
+    fps = frames / secs
+    log(f"cpu baseline: {fps:.2f} frames/s on {cores} threads ({frames} frames, {secs:.1f} s)")
+    return {"value": round(fps, 3), "unit": "frames/s", "cores": cores, "kind": "port",
+            "sample": f"{frames} frames of the 160x288 encoder, fp32, one frame at a time, {cores} row-band threads",
+            "ms_per_frame": round(secs / frames * 1e3, 2)}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,192 @@
+/*
+ * aih_conv.h -- C ABI of the MI355X (gfx950) conv-as-GEMM backend.
+ *
+ * The entry points replace, op for op, what the reference's GPU runtime binds
+ * for a SwOp::Conv (crates/ai-gpu-runtime/src/lowering.rs:99-187):
+ *   - aih_conv_pw     <- GemmPwSpec + its dispatch (crates/ai-gpu/src/kernels/gemm_pw.rs:129-297)
+ *   - aih_conv_igemm  <- ConvIgemmSpec + its dispatch (crates/ai-gpu/src/kernels/conv_igemm.rs:49-558)
+ *   - aih_conv_dw     <- ConvDwSpec + its dispatch (crates/ai-gpu/src/kernels/conv_dw.rs:21-216)
+ *   - aih_conv        <- the Conv arm of lower_op itself (lowering.rs:99-187):
+ *                        routes groups>1 -> dw, 1x1 -> pw, KxK -> igemm
+ *   - aih_*_plan      <- the pure variant policies pick_variant (gemm_pw.rs:91-102)
+ *                        and ConvIgemmSpec::variant (conv_igemm.rs:201-233), re-tuned
+ *                        for MI355X
+ *   - aih_pack_*      <- ai-core pack.rs:34-184 (the converter's output contract)
+ *
+ * Conventions follow the reference's C ABI (crates/ai-ffi/src/lib.rs:45-52,
+ * 130-133): every function returns AIH_OK (0) or AIH_ERR (-1) and never lets
+ * an exception cross the boundary; aih_last_error() returns the calling
+ * thread's message for the last failure.
+ *
+ * Buffers (all device pointers, caller-owned, never allocated by a conv call):
+ *   activations  NHWC-C4: element (b, y, x, c) at ((b*H + y)*W + x)*CG*4 + c,
+ *                CG = ceil(C/4), C padded with zeros to a multiple of 4
+ *                (tensor.rs:1-6,72-74); b is the batch, outermost (new here).
+ *   std weights  [tap][kg_pad][ng][j][comp] vec4, kg_pad = ceil(cin/4) rounded up
+ *                to a multiple of 4 (pack.rs:68-102), dtype wdt.
+ *   dw weights   [tap][cg][comp] vec4 (pack.rs:105-122), dtype dt.
+ *   bias         [ng][4] (pack.rs:178-184), dtype dt; always present.
+ *   residual     same layout and dtype as the output; added AFTER the
+ *                activation: y = act(acc + bias) + res (reference/conv.rs:53-56).
+ * dtypes: AIH_F32 / AIH_F16 as ai-core DType; AIH_BF16 is new. Accumulation
+ * is always fp32.
+ */
+#ifndef AIH_CONV_H
+#define AIH_CONV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AIH_OK 0
+#define AIH_ERR (-1)
+
+/* A hipStream_t. NULL selects the null stream. */
+typedef void *aih_stream;
+
+enum aih_dtype { AIH_F32 = 0, AIH_F16 = 1, AIH_BF16 = 2 };
+
+/* Same order as ai-core Activation (crates/ai-core/src/activation.rs:7-25). */
+enum aih_act {
+  AIH_ACT_NONE = 0,
+  AIH_ACT_RELU = 1,
+  AIH_ACT_SIGMOID = 2,
+  AIH_ACT_TANH = 3,
+  AIH_ACT_HARDSWISH = 4,
+  AIH_ACT_HARDSIGMOID = 5,
+  AIH_ACT_CLAMP01 = 6,
+  AIH_ACT_RELU6 = 7,
+  AIH_ACT_SQRT = 8,
+  AIH_ACT_NEG = 9,
+  AIH_ACT_RECIP = 10
+};
+
+/* Kernel variants chosen by the plan functions. */
+enum aih_variant {
+  AIH_VAR_AUTO = 0,   /* let the policy decide */
+  AIH_VAR_TILE = 1,   /* one MFMA tile per workgroup over the whole K */
+  AIH_VAR_SPLITK = 2  /* K cut into chunks, fp32 partials reduced in a fixed order */
+};
+
+/* Pointwise 1x1 conv GEMM: out[M, N] = act(in[M, K] x W[K, N] + bias) (+ res).
+ * Mirrors GemmPwSpec{m, kg, ng, act, residual, dt, wdt} (gemm_pw.rs:129-142). */
+typedef struct {
+  uint32_t n;       /* images; the reference always has 1 (tensor.rs:37) */
+  uint32_t m;       /* pixels per image (= ih*iw, lowering.rs:145) */
+  uint32_t kg;      /* ceil(cin/4) */
+  uint32_t ng;      /* ceil(cout/4) */
+  uint32_t kg_pad;  /* kg of the packed weights (SwOp::Conv.kg_pad); >= kg */
+  int32_t act;      /* enum aih_act */
+  int32_t residual; /* 0 or 1 */
+  int32_t dt;       /* activation / bias / residual / output dtype */
+  int32_t wdt;      /* weight dtype (independent of dt, format/model.rs:245-254) */
+  int32_t variant;  /* enum aih_variant */
+  int32_t splitk;   /* 0 = policy; otherwise the split-K factor (1 = no split) */
+} aih_pw_desc;
+
+/* One input part of a KxK conv: `c` channels that start at channel `c_off`
+ * of a tensor whose pixels hold `stride_c` channels (SrcView,
+ * crates/ai-gpu/src/kernels/common/source.rs:17). c_off and stride_c are
+ * multiples of 4. */
+typedef struct {
+  uint32_t c, stride_c, c_off;
+} aih_src;
+
+/* KxK implicit-GEMM conv (groups = 1). Mirrors ConvIgemmSpec (conv_igemm.rs:49-76)
+ * plus a batch n; non-square kernels and anisotropic strides are rejected as in
+ * ConvIgemmSpec::from_op (conv_igemm.rs:79-83). */
+typedef struct {
+  uint32_t n, ih, iw, cin, cout;
+  uint32_t k, s, d;
+  uint32_t pad[4]; /* top, left, bottom, right */
+  int32_t act, residual, dt, wdt;
+  int32_t variant; /* enum aih_variant */
+  int32_t splitk;  /* 0 = policy */
+  uint32_t nsrcs;  /* 0 = one dense input; 1..3 = srcs[] (channel view / concat parts) */
+  aih_src srcs[3];
+} aih_igemm_desc;
+
+/* Depthwise conv (groups = cin = cout), any k/s/d/pad. Mirrors ConvDwSpec. */
+typedef struct {
+  uint32_t n, ih, iw, c;
+  uint32_t k, s, d;
+  uint32_t pad[4];
+  int32_t act, residual, dt;
+} aih_dw_desc;
+
+/* A whole SwOp::Conv (format/model.rs:80-111) as lower_op sees it. */
+typedef struct {
+  uint32_t n, ih, iw, cin, cout;
+  uint32_t kh, kw, sh, sw;
+  uint32_t pad[4];
+  uint32_t d, groups;
+  int32_t act, residual;
+  int32_t dt, wdt;
+  uint32_t kg_pad;
+} aih_conv_desc;
+
+/* What a plan function chose; grid is the number of workgroups of the main kernel. */
+typedef struct {
+  int32_t variant;  /* AIH_VAR_TILE or AIH_VAR_SPLITK */
+  uint32_t splitk;  /* K chunks (1 for TILE) */
+  uint32_t bm, bn;  /* output tile: pixels x channels */
+  uint32_t grid;
+  size_t ws_bytes;  /* workspace the call needs */
+} aih_plan;
+
+/* ---- op entry points (asynchronous on `stream`) ---- */
+
+/* Buffer order follows GemmPwSpec::bindings (gemm_pw.rs:276-283): IN, W, BIAS,
+ * [RES], OUT. res must be NULL iff residual == 0. ws may be NULL when the plan
+ * needs no workspace; otherwise ws_bytes >= aih_plan.ws_bytes. */
+int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *bias,
+                const void *res, void *y, void *ws, size_t ws_bytes, aih_stream stream);
+int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out);
+
+/* inputs holds max(1, nsrcs) device pointers: the plain input, or one per part
+ * (the IN0..IN2 bindings of conv_igemm.rs:141-171). */
+int aih_conv_igemm(const aih_igemm_desc *d, const void *const *inputs, const void *w,
+                   const void *bias, const void *res, void *y, void *ws, size_t ws_bytes,
+                   aih_stream stream);
+int aih_conv_igemm_plan(const aih_igemm_desc *d, aih_plan *out);
+
+int aih_conv_dw(const aih_dw_desc *d, const void *x, const void *w, const void *bias,
+                const void *res, void *y, aih_stream stream);
+
+/* Routes like lower_op (lowering.rs:122-168): groups > 1 -> dw, 1x1 -> pw
+ * (stride or pad rejected, :136-140), otherwise igemm. */
+int aih_conv(const aih_conv_desc *d, const void *x, const void *w, const void *bias,
+             const void *res, void *y, void *ws, size_t ws_bytes, aih_stream stream);
+size_t aih_conv_workspace_size(const aih_conv_desc *d);
+
+/* ---- host-side packing (ai-core pack.rs; plain host memory) ---- */
+/* Output bytes = n*h*w*ceil(c/4)*4*sizeof(dt). */
+size_t aih_nhwc_c4_bytes(uint32_t n, uint32_t h, uint32_t w, uint32_t c, int32_t dt);
+int aih_pack_nhwc(const float *data, uint32_t n, uint32_t h, uint32_t w, uint32_t c, int32_t dt,
+                  void *out);
+int aih_unpack_nhwc(const void *bytes, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                    int32_t dt, float *out);
+/* Returns kg_pad (> 0) or 0 on error. */
+uint32_t aih_pack_weights_conv(const float *w_oihw, uint32_t cout, uint32_t cin, uint32_t kh,
+                               uint32_t kw, uint32_t kg_align, int32_t dt, void *out);
+int aih_pack_weights_dw(const float *w, uint32_t c, uint32_t kh, uint32_t kw, int32_t dt,
+                        void *out);
+int aih_pack_bias(const float *b, uint32_t cout, int32_t dt, void *out);
+
+/* ---- device-side layout kernels ---- */
+/* Logical NHWC fp32 (n*h*w*c floats) -> NHWC-C4 in dt, on the device (the
+ * upload path of Model::upload_input, crates/ai-gpu-runtime/src/model.rs:387-399). */
+int aih_pack_nhwc_device(const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                         int32_t dt, void *y, aih_stream stream);
+
+/* ---- errors / info ---- */
+const char *aih_last_error(void);
+const char *aih_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

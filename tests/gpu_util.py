@@ -1,0 +1,150 @@
+"""Helpers for the GPU parity tests: seeded inputs in the reference's stream
+order, packing through the oracle (the converter's byte contract), NaN-poisoned
+outputs, and the two error measures the reference uses."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from ai_engine_amd import conv
+from oracle import oracle as orc
+
+DEV = torch.device("cuda:0")
+NP_DT = {0: np.float32, 1: np.uint16, 2: np.uint16}
+POISON = {0: np.float32(np.nan).view(np.uint32), 1: 0x7E00, 2: 0x7FC0}
+
+
+def stream(seed: int, *sizes: int) -> list[np.ndarray]:
+    """XorShift32::new(seed) drawn in order into tensors of the given sizes."""
+    flat = orc.xs32_fill(seed, int(sum(sizes)))
+    out, o = [], 0
+    for s in sizes:
+        out.append(flat[o:o + s])
+        o += s
+    return out
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).to(DEV)
+    return torch.from_numpy(a).to(DEV)
+
+
+def poisoned(n_elems: int, dt: int) -> torch.Tensor:
+    """Fresh output buffer filled with NaN (so unwritten elements cannot pass)."""
+    if dt == 0:
+        return torch.full((n_elems,), float("nan"), dtype=torch.float32, device=DEV)
+    return torch.full((n_elems,), int(np.int16(np.uint16(POISON[dt]).view(np.int16))), dtype=torch.int16, device=DEV)
+
+
+def host(t: torch.Tensor, dt: int) -> np.ndarray:
+    a = t.detach().cpu().numpy()
+    return a.view(np.uint16) if dt != 0 else a
+
+
+def rel_err(got, want) -> float:
+    """BASELINE metric (the reference's synthetic_e2e.rs:113-116 convention):
+    max |gpu - cpu| / max(|cpu|, 1); NaN counts as infinite."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    if got.shape != want.shape:
+        return float("inf")
+    e = np.abs(got - want) / np.maximum(np.abs(want), 1.0)
+    if np.isnan(e).any():
+        return float("inf")
+    return float(e.max(initial=0.0))
+
+
+def testsuite_ok(got, want, atol, rtol) -> bool:
+    """The reference GPU testsuite's compare (crates/ai-gpu/src/testsuite.rs:33-44)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return bool(np.all(np.abs(got - want) <= atol + rtol * np.abs(want)))
+
+
+ACT = {"none": conv.Activation.NONE, "relu": conv.Activation.RELU, "hardswish": conv.Activation.HARDSWISH,
+       "sigmoid": conv.Activation.SIGMOID, "relu6": conv.Activation.RELU6}
+
+
+def run_pw(h, w, cin, cout, act, residual, dt, seed, wdt=None, n=1, splitk=0, variant=0, xs=None):
+    """pw_case (testsuite.rs:325-371): returns (got, want, plan)."""
+    wdt = dt if wdt is None else wdt
+    if xs is None:
+        x, wts, b, r = stream(seed, n * h * w * cin, cout * cin, cout, n * h * w * cout if residual else 0)
+    else:
+        x, wts, b, r = xs
+    op = orc.conv2d(cin, cout, act=act)
+    want = orc.conv2d_ref(op, h, w, x, wts, b, r if residual else None, n=n)
+    wp, kgp = orc.pack_weights_conv(wts, cout, cin, 1, 1, 4, wdt)
+    xd = dev(orc.pack_nhwc(x, n, h, w, cin, dt))
+    wd = dev(wp)
+    bd = dev(orc.pack_bias(b, cout, dt))
+    rd = dev(orc.pack_nhwc(r, n, h, w, cout, dt)) if residual else None
+    ng = -(-cout // 4)
+    yd = poisoned(n * h * w * ng * 4, dt)
+    spec = conv.GemmPwSpec(m=h * w, kg=-(-cin // 4), ng=ng, act=ACT[act], residual=residual,
+                           dt=conv.DType(dt), wdt=conv.DType(wdt), n=n, kg_pad=kgp,
+                           variant=conv.Variant(variant), splitk=splitk)
+    plan = spec.plan()
+    spec.run(xd, wd, bd, rd, yd)
+    torch.cuda.synchronize()
+    got = orc.unpack_nhwc(host(yd, dt), n, h, w, cout, dt)
+    return got, want, plan
+
+
+def run_igemm(ih, iw, cin, cout, k, s, pad, act, residual, dt, seed, wdt=None, n=1, d=1, splitk=0, variant=0,
+              parts=None):
+    """igemm_case / igemm_concat_case (testsuite.rs:588-720): returns (got, want, plan)."""
+    wdt = dt if wdt is None else wdt
+    op = orc.conv2d(cin, cout, k=k, s=s, pad=list(pad), dil=d, act=act)
+    oh, ow = orc.out_hw(op, ih, iw)
+    if parts is None:
+        x, wts, b, r = stream(seed, n * ih * iw * cin, cout * cin * k * k, cout,
+                              n * oh * ow * cout if residual else 0)
+        xin = x
+        inputs = [dev(orc.pack_nhwc(x, n, ih, iw, cin, dt))]
+        srcs = []
+    else:
+        assert n == 1
+        sizes = [ih * iw * c for c in parts]
+        vals = stream(seed, *sizes, cout * cin * k * k, cout, oh * ow * cout if residual else 0)
+        pv, (wts, b, r) = vals[:len(parts)], vals[len(parts):]
+        xin = np.concatenate([p.reshape(ih * iw, c) for p, c in zip(pv, parts)], axis=1).ravel()
+        inputs = [dev(orc.pack_nhwc(p, 1, ih, iw, c, dt)) for p, c in zip(pv, parts)]
+        srcs = [conv.SrcView(c=c) for c in parts]
+    want = orc.conv2d_ref(op, ih, iw, xin, wts, b, r if residual else None, n=n)
+    wp, _ = orc.pack_weights_conv(wts, cout, cin, k, k, 4, wdt)
+    wd = dev(wp)
+    bd = dev(orc.pack_bias(b, cout, dt))
+    rd = dev(orc.pack_nhwc(r, n, oh, ow, cout, dt)) if residual else None
+    yd = poisoned(n * oh * ow * (-(-cout // 4)) * 4, dt)
+    spec = conv.ConvIgemmSpec(ih=ih, iw=iw, cin=cin, cout=cout, k=k, s=s, d=d, pad=tuple(pad), act=ACT[act],
+                              residual=residual, dt=conv.DType(dt), wdt=conv.DType(wdt), n=n,
+                              variant=conv.Variant(variant), splitk=splitk, srcs=srcs)
+    plan = spec.plan()
+    spec.run(inputs, wd, bd, rd, yd)
+    torch.cuda.synchronize()
+    got = orc.unpack_nhwc(host(yd, dt), n, oh, ow, cout, dt)
+    return got, want, plan
+
+
+def run_dw(ih, iw, c, k, s, act, residual, dt, seed, pad=None, d=1, n=1):
+    """dw_case (testsuite.rs:416-464): returns (got, want)."""
+    if pad is None:
+        pad = [(k - 1) // 2] * 4
+    op = orc.conv2d(c, c, k=k, s=s, pad=list(pad), dil=d, groups=c, act=act)
+    oh, ow = orc.out_hw(op, ih, iw)
+    x, wts, b, r = stream(seed, n * ih * iw * c, c * k * k, c, n * oh * ow * c if residual else 0)
+    want = orc.conv2d_ref(op, ih, iw, x, wts, b, r if residual else None, n=n)
+    xd = dev(orc.pack_nhwc(x, n, ih, iw, c, dt))
+    wd = dev(orc.pack_weights_dw(wts, c, k, k, dt))
+    bd = dev(orc.pack_bias(b, c, dt))
+    rd = dev(orc.pack_nhwc(r, n, oh, ow, c, dt)) if residual else None
+    yd = poisoned(n * oh * ow * (-(-c // 4)) * 4, dt)
+    spec = conv.ConvDwSpec(ih=ih, iw=iw, c=c, k=k, s=s, d=d, pad=tuple(pad), act=ACT[act], residual=residual,
+                           dt=conv.DType(dt), n=n)
+    spec.run(xd, wd, bd, rd, yd)
+    torch.cuda.synchronize()
+    got = orc.unpack_nhwc(host(yd, dt), n, oh, ow, c, dt)
+    return got, want

@@ -1,0 +1,139 @@
+"""CPU checks of the C ABI (no kernel launches): the library loads and exports
+every function include/aih_conv.h declares, the host packing matches the
+oracle's restatement of ai-core pack.rs byte for byte, the variant policy
+behaves as specified, and invalid descriptors fail with -1 and a message
+instead of crashing (the reference FFI's contract, crates/ai-ffi/src/lib.rs:45-52)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from ai_engine_amd import conv
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "aih_conv.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(aih_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    L = conv.lib()
+    declared = header_functions()
+    assert len(declared) >= 16
+    for name in declared:
+        assert hasattr(L, name), name
+    assert set(conv.EXPORTS) == set(declared)
+    assert b"gfx950" in L.aih_version()
+
+
+@pytest.mark.parametrize("dt", [0, 1, 2], ids=["f32", "f16", "bf16"])
+def test_host_packing_matches_oracle(orc, dt):
+    n, h, w, c = 2, 3, 5, 7
+    x = orc.xs32_fill(1, n * h * w * c)
+    assert np.array_equal(conv.pack_nhwc(x, n, h, w, c, conv.DType(dt)), orc.pack_nhwc(x, n, h, w, c, dt))
+    packed = orc.pack_nhwc(x, n, h, w, c, dt)
+    assert np.array_equal(conv.unpack_nhwc(packed, n, h, w, c, conv.DType(dt)),
+                          orc.unpack_nhwc(packed, n, h, w, c, dt))
+    for cout, cin, kh, kw in [(10, 6, 3, 3), (160, 960, 1, 1), (32, 3, 3, 3), (5, 7, 2, 1)]:
+        wt = orc.xs32_fill(2, cout * cin * kh * kw)
+        a, ka = conv.pack_weights_conv(wt, cout, cin, kh, kw, 4, conv.DType(dt))
+        b, kb = orc.pack_weights_conv(wt, cout, cin, kh, kw, 4, dt)
+        assert ka == kb and np.array_equal(a, b)
+    wd = orc.xs32_fill(3, 13 * 9)
+    assert np.array_equal(conv.pack_weights_dw(wd, 13, 3, 3, conv.DType(dt)), orc.pack_weights_dw(wd, 13, 3, 3, dt))
+    b = orc.xs32_fill(4, 13)
+    assert np.array_equal(conv.pack_bias(b, 13, conv.DType(dt)), orc.pack_bias(b, 13, dt))
+
+
+def pw_plan(n, m, cin, cout, dt=0, splitk=0, variant=0):
+    return conv.GemmPwSpec(m=m, kg=-(-cin // 4), ng=-(-cout // 4), dt=conv.DType(dt), n=n, splitk=splitk,
+                           variant=conv.Variant(variant)).plan()
+
+
+def test_pw_policy_splits_small_m_large_k():
+    # skinny 960 -> 160 at 10x18: 2 pixel tiles cannot fill 256 CUs -> split-K
+    p = pw_plan(1, 180, 960, 160)
+    assert p.variant == conv.Variant.SPLITK and p.splitk > 1
+    assert p.ws_bytes == p.splitk * 180 * 160 * 4
+    # same layer at batch 256: 360 tiles -> one tile per workgroup over the whole K
+    p = pw_plan(256, 180, 960, 160)
+    assert p.variant == conv.Variant.TILE and p.splitk == 1 and p.ws_bytes == 0
+    assert p.bn == 160 and p.grid == 360
+    # 1x1 32 -> 64 at 80x144: K is one stage, nothing to split
+    p = pw_plan(1, 11520, 32, 64)
+    assert p.variant == conv.Variant.TILE and p.bn == 64 and p.grid == 90
+
+
+def test_pw_policy_agrees_with_reference_on_its_splitk_kats(orc):
+    # wherever the reference splits K (Splitk) or reduces K across a workgroup
+    # (Gemv) on its own KAT shapes (gemm_pw.rs:337-354), the MI355X policy
+    # splits K as well; where it picks Small/Tiled with a short K, it does not
+    for m, kg, ng in [(144, 240, 40), (144, 40, 240), (144, 168, 28), (576, 30, 10), (2304, 18, 6), (1, 144, 36)]:
+        assert orc.ref_pw_variant(m, kg, ng) in ("Splitk", "Gemv")
+        p = conv.GemmPwSpec(m=m, kg=kg, ng=ng).plan()
+        assert p.variant == conv.Variant.SPLITK, (m, kg, ng, p)
+    for m, kg, ng in [(36864, 6, 4), (36864, 1, 4), (512, 8, 8)]:
+        assert orc.ref_pw_variant(m, kg, ng) == "Small"
+        assert conv.GemmPwSpec(m=m, kg=kg, ng=ng).plan().variant == conv.Variant.TILE
+
+
+def test_forced_splitk_factor_is_honoured():
+    for s in (1, 4, 8):
+        p = pw_plan(1, 180, 960, 160, splitk=s)
+        assert p.splitk == s
+    p = pw_plan(1, 180, 960, 160, variant=conv.Variant.TILE)
+    assert p.splitk == 1
+
+
+def test_igemm_policy():
+    big = conv.ConvIgemmSpec(ih=160, iw=288, cin=16, cout=32, k=3, s=2, pad=(1, 1, 1, 1), n=32)
+    assert big.out_hw() == (80, 144)
+    p = big.plan()
+    assert p.variant == conv.Variant.TILE and p.bn == 32 and p.grid == 32 * 80 * 144 // 128
+    deep = conv.ConvIgemmSpec(ih=9, iw=16, cin=128, cout=128, k=3, pad=(1, 1, 1, 1))
+    assert deep.plan().variant == conv.Variant.SPLITK
+
+
+def _expect_error(fn, fragment):
+    with pytest.raises(conv.AihError) as e:
+        fn()
+    assert fragment in str(e.value)
+
+
+def test_invalid_descriptors_fail_cleanly():
+    L = conv.lib()
+    assert L.aih_conv_pw(None, None, None, None, None, None, None, 0, None) == -1
+    assert "null descriptor" in conv.last_error()
+    _expect_error(lambda: conv.GemmPwSpec(m=0, kg=1, ng=1).plan(), "must be > 0")
+    _expect_error(lambda: conv.GemmPwSpec(m=4, kg=2, ng=1, kg_pad=1).plan(), "kg_pad")
+    _expect_error(lambda: conv.GemmPwSpec(m=4, kg=2, ng=1, dt=conv.DType.F16, wdt=conv.DType.F32).plan(),
+                  "unsupported (dt, wdt)")
+    _expect_error(lambda: conv.GemmPwSpec(m=4, kg=2, ng=1, act=42).plan(), "activation")
+    # null buffers are rejected before anything reaches the device
+    _expect_error(lambda: conv.GemmPwSpec(m=4, kg=2, ng=1).run(None, None, None, None, None, stream=0), "null buffer")
+    _expect_error(lambda: conv.GemmPwSpec(m=4, kg=2, ng=1, residual=True).run(16, 16, 16, None, 16, stream=0),
+                  "res must be given")
+    # lower_op's rejections (lowering.rs:136-140, conv_igemm.rs:80-83)
+    op = conv.ConvOp(ih=8, iw=8, cin=4, cout=4, kh=1, kw=1, sh=2, sw=2)
+    _expect_error(lambda: op.run(16, 16, 16, None, 16, stream=0), "1x1 conv with stride/pad")
+    op = conv.ConvOp(ih=8, iw=8, cin=4, cout=4, kh=3, kw=1, pad=(1, 0, 1, 0))
+    _expect_error(lambda: op.run(16, 16, 16, None, 16, stream=0), "square kernels")
+    op = conv.ConvOp(ih=8, iw=8, cin=8, cout=16, kh=3, kw=3, groups=8)
+    _expect_error(lambda: op.run(16, 16, 16, None, 16, stream=0), "depthwise")
+    ig = conv.ConvIgemmSpec(ih=8, iw=8, cin=12, cout=8, k=3, pad=(1, 1, 1, 1),
+                            srcs=[conv.SrcView(c=6), conv.SrcView(c=6)])
+    _expect_error(lambda: ig.plan(), "only the last part")
+    ig = conv.ConvIgemmSpec(ih=8, iw=8, cin=12, cout=8, k=3, pad=(1, 1, 1, 1),
+                            srcs=[conv.SrcView(c=8), conv.SrcView(c=8)])
+    _expect_error(lambda: ig.plan(), "do not add up")
+    ig = conv.ConvIgemmSpec(ih=2, iw=2, cin=4, cout=4, k=5)
+    _expect_error(lambda: ig.plan(), "larger than the padded input")
+    # split-K without a workspace is an error, not a crash
+    d = conv.GemmPwSpec(m=180, kg=240, ng=40, splitk=4).desc()
+    assert L.aih_conv_pw(C.byref(d), 16, 16, 16, None, 16, None, 0, None) == -1
+    assert "workspace" in conv.last_error()

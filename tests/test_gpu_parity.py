@@ -1,0 +1,215 @@
+"""GPU parity grid through the C ABI: the HIP kernels against the oracle.
+
+Mirrors the reference's shared GPU testsuite (crates/ai-gpu/src/testsuite.rs):
+the same (h, w, cin, cout) shapes, activations, seeds and XorShift32 stream
+order for run_gemm_pw (:373-414), run_conv_dw (:466-496) and run_conv_igemm
+(:722-786), with bf16 added next to every f16 case. Expected values come from
+the oracle's restatement of reference::conv::conv2d on the unrounded fp32
+inputs. Bars: the reference's compare (atol/rtol 1e-4 f32, 1e-2 f16,
+testsuite.rs:21-24) and BASELINE's max |gpu-cpu|/max(|cpu|,1) <= 1e-4 (f32),
+<= 2e-2 (16-bit). Every output buffer starts as NaN.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():  # pragma: no cover - the gpu marker keeps these off CPU runs
+    pytest.skip("no GPU", allow_module_level=True)
+
+from tests import gpu_util as G  # noqa: E402
+
+F32, F16, BF16 = 0, 1, 2
+TOL = {F32: (1e-4, 1e-4, 1e-4), F16: (1e-2, 1e-2, 2e-2), BF16: (1e-2, 1e-2, 2e-2)}
+
+
+def check(name, got, want, dt, ts_tol=None):
+    atol, rtol, bar = TOL[dt]
+    if ts_tol is not None:
+        atol, rtol = ts_tol
+    err = G.rel_err(got, want)
+    print(f"{name}: max_rel_err={err:.3e}", flush=True)
+    assert err <= bar, f"{name}: {err}"
+    assert G.testsuite_ok(got, want, atol, rtol), f"{name}: testsuite compare failed"
+
+
+# ---------------------------------------------------------------- pointwise (testsuite.rs:373-414)
+
+PW_SHAPES = [(1, 1, 64, 16), (9, 16, 128, 24), (3, 5, 6, 10), (72, 128, 16, 64), (24, 32, 6, 10),
+             (23, 33, 8, 20), (9, 16, 960, 160), (9, 16, 240, 68), (11, 13, 72, 68)]
+PW_ACTS = ["none", "relu", "hardswish", "sigmoid"]
+PW_CASES = []
+_seed = 2000
+for _shape in PW_SHAPES:
+    for _act in PW_ACTS:
+        _seed += 1
+        PW_CASES.append((_shape, _act, _seed))
+
+
+@pytest.mark.parametrize("shape,act,seed", PW_CASES, ids=lambda v: str(v))
+def test_pw_f32(shape, act, seed):
+    h, w, cin, cout = shape
+    got, want, plan = G.run_pw(h, w, cin, cout, act, False, F32, seed)
+    check(f"pw {shape} {act} {plan}", got, want, F32)
+
+
+@pytest.mark.parametrize("case", [((9, 16, 32, 32), "relu", 3001), ((9, 16, 960, 160), "relu", 3003),
+                                  ((72, 128, 16, 16), "hardswish", 3002)], ids=str)
+def test_pw_residual_f32(case):
+    (h, w, cin, cout), act, seed = case
+    got, want, _ = G.run_pw(h, w, cin, cout, act, True, F32, seed)
+    check(f"pw res {case}", got, want, F32)
+
+
+PW16 = [((72, 128, 16, 64), "relu", False, 3101), ((9, 16, 128, 24), "hardswish", False, 3102),
+        ((24, 32, 16, 16), "relu", True, 3103), ((9, 16, 960, 160), "none", False, 3104)]
+
+
+@pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("case", PW16, ids=str)
+def test_pw_16bit(case, dt):
+    (h, w, cin, cout), act, res, seed = case
+    got, want, _ = G.run_pw(h, w, cin, cout, act, res, dt, seed)
+    check(f"pw dt{dt} {case}", got, want, dt, ts_tol=(1e-2, 1e-2) if dt == F16 else (4e-2, 1e-2))
+
+
+@pytest.mark.parametrize("wdt", [F16, BF16], ids=["w_f16", "w_bf16"])
+def test_pw_f32_act_16bit_weights(wdt):
+    # dt_weights axis (format/model.rs:245-254): f32 activations, 16-bit weights
+    got, want, _ = G.run_pw(9, 16, 240, 68, "relu", True, F32, 3201, wdt=wdt)
+    check(f"pw f32/w{wdt}", got, want, F16)
+
+
+@pytest.mark.parametrize("splitk", [1, 4, 8])
+@pytest.mark.parametrize("n", [1, 3])
+def test_pw_splitk_factors(splitk, n):
+    # the skinny 960 -> 160 layer at 10x18 with split-K forced to 1 / 4 / 8
+    got, want, plan = G.run_pw(10, 18, 960, 160, "none", False, F32, 3300 + splitk, n=n, splitk=splitk)
+    assert plan.splitk == splitk
+    check(f"pw splitk={splitk} n={n}", got, want, F32)
+
+
+def test_pw_splitk_is_deterministic():
+    a, _, _ = G.run_pw(9, 16, 960, 160, "relu", True, F32, 3401, splitk=8)
+    b, _, _ = G.run_pw(9, 16, 960, 160, "relu", True, F32, 3401, splitk=8)
+    assert np.array_equal(a, b)
+
+
+def test_pw_tail_tiles():
+    # M not a multiple of the 128-pixel tile, N4 not a multiple of any channel tile
+    got, want, _ = G.run_pw(7, 37, 44, 300, "relu6", True, F32, 3501)
+    check("pw tails", got, want, F32)
+
+
+# ---------------------------------------------------------------- depthwise (testsuite.rs:466-496)
+
+DW_SHAPES = [(72, 128, 64, 3, 1), (36, 64, 96, 5, 2), (33, 17, 6, 3, 2), (16, 16, 10, 5, 1)]
+DW_CASES = []
+_seed = 4000
+for _shape in DW_SHAPES:
+    for _act in ["none", "relu", "hardswish"]:
+        _seed += 1
+        DW_CASES.append((_shape, _act, _seed))
+
+
+@pytest.mark.parametrize("shape,act,seed", DW_CASES, ids=lambda v: str(v))
+def test_dw_f32(shape, act, seed):
+    ih, iw, c, k, s = shape
+    got, want = G.run_dw(ih, iw, c, k, s, act, False, F32, seed)
+    check(f"dw {shape} {act}", got, want, F32)
+
+
+def test_dw_residual_and_dilation():
+    got, want = G.run_dw(36, 64, 32, 3, 1, "relu", True, F32, 5001)
+    check("dw res", got, want, F32)
+    got, want = G.run_dw(18, 32, 40, 3, 1, "relu", False, F32, 5201, pad=[2] * 4, d=2)
+    check("dw d2", got, want, F32)
+
+
+@pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
+def test_dw_16bit(dt):
+    got, want = G.run_dw(72, 128, 64, 3, 1, "relu", False, dt, 5101)
+    check("dw16 a", got, want, dt, ts_tol=(1e-2, 1e-2) if dt == F16 else (2e-2, 1e-2))
+    got, want = G.run_dw(36, 64, 96, 5, 2, "none", False, dt, 5102)
+    check("dw16 b", got, want, dt, ts_tol=(1e-2, 1e-2) if dt == F16 else (2e-2, 1e-2))
+
+
+def test_dw_batch():
+    got, want = G.run_dw(20, 36, 64, 3, 2, "relu", True, F32, 5301, n=3)
+    check("dw batch", got, want, F32)
+
+
+# ---------------------------------------------------------------- implicit GEMM (testsuite.rs:722-786)
+
+IG_SHAPES = [(36, 64, 3, 16, 3, 2), (24, 32, 16, 24, 3, 1), (40, 64, 20, 32, 3, 1), (17, 23, 6, 8, 3, 2),
+             (33, 45, 8, 12, 5, 2), (9, 16, 128, 128, 3, 1), (18, 32, 171, 80, 3, 1)]
+IG_CASES = []
+_seed = 6000
+for _shape in IG_SHAPES:
+    for _act in ["none", "relu", "hardswish"]:
+        _seed += 1
+        IG_CASES.append((_shape, _act, _seed))
+
+
+@pytest.mark.parametrize("shape,act,seed", IG_CASES, ids=lambda v: str(v))
+def test_igemm_f32(shape, act, seed):
+    ih, iw, cin, cout, k, s = shape
+    p = (k - 1) // 2
+    got, want, plan = G.run_igemm(ih, iw, cin, cout, k, s, [p] * 4, act, False, F32, seed)
+    check(f"igemm {shape} {act} {plan}", got, want, F32)
+
+
+IG_EXTRA = [
+    # (ih, iw, cin, cout, k, s, pad, act, residual, seed) -- testsuite.rs:745-770
+    (16, 16, 4, 8, 3, 1, [1, 0, 0, 1], "relu", False, 7001),
+    (128, 128, 3, 16, 3, 2, [0, 0, 1, 1], "none", False, 7008),
+    (32, 32, 3, 16, 3, 2, [0, 0, 1, 1], "none", False, 7005),
+    (32, 32, 3, 24, 5, 2, [1, 1, 2, 2], "none", False, 7006),
+    (24, 24, 16, 16, 3, 2, [0, 0, 1, 1], "relu", False, 7007),
+    (24, 32, 16, 16, 3, 1, [1, 1, 1, 1], "hardswish", True, 7002),
+    (9, 16, 8, 8, 3, 1, [1, 1, 1, 1], "none", True, 7003),
+    (9, 16, 128, 128, 3, 1, [1, 1, 1, 1], "relu", True, 7004),
+]
+
+
+@pytest.mark.parametrize("case", IG_EXTRA, ids=lambda c: str(c[-1]))
+def test_igemm_pads_and_residual(case):
+    ih, iw, cin, cout, k, s, pad, act, res, seed = case
+    got, want, _ = G.run_igemm(ih, iw, cin, cout, k, s, pad, act, res, F32, seed)
+    check(f"igemm {case}", got, want, F32)
+
+
+@pytest.mark.parametrize("case", [((24, 32), [16, 16], 24, "relu", False, 7101),
+                                  ((36, 64), [80, 24, 3], 40, "hardswish", False, 7102),
+                                  ((9, 16), [64, 64], 128, "relu", True, 7103)], ids=lambda c: str(c[-1]))
+def test_igemm_concat_parts(case):
+    (ih, iw), parts, cout, act, res, seed = case
+    got, want, _ = G.run_igemm(ih, iw, sum(parts), cout, 3, 1, [1] * 4, act, res, F32, seed, parts=parts)
+    check(f"igemm concat {case}", got, want, F32)
+
+
+def test_igemm_dilated():
+    got, want, _ = G.run_igemm(24, 32, 8, 12, 3, 1, [2] * 4, "hardswish", False, F32, 5202, d=2)
+    check("igemm d2", got, want, F32)
+
+
+@pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("case", [(24, 32, 16, 24, 3, 1, "relu", 7201), (36, 64, 3, 16, 3, 2, "none", 7202),
+                                  (18, 32, 171, 80, 3, 1, "relu", 7203)], ids=lambda c: str(c[-1]))
+def test_igemm_16bit(case, dt):
+    ih, iw, cin, cout, k, s, act, seed = case
+    got, want, _ = G.run_igemm(ih, iw, cin, cout, k, s, [1] * 4, act, False, dt, seed)
+    check(f"igemm dt{dt} {case}", got, want, dt, ts_tol=(1e-2, 1e-2) if dt == F16 else (4e-2, 1e-2))
+
+
+@pytest.mark.parametrize("splitk", [2, 4])
+def test_igemm_splitk(splitk):
+    got, want, plan = G.run_igemm(9, 16, 128, 128, 3, 1, [1] * 4, "relu", True, F32, 7301, splitk=splitk)
+    assert plan.splitk == splitk
+    check(f"igemm splitk {splitk}", got, want, F32)
+
+
+def test_igemm_batch():
+    got, want, _ = G.run_igemm(20, 36, 16, 32, 3, 2, [1] * 4, "relu", True, F32, 7401, n=3)
+    check("igemm batch", got, want, F32)
