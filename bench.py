@@ -1,7 +1,7 @@
 """Benchmark of the MI355X conv-as-GEMM backend (one GPU).
 
 Headline workload (value, frames/s): the MobileNetV4-small-width segmentation
-encoder at 160x288, batch 64, bf16 storage with fp32 accumulation -- 32 convs
+encoder at 160x288, batch 64, f16 storage with fp32 accumulation -- 32 convs
 (stem 3x3 s2 3->32, ten inverted-residual blocks, 1x1 head 128->2) with
 random He-init weights and U[-1,1) synthetic input already resident in HBM.
 One step = pack the fp32 NHWC input to NHWC-C4 on the device + all 32 convs.
@@ -15,7 +15,7 @@ t_roof = max(flops / MFMA peak, bytes / 8 TB/s)):
   igemm3x3s2_16to32_relu_160x288_b32 3x3 s2 pad 1 16->32 + ReLU, [32,160,288,16] fp32
   igemm3x3s1_32to64_relu_80x144_b32  3x3 s1 pad 1 32->64 + ReLU, [32,80,144,32] fp32
   ir_block_chain_4x_64c_40x72_b64    4 inverted-residual blocks at [64,40,72,64] fp32
-  encoder_f16                        the headline workload with f16 storage
+  encoder_bf16                       the headline workload with bf16 storage
 Small configurations are timed over rotated buffer sets larger than the 256 MB
 Infinity Cache, so their GB/s are HBM figures.
 
@@ -63,7 +63,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--dtype", default="bf16", choices=["bf16", "f16"])
+    ap.add_argument("--dtype", default="f16", choices=["bf16", "f16"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-config kernel table")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)

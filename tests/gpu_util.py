@@ -67,8 +67,32 @@ ACT = {"none": conv.Activation.NONE, "relu": conv.Activation.RELU, "hardswish": 
        "sigmoid": conv.Activation.SIGMOID, "relu6": conv.Activation.RELU6}
 
 
+def rounded_ref(op, ih, iw, x, wts, b, r, dt, wdt, n=1):
+    """fp32 reference on the inputs as stored in dt / wdt: separates the
+    kernel's own error from the storage dtype's input quantisation."""
+    return orc.conv2d_ref(op, ih, iw, orc.round_to(x, dt), orc.round_to(wts, wdt), orc.round_to(b, dt),
+                          None if r is None else orc.round_to(r, dt), n=n)
+
+
+def magnitude(op, ih, iw, x, wts, b, r, n=1):
+    """sum |x||w| + |b| (+ |res|) per output: the scale of every rounding error
+    that storing the inputs in a 16-bit dtype can introduce."""
+    aop = orc.Conv2d.from_buffer_copy(op)
+    aop.act = 0
+    m = orc.conv2d_ref(aop, ih, iw, np.abs(x), np.abs(wts), np.abs(b), None, n=n)
+    return m + (np.abs(r) if r is not None else 0.0)
+
+
+class Result:
+    def __init__(self, got, want, plan=None, want_r=None, mag=None):
+        self.got, self.want, self.plan, self.want_r, self.mag = got, want, plan, want_r, mag
+
+    def __iter__(self):  # (got, want, plan) unpacking
+        return iter((self.got, self.want, self.plan))
+
+
 def run_pw(h, w, cin, cout, act, residual, dt, seed, wdt=None, n=1, splitk=0, variant=0, xs=None):
-    """pw_case (testsuite.rs:325-371): returns (got, want, plan)."""
+    """pw_case (testsuite.rs:325-371): returns Result(got, want, plan, want_r)."""
     wdt = dt if wdt is None else wdt
     if xs is None:
         x, wts, b, r = stream(seed, n * h * w * cin, cout * cin, cout, n * h * w * cout if residual else 0)
@@ -90,12 +114,15 @@ def run_pw(h, w, cin, cout, act, residual, dt, seed, wdt=None, n=1, splitk=0, va
     spec.run(xd, wd, bd, rd, yd)
     torch.cuda.synchronize()
     got = orc.unpack_nhwc(host(yd, dt), n, h, w, cout, dt)
-    return got, want, plan
+    rr = r if residual else None
+    want_r = rounded_ref(op, h, w, x, wts, b, rr, dt, wdt, n) if (dt or wdt) else want
+    mag = magnitude(op, h, w, x, wts, b, rr, n) if (dt or wdt) else None
+    return Result(got, want, plan, want_r, mag)
 
 
 def run_igemm(ih, iw, cin, cout, k, s, pad, act, residual, dt, seed, wdt=None, n=1, d=1, splitk=0, variant=0,
               parts=None):
-    """igemm_case / igemm_concat_case (testsuite.rs:588-720): returns (got, want, plan)."""
+    """igemm_case / igemm_concat_case (testsuite.rs:588-720): returns Result."""
     wdt = dt if wdt is None else wdt
     op = orc.conv2d(cin, cout, k=k, s=s, pad=list(pad), dil=d, act=act)
     oh, ow = orc.out_hw(op, ih, iw)
@@ -126,11 +153,14 @@ def run_igemm(ih, iw, cin, cout, k, s, pad, act, residual, dt, seed, wdt=None, n
     spec.run(inputs, wd, bd, rd, yd)
     torch.cuda.synchronize()
     got = orc.unpack_nhwc(host(yd, dt), n, oh, ow, cout, dt)
-    return got, want, plan
+    rr = r if residual else None
+    want_r = rounded_ref(op, ih, iw, xin, wts, b, rr, dt, wdt, n) if (dt or wdt) else want
+    mag = magnitude(op, ih, iw, xin, wts, b, rr, n) if (dt or wdt) else None
+    return Result(got, want, plan, want_r, mag)
 
 
 def run_dw(ih, iw, c, k, s, act, residual, dt, seed, pad=None, d=1, n=1):
-    """dw_case (testsuite.rs:416-464): returns (got, want)."""
+    """dw_case (testsuite.rs:416-464): returns Result."""
     if pad is None:
         pad = [(k - 1) // 2] * 4
     op = orc.conv2d(c, c, k=k, s=s, pad=list(pad), dil=d, groups=c, act=act)
@@ -147,4 +177,7 @@ def run_dw(ih, iw, c, k, s, act, residual, dt, seed, pad=None, d=1, n=1):
     spec.run(xd, wd, bd, rd, yd)
     torch.cuda.synchronize()
     got = orc.unpack_nhwc(host(yd, dt), n, oh, ow, c, dt)
-    return got, want
+    rr = r if residual else None
+    want_r = rounded_ref(op, ih, iw, x, wts, b, rr, dt, dt, n) if dt else want
+    mag = magnitude(op, ih, iw, x, wts, b, rr, n) if dt else None
+    return Result(got, want, None, want_r, mag)

@@ -6,8 +6,17 @@ order for run_gemm_pw (:373-414), run_conv_dw (:466-496) and run_conv_igemm
 (:722-786), with bf16 added next to every f16 case. Expected values come from
 the oracle's restatement of reference::conv::conv2d on the unrounded fp32
 inputs. Bars: the reference's compare (atol/rtol 1e-4 f32, 1e-2 f16,
-testsuite.rs:21-24) and BASELINE's max |gpu-cpu|/max(|cpu|,1) <= 1e-4 (f32),
-<= 2e-2 (16-bit). Every output buffer starts as NaN.
+testsuite.rs:21-24) and max |gpu-cpu|/max(|cpu|,1) <= 1e-4 for fp32.
+16-bit storage is checked three ways: against the fp32 reference on the
+inputs as stored (the kernel's own error: <= 2e-3 f16, <= 8e-3 bf16, a few
+output roundings -- this is the check a wrong index or a lost term fails);
+element-wise against the unrounded fp32 reference within the error that
+storing the inputs can cause, |gpu - ref| <= 3.1 u sum|x||w| + 2 u |ref| with
+u the dtype's unit roundoff (2^-11 f16, 2^-9 bf16); and, for f16, with the
+reference's own 1e-2 compare. (bf16 has no reference counterpart; its 8-bit
+mantissa puts the unrounded error of these U[-1,1]-weight shapes near 1e-1 at
+K = 960, so the 2e-2 bar is applied to the He-init workloads of
+test_gpu_workloads instead.) Every output buffer starts as NaN.
 """
 import numpy as np
 import pytest
@@ -21,17 +30,23 @@ if not torch.cuda.is_available():  # pragma: no cover - the gpu marker keeps the
 from tests import gpu_util as G  # noqa: E402
 
 F32, F16, BF16 = 0, 1, 2
-TOL = {F32: (1e-4, 1e-4, 1e-4), F16: (1e-2, 1e-2, 2e-2), BF16: (1e-2, 1e-2, 2e-2)}
+# dt: (testsuite atol, rtol, bar vs fp32 on stored inputs, unit roundoff)
+TOL = {F32: (1e-4, 1e-4, 1e-4, 0.0), F16: (1e-2, 1e-2, 2e-3, 2.0 ** -11), BF16: (None, None, 8e-3, 2.0 ** -9)}
 
 
-def check(name, got, want, dt, ts_tol=None):
-    atol, rtol, bar = TOL[dt]
-    if ts_tol is not None:
-        atol, rtol = ts_tol
-    err = G.rel_err(got, want)
-    print(f"{name}: max_rel_err={err:.3e}", flush=True)
-    assert err <= bar, f"{name}: {err}"
-    assert G.testsuite_ok(got, want, atol, rtol), f"{name}: testsuite compare failed"
+def check(name, res, dt):
+    atol, rtol, bar_r, u = TOL[dt]
+    err = G.rel_err(res.got, res.want)
+    err_r = G.rel_err(res.got, res.want_r) if res.want_r is not None else err
+    print(f"{name}: max_rel_err={err:.3e} vs_stored_inputs={err_r:.3e}", flush=True)
+    assert err_r <= bar_r, f"{name}: vs stored inputs {err_r}"
+    if dt == F32:
+        assert err <= 1e-4, f"{name}: {err}"
+    else:
+        bound = 3.1 * u * res.mag + 2 * u * np.abs(res.want) + 1e-6
+        assert np.all(np.abs(res.got - res.want) <= bound), f"{name}: exceeds the storage-rounding bound"
+    if atol is not None:
+        assert G.testsuite_ok(res.got, res.want, atol, rtol), f"{name}: testsuite compare failed"
 
 
 # ---------------------------------------------------------------- pointwise (testsuite.rs:373-414)
@@ -50,16 +65,16 @@ for _shape in PW_SHAPES:
 @pytest.mark.parametrize("shape,act,seed", PW_CASES, ids=lambda v: str(v))
 def test_pw_f32(shape, act, seed):
     h, w, cin, cout = shape
-    got, want, plan = G.run_pw(h, w, cin, cout, act, False, F32, seed)
-    check(f"pw {shape} {act} {plan}", got, want, F32)
+    res = G.run_pw(h, w, cin, cout, act, False, F32, seed)
+    check(f"pw {shape} {act} {res.plan}", res, F32)
 
 
 @pytest.mark.parametrize("case", [((9, 16, 32, 32), "relu", 3001), ((9, 16, 960, 160), "relu", 3003),
                                   ((72, 128, 16, 16), "hardswish", 3002)], ids=str)
 def test_pw_residual_f32(case):
     (h, w, cin, cout), act, seed = case
-    got, want, _ = G.run_pw(h, w, cin, cout, act, True, F32, seed)
-    check(f"pw res {case}", got, want, F32)
+    res = G.run_pw(h, w, cin, cout, act, True, F32, seed)
+    check(f"pw res {case}", res, F32)
 
 
 PW16 = [((72, 128, 16, 64), "relu", False, 3101), ((9, 16, 128, 24), "hardswish", False, 3102),
@@ -69,37 +84,38 @@ PW16 = [((72, 128, 16, 64), "relu", False, 3101), ((9, 16, 128, 24), "hardswish"
 @pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
 @pytest.mark.parametrize("case", PW16, ids=str)
 def test_pw_16bit(case, dt):
-    (h, w, cin, cout), act, res, seed = case
-    got, want, _ = G.run_pw(h, w, cin, cout, act, res, dt, seed)
-    check(f"pw dt{dt} {case}", got, want, dt, ts_tol=(1e-2, 1e-2) if dt == F16 else (4e-2, 1e-2))
+    (h, w, cin, cout), act, with_res, seed = case
+    res = G.run_pw(h, w, cin, cout, act, with_res, dt, seed)
+    check(f"pw dt{dt} {case}", res, dt)
 
 
 @pytest.mark.parametrize("wdt", [F16, BF16], ids=["w_f16", "w_bf16"])
 def test_pw_f32_act_16bit_weights(wdt):
     # dt_weights axis (format/model.rs:245-254): f32 activations, 16-bit weights
-    got, want, _ = G.run_pw(9, 16, 240, 68, "relu", True, F32, 3201, wdt=wdt)
-    check(f"pw f32/w{wdt}", got, want, F16)
+    res = G.run_pw(9, 16, 240, 68, "relu", True, F32, 3201, wdt=wdt)
+    check(f"pw f32/w{wdt}", res, wdt)
+    assert G.rel_err(res.got, res.want_r) <= 1e-4  # activations stay fp32: only the weights were rounded
 
 
 @pytest.mark.parametrize("splitk", [1, 4, 8])
 @pytest.mark.parametrize("n", [1, 3])
 def test_pw_splitk_factors(splitk, n):
     # the skinny 960 -> 160 layer at 10x18 with split-K forced to 1 / 4 / 8
-    got, want, plan = G.run_pw(10, 18, 960, 160, "none", False, F32, 3300 + splitk, n=n, splitk=splitk)
-    assert plan.splitk == splitk
-    check(f"pw splitk={splitk} n={n}", got, want, F32)
+    res = G.run_pw(10, 18, 960, 160, "none", False, F32, 3300 + splitk, n=n, splitk=splitk)
+    assert res.plan.splitk == splitk
+    check(f"pw splitk={splitk} n={n}", res, F32)
 
 
 def test_pw_splitk_is_deterministic():
-    a, _, _ = G.run_pw(9, 16, 960, 160, "relu", True, F32, 3401, splitk=8)
-    b, _, _ = G.run_pw(9, 16, 960, 160, "relu", True, F32, 3401, splitk=8)
+    a = G.run_pw(9, 16, 960, 160, "relu", True, F32, 3401, splitk=8).got
+    b = G.run_pw(9, 16, 960, 160, "relu", True, F32, 3401, splitk=8).got
     assert np.array_equal(a, b)
 
 
 def test_pw_tail_tiles():
     # M not a multiple of the 128-pixel tile, N4 not a multiple of any channel tile
-    got, want, _ = G.run_pw(7, 37, 44, 300, "relu6", True, F32, 3501)
-    check("pw tails", got, want, F32)
+    res = G.run_pw(7, 37, 44, 300, "relu6", True, F32, 3501)
+    check("pw tails", res, F32)
 
 
 # ---------------------------------------------------------------- depthwise (testsuite.rs:466-496)
@@ -116,28 +132,28 @@ for _shape in DW_SHAPES:
 @pytest.mark.parametrize("shape,act,seed", DW_CASES, ids=lambda v: str(v))
 def test_dw_f32(shape, act, seed):
     ih, iw, c, k, s = shape
-    got, want = G.run_dw(ih, iw, c, k, s, act, False, F32, seed)
-    check(f"dw {shape} {act}", got, want, F32)
+    res = G.run_dw(ih, iw, c, k, s, act, False, F32, seed)
+    check(f"dw {shape} {act}", res, F32)
 
 
 def test_dw_residual_and_dilation():
-    got, want = G.run_dw(36, 64, 32, 3, 1, "relu", True, F32, 5001)
-    check("dw res", got, want, F32)
-    got, want = G.run_dw(18, 32, 40, 3, 1, "relu", False, F32, 5201, pad=[2] * 4, d=2)
-    check("dw d2", got, want, F32)
+    res = G.run_dw(36, 64, 32, 3, 1, "relu", True, F32, 5001)
+    check("dw res", res, F32)
+    res = G.run_dw(18, 32, 40, 3, 1, "relu", False, F32, 5201, pad=[2] * 4, d=2)
+    check("dw d2", res, F32)
 
 
 @pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
 def test_dw_16bit(dt):
-    got, want = G.run_dw(72, 128, 64, 3, 1, "relu", False, dt, 5101)
-    check("dw16 a", got, want, dt, ts_tol=(1e-2, 1e-2) if dt == F16 else (2e-2, 1e-2))
-    got, want = G.run_dw(36, 64, 96, 5, 2, "none", False, dt, 5102)
-    check("dw16 b", got, want, dt, ts_tol=(1e-2, 1e-2) if dt == F16 else (2e-2, 1e-2))
+    res = G.run_dw(72, 128, 64, 3, 1, "relu", False, dt, 5101)
+    check("dw16 a", res, dt)
+    res = G.run_dw(36, 64, 96, 5, 2, "none", False, dt, 5102)
+    check("dw16 b", res, dt)
 
 
 def test_dw_batch():
-    got, want = G.run_dw(20, 36, 64, 3, 2, "relu", True, F32, 5301, n=3)
-    check("dw batch", got, want, F32)
+    res = G.run_dw(20, 36, 64, 3, 2, "relu", True, F32, 5301, n=3)
+    check("dw batch", res, F32)
 
 
 # ---------------------------------------------------------------- implicit GEMM (testsuite.rs:722-786)
@@ -156,8 +172,8 @@ for _shape in IG_SHAPES:
 def test_igemm_f32(shape, act, seed):
     ih, iw, cin, cout, k, s = shape
     p = (k - 1) // 2
-    got, want, plan = G.run_igemm(ih, iw, cin, cout, k, s, [p] * 4, act, False, F32, seed)
-    check(f"igemm {shape} {act} {plan}", got, want, F32)
+    res = G.run_igemm(ih, iw, cin, cout, k, s, [p] * 4, act, False, F32, seed)
+    check(f"igemm {shape} {act} {res.plan}", res, F32)
 
 
 IG_EXTRA = [
@@ -175,23 +191,23 @@ IG_EXTRA = [
 
 @pytest.mark.parametrize("case", IG_EXTRA, ids=lambda c: str(c[-1]))
 def test_igemm_pads_and_residual(case):
-    ih, iw, cin, cout, k, s, pad, act, res, seed = case
-    got, want, _ = G.run_igemm(ih, iw, cin, cout, k, s, pad, act, res, F32, seed)
-    check(f"igemm {case}", got, want, F32)
+    ih, iw, cin, cout, k, s, pad, act, with_res, seed = case
+    res = G.run_igemm(ih, iw, cin, cout, k, s, pad, act, with_res, F32, seed)
+    check(f"igemm {case}", res, F32)
 
 
 @pytest.mark.parametrize("case", [((24, 32), [16, 16], 24, "relu", False, 7101),
                                   ((36, 64), [80, 24, 3], 40, "hardswish", False, 7102),
                                   ((9, 16), [64, 64], 128, "relu", True, 7103)], ids=lambda c: str(c[-1]))
 def test_igemm_concat_parts(case):
-    (ih, iw), parts, cout, act, res, seed = case
-    got, want, _ = G.run_igemm(ih, iw, sum(parts), cout, 3, 1, [1] * 4, act, res, F32, seed, parts=parts)
-    check(f"igemm concat {case}", got, want, F32)
+    (ih, iw), parts, cout, act, with_res, seed = case
+    res = G.run_igemm(ih, iw, sum(parts), cout, 3, 1, [1] * 4, act, with_res, F32, seed, parts=parts)
+    check(f"igemm concat {case}", res, F32)
 
 
 def test_igemm_dilated():
-    got, want, _ = G.run_igemm(24, 32, 8, 12, 3, 1, [2] * 4, "hardswish", False, F32, 5202, d=2)
-    check("igemm d2", got, want, F32)
+    res = G.run_igemm(24, 32, 8, 12, 3, 1, [2] * 4, "hardswish", False, F32, 5202, d=2)
+    check("igemm d2", res, F32)
 
 
 @pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
@@ -199,17 +215,17 @@ def test_igemm_dilated():
                                   (18, 32, 171, 80, 3, 1, "relu", 7203)], ids=lambda c: str(c[-1]))
 def test_igemm_16bit(case, dt):
     ih, iw, cin, cout, k, s, act, seed = case
-    got, want, _ = G.run_igemm(ih, iw, cin, cout, k, s, [1] * 4, act, False, dt, seed)
-    check(f"igemm dt{dt} {case}", got, want, dt, ts_tol=(1e-2, 1e-2) if dt == F16 else (4e-2, 1e-2))
+    res = G.run_igemm(ih, iw, cin, cout, k, s, [1] * 4, act, False, dt, seed)
+    check(f"igemm dt{dt} {case}", res, dt)
 
 
 @pytest.mark.parametrize("splitk", [2, 4])
 def test_igemm_splitk(splitk):
-    got, want, plan = G.run_igemm(9, 16, 128, 128, 3, 1, [1] * 4, "relu", True, F32, 7301, splitk=splitk)
-    assert plan.splitk == splitk
-    check(f"igemm splitk {splitk}", got, want, F32)
+    res = G.run_igemm(9, 16, 128, 128, 3, 1, [1] * 4, "relu", True, F32, 7301, splitk=splitk)
+    assert res.plan.splitk == splitk
+    check(f"igemm splitk {splitk}", res, F32)
 
 
 def test_igemm_batch():
-    got, want, _ = G.run_igemm(20, 36, 16, 32, 3, 2, [1] * 4, "relu", True, F32, 7401, n=3)
-    check("igemm batch", got, want, F32)
+    res = G.run_igemm(20, 36, 16, 32, 3, 2, [1] * 4, "relu", True, F32, 7401, n=3)
+    check("igemm batch", res, F32)
