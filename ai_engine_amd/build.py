@@ -23,9 +23,14 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 # Packed-FP32 instructions are disabled for all device code: hipcc would
 # otherwise emit v_pk_{add,mul,fma}_f32 from ordinary float code.
+# The VGPR form of MFMA keeps the loop-carried accumulators of the pipelined
+# conv-GEMM in arch VGPRs: with the AGPR form the compiler holds them in both
+# register files and copies between them around every MFMA group (BN=128:
+# 256 VGPR + 64 AGPR, one wave per SIMD, instead of 164 VGPR, three waves).
 DEVICE_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -50,6 +50,25 @@ __device__ __forceinline__ uint32_t f32_to_f16(float f) {
   return b;
 }
 
+// Register-level conversions of 4 packed 16-bit values (one 8-byte vec4).
+template <int DT>
+__device__ __forceinline__ f32x4 unpack4(u32x2 r) {
+  if constexpr (DT == DT_F16)
+    return f32x4{f16_to_f32(r.x & 0xffffu), f16_to_f32(r.x >> 16), f16_to_f32(r.y & 0xffffu),
+                 f16_to_f32(r.y >> 16)};
+  else
+    return f32x4{bf16_to_f32(r.x & 0xffffu), bf16_to_f32(r.x >> 16), bf16_to_f32(r.y & 0xffffu),
+                 bf16_to_f32(r.y >> 16)};
+}
+
+template <int DT>
+__device__ __forceinline__ u32x2 pack4(f32x4 v) {
+  if constexpr (DT == DT_F16)
+    return u32x2{f32_to_f16(v.x) | (f32_to_f16(v.y) << 16), f32_to_f16(v.z) | (f32_to_f16(v.w) << 16)};
+  else
+    return u32x2{f32_to_bf16(v.x) | (f32_to_bf16(v.y) << 16), f32_to_bf16(v.z) | (f32_to_bf16(v.w) << 16)};
+}
+
 // 4 consecutive channels (one vec4 of NHWC-C4) <-> fp32.
 template <int DT> struct Vec4IO;
 

@@ -54,12 +54,13 @@ size_t dsize(int32_t dt) { return dt == AIH_F32 ? 4 : 2; }
 // The reference's policy (gemm_pw.rs:91-102, conv_igemm.rs:201-233) splits K
 // when the tile grid cannot fill its 19-core GPU and K is long enough to be
 // worth cutting. Re-tuned for MI355X: 256 CUs, one 128-pixel MFMA tile per
-// workgroup; split when the tile grid covers fewer than 256 CUs and K spans at
-// least two stages, aiming at two workgroups per CU, at most 8 chunks, and at
-// least one full stage per chunk.
+// workgroup; split when the tile grid covers fewer than 256 CUs and K holds at
+// least 16 channel groups (the reference's own kg >= 16 gate), aiming at two
+// workgroups per CU, at most 8 chunks, and at least one full stage per chunk.
 constexpr uint32_t kCUs = 256;
 
-int stage_kg(int32_t dt, int bn) { return dt == AIH_F32 ? (bn > 160 ? 4 : 8) : 16; }
+// kg per K stage of the kernel: 16 channels for fp32, 32 for 16-bit storage.
+int stage_kg(int32_t dt) { return dt == AIH_F32 ? 4 : 8; }
 
 int pick_bn(uint32_t n4) {
   int best = 32;
@@ -88,14 +89,14 @@ int plan_gemm(uint32_t M, uint32_t N4, uint32_t KK, int32_t dt, int32_t variant,
   p->bn = pick_bn(N4);
   p->mtiles = div_ceil(M, aih::GEMM_BM);
   p->ntiles = div_ceil(N4, p->bn);
-  const uint32_t bkg = (uint32_t)stage_kg(dt, p->bn);
+  const uint32_t bkg = (uint32_t)stage_kg(dt);
   const uint32_t tiles = p->mtiles * p->ntiles;
   uint32_t s = 1;
   if (splitk > 0) {
     s = (uint32_t)splitk;
   } else if (variant == AIH_VAR_SPLITK) {
     s = 4;
-  } else if (variant == AIH_VAR_AUTO && tiles < kCUs && KK >= 2 * bkg) {
+  } else if (variant == AIH_VAR_AUTO && tiles < kCUs && KK >= 16) {
     s = (2 * kCUs) / tiles;
     if (s > 8) s = 8;
     const uint32_t max_s = KK / bkg;
@@ -122,11 +123,12 @@ void fill_plan(const GemmPlan &g, aih_plan *out) {
   out->ws_bytes = g.ws;
 }
 
-int run_gemm(aih::GemmArgs &a, const GemmPlan &g, int32_t dt, int32_t wdt, bool igemm, void *ws,
+int run_gemm(aih::GemmArgs &a, const GemmPlan &g, int32_t dt, int32_t wdt, bool igemm, bool pair, void *ws,
              size_t ws_bytes, hipStream_t st) {
   a.mtiles = g.mtiles;
   a.ntiles = g.ntiles;
   a.nsplit = g.nsplit;
+  a.ntiles_total = g.mtiles * g.ntiles * g.nsplit;
   a.kk_chunk = g.kk_chunk;
   a.partial = nullptr;
   if (g.nsplit > 1) {
@@ -135,7 +137,7 @@ int run_gemm(aih::GemmArgs &a, const GemmPlan &g, int32_t dt, int32_t wdt, bool 
     if (reinterpret_cast<uintptr_t>(ws) % 16) return fail("workspace must be 16-byte aligned");
     a.partial = static_cast<float *>(ws);
   }
-  hipError_t e = aih::launch_conv_gemm(a, dt, wdt, g.bn, igemm, st);
+  hipError_t e = aih::launch_conv_gemm(a, dt, wdt, g.bn, igemm, pair, st);
   if (e != hipSuccess) return fail(std::string("conv_gemm launch: ") + hipGetErrorString(e));
   if (g.nsplit > 1) {
     e = aih::launch_splitk_reduce(a, dt, st);
@@ -235,8 +237,8 @@ int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *
     if (check_pw(d)) return AIH_ERR;
     if (!x || !w || !bias || !y) return fail("pw: null buffer");
     if ((d->residual != 0) != (res != nullptr)) return fail("pw: res must be given iff residual");
-    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 8) || !aligned(bias, 8) || (res && !aligned(res, 8)))
-      return fail("pw: misaligned buffer");
+    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16) || !aligned(bias, 8) || (res && !aligned(res, 16)))
+      return fail("pw: misaligned buffer (x, w, y, res need 16 bytes, bias 8)");
     GemmPlan g;
     if (plan_pw(d, &g)) return AIH_ERR;
     aih::GemmArgs a;
@@ -262,7 +264,9 @@ int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *
     a.N4 = d->ng * 4;
     a.act = d->act;
     a.has_res = d->residual ? 1 : 0;
-    return run_gemm(a, g, d->dt, d->wdt, false, ws, ws_bytes, static_cast<hipStream_t>(stream));
+    // 16-byte A loads take two kg at once: needs an even kg count per pixel
+    const bool pair = d->dt != AIH_F32 && d->kg % 2 == 0;
+    return run_gemm(a, g, d->dt, d->wdt, false, pair, ws, ws_bytes, static_cast<hipStream_t>(stream));
   });
 }
 
@@ -285,11 +289,11 @@ int aih_conv_igemm(const aih_igemm_desc *d, const void *const *inputs, const voi
     const uint32_t nin = d->nsrcs ? d->nsrcs : 1;
     for (uint32_t i = 0; i < nin; ++i) {
       if (!inputs[i]) return fail("igemm: null input part");
-      if (!aligned(inputs[i], 8)) return fail("igemm: misaligned input");
+      if (!aligned(inputs[i], 16)) return fail("igemm: misaligned input (16 bytes)");
     }
     if ((d->residual != 0) != (res != nullptr)) return fail("igemm: res must be given iff residual");
-    if (!aligned(w, 16) || !aligned(y, 8) || !aligned(bias, 8) || (res && !aligned(res, 8)))
-      return fail("igemm: misaligned buffer");
+    if (!aligned(w, 16) || !aligned(y, 16) || !aligned(bias, 8) || (res && !aligned(res, 16)))
+      return fail("igemm: misaligned buffer (w, y, res need 16 bytes, bias 8)");
     uint32_t oh, ow;
     if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
     GemmPlan g;
@@ -332,7 +336,12 @@ int aih_conv_igemm(const aih_igemm_desc *d, const void *const *inputs, const voi
     a.N4 = div_ceil(d->cout, 4) * 4;
     a.act = d->act;
     a.has_res = d->residual ? 1 : 0;
-    return run_gemm(a, g, d->dt, d->wdt, true, ws, ws_bytes, static_cast<hipStream_t>(stream));
+    // 16-byte A loads take two kg at once: every (tap, part) run of kg, every
+    // pixel stride and every part offset must be even
+    bool pair = d->dt != AIH_F32 && kg % 2 == 0;
+    for (uint32_t i = 0; i < a.nparts; ++i)
+      pair = pair && a.part_kg[i] % 2 == 0 && a.stride_kg[i] % 2 == 0 && a.off_kg[i] % 2 == 0;
+    return run_gemm(a, g, d->dt, d->wdt, true, pair, ws, ws_bytes, static_cast<hipStream_t>(stream));
   });
 }
 

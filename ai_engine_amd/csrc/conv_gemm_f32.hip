@@ -1,28 +1,15 @@
-// conv_gemm_f32.hip -- conv-GEMM kernel instantiations for f32 activations.
+// conv_gemm_f32.hip -- conv-GEMM instantiations for fp32 activations
+// (weights fp32, f16 or bf16; fp32 MFMA) and the split-K reduction.
 #include "conv_gemm_launch.h"
 
 namespace aih {
 
-template <int DTW, int BN>
-static hipError_t launch_bn(const GemmArgs &a, bool igemm, hipStream_t st) {
-  const dim3 grid(a.mtiles * a.ntiles * a.nsplit);
-  if (igemm)
-    hipLaunchKernelGGL((conv_gemm_kernel<DT_F32, DTW, BN, true>), grid, dim3(GEMM_THREADS), 0, st, a);
-  else
-    hipLaunchKernelGGL((conv_gemm_kernel<DT_F32, DTW, BN, false>), grid, dim3(GEMM_THREADS), 0, st, a);
-  return hipGetLastError();
-}
-
 template <int DTW>
 static hipError_t launch_w(const GemmArgs &a, int bn, bool igemm, hipStream_t st) {
-  switch (bn) {
-    case 32: return launch_bn<DTW, 32>(a, igemm, st);
-    case 64: return launch_bn<DTW, 64>(a, igemm, st);
-    case 96: return launch_bn<DTW, 96>(a, igemm, st);
-    case 128: return launch_bn<DTW, 128>(a, igemm, st);
-    case 160: return launch_bn<DTW, 160>(a, igemm, st);
-    case 256: return launch_bn<DTW, 256>(a, igemm, st);
-    default: return hipErrorInvalidValue;
+  if (igemm) {
+    AIH_GEMM_BN_SWITCH(DT_F32, DTW, true, false, bn, a, st)
+  } else {
+    AIH_GEMM_BN_SWITCH(DT_F32, DTW, false, false, bn, a, st)
   }
 }
 
@@ -40,13 +27,16 @@ hipError_t launch_splitk_reduce(const GemmArgs &a, int dta, hipStream_t st) {
   const dim3 grid((unsigned)((nvec + 255) / 256));
   switch (dta) {
     case DT_F32:
-      hipLaunchKernelGGL(splitk_reduce_kernel<DT_F32>, grid, dim3(256), 0, st, a.partial, a.nsplit, a.M, a.N4, a.bias, a.res, a.y, a.act, a.has_res);
+      hipLaunchKernelGGL(splitk_reduce_kernel<DT_F32>, grid, dim3(256), 0, st, a.partial, a.nsplit, a.M, a.N4,
+                         a.bias, a.res, a.y, a.act, a.has_res);
       break;
     case DT_F16:
-      hipLaunchKernelGGL(splitk_reduce_kernel<DT_F16>, grid, dim3(256), 0, st, a.partial, a.nsplit, a.M, a.N4, a.bias, a.res, a.y, a.act, a.has_res);
+      hipLaunchKernelGGL(splitk_reduce_kernel<DT_F16>, grid, dim3(256), 0, st, a.partial, a.nsplit, a.M, a.N4,
+                         a.bias, a.res, a.y, a.act, a.has_res);
       break;
     case DT_BF16:
-      hipLaunchKernelGGL(splitk_reduce_kernel<DT_BF16>, grid, dim3(256), 0, st, a.partial, a.nsplit, a.M, a.N4, a.bias, a.res, a.y, a.act, a.has_res);
+      hipLaunchKernelGGL(splitk_reduce_kernel<DT_BF16>, grid, dim3(256), 0, st, a.partial, a.nsplit, a.M, a.N4,
+                         a.bias, a.res, a.y, a.act, a.has_res);
       break;
     default: return hipErrorInvalidValue;
   }

@@ -19,22 +19,31 @@
 // MFMA mapping (operands swapped so the accumulator is channel-major):
 //   MFMA "A" = weights  (32 output channels x K), MFMA "B" = activations
 //   (K x 32 pixels). With v_mfma_f32_32x32x*, lane l of the result holds
-//   pixel l%32 and channels 8*(r/4) + 4*(l/32) + r%4 for r = 0..15, i.e. four
-//   float4 runs of consecutive channels -> 128-bit NHWC-C4 epilogue stores.
+//   pixel l%32 and channels 8*(r/4) + 4*(l/32) + r%4 for r = 0..15.
 //   fp32:    v_mfma_f32_32x32x2f32, four per 16-byte K unit pair
 //   f16/bf16: v_mfma_f32_32x32x16_{f16,bf16}, one per 16-byte K unit pair
 //   Lane half h = l/32 always takes K unit 2p+h of pair p for both operands,
 //   so the K pairing is consistent whatever order the hardware sums in.
 //
-// Tiling: 256 threads = 4 wavefronts; block tile BM = 128 pixels x BN
-// channels; each wave owns 32 pixels x BN channels (BN/32 accumulator tiles of
-// 16 VGPRs). K is staged through LDS in BKU 16-byte units per stage, double
-// buffered: global loads of stage s+1 are issued before the MFMAs of stage s
-// and written to the other LDS buffer afterwards (one barrier per stage).
+// Work decomposition: a tile is 128 pixels x BN channels x one K chunk
+// (split-K); 256 threads = 4 wavefronts of 32 pixels x BN channels each.
+// The grid is persistent: every workgroup walks a contiguous range of tiles
+// (ranges are handed out XCD by XCD, so neighbouring tiles -- which share
+// input rows and halos -- stay in one L2). Each tile's K is staged through
+// LDS in stages of 16 (fp32) or 32 (16-bit) channels, double buffered, and
+// the pipeline runs across
+// tile boundaries: the global loads of the next (tile, stage) are in flight
+// while the current stage's MFMAs and the finished tile's epilogue execute.
 //
-// Split-K: the grid's third axis cuts K into chunks; each chunk writes fp32
-// partials [split][M][N4] and splitk_reduce sums them in split order (a fixed
-// order, so results are deterministic) and applies the epilogue.
+// Epilogue: bias and activation are applied in the MFMA layout, then every
+// wavefront stages its 32x32 fp32 block in a private LDS region and writes
+// it back row by row: each lane stores 16 contiguous bytes (4 f32 or 8
+// 16-bit channels), loading the residual the same way, so both the output
+// stores and the residual loads are full-line 128-bit accesses.
+//
+// Split-K tiles write fp32 partials [split][M][N4] through the same path and
+// splitk_reduce_kernel sums them in split order (deterministic) and applies
+// the epilogue.
 #pragma once
 
 #include <type_traits>
@@ -65,6 +74,7 @@ struct GemmArgs {
   uint32_t kk_chunk;      // kg per split chunk (multiple of the stage depth)
   uint32_t nsplit;
   uint32_t mtiles, ntiles;
+  uint32_t ntiles_total;  // mtiles * ntiles * nsplit
   int32_t act;
   int32_t has_res;
 };
@@ -72,40 +82,45 @@ struct GemmArgs {
 constexpr int GEMM_THREADS = 256;
 constexpr int GEMM_BM = 128;
 
-template <int DTA, int DTW, int BN>
+template <int DTA, int DTW, int BN, bool PAIR>
 struct GemmCfg {
   static constexpr bool F32 = (DTA == DT_F32);
-  static constexpr int KU = F32 ? 1 : 2;                  // kg per 16-byte K unit
-  static constexpr int BKU = (F32 && BN > 160) ? 4 : 8;   // K units per stage
-  static constexpr int BKG = BKU * KU;                    // kg per stage
-  static constexpr int TN = BN / 32;                      // accumulator tiles per wave
-  static constexpr int AROW = GEMM_BM + 1;                // LDS row pitch (units), +1 against bank conflicts
+  static constexpr int KU = F32 ? 1 : 2;       // kg per 16-byte K unit
+  static constexpr int BKU = 4;                // K units per stage (16 f32 / 32 16-bit channels)
+  static constexpr int BKG = BKU * KU;         // kg per stage
+  static constexpr int TN = BN / 32;           // accumulator tiles per wave
+  static constexpr int AROW = GEMM_BM + 1;     // LDS row pitch (units), +1 against bank conflicts
   static constexpr int WROW = BN + 1;
-  // A loads: one kg per item (16 B f32, 8 B 16-bit)
-  static constexpr int A_EPR = BKG;                       // items per pixel row per stage
+  // A items: f32 -> one kg (16 B); 16-bit paired -> two kg (16 B); unpaired -> one kg (8 B)
+  static constexpr int A_KGI = (!F32 && PAIR) ? 2 : 1;
+  static constexpr int A_EPR = BKG / A_KGI;    // items per pixel row per stage
   static constexpr int A_ITEMS = GEMM_BM * A_EPR / GEMM_THREADS;
-  // W loads: f32 compute: one (kg, n) per item; 16-bit: one (kg, n pair) per item (16 B)
+  // W items: f32 compute -> one (kg, n) 16 B (or 8 B 16-bit weights, widened);
+  // 16-bit compute -> one (kg, n..n+1) 16 B
   static constexpr int W_COLS = F32 ? BN : BN / 2;
-  static constexpr int W_ITEMS = BKG * W_COLS / GEMM_THREADS;
+  static constexpr int W_TOTAL = BKG * W_COLS;
+  static constexpr int W_ITEMS = (W_TOTAL + GEMM_THREADS - 1) / GEMM_THREADS;
+  static constexpr int ST_PITCH = 36;          // staging row pitch in floats (32 + 4)
   static_assert(GEMM_BM * A_EPR % GEMM_THREADS == 0, "A tile");
-  static_assert(BKG * W_COLS % GEMM_THREADS == 0, "W tile");
   static_assert(GEMM_THREADS % A_EPR == 0, "A item mapping");
   static_assert(BN % 32 == 0, "BN");
 };
 
-template <int DTA, int DTW, int BN, bool IGEMM>
+template <int DTA, int DTW, int BN, bool IGEMM, bool PAIR>
 __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
-  using Cfg = GemmCfg<DTA, DTW, BN>;
+  using Cfg = GemmCfg<DTA, DTW, BN, PAIR>;
   constexpr bool F32 = Cfg::F32;
   constexpr int BKU = Cfg::BKU, BKG = Cfg::BKG, TN = Cfg::TN;
   constexpr int AROW = Cfg::AROW, WROW = Cfg::WROW;
   constexpr int A_ITEMS = Cfg::A_ITEMS, W_ITEMS = Cfg::W_ITEMS;
-  constexpr int A_EPR = Cfg::A_EPR, W_COLS = Cfg::W_COLS;
+  constexpr int A_EPR = Cfg::A_EPR, A_KGI = Cfg::A_KGI, W_COLS = Cfg::W_COLS, W_TOTAL = Cfg::W_TOTAL;
+  constexpr int ST_PITCH = Cfg::ST_PITCH;
   constexpr int AB = Storage<DTA>::bytes * 4;  // bytes of one activation kg vector
   constexpr int WB = Storage<DTW>::bytes * 4;  // bytes of one weight kg vector
 
   __shared__ u32x4 As[2][BKU][AROW];
   __shared__ u32x4 Ws[2][BKU][WROW];
+  __shared__ float St[4][32 * ST_PITCH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -113,76 +128,87 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
   const int l32 = lane & 31;
   const int lh = lane >> 5;
 
-  // ---- tile coordinates (XCD-aware order; channel tiles of one pixel tile
-  // are adjacent so they share the A rows in L2) ----
-  const uint32_t nblk = a.mtiles * a.ntiles * a.nsplit;
-  const uint32_t L = xcd_remap(blockIdx.x, nblk);
-  const uint32_t nt = L % a.ntiles;
-  const uint32_t mt = (L / a.ntiles) % a.mtiles;
-  const uint32_t split = L / (a.ntiles * a.mtiles);
-  const uint32_t m0 = mt * GEMM_BM;
-  const uint32_t n0 = nt * BN;
-  const uint32_t kk_begin = split * a.kk_chunk;
-  uint32_t kk_end = kk_begin + a.kk_chunk;
-  if (kk_end > a.KK) kk_end = a.KK;
+  // ---- this workgroup's contiguous range of tiles ----
+  const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t t_begin = (uint32_t)(((uint64_t)blk * a.ntiles_total) / gridDim.x);
+  const uint32_t t_end = (uint32_t)(((uint64_t)(blk + 1) * a.ntiles_total) / gridDim.x);
+  if (t_begin >= t_end) return;
 
-  // ---- per-thread A rows: decode the output pixel once ----
-  const int a_e = tid % A_EPR;  // kg slot within a stage (same for every item)
-  int a_row[A_ITEMS];
+  struct TileInfo {
+    uint32_t m0, n0, split, kk_begin, kk_end, nst;
+  };
+  auto tile_info = [&](uint32_t T) {
+    TileInfo ti;
+    const uint32_t nt = T % a.ntiles;
+    const uint32_t mt = (T / a.ntiles) % a.mtiles;
+    ti.split = T / (a.ntiles * a.mtiles);
+    ti.m0 = mt * GEMM_BM;
+    ti.n0 = nt * BN;
+    ti.kk_begin = ti.split * a.kk_chunk;
+    uint32_t e = ti.kk_begin + a.kk_chunk;
+    ti.kk_end = e > a.KK ? a.KK : e;
+    ti.nst = ti.kk_end > ti.kk_begin ? (ti.kk_end - ti.kk_begin + BKG - 1) / BKG : 0;
+    return ti;
+  };
+
+  // ---- per-thread A rows of the tile being loaded (decoded once per tile) ----
+  const int a_e = tid % A_EPR;  // item slot within a stage (same for every row item)
   bool a_ok[A_ITEMS];
   int32_t a_iy0[A_ITEMS], a_ix0[A_ITEMS];
   uint32_t a_px[A_ITEMS];  // IGEMM: first pixel of the image; PW: the pixel itself
+  uint32_t decoded_m0 = 0xffffffffu;
+  auto decode_rows = [&](uint32_t m0) {
 #pragma unroll
-  for (int i = 0; i < A_ITEMS; ++i) {
-    const int r = (i * GEMM_THREADS + tid) / A_EPR;
-    a_row[i] = r;
-    const uint32_t m = m0 + r;
-    a_ok[i] = m < a.M;
-    if constexpr (IGEMM) {
-      const uint32_t mm = a_ok[i] ? m : 0;
-      const uint32_t img = mm / a.OHW;
-      const uint32_t rem = mm - img * a.OHW;
-      const uint32_t oy = rem / a.OW;
-      const uint32_t ox = rem - oy * a.OW;
-      a_iy0[i] = (int32_t)(oy * a.S) - a.PT;
-      a_ix0[i] = (int32_t)(ox * a.S) - a.PL;
-      a_px[i] = img * a.IH * a.IW;
-    } else {
-      a_iy0[i] = 0;
-      a_ix0[i] = 0;
-      a_px[i] = m;
+    for (int i = 0; i < A_ITEMS; ++i) {
+      const uint32_t m = m0 + (i * GEMM_THREADS + tid) / A_EPR;
+      a_ok[i] = m < a.M;
+      if constexpr (IGEMM) {
+        const uint32_t mm = a_ok[i] ? m : 0;
+        const uint32_t img = mm / a.OHW;
+        const uint32_t rem = mm - img * a.OHW;
+        const uint32_t oy = rem / a.OW;
+        const uint32_t ox = rem - oy * a.OW;
+        a_iy0[i] = (int32_t)(oy * a.S) - a.PT;
+        a_ix0[i] = (int32_t)(ox * a.S) - a.PL;
+        a_px[i] = img * a.IH * a.IW;
+      } else {
+        a_iy0[i] = 0;
+        a_ix0[i] = 0;
+        a_px[i] = m;
+      }
     }
-  }
+    decoded_m0 = m0;
+  };
 
-  using AReg = typename std::conditional<F32, u32x4, u32x2>::type;
+  using AReg = typename std::conditional<(F32 || PAIR), u32x4, u32x2>::type;
   using WLoad = typename std::conditional<(F32 && DTW != DT_F32), u32x2, u32x4>::type;
   AReg areg[A_ITEMS];
   WLoad wreg[W_ITEMS];
 
   const char *wbase = reinterpret_cast<const char *>(a.w);
-  const uint32_t wrow_vecs = a.N4;  // kg vectors per packed weight row
 
-  auto load_stage = [&](uint32_t k0) {
-    // ---- A: one kg of one pixel row per item ----
-    const uint32_t kk = k0 + a_e;
-    const bool k_ok = kk < kk_end;
-    uint32_t tap = 0, kg = kk;
+  auto load_stage = [&](const TileInfo &ti, uint32_t s) {
+    if (decoded_m0 != ti.m0) decode_rows(ti.m0);
+    const uint32_t k0 = ti.kk_begin + s * BKG;
+    // ---- A: A_KGI kg of one pixel row per item ----
+    const uint32_t kk = k0 + a_e * A_KGI;
+    const bool k_ok = kk < ti.kk_end;
+    uint32_t kg = kk;
     int32_t dy = 0, dx = 0;
     if constexpr (IGEMM) {
-      tap = kk / a.KG;
+      const uint32_t tap = kk / a.KG;
       kg = kk - tap * a.KG;
       const uint32_t ky = tap / a.K;
       const uint32_t kx = tap - ky * a.K;
       dy = (int32_t)(ky * a.D);
       dx = (int32_t)(kx * a.D);
     }
-    // part of this kg (concat parts / channel views)
     uint32_t p = 0;
     if (a.nparts > 1) p = (kg >= a.part_kg[1]) + (a.nparts > 2 && kg >= a.part_kg[2]);
     const char *src = reinterpret_cast<const char *>(p == 0 ? a.src[0] : (p == 1 ? a.src[1] : a.src[2]));
     const uint32_t pstride = p == 0 ? a.stride_kg[0] : (p == 1 ? a.stride_kg[1] : a.stride_kg[2]);
-    const uint32_t poff = (p == 0 ? a.off_kg[0] : (p == 1 ? a.off_kg[1] : a.off_kg[2])) +
-                          kg - (p == 0 ? a.part_kg[0] : (p == 1 ? a.part_kg[1] : a.part_kg[2]));
+    const uint32_t poff = (p == 0 ? a.off_kg[0] : (p == 1 ? a.off_kg[1] : a.off_kg[2])) + kg -
+                          (p == 0 ? a.part_kg[0] : (p == 1 ? a.part_kg[1] : a.part_kg[2]));
 #pragma unroll
     for (int i = 0; i < A_ITEMS; ++i) {
       bool ok = k_ok && a_ok[i];
@@ -200,22 +226,22 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
       }
       areg[i] = v;
     }
-    // ---- W: row (tap, kg) of the packed weights ----
+    // ---- W: rows (tap, kg) of the packed weights ----
 #pragma unroll
     for (int i = 0; i < W_ITEMS; ++i) {
       const int idx = i * GEMM_THREADS + tid;
       const int col = idx % W_COLS;
       const int kl = idx / W_COLS;
       const uint32_t wkk = k0 + kl;
-      const uint32_t n = n0 + (F32 ? col : 2 * col);
+      const uint32_t n = ti.n0 + (F32 ? col : 2 * col);
       WLoad v = {};
-      if (wkk < kk_end && n < a.N4) {
+      if ((W_TOTAL % GEMM_THREADS == 0 || idx < W_TOTAL) && wkk < ti.kk_end && n < a.N4) {
         uint32_t wt = 0, wkg = wkk;
         if constexpr (IGEMM) {
           wt = wkk / a.KG;
           wkg = wkk - wt * a.KG;
         }
-        const size_t vidx = (size_t)(wt * a.KGP + wkg) * wrow_vecs + n;
+        const size_t vidx = (size_t)(wt * a.KGP + wkg) * a.N4 + n;
         v = *reinterpret_cast<const WLoad *>(wbase + vidx * WB);
       }
       wreg[i] = v;
@@ -225,8 +251,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
   auto store_stage = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < A_ITEMS; ++i) {
-      const int r = a_row[i];
-      if constexpr (F32) {
+      const int r = (i * GEMM_THREADS + tid) / A_EPR;
+      if constexpr (F32 || PAIR) {
         As[buf][a_e][r] = areg[i];
       } else {
         u32x2 *dst = reinterpret_cast<u32x2 *>(&As[buf][a_e >> 1][r]) + (a_e & 1);
@@ -236,6 +262,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < W_ITEMS; ++i) {
       const int idx = i * GEMM_THREADS + tid;
+      if (W_TOTAL % GEMM_THREADS != 0 && idx >= W_TOTAL) continue;
       const int col = idx % W_COLS;
       const int kl = idx / W_COLS;
       if constexpr (F32) {
@@ -254,7 +281,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
           Ws[buf][kl][col] = __builtin_bit_cast(u32x4, f);
         }
       } else {
-        // (kg, n..n+1) -> half (kg & 1) of units (kg >> 1) at columns n and n+1
+        // (kg, n..n+1) -> half (kg & 1) of unit (kg >> 1) at columns n and n+1
         const u32x4 v = wreg[i];
         u32x2 *d0 = reinterpret_cast<u32x2 *>(&Ws[buf][kl >> 1][2 * col]) + (kl & 1);
         u32x2 *d1 = reinterpret_cast<u32x2 *>(&Ws[buf][kl >> 1][2 * col + 1]) + (kl & 1);
@@ -268,7 +295,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
 #pragma unroll
   for (int t = 0; t < TN; ++t) acc[t] = f32x16{};
 
-  const int wm = wave * 32 + l32;  // this lane's pixel row inside the block tile
+  const int wm = wave * 32 + l32;  // this lane's pixel row inside the tile
 
   auto compute_stage = [&](int buf) {
 #pragma unroll
@@ -302,41 +329,109 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
     }
   };
 
-  // ---- double-buffered K loop ----
-  const uint32_t nst = kk_end > kk_begin ? (kk_end - kk_begin + BKG - 1) / BKG : 0;
-  if (nst > 0) {
-    load_stage(kk_begin);
-    store_stage(0);
-    __syncthreads();
-    for (uint32_t s = 0; s < nst; ++s) {
-      const bool more = s + 1 < nst;
-      if (more) load_stage(kk_begin + (s + 1) * BKG);
-      compute_stage(s & 1);
-      if (more) store_stage((s + 1) & 1);
-      __syncthreads();
-    }
-  }
-
-  // ---- epilogue: bias -> act -> +residual, 128-bit stores ----
-  const uint32_t m = m0 + wm;
-  if (m >= a.M) return;
-  const size_t row = (size_t)m * a.N4;
+  float *st = St[wave];
+  auto epilogue = [&](const TileInfo &ti) {
+    const bool split = a.nsplit > 1;
 #pragma unroll
-  for (int t = 0; t < TN; ++t) {
+    for (int t = 0; t < TN; ++t) {
+      // keep each 32-channel block's loads and stores inside its own iteration
+      // (hoisting them across blocks costs more registers than it saves)
+      __builtin_amdgcn_sched_barrier(0);
+      // (1) bias + act in the MFMA layout, staged as fp32 [32 px][32 ch]
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t n = n0 + t * 32 + 8 * q + 4 * lh;
-      if (n >= a.N4) continue;
-      f32x4 v = f32x4{acc[t][4 * q + 0], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]};
-      if (a.nsplit > 1) {
-        reinterpret_cast<f32x4 *>(a.partial)[((size_t)split * a.M * a.N4 + row + n) / 4] = v;
-      } else {
-        v += Vec4IO<DTA>::load(a.bias, n / 4);
-        v = act_apply4(a.act, v);
-        if (a.has_res) v += Vec4IO<DTA>::load(a.res, (row + n) / 4);
-        Vec4IO<DTA>::store(a.y, (row + n) / 4, v);
+      for (int q = 0; q < 4; ++q) {
+        const int cl = 8 * q + 4 * lh;  // channel inside the 32-channel block
+        f32x4 v = f32x4{acc[t][4 * q + 0], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]};
+        const uint32_t n = ti.n0 + t * 32 + cl;
+        if (!split && n < a.N4) {
+          v += Vec4IO<DTA>::load(a.bias, n / 4);
+          v = act_apply4(a.act, v);
+        }
+        *reinterpret_cast<f32x4 *>(st + l32 * ST_PITCH + cl) = v;
       }
+      __builtin_amdgcn_wave_barrier();
+      // (2) row-wise write-back: 16 contiguous bytes per lane
+      const uint32_t nb = ti.n0 + t * 32;
+      if (split || F32) {
+        // 4 fp32 channels per lane: 8 lanes per row, 8 rows per pass
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+          const int r = pass * 8 + (lane >> 3);
+          const int c = (lane & 7) * 4;
+          const uint32_t m = ti.m0 + wave * 32 + r;
+          const uint32_t n = nb + c;
+          if (m < a.M && n < a.N4) {
+            f32x4 v = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c);
+            const size_t vi = ((size_t)m * a.N4 + n) / 4;
+            if (split) {
+              reinterpret_cast<f32x4 *>(a.partial)[(size_t)ti.split * a.M * (a.N4 / 4) + vi] = v;
+            } else {
+              if (a.has_res) v += Vec4IO<DTA>::load(a.res, vi);
+              Vec4IO<DTA>::store(a.y, vi, v);
+            }
+          }
+        }
+      } else {
+        // 8 16-bit channels per lane: 4 lanes per row, 16 rows per pass
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+          const int r = pass * 16 + (lane >> 2);
+          const int c = (lane & 3) * 8;
+          const uint32_t m = ti.m0 + wave * 32 + r;
+          const uint32_t n = nb + c;
+          if (m < a.M && n < a.N4) {
+            f32x4 v0 = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c);
+            f32x4 v1 = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c + 4);
+            const size_t vi = ((size_t)m * a.N4 + n) / 4;
+            if (n + 8 <= a.N4) {
+              if (a.has_res) {
+                const u32x4 rr = reinterpret_cast<const u32x4 *>(a.res)[vi / 2];
+                v0 += unpack4<DTA>(u32x2{rr.x, rr.y});
+                v1 += unpack4<DTA>(u32x2{rr.z, rr.w});
+              }
+              const u32x2 lo = pack4<DTA>(v0), hi = pack4<DTA>(v1);
+              reinterpret_cast<u32x4 *>(a.y)[vi / 2] = u32x4{lo.x, lo.y, hi.x, hi.y};
+            } else {
+              if (a.has_res) v0 += Vec4IO<DTA>::load(a.res, vi);
+              Vec4IO<DTA>::store(a.y, vi, v0);
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
     }
+#pragma unroll
+    for (int t = 0; t < TN; ++t) acc[t] = f32x16{};
+  };
+
+  // ---- software pipeline over (tile, stage) pairs of this workgroup ----
+  uint32_t T = t_begin;
+  TileInfo cur = tile_info(T);
+  uint32_t s = 0;
+  load_stage(cur, 0);
+  store_stage(0);
+  __syncthreads();
+  int buf = 0;
+  for (;;) {
+    // next (tile, stage)
+    uint32_t nT = T, ns = s + 1;
+    TileInfo nxt = cur;
+    if (ns >= cur.nst) {
+      nT = T + 1;
+      ns = 0;
+      if (nT < t_end) nxt = tile_info(nT);
+    }
+    const bool more = nT < t_end;
+    if (more) load_stage(nxt, ns);
+    if (s < cur.nst) compute_stage(buf);
+    if (ns == 0) epilogue(cur);
+    if (more) store_stage(buf ^ 1);
+    __syncthreads();
+    if (!more) break;
+    T = nT;
+    s = ns;
+    cur = nxt;
+    buf ^= 1;
   }
 }
 
