@@ -110,20 +110,29 @@ template <> struct Vec4IO<DT_BF16> {
 };
 
 // Epilogue activation (ai-core Activation::apply, crates/ai-core/src/activation.rs:28-43).
-// `act` is uniform across the grid, so the switch does not diverge.
+// `act` is uniform across the grid, so the switch does not diverge. Every
+// case is a few instructions (hardware exp2 / rcp / sqrt, ~1 ulp), so the
+// fused epilogue stays small: a libm-accurate expf/tanhf inlined at every
+// output element multiplies the kernel's code size and register demand.
+// tanh clamps its input to +-9 as the reference's WGSL does
+// (crates/ai-gpu/src/kernels/common/activation.rs:20); at |x| = 9 tanh is 1
+// to within 2e-8.
 __device__ __forceinline__ float act_apply(int act, float x) {
   switch (act) {
     case AIH_ACT_NONE: return x;
     case AIH_ACT_RELU: return fmaxf(x, 0.0f);
-    case AIH_ACT_SIGMOID: return 1.0f / (1.0f + expf(-x));
-    case AIH_ACT_TANH: return tanhf(x);
-    case AIH_ACT_HARDSWISH: return x * fminf(fmaxf(x / 6.0f + 0.5f, 0.0f), 1.0f);
-    case AIH_ACT_HARDSIGMOID: return fminf(fmaxf(x / 6.0f + 0.5f, 0.0f), 1.0f);
+    case AIH_ACT_SIGMOID: return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+    case AIH_ACT_TANH: {
+      const float e = __expf(2.0f * fminf(fmaxf(x, -9.0f), 9.0f));
+      return (e - 1.0f) * __builtin_amdgcn_rcpf(e + 1.0f);
+    }
+    case AIH_ACT_HARDSWISH: return x * fminf(fmaxf(x * (1.0f / 6.0f) + 0.5f, 0.0f), 1.0f);
+    case AIH_ACT_HARDSIGMOID: return fminf(fmaxf(x * (1.0f / 6.0f) + 0.5f, 0.0f), 1.0f);
     case AIH_ACT_CLAMP01: return fminf(fmaxf(x, 0.0f), 1.0f);
     case AIH_ACT_RELU6: return fminf(fmaxf(x, 0.0f), 6.0f);
-    case AIH_ACT_SQRT: return sqrtf(fmaxf(x, 0.0f));
+    case AIH_ACT_SQRT: return __builtin_amdgcn_sqrtf(fmaxf(x, 0.0f));
     case AIH_ACT_NEG: return -x;
-    case AIH_ACT_RECIP: return 1.0f / x;
+    case AIH_ACT_RECIP: return __builtin_amdgcn_rcpf(x);
     default: return x;
   }
 }

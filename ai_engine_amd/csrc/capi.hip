@@ -355,8 +355,8 @@ int aih_conv_dw(const aih_dw_desc *d, const void *x, const void *w, const void *
     if (!dtype_ok(d->dt)) return fail("dw: unknown dtype");
     if (!x || !w || !bias || !y) return fail("dw: null buffer");
     if ((d->residual != 0) != (res != nullptr)) return fail("dw: res must be given iff residual");
-    if (!aligned(x, 8) || !aligned(w, 8) || !aligned(y, 8) || !aligned(bias, 8) || (res && !aligned(res, 8)))
-      return fail("dw: misaligned buffer");
+    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16) || !aligned(bias, 16) || (res && !aligned(res, 16)))
+      return fail("dw: misaligned buffer (16 bytes)");
     const uint32_t ek = d->d * (d->k - 1) + 1;
     if (d->ih + d->pad[0] + d->pad[2] < ek || d->iw + d->pad[1] + d->pad[3] < ek)
       return fail("dw: kernel larger than the padded input");

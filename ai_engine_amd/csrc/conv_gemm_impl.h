@@ -121,6 +121,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
   __shared__ u32x4 As[2][BKU][AROW];
   __shared__ u32x4 Ws[2][BKU][WROW];
   __shared__ float St[4][32 * ST_PITCH];
+  __shared__ f32x4 Bs[2][BN / 4];  // bias of the tile, by tile parity
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -184,11 +185,16 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
   using WLoad = typename std::conditional<(F32 && DTW != DT_F32), u32x2, u32x4>::type;
   AReg areg[A_ITEMS];
   WLoad wreg[W_ITEMS];
+  f32x4 breg = {};  // bias of the next tile (threads < BN/4, stage 0 only)
 
   const char *wbase = reinterpret_cast<const char *>(a.w);
 
   auto load_stage = [&](const TileInfo &ti, uint32_t s) {
     if (decoded_m0 != ti.m0) decode_rows(ti.m0);
+    if (s == 0 && tid < BN / 4) {
+      const uint32_t n = ti.n0 + 4 * tid;
+      breg = n < a.N4 ? Vec4IO<DTA>::load(a.bias, n / 4) : f32x4{};
+    }
     const uint32_t k0 = ti.kk_begin + s * BKG;
     // ---- A: A_KGI kg of one pixel row per item ----
     const uint32_t kk = k0 + a_e * A_KGI;
@@ -248,7 +254,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
     }
   };
 
-  auto store_stage = [&](int buf) {
+  auto store_stage = [&](int buf, uint32_t s, uint32_t tile_parity) {
+    if (s == 0 && tid < BN / 4) Bs[tile_parity][tid] = breg;
 #pragma unroll
     for (int i = 0; i < A_ITEMS; ++i) {
       const int r = (i * GEMM_THREADS + tid) / A_EPR;
@@ -330,71 +337,102 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
   };
 
   float *st = St[wave];
-  auto epilogue = [&](const TileInfo &ti) {
+  // Residual rows of one 32-channel block, in the lane layout of the
+  // write-back: fp32 -> 4 passes of 8 rows (16 B = 4 channels per lane);
+  // 16-bit -> 2 passes of 16 rows (16 B = 8 channels per lane).
+  constexpr int PASSES = F32 ? 4 : 2;
+  auto wb_row = [&](int pass) { return F32 ? pass * 8 + (lane >> 3) : pass * 16 + (lane >> 2); };
+  auto wb_col = [&]() { return F32 ? (lane & 7) * 4 : (lane & 3) * 8; };
+  // 16-bit rows start 16-byte aligned only when N4 % 8 == 0; otherwise the
+  // 8 channels of a lane are moved as two 8-byte halves.
+  const bool row16 = (a.N4 % 8) == 0;
+  auto load_res = [&](const TileInfo &ti, int t, u32x4 (&r)[PASSES]) {
+#pragma unroll
+    for (int pass = 0; pass < PASSES; ++pass) {
+      const uint32_t m = ti.m0 + wave * 32 + wb_row(pass);
+      const uint32_t n = ti.n0 + t * 32 + wb_col();
+      u32x4 v = {};
+      if (m < a.M && n < a.N4) {
+        const size_t vi = ((size_t)m * a.N4 + n) / 4;  // 4-channel vector index
+        if constexpr (F32) {
+          v = reinterpret_cast<const u32x4 *>(a.res)[vi];
+        } else if (n + 8 <= a.N4 && row16) {
+          v = reinterpret_cast<const u32x4 *>(a.res)[vi / 2];
+        } else {
+          const u32x2 *rp = reinterpret_cast<const u32x2 *>(a.res);
+          const u32x2 h0 = rp[vi];
+          const u32x2 h1 = n + 8 <= a.N4 ? rp[vi + 1] : u32x2{0u, 0u};
+          v = u32x4{h0.x, h0.y, h1.x, h1.y};
+        }
+      }
+      r[pass] = v;
+    }
+  };
+
+  auto epilogue = [&](const TileInfo &ti, uint32_t tile_parity) {
     const bool split = a.nsplit > 1;
+    const bool res = !split && a.has_res;
+    // The residual of block t+1 is requested before block t's stores: vector
+    // memory operations retire in order, so waiting for it never waits for
+    // the stores that follow it.
+    u32x4 rcur[PASSES], rnext[PASSES];
+    if (res) load_res(ti, 0, rnext);
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
-      // keep each 32-channel block's loads and stores inside its own iteration
-      // (hoisting them across blocks costs more registers than it saves)
       __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int pass = 0; pass < PASSES; ++pass) rcur[pass] = rnext[pass];
+      if (res && t + 1 < TN) load_res(ti, t + 1, rnext);
       // (1) bias + act in the MFMA layout, staged as fp32 [32 px][32 ch]
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int cl = 8 * q + 4 * lh;  // channel inside the 32-channel block
         f32x4 v = f32x4{acc[t][4 * q + 0], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]};
-        const uint32_t n = ti.n0 + t * 32 + cl;
-        if (!split && n < a.N4) {
-          v += Vec4IO<DTA>::load(a.bias, n / 4);
-          v = act_apply4(a.act, v);
-        }
+        if (!split) v = act_apply4(a.act, v + Bs[tile_parity][(t * 32 + cl) / 4]);
         *reinterpret_cast<f32x4 *>(st + l32 * ST_PITCH + cl) = v;
       }
       __builtin_amdgcn_wave_barrier();
       // (2) row-wise write-back: 16 contiguous bytes per lane
       const uint32_t nb = ti.n0 + t * 32;
-      if (split || F32) {
-        // 4 fp32 channels per lane: 8 lanes per row, 8 rows per pass
 #pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
-          const int r = pass * 8 + (lane >> 3);
-          const int c = (lane & 7) * 4;
-          const uint32_t m = ti.m0 + wave * 32 + r;
-          const uint32_t n = nb + c;
-          if (m < a.M && n < a.N4) {
-            f32x4 v = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c);
-            const size_t vi = ((size_t)m * a.N4 + n) / 4;
-            if (split) {
-              reinterpret_cast<f32x4 *>(a.partial)[(size_t)ti.split * a.M * (a.N4 / 4) + vi] = v;
-            } else {
-              if (a.has_res) v += Vec4IO<DTA>::load(a.res, vi);
-              Vec4IO<DTA>::store(a.y, vi, v);
-            }
+      for (int pass = 0; pass < PASSES; ++pass) {
+        const int r = wb_row(pass), c = wb_col();
+        const uint32_t m = ti.m0 + wave * 32 + r;
+        const uint32_t n = nb + c;
+        if (m >= a.M || n >= a.N4) continue;
+        const size_t vi = ((size_t)m * a.N4 + n) / 4;
+        if constexpr (F32) {
+          f32x4 v = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c);
+          if (split) {
+            reinterpret_cast<f32x4 *>(a.partial)[(size_t)ti.split * a.M * (a.N4 / 4) + vi] = v;
+          } else {
+            if (res) v += __builtin_bit_cast(f32x4, rcur[pass]);
+            reinterpret_cast<f32x4 *>(a.y)[vi] = v;
           }
-        }
-      } else {
-        // 8 16-bit channels per lane: 4 lanes per row, 16 rows per pass
-#pragma unroll
-        for (int pass = 0; pass < 2; ++pass) {
-          const int r = pass * 16 + (lane >> 2);
-          const int c = (lane & 3) * 8;
-          const uint32_t m = ti.m0 + wave * 32 + r;
-          const uint32_t n = nb + c;
-          if (m < a.M && n < a.N4) {
-            f32x4 v0 = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c);
-            f32x4 v1 = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c + 4);
-            const size_t vi = ((size_t)m * a.N4 + n) / 4;
-            if (n + 8 <= a.N4) {
-              if (a.has_res) {
-                const u32x4 rr = reinterpret_cast<const u32x4 *>(a.res)[vi / 2];
-                v0 += unpack4<DTA>(u32x2{rr.x, rr.y});
-                v1 += unpack4<DTA>(u32x2{rr.z, rr.w});
-              }
-              const u32x2 lo = pack4<DTA>(v0), hi = pack4<DTA>(v1);
+        } else if (split) {
+          // fp32 partials, 8 channels per lane
+          const f32x4 v0 = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c);
+          f32x4 *pp = reinterpret_cast<f32x4 *>(a.partial) + (size_t)ti.split * a.M * (a.N4 / 4) + vi;
+          pp[0] = v0;
+          if (n + 8 <= a.N4) pp[1] = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c + 4);
+        } else {
+          f32x4 v0 = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c);
+          f32x4 v1 = *reinterpret_cast<const f32x4 *>(st + r * ST_PITCH + c + 4);
+          if (res) {
+            v0 += unpack4<DTA>(u32x2{rcur[pass].x, rcur[pass].y});
+            v1 += unpack4<DTA>(u32x2{rcur[pass].z, rcur[pass].w});
+          }
+          const u32x2 lo = pack4<DTA>(v0);
+          if (n + 8 <= a.N4) {
+            const u32x2 hi = pack4<DTA>(v1);
+            if (row16) {
               reinterpret_cast<u32x4 *>(a.y)[vi / 2] = u32x4{lo.x, lo.y, hi.x, hi.y};
             } else {
-              if (a.has_res) v0 += Vec4IO<DTA>::load(a.res, vi);
-              Vec4IO<DTA>::store(a.y, vi, v0);
+              reinterpret_cast<u32x2 *>(a.y)[vi] = lo;
+              reinterpret_cast<u32x2 *>(a.y)[vi + 1] = hi;
             }
+          } else {
+            reinterpret_cast<u32x2 *>(a.y)[vi] = lo;
           }
         }
       }
@@ -408,8 +446,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
   uint32_t T = t_begin;
   TileInfo cur = tile_info(T);
   uint32_t s = 0;
+  uint32_t parity = 0;  // tile parity: which Bs slot holds this tile's bias
   load_stage(cur, 0);
-  store_stage(0);
+  store_stage(0, 0, parity);
   __syncthreads();
   int buf = 0;
   for (;;) {
@@ -424,10 +463,11 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
     const bool more = nT < t_end;
     if (more) load_stage(nxt, ns);
     if (s < cur.nst) compute_stage(buf);
-    if (ns == 0) epilogue(cur);
-    if (more) store_stage(buf ^ 1);
+    if (ns == 0) epilogue(cur, parity);
+    if (more) store_stage(buf ^ 1, ns, ns == 0 ? parity ^ 1 : parity);
     __syncthreads();
     if (!more) break;
+    if (ns == 0) parity ^= 1;
     T = nT;
     s = ns;
     cur = nxt;

@@ -169,6 +169,15 @@ def main() -> int:
     step_roof = roof(tot_fl, tot_by, gpu_ms / 1e3, args.dtype)
     log(f"dominant kernel {dom_key}: {roofline}")
 
+    # plain device copy of 1 GiB (the calibration kernel for HBM counters and
+    # the bandwidth a streaming kernel can reach on this box)
+    src_buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    dst_buf = torch.empty_like(src_buf)
+    t_copy = time_launches(torch, stream, lambda r: dst_buf.copy_(src_buf), 10)
+    copy_gbs = 2 * src_buf.numel() * 4 / t_copy / 1e9
+    del src_buf, dst_buf
+    log(f"device copy 1 GiB: {copy_gbs:.0f} GB/s")
+
     # ------------------------------------------------------------ per-config kernel table (fp32)
     kernels = {}
     if not args.no_kernels:
@@ -193,6 +202,7 @@ def main() -> int:
                           "bound": step_roof["bound"], "frac": round(step_roof["frac"], 4),
                           "algorithmic_flops": tot_fl, "algorithmic_bytes": tot_by},
         "roofline": roofline,
+        "hbm_copy_gbs": round(copy_gbs, 1),
         "cpu_baseline": cpu,
         "kernels": kernels,
     }
