@@ -338,7 +338,7 @@ def cpu_baseline(layers, wts, H, Wd, budget_s: float) -> dict:
     t0 = time.perf_counter()
     frame()
     t1 = time.perf_counter() - t0
-    frames = max(2, min(64, int(budget_s / max(t1, 1e-6))))
+    frames = max(2, min(4096, int(budget_s / max(t1, 1e-6))))
     t0 = time.perf_counter()
     for _ in range(frames):
         frame()
