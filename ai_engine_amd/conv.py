@@ -97,6 +97,24 @@ class _ConvDesc(C.Structure):
                 ("kg_pad", C.c_uint32)]
 
 
+class _IrDesc(C.Structure):
+    _fields_ = [("n", C.c_uint32), ("ih", C.c_uint32), ("iw", C.c_uint32), ("cin", C.c_uint32),
+                ("cexp", C.c_uint32), ("cout", C.c_uint32), ("s", C.c_uint32), ("pad", C.c_uint32 * 4),
+                ("act_expand", C.c_int32), ("act_dw", C.c_int32), ("act_project", C.c_int32),
+                ("residual", C.c_int32), ("dt", C.c_int32), ("tile_h", C.c_uint32), ("tile_w", C.c_uint32),
+                ("ec", C.c_uint32)]
+
+
+class IrPlan(C.Structure):
+    _fields_ = [("th", C.c_uint32), ("tw", C.c_uint32), ("ec", C.c_uint32), ("chunks", C.c_uint32),
+                ("resident", C.c_uint32), ("tiles", C.c_uint32), ("lds_bytes", C.c_uint32),
+                ("occupancy", C.c_uint32), ("grid", C.c_uint32)]
+
+    def __repr__(self):
+        return (f"IrPlan(tile={self.th}x{self.tw}, ec={self.ec}, chunks={self.chunks}, resident={self.resident}, "
+                f"tiles={self.tiles}, lds={self.lds_bytes}, occ={self.occupancy}, grid={self.grid})")
+
+
 class Plan(C.Structure):
     _fields_ = [("variant", C.c_int32), ("splitk", C.c_uint32), ("bm", C.c_uint32), ("bn", C.c_uint32),
                 ("grid", C.c_uint32), ("ws_bytes", C.c_size_t)]
@@ -110,7 +128,7 @@ EXPORTS = (
     "aih_conv_pw", "aih_conv_pw_plan", "aih_conv_igemm", "aih_conv_igemm_plan", "aih_conv_dw", "aih_conv",
     "aih_conv_workspace_size", "aih_nhwc_c4_bytes", "aih_pack_nhwc", "aih_unpack_nhwc",
     "aih_pack_weights_conv", "aih_pack_weights_dw", "aih_pack_bias", "aih_pack_nhwc_device",
-    "aih_last_error", "aih_version",
+    "aih_ir_block_plan", "aih_ir_block", "aih_last_error", "aih_version",
 )
 
 _lib = None
@@ -140,6 +158,8 @@ def lib() -> C.CDLL:
         "aih_pack_weights_dw": (C.c_int, [P, u32, u32, u32, i32, P]),
         "aih_pack_bias": (C.c_int, [P, u32, i32, P]),
         "aih_pack_nhwc_device": (C.c_int, [P, u32, u32, u32, u32, i32, P, P]),
+        "aih_ir_block_plan": (C.c_int, [C.POINTER(_IrDesc), C.POINTER(IrPlan)]),
+        "aih_ir_block": (C.c_int, [C.POINTER(_IrDesc), P, P, P, P, P, P, P, P, P, P]),
         "aih_last_error": (C.c_char_p, []),
         "aih_version": (C.c_char_p, []),
     }
@@ -369,6 +389,54 @@ class ConvOp:
         ws = _workspace(nb, ws, _device_of(y))
         _check(lib().aih_conv(C.byref(self.desc()), _ptr(x), _ptr(w), _ptr(bias), _ptr(res), _ptr(y), _ptr(ws),
                               nb if ws is not None else 0, _stream(stream)))
+        return y
+
+
+@dataclass
+class IrBlockSpec:
+    """Fused inverted-residual block: the three SwOp::Conv a MobileNet block
+    lowers to (1x1 expand, depthwise 3x3 stride s, 1x1 project) in one launch.
+    The reference dispatches them separately (GemmPwSpec, ConvDwSpec,
+    GemmPwSpec; crates/ai-gpu-runtime/src/lowering.rs:122-152)."""
+
+    ih: int
+    iw: int
+    cin: int
+    cexp: int
+    cout: int
+    s: int = 1
+    pad: tuple = (1, 1, 1, 1)
+    act_expand: Activation = Activation.RELU
+    act_dw: Activation = Activation.RELU
+    act_project: Activation = Activation.NONE
+    residual: bool = False
+    dt: DType = DType.F32
+    n: int = 1
+    tile: tuple = (0, 0)  # forced output tile (h, w); (0, 0) = plan's choice
+    ec: int = 0           # forced expanded channels per chunk; 0 = plan's choice
+
+    def out_hw(self) -> tuple[int, int]:
+        return ((self.ih + self.pad[0] + self.pad[2] - 3) // self.s + 1,
+                (self.iw + self.pad[1] + self.pad[3] - 3) // self.s + 1)
+
+    def desc(self) -> _IrDesc:
+        return _IrDesc(self.n, self.ih, self.iw, self.cin, self.cexp, self.cout, self.s, (C.c_uint32 * 4)(*self.pad),
+                       int(self.act_expand), int(self.act_dw), int(self.act_project), int(bool(self.residual)),
+                       int(self.dt), self.tile[0], self.tile[1], self.ec)
+
+    def plan(self) -> IrPlan:
+        p = IrPlan()
+        _check(lib().aih_ir_block_plan(C.byref(self.desc()), C.byref(p)))
+        return p
+
+    def fusable(self) -> bool:
+        p = IrPlan()
+        return lib().aih_ir_block_plan(C.byref(self.desc()), C.byref(p)) == 0
+
+    def run(self, x, w_expand, b_expand, w_dw, b_dw, w_project, b_project, res, y, stream=None):
+        _check(lib().aih_ir_block(C.byref(self.desc()), _ptr(x), _ptr(w_expand), _ptr(b_expand), _ptr(w_dw),
+                                  _ptr(b_dw), _ptr(w_project), _ptr(b_project), _ptr(res), _ptr(y),
+                                  _stream(stream)))
         return y
 
 

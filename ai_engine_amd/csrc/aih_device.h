@@ -61,12 +61,23 @@ __device__ __forceinline__ f32x4 unpack4(u32x2 r) {
                  bf16_to_f32(r.y >> 16)};
 }
 
+// fp32 -> 4 packed 16-bit values, round to nearest even: gfx950's
+// v_cvt_pk_{f16,bf16}_f32 convert two values per instruction.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (DT == DT_F16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
 template <int DT>
 __device__ __forceinline__ u32x2 pack4(f32x4 v) {
-  if constexpr (DT == DT_F16)
-    return u32x2{f32_to_f16(v.x) | (f32_to_f16(v.y) << 16), f32_to_f16(v.z) | (f32_to_f16(v.w) << 16)};
-  else
-    return u32x2{f32_to_bf16(v.x) | (f32_to_bf16(v.y) << 16), f32_to_bf16(v.z) | (f32_to_bf16(v.w) << 16)};
+  return u32x2{pack2<DT>(v.x, v.y), pack2<DT>(v.z, v.w)};
 }
 
 // 4 consecutive channels (one vec4 of NHWC-C4) <-> fp32.
@@ -88,10 +99,7 @@ template <> struct Vec4IO<DT_F16> {
                  f16_to_f32(r.y >> 16)};
   }
   static __device__ __forceinline__ void store(void *base, size_t vec_idx, f32x4 v) {
-    u32x2 r;
-    r.x = f32_to_f16(v.x) | (f32_to_f16(v.y) << 16);
-    r.y = f32_to_f16(v.z) | (f32_to_f16(v.w) << 16);
-    reinterpret_cast<u32x2 *>(base)[vec_idx] = r;
+    reinterpret_cast<u32x2 *>(base)[vec_idx] = pack4<DT_F16>(v);
   }
 };
 
@@ -102,10 +110,7 @@ template <> struct Vec4IO<DT_BF16> {
                  bf16_to_f32(r.y >> 16)};
   }
   static __device__ __forceinline__ void store(void *base, size_t vec_idx, f32x4 v) {
-    u32x2 r;
-    r.x = f32_to_bf16(v.x) | (f32_to_bf16(v.y) << 16);
-    r.y = f32_to_bf16(v.z) | (f32_to_bf16(v.w) << 16);
-    reinterpret_cast<u32x2 *>(base)[vec_idx] = r;
+    reinterpret_cast<u32x2 *>(base)[vec_idx] = pack4<DT_BF16>(v);
   }
 };
 
@@ -139,6 +144,93 @@ __device__ __forceinline__ float act_apply(int act, float x) {
 
 __device__ __forceinline__ f32x4 act_apply4(int act, f32x4 v) {
   return f32x4{act_apply(act, v.x), act_apply(act, v.y), act_apply(act, v.z), act_apply(act, v.w)};
+}
+
+// The activation as wave-uniform parameters, so that inner loops apply it
+// without a per-element switch: every activation the converter fuses into a
+// conv is one of
+//   LINEAR  v = x*s + t                      none (s = 1, t = -0: exact identity), neg
+//   CLAMP   v = min(max(x*s + t, lo), hi)    relu, relu6, clamp01, hardsigmoid
+//   XCLAMP  v = x * min(max(x*s + t, lo), hi)  hardswish
+// and the transcendental ones (sigmoid, tanh, sqrt, recip) go through act_apply.
+struct Act {
+  float s, t, lo, hi;
+  int mode;
+  int act;
+};
+enum : int { ACT_LINEAR = 0, ACT_CLAMP = 1, ACT_XCLAMP = 2, ACT_SPECIAL = 3, ACT_IDENT = 4, ACT_RELU = 5 };
+
+__device__ __forceinline__ Act act_params(int act) {
+  Act p{1.0f, -0.0f, -__builtin_inff(), __builtin_inff(), ACT_LINEAR, act};
+  switch (act) {
+    case AIH_ACT_NONE: p.mode = ACT_IDENT; break;
+    case AIH_ACT_NEG: p.s = -1.0f; break;
+    case AIH_ACT_RELU: p.mode = ACT_RELU; p.lo = 0.0f; break;
+    case AIH_ACT_RELU6: p.mode = ACT_CLAMP; p.lo = 0.0f; p.hi = 6.0f; break;
+    case AIH_ACT_CLAMP01: p.mode = ACT_CLAMP; p.lo = 0.0f; p.hi = 1.0f; break;
+    case AIH_ACT_HARDSIGMOID:
+      p.mode = ACT_CLAMP; p.s = 1.0f / 6.0f; p.t = 0.5f; p.lo = 0.0f; p.hi = 1.0f;
+      break;
+    case AIH_ACT_HARDSWISH:
+      p.mode = ACT_XCLAMP; p.s = 1.0f / 6.0f; p.t = 0.5f; p.lo = 0.0f; p.hi = 1.0f;
+      break;
+    default: p.mode = ACT_SPECIAL; break;
+  }
+  return p;
+}
+
+// Applies p to N values; the only branch is on the uniform mode.
+template <int N>
+__device__ __forceinline__ void act_array(const Act &p, float (&v)[N]) {
+  switch (p.mode) {
+    case ACT_IDENT:
+      break;
+    case ACT_RELU:
+#pragma unroll
+      for (int j = 0; j < N; ++j) v[j] = fmaxf(v[j], 0.0f);
+      break;
+    case ACT_LINEAR:
+#pragma unroll
+      for (int j = 0; j < N; ++j) v[j] = v[j] * p.s + p.t;
+      break;
+    case ACT_CLAMP:
+#pragma unroll
+      for (int j = 0; j < N; ++j) v[j] = fminf(fmaxf(v[j] * p.s + p.t, p.lo), p.hi);
+      break;
+    case ACT_XCLAMP:
+#pragma unroll
+      for (int j = 0; j < N; ++j) v[j] = v[j] * fminf(fmaxf(v[j] * p.s + p.t, p.lo), p.hi);
+      break;
+    default:
+#pragma unroll
+      for (int j = 0; j < N; ++j) v[j] = act_apply(p.act, v[j]);
+      break;
+  }
+}
+
+__device__ __forceinline__ f32x4 act4(const Act &p, f32x4 x) {
+  float v[4] = {x.x, x.y, x.z, x.w};
+  act_array<4>(p, v);
+  return f32x4{v[0], v[1], v[2], v[3]};
+}
+
+// Division by a launch-uniform divisor d without the ~35-instruction
+// integer division: q = (umulhi(n, m) + n) >> s with s = ceil(log2 d) and
+// m = floor(2^32 (2^s - d) / d) + 1 (the round-up multiply-high method of
+// Granlund and Montgomery, 1994), exact for every 32-bit n and d >= 1.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  const uint64_t m = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
+  return FastDiv{d, (uint32_t)m, s};
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) {
+  return (uint32_t)(((uint64_t)__umulhi(n, f.m) + n) >> f.s);
 }
 
 // MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs,

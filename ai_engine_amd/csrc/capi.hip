@@ -9,11 +9,13 @@
 #include <cstdio>
 #include <cstring>
 #include <exception>
+#include <initializer_list>
 #include <string>
 
 #include "../../include/aih_conv.h"
 #include "conv_dw.h"
 #include "conv_gemm_launch.h"
+#include "ir_block.h"
 
 namespace {
 
@@ -212,6 +214,32 @@ int plan_igemm(const aih_igemm_desc *d, GemmPlan *g) {
                    d->variant, d->splitk, g);
 }
 
+// ---------------------------------------------------------------- fused inverted-residual block
+
+int check_ir(const aih_ir_block_desc *d, uint32_t *oh, uint32_t *ow) {
+  if (!d) return fail("null descriptor");
+  if (!d->n || !d->ih || !d->iw || !d->cin || !d->cexp || !d->cout) return fail("ir_block: zero-sized dimension");
+  if (!dtype_ok(d->dt)) return fail("ir_block: unknown dtype");
+  for (int32_t act : {d->act_expand, d->act_dw, d->act_project})
+    if (act < AIH_ACT_NONE || act > AIH_ACT_RECIP) return fail("ir_block: unknown activation");
+  if (d->s != 1 && d->s != 2) return fail("ir_block: depthwise stride must be 1 or 2");
+  if (d->ih + d->pad[0] + d->pad[2] < 3 || d->iw + d->pad[1] + d->pad[3] < 3)
+    return fail("ir_block: kernel larger than the padded input");
+  *oh = (d->ih + d->pad[0] + d->pad[2] - 3) / d->s + 1;
+  *ow = (d->iw + d->pad[1] + d->pad[3] - 3) / d->s + 1;
+  if ((uint64_t)d->n * d->ih * d->iw * d->cin > 0xffffffffull / 4 ||
+      (uint64_t)d->n * *oh * *ow * d->cout > 0xffffffffull / 4)
+    return fail("ir_block: tensor too large");
+  return AIH_OK;
+}
+
+int plan_ir(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, aih::IrPlan *p) {
+  const char *why = aih::ir_plan(d->n, d->ih, d->iw, oh, ow, d->cin, d->cexp, d->cout, d->s, d->dt, d->tile_h,
+                                 d->tile_w, d->ec, p);
+  if (why) return fail(std::string("ir_block: ") + why);
+  return AIH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -383,6 +411,93 @@ int aih_conv_dw(const aih_dw_desc *d, const void *x, const void *w, const void *
       return fail("dw: tensor too large");
     hipError_t e = aih::launch_conv_dw(a, d->dt, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(std::string("conv_dw launch: ") + hipGetErrorString(e));
+    return AIH_OK;
+  });
+}
+
+int aih_ir_block_plan(const aih_ir_block_desc *d, aih_ir_plan *out) {
+  return guarded([&] {
+    uint32_t oh, ow;
+    if (check_ir(d, &oh, &ow)) return AIH_ERR;
+    if (!out) return fail("null plan");
+    aih::IrPlan p;
+    if (plan_ir(d, oh, ow, &p)) return AIH_ERR;
+    *out = aih_ir_plan{p.TH, p.TW, p.EC, d->cexp / p.EC, p.resident, p.ntiles, p.lds, p.occ, p.grid};
+    return AIH_OK;
+  });
+}
+
+int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand, const void *b_expand,
+                 const void *w_dw, const void *b_dw, const void *w_project, const void *b_project, const void *res,
+                 void *y, aih_stream stream) {
+  return guarded([&] {
+    uint32_t oh, ow;
+    if (check_ir(d, &oh, &ow)) return AIH_ERR;
+    if (!x || !w_expand || !b_expand || !w_dw || !b_dw || !w_project || !b_project || !y)
+      return fail("ir_block: null buffer");
+    if ((d->residual != 0) != (res != nullptr)) return fail("ir_block: res must be given iff residual");
+    for (const void *p : {x, w_expand, w_dw, w_project, (const void *)y})
+      if (!aligned(p, 16)) return fail("ir_block: misaligned buffer (x, y and weights need 16 bytes)");
+    for (const void *p : {b_expand, b_dw, b_project})
+      if (!aligned(p, 8)) return fail("ir_block: misaligned bias (8 bytes)");
+    if (res && !aligned(res, 16)) return fail("ir_block: misaligned residual (16 bytes)");
+    aih::IrPlan p;
+    if (plan_ir(d, oh, ow, &p)) return AIH_ERR;
+    aih::IrArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = x;
+    a.we = w_expand;
+    a.be = b_expand;
+    a.wd = w_dw;
+    a.bd = b_dw;
+    a.wp = w_project;
+    a.bp = b_project;
+    a.res = res;
+    a.y = y;
+    a.N = d->n;
+    a.IH = d->ih;
+    a.IW = d->iw;
+    a.OH = oh;
+    a.OW = ow;
+    a.C = d->cin;
+    a.E = d->cexp;
+    a.CO = d->cout;
+    a.S = d->s;
+    a.PT = (int32_t)d->pad[0];
+    a.PL = (int32_t)d->pad[1];
+    a.TH = p.TH;
+    a.TW = p.TW;
+    a.HH = p.HH;
+    a.HW = p.HW;
+    a.NPI = p.NPI;
+    a.NPB = p.NPB;
+    a.EC = p.EC;
+    a.resident = p.resident;
+    a.tiles_y = p.tiles_y;
+    a.tiles_x = p.tiles_x;
+    a.ntiles = p.ntiles;
+    a.act_e = d->act_expand;
+    a.act_d = d->act_dw;
+    a.act_p = d->act_project;
+    a.has_res = d->residual ? 1 : 0;
+    a.lds_x = p.lds_x;
+    a.lds_xe = p.lds_xe;
+    a.lds_we = p.lds_we;
+    a.lds_wp = p.lds_wp;
+    a.lds_wd = p.lds_wd;
+    a.lds_b = p.lds_b;
+    const uint32_t es = d->dt == AIH_F32 ? 4 : 2;
+    const uint32_t wn = p.resident ? d->cexp : p.EC;
+    a.fd_nvx = aih::make_fastdiv(d->cin * es / 16);
+    a.fd_hw = aih::make_fastdiv(p.HW);
+    a.fd_tw = aih::make_fastdiv(p.TW);
+    a.fd_tx = aih::make_fastdiv(p.tiles_x);
+    a.fd_pi = aih::make_fastdiv(p.tiles_x * p.tiles_y);
+    a.fd_co = aih::make_fastdiv(d->cout);
+    a.fd_wn = aih::make_fastdiv(wn);
+    a.fd_wn4 = aih::make_fastdiv(wn / 4);
+    hipError_t e = aih::launch_ir_block(a, d->dt, p.lds, p.grid, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(std::string("ir_block launch: ") + hipGetErrorString(e));
     return AIH_OK;
   });
 }

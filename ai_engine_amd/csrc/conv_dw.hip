@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void conv_dw_kernel(DwArgs a) {
   for (int p = 0; p < PX; ++p) {
     if (ox0 + p >= a.OW) break;
     const size_t vi = (orow + ox0 + p) * cg + g;
-    f32x4 v = act_apply4(a.act, acc[p]);
+    f32x4 v = act4(act_params(a.act), acc[p]);
     if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
     Vec4IO<DT>::store(a.y, vi, v);
   }
@@ -126,6 +126,7 @@ __global__ __launch_bounds__(256) void conv_dw_strip_kernel(DwArgs a) {
     for (int j = 0; j < CV; ++j) acc[p][j] = b[j];
 
   const int32_t ix0 = (int32_t)(ox0 * S) - a.PL;
+  const Act actp = act_params(a.act);
   const size_t img_base = (size_t)img * a.IH * a.IW;
 #pragma unroll
   for (int ky = 0; ky < K; ++ky) {
@@ -160,7 +161,8 @@ __global__ __launch_bounds__(256) void conv_dw_strip_kernel(DwArgs a) {
     const size_t vi = (orow + ox0 + p) * cgv + g;
     float v[CV];
 #pragma unroll
-    for (int j = 0; j < CV; ++j) v[j] = act_apply(a.act, acc[p][j]);
+    for (int j = 0; j < CV; ++j) v[j] = acc[p][j];
+    act_array<CV>(actp, v);
     if (a.has_res) {
       float rr[CV];
       ld_cv<DT, CV>(a.res, vi, rr);

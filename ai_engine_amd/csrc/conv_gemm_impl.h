@@ -188,6 +188,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
   f32x4 breg = {};  // bias of the next tile (threads < BN/4, stage 0 only)
 
   const char *wbase = reinterpret_cast<const char *>(a.w);
+  const Act actp = act_params(a.act);
 
   auto load_stage = [&](const TileInfo &ti, uint32_t s) {
     if (decoded_m0 != ti.m0) decode_rows(ti.m0);
@@ -388,7 +389,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
       for (int q = 0; q < 4; ++q) {
         const int cl = 8 * q + 4 * lh;  // channel inside the 32-channel block
         f32x4 v = f32x4{acc[t][4 * q + 0], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]};
-        if (!split) v = act_apply4(a.act, v + Bs[tile_parity][(t * 32 + cl) / 4]);
+        if (!split) v = act4(actp, v + Bs[tile_parity][(t * 32 + cl) / 4]);
         *reinterpret_cast<f32x4 *>(st + l32 * ST_PITCH + cl) = v;
       }
       __builtin_amdgcn_wave_barrier();
@@ -489,7 +490,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   for (uint32_t s = 1; s < nsplit; ++s) v += p[s * nvec + i];
   const uint32_t n = (uint32_t)(i % (N4 / 4)) * 4;
   v += Vec4IO<DTA>::load(bias, n / 4);
-  v = act_apply4(act, v);
+  v = act4(act_params(act), v);
   if (has_res) v += Vec4IO<DTA>::load(res, i);
   Vec4IO<DTA>::store(y, i, v);
 }

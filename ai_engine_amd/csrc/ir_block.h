@@ -1,0 +1,58 @@
+// ir_block.h -- launch interface of the fused inverted-residual block kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "aih_device.h"
+
+namespace aih {
+
+// One inverted-residual block: 1x1 expand (C -> E) + act, depthwise 3x3
+// (stride S) + act, 1x1 project (E -> CO) + act (+ residual), all tensors
+// NHWC-C4 with the batch outermost, weights in the converter's packed layouts.
+struct IrArgs {
+  const void *x;         // [N][IH][IW][C]
+  const void *we, *be;   // expand weights [kg][E/4][4][4], bias [E]
+  const void *wd, *bd;   // depthwise weights [9][E/4][4], bias [E]
+  const void *wp, *bp;   // project weights [kg][CO/4][4][4], bias [CO]
+  const void *res;       // [N][OH][OW][CO] or null
+  void *y;               // [N][OH][OW][CO]
+  uint32_t N, IH, IW, OH, OW;
+  uint32_t C, E, CO;
+  uint32_t S;
+  int32_t PT, PL;
+  uint32_t TH, TW;       // output tile
+  uint32_t HH, HW;       // input (halo) tile: (TH-1)*S+3 x (TW-1)*S+3
+  uint32_t NPI, NPB;     // 32-pixel blocks of the halo tile / of the output tile
+  uint32_t EC;           // expanded channels per chunk (multiple of 32)
+  uint32_t resident;     // 1: all E channels' weights stay in LDS for every tile
+  uint32_t tiles_y, tiles_x, ntiles;
+  int32_t act_e, act_d, act_p, has_res;
+  uint32_t lds_x, lds_xe, lds_we, lds_wp, lds_wd, lds_b;  // LDS byte offsets
+  // divisors the kernel uses, prepared on the host
+  FastDiv fd_nvx;              // 16-byte vectors per input pixel
+  FastDiv fd_hw, fd_tw;        // halo tile width, output tile width
+  FastDiv fd_tx, fd_pi;        // tiles per row, tiles per image
+  FastDiv fd_co;               // project output channels
+  FastDiv fd_wn, fd_wn4;       // weight channels loaded at once (E or EC), and / 4
+};
+
+// Tile / chunk geometry of one launch, chosen by ir_plan.
+struct IrPlan {
+  uint32_t TH, TW, HH, HW, NPI, NPB, EC, resident;
+  uint32_t tiles_y, tiles_x, ntiles;
+  uint32_t lds_x, lds_xe, lds_we, lds_wp, lds_wd, lds_b, lds;  // LDS byte offsets and total
+  uint32_t occ, grid;  // workgroups per CU, launched workgroups
+};
+
+// Chooses the tile and chunk geometry for an inverted-residual block
+// (depthwise 3x3, stride S). Returns nullptr on success, otherwise the reason
+// the block cannot run fused.
+// tile_h / tile_w / ec force that part of the geometry when non-zero.
+const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
+                    uint32_t CO, uint32_t S, int dt, uint32_t tile_h, uint32_t tile_w, uint32_t ec, IrPlan *p);
+
+hipError_t launch_ir_block(const IrArgs &a, int dt, uint32_t lds, uint32_t grid, hipStream_t st);
+
+}  // namespace aih

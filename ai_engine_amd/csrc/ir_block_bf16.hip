@@ -1,0 +1,12 @@
+// ir_block_bf16.hip -- fused inverted-residual block instantiations, bf16 storage.
+#include "ir_block_impl.h"
+
+namespace aih {
+
+hipError_t launch_ir_block_bf16(const IrArgs &a, uint32_t lds, uint32_t grid, hipStream_t st) {
+  return ir_launch_dt<DT_BF16>(a, lds, grid, st);
+}
+
+int ir_occ_bf16(uint32_t nob, uint32_t npw, uint32_t lds) { return ir_occ_dt<DT_BF16>(nob, npw, lds); }
+
+}  // namespace aih

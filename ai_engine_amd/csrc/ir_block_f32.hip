@@ -1,0 +1,12 @@
+// ir_block_f32.hip -- fused inverted-residual block instantiations, f32 storage.
+#include "ir_block_impl.h"
+
+namespace aih {
+
+hipError_t launch_ir_block_f32(const IrArgs &a, uint32_t lds, uint32_t grid, hipStream_t st) {
+  return ir_launch_dt<DT_F32>(a, lds, grid, st);
+}
+
+int ir_occ_f32(uint32_t nob, uint32_t npw, uint32_t lds) { return ir_occ_dt<DT_F32>(nob, npw, lds); }
+
+}  // namespace aih

@@ -6,13 +6,20 @@
   buffer (the batch is the outermost dimension);
 * `upload_input` = `Model::upload_input` (:387-399): logical NHWC fp32 already
   on the device is packed to NHWC-C4 in the model dtype by a device kernel;
-* `infer` = `Model::infer` (:402-426): every conv is issued in order on one
-  stream through the C ABI (aih_conv routes each op like lower_op);
+* `infer` = `Model::infer` (:402-426): every op is issued in order on one
+  stream through the C ABI (aih_conv routes each conv like lower_op);
 * `read_output` = `Model::read_output` (:442-457).
+
+Load-time fusion (fuse=True): a 1x1 conv feeding a depthwise 3x3 feeding a
+1x1 conv, whose two intermediates have no other reader, becomes one
+aih_ir_block launch (the expanded tensor stays on chip). The fused op reads
+the same packed weights; blocks the fused kernel cannot run (aih_ir_block_plan
+fails) stay three launches.
 """
 from __future__ import annotations
 
 import ctypes as C
+from dataclasses import dataclass, field
 
 import numpy as np
 import torch
@@ -35,65 +42,153 @@ def _to_device(a: np.ndarray, device) -> torch.Tensor:
     return torch.from_numpy(a).to(device)
 
 
+@dataclass
+class ModelOp:
+    """One launch of the graph: a single conv ("conv") or a fused block ("ir_block")."""
+
+    name: str
+    kind: str
+    layers: list
+    fn: object
+    args: tuple
+    spec: object = None
+    keep: list = field(default_factory=list)
+
+    def flops(self, n: int) -> int:
+        return sum(L.flops(n) for L in self.layers)
+
+    def bytes(self, n: int, act_bytes: int, w_bytes: int) -> int:
+        """Algorithmic HBM bytes of this launch: each tensor it must read or
+        write once (a fused block's intermediates never reach HBM)."""
+        if self.kind == "conv":
+            return self.layers[0].bytes(n, act_bytes, w_bytes)
+        e, d, p = self.layers
+        oh, ow = p.out_hw()
+        c4 = lambda c: -(-c // 4) * 4
+        x = n * e.ih * e.iw * c4(e.cin) * act_bytes
+        y = n * oh * ow * p.cout * act_bytes
+        r = y if p.res else 0
+        w = (e.cin * e.cout + d.k * d.k * d.cout + p.cin * p.cout) * w_bytes
+        b = (e.cout + d.cout + p.cout) * act_bytes
+        return x + y + r + w + b
+
+
 class Model:
     def __init__(self, layers: list[Layer], weights: Weights, n: int, ih: int, iw: int, cin: int,
-                 dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0"):
+                 dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0",
+                 fuse: bool = True):
         self.layers = layers
         self.n, self.ih, self.iw, self.cin = n, ih, iw, cin
         self.dt = conv.DType(dt)
         self.wdt = self.dt if wdt is None else conv.DType(wdt)
         self.device = torch.device(device)
         L = conv.lib()
-        self._fn = L.aih_conv
         self.tensors: dict[str, torch.Tensor] = {}
         self.shapes: dict[str, tuple[int, int, int]] = {"input": (ih, iw, cin)}
         self.tensors["input"] = self._alloc(ih, iw, cin)
-        self.ops = []
-        self._keep = []
+        self.ops: list[ModelOp] = []
+        self.output = layers[-1].name
+
+        readers: dict[str, int] = {}
         for Lr in layers:
-            oh, ow = Lr.out_hw()
-            assert self.shapes[Lr.src][:2] == (Lr.ih, Lr.iw), Lr.name
-            op = conv.ConvOp(ih=Lr.ih, iw=Lr.iw, cin=Lr.cin, cout=Lr.cout, kh=Lr.k, kw=Lr.k, sh=Lr.s, sw=Lr.s,
-                             pad=(Lr.pad,) * 4, groups=Lr.groups, act=ACT[Lr.act], residual=Lr.res is not None,
-                             dt=self.dt, wdt=self.wdt, n=n)
+            readers[Lr.src] = readers.get(Lr.src, 0) + 1
+            if Lr.res:
+                readers[Lr.res] = readers.get(Lr.res, 0) + 1
+
+        packed = {}
+        for Lr in layers:
             w = weights.w[Lr.name]
             if Lr.depthwise:
                 wp = conv.pack_weights_dw(w, Lr.cout, Lr.k, Lr.k, self.dt)
             else:
                 wp, _ = conv.pack_weights_conv(w, Lr.cout, Lr.cin, Lr.k, Lr.k, 4, self.wdt)
             bp = conv.pack_bias(weights.b[Lr.name], Lr.cout, self.dt)
-            wd, bd = _to_device(wp, self.device), _to_device(bp, self.device)
-            y = self._alloc(oh, ow, Lr.cout)
-            self.tensors[Lr.name] = y
-            self.shapes[Lr.name] = (oh, ow, Lr.cout)
-            nb = op.workspace_bytes()
-            ws = torch.empty(max(nb // 4, 1), dtype=torch.float32, device=self.device) if nb else None
-            desc = op.desc()
-            res = self.tensors[Lr.res] if Lr.res else None
-            args = (C.byref(desc), self.tensors[Lr.src].data_ptr(), wd.data_ptr(), bd.data_ptr(),
-                    res.data_ptr() if res is not None else None, y.data_ptr(),
-                    ws.data_ptr() if ws is not None else None, nb)
-            self._keep += [desc, wd, bd, ws]
-            self.ops.append((Lr, op, args))
-        self.output = layers[-1].name
+            packed[Lr.name] = (_to_device(wp, self.device), _to_device(bp, self.device))
+            self.shapes[Lr.name] = Lr.out_hw() + (Lr.cout,)
+
+        i = 0
+        while i < len(layers):
+            blk = self._match_block(layers, i, readers) if fuse else None
+            if blk is not None:
+                self.ops.append(self._fused_op(blk, packed, L))
+                i += 3
+                continue
+            self.ops.append(self._conv_op(layers[i], packed, L))
+            i += 1
+
+    # ------------------------------------------------------------ graph building
+
+    def _match_block(self, layers, i, readers):
+        if i + 2 >= len(layers):
+            return None
+        e, d, p = layers[i:i + 3]
+        if e.depthwise or e.k != 1 or e.s != 1:
+            return None
+        if not d.depthwise or d.k != 3 or d.src != e.name or d.cin != e.cout or d.res:
+            return None
+        if p.depthwise or p.k != 1 or p.s != 1 or p.src != d.name or e.res:
+            return None
+        if readers.get(e.name, 0) != 1 or readers.get(d.name, 0) != 1 or self.output in (e.name, d.name):
+            return None
+        if self.wdt != self.dt:
+            return None
+        spec = conv.IrBlockSpec(ih=e.ih, iw=e.iw, cin=e.cin, cexp=e.cout, cout=p.cout, s=d.s, pad=(d.pad,) * 4,
+                                act_expand=ACT[e.act], act_dw=ACT[d.act], act_project=ACT[p.act],
+                                residual=p.res is not None, dt=self.dt, n=self.n)
+        if not spec.fusable():
+            return None
+        return (e, d, p, spec)
+
+    def _fused_op(self, blk, packed, L) -> ModelOp:
+        e, d, p, spec = blk
+        oh, ow = p.out_hw()
+        y = self._alloc(oh, ow, p.cout)
+        self.tensors[p.name] = y
+        desc = spec.desc()
+        res = self.tensors[p.res] if p.res else None
+        args = (C.byref(desc), self.tensors[e.src].data_ptr(), packed[e.name][0].data_ptr(),
+                packed[e.name][1].data_ptr(), packed[d.name][0].data_ptr(), packed[d.name][1].data_ptr(),
+                packed[p.name][0].data_ptr(), packed[p.name][1].data_ptr(),
+                res.data_ptr() if res is not None else None, y.data_ptr())
+        keep = [desc] + [t for nm in (e.name, d.name, p.name) for t in packed[nm]]
+        return ModelOp(p.name.rsplit(".", 1)[0], "ir_block", [e, d, p], L.aih_ir_block, args, spec, keep)
+
+    def _conv_op(self, Lr, packed, L) -> ModelOp:
+        oh, ow = Lr.out_hw()
+        assert self.shapes[Lr.src][:2] == (Lr.ih, Lr.iw), Lr.name
+        op = conv.ConvOp(ih=Lr.ih, iw=Lr.iw, cin=Lr.cin, cout=Lr.cout, kh=Lr.k, kw=Lr.k, sh=Lr.s, sw=Lr.s,
+                         pad=(Lr.pad,) * 4, groups=Lr.groups, act=ACT[Lr.act], residual=Lr.res is not None,
+                         dt=self.dt, wdt=self.wdt, n=self.n)
+        wd, bd = packed[Lr.name]
+        y = self._alloc(oh, ow, Lr.cout)
+        self.tensors[Lr.name] = y
+        nb = op.workspace_bytes()
+        ws = torch.empty(max(nb // 4, 1), dtype=torch.float32, device=self.device) if nb else None
+        desc = op.desc()
+        res = self.tensors[Lr.res] if Lr.res else None
+        args = (C.byref(desc), self.tensors[Lr.src].data_ptr(), wd.data_ptr(), bd.data_ptr(),
+                res.data_ptr() if res is not None else None, y.data_ptr(),
+                ws.data_ptr() if ws is not None else None, nb)
+        return ModelOp(Lr.name, "conv", [Lr], L.aih_conv, args, op, [desc, wd, bd, ws])
 
     def _alloc(self, h: int, w: int, c: int) -> torch.Tensor:
         return torch.empty(self.n * h * w * (-(-c // 4)) * 4, dtype=_storage_torch(self.dt), device=self.device)
+
+    # ------------------------------------------------------------ runtime verbs
 
     def upload_input(self, x_nhwc_f32: torch.Tensor, stream=None):
         conv.pack_nhwc_device(x_nhwc_f32, self.n, self.ih, self.iw, self.cin, self.dt, self.tensors["input"], stream)
 
     def infer(self, stream=None):
         s = conv._stream(stream)
-        fn = self._fn
-        for Lr, _, args in self.ops:
-            if fn(*args, s) != 0:
-                raise conv.AihError(f"{Lr.name}: {conv.last_error()}")
+        for op in self.ops:
+            if op.fn(*op.args, s) != 0:
+                raise conv.AihError(f"{op.name}: {conv.last_error()}")
 
     def launch_op(self, i: int, stream=None):
-        Lr, _, args = self.ops[i]
-        if self._fn(*args, conv._stream(stream)) != 0:
-            raise conv.AihError(f"{Lr.name}: {conv.last_error()}")
+        op = self.ops[i]
+        if op.fn(*op.args, conv._stream(stream)) != 0:
+            raise conv.AihError(f"{op.name}: {conv.last_error()}")
 
     def read_output(self, name: str | None = None) -> np.ndarray:
         """Unpacked logical NHWC fp32 of a tensor (default: the graph output)."""

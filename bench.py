@@ -128,27 +128,16 @@ def main() -> int:
     act_b = 2 if args.dtype != "f32" else 4
     groups: dict[str, dict] = {}
     layer_rows = []
-    for i, (Lr, op, _) in enumerate(model.ops):
+    for i, op in enumerate(model.ops):
         t = sorted(evs[r][i][0].elapsed_time(evs[r][i][1]) for r in range(R))[R // 2] / 1e3
-        fl, by = Lr.flops(n), Lr.bytes(n, act_b, act_b)
-        if Lr.depthwise:
-            key = f"conv_dw_kernel<{args.dtype}>"
-        else:
-            if Lr.k == 1:
-                p = conv.GemmPwSpec(m=Lr.ih * Lr.iw, kg=-(-Lr.cin // 4), ng=-(-Lr.cout // 4), dt=DT[args.dtype],
-                                    n=n).plan()
-            else:
-                p = conv.ConvIgemmSpec(ih=Lr.ih, iw=Lr.iw, cin=Lr.cin, cout=Lr.cout, k=Lr.k, s=Lr.s,
-                                       pad=(Lr.pad,) * 4, dt=DT[args.dtype], n=n).plan()
-            key = f"conv_gemm_kernel<{args.dtype},{args.dtype},BN={p.bn},{'igemm' if Lr.k > 1 else 'pw'}>"
-            if p.splitk > 1:
-                key += "+splitk_reduce"
+        fl, by = op.flops(n), op.bytes(n, act_b, act_b)
+        key = kernel_key(conv, op, n, DT[args.dtype], args.dtype)
         g = groups.setdefault(key, dict(launches=0, secs=0.0, flops=0, bytes=0))
         g["launches"] += 1
         g["secs"] += t
         g["flops"] += fl
         g["bytes"] += by
-        layer_rows.append(dict(layer=Lr.name, kernel=key, us=round(t * 1e6, 2),
+        layer_rows.append(dict(op=op.name, kernel=key, us=round(t * 1e6, 2),
                                gbs=round(by / t / 1e9, 1), tflops=round(fl / t / 1e12, 2)))
     step_secs = sum(g["secs"] for g in groups.values())
     dom_key, dom = max(groups.items(), key=lambda kv: kv[1]["secs"])
@@ -208,6 +197,25 @@ def main() -> int:
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def kernel_key(conv, op, n, dt, dtname) -> str:
+    """Name of the kernel instantiation one model op launches (as the kernel
+    trace names it for the fused block; descriptive for the conv kernels)."""
+    if op.kind == "ir_block":
+        p = op.spec.plan()
+        npw = -(-(-(-p.th * p.tw // 32)) // 4)
+        return f"ir_block_kernel<{int(dt)}, {op.spec.cout // 32}, {npw}>"
+    Lr = op.layers[0]
+    if Lr.depthwise:
+        return f"conv_dw_strip_kernel<{dtname}>"
+    if Lr.k == 1:
+        p = conv.GemmPwSpec(m=Lr.ih * Lr.iw, kg=-(-Lr.cin // 4), ng=-(-Lr.cout // 4), dt=dt, n=n).plan()
+    else:
+        p = conv.ConvIgemmSpec(ih=Lr.ih, iw=Lr.iw, cin=Lr.cin, cout=Lr.cout, k=Lr.k, s=Lr.s, pad=(Lr.pad,) * 4,
+                               dt=dt, n=n).plan()
+    key = f"conv_gemm_kernel<{dtname},{dtname},BN={p.bn},{'igemm' if Lr.k > 1 else 'pw'}>"
+    return key + ("+splitk_reduce" if p.splitk > 1 else "")
 
 
 def time_launches(torch, stream, fn, reps: int, warm: int = 3) -> float:
@@ -286,6 +294,7 @@ def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
     t = time_launches(torch, stream, lambda r: m4.infer(stream), 10)
     fl, by = W.totals(layers, meta["n"], 4, 4)
     row = roof(fl, by, t, "f32")
+    row["launches"] = len(m4.ops)
     row["per_layer_roofline_sum_us"] = sum(
         max(L.flops(meta["n"]) / (PEAK_TF["f32"] * 1e12), L.bytes(meta["n"], 4, 4) / (HBM_GBS * 1e9))
         for L in layers) * 1e6

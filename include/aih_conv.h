@@ -137,6 +137,35 @@ typedef struct {
   size_t ws_bytes;  /* workspace the call needs */
 } aih_plan;
 
+/* Fused inverted-residual block: three consecutive SwOp::Conv that lower_op
+ * would dispatch separately (lowering.rs:122-152) -- a 1x1 expand (cin ->
+ * cexp), a depthwise 3x3 with stride s over cexp channels, and a 1x1 project
+ * (cexp -> cout) -- run as one kernel, so the expanded tensor never goes to
+ * HBM. Each stage keeps its unfused arithmetic: fp32 accumulation,
+ * y = act(acc + bias) (+ res), intermediates rounded to dt where the unfused
+ * ops store them. All weights and biases are in dt, in the converter's
+ * layouts (pack_weights_conv kg_align 4 for the 1x1 convs, pack_weights_dw
+ * for the depthwise). Residual, if any, is added after act_project. */
+typedef struct {
+  uint32_t n, ih, iw;
+  uint32_t cin, cexp, cout;
+  uint32_t s;       /* depthwise stride (1 or 2); the kernel is 3x3 */
+  uint32_t pad[4];  /* depthwise padding: top, left, bottom, right */
+  int32_t act_expand, act_dw, act_project;
+  int32_t residual;
+  int32_t dt;
+  uint32_t tile_h, tile_w; /* output tile; 0 = chosen by the plan */
+  uint32_t ec;             /* expanded channels per chunk; 0 = chosen by the plan */
+} aih_ir_block_desc;
+
+/* Geometry aih_ir_block_plan chose: output tile th x tw, expanded channels
+ * per chunk, whether all expand/project weights stay resident in LDS, LDS
+ * bytes and workgroups per CU, launched workgroups. */
+typedef struct {
+  uint32_t th, tw, ec, chunks, resident;
+  uint32_t tiles, lds_bytes, occupancy, grid;
+} aih_ir_plan;
+
 /* ---- op entry points (asynchronous on `stream`) ---- */
 
 /* Buffer order follows GemmPwSpec::bindings (gemm_pw.rs:276-283): IN, W, BIAS,
@@ -161,6 +190,16 @@ int aih_conv_dw(const aih_dw_desc *d, const void *x, const void *w, const void *
 int aih_conv(const aih_conv_desc *d, const void *x, const void *w, const void *bias,
              const void *res, void *y, void *ws, size_t ws_bytes, aih_stream stream);
 size_t aih_conv_workspace_size(const aih_conv_desc *d);
+
+/* Fused block (no counterpart op in the reference: a fusion of the three
+ * dispatches above). Fails with a message when the shape cannot run fused
+ * (cin % 16 (f16/bf16) or % 8 (f32), cin > 128, cexp % 32, cout % 32 or cout > 128,
+ * s not in {1, 2}); the caller then runs the three ops unfused. Buffers:
+ * x [n][ih][iw][cin], res/y [n][oh][ow][cout], NHWC-C4 in dt. */
+int aih_ir_block_plan(const aih_ir_block_desc *d, aih_ir_plan *out);
+int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand, const void *b_expand,
+                 const void *w_dw, const void *b_dw, const void *w_project, const void *b_project,
+                 const void *res, void *y, aih_stream stream);
 
 /* ---- host-side packing (ai-core pack.rs; plain host memory) ---- */
 /* Output bytes = n*h*w*ceil(c/4)*4*sizeof(dt). */

@@ -137,3 +137,53 @@ def test_invalid_descriptors_fail_cleanly():
     d = conv.GemmPwSpec(m=180, kg=240, ng=40, splitk=4).desc()
     assert L.aih_conv_pw(C.byref(d), 16, 16, 16, None, 16, None, 0, None) == -1
     assert "workspace" in conv.last_error()
+
+
+# ---------------------------------------------------------------- fused inverted-residual block (plan only)
+
+ENCODER_BLOCKS = [  # (n, ih, iw, cin, cexp, cout, s) of the 160x288 encoder's ten blocks, batch 64
+    (64, 80, 144, 32, 128, 32, 1), (64, 80, 144, 32, 128, 32, 1), (64, 80, 144, 32, 128, 64, 2),
+    (64, 40, 72, 64, 256, 64, 1), (64, 40, 72, 64, 256, 64, 1), (64, 40, 72, 64, 256, 96, 2),
+    (64, 20, 36, 96, 384, 96, 1), (64, 20, 36, 96, 384, 96, 1), (64, 20, 36, 96, 384, 128, 2),
+    (64, 10, 18, 128, 512, 128, 1),
+]
+
+
+@pytest.mark.parametrize("dt", [0, 1, 2], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("blk", ENCODER_BLOCKS, ids=lambda b: "x".join(map(str, b)))
+def test_ir_block_plan_covers_the_output_and_fits_lds(blk, dt):
+    n, ih, iw, cin, cexp, cout, s = blk
+    spec = conv.IrBlockSpec(ih=ih, iw=iw, cin=cin, cexp=cexp, cout=cout, s=s, n=n, dt=conv.DType(dt))
+    p = spec.plan()
+    oh, ow = spec.out_hw()
+    tiles_y, tiles_x = -(-oh // p.th), -(-ow // p.tw)
+    assert p.tiles == n * tiles_y * tiles_x
+    assert 16 <= p.th * p.tw <= 256 and p.th <= oh and p.tw <= ow
+    assert cexp % p.ec == 0 and p.ec % 32 == 0 and p.chunks == cexp // p.ec
+    assert p.lds_bytes <= 160 * 1024 and p.occupancy >= 1
+    assert 1 <= p.grid <= p.tiles
+    # the LDS the kernel addresses: input tile with halo, expanded chunk, the
+    # expand / project / depthwise weights and biases of one chunk (or of all
+    # of E when they stay resident)
+    es = 4 if dt == 0 else 2
+    wn = cexp if p.resident else 2 * p.ec
+    halo = -(-(((p.th - 1) * s + 3) * ((p.tw - 1) * s + 3)) // 32) * 32
+    need = halo * (cin * es + 16) + 2 * halo * (p.ec * es + 16) + wn * (cin * es + 16) + cout * (wn * es + 16)
+    need += 9 * wn * es + (2 * wn + cout) * 4
+    assert p.lds_bytes >= need
+
+
+def test_ir_block_rejects_unfusable_shapes():
+    for kw in [dict(cin=12), dict(cexp=48), dict(cout=160), dict(cout=20), dict(s=3)]:
+        base = dict(ih=8, iw=8, cin=32, cexp=128, cout=32, s=1, dt=conv.DType.F16)
+        base.update(kw)
+        spec = conv.IrBlockSpec(**base)
+        assert not spec.fusable(), kw
+        _expect_error(spec.plan, "ir_block")
+    # fp32 needs cin % 8, 16-bit cin % 16
+    assert conv.IrBlockSpec(ih=8, iw=8, cin=8, cexp=32, cout=32, dt=conv.DType.F32).fusable()
+    assert not conv.IrBlockSpec(ih=8, iw=8, cin=8, cexp=32, cout=32, dt=conv.DType.F16).fusable()
+    d = conv.IrBlockSpec(ih=8, iw=8, cin=32, cexp=128, cout=32, residual=True).desc()
+    L = conv.lib()
+    assert L.aih_ir_block(C.byref(d), 16, 16, 16, 16, 16, 16, 16, None, 16, None) == -1
+    assert "res must be given" in conv.last_error()

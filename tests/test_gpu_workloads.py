@@ -115,8 +115,8 @@ def oracle_chain(layers, wts, x_img, h, w):
     return bufs
 
 
-def gpu_chain(layers, wts, meta, n, x, dt):
-    m = Model(layers, wts, n, meta["h"], meta["w"], meta["c"], dt=conv.DType(dt))
+def gpu_chain(layers, wts, meta, n, x, dt, fuse=False):
+    m = Model(layers, wts, n, meta["h"], meta["w"], meta["c"], dt=conv.DType(dt), fuse=fuse)
     m.upload_input(G.dev(x))
     m.infer()
     torch.cuda.synchronize()
@@ -160,6 +160,50 @@ def test_ir_block_chain_4x_64c_40x72():
     local, e2e = check_chain("ir chain 4 blocks f32", layers, wts, meta, n, x, F32, sample_images(n))
     report("ir chain local", local, 1e-4)
     report("ir chain end-to-end", e2e, 1e-4)
+
+
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
+def test_ir_block_chain_fused(dt):
+    """The four blocks as four fused launches, against the oracle's fp32 chain:
+    fp32 within 1e-4; 16-bit storage no further from it than the same model
+    run unfused (both round the expanded and depthwise tensors to dt at the
+    same places; they differ by accumulation order, i.e. by which elements
+    round up or down)."""
+    layers, meta = W.ir_chain_40x72(4)
+    wts = oracle_weights(layers, 5)
+    n = 4
+    x = orc.xs32_fill(5000, n * meta["h"] * meta["w"] * meta["c"])
+    mf = gpu_chain(layers, wts, meta, n, x, dt, fuse=True)
+    assert [op.kind for op in mf.ops] == ["ir_block"] * 4
+    got = mf.read_output().reshape(n, -1)
+    img = meta["h"] * meta["w"] * meta["c"]
+    refs = {i: oracle_chain(layers, wts, x[i * img:(i + 1) * img], meta["h"], meta["w"])[layers[-1].name]
+            for i in sample_images(n)}
+    e_fused = max(G.rel_err(got[i], refs[i]) for i in refs)
+    if dt == F32:
+        report("ir chain fused f32 end-to-end", e_fused, 1e-4)
+        return
+    mu = gpu_chain(layers, wts, meta, n, x, dt, fuse=False)
+    unf = mu.read_output().reshape(n, -1)
+    e_unfused = max(G.rel_err(unf[i], refs[i]) for i in refs)
+    print(f"ir chain dt{dt}: fused {e_fused:.3e}, unfused {e_unfused:.3e} (vs fp32 chain); "
+          f"fused vs unfused {G.rel_err(got, unf):.3e}", flush=True)
+    assert e_fused <= 1.25 * e_unfused + 2e-3, (e_fused, e_unfused)
+
+
+def test_ir_block_chain_fused_full_batch_f32():
+    """The full 64-image fp32 chain, fused: sampled images against the oracle
+    run of each image alone (images of a batch never interact)."""
+    layers, meta = W.ir_chain_40x72(64)
+    wts = oracle_weights(layers, 5)
+    n = 64
+    x = orc.xs32_fill(5001, n * meta["h"] * meta["w"] * meta["c"])
+    mf = gpu_chain(layers, wts, meta, n, x, F32, fuse=True)
+    got = mf.read_output().reshape(n, -1)
+    img = meta["h"] * meta["w"] * meta["c"]
+    e2e = max(G.rel_err(got[i], oracle_chain(layers, wts, x[i * img:(i + 1) * img], meta["h"], meta["w"])
+                        [layers[-1].name]) for i in sample_images(n))
+    report("ir chain fused f32 b64 end-to-end", e2e, 1e-4)
 
 
 def oracle_chain_stored(layers, wts, x_img, dt):
@@ -218,7 +262,7 @@ def test_mnv4_small_encoder_160x288(dt):
                           refs[i][layers[-1].name]) for i in range(n))
     print(f"encoder dt{dt}: end-to-end drift {e2e:.3e}, ideal-storage drift {ideal:.3e}", flush=True)
     assert e2e <= 3 * ideal + 1e-3, (e2e, ideal)
-    m = Model(layers, wts, n, h, w, 3, dt=conv.DType(dt))
+    m = Model(layers, wts, n, h, w, 3, dt=conv.DType(dt), fuse=False)
     worst_scaled = 0.0
     for i, L in enumerate(layers):
         shp = m.shapes[L.src]
@@ -246,3 +290,41 @@ def test_mnv4_small_encoder_160x288(dt):
               flush=True)
         assert e_gpu <= 1.25 * e_ideal + 2e-3, (L.name, e_gpu, e_ideal)
     report(f"encoder dt{dt} per-layer rms-scaled", worst_scaled, 2e-2 if dt == F16 else 0.1)
+
+
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
+def test_mnv4_small_encoder_fused(dt):
+    """The encoder with its ten blocks fused (the headline configuration).
+
+    fp32: within 1e-4 of the ai-cpu chain end to end.
+    16-bit storage: the same model run unfused rounds the same tensors at the
+    same places, so the fused run must be no further from the fp32 chain:
+    its rms-scaled end-to-end error within 1.5x (+2e-3) of the unfused run's.
+    (The literal max |g-c|/max(|c|,1) of this ill-conditioned random network
+    is dominated by a few near-zero outputs after cancellation and swings
+    between runs that differ only in rounding order; it is printed, and for
+    f16 held to 3x the ideal-storage drift as in the unfused test.)"""
+    layers, meta = W.mnv4_small_encoder_160x288(2)
+    wts = oracle_weights(layers, 6)
+    n, h, w = 2, meta["h"], meta["w"]
+    x = orc.xs32_fill(6000, n * h * w * 3)
+    m = gpu_chain(layers, wts, meta, n, x, dt, fuse=True)
+    assert sum(op.kind == "ir_block" for op in m.ops) == 10
+    got = m.read_output().reshape(n, -1)
+    img = h * w * 3
+    refs = [oracle_chain(layers, wts, x[i * img:(i + 1) * img], h, w)[layers[-1].name] for i in range(n)]
+    e2e = max(G.rel_err(got[i], refs[i]) for i in range(n))
+    if dt == F32:
+        report("encoder fused f32 end-to-end", e2e, 1e-4)
+        return
+    unf = gpu_chain(layers, wts, meta, n, x, dt, fuse=False).read_output().reshape(n, -1)
+    e2e_u = max(G.rel_err(unf[i], refs[i]) for i in range(n))
+    s_f = max(scaled_err(got[i], refs[i]) for i in range(n))
+    s_u = max(scaled_err(unf[i], refs[i]) for i in range(n))
+    ideal = max(G.rel_err(oracle_chain_stored(layers, wts, x[i * img:(i + 1) * img], dt)[layers[-1].name], refs[i])
+                for i in range(n))
+    print(f"encoder dt{dt}: literal drift fused {e2e:.3e} unfused {e2e_u:.3e} ideal-storage {ideal:.3e}; "
+          f"rms-scaled fused {s_f:.3e} unfused {s_u:.3e}", flush=True)
+    assert s_f <= 1.5 * s_u + 2e-3, (s_f, s_u)
+    if dt == F16:
+        assert e2e <= 3 * ideal + 1e-3, (e2e, ideal)
