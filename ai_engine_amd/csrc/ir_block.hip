@@ -52,7 +52,7 @@ int reg_occupancy(int dt, uint32_t nob, uint32_t npw) {
   return occ;
 }
 
-// LDS regions of the kernel: input tile, two expanded-chunk buffers, and the
+// LDS regions of the kernel: input tile, the expanded chunk, and the
 // expand / project / depthwise weights and biases for WR expanded channels
 // (all of E when the weights are resident, else two chunk slots).
 void lds_layout(uint32_t C, uint32_t CO, uint32_t WR, uint32_t NPI, int dt, IrPlan *p) {
@@ -62,7 +62,7 @@ void lds_layout(uint32_t C, uint32_t CO, uint32_t WR, uint32_t NPI, int dt, IrPl
   p->lds_x = off;
   off = align16(off + NPI * 32 * rpx);
   p->lds_xe = off;
-  off = align16(off + 2 * NPI * 32 * rpe);
+  off = align16(off + NPI * 32 * rpe);
   p->lds_we = off;
   off = align16(off + WR * rpx);
   p->lds_wp = off;

@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   // -> two slots of one chunk each (chunk c in slot c & 1).
   const uint32_t WR = a.resident ? a.E : 2 * EC;
   char *XL = lds + a.lds_x;    // [NPI*32][RPX]   input tile
-  char *XeL = lds + a.lds_xe;  // 2 x [NPI*32][RPE] expanded chunks (double buffer)
+  char *XeL = lds + a.lds_xe;  // [NPI*32][RPE]   expanded chunk
   char *WeL = lds + a.lds_we;  // [WR][RPX]       expand weights, K contiguous
   char *WpL = lds + a.lds_wp;  // [CO][RPW]       project weights, K contiguous
   char *WdL = lds + a.lds_wd;  // [9][WR]         depthwise weights (storage dtype)
@@ -137,7 +137,6 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   float *BdL = BeL + WR;                                   // [WR]
   float *BpL = BdL + WR;                                   // [CO]
   const uint32_t RPX = a.C * ES + 16, RPW = WR * ES + 16;
-  const uint32_t XEB = a.NPI * 32 * RPE;  // bytes of one expanded-chunk buffer
   const uint32_t NVX = a.C * ES / 16;     // 16-byte vectors per input pixel
   const uint32_t nchunks = a.E / EC;
   const uint32_t nks_e = a.C / KSTEP;
@@ -241,11 +240,6 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
     }
     if (expand_part && tid < NSMALL_E) st_small(s, 10, tid, ld_small(c, 10, tid));
   };
-  // streamed weights staged in registers during an iteration: the expand part
-  // of one chunk and the projection part of another
-  constexpr int WE_PT = (EC * (128 / HK) + 255) / 256;  // per thread, cin <= 128
-  constexpr int WP_PT = (128 * (EC / HK) + 255) / 256;  // per thread, cout <= 128
-  u32x4 stg_we[WE_PT], stg_wp[WP_PT], stg_be, stg_small;
 
   for (uint32_t i = tid; i < a.CO / 4; i += 256)
     *reinterpret_cast<f32x4 *>(BpL + 4 * i) = Vec4IO<DT>::load(a.bp, i);
@@ -288,10 +282,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
           if (i0 + 256 * b < nitems) *reinterpret_cast<u32x4 *>(XL + dst[b]) = val[b];
       }
     }
-    if (!a.resident) {
-      load_chunk(0, true, true);
-      if (nchunks > 1) load_chunk(1, true, false);
-    }
+    if (!a.resident) load_chunk(0, true, true);
     __syncthreads();
 
     // tap row offsets (bytes, buffer 0) of this wavefront's output pixel blocks
@@ -310,10 +301,10 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
       for (int t = 0; t < 9; ++t) rowo[i][t] = (base + (t / 3) * a.HW + t % 3) * RPE + lh * 16;
     }
 
-    // (1) expand chunk c over the halo tile -> XeL buffer (c & 1)
+    // (1) expand chunk c over the halo tile -> XeL
     auto expand = [&](uint32_t c) {
       const uint32_t ws = slot(c);
-      char *xe = XeL + (c & 1) * XEB;
+      char *xe = XeL;
       for (uint32_t b = wave; b < a.NPI; b += 4) {
         const char *ap = WeL + (ws + l32) * RPX + lh * 16;
         const char *bp = XL + (b * 32 + l32) * RPX + lh * 16;
@@ -355,40 +346,24 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
 #pragma unroll
       for (int o = 0; o < NOB; ++o) acc[i][o] = f32x16{};
 
-    expand(0);
-    __syncthreads();
-
+    // Chunk loop: expand(c) | barrier | depthwise + project(c), then the next
+    // chunk's streamed weights into the other slot | barrier.
     for (uint32_t c = 0; c < nchunks; ++c) {
-      const bool stream = !a.resident;
-      // prefetch for the next iteration: expand weights of chunk c + 2 and
-      // projection weights of chunk c + 1 (their slots are free after this
-      // iteration's barrier... they are written just before it)
-      const bool pf_we = stream && c + 2 < nchunks, pf_wp = stream && c + 1 < nchunks;
-      if (pf_we) {
-#pragma unroll
-        for (int j = 0; j < WE_PT; ++j)
-          if (tid + 256 * j < nwe) stg_we[j] = ld_we(c + 2, tid + 256 * j);
-        if (tid < NSMALL_E) stg_be = ld_small(c + 2, 10, tid);
-      }
-      if (pf_wp) {
-#pragma unroll
-        for (int j = 0; j < WP_PT; ++j)
-          if (tid + 256 * j < nwp) stg_wp[j] = ld_wp(c + 1, tid + 256 * j);
-        if (tid < NSMALL_P) stg_small = ld_small(c + 1, tid / (EC / 4), tid % (EC / 4));
-      }
-
-      if (c + 1 < nchunks) expand(c + 1);
+      expand(c);
+      __syncthreads();
 
       // (2) depthwise of chunk c straight into the projection's B operand;
       // the wavefront's pixel blocks share every K step's weight reads
       {
         const uint32_t ws = slot(c);
-        const char *xe = XeL + (c & 1) * XEB;
+        const char *xe = XeL;
         const char *wdp = WdL + ws * ES + lh * 16;
         const uint32_t wd_row = WR * ES;
         const float *bdp = BdL + ws + lh * HK;
         const char *wpp = WpL + l32 * RPW + ws * ES + lh * 16;
-#pragma unroll
+        // one K step at a time: hoisting the next step's 18 operand reads
+        // above this one doubles the live registers and halves occupancy
+#pragma unroll 1
         for (int ks = 0; ks < NKS; ++ks) {
           u32x4 wv[9];
 #pragma unroll
@@ -422,21 +397,9 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
         }
       }
 
-      // commit the prefetched weights: expand slot of chunk c + 2 held chunk
-      // c (its expand ran last iteration); projection slot of chunk c + 1
-      // held chunk c - 1 (used last iteration)
-      if (pf_we) {
-#pragma unroll
-        for (int j = 0; j < WE_PT; ++j)
-          if (tid + 256 * j < nwe) st_we(slot(c + 2), tid + 256 * j, stg_we[j]);
-        if (tid < NSMALL_E) st_small(slot(c + 2), 10, tid, stg_be);
-      }
-      if (pf_wp) {
-#pragma unroll
-        for (int j = 0; j < WP_PT; ++j)
-          if (tid + 256 * j < nwp) st_wp(slot(c + 1), tid + 256 * j, stg_wp[j]);
-        if (tid < NSMALL_P) st_small(slot(c + 1), tid / (EC / 4), tid % (EC / 4), stg_small);
-      }
+      // the other slot held chunk c - 1, whose depthwise finished before this
+      // chunk's expand
+      if (!a.resident && c + 1 < nchunks) load_chunk(c + 1, true, true);
       __syncthreads();
     }
 

@@ -10,11 +10,13 @@
   stream through the C ABI (aih_conv routes each conv like lower_op);
 * `read_output` = `Model::read_output` (:442-457).
 
-Load-time fusion (fuse=True): a 1x1 conv feeding a depthwise 3x3 feeding a
-1x1 conv, whose two intermediates have no other reader, becomes one
-aih_ir_block launch (the expanded tensor stays on chip). The fused op reads
-the same packed weights; blocks the fused kernel cannot run (aih_ir_block_plan
-fails) stay three launches.
+Load-time fusion: a 1x1 conv feeding a depthwise 3x3 feeding a 1x1 conv,
+whose two intermediates have no other reader, becomes one aih_ir_block launch
+(the expanded tensor stays on chip). The fused op reads the same packed
+weights; blocks the fused kernel cannot run (aih_ir_block_plan fails) stay
+three launches. fuse="auto" fuses 16-bit models (where the fused kernel is
+the faster one on MI355X; for fp32 the three MFMA/VALU kernels are faster),
+True / False force it.
 """
 from __future__ import annotations
 
@@ -76,7 +78,7 @@ class ModelOp:
 class Model:
     def __init__(self, layers: list[Layer], weights: Weights, n: int, ih: int, iw: int, cin: int,
                  dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0",
-                 fuse: bool = True):
+                 fuse="auto"):
         self.layers = layers
         self.n, self.ih, self.iw, self.cin = n, ih, iw, cin
         self.dt = conv.DType(dt)
@@ -106,6 +108,8 @@ class Model:
             packed[Lr.name] = (_to_device(wp, self.device), _to_device(bp, self.device))
             self.shapes[Lr.name] = Lr.out_hw() + (Lr.cout,)
 
+        if fuse == "auto":
+            fuse = self.dt != conv.DType.F32
         i = 0
         while i < len(layers):
             blk = self._match_block(layers, i, readers) if fuse else None

@@ -168,7 +168,7 @@ def test_ir_block_plan_covers_the_output_and_fits_lds(blk, dt):
     es = 4 if dt == 0 else 2
     wn = cexp if p.resident else 2 * p.ec
     halo = -(-(((p.th - 1) * s + 3) * ((p.tw - 1) * s + 3)) // 32) * 32
-    need = halo * (cin * es + 16) + 2 * halo * (p.ec * es + 16) + wn * (cin * es + 16) + cout * (wn * es + 16)
+    need = halo * (cin * es + 16) + halo * (p.ec * es + 16) + wn * (cin * es + 16) + cout * (wn * es + 16)
     need += 9 * wn * es + (2 * wn + cout) * 4
     assert p.lds_bytes >= need
 
