@@ -149,6 +149,7 @@ def main() -> int:
     else:
         roofline = dict(bound="mfma", achieved=round(dr["tflops"], 2), peak=PEAK_TF[args.dtype], unit="TFLOP/s",
                         frac=round(dr["tflops"] / PEAK_TF[args.dtype], 4), traffic=None)
+    roofline["traffic"] = measured_traffic(dom_key)
     roofline.update(kernel=dom_key, launches_per_step=dom["launches"],
                     avg_launch_us=round(dom["secs"] / dom["launches"] * 1e6, 2),
                     algorithmic_bytes_per_launch=int(dom["bytes"] / dom["launches"]),
@@ -197,6 +198,21 @@ def main() -> int:
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def measured_traffic(key: str):
+    """HBM bytes per launch of kernel `key` as the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary under profiles/ reports it (calibrated against a 1 GiB
+    copy in the same run), or None when no summary covers this kernel."""
+    import glob
+    import re
+
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*hbm_traffic*.md"))):
+        for line in open(path):
+            m = re.match(r"traffic_bytes_per_launch (.+) = (\d+)\s*$", line)
+            if m and m.group(1) == key:
+                return int(m.group(2))
+    return None
 
 
 def kernel_key(conv, op, n, dt, dtname) -> str:
