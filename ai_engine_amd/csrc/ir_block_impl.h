@@ -120,7 +120,10 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   constexpr int EC = IR_EC;             // expanded channels per chunk
   constexpr int NKS = EC / KSTEP;       // projection K steps per chunk
   constexpr int RPE = EC * ES + 16;     // expanded-chunk LDS row pitch
-  constexpr int LB = 4;                 // global loads in flight per thread in the copy loops
+  // Loads in flight per thread in the copy loops: batching them costs more
+  // registers than it saves in latency -- the kernel is occupancy-bound.
+  constexpr int LB = 1;                 // weights
+  constexpr int LBX = 1;                // input tile
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, l32 = lane & 31, lh = lane >> 5;
@@ -261,11 +264,11 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
     // streamed weights the first chunks: expand of 0 and 1, projection of 0
     {
       const uint32_t nitems = a.NPI * 32 * NVX;
-      for (uint32_t i0 = tid; i0 < nitems; i0 += 256 * LB) {
-        u32x4 val[LB];
-        uint32_t dst[LB];
+      for (uint32_t i0 = tid; i0 < nitems; i0 += 256 * LBX) {
+        u32x4 val[LBX];
+        uint32_t dst[LBX];
 #pragma unroll
-        for (int b = 0; b < LB; ++b) {
+        for (int b = 0; b < LBX; ++b) {
           const uint32_t i = i0 + 256 * b;
           if (i < nitems) {
             const uint32_t r = fdiv(i, a.fd_nvx), v = i - r * NVX;
@@ -278,7 +281,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
           }
         }
 #pragma unroll
-        for (int b = 0; b < LB; ++b)
+        for (int b = 0; b < LBX; ++b)
           if (i0 + 256 * b < nitems) *reinterpret_cast<u32x4 *>(XL + dst[b]) = val[b];
       }
     }
