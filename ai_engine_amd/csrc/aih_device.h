@@ -149,34 +149,52 @@ __device__ __forceinline__ f32x4 act_apply4(int act, f32x4 v) {
 // The activation as wave-uniform parameters, so that inner loops apply it
 // without a per-element switch: every activation the converter fuses into a
 // conv is one of
-//   LINEAR  v = x*s + t                      none (s = 1, t = -0: exact identity), neg
-//   CLAMP   v = min(max(x*s + t, lo), hi)    relu, relu6, clamp01, hardsigmoid
-//   XCLAMP  v = x * min(max(x*s + t, lo), hi)  hardswish
+//   IDENT   v = x                              none
+//   LINEAR  v = x*s + t                        neg
+//   RELU    v = max(x, 0)                      relu
+//   CLAMP0  v = min(max(x, 0), hi)             relu6, clamp01
+//   CLAMP   v = min(max(x*s + t, 0), hi)       hardsigmoid
+//   XCLAMP  v = x * min(max(x*s + t, 0), hi)   hardswish
 // and the transcendental ones (sigmoid, tanh, sqrt, recip) go through act_apply.
+// Clamps to [0, hi] with hi >= 0 are taken on the float bits as signed
+// integers, whose order agrees with the floats' for non-negative values while
+// every negative float (and -0) is a negative integer: one v_max_i32 /
+// v_med3_i32 instead of a float max that must first quiet signalling NaNs.
+// They return +0 for negative inputs (and -0) like max(x, 0); NaN inputs are
+// the one difference from the float form (a NaN with the sign bit clear is
+// kept, one with it set becomes 0).
 struct Act {
-  float s, t, lo, hi;
+  float s, t, hi;
+  int hib;  // bits of hi
   int mode;
   int act;
 };
-enum : int { ACT_LINEAR = 0, ACT_CLAMP = 1, ACT_XCLAMP = 2, ACT_SPECIAL = 3, ACT_IDENT = 4, ACT_RELU = 5 };
+enum : int { ACT_LINEAR = 0, ACT_CLAMP = 1, ACT_XCLAMP = 2, ACT_SPECIAL = 3, ACT_IDENT = 4, ACT_RELU = 5,
+             ACT_CLAMP0 = 6 };
 
 __device__ __forceinline__ Act act_params(int act) {
-  Act p{1.0f, -0.0f, -__builtin_inff(), __builtin_inff(), ACT_LINEAR, act};
+  Act p{1.0f, -0.0f, 0.0f, 0, ACT_LINEAR, act};
   switch (act) {
     case AIH_ACT_NONE: p.mode = ACT_IDENT; break;
     case AIH_ACT_NEG: p.s = -1.0f; break;
-    case AIH_ACT_RELU: p.mode = ACT_RELU; p.lo = 0.0f; break;
-    case AIH_ACT_RELU6: p.mode = ACT_CLAMP; p.lo = 0.0f; p.hi = 6.0f; break;
-    case AIH_ACT_CLAMP01: p.mode = ACT_CLAMP; p.lo = 0.0f; p.hi = 1.0f; break;
+    case AIH_ACT_RELU: p.mode = ACT_RELU; break;
+    case AIH_ACT_RELU6: p.mode = ACT_CLAMP0; p.hi = 6.0f; break;
+    case AIH_ACT_CLAMP01: p.mode = ACT_CLAMP0; p.hi = 1.0f; break;
     case AIH_ACT_HARDSIGMOID:
-      p.mode = ACT_CLAMP; p.s = 1.0f / 6.0f; p.t = 0.5f; p.lo = 0.0f; p.hi = 1.0f;
+      p.mode = ACT_CLAMP; p.s = 1.0f / 6.0f; p.t = 0.5f; p.hi = 1.0f;
       break;
     case AIH_ACT_HARDSWISH:
-      p.mode = ACT_XCLAMP; p.s = 1.0f / 6.0f; p.t = 0.5f; p.lo = 0.0f; p.hi = 1.0f;
+      p.mode = ACT_XCLAMP; p.s = 1.0f / 6.0f; p.t = 0.5f; p.hi = 1.0f;
       break;
     default: p.mode = ACT_SPECIAL; break;
   }
+  p.hib = __float_as_int(p.hi);
   return p;
+}
+
+__device__ __forceinline__ float act_relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+__device__ __forceinline__ float act_clamp_bits(float x, int hib) {
+  return __int_as_float(min(max(__float_as_int(x), 0), hib));
 }
 
 // Applies p to N values; the only branch is on the uniform mode.
@@ -187,7 +205,11 @@ __device__ __forceinline__ void act_array(const Act &p, float (&v)[N]) {
       break;
     case ACT_RELU:
 #pragma unroll
-      for (int j = 0; j < N; ++j) v[j] = fmaxf(v[j], 0.0f);
+      for (int j = 0; j < N; ++j) v[j] = act_relu_bits(v[j]);
+      break;
+    case ACT_CLAMP0:
+#pragma unroll
+      for (int j = 0; j < N; ++j) v[j] = act_clamp_bits(v[j], p.hib);
       break;
     case ACT_LINEAR:
 #pragma unroll
@@ -195,11 +217,11 @@ __device__ __forceinline__ void act_array(const Act &p, float (&v)[N]) {
       break;
     case ACT_CLAMP:
 #pragma unroll
-      for (int j = 0; j < N; ++j) v[j] = fminf(fmaxf(v[j] * p.s + p.t, p.lo), p.hi);
+      for (int j = 0; j < N; ++j) v[j] = act_clamp_bits(v[j] * p.s + p.t, p.hib);
       break;
     case ACT_XCLAMP:
 #pragma unroll
-      for (int j = 0; j < N; ++j) v[j] = v[j] * fminf(fmaxf(v[j] * p.s + p.t, p.lo), p.hi);
+      for (int j = 0; j < N; ++j) v[j] = v[j] * act_clamp_bits(v[j] * p.s + p.t, p.hib);
       break;
     default:
 #pragma unroll

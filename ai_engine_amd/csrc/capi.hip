@@ -230,6 +230,12 @@ int check_ir(const aih_ir_block_desc *d, uint32_t *oh, uint32_t *ow) {
   if ((uint64_t)d->n * d->ih * d->iw * d->cin > 0xffffffffull / 4 ||
       (uint64_t)d->n * *oh * *ow * d->cout > 0xffffffffull / 4)
     return fail("ir_block: tensor too large");
+  // the kernel addresses one image of x and each weight tensor with 31-bit
+  // byte offsets (buffer resources)
+  const uint64_t es = d->dt == AIH_F32 ? 4 : 2;
+  if ((uint64_t)d->ih * d->iw * d->cin * es >= 0x80000000ull || (uint64_t)d->cin * d->cexp * es >= 0x80000000ull ||
+      (uint64_t)d->cexp * d->cout * es >= 0x80000000ull)
+    return fail("ir_block: image or weights of 2 GiB or more");
   return AIH_OK;
 }
 
@@ -484,18 +490,14 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
     a.lds_xe = p.lds_xe;
     a.lds_we = p.lds_we;
     a.lds_wp = p.lds_wp;
-    a.lds_wd = p.lds_wd;
-    a.lds_b = p.lds_b;
+    a.lds_sm = p.lds_sm;
+    a.lds_bp = p.lds_bp;
     const uint32_t es = d->dt == AIH_F32 ? 4 : 2;
-    const uint32_t wn = p.resident ? d->cexp : p.EC;
-    a.fd_nvx = aih::make_fastdiv(d->cin * es / 16);
+    a.fd_rpx = aih::make_fastdiv(d->cin * es / 16 + 1);
     a.fd_hw = aih::make_fastdiv(p.HW);
     a.fd_tw = aih::make_fastdiv(p.TW);
     a.fd_tx = aih::make_fastdiv(p.tiles_x);
     a.fd_pi = aih::make_fastdiv(p.tiles_x * p.tiles_y);
-    a.fd_co = aih::make_fastdiv(d->cout);
-    a.fd_wn = aih::make_fastdiv(wn);
-    a.fd_wn4 = aih::make_fastdiv(wn / 4);
     hipError_t e = aih::launch_ir_block(a, d->dt, p.lds, p.grid, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(std::string("ir_block launch: ") + hipGetErrorString(e));
     return AIH_OK;

@@ -13,9 +13,9 @@ namespace aih {
 // NHWC-C4 with the batch outermost, weights in the converter's packed layouts.
 struct IrArgs {
   const void *x;         // [N][IH][IW][C]
-  const void *we, *be;   // expand weights [kg][E/4][4][4], bias [E]
+  const void *we, *be;   // expand weights [C/4][E][4], bias [E]
   const void *wd, *bd;   // depthwise weights [9][E/4][4], bias [E]
-  const void *wp, *bp;   // project weights [kg][CO/4][4][4], bias [CO]
+  const void *wp, *bp;   // project weights [E/4][CO][4], bias [CO]
   const void *res;       // [N][OH][OW][CO] or null
   void *y;               // [N][OH][OW][CO]
   uint32_t N, IH, IW, OH, OW;
@@ -29,20 +29,18 @@ struct IrArgs {
   uint32_t resident;     // 1: all E channels' weights stay in LDS for every tile
   uint32_t tiles_y, tiles_x, ntiles;
   int32_t act_e, act_d, act_p, has_res;
-  uint32_t lds_x, lds_xe, lds_we, lds_wp, lds_wd, lds_b;  // LDS byte offsets
+  uint32_t lds_x, lds_xe, lds_we, lds_wp, lds_sm, lds_bp;  // LDS byte offsets
   // divisors the kernel uses, prepared on the host
-  FastDiv fd_nvx;              // 16-byte vectors per input pixel
+  FastDiv fd_rpx;              // 16-byte items per LDS input row (vectors per pixel + 1)
   FastDiv fd_hw, fd_tw;        // halo tile width, output tile width
   FastDiv fd_tx, fd_pi;        // tiles per row, tiles per image
-  FastDiv fd_co;               // project output channels
-  FastDiv fd_wn, fd_wn4;       // weight channels loaded at once (E or EC), and / 4
 };
 
 // Tile / chunk geometry of one launch, chosen by ir_plan.
 struct IrPlan {
   uint32_t TH, TW, HH, HW, NPI, NPB, EC, resident;
   uint32_t tiles_y, tiles_x, ntiles;
-  uint32_t lds_x, lds_xe, lds_we, lds_wp, lds_wd, lds_b, lds;  // LDS byte offsets and total
+  uint32_t lds_x, lds_xe, lds_we, lds_wp, lds_sm, lds_bp, lds;  // LDS byte offsets and total
   uint32_t occ, grid;  // workgroups per CU, launched workgroups
 };
 

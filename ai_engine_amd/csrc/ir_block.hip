@@ -52,25 +52,26 @@ int reg_occupancy(int dt, uint32_t nob, uint32_t npw) {
   return occ;
 }
 
-// LDS regions of the kernel: input tile, the expanded chunk, and the
-// expand / project / depthwise weights and biases for WR expanded channels
-// (all of E when the weights are resident, else two chunk slots).
+// LDS regions of the kernel: input tile, the expanded chunk, and WR/32 weight
+// slots, each holding one 32-channel chunk's expand, project and depthwise
+// weights and biases in their packed layouts (all of E when the weights are
+// resident, else two slots), and the fp32 projection bias.
 void lds_layout(uint32_t C, uint32_t CO, uint32_t WR, uint32_t NPI, int dt, IrPlan *p) {
   const uint32_t es = dt == DT_F32 ? 4 : 2;
-  const uint32_t rpx = C * es + 16, rpe = IR_EC * es + 16, rpw = WR * es + 16;
+  const uint32_t rpx = C * es + 16, rpe = IR_EC * es + 16;
   uint32_t off = 0;
   p->lds_x = off;
   off = align16(off + NPI * 32 * rpx);
   p->lds_xe = off;
   off = align16(off + NPI * 32 * rpe);
   p->lds_we = off;
-  off = align16(off + WR * rpx);
+  off = align16(off + WR * C * es);
   p->lds_wp = off;
-  off = align16(off + CO * rpw);
-  p->lds_wd = off;
-  off = align16(off + 9 * WR * es);
-  p->lds_b = off;
-  off = align16(off + (2 * WR + CO) * 4);
+  off = align16(off + WR * CO * es);
+  p->lds_sm = off;
+  off = align16(off + WR * 11 * es);
+  p->lds_bp = off;
+  off = align16(off + CO * 4);
   p->lds = off;
 }
 

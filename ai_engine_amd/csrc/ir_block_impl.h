@@ -110,6 +110,46 @@ __device__ __forceinline__ void ir_fma_taps(u32x4 xv, u32x4 wv, float (&d)[HK]) 
   }
 }
 
+// Global -> LDS copies without registers: buffer_load_dword{,x4} ... lds
+// writes lane i's SZ bytes to LDS at a wavefront-uniform base + SZ * i.
+// A lane whose offset lies at or past the buffer's size writes zeros.
+typedef __attribute__((address_space(3))) void ir_lds_void;
+// An offset past every buffer the kernel reads (the host keeps each below 2 GiB).
+constexpr uint32_t IR_OOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ir_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+
+// Copies n items of SZ bytes to dst[0, n * SZ), item g from byte offset src(g)
+// of the buffer. The four wavefronts take 64-item rows in turn, the first row
+// going to wavefront w0. The copy is asynchronous: ir_dma_wait() and then a
+// workgroup barrier publish it.
+template <int SZ, class F>
+__device__ __forceinline__ void ir_dma(char *dst, uint32_t n, __amdgpu_buffer_rsrc_t rs, int wave, int lane, int w0,
+                                       F src) {
+  for (uint32_t g0 = (uint32_t)((wave - w0) & 3) * 64; g0 < n; g0 += 256) {
+    const uint32_t g = g0 + lane;
+    if (g < n) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (ir_lds_void *)(dst + g0 * SZ), SZ, src(g), 0, 0, 0);
+  }
+}
+
+// This wavefront's copies to LDS (and every other global load) have landed.
+__device__ __forceinline__ void ir_dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// A weight operand of one lane: HK consecutive K of one output channel, held
+// in LDS as packed groups of 4 K (pack.rs:95) -- one 16-byte group for fp32,
+// two 8-byte groups `next` bytes apart for 16-bit storage.
+template <int DT>
+__device__ __forceinline__ u32x4 ir_ld_w(const char *p, uint32_t next) {
+  if constexpr (DT == DT_F32) {
+    return *reinterpret_cast<const u32x4 *>(p);
+  } else {
+    const u32x2 lo = *reinterpret_cast<const u32x2 *>(p), hi = *reinterpret_cast<const u32x2 *>(p + next);
+    return u32x4{lo.x, lo.y, hi.x, hi.y};
+  }
+}
+
 template <int DT, int NOB, int NPW>
 __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   extern __shared__ __align__(16) char lds[];
@@ -120,33 +160,34 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   constexpr int EC = IR_EC;             // expanded channels per chunk
   constexpr int NKS = EC / KSTEP;       // projection K steps per chunk
   constexpr int RPE = EC * ES + 16;     // expanded-chunk LDS row pitch
-  // Loads in flight per thread in the copy loops: batching them costs more
-  // registers than it saves in latency -- the kernel is occupancy-bound.
-  constexpr int LB = 1;                 // weights
-  constexpr int LBX = 1;                // input tile
+  constexpr uint32_t GB = 4 * ES;       // bytes of one packed weight group (4 K of one channel)
+  constexpr uint32_t SMB = 11 * EC * ES;  // per-chunk small tensors: 9 depthwise taps, its bias, expand bias
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6, l32 = lane & 31, lh = lane >> 5;
+  const int lane = tid & 63, l32 = lane & 31, lh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // Weight slots: resident -> the whole E (chunk c at channel 32c); streamed
-  // -> two slots of one chunk each (chunk c in slot c & 1).
-  const uint32_t WR = a.resident ? a.E : 2 * EC;
+  // Weight slots: resident -> one per chunk (all of E); streamed -> two,
+  // chunk c in slot c & 1. Every slot holds the chunk's weights byte for byte
+  // as packed by the converter:
+  //   WeL [slot][C/4 groups][32 channels][GB]    expand, group kq of channel e
+  //   WpL [slot][EC/4 groups][CO][GB]            project (one contiguous range)
+  //   SmL [slot][11][32] x ES                    depthwise taps 0..8, depthwise bias, expand bias
   char *XL = lds + a.lds_x;    // [NPI*32][RPX]   input tile
   char *XeL = lds + a.lds_xe;  // [NPI*32][RPE]   expanded chunk
-  char *WeL = lds + a.lds_we;  // [WR][RPX]       expand weights, K contiguous
-  char *WpL = lds + a.lds_wp;  // [CO][RPW]       project weights, K contiguous
-  char *WdL = lds + a.lds_wd;  // [9][WR]         depthwise weights (storage dtype)
-  float *BeL = reinterpret_cast<float *>(lds + a.lds_b);  // [WR]
-  float *BdL = BeL + WR;                                   // [WR]
-  float *BpL = BdL + WR;                                   // [CO]
-  const uint32_t RPX = a.C * ES + 16, RPW = WR * ES + 16;
+  char *WeL = lds + a.lds_we;
+  char *WpL = lds + a.lds_wp;
+  char *SmL = lds + a.lds_sm;
+  float *BpL = reinterpret_cast<float *>(lds + a.lds_bp);  // [CO] fp32
+  const uint32_t RPX = a.C * ES + 16;
   const uint32_t NVX = a.C * ES / 16;     // 16-byte vectors per input pixel
   const uint32_t nchunks = a.E / EC;
   const uint32_t nks_e = a.C / KSTEP;
   const uint32_t HPIX = a.HH * a.HW;
   const uint32_t TPIX = a.TH * a.TW;
+  const uint32_t WES = EC * a.C * ES, WPS = EC * a.CO * ES;  // bytes of one slot
   const Act act_e = act_params(a.act_e), act_d = act_params(a.act_d), act_p = act_params(a.act_p);
-  auto slot = [&](uint32_t c) -> uint32_t { return a.resident ? c * EC : (c & 1) * EC; };
+  auto slot = [&](uint32_t c) -> uint32_t { return a.resident ? c : (c & 1); };
 
   const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x);
   const uint32_t t_begin = (uint32_t)(((uint64_t)blk * a.ntiles) / gridDim.x);
@@ -154,101 +195,41 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   if (t_begin >= t_end) return;
 
   const char *xg = reinterpret_cast<const char *>(a.x);
-  const char *weg = reinterpret_cast<const char *>(a.we);
-  const char *wpg = reinterpret_cast<const char *>(a.wp);
+  const __amdgpu_buffer_rsrc_t rs_we = ir_rsrc(a.we, a.C * a.E * ES);
+  const __amdgpu_buffer_rsrc_t rs_wp = ir_rsrc(a.wp, a.E * a.CO * ES);
+  const __amdgpu_buffer_rsrc_t rs_wd = ir_rsrc(a.wd, 9 * a.E * ES);
+  const __amdgpu_buffer_rsrc_t rs_bd = ir_rsrc(a.bd, a.E * ES);
+  const __amdgpu_buffer_rsrc_t rs_be = ir_rsrc(a.be, a.E * ES);
 
-  // ---- weights of chunk c (channels [32c, 32c + 32)) -> weight slot s --------
+  // ---- weights of chunk c (expanded channels [32c, 32c + 32)) -> slot s ----
   // Packed 1x1 weights hold element (k, n) at (k/4 * Nn + n) * 4 + k%4
-  // (pack.rs:95 with one tap), so HK consecutive K of one output channel are
-  // one (fp32) or two (16-bit) vectors of 4.
-  auto ld_we = [&](uint32_t c, uint32_t i) -> u32x4 {  // item i = (kq, e)
-    const uint32_t kq = i / EC, e = i - kq * EC;
-    if constexpr (F32) {
-      return *reinterpret_cast<const u32x4 *>(weg + ((size_t)kq * a.E + c * EC + e) * 16);
-    } else {
-      const u32x2 lo = *reinterpret_cast<const u32x2 *>(weg + ((size_t)(2 * kq) * a.E + c * EC + e) * 8);
-      const u32x2 hi = *reinterpret_cast<const u32x2 *>(weg + ((size_t)(2 * kq + 1) * a.E + c * EC + e) * 8);
-      return u32x4{lo.x, lo.y, hi.x, hi.y};
-    }
-  };
-  auto st_we = [&](uint32_t s, uint32_t i, u32x4 v) {
-    const uint32_t kq = i / EC, e = i - kq * EC;
-    *reinterpret_cast<u32x4 *>(WeL + (s + e) * RPX + kq * 16) = v;
-  };
-  auto ld_wp = [&](uint32_t c, uint32_t i) -> u32x4 {  // item i = (kq, o)
-    const uint32_t kq = fdiv(i, a.fd_co), o = i - kq * a.CO;
-    const uint32_t kg = c * (EC / 4) + kq * (HK / 4);
-    if constexpr (F32) {
-      return *reinterpret_cast<const u32x4 *>(wpg + ((size_t)kg * a.CO + o) * 16);
-    } else {
-      const u32x2 lo = *reinterpret_cast<const u32x2 *>(wpg + ((size_t)kg * a.CO + o) * 8);
-      const u32x2 hi = *reinterpret_cast<const u32x2 *>(wpg + ((size_t)(kg + 1) * a.CO + o) * 8);
-      return u32x4{lo.x, lo.y, hi.x, hi.y};
-    }
-  };
-  auto st_wp = [&](uint32_t s, uint32_t i, u32x4 v) {
-    const uint32_t kq = fdiv(i, a.fd_co), o = i - kq * a.CO;
-    *reinterpret_cast<u32x4 *>(WpL + o * RPW + (s + kq * HK) * ES) = v;
-  };
-  // Small per-chunk tensors, EC/4 vec4 per row: rows 0..8 depthwise weights
-  // and row 9 its bias travel with the projection part; row 10, the expand
-  // bias, travels with the expand part.
-  constexpr int NSMALL_P = 10 * (EC / 4), NSMALL_E = EC / 4;
-  auto ld_small = [&](uint32_t c, uint32_t row, uint32_t g) -> u32x4 {
-    if (row < 9) {
-      const size_t vi = (size_t)row * (a.E / 4) + c * (EC / 4) + g;
-      if constexpr (F32) return reinterpret_cast<const u32x4 *>(a.wd)[vi];
-      const u32x2 h = reinterpret_cast<const u32x2 *>(a.wd)[vi];
-      return u32x4{h.x, h.y, 0u, 0u};
-    }
-    return __builtin_bit_cast(u32x4, Vec4IO<DT>::load(row == 9 ? a.bd : a.be, c * (EC / 4) + g));  // fp32
-  };
-  auto st_small = [&](uint32_t s, uint32_t row, uint32_t g, u32x4 v) {
-    if (row < 9) {
-      char *dst = WdL + ((size_t)row * WR + s + 4 * g) * ES;
-      if constexpr (F32)
-        *reinterpret_cast<u32x4 *>(dst) = v;
-      else
-        *reinterpret_cast<u32x2 *>(dst) = u32x2{v.x, v.y};
-    } else {
-      *reinterpret_cast<u32x4 *>((row == 9 ? BdL : BeL) + s + 4 * g) = v;
-    }
-  };
-  const uint32_t nwe = EC * (a.C / HK), nwp = a.CO * (EC / HK);
-  // synchronous load of chunk c's weights (batched so the loads overlap)
-  auto load_chunk = [&](uint32_t c, bool expand_part, bool project_part) {
-    const uint32_t s = slot(c);
-    if (expand_part) {
-      for (uint32_t i0 = tid; i0 < nwe; i0 += 256 * LB) {
-        u32x4 v[LB];
-#pragma unroll
-        for (int b = 0; b < LB; ++b)
-          if (i0 + 256 * b < nwe) v[b] = ld_we(c, i0 + 256 * b);
-#pragma unroll
-        for (int b = 0; b < LB; ++b)
-          if (i0 + 256 * b < nwe) st_we(s, i0 + 256 * b, v[b]);
-      }
-    }
-    if (project_part) {
-      for (uint32_t i0 = tid; i0 < nwp; i0 += 256 * LB) {
-        u32x4 v[LB];
-#pragma unroll
-        for (int b = 0; b < LB; ++b)
-          if (i0 + 256 * b < nwp) v[b] = ld_wp(c, i0 + 256 * b);
-#pragma unroll
-        for (int b = 0; b < LB; ++b)
-          if (i0 + 256 * b < nwp) st_wp(s, i0 + 256 * b, v[b]);
-      }
-      if (tid < NSMALL_P) st_small(s, tid / (EC / 4), tid % (EC / 4), ld_small(c, tid / (EC / 4), tid % (EC / 4)));
-    }
-    if (expand_part && tid < NSMALL_E) st_small(s, 10, tid, ld_small(c, 10, tid));
+  // (pack.rs:95 with one tap): the chunk's expand weights are C/4 runs of
+  // 32 * GB bytes, its project weights one run of WPS bytes; depthwise
+  // weights [tap][E/4][4] give 9 runs of 32 * ES bytes.
+  auto dma_chunk = [&](uint32_t c, uint32_t s) {
+    constexpr uint32_t GR = EC * GB / 16;  // 16-byte items per expand run
+    ir_dma<16>(WeL + s * WES, (a.C / 4) * GR, rs_we, wave, lane, 0, [&](uint32_t g) -> uint32_t {
+      return ((g / GR) * a.E + EC * c) * GB + (g % GR) * 16;
+    });
+    ir_dma<16>(WpL + s * WPS, WPS / 16, rs_wp, wave, lane, 1, [&](uint32_t g) -> uint32_t { return c * WPS + g * 16; });
+    constexpr uint32_t TR = EC * ES / 16;  // 16-byte items per depthwise tap run
+    char *sm = SmL + s * SMB;
+    ir_dma<16>(sm, 9 * TR, rs_wd, wave, lane, 2, [&](uint32_t g) -> uint32_t {
+      return ((g / TR) * a.E + EC * c) * ES + (g % TR) * 16;
+    });
+    // biases need only 4-byte alignment: copied 4 bytes per lane
+    ir_dma<4>(sm + 9 * EC * ES, EC * ES / 4, rs_bd, wave, lane, 3,
+              [&](uint32_t g) -> uint32_t { return EC * c * ES + g * 4; });
+    ir_dma<4>(sm + 10 * EC * ES, EC * ES / 4, rs_be, wave, lane, 0,
+              [&](uint32_t g) -> uint32_t { return EC * c * ES + g * 4; });
   };
 
   for (uint32_t i = tid; i < a.CO / 4; i += 256)
     *reinterpret_cast<f32x4 *>(BpL + 4 * i) = Vec4IO<DT>::load(a.bp, i);
   if (a.resident)
-    for (uint32_t c = 0; c < nchunks; ++c) load_chunk(c, true, true);
+    for (uint32_t c = 0; c < nchunks; ++c) dma_chunk(c, c);
 
+  const uint32_t img_bytes = a.IH * a.IW * a.C * ES;
   for (uint32_t T = t_begin; T < t_end; ++T) {
     const uint32_t per_img = a.tiles_y * a.tiles_x;
     const uint32_t img = fdiv(T, a.fd_pi);
@@ -256,39 +237,27 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
     const uint32_t tyi = fdiv(trem, a.fd_tx);
     const uint32_t ty0 = tyi * a.TH, tx0 = (trem - tyi * a.tiles_x) * a.TW;
     const int32_t iy0 = (int32_t)(ty0 * a.S) - a.PT, ix0 = (int32_t)(tx0 * a.S) - a.PL;
-    const size_t img_px = (size_t)img * a.IH * a.IW;
 
     // every wavefront is done with the previous tile's LDS
     __syncthreads();
-    // (0) input tile with halo -> XL (zero outside the image), and for
-    // streamed weights the first chunks: expand of 0 and 1, projection of 0
+    // (0) input tile with halo -> XL: item g is 16 bytes of halo row
+    // r = g / (NVX + 1); the row's last item (the pitch padding) and pixels
+    // outside the image read as zeros. Streamed weights: chunk 0 -> slot 0.
     {
-      const uint32_t nitems = a.NPI * 32 * NVX;
-      for (uint32_t i0 = tid; i0 < nitems; i0 += 256 * LBX) {
-        u32x4 val[LBX];
-        uint32_t dst[LBX];
-#pragma unroll
-        for (int b = 0; b < LBX; ++b) {
-          const uint32_t i = i0 + 256 * b;
-          if (i < nitems) {
-            const uint32_t r = fdiv(i, a.fd_nvx), v = i - r * NVX;
-            const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
-            const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
-            dst[b] = r * RPX + v * 16;
-            val[b] = u32x4{};
-            if (r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW)
-              val[b] = *reinterpret_cast<const u32x4 *>(xg + (img_px + (size_t)iy * a.IW + ix) * a.C * ES + v * 16);
-          }
-        }
-#pragma unroll
-        for (int b = 0; b < LBX; ++b)
-          if (i0 + 256 * b < nitems) *reinterpret_cast<u32x4 *>(XL + dst[b]) = val[b];
-      }
+      const __amdgpu_buffer_rsrc_t rs_x = ir_rsrc(xg + (size_t)img * img_bytes, img_bytes);
+      ir_dma<16>(XL, a.NPI * 32 * (NVX + 1), rs_x, wave, lane, 0, [&](uint32_t g) -> uint32_t {
+        const uint32_t r = fdiv(g, a.fd_rpx), v = g - r * (NVX + 1);
+        const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
+        const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
+        const bool in = v < NVX && r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
+        return in ? ((uint32_t)iy * a.IW + (uint32_t)ix) * (NVX * 16) + v * 16 : IR_OOB;
+      });
     }
-    if (!a.resident) load_chunk(0, true, true);
+    if (!a.resident) dma_chunk(0, 0);
+    ir_dma_wait();
     __syncthreads();
 
-    // tap row offsets (bytes, buffer 0) of this wavefront's output pixel blocks
+    // tap row offsets (bytes) of this wavefront's output pixel blocks
     uint32_t rowo[NPW][9];
     bool live[NPW];
 #pragma unroll
@@ -306,17 +275,19 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
 
     // (1) expand chunk c over the halo tile -> XeL
     auto expand = [&](uint32_t c) {
-      const uint32_t ws = slot(c);
-      char *xe = XeL;
+      const uint32_t s = slot(c);
+      // lane: channel l32 of the chunk, K groups from 2*lh (16-bit) / lh (fp32);
+      // a K step advances KSTEP/4 groups = 1024 bytes
+      const char *ap = WeL + s * WES + ((uint32_t)lh * (HK / 4) * EC + l32) * GB;
+      const char *bes = SmL + s * SMB + 10 * EC * ES;
       for (uint32_t b = wave; b < a.NPI; b += 4) {
-        const char *ap = WeL + (ws + l32) * RPX + lh * 16;
         const char *bp = XL + (b * 32 + l32) * RPX + lh * 16;
         f32x16 acc = {};
-        u32x4 a0 = *reinterpret_cast<const u32x4 *>(ap), b0 = *reinterpret_cast<const u32x4 *>(bp);
+        u32x4 a0 = ir_ld_w<DT>(ap, EC * GB), b0 = *reinterpret_cast<const u32x4 *>(bp);
         for (uint32_t ks = 0; ks < nks_e; ++ks) {
           u32x4 a1 = a0, b1 = b0;
           if (ks + 1 < nks_e) {
-            a1 = *reinterpret_cast<const u32x4 *>(ap + (ks + 1) * 32);
+            a1 = ir_ld_w<DT>(ap + (ks + 1) * (KSTEP * EC * ES), EC * GB);
             b1 = *reinterpret_cast<const u32x4 *>(bp + (ks + 1) * 32);
           }
           acc = ir_mma<DT>(a0, b0, acc);
@@ -327,18 +298,25 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
         const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
         const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
         const bool inside = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
+        // pixels outside the image: the masking is skipped for blocks wholly
+        // inside (a wave-uniform test)
+        const bool mask = !__all(inside);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t el = 8 * q + 4 * lh;
           float v[4] = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
-          const f32x4 bb = *reinterpret_cast<const f32x4 *>(BeL + ws + el);
+          f32x4 bb;
+          if constexpr (F32)
+            bb = *reinterpret_cast<const f32x4 *>(bes + el * 4);
+          else
+            bb = unpack4<DT>(*reinterpret_cast<const u32x2 *>(bes + el * 2));
           v[0] += bb.x; v[1] += bb.y; v[2] += bb.z; v[3] += bb.w;
           act_array<4>(act_e, v);
-          if (!inside) v[0] = v[1] = v[2] = v[3] = 0.0f;
+          if (mask && !inside) v[0] = v[1] = v[2] = v[3] = 0.0f;
           if constexpr (F32)
-            *reinterpret_cast<f32x4 *>(xe + r * RPE + el * 4) = f32x4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<f32x4 *>(XeL + r * RPE + el * 4) = f32x4{v[0], v[1], v[2], v[3]};
           else
-            *reinterpret_cast<u32x2 *>(xe + r * RPE + el * 2) = pack4<DT>(f32x4{v[0], v[1], v[2], v[3]});
+            *reinterpret_cast<u32x2 *>(XeL + r * RPE + el * 2) = pack4<DT>(f32x4{v[0], v[1], v[2], v[3]});
         }
       }
     };
@@ -349,34 +327,32 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
 #pragma unroll
       for (int o = 0; o < NOB; ++o) acc[i][o] = f32x16{};
 
-    // Chunk loop: expand(c) | barrier | depthwise + project(c), then the next
-    // chunk's streamed weights into the other slot | barrier.
+    // Chunk loop: the next chunk's streamed weights start towards the other
+    // slot (last read by chunk c - 1, before the barrier that closed it), then
+    // expand(c) | barrier | depthwise + project(c) | copies landed + barrier.
     for (uint32_t c = 0; c < nchunks; ++c) {
+      if (!a.resident && c + 1 < nchunks) dma_chunk(c + 1, (c + 1) & 1);
       expand(c);
       __syncthreads();
 
       // (2) depthwise of chunk c straight into the projection's B operand;
       // the wavefront's pixel blocks share every K step's weight reads
       {
-        const uint32_t ws = slot(c);
-        const char *xe = XeL;
-        const char *wdp = WdL + ws * ES + lh * 16;
-        const uint32_t wd_row = WR * ES;
-        const float *bdp = BdL + ws + lh * HK;
-        const char *wpp = WpL + l32 * RPW + ws * ES + lh * 16;
+        const uint32_t s = slot(c);
+        const char *wdp = SmL + s * SMB + lh * 16;            // tap t at + t * EC * ES
+        const char *bdp = SmL + s * SMB + 9 * EC * ES + lh * 16;
+        // lane: output channel l32 of block o, K groups as in the expand
+        const char *wpp = WpL + s * WPS + ((uint32_t)lh * (HK / 4) * a.CO + l32) * GB;
+        const uint32_t wp_ks = KSTEP / 4 * a.CO * GB, wp_next = a.CO * GB;
         // one K step at a time: hoisting the next step's 18 operand reads
         // above this one doubles the live registers and halves occupancy
 #pragma unroll 1
         for (int ks = 0; ks < NKS; ++ks) {
           u32x4 wv[9];
 #pragma unroll
-          for (int t = 0; t < 9; ++t) wv[t] = *reinterpret_cast<const u32x4 *>(wdp + t * wd_row + ks * 32);
+          for (int t = 0; t < 9; ++t) wv[t] = *reinterpret_cast<const u32x4 *>(wdp + t * (EC * ES) + ks * 32);
           float bias[HK];
-#pragma unroll
-          for (int j = 0; j < HK; j += 4) {
-            const f32x4 bb = *reinterpret_cast<const f32x4 *>(bdp + ks * KSTEP + j);
-            bias[j] = bb.x; bias[j + 1] = bb.y; bias[j + 2] = bb.z; bias[j + 3] = bb.w;
-          }
+          ir_unpack<DT, HK>(*reinterpret_cast<const u32x4 *>(bdp + ks * 32), bias);
           u32x4 bop[NPW];
 #pragma unroll
           for (int i = 0; i < NPW; ++i) {
@@ -386,13 +362,13 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
             for (int j = 0; j < HK; ++j) d[j] = bias[j];
 #pragma unroll
             for (int t = 0; t < 9; ++t)
-              ir_fma_taps<DT, HK>(*reinterpret_cast<const u32x4 *>(xe + rowo[i][t] + ks * 32), wv[t], d);
+              ir_fma_taps<DT, HK>(*reinterpret_cast<const u32x4 *>(XeL + rowo[i][t] + ks * 32), wv[t], d);
             act_array<HK>(act_d, d);
             bop[i] = ir_pack<DT, HK>(d);
           }
 #pragma unroll
           for (int o = 0; o < NOB; ++o) {
-            const u32x4 av = *reinterpret_cast<const u32x4 *>(wpp + o * 32 * RPW + ks * 32);
+            const u32x4 av = ir_ld_w<DT>(wpp + o * (32 * GB) + ks * wp_ks, wp_next);
 #pragma unroll
             for (int i = 0; i < NPW; ++i)
               if (live[i]) acc[i][o] = ir_mma<DT>(av, bop[i], acc[i][o]);
@@ -400,9 +376,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
         }
       }
 
-      // the other slot held chunk c - 1, whose depthwise finished before this
-      // chunk's expand
-      if (!a.resident && c + 1 < nchunks) load_chunk(c + 1, true, true);
+      ir_dma_wait();
       __syncthreads();
     }
 

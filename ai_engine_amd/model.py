@@ -14,13 +14,21 @@ Load-time fusion: a 1x1 conv feeding a depthwise 3x3 feeding a 1x1 conv,
 whose two intermediates have no other reader, becomes one aih_ir_block launch
 (the expanded tensor stays on chip). The fused op reads the same packed
 weights; blocks the fused kernel cannot run (aih_ir_block_plan fails) stay
-three launches. fuse="auto" fuses 16-bit models (where the fused kernel is
-the faster one on MI355X; for fp32 the three MFMA/VALU kernels are faster),
-True / False force it.
+three launches.
+
+Load-time tuning (tune=True, the default): for every fusable block the
+candidates -- the three separate launches, and the fused launch at the
+planner's tile and at a set of forced tiles -- are timed on the device at
+load, a few launches each, and the fastest is kept (like the reference's
+Model::load, which does its per-model work -- pipeline compilation -- once at
+load). fuse="auto" lets the timing choose between fused and separate; True
+keeps only fused candidates, False never fuses. With tune=False the planner's
+tile is used and "auto" fuses 16-bit models only.
 """
 from __future__ import annotations
 
 import ctypes as C
+import dataclasses
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -76,9 +84,13 @@ class ModelOp:
 
 
 class Model:
+    # forced output tiles (h, w) tried for a fused block besides the planner's
+    TUNE_TILES = [(2, 8), (4, 4), (4, 8), (8, 4), (4, 16), (8, 8), (16, 4), (2, 32), (4, 32), (8, 16), (16, 8),
+                  (8, 32), (16, 16)]
+
     def __init__(self, layers: list[Layer], weights: Weights, n: int, ih: int, iw: int, cin: int,
                  dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0",
-                 fuse="auto"):
+                 fuse="auto", tune: bool = True):
         self.layers = layers
         self.n, self.ih, self.iw, self.cin = n, ih, iw, cin
         self.dt = conv.DType(dt)
@@ -108,13 +120,17 @@ class Model:
             packed[Lr.name] = (_to_device(wp, self.device), _to_device(bp, self.device))
             self.shapes[Lr.name] = Lr.out_hw() + (Lr.cout,)
 
-        if fuse == "auto":
+        self.choices: dict[str, tuple[str, float]] = {}  # block -> (chosen candidate, us), when tuned
+        if fuse == "auto" and not tune:
             fuse = self.dt != conv.DType.F32
         i = 0
         while i < len(layers):
             blk = self._match_block(layers, i, readers) if fuse else None
             if blk is not None:
-                self.ops.append(self._fused_op(blk, packed, L))
+                if tune:
+                    self.ops.extend(self._tuned_block(blk, packed, L, allow_unfused=fuse == "auto"))
+                else:
+                    self.ops.append(self._fused_op(blk, packed, L))
                 i += 3
                 continue
             self.ops.append(self._conv_op(layers[i], packed, L))
@@ -143,10 +159,62 @@ class Model:
             return None
         return (e, d, p, spec)
 
-    def _fused_op(self, blk, packed, L) -> ModelOp:
+    def _tuned_block(self, blk, packed, L, allow_unfused: bool) -> list:
+        """Times the block's candidates on the device and returns the fastest
+        one's ops (an unfused winner keeps its intermediates)."""
+        e, d, p, spec = blk
+        cands = []
+        if allow_unfused:
+            cands.append(("unfused", [self._conv_op(Lr, packed, L) for Lr in (e, d, p)]))
+        else:
+            oh, ow = p.out_hw()
+            self.tensors[p.name] = self._alloc(oh, ow, p.cout)
+        y = self.tensors[p.name]
+        seen = set()
+        for tile in [(0, 0)] + self.TUNE_TILES:
+            sp = dataclasses.replace(spec, tile=tile)
+            if not sp.fusable():
+                continue
+            pl = sp.plan()
+            key = (pl.th, pl.tw, pl.resident)
+            if key in seen:
+                continue
+            seen.add(key)
+            cands.append((f"fused {pl.th}x{pl.tw}{' resident' if pl.resident else ''}",
+                          [self._fused_op((e, d, p, sp), packed, L, y=y)]))
+        timed = [(self._time_ops(ops), label, ops) for label, ops in cands]
+        us, label, ops = min(timed, key=lambda t: t[0])
+        self.choices[p.name.rsplit(".", 1)[0]] = (label, us)
+        if label != "unfused":
+            for nm in (e.name, d.name):
+                self.tensors.pop(nm, None)
+        return ops
+
+    def _time_ops(self, ops, reps: int = 5) -> float:
+        """Median device time (us) of one pass over ops, on the current stream."""
+        s = conv._stream(None)
+
+        def once():
+            for op in ops:
+                if op.fn(*op.args, s) != 0:
+                    raise conv.AihError(f"{op.name}: {conv.last_error()}")
+
+        once()
+        once()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in ev:
+            a.record()
+            once()
+            b.record()
+        torch.cuda.synchronize(self.device)
+        ts = sorted(a.elapsed_time(b) for a, b in ev)
+        return ts[len(ts) // 2] * 1e3
+
+    def _fused_op(self, blk, packed, L, y=None) -> ModelOp:
         e, d, p, spec = blk
         oh, ow = p.out_hw()
-        y = self._alloc(oh, ow, p.cout)
+        if y is None:
+            y = self._alloc(oh, ow, p.cout)
         self.tensors[p.name] = y
         desc = spec.desc()
         res = self.tensors[p.res] if p.res else None

@@ -92,6 +92,7 @@ def main() -> int:
     x = (torch.rand(n, H, Wd, 3, device=dev) * 2 - 1).contiguous()
     model = Model(layers, wts, n, H, Wd, 3, dt=DT[args.dtype])
     stream = torch.cuda.current_stream()
+    log("load-time block choices: " + ", ".join(f"{k} {v[0]} ({v[1]:.1f} us)" for k, v in model.choices.items()))
 
     def step():
         model.upload_input(x)
@@ -175,6 +176,7 @@ def main() -> int:
         kernels["encoder_f16" if args.dtype == "bf16" else "encoder_bf16"] = encoder_other(
             torch, W, Model, layers, wts, x, n, H, Wd, "f16" if args.dtype == "bf16" else "bf16", DT, stream)
     kernels["encoder_layers"] = layer_rows
+    kernels["encoder_block_choices"] = {k: {"choice": v[0], "us": round(v[1], 2)} for k, v in model.choices.items()}
 
     # ------------------------------------------------------------ CPU baseline (oracle ai-cpu restatement)
     cpu = None

@@ -162,14 +162,15 @@ def test_ir_block_plan_covers_the_output_and_fits_lds(blk, dt):
     assert cexp % p.ec == 0 and p.ec % 32 == 0 and p.chunks == cexp // p.ec
     assert p.lds_bytes <= 160 * 1024 and p.occupancy >= 1
     assert 1 <= p.grid <= p.tiles
-    # the LDS the kernel addresses: input tile with halo, expanded chunk, the
-    # expand / project / depthwise weights and biases of one chunk (or of all
-    # of E when they stay resident)
+    # the LDS the kernel addresses: input tile with halo (rows padded by 16
+    # bytes), expanded chunk, the packed expand / project / depthwise weights
+    # and both biases of two chunks (or of all of E when they stay resident),
+    # and the fp32 projection bias
     es = 4 if dt == 0 else 2
     wn = cexp if p.resident else 2 * p.ec
     halo = -(-(((p.th - 1) * s + 3) * ((p.tw - 1) * s + 3)) // 32) * 32
-    need = halo * (cin * es + 16) + halo * (p.ec * es + 16) + wn * (cin * es + 16) + cout * (wn * es + 16)
-    need += 9 * wn * es + (2 * wn + cout) * 4
+    need = halo * (cin * es + 16) + halo * (p.ec * es + 16) + wn * cin * es + wn * cout * es
+    need += 11 * wn * es + cout * 4
     assert p.lds_bytes >= need
 
 
