@@ -128,7 +128,7 @@ EXPORTS = (
     "aih_conv_pw", "aih_conv_pw_plan", "aih_conv_igemm", "aih_conv_igemm_plan", "aih_conv_dw", "aih_conv",
     "aih_conv_workspace_size", "aih_nhwc_c4_bytes", "aih_pack_nhwc", "aih_unpack_nhwc",
     "aih_pack_weights_conv", "aih_pack_weights_dw", "aih_pack_bias", "aih_pack_nhwc_device",
-    "aih_ir_block_plan", "aih_ir_block", "aih_last_error", "aih_version",
+    "aih_ir_block_plan", "aih_ir_block", "aih_last_error", "aih_version", "aih_conv_check",
 )
 
 _lib = None

@@ -11,30 +11,26 @@
 #include <exception>
 #include <initializer_list>
 #include <string>
+#include <utility>
 
 #include "../../include/aih_conv.h"
+#include "capi_util.h"
 #include "conv_dw.h"
 #include "conv_gemm_launch.h"
 #include "ir_block.h"
 
+std::string &aih::last_error_slot() {
+  thread_local std::string msg;
+  return msg;
+}
+
 namespace {
 
-thread_local std::string g_err;
-
-int fail(const std::string &msg) {
-  g_err = msg;
-  return AIH_ERR;
-}
+int fail(const std::string &msg) { return aih::api_fail(msg); }
 
 template <class F>
 int guarded(F &&f) {
-  try {
-    return f();
-  } catch (const std::exception &e) {
-    return fail(std::string("exception: ") + e.what());
-  } catch (...) {
-    return fail("unknown exception");
-  }
+  return aih::api_guarded(std::forward<F>(f));
 }
 
 inline uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
@@ -250,7 +246,7 @@ int plan_ir(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, aih::IrPlan *p
 
 extern "C" {
 
-const char *aih_last_error(void) { return g_err.c_str(); }
+const char *aih_last_error(void) { return aih::last_error_slot().c_str(); }
 
 const char *aih_version(void) { return "aih_conv 0.1 gfx950"; }
 
@@ -379,21 +375,27 @@ int aih_conv_igemm(const aih_igemm_desc *d, const void *const *inputs, const voi
   });
 }
 
+static int check_dw(const aih_dw_desc *d) {
+  if (!d) return fail("null descriptor");
+  if (d->n == 0 || d->ih == 0 || d->iw == 0 || d->c == 0) return fail("dw: zero-sized dimension");
+  if (d->k == 0 || d->s == 0 || d->d == 0) return fail("dw: k, s, d must be > 0");
+  if (d->act < AIH_ACT_NONE || d->act > AIH_ACT_RECIP) return fail("dw: unknown activation");
+  if (!dtype_ok(d->dt)) return fail("dw: unknown dtype");
+  const uint32_t ek = d->d * (d->k - 1) + 1;
+  if (d->ih + d->pad[0] + d->pad[2] < ek || d->iw + d->pad[1] + d->pad[3] < ek)
+    return fail("dw: kernel larger than the padded input");
+  return AIH_OK;
+}
+
 int aih_conv_dw(const aih_dw_desc *d, const void *x, const void *w, const void *bias, const void *res, void *y,
                 aih_stream stream) {
   return guarded([&] {
-    if (!d) return fail("null descriptor");
-    if (d->n == 0 || d->ih == 0 || d->iw == 0 || d->c == 0) return fail("dw: zero-sized dimension");
-    if (d->k == 0 || d->s == 0 || d->d == 0) return fail("dw: k, s, d must be > 0");
-    if (d->act < AIH_ACT_NONE || d->act > AIH_ACT_RECIP) return fail("dw: unknown activation");
-    if (!dtype_ok(d->dt)) return fail("dw: unknown dtype");
+    if (check_dw(d)) return AIH_ERR;
     if (!x || !w || !bias || !y) return fail("dw: null buffer");
     if ((d->residual != 0) != (res != nullptr)) return fail("dw: res must be given iff residual");
     if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16) || !aligned(bias, 16) || (res && !aligned(res, 16)))
       return fail("dw: misaligned buffer (16 bytes)");
     const uint32_t ek = d->d * (d->k - 1) + 1;
-    if (d->ih + d->pad[0] + d->pad[2] < ek || d->iw + d->pad[1] + d->pad[3] < ek)
-      return fail("dw: kernel larger than the padded input");
     aih::DwArgs a;
     a.x = x;
     a.w = w;
@@ -532,6 +534,20 @@ static int conv_route(const aih_conv_desc *d, aih_pw_desc *pw, aih_igemm_desc *i
   return 1;
 }
 
+int aih_conv_check(const aih_conv_desc *d) {
+  return guarded([&] {
+    aih_pw_desc pw;
+    aih_igemm_desc ig;
+    aih_dw_desc dw;
+    GemmPlan g;
+    const int r = conv_route(d, &pw, &ig, &dw);
+    if (r < 0) return AIH_ERR;
+    if (r == 0) return check_pw(&pw) ? AIH_ERR : plan_pw(&pw, &g);
+    if (r == 1) return check_igemm(&ig) ? AIH_ERR : plan_igemm(&ig, &g);
+    return check_dw(&dw);
+  });
+}
+
 size_t aih_conv_workspace_size(const aih_conv_desc *d) {
   aih_pw_desc pw;
   aih_igemm_desc ig;
@@ -630,7 +646,7 @@ int aih_unpack_nhwc(const void *bytes, uint32_t n, uint32_t h, uint32_t w, uint3
 uint32_t aih_pack_weights_conv(const float *wt, uint32_t cout, uint32_t cin, uint32_t kh, uint32_t kw,
                                uint32_t kg_align, int32_t dt, void *out) {
   if (!wt || !out || !dtype_ok(dt) || !cout || !cin || !kh || !kw) {
-    g_err = "pack_weights_conv: bad argument";
+    aih::last_error_slot() = "pack_weights_conv: bad argument";
     return 0;
   }
   const uint32_t al = kg_align ? kg_align : 1;

@@ -1,0 +1,666 @@
+// sw_model.hip -- a .sw model resident on the GPU (include/aih_model.h), the
+// native counterpart of ai_gpu_runtime::Model (crates/ai-gpu-runtime/src/model.rs).
+//
+// Load (Model::load, model.rs:56-366): parse the container and graph, put the
+// weight blob on the device once (converted to 16-bit storage when asked),
+// give every tensor that is not an alias its own NHWC-C4 buffer with the
+// batch outermost (aliases are views: the backing buffer plus a channel-group
+// offset, model.rs:29-35,300-307), and lower every op to a launch closure
+// with its descriptor built once (lower_op, lowering.rs:88-516). Conv ops go
+// through the conv entry points of aih_conv.h exactly as the op-level boundary
+// routes them; the other op kinds through aih_model.h's op entry points.
+// The converter has already decided fusion, topological order and liveness
+// (format/model.rs:1-9); the runtime keeps one buffer per tensor (HBM is not
+// the constraint at these sizes) and does no graph analysis.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/aih_model.h"
+#include "capi_util.h"
+#include "sw_format.h"
+
+namespace aih {
+namespace {
+
+size_t es_of(int32_t dt) { return dt == AIH_F32 ? 4 : 2; }
+uint32_t c4(uint32_t c) { return (c + 3) / 4 * 4; }
+
+// f32 -> f16 / bf16 bits, round to nearest even (IEEE 754; the half crate's
+// from_f32 used by pack.rs:16-31 rounds the same way). NaN stays NaN.
+uint16_t f32_to_f16_bits(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // rounds to >= 65520: inf
+  if (ax < 0x38800000u) {                                    // below the f16 normal range
+    if (ax < 0x33000000u) return (uint16_t)sign;             // below half the smallest subnormal
+    const uint32_t e = ax >> 23, m = (ax & 0x7fffffu) | 0x800000u;
+    const uint32_t shift = 126 - e;                          // 14..24
+    uint32_t v = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (v & 1u))) ++v;
+    return (uint16_t)(sign | v);
+  }
+  uint32_t v = ((ax >> 13) - (112u << 10));
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (v & 1u))) ++v;
+  return (uint16_t)(sign | v);
+}
+
+uint16_t f32_to_bf16_bits(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+
+float f16_bits_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  uint32_t x;
+  if (e == 0) {
+    if (m == 0) {
+      x = sign;
+    } else {  // subnormal: normalise
+      e = 113;
+      while (!(m & 0x400u)) {
+        m <<= 1;
+        --e;
+      }
+      x = sign | (e << 23) | ((m & 0x3ffu) << 13);
+    }
+  } else if (e == 31) {
+    x = sign | 0x7f800000u | (m << 13);
+  } else {
+    x = sign | ((e + 112) << 23) | (m << 13);
+  }
+  float f;
+  std::memcpy(&f, &x, 4);
+  return f;
+}
+
+float bf16_bits_to_f32(uint16_t h) {
+  const uint32_t x = (uint32_t)h << 16;
+  float f;
+  std::memcpy(&f, &x, 4);
+  return f;
+}
+
+int hip_fail(const char *what, hipError_t e) { return api_fail(std::string(what) + ": " + hipGetErrorString(e)); }
+
+// A JSON string literal of s (quotes, backslashes and control characters escaped).
+std::string json_quote(const std::string &s) {
+  std::string o = "\"";
+  for (unsigned char ch : s) {
+    if (ch == '"' || ch == '\\') {
+      o.push_back('\\');
+      o.push_back((char)ch);
+    } else if (ch < 0x20) {
+      char b[8];
+      std::snprintf(b, sizeof(b), "\\u%04x", ch);
+      o += b;
+    } else {
+      o.push_back((char)ch);
+    }
+  }
+  return o + "\"";
+}
+
+}  // namespace
+}  // namespace aih
+
+using namespace aih;
+
+struct aih_model {
+  sw::Model g;
+  uint32_t n = 1;
+  int32_t dt = AIH_F32, wdt = AIH_F32;
+  std::vector<void *> allocs;
+  char *wdev = nullptr;                      // weights on the device
+  std::map<uint64_t, uint64_t> woff;         // blob offset -> device offset (identity unless converted)
+  int32_t blob_dt = AIH_F32;                 // storage of the blob's float data before conversion
+  struct View {
+    char *base = nullptr;  // backing buffer
+    size_t bytes = 0;      // backing buffer size
+    uint32_t stride_c = 0; // channels per pixel of the backing buffer
+    uint32_t c_off = 0;    // first channel of the view
+  };
+  std::vector<View> views;                   // per tid
+  void *ws = nullptr;
+  size_t ws_bytes = 0;
+  float *staging = nullptr;
+  size_t staging_floats = 0;
+  std::vector<std::function<int(hipStream_t)>> launches;
+  size_t device_bytes = 0;
+
+  ~aih_model() {
+    for (void *p : allocs) (void)hipFree(p);
+  }
+
+  void *dalloc(size_t bytes) {
+    void *p = nullptr;
+    const hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+    if (e != hipSuccess) throw std::runtime_error(std::string("hipMalloc: ") + hipGetErrorString(e));
+    allocs.push_back(p);
+    device_bytes += bytes;
+    return p;
+  }
+
+  int64_t find(const char *name) const {
+    if (!name) return -1;
+    for (size_t i = 0; i < g.tensors.size(); ++i)
+      if (g.tensors[i].name == name) return (int64_t)i;
+    return -1;
+  }
+
+  bool dense(uint32_t tid) const {
+    const View &v = views[tid];
+    return v.c_off == 0 && v.stride_c == c4(g.tensors[tid].c);
+  }
+  void *ptr(uint32_t tid) const { return views[tid].base + (size_t)views[tid].c_off * es_of(dt); }
+  const void *wptr(const sw::WRef &r) const {
+    auto it = woff.find(r.off);
+    if (it == woff.end()) throw std::runtime_error("weight reference not prepared");
+    return wdev + it->second;
+  }
+  aih_src src_of(uint32_t tid, uint32_t c) const {
+    const View &v = views[tid];
+    return aih_src{c, v.stride_c, v.c_off};
+  }
+};
+
+namespace {
+
+// Weight blob -> device. Every WRef the ops use must lie inside the blob; with
+// a dtype change its fp32 elements are converted one by one (the packed
+// layouts index elements, so the layout is unchanged at the new size).
+void prepare_weights(aih_model *m, const sw::Container &c) {
+  std::vector<sw::WRef> refs;
+  for (const sw::Op &op : m->g.ops) {
+    if (op.kind == sw::OP_CONV) refs.push_back(op.w), refs.push_back(op.b);
+    if (op.kind == sw::OP_BINARY && op.opnd == sw::OPND_CVEC) refs.push_back(op.cvec);
+  }
+  for (const sw::WRef &r : refs)
+    if (r.off > c.blob_len || r.len > c.blob_len - r.off) throw sw::Error(".sw: weight reference outside the blob");
+  const bool convert = m->blob_dt == AIH_F32 && m->dt != AIH_F32;
+  if (!convert) {
+    m->wdev = static_cast<char *>(m->dalloc(c.blob_len));
+    if (c.blob_len) {
+      const hipError_t e = hipMemcpy(m->wdev, c.blob, c.blob_len, hipMemcpyHostToDevice);
+      if (e != hipSuccess) throw std::runtime_error(std::string("weights upload: ") + hipGetErrorString(e));
+    }
+    for (const sw::WRef &r : refs) m->woff[r.off] = r.off;
+    return;
+  }
+  std::vector<uint8_t> host;
+  for (const sw::WRef &r : refs) {
+    if (m->woff.count(r.off)) continue;
+    if (r.len % 4) throw sw::Error(".sw: fp32 weight reference with a length not a multiple of 4");
+    const size_t off = (host.size() + 255) / 256 * 256;
+    const size_t cnt = r.len / 4;
+    host.resize(off + cnt * 2);
+    for (size_t i = 0; i < cnt; ++i) {
+      float f;
+      std::memcpy(&f, c.blob + r.off + i * 4, 4);
+      const uint16_t h = m->dt == AIH_F16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f);
+      std::memcpy(&host[off + i * 2], &h, 2);
+    }
+    m->woff[r.off] = off;
+  }
+  m->wdev = static_cast<char *>(m->dalloc(host.size()));
+  if (!host.empty()) {
+    const hipError_t e = hipMemcpy(m->wdev, host.data(), host.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) throw std::runtime_error(std::string("weights upload: ") + hipGetErrorString(e));
+  }
+}
+
+void alloc_tensors(aih_model *m) {
+  const size_t es = es_of(m->dt);
+  const auto &T = m->g.tensors;
+  m->views.assign(T.size(), aih_model::View{});
+  size_t total = 0;
+  std::vector<size_t> off(T.size(), 0);
+  for (size_t i = 0; i < T.size(); ++i) {
+    if (T[i].alias_of >= 0) continue;
+    off[i] = total;
+    total += ((size_t)m->n * T[i].h * T[i].w * c4(T[i].c) * es + 255) / 256 * 256;
+  }
+  char *arena = static_cast<char *>(m->dalloc(total));
+  const hipError_t e = hipMemset(arena, 0, total ? total : 16);
+  if (e != hipSuccess) throw std::runtime_error(std::string("tensor arena clear: ") + hipGetErrorString(e));
+  for (size_t i = 0; i < T.size(); ++i) {
+    if (T[i].alias_of >= 0) continue;
+    m->views[i] = aih_model::View{arena + off[i], (size_t)m->n * T[i].h * T[i].w * c4(T[i].c) * es, c4(T[i].c), 0};
+  }
+  for (size_t i = 0; i < T.size(); ++i) {
+    if (T[i].alias_of < 0) continue;
+    const auto r = m->g.resolve((uint32_t)i);
+    const auto &B = T[r.first];
+    aih_model::View v = m->views[r.first];
+    v.c_off = r.second * 4;
+    if (T[i].h != B.h || T[i].w != B.w || v.c_off + T[i].c > v.stride_c)
+      throw sw::Error(".sw: alias '" + T[i].name + "' does not fit inside '" + B.name + "'");
+    m->views[i] = v;
+  }
+}
+
+void need_dense(const aih_model *m, uint32_t tid, const char *role, size_t op_index) {
+  if (!m->dense(tid))
+    throw sw::Error(".sw: op " + std::to_string(op_index) + ": " + role + " '" + m->g.tensors[tid].name +
+                    "' is a channel view; this op needs a whole tensor");
+}
+
+void lower(aih_model *m) {
+  const auto &T = m->g.tensors;
+  for (size_t k = 0; k < m->g.ops.size(); ++k) {
+    const sw::Op &op = m->g.ops[k];
+    const auto &O = T[op.out];
+    need_dense(m, op.out, "output", k);
+    void *y = m->ptr(op.out);
+    switch (op.kind) {
+      case sw::OP_CONV: {
+        const auto &I = T[op.in];
+        const void *w = m->wptr(op.w), *b = m->wptr(op.b);
+        const void *res = nullptr;
+        if (op.res >= 0) {
+          need_dense(m, (uint32_t)op.res, "residual", k);
+          res = m->ptr((uint32_t)op.res);
+        }
+        // std conv weights in dt_weights, dw weights and biases in dt_default
+        // (lowering.rs:94-97, format/model.rs:245-254)
+        const int32_t wdt = op.groups > 1 ? m->dt : m->wdt;
+        if (!op.srcs.empty() || !m->dense(op.in)) {
+          // concat-into-conv parts or a channel view: the implicit-GEMM path
+          // reads each part through its own view (conv_igemm.rs:141-171)
+          if (op.groups != 1 || op.kh != op.kw || op.sh != op.sw || op.kh == 1)
+            throw sw::Error(".sw: op " + std::to_string(k) +
+                            ": concat parts / channel views feed only KxK (k > 1) dense convs here");
+          aih_igemm_desc d{};
+          d.n = m->n;
+          d.ih = I.h;
+          d.iw = I.w;
+          d.cin = op.cin;
+          d.cout = op.cout;
+          d.k = op.kh;
+          d.s = op.sh;
+          d.d = op.d;
+          std::memcpy(d.pad, op.pad, sizeof(d.pad));
+          d.act = op.act;
+          d.residual = res ? 1 : 0;
+          d.dt = m->dt;
+          d.wdt = wdt;
+          std::vector<const void *> ins;
+          if (op.srcs.empty()) {
+            d.nsrcs = 1;
+            d.srcs[0] = m->src_of(op.in, op.cin);
+            ins.push_back(m->views[op.in].base);
+          } else {
+            if (op.srcs.size() > 3) throw sw::Error(".sw: conv with more than 3 concat parts");
+            d.nsrcs = (uint32_t)op.srcs.size();
+            for (size_t i = 0; i < op.srcs.size(); ++i) {
+              const auto &P = T[op.srcs[i].tid];
+              if (P.h != I.h || P.w != I.w) throw sw::Error(".sw: concat part of another size");
+              d.srcs[i] = m->src_of(op.srcs[i].tid, op.srcs[i].c);
+              ins.push_back(m->views[op.srcs[i].tid].base);
+            }
+          }
+          aih_plan p;
+          if (aih_conv_igemm_plan(&d, &p)) throw sw::Error(std::string("op ") + std::to_string(k) + ": " + aih_last_error());
+          m->ws_bytes = std::max(m->ws_bytes, p.ws_bytes);
+          aih_model *mm = m;
+          m->launches.push_back([mm, d, ins, w, b, res, y](hipStream_t s) {
+            return aih_conv_igemm(&d, ins.data(), w, b, res, y, mm->ws, mm->ws_bytes, s);
+          });
+        } else {
+          aih_conv_desc d{};
+          d.n = m->n;
+          d.ih = I.h;
+          d.iw = I.w;
+          d.cin = op.cin;
+          d.cout = op.cout;
+          d.kh = op.kh;
+          d.kw = op.kw;
+          d.sh = op.sh;
+          d.sw = op.sw;
+          std::memcpy(d.pad, op.pad, sizeof(d.pad));
+          d.d = op.d;
+          d.groups = op.groups;
+          d.act = op.act;
+          d.residual = res ? 1 : 0;
+          d.dt = m->dt;
+          d.wdt = wdt;
+          d.kg_pad = op.kg_pad;
+          if (c4(I.c) != c4(op.cin)) throw sw::Error(".sw: op " + std::to_string(k) + ": input channels != cin");
+          if (aih_conv_check(&d)) throw sw::Error(".sw: op " + std::to_string(k) + ": " + aih_last_error());
+          const size_t ws = aih_conv_workspace_size(&d);
+          m->ws_bytes = std::max(m->ws_bytes, ws);
+          const void *x = m->ptr(op.in);
+          aih_model *mm = m;
+          m->launches.push_back([mm, d, x, w, b, res, y](hipStream_t s) {
+            return aih_conv(&d, x, w, b, res, y, mm->ws, mm->ws_bytes, s);
+          });
+        }
+        break;
+      }
+      case sw::OP_BINARY: {
+        need_dense(m, op.in, "input", k);
+        aih_binary_desc d{};
+        d.n = m->n;
+        d.h = O.h;
+        d.w = O.w;
+        d.c = O.c;
+        d.op = op.bin;
+        d.act = op.act;
+        d.dt = m->dt;
+        d.operand = op.opnd;
+        d.scalar = op.scalar;
+        d.scalar_first = op.scalar_first ? 1 : 0;
+        const void *a = m->ptr(op.in), *b = nullptr;
+        if (op.opnd == sw::OPND_CVEC) {
+          b = m->wptr(op.cvec);
+        } else if (op.opnd != sw::OPND_SCALAR) {
+          need_dense(m, op.b_tid, "operand", k);
+          b = m->ptr(op.b_tid);
+          d.b_c = T[op.b_tid].c;
+        }
+        m->launches.push_back([d, a, b, y](hipStream_t s) { return aih_binary(&d, a, b, y, s); });
+        break;
+      }
+      case sw::OP_GPOOL: {
+        need_dense(m, op.in, "input", k);
+        const auto &I = T[op.in];
+        aih_gpool_desc d{m->n, I.h, I.w, I.c, m->dt};
+        const void *x = m->ptr(op.in);
+        m->launches.push_back([d, x, y](hipStream_t s) { return aih_gpool(&d, x, y, s); });
+        break;
+      }
+      case sw::OP_RESIZE: {
+        const auto &I = T[op.in];
+        aih_resize_desc d{};
+        d.n = m->n;
+        d.ih = I.h;
+        d.iw = I.w;
+        d.oh = op.oh;
+        d.ow = op.ow;
+        d.mode = op.coord;
+        d.dt = m->dt;
+        std::vector<const void *> ins;
+        std::vector<sw::Part> parts = op.srcs;
+        if (parts.empty()) parts.push_back(sw::Part{op.in, I.c});
+        if (parts.size() > 8) throw sw::Error(".sw: resize with more than 8 parts");
+        d.nsrcs = (uint32_t)parts.size();
+        for (size_t i = 0; i < parts.size(); ++i) {
+          d.srcs[i] = m->src_of(parts[i].tid, parts[i].c);
+          ins.push_back(m->views[parts[i].tid].base);
+        }
+        m->launches.push_back([d, ins, y](hipStream_t s) { return aih_resize(&d, ins.data(), y, s); });
+        break;
+      }
+      case sw::OP_CONCAT: {
+        aih_concat_desc d{};
+        d.n = m->n;
+        d.h = O.h;
+        d.w = O.w;
+        d.dt = m->dt;
+        if (op.srcs.size() > 8) throw sw::Error(".sw: concat with more than 8 parts");
+        d.nparts = (uint32_t)op.srcs.size();
+        std::vector<const void *> ins;
+        for (size_t i = 0; i < op.srcs.size(); ++i) {
+          d.parts[i] = m->src_of(op.srcs[i].tid, op.srcs[i].c);
+          ins.push_back(m->views[op.srcs[i].tid].base);
+        }
+        m->launches.push_back([d, ins, y](hipStream_t s) { return aih_concat(&d, ins.data(), y, s); });
+        break;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt) {
+  aih_model *out = nullptr;
+  const int rc = api_guarded([&] {
+    if (n == 0) return api_fail("model_load: n must be >= 1");
+    if (dt != -1 && dt != AIH_F32 && dt != AIH_F16 && dt != AIH_BF16) return api_fail("model_load: unknown dtype");
+    sw::Container c = sw::parse_container(bytes, len);
+    std::unique_ptr<aih_model> m(new aih_model);
+    m->g = sw::parse_model(c.json, c.json_len);
+    m->n = n;
+    m->blob_dt = m->g.dt_default == sw::F16 ? AIH_F16 : AIH_F32;
+    for (const auto &t : m->g.tensors)
+      if (t.dt != m->g.dt_default)
+        return api_fail("model_load: tensor '" + t.name + "' has a dtype other than dt_default");
+    if (dt == -1) {
+      m->dt = m->g.dt_default == sw::F16 ? AIH_F16 : AIH_F32;
+      m->wdt = m->g.dt_weights == sw::F16 ? AIH_F16 : AIH_F32;
+    } else {
+      if (dt != AIH_F32 && (m->g.dt_default != sw::F32 || m->g.dt_weights != sw::F32))
+        return api_fail("model_load: a dtype change needs an fp32 file");
+      if (dt == AIH_F32 && m->g.dt_default != sw::F32) return api_fail("model_load: cannot widen a 16-bit file");
+      m->dt = m->wdt = dt;
+    }
+    if (!m->g.consts.empty()) return api_fail("model_load: constant tensors are not supported");
+    prepare_weights(m.get(), c);
+    alloc_tensors(m.get());
+    lower(m.get());
+    if (m->ws_bytes) m->ws = m->dalloc(m->ws_bytes);
+    for (uint32_t t : m->g.inputs)
+      m->staging_floats = std::max(m->staging_floats, (size_t)n * m->g.tensors[t].h * m->g.tensors[t].w * m->g.tensors[t].c);
+    if (m->staging_floats) m->staging = static_cast<float *>(m->dalloc(m->staging_floats * 4));
+    out = m.release();
+    return AIH_OK;
+  });
+  return rc == AIH_OK ? out : nullptr;
+}
+
+void aih_model_free(aih_model *m) { delete m; }
+
+static int upload(aih_model *m, const char *name, const float *src, size_t count, bool host, aih_stream stream) {
+  return api_guarded([&] {
+    if (!m || !src) return api_fail("upload_input: null argument");
+    const int64_t tid = m->find(name);
+    if (tid < 0 || std::find(m->g.inputs.begin(), m->g.inputs.end(), (uint32_t)tid) == m->g.inputs.end())
+      return api_fail(std::string("upload_input: no input named '") + (name ? name : "") + "'");
+    const auto &t = m->g.tensors[tid];
+    const size_t want = (size_t)m->n * t.h * t.w * t.c;
+    if (count != want) return api_fail("upload_input: expected " + std::to_string(want) + " floats");
+    if (!m->dense((uint32_t)tid)) return api_fail("upload_input: input is a channel view");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const float *x = src;
+    if (host) {
+      const hipError_t e = hipMemcpyAsync(m->staging, src, count * 4, hipMemcpyHostToDevice, s);
+      if (e != hipSuccess) return hip_fail("upload_input copy", e);
+      x = m->staging;
+    }
+    if (aih_pack_nhwc_device(x, m->n, t.h, t.w, t.c, m->dt, m->ptr((uint32_t)tid), stream)) return AIH_ERR;
+    if (host) {
+      const hipError_t e = hipStreamSynchronize(s);
+      if (e != hipSuccess) return hip_fail("upload_input", e);
+    }
+    return AIH_OK;
+  });
+}
+
+int aih_model_upload_input(aih_model *m, const char *name, const float *host_nhwc, size_t count, aih_stream stream) {
+  return upload(m, name, host_nhwc, count, true, stream);
+}
+
+int aih_model_upload_input_device(aih_model *m, const char *name, const float *dev_nhwc, size_t count,
+                                  aih_stream stream) {
+  return upload(m, name, dev_nhwc, count, false, stream);
+}
+
+int aih_model_infer(aih_model *m, aih_stream stream) {
+  return api_guarded([&] {
+    if (!m) return api_fail("infer: null model");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (size_t i = 0; i < m->launches.size(); ++i)
+      if (m->launches[i](s) != AIH_OK) return api_fail("infer: op " + std::to_string(i) + ": " + aih_last_error());
+    return AIH_OK;
+  });
+}
+
+int aih_model_infer_range(aih_model *m, uint32_t first, uint32_t last, aih_stream stream) {
+  return api_guarded([&] {
+    if (!m) return api_fail("infer_range: null model");
+    if (first > last || last > m->launches.size()) return api_fail("infer_range: bad op range");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (uint32_t i = first; i < last; ++i)
+      if (m->launches[i](s) != AIH_OK) return api_fail("infer: op " + std::to_string(i) + ": " + aih_last_error());
+    return AIH_OK;
+  });
+}
+
+int aih_model_read_output(aih_model *m, const char *name, float *host_nhwc, size_t count, aih_stream stream) {
+  return api_guarded([&] {
+    if (!m || !host_nhwc) return api_fail("read_output: null argument");
+    const int64_t tid = m->find(name);
+    if (tid < 0) return api_fail(std::string("read_output: no tensor named '") + (name ? name : "") + "'");
+    const auto &t = m->g.tensors[tid];
+    const size_t want = (size_t)m->n * t.h * t.w * t.c;
+    if (count != want) return api_fail("read_output: expected " + std::to_string(want) + " floats");
+    const aih_model::View &v = m->views[tid];
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("read_output", e);
+    std::vector<uint8_t> buf(v.bytes);
+    e = hipMemcpy(buf.data(), v.base, v.bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail("read_output copy", e);
+    const size_t es = es_of(m->dt);
+    const size_t px = (size_t)m->n * t.h * t.w;
+    for (size_t p = 0; p < px; ++p)
+      for (uint32_t ch = 0; ch < t.c; ++ch) {
+        const uint8_t *q = buf.data() + (p * v.stride_c + v.c_off + ch) * es;
+        float f;
+        if (m->dt == AIH_F32) {
+          std::memcpy(&f, q, 4);
+        } else {
+          uint16_t h;
+          std::memcpy(&h, q, 2);
+          f = m->dt == AIH_F16 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
+        }
+        host_nhwc[p * t.c + ch] = f;
+      }
+    return AIH_OK;
+  });
+}
+
+int aih_model_write_tensor(aih_model *m, const char *name, const float *host_nhwc, size_t count,
+                           aih_stream stream) {
+  return api_guarded([&] {
+    if (!m || !host_nhwc) return api_fail("write_tensor: null argument");
+    const int64_t tid = m->find(name);
+    if (tid < 0) return api_fail(std::string("write_tensor: no tensor named '") + (name ? name : "") + "'");
+    const auto &t = m->g.tensors[tid];
+    const size_t want = (size_t)m->n * t.h * t.w * t.c;
+    if (count != want) return api_fail("write_tensor: expected " + std::to_string(want) + " floats");
+    const aih_model::View &v = m->views[tid];
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail("write_tensor", e);
+    std::vector<uint8_t> buf(v.bytes);
+    e = hipMemcpy(buf.data(), v.base, v.bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail("write_tensor read", e);
+    const size_t es = es_of(m->dt);
+    const size_t px = (size_t)m->n * t.h * t.w;
+    for (size_t p = 0; p < px; ++p)
+      for (uint32_t ch = 0; ch < t.c; ++ch) {
+        uint8_t *q = buf.data() + (p * v.stride_c + v.c_off + ch) * es;
+        const float f = host_nhwc[p * t.c + ch];
+        if (m->dt == AIH_F32) {
+          std::memcpy(q, &f, 4);
+        } else {
+          const uint16_t h = m->dt == AIH_F16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f);
+          std::memcpy(q, &h, 2);
+        }
+      }
+    e = hipMemcpy(v.base, buf.data(), v.bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail("write_tensor write", e);
+    return AIH_OK;
+  });
+}
+
+int aih_model_reset(aih_model *m, aih_stream stream) {
+  return api_guarded([&] {
+    if (!m) return api_fail("reset: null model");
+    for (const auto &st : m->g.states)
+      for (uint32_t tid : {st.first, st.second}) {
+        const aih_model::View &v = m->views[tid];
+        const hipError_t e = hipMemsetAsync(v.base, 0, v.bytes, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail("reset", e);
+      }
+    return AIH_OK;
+  });
+}
+
+int aih_model_tensor(const aih_model *m, const char *name, aih_tensor_info *out) {
+  return api_guarded([&] {
+    if (!m || !out) return api_fail("tensor: null argument");
+    const int64_t tid = m->find(name);
+    if (tid < 0) return api_fail(std::string("tensor: no tensor named '") + (name ? name : "") + "'");
+    const auto &t = m->g.tensors[tid];
+    const aih_model::View &v = m->views[tid];
+    const size_t skip = (size_t)v.c_off * es_of(m->dt);
+    *out = aih_tensor_info{v.base + skip, v.bytes - skip, m->n, t.h, t.w, t.c, v.stride_c, m->dt};
+    return AIH_OK;
+  });
+}
+
+int aih_model_get_info(const aih_model *m, aih_model_info *out) {
+  return api_guarded([&] {
+    if (!m || !out) return api_fail("info: null argument");
+    *out = aih_model_info{(uint32_t)m->g.tensors.size(), (uint32_t)m->g.ops.size(), (uint32_t)m->g.inputs.size(),
+                          (uint32_t)m->g.outputs.size(), (uint32_t)m->launches.size(), m->dt, m->wdt,
+                          m->device_bytes};
+    return AIH_OK;
+  });
+}
+
+const char *aih_model_input_name(const aih_model *m, uint32_t i) {
+  return m && i < m->g.inputs.size() ? m->g.tensors[m->g.inputs[i]].name.c_str() : nullptr;
+}
+
+const char *aih_model_output_name(const aih_model *m, uint32_t i) {
+  return m && i < m->g.outputs.size() ? m->g.tensors[m->g.outputs[i]].name.c_str() : nullptr;
+}
+
+int aih_sw_describe(const void *bytes, size_t len, char *buf, size_t buflen) {
+  return api_guarded([&] {
+    sw::Container c = sw::parse_container(bytes, len);
+    sw::Model g = sw::parse_model(c.json, c.json_len);
+    int counts[5] = {0, 0, 0, 0, 0};
+    for (const auto &op : g.ops) ++counts[op.kind];
+    int aliases = 0;
+    for (const auto &t : g.tensors) aliases += t.alias_of >= 0;
+    char tmp[1024];
+    const std::string qname = json_quote(g.name.substr(0, 256));
+    const int k = std::snprintf(
+        tmp, sizeof(tmp),
+        "{\"name\": %s, \"h\": %u, \"w\": %u, \"dt_default\": \"%s\", \"dt_weights\": \"%s\", \"tensors\": %zu, "
+        "\"aliases\": %d, \"inputs\": %zu, \"outputs\": %zu, \"ops\": %zu, \"conv\": %d, \"binary\": %d, \"gpool\": %d, "
+        "\"resize\": %d, \"concat\": %d, \"json_bytes\": %zu, \"blob_bytes\": %zu}",
+        qname.c_str(), g.size_h, g.size_w, g.dt_default == sw::F16 ? "f16" : "f32",
+        g.dt_weights == sw::F16 ? "f16" : "f32", g.tensors.size(), aliases, g.inputs.size(), g.outputs.size(),
+        g.ops.size(), counts[sw::OP_CONV], counts[sw::OP_BINARY], counts[sw::OP_GPOOL], counts[sw::OP_RESIZE],
+        counts[sw::OP_CONCAT], c.json_len, c.blob_len);
+    if (k < 0 || (size_t)k >= sizeof(tmp)) return api_fail("describe: summary too long");
+    if (!buf || buflen <= (size_t)k) return api_fail("describe: buffer too small");
+    std::memcpy(buf, tmp, (size_t)k + 1);
+    return k;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,321 @@
+// sw_ops.hip -- the non-conv ops of a segmentation graph (include/aih_model.h):
+// bilinear resize with concat parts, global average pool, binary elementwise
+// with the six SwOperand kinds, channel concat. All are HBM-bound streaming
+// kernels over NHWC-C4 (one thread per output vec4, fp32 arithmetic on the
+// storage dtype); the grids cover the output exactly and every index is
+// checked against it.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../../include/aih_model.h"
+#include "aih_device.h"
+#include "capi_util.h"
+
+namespace aih {
+namespace {
+
+constexpr int kMaxParts = 8;
+
+// One input part: device base, channels per pixel of its buffer, first
+// channel, channels, first output channel.
+struct PartArg {
+  const void *p;
+  uint32_t stride_c, c_off, c, out_c0;
+};
+struct Parts {
+  PartArg v[kMaxParts];
+  uint32_t n;
+};
+
+template <int DT>
+__device__ __forceinline__ float ld1(const void *base, size_t i) {
+  if constexpr (DT == DT_F32) return reinterpret_cast<const float *>(base)[i];
+  else if constexpr (DT == DT_F16) return f16_to_f32(reinterpret_cast<const uint16_t *>(base)[i]);
+  else return bf16_to_f32(reinterpret_cast<const uint16_t *>(base)[i]);
+}
+
+// ---------------------------------------------------------------- resize
+
+// reference/resize.rs:13-43: src coordinate, taps clamped to the image,
+// weights clamped to [0, 1]; out = top*(1-ty) + bot*ty.
+__device__ __forceinline__ void resize_coord(uint32_t o, float scale, int mode, uint32_t in, uint32_t &i0,
+                                             uint32_t &i1, float &t) {
+  const float f = mode == AIH_COORD_HALF_PIXEL ? ((float)o + 0.5f) * scale - 0.5f : (float)o * scale;
+  const float fl = floorf(f);
+  const int64_t b = (int64_t)fl;
+  const int64_t hi = (int64_t)in - 1;
+  i0 = (uint32_t)(b < 0 ? 0 : (b > hi ? hi : b));
+  i1 = (uint32_t)(b + 1 < 0 ? 0 : (b + 1 > hi ? hi : b + 1));
+  t = fminf(fmaxf(f - fl, 0.0f), 1.0f);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void resize_kernel(Parts parts, uint32_t n, uint32_t ih, uint32_t iw, uint32_t oh,
+                                                     uint32_t ow, int mode, uint32_t cg_out, void *y) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  const uint64_t total = (uint64_t)n * oh * ow * cg_out;
+  if (i >= total) return;
+  const uint32_t g = (uint32_t)(i % cg_out);
+  const uint64_t pix = i / cg_out;
+  const uint32_t ox = (uint32_t)(pix % ow);
+  const uint64_t t2 = pix / ow;
+  const uint32_t oy = (uint32_t)(t2 % oh);
+  const uint32_t img = (uint32_t)(t2 / oh);
+  // the output vec4 lies in one part (all parts but the last hold a multiple of 4 channels)
+  uint32_t p = 0;
+  while (p + 1 < parts.n && g * 4 >= parts.v[p + 1].out_c0) ++p;
+  const PartArg &pa = parts.v[p];
+  const uint32_t k0 = g * 4 - pa.out_c0;
+  uint32_t y0, y1, x0, x1;
+  float ty, tx;
+  resize_coord(oy, (float)ih / (float)oh, mode, ih, y0, y1, ty);
+  resize_coord(ox, (float)iw / (float)ow, mode, iw, x0, x1, tx);
+  const uint32_t cgi = pa.stride_c / 4;
+  auto at = [&](uint32_t yy, uint32_t xx) {
+    return Vec4IO<DT>::load(pa.p, (((size_t)img * ih + yy) * iw + xx) * cgi + (pa.c_off + k0) / 4);
+  };
+  const f32x4 top = at(y0, x0) * (1.0f - tx) + at(y0, x1) * tx;
+  const f32x4 bot = at(y1, x0) * (1.0f - tx) + at(y1, x1) * tx;
+  Vec4IO<DT>::store(y, i, top * (1.0f - ty) + bot * ty);
+}
+
+// ---------------------------------------------------------------- gpool
+
+// reference/pool.rs:6-19: sum over pixels, times 1/(h*w). One workgroup per
+// (image, channel group); the 256 threads stride over the pixels and reduce
+// in LDS.
+template <int DT>
+__global__ __launch_bounds__(256) void gpool_kernel(const void *x, uint32_t hw, uint32_t cg, float inv, void *y) {
+  __shared__ f32x4 red[256];
+  const uint32_t img = blockIdx.x / cg, g = blockIdx.x % cg;
+  f32x4 s = {};
+  for (uint32_t p = threadIdx.x; p < hw; p += 256) s += Vec4IO<DT>::load(x, ((size_t)img * hw + p) * cg + g);
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (uint32_t o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) Vec4IO<DT>::store(y, (size_t)img * cg + g, red[0] * inv);
+}
+
+// ---------------------------------------------------------------- binary
+
+__device__ __forceinline__ float bin_apply(int op, float a, float b) {
+  switch (op) {
+    case AIH_BIN_ADD: return a + b;
+    case AIH_BIN_SUB: return a - b;
+    case AIH_BIN_MUL: return a * b;
+    default: return a > 0.0f ? a : a * b;  // prelu
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void binary_kernel(const void *a, const void *b, void *y, uint32_t n, uint32_t hw,
+                                                     uint32_t c, int op, int act, int operand, float scalar,
+                                                     int scalar_first, uint32_t b_c) {
+  const uint32_t cg = (c + 3) / 4;
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (uint64_t)n * hw * cg) return;
+  const uint32_t g = (uint32_t)(i % cg);
+  const uint64_t pix = i / cg;  // image-major pixel index
+  const uint32_t img = (uint32_t)(pix / hw);
+  const f32x4 va = Vec4IO<DT>::load(a, i);
+  f32x4 vb;
+  switch (operand) {
+    case AIH_OPND_TENSOR: vb = Vec4IO<DT>::load(b, i); break;
+    case AIH_OPND_SCALAR: vb = f32x4{scalar, scalar, scalar, scalar}; break;
+    case AIH_OPND_CVEC: vb = Vec4IO<DT>::load(b, g); break;
+    case AIH_OPND_CVEC_TENSOR: {
+      // a one-channel vector is a runtime scalar (ai-cpu model.rs:483-491)
+      if (b_c == 1) {
+        const float s = ld1<DT>(b, (size_t)img * 4);
+        vb = f32x4{s, s, s, s};
+      } else {
+        vb = Vec4IO<DT>::load(b, (size_t)img * ((b_c + 3) / 4) + g);
+      }
+      break;
+    }
+    case AIH_OPND_PVEC_TENSOR: {
+      // one value per pixel: a pixel grid with one channel, or a 1x1 vector
+      // of hw channels (ai-cpu model.rs:494-500)
+      const uint64_t p = pix - (uint64_t)img * hw;
+      const float s = b_c == 1 ? ld1<DT>(b, pix * 4) : ld1<DT>(b, (size_t)img * ((b_c + 3) / 4) * 4 + p);
+      vb = f32x4{s, s, s, s};
+      break;
+    }
+    default: {  // tiled: channel k takes b[k % b_c]
+      const uint32_t bcg = (b_c + 3) / 4;
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        const uint32_t k = (g * 4 + l) % b_c;
+        vb[l] = ld1<DT>(b, ((size_t)img * bcg) * 4 + k);
+      }
+      break;
+    }
+  }
+  const Act ap = act_params(act);
+  float v[4];
+#pragma unroll
+  for (int l = 0; l < 4; ++l) v[l] = scalar_first ? bin_apply(op, vb[l], va[l]) : bin_apply(op, va[l], vb[l]);
+  act_array<4>(ap, v);
+  Vec4IO<DT>::store(y, i, f32x4{v[0], v[1], v[2], v[3]});
+}
+
+// ---------------------------------------------------------------- concat
+
+// Any channel counts: every output lane finds its part; padding lanes are 0.
+template <int DT>
+__global__ __launch_bounds__(256) void concat_kernel(Parts parts, uint64_t px, uint32_t c_out, void *y) {
+  const uint32_t cg = (c_out + 3) / 4;
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= px * cg) return;
+  const uint32_t g = (uint32_t)(i % cg);
+  const uint64_t pix = i / cg;
+  f32x4 v = {};
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const uint32_t ch = g * 4 + l;
+    if (ch >= c_out) continue;
+    uint32_t p = 0;
+    while (p + 1 < parts.n && ch >= parts.v[p + 1].out_c0) ++p;
+    const PartArg &pa = parts.v[p];
+    v[l] = ld1<DT>(pa.p, pix * pa.stride_c + pa.c_off + (ch - pa.out_c0));
+  }
+  Vec4IO<DT>::store(y, i, v);
+}
+
+// ---------------------------------------------------------------- host side
+
+bool dt_ok(int32_t dt) { return dt == AIH_F32 || dt == AIH_F16 || dt == AIH_BF16; }
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+size_t vec_bytes(int32_t dt) { return dt == AIH_F32 ? 16 : 8; }
+
+dim3 grid_for(uint64_t threads) { return dim3((unsigned)((threads + 255) / 256)); }
+
+// Validates parts and fills the kernel's table; out_c = total channels.
+int fill_parts(const aih_src *src, uint32_t nsrc, const void *const *inputs, int32_t dt, bool vec_aligned,
+               Parts *parts, uint32_t *out_c) {
+  if (nsrc == 0 || nsrc > kMaxParts) return api_fail("1 to 8 parts");
+  if (!inputs) return api_fail("null inputs");
+  uint32_t c0 = 0;
+  for (uint32_t i = 0; i < nsrc; ++i) {
+    const aih_src &s = src[i];
+    if (!inputs[i]) return api_fail("null input part");
+    if (s.c == 0 || s.stride_c == 0 || s.stride_c % 4 || s.c_off % 4 || s.c_off + s.c > s.stride_c)
+      return api_fail("part view: need c > 0, stride_c and c_off multiples of 4, c_off + c <= stride_c");
+    if (vec_aligned && i + 1 < nsrc && s.c % 4) return api_fail("every part but the last needs a multiple of 4 channels");
+    if (!aligned(inputs[i], vec_bytes(dt))) return api_fail("misaligned input part");
+    parts->v[i] = PartArg{inputs[i], s.stride_c, s.c_off, s.c, c0};
+    c0 += s.c;
+  }
+  parts->n = nsrc;
+  *out_c = c0;
+  return AIH_OK;
+}
+
+}  // namespace
+}  // namespace aih
+
+using namespace aih;
+
+#define AIH_LAUNCH_DT(KERNEL, dt, grid, st, ...)                                           \
+  do {                                                                                     \
+    switch (dt) {                                                                          \
+      case AIH_F32: hipLaunchKernelGGL(KERNEL<DT_F32>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
+      case AIH_F16: hipLaunchKernelGGL(KERNEL<DT_F16>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
+      default: hipLaunchKernelGGL(KERNEL<DT_BF16>, grid, dim3(256), 0, st, __VA_ARGS__); break;     \
+    }                                                                                      \
+  } while (0)
+
+extern "C" {
+
+int aih_resize(const aih_resize_desc *d, const void *const *inputs, void *y, aih_stream stream) {
+  return api_guarded([&] {
+    if (!d) return api_fail("resize: null descriptor");
+    if (!dt_ok(d->dt)) return api_fail("resize: unknown dtype");
+    if (!d->n || !d->ih || !d->iw || !d->oh || !d->ow) return api_fail("resize: zero-sized dimension");
+    if (d->mode != AIH_COORD_HALF_PIXEL && d->mode != AIH_COORD_ASYMMETRIC) return api_fail("resize: unknown mode");
+    if (!y || !aligned(y, vec_bytes(d->dt))) return api_fail("resize: null or misaligned output");
+    Parts parts;
+    uint32_t c = 0;
+    if (fill_parts(d->srcs, d->nsrcs, inputs, d->dt, true, &parts, &c)) return AIH_ERR;
+    const uint32_t cg = (c + 3) / 4;
+    const uint64_t total = (uint64_t)d->n * d->oh * d->ow * cg;
+    if (total == 0 || total > 0xffffffffull * 256) return api_fail("resize: output too large");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    AIH_LAUNCH_DT(resize_kernel, d->dt, grid_for(total), st, parts, d->n, d->ih, d->iw, d->oh, d->ow, (int)d->mode,
+                  cg, y);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? AIH_OK : api_fail(std::string("resize launch: ") + hipGetErrorString(e));
+  });
+}
+
+int aih_gpool(const aih_gpool_desc *d, const void *x, void *y, aih_stream stream) {
+  return api_guarded([&] {
+    if (!d) return api_fail("gpool: null descriptor");
+    if (!dt_ok(d->dt)) return api_fail("gpool: unknown dtype");
+    if (!d->n || !d->h || !d->w || !d->c) return api_fail("gpool: zero-sized dimension");
+    if (!x || !y || !aligned(x, vec_bytes(d->dt)) || !aligned(y, vec_bytes(d->dt)))
+      return api_fail("gpool: null or misaligned buffer");
+    const uint32_t cg = (d->c + 3) / 4;
+    const uint64_t blocks = (uint64_t)d->n * cg;
+    if (blocks > 0x7fffffffull || (uint64_t)d->h * d->w > 0xffffffffull) return api_fail("gpool: too large");
+    const float inv = 1.0f / (float)(d->h * d->w);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    AIH_LAUNCH_DT(gpool_kernel, d->dt, dim3((unsigned)blocks), st, x, d->h * d->w, cg, inv, y);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? AIH_OK : api_fail(std::string("gpool launch: ") + hipGetErrorString(e));
+  });
+}
+
+int aih_binary(const aih_binary_desc *d, const void *a, const void *b, void *y, aih_stream stream) {
+  return api_guarded([&] {
+    if (!d) return api_fail("binary: null descriptor");
+    if (!dt_ok(d->dt)) return api_fail("binary: unknown dtype");
+    if (!d->n || !d->h || !d->w || !d->c) return api_fail("binary: zero-sized dimension");
+    if (d->op < AIH_BIN_ADD || d->op > AIH_BIN_PRELU) return api_fail("binary: unknown op");
+    if (d->act < AIH_ACT_NONE || d->act > AIH_ACT_RECIP) return api_fail("binary: unknown activation");
+    if (d->operand < AIH_OPND_TENSOR || d->operand > AIH_OPND_TILED_TENSOR) return api_fail("binary: unknown operand");
+    const bool tensor_b = d->operand == AIH_OPND_CVEC_TENSOR || d->operand == AIH_OPND_PVEC_TENSOR ||
+                          d->operand == AIH_OPND_TILED_TENSOR;
+    if (tensor_b && d->b_c == 0) return api_fail("binary: vector operands need b_c > 0");
+    if (d->operand == AIH_OPND_CVEC_TENSOR && d->b_c != 1 && d->b_c != d->c)
+      return api_fail("binary: a channel vector needs 1 or c channels");
+    if (d->operand == AIH_OPND_PVEC_TENSOR && d->b_c != 1 && d->b_c != d->h * d->w)
+      return api_fail("binary: a pixel vector needs 1 channel or h*w channels");
+    const size_t vb = vec_bytes(d->dt);
+    if (!a || !y || !aligned(a, vb) || !aligned(y, vb)) return api_fail("binary: null or misaligned a / y");
+    if (d->operand != AIH_OPND_SCALAR && (!b || !aligned(b, tensor_b ? vb / 4 : vb)))
+      return api_fail("binary: null or misaligned b");
+    const uint64_t total = (uint64_t)d->n * d->h * d->w * ((d->c + 3) / 4);
+    if (total > 0xffffffffull * 256) return api_fail("binary: too large");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    AIH_LAUNCH_DT(binary_kernel, d->dt, grid_for(total), st, a, b, y, d->n, d->h * d->w, d->c, (int)d->op,
+                  (int)d->act, (int)d->operand, d->scalar, (int)d->scalar_first, d->b_c);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? AIH_OK : api_fail(std::string("binary launch: ") + hipGetErrorString(e));
+  });
+}
+
+int aih_concat(const aih_concat_desc *d, const void *const *inputs, void *y, aih_stream stream) {
+  return api_guarded([&] {
+    if (!d) return api_fail("concat: null descriptor");
+    if (!dt_ok(d->dt)) return api_fail("concat: unknown dtype");
+    if (!d->n || !d->h || !d->w) return api_fail("concat: zero-sized dimension");
+    if (!y || !aligned(y, vec_bytes(d->dt))) return api_fail("concat: null or misaligned output");
+    Parts parts;
+    uint32_t c = 0;
+    if (fill_parts(d->parts, d->nparts, inputs, d->dt, false, &parts, &c)) return AIH_ERR;
+    const uint64_t px = (uint64_t)d->n * d->h * d->w;
+    const uint64_t total = px * ((c + 3) / 4);
+    if (total > 0xffffffffull * 256) return api_fail("concat: too large");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    AIH_LAUNCH_DT(concat_kernel, d->dt, grid_for(total), st, parts, px, c, y);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? AIH_OK : api_fail(std::string("concat launch: ") + hipGetErrorString(e));
+  });
+}
+
+}  // extern "C"

@@ -190,6 +190,10 @@ int aih_conv_dw(const aih_dw_desc *d, const void *x, const void *w, const void *
 int aih_conv(const aih_conv_desc *d, const void *x, const void *w, const void *bias,
              const void *res, void *y, void *ws, size_t ws_bytes, aih_stream stream);
 size_t aih_conv_workspace_size(const aih_conv_desc *d);
+/* Validates a descriptor as aih_conv would (routing, shapes, dtypes, plan)
+ * without launching: AIH_OK, or AIH_ERR with the reason (lower_op's load-time
+ * rejection of a conv it cannot run, lowering.rs:136-140). */
+int aih_conv_check(const aih_conv_desc *d);
 
 /* Fused block (no counterpart op in the reference: a fusion of the three
  * dispatches above). Fails with a message when the shape cannot run fused

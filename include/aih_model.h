@@ -1,0 +1,174 @@
+/*
+ * aih_model.h -- the graph-level C ABI: a .sw model resident on one MI355X,
+ * and the non-conv ops a segmentation graph needs around the conv path.
+ *
+ * Model verbs replace ai_gpu_runtime::Model (crates/ai-gpu-runtime/src/model.rs):
+ *   - aih_model_load          <- Model::load (:56): parse the .sw container
+ *                                (crates/ai-core/src/format/header.rs:58-86, model.rs:79-307),
+ *                                upload the weight blob once, allocate every tensor,
+ *                                lower every op (lower_op, lowering.rs:88-516)
+ *   - aih_model_upload_input  <- Model::upload_input (:387-399)
+ *   - aih_model_infer         <- Model::infer (:402-426): submit only
+ *   - aih_model_read_output   <- Model::read_output (:442-457)
+ *   - aih_model_reset         <- Model::reset (:368-385): zero the state tensors
+ *   - aih_model_tensor        <- Model::input_storage / output_storage (:465-478):
+ *                                the device buffer of a tensor, for zero-copy callers
+ *   - aih_model_free          <- Drop
+ * Op entry points replace the reference's non-conv lowerings (lowering.rs:188-516):
+ *   - aih_resize  <- SwOp::Resize (bilinear, half_pixel / asymmetric, concat parts)
+ *   - aih_gpool   <- SwOp::Gpool (channel mean)
+ *   - aih_binary  <- SwOp::Binary (add / sub / mul / prelu, six operand kinds) + act
+ *   - aih_concat  <- SwOp::Concat (channel concat)
+ *
+ * Supported .sw ops: Conv (all of lower_op's routes, concat parts, residual),
+ * Binary, Gpool, Resize, Concat. Any other op kind makes aih_model_load fail
+ * with a message naming it. Conventions as in aih_conv.h: AIH_OK / AIH_ERR,
+ * aih_last_error(), NHWC-C4 activations with the batch outermost, fp32
+ * arithmetic on f32 / f16 / bf16 storage.
+ */
+#ifndef AIH_MODEL_H
+#define AIH_MODEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "aih_conv.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- non-conv ops (asynchronous on `stream`; caller-owned device buffers) ---- */
+
+/* Bilinear resize (crates/ai-core/src/reference/resize.rs:6-44): src coordinate
+ * (dst + 0.5) * in/out - 0.5 (half_pixel) or dst * in/out (asymmetric), taps
+ * clamped to the image. The output holds the parts' channels one after the
+ * other (concat-into-resize, model.rs:150-159): part i is srcs[i] of
+ * inputs[i]; every part but the last has a multiple of 4 channels. */
+enum aih_coord { AIH_COORD_HALF_PIXEL = 0, AIH_COORD_ASYMMETRIC = 1 };
+typedef struct {
+  uint32_t n, ih, iw, oh, ow;
+  int32_t mode; /* enum aih_coord */
+  int32_t dt;
+  uint32_t nsrcs; /* 1..8 */
+  aih_src srcs[8];
+} aih_resize_desc;
+int aih_resize(const aih_resize_desc *d, const void *const *inputs, void *y, aih_stream stream);
+
+/* Global average pool (reference/pool.rs:6-19): y[b][0][0][c] = mean over the
+ * h*w pixels of x[b][.][.][c]. */
+typedef struct {
+  uint32_t n, h, w, c;
+  int32_t dt;
+} aih_gpool_desc;
+int aih_gpool(const aih_gpool_desc *d, const void *x, void *y, aih_stream stream);
+
+/* y = act(a op b) (ops/elementwise.rs:13-27, reference/elementwise.rs:7-30),
+ * a and y [n][h][w][c]. The operand b (SwOperand, model.rs:60-78):
+ *   TENSOR       [n][h][w][c]
+ *   SCALAR       `scalar`; scalar_first = 1 computes scalar op a
+ *   CVEC         [c] constant channel vector (NHWC-C4 of 1x1xc, no batch)
+ *   CVEC_TENSOR  [n][1][1][b_c] runtime channel vector (an SE gate), b_c = c;
+ *                b_c = 1 is a runtime scalar
+ *   PVEC_TENSOR  one runtime value per pixel, broadcast over channels:
+ *                [n][h][w][1] (b_c = 1) or [n][1][1][h*w] (b_c = h*w)
+ *   TILED_TENSOR [n][1][1][b_c] runtime vector, channel k takes element k % b_c
+ * (ai-cpu model.rs:478-507). */
+enum aih_binop { AIH_BIN_ADD = 0, AIH_BIN_SUB = 1, AIH_BIN_MUL = 2, AIH_BIN_PRELU = 3 };
+enum aih_operand {
+  AIH_OPND_TENSOR = 0,
+  AIH_OPND_SCALAR = 1,
+  AIH_OPND_CVEC = 2,
+  AIH_OPND_CVEC_TENSOR = 3,
+  AIH_OPND_PVEC_TENSOR = 4,
+  AIH_OPND_TILED_TENSOR = 5
+};
+typedef struct {
+  uint32_t n, h, w, c;
+  int32_t op;      /* enum aih_binop */
+  int32_t act;     /* enum aih_act, applied after op */
+  int32_t dt;
+  int32_t operand; /* enum aih_operand */
+  float scalar;
+  int32_t scalar_first;
+  uint32_t b_c;    /* channels of a tensor operand b (vector kinds) */
+} aih_binary_desc;
+int aih_binary(const aih_binary_desc *d, const void *a, const void *b, void *y, aih_stream stream);
+
+/* Channel concat (model.rs:160-164): the output holds parts[0] channels, then
+ * parts[1] ..., any channel counts. */
+typedef struct {
+  uint32_t n, h, w;
+  int32_t dt;
+  uint32_t nparts; /* 1..8 */
+  aih_src parts[8];
+} aih_concat_desc;
+int aih_concat(const aih_concat_desc *d, const void *const *inputs, void *y, aih_stream stream);
+
+/* ---- model ---- */
+
+typedef struct aih_model aih_model;
+
+/* Parses `bytes` (a whole .sw container, copied; the caller may free it
+ * afterwards), uploads the weights and allocates every tensor for a batch of
+ * n images (n >= 1; the reference has n = 1). dt = -1 keeps the file's dtypes
+ * (dt_default for activations, dt_weights for std conv weights,
+ * format/model.rs:245-254); AIH_F16 / AIH_BF16 converts an fp32 file's
+ * weights and biases to that dtype at load (round to nearest even) and runs
+ * every activation in it. Returns NULL on failure (aih_last_error). The model
+ * uses the current HIP device. */
+aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt);
+void aih_model_free(aih_model *m);
+
+/* Logical NHWC fp32 (n*h*w*c floats) of an input -> its NHWC-C4 tensor. host
+ * memory (the copy completes before the call returns) or, for the _device
+ * variant, device memory. */
+int aih_model_upload_input(aih_model *m, const char *name, const float *host_nhwc, size_t count,
+                           aih_stream stream);
+int aih_model_upload_input_device(aih_model *m, const char *name, const float *dev_nhwc, size_t count,
+                                  aih_stream stream);
+/* Runs every op in order on `stream` (asynchronous). */
+int aih_model_infer(aih_model *m, aih_stream stream);
+/* Runs ops [first, last) only (per-op timing and parity; the reference's
+ * ai-cpu profiler times op by op, crates/ai-cpu/src/model.rs:241-272). */
+int aih_model_infer_range(aih_model *m, uint32_t first, uint32_t last, aih_stream stream);
+/* A tensor (by name; outputs and any other tensor) as logical NHWC fp32,
+ * n*h*w*c floats; waits for `stream`. */
+int aih_model_read_output(aih_model *m, const char *name, float *host_nhwc, size_t count, aih_stream stream);
+/* Overwrites any tensor (a channel view too: the other channels of its
+ * backing buffer are kept) with logical NHWC fp32 values, n*h*w*c floats;
+ * waits for `stream` and completes before returning. */
+int aih_model_write_tensor(aih_model *m, const char *name, const float *host_nhwc, size_t count,
+                           aih_stream stream);
+/* Zeroes the state tensors (SwState inputs and outputs). */
+int aih_model_reset(aih_model *m, aih_stream stream);
+
+typedef struct {
+  void *data;       /* device pointer of the tensor's first element (its view start) */
+  size_t bytes;     /* bytes of the backing NHWC-C4 buffer from `data` on */
+  uint32_t n, h, w, c;
+  uint32_t stride_c; /* channels per pixel of the backing buffer (multiple of 4) */
+  int32_t dt;
+} aih_tensor_info;
+int aih_model_tensor(const aih_model *m, const char *name, aih_tensor_info *out);
+
+typedef struct {
+  uint32_t n_tensors, n_ops, n_inputs, n_outputs, n_launches;
+  int32_t dt, wdt;
+  size_t device_bytes; /* weights + tensors + workspace */
+} aih_model_info;
+int aih_model_get_info(const aih_model *m, aih_model_info *out);
+/* Name of input / output i (valid while m lives). */
+const char *aih_model_input_name(const aih_model *m, uint32_t i);
+const char *aih_model_output_name(const aih_model *m, uint32_t i);
+
+/* Parses a .sw container without a device and writes a one-line JSON summary
+ * (name, dtypes, tensor / op counts per kind) into buf. Returns the summary's
+ * length, or AIH_ERR (the container or graph is invalid or unsupported). */
+int aih_sw_describe(const void *bytes, size_t len, char *buf, size_t buflen);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AIH_MODEL_H */

@@ -16,18 +16,25 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def header_functions():
-    text = open(os.path.join(ROOT, "include", "aih_conv.h")).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(aih_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if not h.endswith(".h"):
+            continue
+        text = open(os.path.join(ROOT, "include", h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(aih_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_function():
-    L = conv.lib()
+    from ai_engine_amd import sw
+
+    L = sw.lib()
     declared = header_functions()
-    assert len(declared) >= 16
+    assert len(declared) >= 33
     for name in declared:
         assert hasattr(L, name), name
-    assert set(conv.EXPORTS) == set(declared)
+    assert set(conv.EXPORTS) | set(sw.EXPORTS) == set(declared)
     assert b"gfx950" in L.aih_version()
 
 
