@@ -173,6 +173,7 @@ def main() -> int:
     kernels = {}
     if not args.no_kernels:
         kernels = kernel_table(torch, conv, W, Model, dev, stream, DT)
+        kernels.update(real_model(torch, conv, dev, stream))
         kernels["encoder_f16" if args.dtype == "bf16" else "encoder_bf16"] = encoder_other(
             torch, W, Model, layers, wts, x, n, H, Wd, "f16" if args.dtype == "bf16" else "bf16", DT, stream)
     kernels["encoder_layers"] = layer_rows
@@ -320,6 +321,40 @@ def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
     log(f"ir chain: {row['us']:.1f} us frac {row['frac']:.3f}")
     del m4
     return res
+
+
+def real_model(torch, conv, dev, stream) -> dict:
+    """The reference converter's real segmentation model (tests/golden/
+    segm_r11_160x288.sw: 36 convs + resize / gpool / binary / concat) through
+    the native .sw runtime, batch 64, fp32 as converted and with 16-bit
+    storage converted at load; one step = device upload + the whole graph."""
+    from ai_engine_amd import sw
+
+    data = open(os.path.join(ROOT, "tests", "golden", "segm_r11_160x288.sw"), "rb").read()
+    g, _ = sw.read_container(data)
+    T = g["tensors"]
+    macs = 0
+    for op in g["ops"]:
+        if op["kind"] == "conv":
+            o = T[op["out"]]
+            macs += o["h"] * o["w"] * op["kh"] * op["kw"] * op["cin"] * op["cout"] // op["groups"]
+    n = 64
+    x = (torch.rand(n, 160, 288, 3, device=dev) * 2 - 1).contiguous()
+    out = {}
+    for dt in ("f32", "f16"):
+        m = sw.SwModel(data, n=n, dt=None if dt == "f32" else conv.DType.F16)
+
+        def step(_):
+            m.upload_input("input_1", x, stream)
+            m.infer(stream)
+
+        t = time_launches(torch, stream, step, 10)
+        out[f"segm_r11_real_160x288_b{n}_{dt}"] = dict(us=round(t * 1e6, 1), frames_per_s=round(n / t, 1),
+                                                     tflops=round(2 * macs * n / t / 1e12, 2),
+                                                     gflop_per_frame=round(2 * macs / 1e9, 3), ops=len(g["ops"]))
+        log(f"real segm model {dt} b{n}: {t * 1e3:.3f} ms {n / t:.0f} frames/s")
+        m.close()
+    return out
 
 
 def encoder_other(torch, W, Model, layers, wts, x, n, H, Wd, dtname, DT, stream) -> dict:
