@@ -6,6 +6,7 @@
 // for aih_last_error().
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <exception>
@@ -54,7 +55,8 @@ size_t dsize(int32_t dt) { return dt == AIH_F32 ? 4 : 2; }
 // worth cutting. Re-tuned for MI355X: 256 CUs, one 128-pixel MFMA tile per
 // workgroup; split when the tile grid covers fewer than 256 CUs and K holds at
 // least 16 channel groups (the reference's own kg >= 16 gate), aiming at two
-// workgroups per CU, at most 8 chunks, and at least one full stage per chunk.
+// workgroups per CU, at most 32 chunks, and at least one full stage per chunk;
+// such grids also take narrower column tiles first.
 constexpr uint32_t kCUs = 256;
 
 // kg per K stage of the kernel: 16 channels for fp32, 32 for 16-bit storage.
@@ -87,6 +89,22 @@ int plan_gemm(uint32_t M, uint32_t N4, uint32_t KK, int32_t dt, int32_t variant,
   p->bn = pick_bn(N4);
   p->mtiles = div_ceil(M, aih::GEMM_BM);
   p->ntiles = div_ceil(N4, p->bn);
+  if (p->mtiles * p->ntiles < kCUs) {
+    // a grid below the CU count: narrower column tiles give more workgroups,
+    // as long as the padded columns stay within 25 % of the tightest fit
+    const uint64_t best_cols = (uint64_t)p->ntiles * p->bn;
+    uint32_t best_tiles = p->mtiles * p->ntiles;
+    for (int bn : aih::kGemmBN) {
+      const uint32_t nt = div_ceil(N4, bn);
+      if ((uint64_t)nt * bn * 4 > best_cols * 5) continue;
+      const uint32_t t = std::min<uint32_t>(p->mtiles * nt, kCUs);
+      if (t > best_tiles) {
+        best_tiles = t;
+        p->bn = bn;
+        p->ntiles = nt;
+      }
+    }
+  }
   const uint32_t bkg = (uint32_t)stage_kg(dt);
   const uint32_t tiles = p->mtiles * p->ntiles;
   uint32_t s = 1;
@@ -96,7 +114,7 @@ int plan_gemm(uint32_t M, uint32_t N4, uint32_t KK, int32_t dt, int32_t variant,
     s = 4;
   } else if (variant == AIH_VAR_AUTO && tiles < kCUs && KK >= 16) {
     s = (2 * kCUs) / tiles;
-    if (s > 8) s = 8;
+    if (s > 32) s = 32;
     const uint32_t max_s = KK / bkg;
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
@@ -128,6 +146,12 @@ int run_gemm(aih::GemmArgs &a, const GemmPlan &g, int32_t dt, int32_t wdt, bool 
   a.nsplit = g.nsplit;
   a.ntiles_total = g.mtiles * g.ntiles * g.nsplit;
   a.kk_chunk = g.kk_chunk;
+  a.fd_ntiles = aih::make_fastdiv(a.ntiles);
+  a.fd_mtiles = aih::make_fastdiv(a.mtiles);
+  a.fd_KG = aih::make_fastdiv(a.KG);
+  a.fd_K = aih::make_fastdiv(a.K);
+  a.fd_OHW = aih::make_fastdiv(a.OHW);
+  a.fd_OW = aih::make_fastdiv(a.OW);
   a.partial = nullptr;
   if (g.nsplit > 1) {
     if (ws == nullptr || ws_bytes < g.ws)

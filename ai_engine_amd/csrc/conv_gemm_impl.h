@@ -77,6 +77,8 @@ struct GemmArgs {
   uint32_t ntiles_total;  // mtiles * ntiles * nsplit
   int32_t act;
   int32_t has_res;
+  // the divisors above the kernel divides by, prepared on the host
+  FastDiv fd_ntiles, fd_mtiles, fd_KG, fd_K, fd_OHW, fd_OW;
 };
 
 constexpr int GEMM_THREADS = 256;
@@ -140,9 +142,11 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
   };
   auto tile_info = [&](uint32_t T) {
     TileInfo ti;
-    const uint32_t nt = T % a.ntiles;
-    const uint32_t mt = (T / a.ntiles) % a.mtiles;
-    ti.split = T / (a.ntiles * a.mtiles);
+    const uint32_t q = fdiv(T, a.fd_ntiles);
+    const uint32_t nt = T - q * a.ntiles;
+    const uint32_t q2 = fdiv(q, a.fd_mtiles);
+    const uint32_t mt = q - q2 * a.mtiles;
+    ti.split = q2;
     ti.m0 = mt * GEMM_BM;
     ti.n0 = nt * BN;
     ti.kk_begin = ti.split * a.kk_chunk;
@@ -165,9 +169,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
       a_ok[i] = m < a.M;
       if constexpr (IGEMM) {
         const uint32_t mm = a_ok[i] ? m : 0;
-        const uint32_t img = mm / a.OHW;
+        const uint32_t img = fdiv(mm, a.fd_OHW);
         const uint32_t rem = mm - img * a.OHW;
-        const uint32_t oy = rem / a.OW;
+        const uint32_t oy = fdiv(rem, a.fd_OW);
         const uint32_t ox = rem - oy * a.OW;
         a_iy0[i] = (int32_t)(oy * a.S) - a.PT;
         a_ix0[i] = (int32_t)(ox * a.S) - a.PL;
@@ -203,9 +207,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
     uint32_t kg = kk;
     int32_t dy = 0, dx = 0;
     if constexpr (IGEMM) {
-      const uint32_t tap = kk / a.KG;
+      const uint32_t tap = fdiv(kk, a.fd_KG);
       kg = kk - tap * a.KG;
-      const uint32_t ky = tap / a.K;
+      const uint32_t ky = fdiv(tap, a.fd_K);
       const uint32_t kx = tap - ky * a.K;
       dy = (int32_t)(ky * a.D);
       dx = (int32_t)(kx * a.D);
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
       if ((W_TOTAL % GEMM_THREADS == 0 || idx < W_TOTAL) && wkk < ti.kk_end && n < a.N4) {
         uint32_t wt = 0, wkg = wkk;
         if constexpr (IGEMM) {
-          wt = wkk / a.KG;
+          wt = fdiv(wkk, a.fd_KG);
           wkg = wkk - wt * a.KG;
         }
         const size_t vidx = (size_t)(wt * a.KGP + wkg) * a.N4 + n;

@@ -301,6 +301,7 @@ def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
     pw_case("pw_32to64_relu6_80x144", 1, 80, 144, 32, 64, A.RELU6, reps=200)
     for s in (1, 4, 8):
         pw_case(f"pw_960to160_10x18_b1_splitk{s}", 1, 10, 18, 960, 160, A.NONE, splitk=s, reps=200)
+    pw_case("pw_960to160_10x18_b1_policy", 1, 10, 18, 960, 160, A.NONE, splitk=0, reps=200)
     pw_case("pw_960to160_10x18_b256", 256, 10, 18, 960, 160, A.NONE, reps=40)
     ig_case("igemm3x3s2_16to32_relu_160x288_b32", 32, 160, 288, 16, 32, 2, A.RELU)
     ig_case("igemm3x3s1_32to64_relu_80x144_b32", 32, 80, 144, 32, 64, 1, A.RELU)

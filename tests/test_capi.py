@@ -71,9 +71,10 @@ def test_pw_policy_splits_small_m_large_k():
     p = pw_plan(256, 180, 960, 160)
     assert p.variant == conv.Variant.TILE and p.splitk == 1 and p.ws_bytes == 0
     assert p.bn == 160 and p.grid == 360
-    # 1x1 32 -> 64 at 80x144: K is one stage, nothing to split
+    # 1x1 32 -> 64 at 80x144: K is one stage, nothing to split; 90 pixel
+    # tiles cannot fill 256 CUs, so the columns are cut into two 32-wide tiles
     p = pw_plan(1, 11520, 32, 64)
-    assert p.variant == conv.Variant.TILE and p.bn == 64 and p.grid == 90
+    assert p.variant == conv.Variant.TILE and p.bn == 32 and p.grid == 180
 
 
 def test_pw_policy_agrees_with_reference_on_its_splitk_kats(orc):
