@@ -56,7 +56,7 @@ size_t dsize(int32_t dt) { return dt == AIH_F32 ? 4 : 2; }
 // workgroup; split when the tile grid covers fewer than 256 CUs and K holds at
 // least 16 channel groups (the reference's own kg >= 16 gate), aiming at two
 // workgroups per CU, at most 32 chunks, and at least one full stage per chunk;
-// such grids also take narrower column tiles first.
+// a grid that splitting cannot bring there takes narrower column tiles first.
 constexpr uint32_t kCUs = 256;
 
 // kg per K stage of the kernel: 16 channels for fp32, 32 for 16-bit storage.
@@ -89,9 +89,16 @@ int plan_gemm(uint32_t M, uint32_t N4, uint32_t KK, int32_t dt, int32_t variant,
   p->bn = pick_bn(N4);
   p->mtiles = div_ceil(M, aih::GEMM_BM);
   p->ntiles = div_ceil(N4, p->bn);
-  if (p->mtiles * p->ntiles < kCUs) {
-    // a grid below the CU count: narrower column tiles give more workgroups,
-    // as long as the padded columns stay within 25 % of the tightest fit
+  const uint32_t bkg = (uint32_t)stage_kg(dt);
+  // the most K chunks this call may use
+  uint32_t split_cap = 1;
+  if (splitk > 0) split_cap = (uint32_t)splitk;
+  else if (variant == AIH_VAR_SPLITK) split_cap = 4;
+  else if (variant == AIH_VAR_AUTO && KK >= 16) split_cap = std::min<uint32_t>(32, std::max<uint32_t>(KK / bkg, 1));
+  if ((uint64_t)p->mtiles * p->ntiles * split_cap < 2 * kCUs) {
+    // a grid that splitting K cannot bring to two workgroups per CU: narrower
+    // column tiles give more workgroups, as long as the padded columns stay
+    // within 25 % of the tightest fit
     const uint64_t best_cols = (uint64_t)p->ntiles * p->bn;
     uint32_t best_tiles = p->mtiles * p->ntiles;
     for (int bn : aih::kGemmBN) {
@@ -105,7 +112,6 @@ int plan_gemm(uint32_t M, uint32_t N4, uint32_t KK, int32_t dt, int32_t variant,
       }
     }
   }
-  const uint32_t bkg = (uint32_t)stage_kg(dt);
   const uint32_t tiles = p->mtiles * p->ntiles;
   uint32_t s = 1;
   if (splitk > 0) {
@@ -512,6 +518,10 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
     a.act_d = d->act_dw;
     a.act_p = d->act_project;
     a.has_res = d->residual ? 1 : 0;
+    // activations with act(0) != 0 (the depthwise's zero padding is 0 after
+    // the expand's activation, not act(0))
+    a.mask_e = (d->act_expand == AIH_ACT_SIGMOID || d->act_expand == AIH_ACT_HARDSIGMOID ||
+                d->act_expand == AIH_ACT_RECIP) ? 1 : 0;
     a.lds_x = p.lds_x;
     a.lds_xe = p.lds_xe;
     a.lds_we = p.lds_we;

@@ -29,6 +29,7 @@ struct IrArgs {
   uint32_t resident;     // 1: all E channels' weights stay in LDS for every tile
   uint32_t tiles_y, tiles_x, ntiles;
   int32_t act_e, act_d, act_p, has_res;
+  int32_t mask_e;        // act_e(0) != 0: expanded halo pixels outside the image are masked to 0
   uint32_t lds_x, lds_xe, lds_we, lds_wp, lds_sm, lds_bp;  // LDS byte offsets
   // divisors the kernel uses, prepared on the host
   FastDiv fd_rpx;              // 16-byte items per LDS input row (vectors per pixel + 1)

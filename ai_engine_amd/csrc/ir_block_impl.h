@@ -18,10 +18,13 @@
 // pixels of one image and walks E in chunks of EC channels:
 //   (0) the input tile with its halo, HH x HW pixels x C channels, is copied
 //       to LDS once per tile (zeros outside the image);
-//   (1) expand: [halo px x C] x [C x EC] on MFMA, in 32-pixel x 32-channel
-//       blocks dealt round-robin to the wavefronts; bias + act in the MFMA
-//       layout; halo pixels outside the image are set to 0 (they are the
-//       depthwise zero padding, not expand(0)); the chunk is stored to LDS;
+//   (1) expand: [halo px x (C + 1)] x [(C + 1) x EC] on MFMA, in 32-pixel x
+//       32-channel blocks dealt round-robin to the wavefronts, the bias being
+//       the extra K row against a column that is 1 inside the image and 0
+//       outside; act in the MFMA layout; halo pixels outside the image come
+//       out 0 (the depthwise zero padding, not act(expand(0))) -- masked
+//       explicitly only for activations with act(0) != 0; the chunk is stored
+//       to LDS;
 //   (2) depthwise + project: every wavefront owns NPW 32-pixel blocks of the
 //       output tile. Lane l computes the depthwise output of pixel l%32 for
 //       the K slice that lane l feeds to the projection MFMA, so the
@@ -116,6 +119,8 @@ __device__ __forceinline__ void ir_fma_taps(u32x4 xv, u32x4 wv, float (&d)[HK]) 
 typedef __attribute__((address_space(3))) void ir_lds_void;
 // An offset past every buffer the kernel reads (the host keeps each below 2 GiB).
 constexpr uint32_t IR_OOB = 0x80000000u;
+// A source offset meaning "leave this item of LDS as it is" (the lane issues nothing).
+constexpr uint32_t IR_SKIP = 0xffffffffu;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ir_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
@@ -130,7 +135,13 @@ __device__ __forceinline__ void ir_dma(char *dst, uint32_t n, __amdgpu_buffer_rs
                                        F src) {
   for (uint32_t g0 = (uint32_t)((wave - w0) & 3) * 64; g0 < n; g0 += 256) {
     const uint32_t g = g0 + lane;
-    if (g < n) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (ir_lds_void *)(dst + g0 * SZ), SZ, src(g), 0, 0, 0);
+    const uint32_t off = g < n ? src(g) : IR_SKIP;
+    if (off == IR_SKIP) continue;
+    ir_lds_void *d = (ir_lds_void *)(dst + g0 * SZ);
+    if constexpr (SZ == 16)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, d, 16, off, 0, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, d, 4, off, 0, 0, 0);
   }
 }
 
@@ -241,17 +252,27 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
     // every wavefront is done with the previous tile's LDS
     __syncthreads();
     // (0) input tile with halo -> XL: item g is 16 bytes of halo row
-    // r = g / (NVX + 1); the row's last item (the pitch padding) and pixels
-    // outside the image read as zeros. Streamed weights: chunk 0 -> slot 0.
+    // r = g / (NVX + 1); pixels outside the image read as zeros. The row's
+    // last item (the pitch padding) is the bias column of the expand: 1.0 in
+    // its first K slot for pixels inside the image, 0 outside, so the expand
+    // of an outside pixel is exactly 0. Streamed weights: chunk 0 -> slot 0.
     {
       const __amdgpu_buffer_rsrc_t rs_x = ir_rsrc(xg + (size_t)img * img_bytes, img_bytes);
       ir_dma<16>(XL, a.NPI * 32 * (NVX + 1), rs_x, wave, lane, 0, [&](uint32_t g) -> uint32_t {
         const uint32_t r = fdiv(g, a.fd_rpx), v = g - r * (NVX + 1);
+        if (v == NVX) return IR_SKIP;
         const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
         const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
-        const bool in = v < NVX && r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
+        const bool in = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
         return in ? ((uint32_t)iy * a.IW + (uint32_t)ix) * (NVX * 16) + v * 16 : IR_OOB;
       });
+      constexpr uint32_t ONE = F32 ? 0x3F800000u : (DT == DT_F16 ? 0x3C00u : 0x3F80u);
+      for (uint32_t r = tid; r < a.NPI * 32; r += 256) {
+        const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
+        const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
+        const bool in = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
+        *reinterpret_cast<u32x4 *>(XL + r * RPX + NVX * 16) = u32x4{in ? ONE : 0u, 0u, 0u, 0u};
+      }
     }
     if (!a.resident) dma_chunk(0, 0);
     ir_dma_wait();
@@ -294,23 +315,34 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
           a0 = a1;
           b0 = b1;
         }
+        // the bias as one more K step: bias of channel l32 (A) x the tile's
+        // bias column (B), both in the first K slot of lane half 0
+        {
+          const u32x4 bx = *reinterpret_cast<const u32x4 *>(XL + (b * 32 + l32) * RPX + NVX * 16);
+          if constexpr (F32) {
+            const float bw = lh == 0 ? *reinterpret_cast<const float *>(bes + l32 * 4) : 0.0f;
+            const float bo = lh == 0 ? __uint_as_float(bx.x) : 0.0f;
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(bw, bo, acc, 0, 0, 0);
+          } else {
+            const uint32_t bw = lh == 0 ? (uint32_t)*reinterpret_cast<const uint16_t *>(bes + l32 * 2) : 0u;
+            acc = ir_mma<DT>(u32x4{bw, 0u, 0u, 0u}, lh == 0 ? bx : u32x4{0u, 0u, 0u, 0u}, acc);
+          }
+        }
         const uint32_t r = b * 32 + l32;
-        const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
-        const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
-        const bool inside = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
-        // pixels outside the image: the masking is skipped for blocks wholly
-        // inside (a wave-uniform test)
-        const bool mask = !__all(inside);
+        // outside pixels are 0 before the activation; only an activation with
+        // act(0) != 0 needs them masked (a wave-uniform test skips blocks
+        // wholly inside)
+        bool mask = false, inside = true;
+        if (a.mask_e) {
+          const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
+          const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
+          inside = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
+          mask = !__all(inside);
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t el = 8 * q + 4 * lh;
           float v[4] = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
-          f32x4 bb;
-          if constexpr (F32)
-            bb = *reinterpret_cast<const f32x4 *>(bes + el * 4);
-          else
-            bb = unpack4<DT>(*reinterpret_cast<const u32x2 *>(bes + el * 2));
-          v[0] += bb.x; v[1] += bb.y; v[2] += bb.z; v[3] += bb.w;
           act_array<4>(act_e, v);
           if (mask && !inside) v[0] = v[1] = v[2] = v[3] = 0.0f;
           if constexpr (F32)
