@@ -291,3 +291,35 @@ def test_synthetic_chain_through_the_native_loader(orc):
     m.upload_input("input", x)
     m.infer()
     assert G.rel_err(m.read_output(), want) <= 1e-4
+
+
+def test_model_load_rejects_what_it_cannot_run(segm):
+    """aih_model_load returns NULL with a message (no device work) for graphs
+    it cannot run: an unsupported op kind, a weight reference outside the
+    blob, a 16-bit file asked to widen, a zero batch."""
+    from oracle import sw_oracle
+
+    data, _ = segm
+    g, blob = sw_oracle.read_container(data)
+    bad = json_copy(g)
+    bad["ops"].append({"kind": "maxpool", "in": 44, "out": 45, "kh": 2, "kw": 2, "sh": 2, "sw": 2, "pad": [0] * 4})
+    with pytest.raises(conv.AihError, match="maxpool"):
+        sw.SwModel(sw.write_container(bad, blob))
+    bad = json_copy(g)
+    bad["ops"][0]["w"]["off"] = len(blob)
+    with pytest.raises(conv.AihError, match="outside the blob"):
+        sw.SwModel(sw.write_container(bad, blob))
+    bad = json_copy(g)
+    bad["dt_default"] = "f16"
+    for t in bad["tensors"]:
+        t["dt"] = "f16"
+    with pytest.raises(conv.AihError, match="fp32 file"):
+        sw.SwModel(sw.write_container(bad, blob), dt=conv.DType.BF16)
+    with pytest.raises(conv.AihError, match="n must be"):
+        sw.SwModel(data, n=0)
+
+
+def json_copy(g):
+    import json
+
+    return json.loads(json.dumps(g))
