@@ -18,6 +18,7 @@
 #include "capi_util.h"
 #include "conv_dw.h"
 #include "conv_gemm_launch.h"
+#include "conv_pw_narrow.h"
 #include "ir_block.h"
 
 std::string &aih::last_error_slot() {
@@ -299,6 +300,14 @@ int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *
     if ((d->residual != 0) != (res != nullptr)) return fail("pw: res must be given iff residual");
     if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16) || !aligned(bias, 8) || (res && !aligned(res, 16)))
       return fail("pw: misaligned buffer (x, w, y, res need 16 bytes, bias 8)");
+    if (d->ng == 1 && d->variant == AIH_VAR_AUTO && d->splitk == 0 && d->kg <= aih::kPwNarrowMaxKG) {
+      // at most 4 output channels: one pixel per thread on the VALU
+      const uint64_t M = (uint64_t)d->n * d->m;
+      if (M > 0xffffffffull) return fail("pw: too many pixels");
+      aih::PwNarrowArgs na{x, w, bias, res, y, (uint32_t)M, d->kg, d->kg, d->act, d->residual ? 1 : 0};
+      const hipError_t e = aih::launch_pw_narrow(na, d->dt, d->wdt, static_cast<hipStream_t>(stream));
+      return e == hipSuccess ? AIH_OK : fail(std::string("pw narrow launch: ") + hipGetErrorString(e));
+    }
     GemmPlan g;
     if (plan_pw(d, &g)) return AIH_ERR;
     aih::GemmArgs a;

@@ -3,7 +3,8 @@
 // with the six SwOperand kinds, channel concat. All are HBM-bound streaming
 // kernels over NHWC-C4 (one thread per output vec4, fp32 arithmetic on the
 // storage dtype); the grids cover the output exactly and every index is
-// checked against it.
+// checked against it. Output vec4 counts are kept below 2^32 (checked on the
+// host) so the index decomposition is 32-bit with precomputed divisors.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -51,17 +52,17 @@ __device__ __forceinline__ void resize_coord(uint32_t o, float scale, int mode, 
 }
 
 template <int DT>
-__global__ __launch_bounds__(256) void resize_kernel(Parts parts, uint32_t n, uint32_t ih, uint32_t iw, uint32_t oh,
-                                                     uint32_t ow, int mode, uint32_t cg_out, void *y) {
-  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  const uint64_t total = (uint64_t)n * oh * ow * cg_out;
+__global__ __launch_bounds__(256) void resize_kernel(Parts parts, uint32_t total, uint32_t ih, uint32_t iw,
+                                                     uint32_t oh, uint32_t ow, int mode, uint32_t cg_out,
+                                                     FastDiv fd_cg, FastDiv fd_ow, FastDiv fd_oh, void *y) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
   if (i >= total) return;
-  const uint32_t g = (uint32_t)(i % cg_out);
-  const uint64_t pix = i / cg_out;
-  const uint32_t ox = (uint32_t)(pix % ow);
-  const uint64_t t2 = pix / ow;
-  const uint32_t oy = (uint32_t)(t2 % oh);
-  const uint32_t img = (uint32_t)(t2 / oh);
+  const uint32_t pix = fdiv(i, fd_cg);
+  const uint32_t g = i - pix * cg_out;
+  const uint32_t t2 = fdiv(pix, fd_ow);
+  const uint32_t ox = pix - t2 * ow;
+  const uint32_t img = fdiv(t2, fd_oh);
+  const uint32_t oy = t2 - img * oh;
   // the output vec4 lies in one part (all parts but the last hold a multiple of 4 channels)
   uint32_t p = 0;
   while (p + 1 < parts.n && g * 4 >= parts.v[p + 1].out_c0) ++p;
@@ -72,8 +73,9 @@ __global__ __launch_bounds__(256) void resize_kernel(Parts parts, uint32_t n, ui
   resize_coord(oy, (float)ih / (float)oh, mode, ih, y0, y1, ty);
   resize_coord(ox, (float)iw / (float)ow, mode, iw, x0, x1, tx);
   const uint32_t cgi = pa.stride_c / 4;
+  const size_t ibase = (size_t)img * ih * iw;
   auto at = [&](uint32_t yy, uint32_t xx) {
-    return Vec4IO<DT>::load(pa.p, (((size_t)img * ih + yy) * iw + xx) * cgi + (pa.c_off + k0) / 4);
+    return Vec4IO<DT>::load(pa.p, (ibase + yy * iw + xx) * cgi + (pa.c_off + k0) / 4);
   };
   const f32x4 top = at(y0, x0) * (1.0f - tx) + at(y0, x1) * tx;
   const f32x4 bot = at(y1, x0) * (1.0f - tx) + at(y1, x1) * tx;
@@ -112,15 +114,16 @@ __device__ __forceinline__ float bin_apply(int op, float a, float b) {
 }
 
 template <int DT>
-__global__ __launch_bounds__(256) void binary_kernel(const void *a, const void *b, void *y, uint32_t n, uint32_t hw,
-                                                     uint32_t c, int op, int act, int operand, float scalar,
-                                                     int scalar_first, uint32_t b_c) {
+__global__ __launch_bounds__(256) void binary_kernel(const void *a, const void *b, void *y, uint32_t total,
+                                                     uint32_t hw, uint32_t c, int op, int act, int operand,
+                                                     float scalar, int scalar_first, uint32_t b_c, FastDiv fd_cg,
+                                                     FastDiv fd_hw) {
   const uint32_t cg = (c + 3) / 4;
-  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (uint64_t)n * hw * cg) return;
-  const uint32_t g = (uint32_t)(i % cg);
-  const uint64_t pix = i / cg;  // image-major pixel index
-  const uint32_t img = (uint32_t)(pix / hw);
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const uint32_t pix = fdiv(i, fd_cg);  // image-major pixel index
+  const uint32_t g = i - pix * cg;
+  const uint32_t img = fdiv(pix, fd_hw);
   const f32x4 va = Vec4IO<DT>::load(a, i);
   f32x4 vb;
   switch (operand) {
@@ -140,8 +143,8 @@ __global__ __launch_bounds__(256) void binary_kernel(const void *a, const void *
     case AIH_OPND_PVEC_TENSOR: {
       // one value per pixel: a pixel grid with one channel, or a 1x1 vector
       // of hw channels (ai-cpu model.rs:494-500)
-      const uint64_t p = pix - (uint64_t)img * hw;
-      const float s = b_c == 1 ? ld1<DT>(b, pix * 4) : ld1<DT>(b, (size_t)img * ((b_c + 3) / 4) * 4 + p);
+      const uint32_t p = pix - img * hw;
+      const float s = b_c == 1 ? ld1<DT>(b, (size_t)pix * 4) : ld1<DT>(b, (size_t)img * ((b_c + 3) / 4) * 4 + p);
       vb = f32x4{s, s, s, s};
       break;
     }
@@ -166,13 +169,29 @@ __global__ __launch_bounds__(256) void binary_kernel(const void *a, const void *
 // ---------------------------------------------------------------- concat
 
 // Any channel counts: every output lane finds its part; padding lanes are 0.
-template <int DT>
-__global__ __launch_bounds__(256) void concat_kernel(Parts parts, uint64_t px, uint32_t c_out, void *y) {
+// When every part but the last holds a multiple of 4 channels (VEC), each
+// output vec4 lies in one part and is one vector copy (padding lanes of the
+// last part's vec4 are zeroed).
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void concat_kernel(Parts parts, uint32_t total, uint32_t c_out, FastDiv fd_cg,
+                                                     void *y) {
   const uint32_t cg = (c_out + 3) / 4;
-  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= px * cg) return;
-  const uint32_t g = (uint32_t)(i % cg);
-  const uint64_t pix = i / cg;
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const uint32_t pix = fdiv(i, fd_cg);
+  const uint32_t g = i - pix * cg;
+  if constexpr (VEC) {
+    uint32_t p = 0;
+    while (p + 1 < parts.n && g * 4 >= parts.v[p + 1].out_c0) ++p;
+    const PartArg &pa = parts.v[p];
+    const uint32_t k0 = g * 4 - pa.out_c0;
+    f32x4 v = Vec4IO<DT>::load(pa.p, ((size_t)pix * pa.stride_c + pa.c_off + k0) / 4);
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+      if (k0 + l >= pa.c) v[l] = 0.0f;
+    Vec4IO<DT>::store(y, i, v);
+    return;
+  }
   f32x4 v = {};
 #pragma unroll
   for (int l = 0; l < 4; ++l) {
@@ -181,7 +200,7 @@ __global__ __launch_bounds__(256) void concat_kernel(Parts parts, uint64_t px, u
     uint32_t p = 0;
     while (p + 1 < parts.n && ch >= parts.v[p + 1].out_c0) ++p;
     const PartArg &pa = parts.v[p];
-    v[l] = ld1<DT>(pa.p, pix * pa.stride_c + pa.c_off + (ch - pa.out_c0));
+    v[l] = ld1<DT>(pa.p, (size_t)pix * pa.stride_c + pa.c_off + (ch - pa.out_c0));
   }
   Vec4IO<DT>::store(y, i, v);
 }
@@ -229,6 +248,15 @@ using namespace aih;
     }                                                                                      \
   } while (0)
 
+#define AIH_LAUNCH_DT2(KERNEL, B, dt, grid, st, ...)                                                  \
+  do {                                                                                               \
+    switch (dt) {                                                                                    \
+      case AIH_F32: hipLaunchKernelGGL((KERNEL<DT_F32, B>), grid, dim3(256), 0, st, __VA_ARGS__); break;  \
+      case AIH_F16: hipLaunchKernelGGL((KERNEL<DT_F16, B>), grid, dim3(256), 0, st, __VA_ARGS__); break;  \
+      default: hipLaunchKernelGGL((KERNEL<DT_BF16, B>), grid, dim3(256), 0, st, __VA_ARGS__); break;      \
+    }                                                                                                \
+  } while (0)
+
 extern "C" {
 
 int aih_resize(const aih_resize_desc *d, const void *const *inputs, void *y, aih_stream stream) {
@@ -243,10 +271,10 @@ int aih_resize(const aih_resize_desc *d, const void *const *inputs, void *y, aih
     if (fill_parts(d->srcs, d->nsrcs, inputs, d->dt, true, &parts, &c)) return AIH_ERR;
     const uint32_t cg = (c + 3) / 4;
     const uint64_t total = (uint64_t)d->n * d->oh * d->ow * cg;
-    if (total == 0 || total > 0xffffffffull * 256) return api_fail("resize: output too large");
+    if (total == 0 || total > 0xffffff00ull) return api_fail("resize: output too large");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    AIH_LAUNCH_DT(resize_kernel, d->dt, grid_for(total), st, parts, d->n, d->ih, d->iw, d->oh, d->ow, (int)d->mode,
-                  cg, y);
+    AIH_LAUNCH_DT(resize_kernel, d->dt, grid_for(total), st, parts, (uint32_t)total, d->ih, d->iw, d->oh, d->ow,
+                  (int)d->mode, cg, make_fastdiv(cg), make_fastdiv(d->ow), make_fastdiv(d->oh), y);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? AIH_OK : api_fail(std::string("resize launch: ") + hipGetErrorString(e));
   });
@@ -290,10 +318,11 @@ int aih_binary(const aih_binary_desc *d, const void *a, const void *b, void *y, 
     if (d->operand != AIH_OPND_SCALAR && (!b || !aligned(b, tensor_b ? vb / 4 : vb)))
       return api_fail("binary: null or misaligned b");
     const uint64_t total = (uint64_t)d->n * d->h * d->w * ((d->c + 3) / 4);
-    if (total > 0xffffffffull * 256) return api_fail("binary: too large");
+    if (total > 0xffffff00ull) return api_fail("binary: too large");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    AIH_LAUNCH_DT(binary_kernel, d->dt, grid_for(total), st, a, b, y, d->n, d->h * d->w, d->c, (int)d->op,
-                  (int)d->act, (int)d->operand, d->scalar, (int)d->scalar_first, d->b_c);
+    AIH_LAUNCH_DT(binary_kernel, d->dt, grid_for(total), st, a, b, y, (uint32_t)total, d->h * d->w, d->c,
+                  (int)d->op, (int)d->act, (int)d->operand, d->scalar, (int)d->scalar_first, d->b_c,
+                  make_fastdiv((d->c + 3) / 4), make_fastdiv(d->h * d->w));
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? AIH_OK : api_fail(std::string("binary launch: ") + hipGetErrorString(e));
   });
@@ -310,9 +339,15 @@ int aih_concat(const aih_concat_desc *d, const void *const *inputs, void *y, aih
     if (fill_parts(d->parts, d->nparts, inputs, d->dt, false, &parts, &c)) return AIH_ERR;
     const uint64_t px = (uint64_t)d->n * d->h * d->w;
     const uint64_t total = px * ((c + 3) / 4);
-    if (total > 0xffffffffull * 256) return api_fail("concat: too large");
+    if (total > 0xffffff00ull) return api_fail("concat: too large");
+    bool vec = true;
+    for (uint32_t i = 0; i + 1 < d->nparts; ++i) vec = vec && d->parts[i].c % 4 == 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    AIH_LAUNCH_DT(concat_kernel, d->dt, grid_for(total), st, parts, px, c, y);
+    const FastDiv fd = make_fastdiv((c + 3) / 4);
+    if (vec)
+      AIH_LAUNCH_DT2(concat_kernel, true, d->dt, grid_for(total), st, parts, (uint32_t)total, c, fd, y);
+    else
+      AIH_LAUNCH_DT2(concat_kernel, false, d->dt, grid_for(total), st, parts, (uint32_t)total, c, fd, y);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? AIH_OK : api_fail(std::string("concat launch: ") + hipGetErrorString(e));
   });

@@ -228,6 +228,8 @@ def kernel_key(conv, op, n, dt, dtname) -> str:
     Lr = op.layers[0]
     if Lr.depthwise:
         return f"conv_dw_strip_kernel<{dtname}>"
+    if Lr.k == 1 and -(-Lr.cout // 4) == 1:
+        return f"pw_narrow_kernel<{dtname}>"
     if Lr.k == 1:
         p = conv.GemmPwSpec(m=Lr.ih * Lr.iw, kg=-(-Lr.cin // 4), ng=-(-Lr.cout // 4), dt=dt, n=n).plan()
     else:

@@ -170,7 +170,10 @@ typedef struct {
 
 /* Buffer order follows GemmPwSpec::bindings (gemm_pw.rs:276-283): IN, W, BIAS,
  * [RES], OUT. res must be NULL iff residual == 0. ws may be NULL when the plan
- * needs no workspace; otherwise ws_bytes >= aih_plan.ws_bytes. */
+ * needs no workspace; otherwise ws_bytes >= aih_plan.ws_bytes. With ng == 1
+ * (at most 4 output channels), AIH_VAR_AUTO and splitk == 0 the call runs a
+ * VALU kernel (one pixel per thread, the reference's Gemv role) instead of
+ * the planned MFMA tile, and needs no workspace. */
 int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *bias,
                 const void *res, void *y, void *ws, size_t ws_bytes, aih_stream stream);
 int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out);

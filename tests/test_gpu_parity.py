@@ -99,6 +99,27 @@ def test_pw_f32_act_16bit_weights(wdt):
     assert G.rel_err(res.got, res.want_r) <= 1e-4  # activations stay fp32: only the weights were rounded
 
 
+# at most 4 output channels (the segmentation heads 24 -> 2 and 128 -> 2):
+# the one-pixel-per-thread kernel
+PW_NARROW = [((80, 144, 24, 2), "none", False, 3401), ((10, 18, 128, 2), "sigmoid", False, 3402),
+             ((9, 16, 960, 4), "relu", True, 3403), ((5, 7, 6, 1), "hardswish", True, 3404),
+             ((13, 11, 44, 3), "relu6", False, 3405)]
+
+
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("case", PW_NARROW, ids=str)
+def test_pw_narrow_cout(case, dt):
+    (h, w, cin, cout), act, with_res, seed = case
+    res = G.run_pw(h, w, cin, cout, act, with_res, dt, seed, n=2)
+    check(f"pw narrow dt{dt} {case}", res, dt)
+
+
+def test_pw_narrow_f32_act_16bit_weights():
+    res = G.run_pw(10, 18, 128, 2, "none", True, F32, 3410, wdt=F16)
+    check("pw narrow f32/wf16", res, F16)
+    assert G.rel_err(res.got, res.want_r) <= 1e-4
+
+
 @pytest.mark.parametrize("splitk", [1, 4, 8])
 @pytest.mark.parametrize("n", [1, 3])
 def test_pw_splitk_factors(splitk, n):
