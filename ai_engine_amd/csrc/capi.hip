@@ -19,6 +19,7 @@
 #include "conv_dw.h"
 #include "conv_gemm_launch.h"
 #include "conv_pw_narrow.h"
+#include "conv_stem.h"
 #include "ir_block.h"
 
 std::string &aih::last_error_slot() {
@@ -365,6 +366,38 @@ int aih_conv_igemm(const aih_igemm_desc *d, const void *const *inputs, const voi
       return fail("igemm: misaligned buffer (w, y, res need 16 bytes, bias 8)");
     uint32_t oh, ow;
     if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
+    const bool dense_in = d->nsrcs == 0 || (d->nsrcs == 1 && d->srcs[0].c_off == 0 && d->srcs[0].stride_c == 4);
+    if (d->k == 3 && d->d == 1 && d->cin <= 3 && dense_in && d->cout % 32 == 0 && d->cout <= 64 &&
+        d->variant == AIH_VAR_AUTO && d->splitk == 0 && d->dt == d->wdt) {
+      // the stem: <= 3 input channels, every (tap, channel) gathered into one
+      // 32-deep MFMA operand
+      const uint64_t M = (uint64_t)d->n * oh * ow;
+      if (M > 0xffffff00ull) return fail("igemm: too many output pixels");
+      aih::StemArgs sa;
+      std::memset(&sa, 0, sizeof(sa));
+      sa.x = inputs[0];
+      sa.w = w;
+      sa.bias = bias;
+      sa.res = res;
+      sa.y = y;
+      sa.IH = d->ih;
+      sa.IW = d->iw;
+      sa.OHW = oh * ow;
+      sa.OW = ow;
+      sa.S = d->s;
+      sa.PT = (int32_t)d->pad[0];
+      sa.PL = (int32_t)d->pad[1];
+      sa.CO = d->cout;
+      sa.KGP = 4;
+      sa.M = (uint32_t)M;
+      sa.nblocks = (uint32_t)((M + 31) / 32);
+      sa.act = d->act;
+      sa.has_res = d->residual ? 1 : 0;
+      sa.fd_ohw = aih::make_fastdiv(oh * ow);
+      sa.fd_ow = aih::make_fastdiv(ow);
+      const hipError_t e = aih::launch_conv_stem(sa, d->dt, static_cast<hipStream_t>(stream));
+      return e == hipSuccess ? AIH_OK : fail(std::string("conv stem launch: ") + hipGetErrorString(e));
+    }
     GemmPlan g;
     if (plan_igemm(d, &g)) return AIH_ERR;
     aih::GemmArgs a;

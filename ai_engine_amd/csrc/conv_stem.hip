@@ -1,0 +1,178 @@
+// conv_stem.hip -- 3x3 conv over an image with at most 3 channels (the stem:
+// 3 -> 32, stride 2, of the segmentation encoders).
+//
+// The generic implicit GEMM walks K in (tap, 4-channel group) units: with one
+// group per tap its K of 9 groups is padded to two 32-channel stages and every
+// A load is half a vector. The ai-cpu path gives this layer its own route for
+// the same reason (im2row then a 1x1 GEMM, crates/ai-cpu/src/kernels/im2row.rs:22-104,
+// K order (ky, kx, ic)). Here the 27 (tap, channel) values of an output pixel
+// are gathered straight into the MFMA B operand -- K = tap*3 + ic, padded to
+// 32 -- so one 32-pixel x 32-channel block is 2 MFMAs (f16 / bf16, K 16 each)
+// or 16 MFMAs (fp32, K 2 each). A wavefront owns 32 output pixels at a time
+// (grid-stride over the blocks); the 9 input pixels of a lane are 9 vector
+// loads of its image row neighbourhood (cached); the weights sit in registers
+// for the whole launch. The epilogue is act(acc + bias) (+ residual) in the
+// MFMA layout, stored as one vector of 4 channels per lane and group.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "aih_device.h"
+#include "conv_stem.h"
+
+namespace aih {
+namespace {
+
+// channel c (0..2) of a packed 4-channel 16-bit vector
+__device__ __forceinline__ uint32_t h16(u32x2 v, int c) {
+  return c == 0 ? (v.x & 0xffffu) : (c == 1 ? (v.x >> 16) : (v.y & 0xffffu));
+}
+__device__ __forceinline__ uint32_t pk(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
+
+template <int DT, int NOB>
+__global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
+  constexpr bool F32 = DT == DT_F32;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, lh = lane >> 5;
+  const uint32_t NG = a.CO / 4;
+
+  // ---- weights of output channel row ob*32 + l32, in K order tap*3 + ic ----
+  // packed element (tap, kg 0, n = o, comp = ic) at ((tap*KGP)*NG + o/4)*16 + (o%4)*4 + ic (pack.rs:95)
+  auto wval = [&](uint32_t o, int k) -> uint32_t {  // raw storage bits, 0 for the K padding
+    if (k >= 27) return 0u;
+    const int tap = k / 3, ic = k % 3;
+    const size_t idx = ((size_t)tap * a.KGP * NG + o / 4) * 16 + (o % 4) * 4 + ic;
+    if constexpr (F32) return reinterpret_cast<const uint32_t *>(a.w)[idx];
+    else return reinterpret_cast<const uint16_t *>(a.w)[idx];
+  };
+  // 16-bit: A[ob][s] holds K = s*16 + lh*8 + j; fp32: Af[ob][s] holds K = 2s + lh
+  u32x4 A[NOB][2];
+  float Af[F32 ? NOB : 1][16];
+#pragma unroll
+  for (int ob = 0; ob < NOB; ++ob) {
+    const uint32_t o = ob * 32 + l32;
+    if constexpr (F32) {
+#pragma unroll
+      for (int s = 0; s < 16; ++s) Af[ob][s] = __uint_as_float(wval(o, 2 * s + lh));
+    } else {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int k0 = s * 16 + lh * 8;
+        A[ob][s] = u32x4{pk(wval(o, k0), wval(o, k0 + 1)), pk(wval(o, k0 + 2), wval(o, k0 + 3)),
+                         pk(wval(o, k0 + 4), wval(o, k0 + 5)), pk(wval(o, k0 + 6), wval(o, k0 + 7))};
+      }
+    }
+  }
+  // bias of the lane's 16 channels per output block: groups 8q + 4lh
+  f32x4 bias[NOB][4];
+#pragma unroll
+  for (int ob = 0; ob < NOB; ++ob)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bias[ob][q] = Vec4IO<DT>::load(a.bias, (ob * 32 + 8 * q + 4 * lh) / 4);
+  const Act actp = act_params(a.act);
+
+  const uint32_t waves = gridDim.x * 4;
+  for (uint32_t blk = blockIdx.x * 4 + (threadIdx.x >> 6); blk < a.nblocks; blk += waves) {
+    const uint32_t p = blk * 32 + l32;
+    const bool valid = p < a.M;
+    const uint32_t pp = valid ? p : 0;
+    const uint32_t img = fdiv(pp, a.fd_ohw);
+    const uint32_t rem = pp - img * a.OHW;
+    const uint32_t oy = fdiv(rem, a.fd_ow);
+    const uint32_t ox = rem - oy * a.OW;
+    const int32_t iy0 = (int32_t)(oy * a.S) - a.PT, ix0 = (int32_t)(ox * a.S) - a.PL;
+    const size_t ibase = (size_t)img * a.IH * a.IW;
+    // the 9 input pixels (4 channels each, the 4th is the C4 padding)
+    u32x2 th[F32 ? 1 : 9];
+    f32x4 tf[F32 ? 9 : 1];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+      const int32_t iy = iy0 + t / 3, ix = ix0 + t % 3;
+      const bool in = valid && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
+      const size_t vi = ibase + (size_t)(in ? iy : 0) * a.IW + (in ? ix : 0);
+      if constexpr (F32) {
+        tf[t] = in ? reinterpret_cast<const f32x4 *>(a.x)[vi] : f32x4{};
+      } else {
+        th[t] = in ? reinterpret_cast<const u32x2 *>(a.x)[vi] : u32x2{0u, 0u};
+      }
+    }
+    f32x16 acc[NOB];
+#pragma unroll
+    for (int ob = 0; ob < NOB; ++ob) acc[ob] = f32x16{};
+    if constexpr (F32) {
+      // lane half lh feeds K = 2s + lh: even K for lh = 0, odd for lh = 1
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const int k = 2 * s + lh;  // lh is 0 or 1: both candidates are compile-time indices
+        const int ke = 2 * s, ko = 2 * s + 1;
+        const float ve = ke < 27 ? tf[ke / 3][ke % 3] : 0.0f;
+        const float vo = ko < 27 ? tf[ko / 3][ko % 3] : 0.0f;
+        const float b = (k & 1) ? vo : ve;
+#pragma unroll
+        for (int ob = 0; ob < NOB; ++ob) acc[ob] = __builtin_amdgcn_mfma_f32_32x32x2f32(Af[ob][s], b, acc[ob], 0, 0, 0);
+      }
+    } else {
+      // K = s*16 + lh*8 + j: lane half 0 / 1 of step 0 and 1 (taps 0-2 / 2-5 / 5-7 / 8)
+      auto v = [&](int k) -> uint32_t { return k < 27 ? h16(th[k / 3], k % 3) : 0u; };
+      const u32x4 b0l = u32x4{pk(v(0), v(1)), pk(v(2), v(3)), pk(v(4), v(5)), pk(v(6), v(7))};
+      const u32x4 b0h = u32x4{pk(v(8), v(9)), pk(v(10), v(11)), pk(v(12), v(13)), pk(v(14), v(15))};
+      const u32x4 b1l = u32x4{pk(v(16), v(17)), pk(v(18), v(19)), pk(v(20), v(21)), pk(v(22), v(23))};
+      const u32x4 b1h = u32x4{pk(v(24), v(25)), pk(v(26), 0u), 0u, 0u};
+      const u32x4 b0 = lh ? b0h : b0l, b1 = lh ? b1h : b1l;
+#pragma unroll
+      for (int ob = 0; ob < NOB; ++ob) {
+        if constexpr (DT == DT_F16) {
+          acc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, A[ob][0]),
+                                                          __builtin_bit_cast(f16x8, b0), acc[ob], 0, 0, 0);
+          acc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, A[ob][1]),
+                                                          __builtin_bit_cast(f16x8, b1), acc[ob], 0, 0, 0);
+        } else {
+          acc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, A[ob][0]),
+                                                           __builtin_bit_cast(bf16x8, b0), acc[ob], 0, 0, 0);
+          acc[ob] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, A[ob][1]),
+                                                           __builtin_bit_cast(bf16x8, b1), acc[ob], 0, 0, 0);
+        }
+      }
+    }
+    if (!valid) continue;
+    // lane: pixel p, channels ob*32 + 8q + 4lh + (0..3) in acc[ob][4q..4q+3]
+#pragma unroll
+    for (int ob = 0; ob < NOB; ++ob)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4 o = f32x4{acc[ob][4 * q], acc[ob][4 * q + 1], acc[ob][4 * q + 2], acc[ob][4 * q + 3]} + bias[ob][q];
+        o = act4(actp, o);
+        const size_t vi = (size_t)p * NG + (ob * 32 + 8 * q + 4 * lh) / 4;
+        if (a.has_res) o += Vec4IO<DT>::load(a.res, vi);
+        Vec4IO<DT>::store(a.y, vi, o);
+      }
+  }
+}
+
+template <int DT, int NOB>
+hipError_t launch_inst(const StemArgs &a, hipStream_t st) {
+  const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblocks + 3) / 4, 256u * 8u);
+  hipLaunchKernelGGL((conv_stem_kernel<DT, NOB>), dim3(wgs), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_dt(const StemArgs &a, hipStream_t st) {
+  switch (a.CO / 32) {
+    case 1: return launch_inst<DT, 1>(a, st);
+    case 2: return launch_inst<DT, 2>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_conv_stem(const StemArgs &a, int dt, hipStream_t st) {
+  switch (dt) {
+    case DT_F32: return launch_dt<DT_F32>(a, st);
+    case DT_F16: return launch_dt<DT_F16>(a, st);
+    case DT_BF16: return launch_dt<DT_BF16>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace aih

@@ -317,11 +317,13 @@ def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
     fl, by = W.totals(layers, meta["n"], 4, 4)
     row = roof(fl, by, t, "f32")
     row["launches"] = len(m4.ops)
+    row["block_choices"] = {k: {"choice": v[0], "us": round(v[1], 2)} for k, v in m4.choices.items()}
     row["per_layer_roofline_sum_us"] = sum(
         max(L.flops(meta["n"]) / (PEAK_TF["f32"] * 1e12), L.bytes(meta["n"], 4, 4) / (HBM_GBS * 1e9))
         for L in layers) * 1e6
     res["ir_block_chain_4x_64c_40x72_b64"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
-    log(f"ir chain: {row['us']:.1f} us frac {row['frac']:.3f}")
+    log(f"ir chain: {row['us']:.1f} us frac {row['frac']:.3f}; blocks: " +
+        ", ".join(f"{k} {v[0]} ({v[1]:.0f} us)" for k, v in m4.choices.items()))
     del m4
     return res
 

@@ -179,7 +179,11 @@ int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *
 int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out);
 
 /* inputs holds max(1, nsrcs) device pointers: the plain input, or one per part
- * (the IN0..IN2 bindings of conv_igemm.rs:141-171). */
+ * (the IN0..IN2 bindings of conv_igemm.rs:141-171). A dense 3x3 conv (d = 1)
+ * over at most 3 input channels with cout 32 or 64, AIH_VAR_AUTO, splitk 0 and
+ * dt == wdt -- the stem -- runs a dedicated kernel (all 27 tap-channel values
+ * in one MFMA operand) instead of the planned implicit GEMM; it needs no
+ * workspace. */
 int aih_conv_igemm(const aih_igemm_desc *d, const void *const *inputs, const void *w,
                    const void *bias, const void *res, void *y, void *ws, size_t ws_bytes,
                    aih_stream stream);

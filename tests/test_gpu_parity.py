@@ -252,3 +252,22 @@ def test_igemm_splitk(splitk):
 def test_igemm_batch():
     res = G.run_igemm(20, 36, 16, 32, 3, 2, [1] * 4, "relu", True, F32, 7401, n=3)
     check("igemm batch", res, F32)
+
+
+# ---------------------------------------------------------------- the stem (3x3 over <= 3 channels)
+
+STEM = [((160, 288, 3, 32, 2, (1, 1, 1, 1)), "relu", False, 3601, 2),
+        ((33, 17, 3, 64, 1, (0, 1, 2, 1)), "hardswish", True, 3602, 1),
+        ((16, 16, 1, 32, 2, (0, 0, 1, 1)), "none", False, 3603, 3),
+        ((9, 9, 2, 32, 1, (1, 1, 1, 1)), "sigmoid", True, 3604, 2),
+        ((7, 40, 3, 64, 2, (1, 1, 1, 1)), "relu6", False, 3605, 1)]
+
+
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("case", STEM, ids=str)
+def test_stem_kernel(case, dt):
+    """dense 3x3, d = 1, <= 3 input channels, cout 32 / 64: the stem route of
+    aih_conv_igemm (every tap-channel value in one MFMA operand)."""
+    (ih, iw, cin, cout, s, pad), act, with_res, seed, n = case
+    res = G.run_igemm(ih, iw, cin, cout, 3, s, pad, act, with_res, dt, seed, n=n)
+    check(f"stem dt{dt} {case}", res, dt)
