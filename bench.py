@@ -133,8 +133,10 @@ def main() -> int:
         t = sorted(evs[r][i][0].elapsed_time(evs[r][i][1]) for r in range(R))[R // 2] / 1e3
         fl, by = op.flops(n), op.bytes(n, act_b, act_b)
         key = kernel_key(conv, op, n, DT[args.dtype], args.dtype)
-        g = groups.setdefault(key, dict(launches=0, secs=0.0, flops=0, bytes=0))
+        g = groups.setdefault(key, dict(launches=0, secs=0.0, flops=0, bytes=0, grids=[]))
         g["launches"] += 1
+        if op.kind == "ir_block":
+            g["grids"].append(op.spec.plan().grid * 256)  # dispatch size in threads, as rocprofv3 lists it
         g["secs"] += t
         g["flops"] += fl
         g["bytes"] += by
@@ -151,7 +153,7 @@ def main() -> int:
         roofline = dict(bound="mfma", achieved=round(dr["tflops"], 2), peak=PEAK_TF[args.dtype], unit="TFLOP/s",
                         frac=round(dr["tflops"] / PEAK_TF[args.dtype], 4), traffic=None)
     roofline["traffic"] = measured_traffic(dom_key)
-    roofline.update(kernel=dom_key, launches_per_step=dom["launches"],
+    roofline.update(kernel=dom_key, launches_per_step=dom["launches"], dispatch_threads=sorted(dom["grids"]),
                     avg_launch_us=round(dom["secs"] / dom["launches"] * 1e6, 2),
                     algorithmic_bytes_per_launch=int(dom["bytes"] / dom["launches"]),
                     algorithmic_flops_per_launch=int(dom["flops"] / dom["launches"]),
