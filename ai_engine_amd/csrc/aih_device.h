@@ -168,12 +168,20 @@ struct Act {
   int hib;  // bits of hi
   int mode;
   int act;
+  int lob;  // clamp-type activations: lower bound bits (INT_MIN for the identity, 0 otherwise)
 };
 enum : int { ACT_LINEAR = 0, ACT_CLAMP = 1, ACT_XCLAMP = 2, ACT_SPECIAL = 3, ACT_IDENT = 4, ACT_RELU = 5,
              ACT_CLAMP0 = 6 };
 
+// Activations that are a clamp of the float bits as signed integers to
+// [lob, hib]: the identity, ReLU, ReLU6 and clamp01 (non-negative floats order
+// like their bits; negative floats are negative integers).
+__host__ __device__ __forceinline__ bool act_is_clamp(int act) {
+  return act == AIH_ACT_NONE || act == AIH_ACT_RELU || act == AIH_ACT_RELU6 || act == AIH_ACT_CLAMP01;
+}
+
 __device__ __forceinline__ Act act_params(int act) {
-  Act p{1.0f, -0.0f, 0.0f, 0, ACT_LINEAR, act};
+  Act p{1.0f, -0.0f, 0.0f, 0, ACT_LINEAR, act, 0};
   switch (act) {
     case AIH_ACT_NONE: p.mode = ACT_IDENT; break;
     case AIH_ACT_NEG: p.s = -1.0f; break;
@@ -189,7 +197,18 @@ __device__ __forceinline__ Act act_params(int act) {
     default: p.mode = ACT_SPECIAL; break;
   }
   p.hib = __float_as_int(p.hi);
+  if (p.mode == ACT_IDENT) {
+    p.lob = (int)0x80000000;
+    p.hib = 0x7fffffff;
+  } else if (p.mode == ACT_RELU) {
+    p.hib = 0x7fffffff;
+  }
   return p;
+}
+
+// A clamp-type activation (act_is_clamp) without a branch: one v_med3_i32.
+__device__ __forceinline__ float act_clamp_any(const Act &p, float x) {
+  return __int_as_float(min(max(__float_as_int(x), p.lob), p.hib));
 }
 
 __device__ __forceinline__ float act_relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }

@@ -267,9 +267,13 @@ int check_ir(const aih_ir_block_desc *d, uint32_t *oh, uint32_t *ow) {
   return AIH_OK;
 }
 
+bool ir_clamp_acts(const aih_ir_block_desc *d) {
+  return aih::act_is_clamp(d->act_expand) && aih::act_is_clamp(d->act_dw) && aih::act_is_clamp(d->act_project);
+}
+
 int plan_ir(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, aih::IrPlan *p) {
-  const char *why = aih::ir_plan(d->n, d->ih, d->iw, oh, ow, d->cin, d->cexp, d->cout, d->s, d->dt, d->tile_h,
-                                 d->tile_w, d->ec, p);
+  const char *why = aih::ir_plan(d->n, d->ih, d->iw, oh, ow, d->cin, d->cexp, d->cout, d->s, d->dt,
+                                 ir_clamp_acts(d), d->tile_h, d->tile_w, d->ec, p);
   if (why) return fail(std::string("ir_block: ") + why);
   return AIH_OK;
 }
@@ -564,6 +568,7 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
     // the expand's activation, not act(0))
     a.mask_e = (d->act_expand == AIH_ACT_SIGMOID || d->act_expand == AIH_ACT_HARDSIGMOID ||
                 d->act_expand == AIH_ACT_RECIP) ? 1 : 0;
+    a.clamp_acts = ir_clamp_acts(d) ? 1 : 0;
     a.lds_x = p.lds_x;
     a.lds_xe = p.lds_xe;
     a.lds_we = p.lds_we;

@@ -32,18 +32,18 @@ int cus_of_current_device() {
 }
 
 // Workgroups per CU allowed by registers alone, per instantiation (queried once).
-int reg_occupancy(int dt, uint32_t nob, uint32_t npw) {
+int reg_occupancy(int dt, uint32_t nob, uint32_t npw, bool cl) {
   static std::mutex mu;
-  static std::map<std::tuple<int, uint32_t, uint32_t>, int> cache;
+  static std::map<std::tuple<int, uint32_t, uint32_t, bool>, int> cache;
   std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_tuple(dt, nob, npw);
+  const auto key = std::make_tuple(dt, nob, npw, cl);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int occ = 0;
   switch (dt) {
-    case DT_F32: occ = ir_occ_f32(nob, npw, 0); break;
-    case DT_F16: occ = ir_occ_f16(nob, npw, 0); break;
-    case DT_BF16: occ = ir_occ_bf16(nob, npw, 0); break;
+    case DT_F32: occ = ir_occ_f32(nob, npw, cl, 0); break;
+    case DT_F16: occ = ir_occ_f16(nob, npw, cl, 0); break;
+    case DT_BF16: occ = ir_occ_bf16(nob, npw, cl, 0); break;
     default: break;
   }
   // Without a device the runtime cannot answer; plan for one workgroup per CU.
@@ -87,7 +87,7 @@ constexpr uint32_t kMaxLds = 160 * 1024;
 // number of tile rounds the grid needs. The cheapest candidate that fits in
 // LDS wins; candidates with a single workgroup per CU pay a latency penalty.
 const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
-                    uint32_t CO, uint32_t S, int dt, uint32_t tile_h, uint32_t tile_w, uint32_t ec_force,
+                    uint32_t CO, uint32_t S, int dt, bool cl, uint32_t tile_h, uint32_t tile_w, uint32_t ec_force,
                     IrPlan *out) {
   if (dt != DT_F32 && dt != DT_F16 && dt != DT_BF16) return "unknown dtype";
   const bool f32 = dt == DT_F32;
@@ -156,7 +156,7 @@ const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t 
         lds_layout(C, CO, resident ? E : 2 * ec, npi, dt, &p);
         if (p.lds > kMaxLds) continue;
         const uint32_t npw = cdiv(npb, 4);
-        const int occ_r = reg_occupancy(dt, nob, npw);
+        const int occ_r = reg_occupancy(dt, nob, npw, cl);
         const int occ = std::min<int>(occ_r, (int)(kMaxLds / p.lds));
         if (occ < 1) continue;
         p.tiles_y = cdiv(OH, thx);

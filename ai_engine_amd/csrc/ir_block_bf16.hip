@@ -7,6 +7,8 @@ hipError_t launch_ir_block_bf16(const IrArgs &a, uint32_t lds, uint32_t grid, hi
   return ir_launch_dt<DT_BF16>(a, lds, grid, st);
 }
 
-int ir_occ_bf16(uint32_t nob, uint32_t npw, uint32_t lds) { return ir_occ_dt<DT_BF16>(nob, npw, lds); }
+int ir_occ_bf16(uint32_t nob, uint32_t npw, bool cl, uint32_t lds) {
+  return ir_occ_dt<DT_BF16>(nob, npw, cl, lds);
+}
 
 }  // namespace aih

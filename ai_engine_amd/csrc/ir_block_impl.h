@@ -161,7 +161,19 @@ __device__ __forceinline__ u32x4 ir_ld_w(const char *p, uint32_t next) {
   }
 }
 
-template <int DT, int NOB, int NPW>
+// Activation of N values: CL (all three activations of the block are
+// clamp-type) applies one integer clamp per value with no branch on the mode.
+template <bool CL, int N>
+__device__ __forceinline__ void ir_act(const Act &p, float (&v)[N]) {
+  if constexpr (CL) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = act_clamp_any(p, v[j]);
+  } else {
+    act_array<N>(p, v);
+  }
+}
+
+template <int DT, int NOB, int NPW, bool CL>
 __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   extern __shared__ __align__(16) char lds[];
   constexpr bool F32 = DT == DT_F32;
@@ -343,7 +355,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
         for (int q = 0; q < 4; ++q) {
           const uint32_t el = 8 * q + 4 * lh;
           float v[4] = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
-          act_array<4>(act_e, v);
+          ir_act<CL, 4>(act_e, v);
           if (mask && !inside) v[0] = v[1] = v[2] = v[3] = 0.0f;
           if constexpr (F32)
             *reinterpret_cast<f32x4 *>(XeL + r * RPE + el * 4) = f32x4{v[0], v[1], v[2], v[3]};
@@ -395,7 +407,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
 #pragma unroll
             for (int t = 0; t < 9; ++t)
               ir_fma_taps<DT, HK>(*reinterpret_cast<const u32x4 *>(XeL + rowo[i][t] + ks * 32), wv[t], d);
-            act_array<HK>(act_d, d);
+            ir_act<CL, HK>(act_d, d);
             bop[i] = ir_pack<DT, HK>(d);
           }
 #pragma unroll
@@ -429,7 +441,11 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
           const uint32_t oc = o * 32 + 8 * q + 4 * lh;
           f32x4 v = f32x4{acc[i][o][4 * q], acc[i][o][4 * q + 1], acc[i][o][4 * q + 2], acc[i][o][4 * q + 3]} +
                     *reinterpret_cast<const f32x4 *>(BpL + oc);
-          v = act4(act_p, v);
+          {
+            float t[4] = {v.x, v.y, v.z, v.w};
+            ir_act<CL, 4>(act_p, t);
+            v = f32x4{t[0], t[1], t[2], t[3]};
+          }
           const size_t vi = pix * (a.CO / 4) + oc / 4;
           if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
           Vec4IO<DT>::store(a.y, vi, v);
@@ -440,70 +456,82 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
 }
 
 // The kernel may use up to the device's whole LDS (160 KB on gfx950).
-template <int DT, int NOB, int NPW>
+template <int DT, int NOB, int NPW, bool CL>
 inline hipError_t ir_prepare_inst() {
-  static const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(ir_block_kernel<DT, NOB, NPW>),
+  static const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(ir_block_kernel<DT, NOB, NPW, CL>),
                                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   return e;
 }
 
-template <int DT, int NOB, int NPW>
+template <int DT, int NOB, int NPW, bool CL>
 inline hipError_t ir_launch_inst(const IrArgs &a, uint32_t lds, uint32_t grid, hipStream_t st) {
-  hipError_t e = ir_prepare_inst<DT, NOB, NPW>();
+  hipError_t e = ir_prepare_inst<DT, NOB, NPW, CL>();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((ir_block_kernel<DT, NOB, NPW>), dim3(grid), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((ir_block_kernel<DT, NOB, NPW, CL>), dim3(grid), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
 // Workgroups per CU for this instantiation at `lds` bytes of dynamic LDS
 // (registers and LDS both counted by the runtime).
-template <int DT, int NOB, int NPW>
+template <int DT, int NOB, int NPW, bool CL>
 inline int ir_occ_inst(uint32_t lds) {
-  if (ir_prepare_inst<DT, NOB, NPW>() != hipSuccess) return 0;
+  if (ir_prepare_inst<DT, NOB, NPW, CL>() != hipSuccess) return 0;
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_block_kernel<DT, NOB, NPW>, 256, lds) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_block_kernel<DT, NOB, NPW, CL>, 256, lds) !=
+      hipSuccess)
     return 0;
   return per_cu;
 }
 
-// Dispatch on the projection width (NOB = CO / 32 output-channel blocks) and
-// the output pixel blocks per wavefront (NPW).
-template <int DT>
-inline hipError_t ir_launch_dt(const IrArgs &a, uint32_t lds, uint32_t grid, hipStream_t st) {
+// Dispatch on the projection width (NOB = CO / 32 output-channel blocks), the
+// output pixel blocks per wavefront (NPW) and whether every activation is
+// clamp-type.
+template <int DT, bool CL>
+inline hipError_t ir_launch_cl(const IrArgs &a, uint32_t lds, uint32_t grid, hipStream_t st) {
   const uint32_t nob = a.CO / 32, npw = (a.NPB + 3) / 4;
   switch (nob * 4 + npw) {
-    case 1 * 4 + 1: return ir_launch_inst<DT, 1, 1>(a, lds, grid, st);
-    case 1 * 4 + 2: return ir_launch_inst<DT, 1, 2>(a, lds, grid, st);
-    case 2 * 4 + 1: return ir_launch_inst<DT, 2, 1>(a, lds, grid, st);
-    case 2 * 4 + 2: return ir_launch_inst<DT, 2, 2>(a, lds, grid, st);
-    case 3 * 4 + 1: return ir_launch_inst<DT, 3, 1>(a, lds, grid, st);
-    case 3 * 4 + 2: return ir_launch_inst<DT, 3, 2>(a, lds, grid, st);
-    case 4 * 4 + 1: return ir_launch_inst<DT, 4, 1>(a, lds, grid, st);
-    case 4 * 4 + 2: return ir_launch_inst<DT, 4, 2>(a, lds, grid, st);
+    case 1 * 4 + 1: return ir_launch_inst<DT, 1, 1, CL>(a, lds, grid, st);
+    case 1 * 4 + 2: return ir_launch_inst<DT, 1, 2, CL>(a, lds, grid, st);
+    case 2 * 4 + 1: return ir_launch_inst<DT, 2, 1, CL>(a, lds, grid, st);
+    case 2 * 4 + 2: return ir_launch_inst<DT, 2, 2, CL>(a, lds, grid, st);
+    case 3 * 4 + 1: return ir_launch_inst<DT, 3, 1, CL>(a, lds, grid, st);
+    case 3 * 4 + 2: return ir_launch_inst<DT, 3, 2, CL>(a, lds, grid, st);
+    case 4 * 4 + 1: return ir_launch_inst<DT, 4, 1, CL>(a, lds, grid, st);
+    case 4 * 4 + 2: return ir_launch_inst<DT, 4, 2, CL>(a, lds, grid, st);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <int DT>
-inline int ir_occ_dt(uint32_t nob, uint32_t npw, uint32_t lds) {
+inline hipError_t ir_launch_dt(const IrArgs &a, uint32_t lds, uint32_t grid, hipStream_t st) {
+  return a.clamp_acts ? ir_launch_cl<DT, true>(a, lds, grid, st) : ir_launch_cl<DT, false>(a, lds, grid, st);
+}
+
+template <int DT, bool CL>
+inline int ir_occ_cl(uint32_t nob, uint32_t npw, uint32_t lds) {
   switch (nob * 4 + npw) {
-    case 1 * 4 + 1: return ir_occ_inst<DT, 1, 1>(lds);
-    case 1 * 4 + 2: return ir_occ_inst<DT, 1, 2>(lds);
-    case 2 * 4 + 1: return ir_occ_inst<DT, 2, 1>(lds);
-    case 2 * 4 + 2: return ir_occ_inst<DT, 2, 2>(lds);
-    case 3 * 4 + 1: return ir_occ_inst<DT, 3, 1>(lds);
-    case 3 * 4 + 2: return ir_occ_inst<DT, 3, 2>(lds);
-    case 4 * 4 + 1: return ir_occ_inst<DT, 4, 1>(lds);
-    case 4 * 4 + 2: return ir_occ_inst<DT, 4, 2>(lds);
+    case 1 * 4 + 1: return ir_occ_inst<DT, 1, 1, CL>(lds);
+    case 1 * 4 + 2: return ir_occ_inst<DT, 1, 2, CL>(lds);
+    case 2 * 4 + 1: return ir_occ_inst<DT, 2, 1, CL>(lds);
+    case 2 * 4 + 2: return ir_occ_inst<DT, 2, 2, CL>(lds);
+    case 3 * 4 + 1: return ir_occ_inst<DT, 3, 1, CL>(lds);
+    case 3 * 4 + 2: return ir_occ_inst<DT, 3, 2, CL>(lds);
+    case 4 * 4 + 1: return ir_occ_inst<DT, 4, 1, CL>(lds);
+    case 4 * 4 + 2: return ir_occ_inst<DT, 4, 2, CL>(lds);
     default: return 0;
   }
+}
+
+template <int DT>
+inline int ir_occ_dt(uint32_t nob, uint32_t npw, bool cl, uint32_t lds) {
+  return cl ? ir_occ_cl<DT, true>(nob, npw, lds) : ir_occ_cl<DT, false>(nob, npw, lds);
 }
 
 hipError_t launch_ir_block_f32(const IrArgs &a, uint32_t lds, uint32_t grid, hipStream_t st);
 hipError_t launch_ir_block_f16(const IrArgs &a, uint32_t lds, uint32_t grid, hipStream_t st);
 hipError_t launch_ir_block_bf16(const IrArgs &a, uint32_t lds, uint32_t grid, hipStream_t st);
-int ir_occ_f32(uint32_t nob, uint32_t npw, uint32_t lds);
-int ir_occ_f16(uint32_t nob, uint32_t npw, uint32_t lds);
-int ir_occ_bf16(uint32_t nob, uint32_t npw, uint32_t lds);
+int ir_occ_f32(uint32_t nob, uint32_t npw, bool cl, uint32_t lds);
+int ir_occ_f16(uint32_t nob, uint32_t npw, bool cl, uint32_t lds);
+int ir_occ_bf16(uint32_t nob, uint32_t npw, bool cl, uint32_t lds);
 
 }  // namespace aih

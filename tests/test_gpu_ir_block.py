@@ -31,7 +31,9 @@ from tests import gpu_util as G  # noqa: E402
 F32, F16, BF16 = 0, 1, 2
 BAR_STORED = {F32: 1e-4, F16: 2e-3, BF16: 8e-3}
 
-# (n, ih, iw, cin, cexp, cout, s, pad, residual, act_expand)
+# (n, ih, iw, cin, cexp, cout, s, pad, residual, activations): "e" alone is the
+# expand's activation with a ReLU depthwise and a linear projection; "e/d/p"
+# names all three
 CASES = [
     (2, 12, 20, 32, 128, 32, 1, (1, 1, 1, 1), True, "relu"),
     (2, 13, 21, 32, 128, 64, 2, (1, 1, 1, 1), False, "relu"),
@@ -42,19 +44,26 @@ CASES = [
     (3, 7, 33, 16, 32, 32, 1, (1, 1, 1, 1), True, "relu"),
     (1, 16, 16, 32, 64, 32, 2, (0, 0, 1, 1), False, "relu"),
     (1, 40, 72, 64, 256, 64, 1, (1, 1, 1, 1), True, "relu"),
+    # "expand/dw/project" activations: every one clamp-type (the branch-free
+    # instantiation) with the identity and ReLU6 in it, and a sigmoid expand
+    # (act(0) != 0: the border mask, generic activations)
+    (2, 11, 19, 32, 128, 32, 1, (1, 1, 1, 1), True, "none/relu6/relu"),
+    (2, 12, 20, 32, 128, 64, 2, (1, 1, 1, 1), False, "sigmoid/relu6/none"),
 ]
 
 
 def _id(c):
     n, ih, iw, cin, cexp, cout, s, pad, res, act = c
-    return f"n{n}_{ih}x{iw}_{cin}-{cexp}-{cout}_s{s}_p{''.join(map(str, pad))}{'_res' if res else ''}_{act}"
+    return f"n{n}_{ih}x{iw}_{cin}-{cexp}-{cout}_s{s}_p{''.join(map(str, pad))}{'_res' if res else ''}_{act.replace('/', '-')}"
 
 
 def run_case(case, dt, seed):
-    n, ih, iw, cin, cexp, cout, s, pad, residual, act_e = case
+    n, ih, iw, cin, cexp, cout, s, pad, residual, acts = case
+    parts = acts.split("/")
+    act_e, act_d, act_p = parts if len(parts) == 3 else (parts[0], "relu", "none")
     op_e = orc.conv2d(cin, cexp, act=act_e)
-    op_d = orc.conv2d(cexp, cexp, k=3, s=s, pad=list(pad), groups=cexp, act="relu")
-    op_p = orc.conv2d(cexp, cout, act="none")
+    op_d = orc.conv2d(cexp, cexp, k=3, s=s, pad=list(pad), groups=cexp, act=act_d)
+    op_p = orc.conv2d(cexp, cout, act=act_p)
     oh, ow = orc.out_hw(op_d, ih, iw)
     x = orc.xs32_fill(seed, n * ih * iw * cin)
     we = orc.gauss_fill(seed + 1, 0.0, float(np.sqrt(2.0 / cin)), cexp * cin)
@@ -77,8 +86,8 @@ def run_case(case, dt, seed):
 
     yd = G.poisoned(n * oh * ow * cout, dt)
     spec = conv.IrBlockSpec(ih=ih, iw=iw, cin=cin, cexp=cexp, cout=cout, s=s, pad=pad,
-                            act_expand=G.ACT[act_e], act_dw=conv.Activation.RELU,
-                            act_project=conv.Activation.NONE, residual=residual, dt=conv.DType(dt), n=n)
+                            act_expand=G.ACT[act_e], act_dw=G.ACT[act_d],
+                            act_project=G.ACT[act_p], residual=residual, dt=conv.DType(dt), n=n)
     plan = spec.plan()
     print(f"case {_id(case)} dt{dt}: {plan}", flush=True)
     wep, _ = orc.pack_weights_conv(we, cexp, cin, 1, 1, 4, dt)
