@@ -315,37 +315,30 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
       const char *bes = SmL + s * SMB + 10 * EC * ES;
       for (uint32_t b = wave; b < a.NPI; b += 4) {
         const char *bp = XL + (b * 32 + l32) * RPX + lh * 16;
-        f32x16 acc = {};
-        u32x4 a0 = ir_ld_w<DT>(ap, EC * GB), b0 = *reinterpret_cast<const u32x4 *>(bp);
-        for (uint32_t ks = 0; ks < nks_e; ++ks) {
-          u32x4 a1 = a0, b1 = b0;
-          if (ks + 1 < nks_e) {
-            a1 = ir_ld_w<DT>(ap + (ks + 1) * (KSTEP * EC * ES), EC * GB);
-            b1 = *reinterpret_cast<const u32x4 *>(bp + (ks + 1) * 32);
-          }
-          acc = ir_mma<DT>(a0, b0, acc);
-          a0 = a1;
-          b0 = b1;
-        }
-        // the bias as one more K step: bias of channel l32 (A) x the tile's
+        // the bias as the first K step: bias of channel l32 (A) x the tile's
         // bias column (B), both in the first K slot of lane half 0
+        f32x16 acc;
         {
           const u32x4 bx = *reinterpret_cast<const u32x4 *>(XL + (b * 32 + l32) * RPX + NVX * 16);
           if constexpr (F32) {
             const float bw = lh == 0 ? *reinterpret_cast<const float *>(bes + l32 * 4) : 0.0f;
             const float bo = lh == 0 ? __uint_as_float(bx.x) : 0.0f;
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(bw, bo, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(bw, bo, f32x16{}, 0, 0, 0);
           } else {
             const uint32_t bw = lh == 0 ? (uint32_t)*reinterpret_cast<const uint16_t *>(bes + l32 * 2) : 0u;
-            acc = ir_mma<DT>(u32x4{bw, 0u, 0u, 0u}, lh == 0 ? bx : u32x4{0u, 0u, 0u, 0u}, acc);
+            acc = ir_mma<DT>(u32x4{bw, 0u, 0u, 0u}, lh == 0 ? bx : u32x4{0u, 0u, 0u, 0u}, f32x16{});
           }
         }
+#pragma unroll 2
+        for (uint32_t ks = 0; ks < nks_e; ++ks)
+          acc = ir_mma<DT>(ir_ld_w<DT>(ap + ks * (KSTEP * EC * ES), EC * GB),
+                           *reinterpret_cast<const u32x4 *>(bp + ks * 32), acc);
         const uint32_t r = b * 32 + l32;
         // outside pixels are 0 before the activation; only an activation with
         // act(0) != 0 needs them masked (a wave-uniform test skips blocks
-        // wholly inside)
+        // wholly inside); clamp-type activations all have act(0) = 0
         bool mask = false, inside = true;
-        if (a.mask_e) {
+        if (!CL && a.mask_e) {
           const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
           const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
           inside = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
