@@ -290,8 +290,10 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
     ir_dma_wait();
     __syncthreads();
 
-    // tap row offsets (bytes) of this wavefront's output pixel blocks
-    uint32_t rowo[NPW][9];
+    // LDS byte addresses of the depthwise tap rows of this wavefront's output
+    // pixel blocks (the tap column and the K step add constants: immediate
+    // offsets)
+    uint32_t rowo[NPW][3];
     bool live[NPW];
 #pragma unroll
     for (int i = 0; i < NPW; ++i) {
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
       const uint32_t ox = valid ? op - oy * a.TW : 0;
       const uint32_t base = oy * a.S * a.HW + ox * a.S;
 #pragma unroll
-      for (int t = 0; t < 9; ++t) rowo[i][t] = (base + (t / 3) * a.HW + t % 3) * RPE + lh * 16;
+      for (int dy = 0; dy < 3; ++dy) rowo[i][dy] = a.lds_xe + (base + dy * a.HW) * RPE + lh * 16;
     }
 
     // (1) expand chunk c over the halo tile -> XeL
@@ -381,8 +383,9 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
         // lane: output channel l32 of block o, K groups as in the expand
         const char *wpp = WpL + s * WPS + ((uint32_t)lh * (HK / 4) * a.CO + l32) * GB;
         const uint32_t wp_ks = KSTEP / 4 * a.CO * GB, wp_next = a.CO * GB;
-        // one K step at a time: hoisting the next step's 18 operand reads
-        // above this one doubles the live registers and halves occupancy
+        // one K step at a time (unrolled, so that every LDS offset is an
+        // immediate; the scheduling barrier keeps the next step's 18 operand
+        // reads below this one, which would double the live registers)
 #pragma unroll 1
         for (int ks = 0; ks < NKS; ++ks) {
           u32x4 wv[9];
@@ -399,7 +402,8 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
             for (int j = 0; j < HK; ++j) d[j] = bias[j];
 #pragma unroll
             for (int t = 0; t < 9; ++t)
-              ir_fma_taps<DT, HK>(*reinterpret_cast<const u32x4 *>(XeL + rowo[i][t] + ks * 32), wv[t], d);
+              ir_fma_taps<DT, HK>(
+                  *reinterpret_cast<const u32x4 *>(lds + rowo[i][t / 3] + (t % 3) * RPE + ks * 32), wv[t], d);
             ir_act<CL, HK>(act_d, d);
             bop[i] = ir_pack<DT, HK>(d);
           }
@@ -410,6 +414,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
             for (int i = 0; i < NPW; ++i)
               if (live[i]) acc[i][o] = ir_mma<DT>(av, bop[i], acc[i][o]);
           }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
 
