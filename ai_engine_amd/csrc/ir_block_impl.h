@@ -210,7 +210,6 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   const uint32_t TPIX = a.TH * a.TW;
   const uint32_t WES = EC * a.C * ES, WPS = EC * a.CO * ES;  // bytes of one slot
   const Act act_e = act_params(a.act_e), act_d = act_params(a.act_d), act_p = act_params(a.act_p);
-  auto slot = [&](uint32_t c) -> uint32_t { return a.resident ? c : (c & 1); };
 
   const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x);
   const uint32_t t_begin = (uint32_t)(((uint64_t)blk * a.ntiles) / gridDim.x);
@@ -253,40 +252,58 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
     for (uint32_t c = 0; c < nchunks; ++c) dma_chunk(c, c);
 
   const uint32_t img_bytes = a.IH * a.IW * a.C * ES;
-  for (uint32_t T = t_begin; T < t_end; ++T) {
-    const uint32_t per_img = a.tiles_y * a.tiles_x;
-    const uint32_t img = fdiv(T, a.fd_pi);
+  const uint32_t per_img = a.tiles_y * a.tiles_x;
+  // output origin of tile T: image, first row, first column
+  auto tile_origin = [&](uint32_t T, uint32_t &img, uint32_t &ty0, uint32_t &tx0) {
+    img = fdiv(T, a.fd_pi);
     const uint32_t trem = T - img * per_img;
     const uint32_t tyi = fdiv(trem, a.fd_tx);
-    const uint32_t ty0 = tyi * a.TH, tx0 = (trem - tyi * a.tiles_x) * a.TW;
+    ty0 = tyi * a.TH;
+    tx0 = (trem - tyi * a.tiles_x) * a.TW;
+  };
+  // (0) input tile T with halo -> XL: item g is 16 bytes of halo row
+  // r = g / (NVX + 1); pixels outside the image read as zeros. The row's
+  // last item (the pitch padding) is the bias column of the expand: 1.0 in
+  // its first K slot for pixels inside the image, 0 outside, so the expand
+  // of an outside pixel is exactly 0. Asynchronous: published by the next
+  // ir_dma_wait() and barrier.
+  auto load_x = [&](uint32_t T) {
+    uint32_t img, ty0, tx0;
+    tile_origin(T, img, ty0, tx0);
+    const int32_t iy0 = (int32_t)(ty0 * a.S) - a.PT, ix0 = (int32_t)(tx0 * a.S) - a.PL;
+    const __amdgpu_buffer_rsrc_t rs_x = ir_rsrc(xg + (size_t)img * img_bytes, img_bytes);
+    ir_dma<16>(XL, a.NPI * 32 * (NVX + 1), rs_x, wave, lane, 0, [&](uint32_t g) -> uint32_t {
+      const uint32_t r = fdiv(g, a.fd_rpx), v = g - r * (NVX + 1);
+      if (v == NVX) return IR_SKIP;
+      const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
+      const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
+      const bool in = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
+      return in ? ((uint32_t)iy * a.IW + (uint32_t)ix) * (NVX * 16) + v * 16 : IR_OOB;
+    });
+    constexpr uint32_t ONE = F32 ? 0x3F800000u : (DT == DT_F16 ? 0x3C00u : 0x3F80u);
+    for (uint32_t r = tid; r < a.NPI * 32; r += 256) {
+      const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
+      const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
+      const bool in = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
+      *reinterpret_cast<u32x4 *>(XL + r * RPX + NVX * 16) = u32x4{in ? ONE : 0u, 0u, 0u, 0u};
+    }
+  };
+
+  // Pipeline across tiles: the next tile's input tile (and, streamed, its
+  // first chunk's weights) are copied while the current tile's last chunk
+  // runs its depthwise and projection, so a tile starts with its operands in
+  // LDS. Streamed weights alternate between two slots over the workgroup's
+  // whole run of chunks: chunk number gc sits in slot gc & 1.
+  load_x(t_begin);
+  if (!a.resident) dma_chunk(0, 0);
+  uint32_t gc = 0;
+  for (uint32_t T = t_begin; T < t_end; ++T) {
+    uint32_t img, ty0, tx0;
+    tile_origin(T, img, ty0, tx0);
     const int32_t iy0 = (int32_t)(ty0 * a.S) - a.PT, ix0 = (int32_t)(tx0 * a.S) - a.PL;
 
-    // every wavefront is done with the previous tile's LDS
-    __syncthreads();
-    // (0) input tile with halo -> XL: item g is 16 bytes of halo row
-    // r = g / (NVX + 1); pixels outside the image read as zeros. The row's
-    // last item (the pitch padding) is the bias column of the expand: 1.0 in
-    // its first K slot for pixels inside the image, 0 outside, so the expand
-    // of an outside pixel is exactly 0. Streamed weights: chunk 0 -> slot 0.
-    {
-      const __amdgpu_buffer_rsrc_t rs_x = ir_rsrc(xg + (size_t)img * img_bytes, img_bytes);
-      ir_dma<16>(XL, a.NPI * 32 * (NVX + 1), rs_x, wave, lane, 0, [&](uint32_t g) -> uint32_t {
-        const uint32_t r = fdiv(g, a.fd_rpx), v = g - r * (NVX + 1);
-        if (v == NVX) return IR_SKIP;
-        const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
-        const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
-        const bool in = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
-        return in ? ((uint32_t)iy * a.IW + (uint32_t)ix) * (NVX * 16) + v * 16 : IR_OOB;
-      });
-      constexpr uint32_t ONE = F32 ? 0x3F800000u : (DT == DT_F16 ? 0x3C00u : 0x3F80u);
-      for (uint32_t r = tid; r < a.NPI * 32; r += 256) {
-        const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
-        const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
-        const bool in = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
-        *reinterpret_cast<u32x4 *>(XL + r * RPX + NVX * 16) = u32x4{in ? ONE : 0u, 0u, 0u, 0u};
-      }
-    }
-    if (!a.resident) dma_chunk(0, 0);
+    // the tile's input (and weights) have landed; every wavefront is done
+    // with the previous tile's LDS
     ir_dma_wait();
     __syncthreads();
 
@@ -308,9 +325,8 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
       for (int dy = 0; dy < 3; ++dy) rowo[i][dy] = a.lds_xe + (base + dy * a.HW) * RPE + lh * 16;
     }
 
-    // (1) expand chunk c over the halo tile -> XeL
-    auto expand = [&](uint32_t c) {
-      const uint32_t s = slot(c);
+    // (1) expand chunk c (weights in slot s) over the halo tile -> XeL
+    auto expand = [&](uint32_t s) {
       // lane: channel l32 of the chunk, K groups from 2*lh (16-bit) / lh (fp32);
       // a K step advances KSTEP/4 groups = 1024 bytes
       const char *ap = WeL + s * WES + ((uint32_t)lh * (HK / 4) * EC + l32) * GB;
@@ -366,18 +382,61 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
 #pragma unroll
       for (int o = 0; o < NOB; ++o) acc[i][o] = f32x16{};
 
-    // Chunk loop: the next chunk's streamed weights start towards the other
-    // slot (last read by chunk c - 1, before the barrier that closed it), then
+    // Residual of the output pixels, read into registers while the last
+    // chunk runs when it takes at most 16 registers a lane.
+    constexpr bool PREF_RES = false;
+    u32x4 resv[PREF_RES ? NPW : 1][PREF_RES ? NOB : 1][4];
+    // output pixel of lane l32 in block i (false: outside the tile or image)
+    auto out_pixel = [&](int i, size_t &pix) -> bool {
+      const uint32_t pbo = wave + 4 * i;
+      if (pbo >= a.NPB) return false;
+      const uint32_t op = pbo * 32 + l32;
+      const uint32_t oy = fdiv(op, a.fd_tw), ox = op - oy * a.TW;
+      const uint32_t gy = ty0 + oy, gx = tx0 + ox;
+      if (op >= TPIX || gy >= a.OH || gx >= a.OW) return false;
+      pix = ((size_t)img * a.OH + gy) * a.OW + gx;
+      return true;
+    };
+
+    // Chunk loop: the next chunk's streamed weights (the next tile's first
+    // chunk after the last) start towards the other slot (last read by the
+    // previous chunk, before the barrier that closed it), then
     // expand(c) | barrier | depthwise + project(c) | copies landed + barrier.
     for (uint32_t c = 0; c < nchunks; ++c) {
-      if (!a.resident && c + 1 < nchunks) dma_chunk(c + 1, (c + 1) & 1);
-      expand(c);
+      const bool last = c + 1 == nchunks, next_tile = T + 1 < t_end;
+      const uint32_t s = a.resident ? c : (gc & 1);
+      if (!a.resident && (!last || next_tile)) dma_chunk(last ? 0 : c + 1, (gc + 1) & 1);
+      expand(s);
       __syncthreads();
+      if (last) {
+        // the input tile is no longer read: the next one can land in XL
+        if constexpr (PREF_RES) {
+          if (a.has_res) {
+#pragma unroll
+            for (int i = 0; i < NPW; ++i) {
+              size_t pix;
+              if (!out_pixel(i, pix)) continue;
+#pragma unroll
+              for (int o = 0; o < NOB; ++o)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  const size_t vi = pix * (a.CO / 4) + (o * 32 + 8 * q + 4 * lh) / 4;
+                  if constexpr (F32) {
+                    resv[i][o][q] = reinterpret_cast<const u32x4 *>(a.res)[vi];
+                  } else {
+                    const u32x2 r2 = reinterpret_cast<const u32x2 *>(a.res)[vi];
+                    resv[i][o][q] = u32x4{r2.x, r2.y, 0u, 0u};
+                  }
+                }
+            }
+          }
+        }
+        if (next_tile) load_x(T + 1);
+      }
 
       // (2) depthwise of chunk c straight into the projection's B operand;
       // the wavefront's pixel blocks share every K step's weight reads
       {
-        const uint32_t s = slot(c);
         const char *wdp = SmL + s * SMB + lh * 16;            // tap t at + t * EC * ES
         const char *bdp = SmL + s * SMB + 9 * EC * ES + lh * 16;
         // lane: output channel l32 of block o, K groups as in the expand
@@ -418,20 +477,19 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
         }
       }
 
-      ir_dma_wait();
-      __syncthreads();
+      ++gc;
+      if (!last) {
+        ir_dma_wait();
+        __syncthreads();
+      }
     }
 
-    // epilogue: bias -> act -> (+ residual) -> HBM
+    // epilogue: bias -> act -> (+ residual) -> HBM (the next tile's top
+    // barrier orders this tile's last LDS reads before its writes)
 #pragma unroll
     for (int i = 0; i < NPW; ++i) {
-      const uint32_t pbo = wave + 4 * i;
-      if (pbo >= a.NPB) continue;
-      const uint32_t op = pbo * 32 + l32;
-      const uint32_t oy = fdiv(op, a.fd_tw), ox = op - oy * a.TW;
-      const uint32_t gy = ty0 + oy, gx = tx0 + ox;
-      if (op >= TPIX || gy >= a.OH || gx >= a.OW) continue;
-      const size_t pix = ((size_t)img * a.OH + gy) * a.OW + gx;
+      size_t pix;
+      if (!out_pixel(i, pix)) continue;
 #pragma unroll
       for (int o = 0; o < NOB; ++o) {
 #pragma unroll
@@ -445,7 +503,15 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
             v = f32x4{t[0], t[1], t[2], t[3]};
           }
           const size_t vi = pix * (a.CO / 4) + oc / 4;
-          if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
+          if (a.has_res) {
+            if constexpr (!PREF_RES) {
+              v += Vec4IO<DT>::load(a.res, vi);
+            } else if constexpr (F32) {
+              v += __builtin_bit_cast(f32x4, resv[i][o][q]);
+            } else {
+              v += unpack4<DT>(u32x2{resv[i][o][q].x, resv[i][o][q].y});
+            }
+          }
           Vec4IO<DT>::store(a.y, vi, v);
         }
       }
