@@ -206,12 +206,12 @@ __device__ __forceinline__ Act act_params(int act) {
   return p;
 }
 
-// A clamp-type activation (act_is_clamp) without a branch: one v_med3_i32
-// (the compiler forms med3 only for constant bounds; lob <= hib holds here).
+// A clamp-type activation (act_is_clamp) without a branch: an integer max
+// and min on the float bits. (Not inline asm: the values often come straight
+// from an MFMA, and only instructions the compiler sees get the wait states
+// that a read of an MFMA result needs.)
 __device__ __forceinline__ float act_clamp_any(const Act &p, float x) {
-  int r;
-  asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"(__float_as_int(x)), "v"(p.lob), "s"(p.hib));
-  return __int_as_float(r);
+  return __int_as_float(min(max(__float_as_int(x), p.lob), p.hib));
 }
 
 __device__ __forceinline__ float act_relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
