@@ -168,20 +168,19 @@ struct Act {
   int hib;  // bits of hi
   int mode;
   int act;
-  int lob;  // clamp-type activations: lower bound bits (INT_MIN for the identity, 0 otherwise)
+  float clo, chi;  // clamp-type activations: the clamp interval ([-inf, inf] for the identity)
 };
 enum : int { ACT_LINEAR = 0, ACT_CLAMP = 1, ACT_XCLAMP = 2, ACT_SPECIAL = 3, ACT_IDENT = 4, ACT_RELU = 5,
              ACT_CLAMP0 = 6 };
 
-// Activations that are a clamp of the float bits as signed integers to
-// [lob, hib]: the identity, ReLU, ReLU6 and clamp01 (non-negative floats order
-// like their bits; negative floats are negative integers).
+// Activations that are a clamp to an interval [clo, chi]: the identity,
+// ReLU, ReLU6 and clamp01.
 __host__ __device__ __forceinline__ bool act_is_clamp(int act) {
   return act == AIH_ACT_NONE || act == AIH_ACT_RELU || act == AIH_ACT_RELU6 || act == AIH_ACT_CLAMP01;
 }
 
 __device__ __forceinline__ Act act_params(int act) {
-  Act p{1.0f, -0.0f, 0.0f, 0, ACT_LINEAR, act, 0};
+  Act p{1.0f, -0.0f, 0.0f, 0, ACT_LINEAR, act, 0.0f, 0.0f};
   switch (act) {
     case AIH_ACT_NONE: p.mode = ACT_IDENT; break;
     case AIH_ACT_NEG: p.s = -1.0f; break;
@@ -197,21 +196,18 @@ __device__ __forceinline__ Act act_params(int act) {
     default: p.mode = ACT_SPECIAL; break;
   }
   p.hib = __float_as_int(p.hi);
-  if (p.mode == ACT_IDENT) {
-    p.lob = (int)0x80000000;
-    p.hib = 0x7fffffff;
-  } else if (p.mode == ACT_RELU) {
-    p.hib = 0x7fffffff;
-  }
+  p.clo = p.mode == ACT_IDENT ? -__builtin_huge_valf() : 0.0f;
+  p.chi = p.mode == ACT_CLAMP0 ? p.hi : __builtin_huge_valf();
   return p;
 }
 
-// A clamp-type activation (act_is_clamp) without a branch: an integer max
-// and min on the float bits. (Not inline asm: the values often come straight
-// from an MFMA, and only instructions the compiler sees get the wait states
-// that a read of an MFMA result needs.)
+// A clamp-type activation (act_is_clamp) without a branch: one v_med3_f32
+// with the interval [clo, chi] (the identity is [-inf, inf]). Only a zero's
+// sign can differ from max / min; a NaN input stays NaN. (A builtin rather
+// than inline asm: the values often come straight from an MFMA, and only
+// instructions the compiler sees get the wait states an MFMA result needs.)
 __device__ __forceinline__ float act_clamp_any(const Act &p, float x) {
-  return __int_as_float(min(max(__float_as_int(x), p.lob), p.hib));
+  return __builtin_amdgcn_fmed3f(x, p.clo, p.chi);
 }
 
 __device__ __forceinline__ float act_relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
