@@ -226,7 +226,10 @@ def kernel_key(conv, op, n, dt, dtname) -> str:
     if op.kind == "ir_block":
         p = op.spec.plan()
         npw = -(-(-(-p.th * p.tw // 32)) // 4)
-        return f"ir_block_kernel<{int(dt)}, {op.spec.cout // 32}, {npw}>"
+        A = conv.Activation
+        clamp = all(int(x) in (A.NONE, A.RELU, A.RELU6, A.CLAMP01)
+                    for x in (op.spec.act_expand, op.spec.act_dw, op.spec.act_project))
+        return f"ir_block_kernel<{int(dt)}, {op.spec.cout // 32}, {npw}, {'true' if clamp else 'false'}>"
     Lr = op.layers[0]
     if Lr.depthwise:
         return f"conv_dw_strip_kernel<{dtname}>"
