@@ -104,11 +104,17 @@ __device__ __forceinline__ void ir_fma_taps(u32x4 xv, u32x4 wv, float (&d)[HK]) 
 #pragma unroll
     for (int j = 0; j < HK; ++j) d[j] += (float)x[j] * (float)w[j];
   } else {
+    // bf16: v_dot2c_f32_bf16 against the weight with its other half zeroed,
+    // x.lo * w.lo + x.hi * 0 + d (the bf16 product is exact in fp32, so this
+    // is the FMA of the widened operands) -- two instructions per channel
+    // pair instead of four widenings and two FMAs
     const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w}, ws[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      d[2 * j] += __uint_as_float(xs[j] << 16) * __uint_as_float(ws[j] << 16);
-      d[2 * j + 1] += __uint_as_float(xs[j] & 0xffff0000u) * __uint_as_float(ws[j] & 0xffff0000u);
+      const bf16x2 x2 = __builtin_bit_cast(bf16x2, xs[j]);
+      d[2 * j] = __builtin_amdgcn_fdot2_f32_bf16(x2, __builtin_bit_cast(bf16x2, ws[j] & 0x0000ffffu), d[2 * j], false);
+      d[2 * j + 1] =
+          __builtin_amdgcn_fdot2_f32_bf16(x2, __builtin_bit_cast(bf16x2, ws[j] & 0xffff0000u), d[2 * j + 1], false);
     }
   }
 }
