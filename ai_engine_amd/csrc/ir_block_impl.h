@@ -388,10 +388,6 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
 #pragma unroll
       for (int o = 0; o < NOB; ++o) acc[i][o] = f32x16{};
 
-    // Residual of the output pixels, read into registers while the last
-    // chunk runs when it takes at most 16 registers a lane.
-    constexpr bool PREF_RES = false;
-    u32x4 resv[PREF_RES ? NPW : 1][PREF_RES ? NOB : 1][4];
     // output pixel of lane l32 in block i (false: outside the tile or image)
     auto out_pixel = [&](int i, size_t &pix) -> bool {
       const uint32_t pbo = wave + 4 * i;
@@ -416,27 +412,6 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
       __syncthreads();
       if (last) {
         // the input tile is no longer read: the next one can land in XL
-        if constexpr (PREF_RES) {
-          if (a.has_res) {
-#pragma unroll
-            for (int i = 0; i < NPW; ++i) {
-              size_t pix;
-              if (!out_pixel(i, pix)) continue;
-#pragma unroll
-              for (int o = 0; o < NOB; ++o)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                  const size_t vi = pix * (a.CO / 4) + (o * 32 + 8 * q + 4 * lh) / 4;
-                  if constexpr (F32) {
-                    resv[i][o][q] = reinterpret_cast<const u32x4 *>(a.res)[vi];
-                  } else {
-                    const u32x2 r2 = reinterpret_cast<const u32x2 *>(a.res)[vi];
-                    resv[i][o][q] = u32x4{r2.x, r2.y, 0u, 0u};
-                  }
-                }
-            }
-          }
-        }
         if (next_tile) load_x(T + 1);
       }
 
@@ -509,15 +484,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
             v = f32x4{t[0], t[1], t[2], t[3]};
           }
           const size_t vi = pix * (a.CO / 4) + oc / 4;
-          if (a.has_res) {
-            if constexpr (!PREF_RES) {
-              v += Vec4IO<DT>::load(a.res, vi);
-            } else if constexpr (F32) {
-              v += __builtin_bit_cast(f32x4, resv[i][o][q]);
-            } else {
-              v += unpack4<DT>(u32x2{resv[i][o][q].x, resv[i][o][q].y});
-            }
-          }
+          if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
           Vec4IO<DT>::store(a.y, vi, v);
         }
       }
