@@ -61,6 +61,8 @@ class Variant(enum.IntEnum):
     AUTO = 0
     TILE = 1
     SPLITK = 2
+    ROWS = 3    # reported by the pointwise plan: one pixel per thread (ng == 1)
+    DIRECT = 4  # reported by the pointwise plan: short K, operands straight into MFMA registers
 
 
 # ---------------------------------------------------------------- ctypes structs (include/aih_conv.h)

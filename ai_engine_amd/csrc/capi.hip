@@ -18,6 +18,7 @@
 #include "capi_util.h"
 #include "conv_dw.h"
 #include "conv_gemm_launch.h"
+#include "conv_pw_direct.h"
 #include "conv_pw_narrow.h"
 #include "conv_stem.h"
 #include "ir_block.h"
@@ -145,6 +146,19 @@ void fill_plan(const GemmPlan &g, aih_plan *out) {
   out->bn = (uint32_t)g.bn;
   out->grid = g.mtiles * g.ntiles * g.nsplit;
   out->ws_bytes = g.ws;
+}
+
+// Which kernel a pointwise call runs: with AIH_VAR_AUTO and no forced split,
+// one output channel group goes to the one-pixel-per-thread kernel and short
+// K with at most 64 output channels (same storage for activations and
+// weights) to the direct MFMA kernel; everything else to the tiled GEMM.
+enum { PW_TILED = 0, PW_ROWS = 1, PW_DIRECT = 2 };
+int pw_route(const aih_pw_desc *d) {
+  if (d->variant != AIH_VAR_AUTO || d->splitk != 0) return PW_TILED;
+  if (d->ng == 1 && d->kg <= aih::kPwNarrowMaxKG) return PW_ROWS;
+  const uint32_t kmax = d->dt == AIH_F32 ? aih::kPwDirectMaxK32 : aih::kPwDirectMaxK16;
+  if (d->dt == d->wdt && d->ng >= 2 && d->ng * 4 <= aih::kPwDirectMaxN4 && d->kg * 4 <= kmax) return PW_DIRECT;
+  return PW_TILED;
 }
 
 int run_gemm(aih::GemmArgs &a, const GemmPlan &g, int32_t dt, int32_t wdt, bool igemm, bool pair, void *ws,
@@ -290,6 +304,18 @@ int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out) {
   return guarded([&] {
     if (check_pw(d)) return AIH_ERR;
     if (!out) return fail("null plan");
+    const uint64_t M = (uint64_t)d->n * d->m;
+    switch (pw_route(d)) {
+      case PW_ROWS:
+        *out = aih_plan{AIH_VAR_ROWS, 1, 256, 4, (uint32_t)std::min<uint64_t>((M + 255) / 256, 4096), 0};
+        return AIH_OK;
+      case PW_DIRECT:
+        *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->ng * 4 <= 32 ? 32u : 64u,
+                        (uint32_t)std::min<uint64_t>((M + 127) / 128, 256u * 8u), 0};
+        return AIH_OK;
+      default:
+        break;
+    }
     GemmPlan g;
     if (plan_pw(d, &g)) return AIH_ERR;
     fill_plan(g, out);
@@ -305,13 +331,24 @@ int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *
     if ((d->residual != 0) != (res != nullptr)) return fail("pw: res must be given iff residual");
     if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16) || !aligned(bias, 8) || (res && !aligned(res, 16)))
       return fail("pw: misaligned buffer (x, w, y, res need 16 bytes, bias 8)");
-    if (d->ng == 1 && d->variant == AIH_VAR_AUTO && d->splitk == 0 && d->kg <= aih::kPwNarrowMaxKG) {
+    const int route = pw_route(d);
+    if (route == PW_ROWS) {
       // at most 4 output channels: one pixel per thread on the VALU
       const uint64_t M = (uint64_t)d->n * d->m;
       if (M > 0xffffffffull) return fail("pw: too many pixels");
       aih::PwNarrowArgs na{x, w, bias, res, y, (uint32_t)M, d->kg, d->kg, d->act, d->residual ? 1 : 0};
       const hipError_t e = aih::launch_pw_narrow(na, d->dt, d->wdt, static_cast<hipStream_t>(stream));
       return e == hipSuccess ? AIH_OK : fail(std::string("pw narrow launch: ") + hipGetErrorString(e));
+    }
+    if (route == PW_DIRECT) {
+      // short K and at most 64 output channels: operands from memory straight
+      // into MFMA registers, no LDS staging
+      const uint64_t M = (uint64_t)d->n * d->m;
+      if (M > 0xffffff00ull) return fail("pw: too many pixels");
+      aih::PwDirectArgs da{x, w, bias, res, y, (uint32_t)M, d->kg, d->ng * 4, (uint32_t)((M + 31) / 32),
+                           d->act, d->residual ? 1 : 0};
+      const hipError_t e = aih::launch_pw_direct(da, d->dt, static_cast<hipStream_t>(stream));
+      return e == hipSuccess ? AIH_OK : fail(std::string("pw direct launch: ") + hipGetErrorString(e));
     }
     GemmPlan g;
     if (plan_pw(d, &g)) return AIH_ERR;

@@ -1,0 +1,27 @@
+// conv_pw_direct.h -- launch interface of the pointwise conv with short K and
+// at most 64 output channels (operands straight from memory into MFMA
+// registers, no LDS).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace aih {
+
+struct PwDirectArgs {
+  const void *x, *w, *bias, *res;
+  void *y;
+  uint32_t M;     // pixels over the whole batch
+  uint32_t KG;    // input kg (4-channel groups) per pixel (the input's pixel stride)
+  uint32_t N4;    // output channels padded to 4 (the weights' and the output's column count)
+  uint32_t nblk;  // 32-pixel blocks
+  int32_t act, has_res;
+};
+
+// Largest K (channels) and N4 the kernel takes: its operands of one 32-pixel
+// block stay in registers.
+constexpr uint32_t kPwDirectMaxK16 = 128, kPwDirectMaxK32 = 64, kPwDirectMaxN4 = 64;
+
+hipError_t launch_pw_direct(const PwDirectArgs &a, int dt, hipStream_t st);
+
+}  // namespace aih

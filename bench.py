@@ -237,6 +237,8 @@ def kernel_key(conv, op, n, dt, dtname) -> str:
         return f"pw_narrow_kernel<{dtname}>"
     if Lr.k == 1:
         p = conv.GemmPwSpec(m=Lr.ih * Lr.iw, kg=-(-Lr.cin // 4), ng=-(-Lr.cout // 4), dt=dt, n=n).plan()
+        if p.variant == conv.Variant.DIRECT:
+            return f"pw_direct_kernel<{dtname}>"
     else:
         p = conv.ConvIgemmSpec(ih=Lr.ih, iw=Lr.iw, cin=Lr.cin, cout=Lr.cout, k=Lr.k, s=Lr.s, pad=(Lr.pad,) * 4,
                                dt=dt, n=n).plan()

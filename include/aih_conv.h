@@ -64,11 +64,15 @@ enum aih_act {
   AIH_ACT_RECIP = 10
 };
 
-/* Kernel variants chosen by the plan functions. */
+/* Kernel variants chosen by the plan functions (a caller asks for the first
+ * three; the pointwise plan also reports the last two). */
 enum aih_variant {
-  AIH_VAR_AUTO = 0,   /* let the policy decide */
-  AIH_VAR_TILE = 1,   /* one MFMA tile per workgroup over the whole K */
-  AIH_VAR_SPLITK = 2  /* K cut into chunks, fp32 partials reduced in a fixed order */
+  AIH_VAR_AUTO = 0,    /* let the policy decide */
+  AIH_VAR_TILE = 1,    /* one MFMA tile per workgroup over the whole K */
+  AIH_VAR_SPLITK = 2,  /* K cut into chunks, fp32 partials reduced in a fixed order */
+  AIH_VAR_ROWS = 3,    /* pointwise, ng == 1: one pixel per thread on the VALU */
+  AIH_VAR_DIRECT = 4   /* pointwise, short K, ng <= 16: 32 pixels per wavefront,
+                          operands from memory into MFMA registers */
 };
 
 /* Pointwise 1x1 conv GEMM: out[M, N] = act(in[M, K] x W[K, N] + bias) (+ res).
@@ -130,7 +134,7 @@ typedef struct {
 
 /* What a plan function chose; grid is the number of workgroups of the main kernel. */
 typedef struct {
-  int32_t variant;  /* AIH_VAR_TILE or AIH_VAR_SPLITK */
+  int32_t variant;  /* AIH_VAR_TILE, AIH_VAR_SPLITK, AIH_VAR_ROWS or AIH_VAR_DIRECT */
   uint32_t splitk;  /* K chunks (1 for TILE) */
   uint32_t bm, bn;  /* output tile: pixels x channels */
   uint32_t grid;
@@ -170,10 +174,12 @@ typedef struct {
 
 /* Buffer order follows GemmPwSpec::bindings (gemm_pw.rs:276-283): IN, W, BIAS,
  * [RES], OUT. res must be NULL iff residual == 0. ws may be NULL when the plan
- * needs no workspace; otherwise ws_bytes >= aih_plan.ws_bytes. With ng == 1
- * (at most 4 output channels), AIH_VAR_AUTO and splitk == 0 the call runs a
- * VALU kernel (one pixel per thread, the reference's Gemv role) instead of
- * the planned MFMA tile, and needs no workspace. */
+ * needs no workspace; otherwise ws_bytes >= aih_plan.ws_bytes. With
+ * AIH_VAR_AUTO and splitk == 0 two shapes skip the planned MFMA tile and need
+ * no workspace: ng == 1 (at most 4 output channels) runs a VALU kernel (one
+ * pixel per thread, the reference's Gemv role); dt == wdt, 2 <= ng <= 16 and
+ * at most 128 (16-bit) / 64 (fp32) input channels run a direct MFMA kernel
+ * (32 pixels per wavefront, operands from memory into registers). */
 int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *bias,
                 const void *res, void *y, void *ws, size_t ws_bytes, aih_stream stream);
 int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out);

@@ -71,10 +71,17 @@ def test_pw_policy_splits_small_m_large_k():
     p = pw_plan(256, 180, 960, 160)
     assert p.variant == conv.Variant.TILE and p.splitk == 1 and p.ws_bytes == 0
     assert p.bn == 160 and p.grid == 360
-    # 1x1 32 -> 64 at 80x144: K is one stage, nothing to split; 90 pixel
-    # tiles cannot fill 256 CUs, so the columns are cut into two 32-wide tiles
+    # 1x1 32 -> 64 at 80x144: short K (32) and 64 output channels -> the
+    # direct kernel, 32 pixels a wavefront, no workspace
     p = pw_plan(1, 11520, 32, 64)
+    assert p.variant == conv.Variant.DIRECT and p.bm == 32 and p.bn == 64 and p.grid == 90 and p.ws_bytes == 0
+    # the tiled GEMM forced: K is one stage, nothing to split; 90 pixel tiles
+    # cannot fill 256 CUs, so the columns are cut into two 32-wide tiles
+    p = pw_plan(1, 11520, 32, 64, variant=conv.Variant.TILE)
     assert p.variant == conv.Variant.TILE and p.bn == 32 and p.grid == 180
+    # one output channel group: the one-pixel-per-thread kernel
+    p = pw_plan(1, 11520, 128, 2)
+    assert p.variant == conv.Variant.ROWS and p.ws_bytes == 0
 
 
 def test_pw_policy_agrees_with_reference_on_its_splitk_kats(orc):
@@ -87,7 +94,8 @@ def test_pw_policy_agrees_with_reference_on_its_splitk_kats(orc):
         assert p.variant == conv.Variant.SPLITK, (m, kg, ng, p)
     for m, kg, ng in [(36864, 6, 4), (36864, 1, 4), (512, 8, 8)]:
         assert orc.ref_pw_variant(m, kg, ng) == "Small"
-        assert conv.GemmPwSpec(m=m, kg=kg, ng=ng).plan().variant == conv.Variant.TILE
+        p = conv.GemmPwSpec(m=m, kg=kg, ng=ng).plan()
+        assert p.variant in (conv.Variant.TILE, conv.Variant.DIRECT) and p.splitk == 1, (m, kg, ng, p)
 
 
 def test_forced_splitk_factor_is_honoured():

