@@ -62,7 +62,7 @@ class Variant(enum.IntEnum):
     TILE = 1
     SPLITK = 2
     ROWS = 3    # reported by the pointwise plan: one pixel per thread (ng == 1)
-    DIRECT = 4  # reported by the pointwise plan: short K, operands straight into MFMA registers
+    DIRECT = 4  # reported by the plans: operands straight into MFMA registers (short-K pointwise, 3x3 <= 64 outputs)
 
 
 # ---------------------------------------------------------------- ctypes structs (include/aih_conv.h)

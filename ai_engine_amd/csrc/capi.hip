@@ -18,6 +18,7 @@
 #include "capi_util.h"
 #include "conv_dw.h"
 #include "conv_gemm_launch.h"
+#include "conv_igemm_direct.h"
 #include "conv_pw_direct.h"
 #include "conv_pw_narrow.h"
 #include "conv_stem.h"
@@ -249,11 +250,74 @@ int check_igemm(const aih_igemm_desc *d) {
   return AIH_OK;
 }
 
+// The stem route: <= 3 input channels of a dense input, 3x3, 32 or 64 outputs.
+bool igemm_is_stem(const aih_igemm_desc *d) {
+  const bool dense_in = d->nsrcs == 0 || (d->nsrcs == 1 && d->srcs[0].c_off == 0 && d->srcs[0].stride_c == 4);
+  return d->k == 3 && d->d == 1 && d->cin <= 3 && dense_in && d->cout % 32 == 0 && d->cout <= 64 &&
+         d->variant == AIH_VAR_AUTO && d->splitk == 0 && d->dt == d->wdt;
+}
+
 int plan_igemm(const aih_igemm_desc *d, GemmPlan *g) {
   uint32_t oh, ow;
   if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
   return plan_gemm(d->n * oh * ow, div_ceil(d->cout, 4) * 4, d->k * d->k * div_ceil(d->cin, 4), d->dt,
                    d->variant, d->splitk, g);
+}
+
+// The 3x3 direct kernel's arguments for an igemm call (buffers aside), or
+// false when the call goes to the tiled GEMM: AIH_VAR_AUTO without a forced
+// split, a 3x3 kernel, the same storage for activations and weights, at most
+// 64 output channels, at most two input parts whose kg runs, pixel strides
+// and offsets are whole 16-byte units (two kg for 16-bit storage), at most 8
+// MFMA steps per tap and every part below 2 GiB.
+bool ig_direct_plan(const aih_igemm_desc *d, uint32_t oh, uint32_t ow, aih::IgDirectArgs *a) {
+  if (d->variant != AIH_VAR_AUTO || d->splitk != 0 || d->k != 3 || d->dt != d->wdt) return false;
+  const uint32_t n4 = div_ceil(d->cout, 4) * 4;
+  if (n4 > 64) return false;
+  const uint32_t nparts = d->nsrcs ? d->nsrcs : 1;
+  if (nparts > 2) return false;
+  const uint32_t ku = d->dt == AIH_F32 ? 1 : 2, es = d->dt == AIH_F32 ? 4 : 2;
+  std::memset(a, 0, sizeof(*a));
+  uint32_t kg0 = 0, nj = 0;
+  for (uint32_t i = 0; i < nparts; ++i) {
+    const uint32_t kgi = div_ceil(d->nsrcs ? d->srcs[i].c : d->cin, 4);
+    const uint32_t stride = d->nsrcs ? d->srcs[i].stride_c / 4 : kgi;
+    const uint32_t off = d->nsrcs ? d->srcs[i].c_off / 4 : 0;
+    if (kgi % ku || stride % ku || off % ku) return false;
+    const uint64_t bytes = (uint64_t)d->n * d->ih * d->iw * stride * 4 * es;
+    if (bytes >= 0x80000000ull) return false;
+    a->src_bytes[i] = (uint32_t)bytes;
+    a->stride_u[i] = stride / ku;
+    a->off_u[i] = off / ku;
+    a->nu[i] = kgi / ku;
+    a->kg_first[i] = kg0;
+    kg0 += kgi;
+    nj += div_ceil(a->nu[i], 2);
+    if (i == 0) a->nj0 = nj;
+  }
+  if (nparts == 1) {
+    a->src_bytes[1] = a->src_bytes[0];
+    a->stride_u[1] = a->stride_u[0];
+  }
+  if (nj == 0 || nj > aih::kIgDirectMaxSteps || aih::ig_direct_lds_bytes(nj, n4) > 160u * 1024u) return false;
+  a->nj = nj;
+  a->KGP = div_ceil(div_ceil(d->cin, 4), 4) * 4;
+  a->N4 = n4;
+  a->M = d->n * oh * ow;
+  a->OHW = oh * ow;
+  a->OW = ow;
+  a->IH = d->ih;
+  a->IW = d->iw;
+  a->S = d->s;
+  a->D = d->d;
+  a->PT = (int32_t)d->pad[0];
+  a->PL = (int32_t)d->pad[1];
+  a->nblk = div_ceil(a->M, 32);
+  a->act = d->act;
+  a->has_res = d->residual ? 1 : 0;
+  a->fd_ohw = aih::make_fastdiv(oh * ow);
+  a->fd_ow = aih::make_fastdiv(ow);
+  return true;
 }
 
 // ---------------------------------------------------------------- fused inverted-residual block
@@ -385,6 +449,13 @@ int aih_conv_igemm_plan(const aih_igemm_desc *d, aih_plan *out) {
   return guarded([&] {
     if (check_igemm(d)) return AIH_ERR;
     if (!out) return fail("null plan");
+    uint32_t oh, ow;
+    if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
+    aih::IgDirectArgs da;
+    if (!igemm_is_stem(d) && ig_direct_plan(d, oh, ow, &da)) {
+      *out = aih_plan{AIH_VAR_DIRECT, 1, 32, da.N4 <= 32 ? 32u : 64u, aih::ig_direct_grid(da.nblk, da.nj, da.N4), 0};
+      return AIH_OK;
+    }
     GemmPlan g;
     if (plan_igemm(d, &g)) return AIH_ERR;
     fill_plan(g, out);
@@ -407,9 +478,7 @@ int aih_conv_igemm(const aih_igemm_desc *d, const void *const *inputs, const voi
       return fail("igemm: misaligned buffer (w, y, res need 16 bytes, bias 8)");
     uint32_t oh, ow;
     if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
-    const bool dense_in = d->nsrcs == 0 || (d->nsrcs == 1 && d->srcs[0].c_off == 0 && d->srcs[0].stride_c == 4);
-    if (d->k == 3 && d->d == 1 && d->cin <= 3 && dense_in && d->cout % 32 == 0 && d->cout <= 64 &&
-        d->variant == AIH_VAR_AUTO && d->splitk == 0 && d->dt == d->wdt) {
+    if (igemm_is_stem(d)) {
       // the stem: <= 3 input channels, every (tap, channel) gathered into one
       // 32-deep MFMA operand
       const uint64_t M = (uint64_t)d->n * oh * ow;
@@ -438,6 +507,19 @@ int aih_conv_igemm(const aih_igemm_desc *d, const void *const *inputs, const voi
       sa.fd_ow = aih::make_fastdiv(ow);
       const hipError_t e = aih::launch_conv_stem(sa, d->dt, static_cast<hipStream_t>(stream));
       return e == hipSuccess ? AIH_OK : fail(std::string("conv stem launch: ") + hipGetErrorString(e));
+    }
+    aih::IgDirectArgs da;
+    if (ig_direct_plan(d, oh, ow, &da)) {
+      // 3x3 with at most 64 output channels: weights resident in LDS,
+      // activations straight into MFMA registers, no barriers after the load
+      for (uint32_t i = 0; i < (d->nsrcs ? d->nsrcs : 1); ++i) da.src[i] = inputs[i];
+      if (!d->nsrcs || d->nsrcs == 1) da.src[1] = da.src[0];
+      da.w = w;
+      da.bias = bias;
+      da.res = res;
+      da.y = y;
+      const hipError_t e = aih::launch_ig_direct(da, d->dt, static_cast<hipStream_t>(stream));
+      return e == hipSuccess ? AIH_OK : fail(std::string("igemm direct launch: ") + hipGetErrorString(e));
     }
     GemmPlan g;
     if (plan_igemm(d, &g)) return AIH_ERR;

@@ -1,0 +1,211 @@
+// conv_igemm_direct.hip -- 3x3 implicit-GEMM conv with at most 64 output
+// channels, the weights resident in LDS and the activations loaded straight
+// into MFMA operand registers.
+//
+// The tiled GEMM stages A and B through LDS in 16/32-channel steps behind a
+// workgroup barrier each; with 32 or 64 output columns a step holds only 2-8
+// MFMAs per wavefront, so the barrier and the staging round trip set the pace
+// (a 72 -> 32 3x3 conv at 40x72 batch 64 ran at 7 % of both rooflines).
+// Here the workgroup copies the whole packed weight tensor (9 taps x K x N)
+// into LDS once, reordered into MFMA A operands, and then never synchronises
+// again: each of its eight wavefronts owns 32 output pixels at a time, decodes
+// their source pixels per tap in registers (implicit im2col, no buffer) and
+// loads the tap's input channels as 16-byte buffer loads straight into MFMA B
+// operands -- out-of-image taps and padding units read zeros from the buffer
+// range check. The next tap's loads are in flight while the current tap's
+// MFMAs run. The reference's route for the same layers is
+// conv_igemm_{tiled,direct}.wgsl (crates/ai-gpu/src/kernels/conv_igemm.rs).
+//
+// K order: tap-major (ky, kx), then the input parts in order, then 16-byte
+// units of each part; MFMA step j of a tap pairs unit 2j (lane half 0) with
+// unit 2j + 1 (lane half 1) of one part, the same pairing for both operands.
+// A 16-byte unit is 4 fp32 channels (one kg: four v_mfma_f32_32x32x2f32, one
+// per component) or 8 16-bit channels (two kg: one v_mfma_f32_32x32x16).
+// Lane l of the result holds pixel l%32 and channels 8*(r/4) + 4*(l/32) + r%4;
+// the epilogue is act(acc + bias) (+ residual) (common/epilogue.rs:13-30),
+// one 4-channel vector per lane and group.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "conv_igemm_direct.h"
+
+namespace aih {
+namespace {
+
+constexpr uint32_t kOob = 0x80000000u;  // a byte offset past every part's buffer
+constexpr int kWaves = kIgDirectThreads / 64;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ig_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+
+template <int DT, int NOB, int NJM>
+__global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgDirectArgs a) {
+  constexpr bool F32 = DT == DT_F32;
+  constexpr int NC = NOB * 32;  // weight columns in LDS
+  extern __shared__ __align__(16) char lds[];
+  u32x4 *Wl = reinterpret_cast<u32x4 *>(lds);
+  const uint32_t nj = a.nj, nj0 = a.nj0;
+  float *Bl = reinterpret_cast<float *>(lds + 9 * nj * 2 * NC * 16);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, lh = lane >> 5;
+
+  // ---- weights -> LDS as [tap][step][half][column] operands (zero padding) ----
+  const uint32_t nw = 9 * nj * 2 * NC;
+  for (uint32_t i = tid; i < nw; i += kIgDirectThreads) {
+    const uint32_t n = i % NC, r = i / NC, h = r & 1, r2 = r >> 1, j = r2 % nj, tap = r2 / nj;
+    const uint32_t p = j >= nj0 ? 1 : 0;
+    const uint32_t u = 2 * (j - (p ? nj0 : 0)) + h;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (u < a.nu[p] && n < a.N4) {
+      if constexpr (F32) {
+        const uint32_t kg = a.kg_first[p] + u;
+        v = reinterpret_cast<const u32x4 *>(a.w)[(size_t)(tap * a.KGP + kg) * a.N4 + n];
+      } else {
+        const uint32_t kg = a.kg_first[p] + 2 * u;
+        const u32x2 *wp = reinterpret_cast<const u32x2 *>(a.w);
+        const u32x2 lo = wp[(size_t)(tap * a.KGP + kg) * a.N4 + n];
+        const u32x2 hi = wp[(size_t)(tap * a.KGP + kg + 1) * a.N4 + n];
+        v = u32x4{lo.x, lo.y, hi.x, hi.y};
+      }
+    }
+    Wl[i] = v;
+  }
+  if (tid < NC) Bl[tid] = (uint32_t)tid < a.N4 ? Vec4IO<DT>::load(a.bias, tid / 4)[tid % 4] : 0.0f;
+  __syncthreads();
+
+  const __amdgpu_buffer_rsrc_t rs0 = ig_rsrc(a.src[0], a.src_bytes[0]);
+  const __amdgpu_buffer_rsrc_t rs1 = ig_rsrc(a.src[1], a.src_bytes[1]);
+  const Act actp = act_params(a.act);
+
+  // this workgroup's contiguous range of blocks (ranges go out XCD by XCD so
+  // neighbouring blocks, which share input rows, meet in one L2)
+  const uint32_t g = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t b_begin = (uint32_t)(((uint64_t)g * a.nblk) / gridDim.x);
+  const uint32_t b_end = (uint32_t)(((uint64_t)(g + 1) * a.nblk) / gridDim.x);
+
+  // lane's weight operand of (tap, step, column block o) at Wl[wl + (tap*nj + step)*2*NC + o*32]
+  const uint32_t wl = lh * NC + l32;
+
+  for (uint32_t blk = b_begin + wave; blk < b_end; blk += kWaves) {
+    const uint32_t pix_out = blk * 32 + l32;
+    const bool valid = pix_out < a.M;
+    const uint32_t pp = valid ? pix_out : 0;
+    const uint32_t img = fdiv(pp, a.fd_ohw);
+    const uint32_t rem = pp - img * a.OHW;
+    const uint32_t oy = fdiv(rem, a.fd_ow);
+    const uint32_t ox = rem - oy * a.OW;
+    const int32_t iy0 = (int32_t)(oy * a.S) - a.PT, ix0 = (int32_t)(ox * a.S) - a.PL;
+    const uint32_t img_pix = img * a.IH * a.IW;
+
+    // the tap's NJM operand loads: unit 2(j - part start) + lh of step j's part
+    auto load_tap = [&](int tap, u32x4 (&x)[NJM]) {
+      const int32_t iy = iy0 + (int32_t)((tap / 3) * a.D), ix = ix0 + (int32_t)((tap % 3) * a.D);
+      const bool ok = valid && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
+      const uint32_t pix = img_pix + (uint32_t)iy * a.IW + (uint32_t)ix;
+      const uint32_t b0 = pix * a.stride_u[0] + a.off_u[0];
+      const uint32_t b1 = pix * a.stride_u[1] + a.off_u[1];
+#pragma unroll
+      for (int j = 0; j < NJM; ++j) {
+        x[j] = u32x4{0u, 0u, 0u, 0u};
+        if ((uint32_t)j >= nj) continue;
+        const bool p1 = (uint32_t)j >= nj0;
+        const uint32_t u = 2 * ((uint32_t)j - (p1 ? nj0 : 0u)) + lh;
+        const bool in = ok && u < (p1 ? a.nu[1] : a.nu[0]);
+        const uint32_t off = in ? ((p1 ? b1 : b0) + u) * 16u : kOob;
+        x[j] = __builtin_amdgcn_raw_buffer_load_b128(p1 ? rs1 : rs0, off, 0, 0);
+      }
+    };
+
+    f32x16 acc[NOB];
+#pragma unroll
+    for (int o = 0; o < NOB; ++o) acc[o] = f32x16{};
+    u32x4 xc[NJM], xn[NJM];
+    load_tap(0, xc);
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+      if (tap + 1 < 9) load_tap(tap + 1, xn);
+      const u32x4 *wt = Wl + wl + (uint32_t)tap * nj * 2 * NC;
+#pragma unroll
+      for (int j = 0; j < NJM; ++j) {
+        if ((uint32_t)j >= nj) break;
+#pragma unroll
+        for (int o = 0; o < NOB; ++o) {
+          const u32x4 wv = wt[j * 2 * NC + o * 32];
+          if constexpr (F32) {
+            const f32x4 w4 = __builtin_bit_cast(f32x4, wv), x4 = __builtin_bit_cast(f32x4, xc[j]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(w4[c], x4[c], acc[o], 0, 0, 0);
+          } else if constexpr (DT == DT_F16) {
+            acc[o] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wv),
+                                                           __builtin_bit_cast(f16x8, xc[j]), acc[o], 0, 0, 0);
+          } else {
+            acc[o] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wv),
+                                                            __builtin_bit_cast(bf16x8, xc[j]), acc[o], 0, 0, 0);
+          }
+        }
+      }
+      if (tap + 1 < 9) {
+#pragma unroll
+        for (int j = 0; j < NJM; ++j) xc[j] = xn[j];
+      }
+    }
+
+    if (!valid) continue;
+#pragma unroll
+    for (int o = 0; o < NOB; ++o) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t c = o * 32 + 8 * q + 4 * lh;
+        if (c >= a.N4) continue;
+        f32x4 v = f32x4{acc[o][4 * q], acc[o][4 * q + 1], acc[o][4 * q + 2], acc[o][4 * q + 3]} +
+                  *reinterpret_cast<const f32x4 *>(Bl + c);
+        v = act4(actp, v);
+        const size_t vi = (size_t)pix_out * (a.N4 / 4) + c / 4;
+        if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
+        Vec4IO<DT>::store(a.y, vi, v);
+      }
+    }
+  }
+}
+
+template <int DT, int NOB, int NJM>
+hipError_t launch_inst(const IgDirectArgs &a, hipStream_t st) {
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(conv_igemm_direct_kernel<DT, NOB, NJM>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (attr != hipSuccess) return attr;
+  const uint32_t lds = ig_direct_lds_bytes(a.nj, a.N4);
+  const uint32_t grid = ig_direct_grid(a.nblk, a.nj, a.N4);
+  hipLaunchKernelGGL((conv_igemm_direct_kernel<DT, NOB, NJM>), dim3(grid), dim3(kIgDirectThreads), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int DT, int NOB>
+hipError_t launch_nob(const IgDirectArgs &a, hipStream_t st) {
+  if (a.nj <= 2) return launch_inst<DT, NOB, 2>(a, st);
+  if (a.nj <= 4) return launch_inst<DT, NOB, 4>(a, st);
+  return launch_inst<DT, NOB, 8>(a, st);
+}
+
+template <int DT>
+hipError_t launch_dt(const IgDirectArgs &a, hipStream_t st) {
+  return a.N4 <= 32 ? launch_nob<DT, 1>(a, st) : launch_nob<DT, 2>(a, st);
+}
+
+}  // namespace
+
+hipError_t launch_ig_direct(const IgDirectArgs &a, int dt, hipStream_t st) {
+  if (a.N4 == 0 || a.N4 > 64 || a.N4 % 4 || a.nj == 0 || a.nj > kIgDirectMaxSteps || a.nj0 > a.nj ||
+      ig_direct_lds_bytes(a.nj, a.N4) > 160u * 1024u)
+    return hipErrorInvalidValue;
+  switch (dt) {
+    case DT_F32: return launch_dt<DT_F32>(a, st);
+    case DT_F16: return launch_dt<DT_F16>(a, st);
+    case DT_BF16: return launch_dt<DT_BF16>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace aih

@@ -109,10 +109,43 @@ def test_forced_splitk_factor_is_honoured():
 def test_igemm_policy():
     big = conv.ConvIgemmSpec(ih=160, iw=288, cin=16, cout=32, k=3, s=2, pad=(1, 1, 1, 1), n=32)
     assert big.out_hw() == (80, 144)
+    # 3x3 with <= 64 outputs: the direct kernel, 8 blocks of 32 pixels per
+    # workgroup, two workgroups per CU (18.1 KB of LDS weights)
+    p = big.plan()
+    assert p.variant == conv.Variant.DIRECT and p.bm == 32 and p.bn == 32 and p.grid == 512 and p.ws_bytes == 0
+    big.variant = conv.Variant.TILE
     p = big.plan()
     assert p.variant == conv.Variant.TILE and p.bn == 32 and p.grid == 32 * 80 * 144 // 128
     deep = conv.ConvIgemmSpec(ih=9, iw=16, cin=128, cout=128, k=3, pad=(1, 1, 1, 1))
     assert deep.plan().variant == conv.Variant.SPLITK
+
+
+def test_igemm_direct_route_limits():
+    """Shapes the direct route leaves to the tiled GEMM: an odd kg count per
+    part at 16-bit storage, more than 64 outputs, a forced variant, a 5x5
+    kernel, more than 8 MFMA steps per tap, mixed storage."""
+    V, D = conv.Variant, conv.DType
+
+    def variant(**kw):
+        base = dict(ih=16, iw=16, cin=32, cout=32, k=3, pad=(1, 1, 1, 1))
+        base.update(kw)
+        return conv.ConvIgemmSpec(**base).plan().variant
+
+    assert variant() == V.DIRECT
+    assert variant(cin=12) == V.DIRECT
+    assert variant(cin=12, dt=D.F16) != V.DIRECT
+    assert variant(cin=128, dt=D.F16) == V.DIRECT
+    assert variant(cin=136, dt=D.F16) != V.DIRECT
+    assert variant(cin=64) == V.DIRECT
+    assert variant(cin=68) != V.DIRECT
+    assert variant(cout=64) == V.DIRECT
+    assert variant(cout=68) != V.DIRECT
+    assert variant(variant=V.TILE) == V.TILE
+    assert variant(splitk=2) == V.SPLITK
+    assert variant(k=5, pad=(2, 2, 2, 2)) != V.DIRECT
+    assert variant(wdt=D.F16) != V.DIRECT
+    assert variant(cin=72, srcs=[conv.SrcView(c=48), conv.SrcView(c=24)], dt=D.F16) == V.DIRECT
+    assert variant(cin=72, srcs=[conv.SrcView(c=48), conv.SrcView(c=24)]) != V.DIRECT  # 9 fp32 steps per tap
 
 
 def _expect_error(fn, fragment):

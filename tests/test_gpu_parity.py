@@ -286,6 +286,38 @@ def test_igemm_batch():
     check("igemm batch", res, F32)
 
 
+# ---------------------------------------------------------------- the 3x3 direct route (<= 64 outputs)
+
+# (ih, iw, cin or parts, cout, s, d, pad, act, residual, n, seed): every one is
+# routed to the direct kernel in all three dtypes -- odd unit counts per part
+# (a half-empty last step), output channels that do not fill a 32-column
+# block, two parts, stride 2, dilation 2, asymmetric padding, residual, a
+# ragged last block of 32 pixels, the largest K per tap
+IG_DIRECT = [
+    (20, 36, 16, 32, 1, 1, (1, 1, 1, 1), "relu", False, 2, 7501),
+    (21, 37, 32, 64, 2, 1, (0, 1, 1, 0), "hardswish", True, 1, 7502),
+    (16, 24, 24, 20, 1, 2, (2, 2, 2, 2), "sigmoid", False, 1, 7503),
+    (13, 19, 40, 48, 1, 1, (1, 1, 1, 1), "relu6", True, 3, 7504),
+    (24, 32, [32, 24], 32, 1, 1, (1, 1, 1, 1), "relu", False, 1, 7505),
+    (17, 29, [16, 8], 12, 2, 1, (1, 1, 1, 1), "none", True, 1, 7506),
+    (12, 20, 64, 64, 1, 1, (1, 1, 1, 1), "relu", False, 1, 7507),
+]
+
+
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("case", IG_DIRECT, ids=lambda c: str(c[-1]))
+def test_igemm_direct(case, dt):
+    """3x3, cout <= 64, same storage for activations and weights, whole
+    16-byte units per part: the direct route of aih_conv_igemm (weights in
+    LDS, activations straight into MFMA registers)."""
+    ih, iw, cin, cout, s, d, pad, act, with_res, n, seed = case
+    parts = cin if isinstance(cin, list) else None
+    res = G.run_igemm(ih, iw, sum(parts) if parts else cin, cout, 3, s, pad, act, with_res, dt, seed, n=n, d=d,
+                      parts=parts)
+    assert res.plan.variant == G.conv.Variant.DIRECT, res.plan
+    check(f"igemm direct dt{dt} {case}", res, dt)
+
+
 # ---------------------------------------------------------------- the stem (3x3 over <= 3 channels)
 
 STEM = [((160, 288, 3, 32, 2, (1, 1, 1, 1)), "relu", False, 3601, 2),
