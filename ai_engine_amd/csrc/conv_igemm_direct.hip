@@ -40,25 +40,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t ig_rsrc(const void *base, uint
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
 
-template <int DT, int NOB, int NJM>
+template <int DT, int NOB, int NJ, int D>
 __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgDirectArgs a) {
   constexpr bool F32 = DT == DT_F32;
   constexpr int NC = NOB * 32;  // weight columns in LDS
   extern __shared__ __align__(16) char lds[];
   u32x4 *Wl = reinterpret_cast<u32x4 *>(lds);
-  const uint32_t nj = a.nj, nj0 = a.nj0;
-  float *Bl = reinterpret_cast<float *>(lds + 9 * nj * 2 * NC * 16);
+  const uint32_t nj0 = a.nj0;
+  float *Bl = reinterpret_cast<float *>(lds + 9 * NJ * 2 * NC * 16);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, lh = lane >> 5;
 
   // ---- weights -> LDS as [tap][step][half][column] operands (zero padding) ----
-  const uint32_t nw = 9 * nj * 2 * NC;
-  for (uint32_t i = tid; i < nw; i += kIgDirectThreads) {
-    const uint32_t n = i % NC, r = i / NC, h = r & 1, r2 = r >> 1, j = r2 % nj, tap = r2 / nj;
+  // every thread issues all of its loads before its first LDS store, so the
+  // copy costs one memory latency
+  constexpr int NW = 9 * NJ * 2 * NC;
+  constexpr int PER = (NW + kIgDirectThreads - 1) / kIgDirectThreads;
+  static_assert(kIgDirectThreads % NC == 0, "column of an entry");
+  u32x4 wst[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint32_t i = tid + k * kIgDirectThreads;
+    const uint32_t n = i % NC, r = i / NC, h = r & 1, r2 = r >> 1, j = r2 % NJ, tap = r2 / NJ;
     const uint32_t p = j >= nj0 ? 1 : 0;
     const uint32_t u = 2 * (j - (p ? nj0 : 0)) + h;
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (u < a.nu[p] && n < a.N4) {
+    if ((NW % kIgDirectThreads == 0 || i < (uint32_t)NW) && u < a.nu[p] && n < a.N4) {
       if constexpr (F32) {
         const uint32_t kg = a.kg_first[p] + u;
         v = reinterpret_cast<const u32x4 *>(a.w)[(size_t)(tap * a.KGP + kg) * a.N4 + n];
@@ -70,7 +77,12 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
         v = u32x4{lo.x, lo.y, hi.x, hi.y};
       }
     }
-    Wl[i] = v;
+    wst[k] = v;
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint32_t i = tid + k * kIgDirectThreads;
+    if (NW % kIgDirectThreads == 0 || i < (uint32_t)NW) Wl[i] = wst[k];
   }
   if (tid < NC) Bl[tid] = (uint32_t)tid < a.N4 ? Vec4IO<DT>::load(a.bias, tid / 4)[tid % 4] : 0.0f;
   __syncthreads();
@@ -85,108 +97,173 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
   const uint32_t b_begin = (uint32_t)(((uint64_t)g * a.nblk) / gridDim.x);
   const uint32_t b_end = (uint32_t)(((uint64_t)(g + 1) * a.nblk) / gridDim.x);
 
-  // lane's weight operand of (tap, step, column block o) at Wl[wl + (tap*nj + step)*2*NC + o*32]
+  // lane's weight operand of (tap, step, column block o) at Wl[wl + (tap*NJ + step)*2*NC + o*32]
   const uint32_t wl = lh * NC + l32;
 
-  for (uint32_t blk = b_begin + wave; blk < b_end; blk += kWaves) {
-    const uint32_t pix_out = blk * 32 + l32;
-    const bool valid = pix_out < a.M;
-    const uint32_t pp = valid ? pix_out : 0;
+  // a block's output pixels decoded: lane pixel, its tap-(0, 0) source row and
+  // column, and the unit index (per part) of that source pixel
+  struct Blk {
+    uint32_t pix_out, b0, b1;
+    int32_t iy0, ix0;
+    bool valid;
+  };
+  auto decode = [&](uint32_t blk) {
+    Blk b;
+    b.pix_out = blk * 32 + l32;
+    b.valid = b.pix_out < a.M;
+    const uint32_t pp = b.valid ? b.pix_out : 0;
     const uint32_t img = fdiv(pp, a.fd_ohw);
     const uint32_t rem = pp - img * a.OHW;
     const uint32_t oy = fdiv(rem, a.fd_ow);
     const uint32_t ox = rem - oy * a.OW;
-    const int32_t iy0 = (int32_t)(oy * a.S) - a.PT, ix0 = (int32_t)(ox * a.S) - a.PL;
-    const uint32_t img_pix = img * a.IH * a.IW;
-
-    // the tap's NJM operand loads: unit 2(j - part start) + lh of step j's part
-    auto load_tap = [&](int tap, u32x4 (&x)[NJM]) {
-      const int32_t iy = iy0 + (int32_t)((tap / 3) * a.D), ix = ix0 + (int32_t)((tap % 3) * a.D);
-      const bool ok = valid && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
-      const uint32_t pix = img_pix + (uint32_t)iy * a.IW + (uint32_t)ix;
-      const uint32_t b0 = pix * a.stride_u[0] + a.off_u[0];
-      const uint32_t b1 = pix * a.stride_u[1] + a.off_u[1];
+    b.iy0 = (int32_t)(oy * a.S) - a.PT;
+    b.ix0 = (int32_t)(ox * a.S) - a.PL;
+    // wraps (unsigned) when the tap-(0, 0) pixel lies above or left of the
+    // image; tap offsets bring in-image taps back, the others are not read
+    const uint32_t pix = (img * a.IH + (uint32_t)b.iy0) * a.IW + (uint32_t)b.ix0;
+    b.b0 = pix * a.stride_u[0] + a.off_u[0];
+    b.b1 = pix * a.stride_u[1] + a.off_u[1];
+    return b;
+  };
+  // a lane's source of one tap: both parts' unit index of its pixel, or
+  // ok = false (outside the image, or no pixel) for zeros
+  struct TapSrc {
+    uint32_t b0, b1;
+    bool ok;
+  };
+  auto tap_src = [&](const Blk &b, int tap) {
+    TapSrc t;
+    const uint32_t dy = (tap / 3) * a.D, dx = (tap % 3) * a.D;
+    t.ok = b.valid && (uint32_t)(b.iy0 + (int32_t)dy) < a.IH && (uint32_t)(b.ix0 + (int32_t)dx) < a.IW;
+    const uint32_t dpix = dy * a.IW + dx;
+    t.b0 = b.b0 + dpix * a.stride_u[0];
+    t.b1 = b.b1 + dpix * a.stride_u[1];
+    return t;
+  };
+  // the MFMA operand of step j: unit 2(j - part start) + lh of step j's part
+  auto load_step = [&](const TapSrc &t, int j) {
+    const bool p1 = (uint32_t)j >= nj0;
+    const uint32_t u = 2 * ((uint32_t)j - (p1 ? nj0 : 0u)) + lh;
+    const bool in = t.ok && u < (p1 ? a.nu[1] : a.nu[0]);
+    const uint32_t off = in ? ((p1 ? t.b1 : t.b0) + u) * 16u : kOob;
+    return __builtin_amdgcn_raw_buffer_load_b128(p1 ? rs1 : rs0, off, 0, 0);
+  };
+  // the lane's weight operands of step s (tap s / NJ, step s % NJ); wlo is
+  // wl passed through an empty asm once per block, so the compiler cannot
+  // hoist the (loop-invariant) reads out of the block loop into registers
+  uint32_t wlo = wl;
+  auto load_w = [&](int s, u32x4 (&w)[NOB]) {
 #pragma unroll
-      for (int j = 0; j < NJM; ++j) {
-        x[j] = u32x4{0u, 0u, 0u, 0u};
-        if ((uint32_t)j >= nj) continue;
-        const bool p1 = (uint32_t)j >= nj0;
-        const uint32_t u = 2 * ((uint32_t)j - (p1 ? nj0 : 0u)) + lh;
-        const bool in = ok && u < (p1 ? a.nu[1] : a.nu[0]);
-        const uint32_t off = in ? ((p1 ? b1 : b0) + u) * 16u : kOob;
-        x[j] = __builtin_amdgcn_raw_buffer_load_b128(p1 ? rs1 : rs0, off, 0, 0);
-      }
-    };
+    for (int o = 0; o < NOB; ++o) w[o] = Wl[wlo + s * 2 * NC + o * 32];
+  };
 
+  // Software pipeline over the 9 * NJ MFMA steps of each block: a ring of D
+  // operand registers (D divides 9 * NJ, so step s of every block uses slot
+  // s % D); right after step s's MFMAs its slot is refilled with step s + D
+  // -- of the next block for the last D steps -- so D - 1 steps of MFMAs
+  // cover every load, across block ends too. Within a block the weights of
+  // step s + 1 are read from LDS before step s's MFMAs.
+  constexpr int NS = 9 * NJ;
+  static_assert(NS % D == 0, "operand ring");
+  uint32_t blk = b_begin + wave;
+  if (blk >= b_end) return;
+  Blk cur = decode(blk);
+  u32x4 x[D];
+  TapSrc ts = tap_src(cur, 0);
+#pragma unroll
+  for (int s = 0; s < D; ++s) {
+    if (s > 0 && s % NJ == 0) ts = tap_src(cur, s / NJ);
+    x[s] = load_step(ts, s % NJ);
+  }
+  for (;;) {
+    __asm__ volatile("" : "+v"(wlo));
+    u32x4 wv[2][NOB];
+    load_w(0, wv[0]);
+    const uint32_t blk_next = blk + kWaves;
+    const bool more = blk_next < b_end;
+    const Blk nxt = decode(more ? blk_next : blk);
     f32x16 acc[NOB];
 #pragma unroll
     for (int o = 0; o < NOB; ++o) acc[o] = f32x16{};
-    u32x4 xc[NJM], xn[NJM];
-    load_tap(0, xc);
 #pragma unroll
-    for (int tap = 0; tap < 9; ++tap) {
-      if (tap + 1 < 9) load_tap(tap + 1, xn);
-      const u32x4 *wt = Wl + wl + (uint32_t)tap * nj * 2 * NC;
+    for (int s = 0; s < NS; ++s) {
+      if (s + 1 < NS) load_w(s + 1, wv[(s + 1) & 1]);
+      const u32x4 xs = x[s % D];
 #pragma unroll
-      for (int j = 0; j < NJM; ++j) {
-        if ((uint32_t)j >= nj) break;
+      for (int o = 0; o < NOB; ++o) {
+        const u32x4 w = wv[s & 1][o];
+        if constexpr (F32) {
+          const f32x4 w4 = __builtin_bit_cast(f32x4, w), x4 = __builtin_bit_cast(f32x4, xs);
 #pragma unroll
-        for (int o = 0; o < NOB; ++o) {
-          const u32x4 wv = wt[j * 2 * NC + o * 32];
-          if constexpr (F32) {
-            const f32x4 w4 = __builtin_bit_cast(f32x4, wv), x4 = __builtin_bit_cast(f32x4, xc[j]);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(w4[c], x4[c], acc[o], 0, 0, 0);
-          } else if constexpr (DT == DT_F16) {
-            acc[o] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, wv),
-                                                           __builtin_bit_cast(f16x8, xc[j]), acc[o], 0, 0, 0);
-          } else {
-            acc[o] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wv),
-                                                            __builtin_bit_cast(bf16x8, xc[j]), acc[o], 0, 0, 0);
-          }
+          for (int c = 0; c < 4; ++c) acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(w4[c], x4[c], acc[o], 0, 0, 0);
+        } else if constexpr (DT == DT_F16) {
+          acc[o] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, w), __builtin_bit_cast(f16x8, xs),
+                                                         acc[o], 0, 0, 0);
+        } else {
+          acc[o] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w),
+                                                          __builtin_bit_cast(bf16x8, xs), acc[o], 0, 0, 0);
         }
       }
-      if (tap + 1 < 9) {
-#pragma unroll
-        for (int j = 0; j < NJM; ++j) xc[j] = xn[j];
+      // refill: step s + D, a new tap's source when it starts one
+      const int sl = s + D;
+      if (sl < NS) {
+        if (sl % NJ == 0) ts = tap_src(cur, sl / NJ);
+        x[s % D] = load_step(ts, sl % NJ);
+      } else if (more) {
+        if ((sl - NS) % NJ == 0) ts = tap_src(nxt, (sl - NS) / NJ);
+        x[s % D] = load_step(ts, (sl - NS) % NJ);
       }
+      // keep the scheduler from hoisting later steps' reads (registers)
+      __builtin_amdgcn_sched_barrier(0);
     }
 
-    if (!valid) continue;
+    if (cur.valid) {
 #pragma unroll
-    for (int o = 0; o < NOB; ++o) {
+      for (int o = 0; o < NOB; ++o) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t c = o * 32 + 8 * q + 4 * lh;
-        if (c >= a.N4) continue;
-        f32x4 v = f32x4{acc[o][4 * q], acc[o][4 * q + 1], acc[o][4 * q + 2], acc[o][4 * q + 3]} +
-                  *reinterpret_cast<const f32x4 *>(Bl + c);
-        v = act4(actp, v);
-        const size_t vi = (size_t)pix_out * (a.N4 / 4) + c / 4;
-        if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
-        Vec4IO<DT>::store(a.y, vi, v);
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t c = o * 32 + 8 * q + 4 * lh;
+          if (c >= a.N4) continue;
+          f32x4 v = f32x4{acc[o][4 * q], acc[o][4 * q + 1], acc[o][4 * q + 2], acc[o][4 * q + 3]} +
+                    *reinterpret_cast<const f32x4 *>(Bl + c);
+          v = act4(actp, v);
+          const size_t vi = (size_t)cur.pix_out * (a.N4 / 4) + c / 4;
+          if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
+          Vec4IO<DT>::store(a.y, vi, v);
+        }
       }
     }
+    if (!more) break;
+    blk = blk_next;
+    cur = nxt;
   }
 }
 
-template <int DT, int NOB, int NJM>
+template <int DT, int NOB, int NJ, int D>
 hipError_t launch_inst(const IgDirectArgs &a, hipStream_t st) {
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void *>(conv_igemm_direct_kernel<DT, NOB, NJM>),
+      hipFuncSetAttribute(reinterpret_cast<const void *>(conv_igemm_direct_kernel<DT, NOB, NJ, D>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (attr != hipSuccess) return attr;
   const uint32_t lds = ig_direct_lds_bytes(a.nj, a.N4);
   const uint32_t grid = ig_direct_grid(a.nblk, a.nj, a.N4);
-  hipLaunchKernelGGL((conv_igemm_direct_kernel<DT, NOB, NJM>), dim3(grid), dim3(kIgDirectThreads), lds, st, a);
+  hipLaunchKernelGGL((conv_igemm_direct_kernel<DT, NOB, NJ, D>), dim3(grid), dim3(kIgDirectThreads), lds, st, a);
   return hipGetLastError();
 }
 
 template <int DT, int NOB>
 hipError_t launch_nob(const IgDirectArgs &a, hipStream_t st) {
-  if (a.nj <= 2) return launch_inst<DT, NOB, 2>(a, st);
-  if (a.nj <= 4) return launch_inst<DT, NOB, 4>(a, st);
-  return launch_inst<DT, NOB, 8>(a, st);
+  switch (a.nj) {
+    case 1: return launch_inst<DT, NOB, 1, 9>(a, st);
+    case 2: return launch_inst<DT, NOB, 2, 9>(a, st);
+    case 3: return launch_inst<DT, NOB, 3, 9>(a, st);
+    case 4: return launch_inst<DT, NOB, 4, 9>(a, st);
+    case 5: return launch_inst<DT, NOB, 5, 9>(a, st);
+    case 6: return launch_inst<DT, NOB, 6, 9>(a, st);
+    case 7: return launch_inst<DT, NOB, 7, 9>(a, st);
+    case 8: return launch_inst<DT, NOB, 8, 9>(a, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int DT>

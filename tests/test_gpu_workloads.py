@@ -74,25 +74,30 @@ def test_skinny_960to160_b256():
     report(f"pw 960->160 10x18 b256 {plan}", err, 1e-4)
 
 
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
 @pytest.mark.parametrize("case", [(3, 32, 160, 288, 16, 32, 2), (4, 32, 80, 144, 32, 64, 1)],
                          ids=["3x3s2_16to32_160x288_b32", "3x3s1_32to64_80x144_b32"])
-def test_implicit_gemm_3x3(case):
+def test_implicit_gemm_3x3(case, dt):
+    """Full size, so every wavefront of the direct kernel runs several
+    32-pixel blocks (its loads for the next block overlap the current one's
+    MFMAs). 16-bit storage: inputs, weights and bias rounded to dt, checked
+    against the fp32 run on the unrounded values."""
     wid, n, ih, iw, cin, cout, s = case
     x = orc.xs32_fill(1000 * wid + 0, n * ih * iw * cin)
     wts = orc.gauss_fill(1000 * wid + 1, 0.0, float(np.sqrt(2.0 / (9 * cin))), cout * cin * 9)
     b = orc.gauss_fill(1000 * wid + 2, 0.0, 0.01, cout)
     spec = conv.ConvIgemmSpec(ih=ih, iw=iw, cin=cin, cout=cout, k=3, s=s, pad=(1, 1, 1, 1), act=conv.Activation.RELU,
-                              n=n)
+                              n=n, dt=conv.DType(dt))
     oh, ow = spec.out_hw()
-    wp, _ = orc.pack_weights_conv(wts, cout, cin, 3, 3, 4)
-    yd = G.poisoned(n * oh * ow * cout, F32)
-    spec.run([G.dev(orc.pack_nhwc(x, n, ih, iw, cin))], G.dev(wp), G.dev(orc.pack_bias(b, cout)), None, yd)
+    wp, _ = orc.pack_weights_conv(wts, cout, cin, 3, 3, 4, dt)
+    yd = G.poisoned(n * oh * ow * cout, dt)
+    spec.run([G.dev(orc.pack_nhwc(x, n, ih, iw, cin, dt))], G.dev(wp), G.dev(orc.pack_bias(b, cout, dt)), None, yd)
     torch.cuda.synchronize()
-    got = yd.cpu().numpy().reshape(n, -1)
+    got = orc.unpack_nhwc(G.host(yd, dt), n, oh, ow, cout, dt).reshape(n, -1)
     cc = orc.CpuConv(orc.conv2d(cin, cout, k=3, s=s, pad=1, act="relu"), ih, iw, wts, b)
     img = ih * iw * cin
     err = max(G.rel_err(got[i], cc.run(x[i * img:(i + 1) * img], 1, threads=8)) for i in sample_images(n))
-    report(f"igemm 3x3 s{s} {cin}->{cout} {ih}x{iw} b{n} {spec.plan()}", err, 1e-4)
+    report(f"igemm 3x3 s{s} {cin}->{cout} {ih}x{iw} b{n} dt{dt} {spec.plan()}", err, 1e-4 if dt == F32 else 2e-2)
 
 
 def oracle_weights(layers, wid):
