@@ -43,14 +43,16 @@ inline uint32_t ig_direct_lds_bytes(uint32_t nj, uint32_t N4) {
   return 9u * nj * 2u * nob * 32u * 16u + nob * 32u * 4u;
 }
 
-// Workgroups of a launch: one per 8 blocks, at most what stays resident --
-// two workgroups per CU when their LDS allows and the kernel keeps to 128
-// VGPRs (one 32-column block: <= 124), one otherwise (two blocks: 115-154).
+// Workgroups of a launch: one per 8 blocks, at most one per CU. A second
+// resident workgroup per CU (when registers and LDS allow it) measured
+// slower on every shape tried: its extra loads in flight contend for the
+// same caches (3x3 16 -> 32 stride 2 at 160x288 batch 32, fp32: 62.0 us
+// with two per CU, 57.6 us with one).
 inline uint32_t ig_direct_grid(uint32_t nblk, uint32_t nj, uint32_t N4) {
-  const uint32_t lds = ig_direct_lds_bytes(nj, N4);
-  const uint32_t occ = N4 <= 32 && lds * 2 <= 160u * 1024u ? 2u : 1u;
+  (void)nj;
+  (void)N4;
   const uint64_t want = ((uint64_t)nblk + kIgDirectThreads / 64 - 1) / (kIgDirectThreads / 64);
-  return (uint32_t)(want < 256ull * occ ? want : 256ull * occ);
+  return (uint32_t)(want < 256ull ? want : 256ull);
 }
 
 hipError_t launch_ig_direct(const IgDirectArgs &a, int dt, hipStream_t st);

@@ -109,10 +109,10 @@ def test_forced_splitk_factor_is_honoured():
 def test_igemm_policy():
     big = conv.ConvIgemmSpec(ih=160, iw=288, cin=16, cout=32, k=3, s=2, pad=(1, 1, 1, 1), n=32)
     assert big.out_hw() == (80, 144)
-    # 3x3 with <= 64 outputs: the direct kernel, 8 blocks of 32 pixels per
-    # workgroup, two workgroups per CU (18.1 KB of LDS weights)
+    # 3x3 with <= 64 outputs: the direct kernel, eight wavefronts of 32-pixel
+    # blocks per workgroup, one workgroup per CU
     p = big.plan()
-    assert p.variant == conv.Variant.DIRECT and p.bm == 32 and p.bn == 32 and p.grid == 512 and p.ws_bytes == 0
+    assert p.variant == conv.Variant.DIRECT and p.bm == 32 and p.bn == 32 and p.grid == 256 and p.ws_bytes == 0
     big.variant = conv.Variant.TILE
     p = big.plan()
     assert p.variant == conv.Variant.TILE and p.bn == 32 and p.grid == 32 * 80 * 144 // 128
