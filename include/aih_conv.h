@@ -65,14 +65,15 @@ enum aih_act {
 };
 
 /* Kernel variants chosen by the plan functions (a caller asks for the first
- * three; the pointwise plan also reports the last two). */
+ * three; the plans also report the last two). */
 enum aih_variant {
   AIH_VAR_AUTO = 0,    /* let the policy decide */
   AIH_VAR_TILE = 1,    /* one MFMA tile per workgroup over the whole K */
   AIH_VAR_SPLITK = 2,  /* K cut into chunks, fp32 partials reduced in a fixed order */
   AIH_VAR_ROWS = 3,    /* pointwise, ng == 1: one pixel per thread on the VALU */
-  AIH_VAR_DIRECT = 4   /* pointwise, short K, ng <= 16: 32 pixels per wavefront,
-                          operands from memory into MFMA registers */
+  AIH_VAR_DIRECT = 4   /* 32 pixels per wavefront, activations from memory into
+                          MFMA registers: pointwise with short K and ng <= 16;
+                          3x3 igemm with cout <= 64 (weights resident in LDS) */
 };
 
 /* Pointwise 1x1 conv GEMM: out[M, N] = act(in[M, K] x W[K, N] + bias) (+ res).
@@ -101,7 +102,13 @@ typedef struct {
 
 /* KxK implicit-GEMM conv (groups = 1). Mirrors ConvIgemmSpec (conv_igemm.rs:49-76)
  * plus a batch n; non-square kernels and anisotropic strides are rejected as in
- * ConvIgemmSpec::from_op (conv_igemm.rs:79-83). */
+ * ConvIgemmSpec::from_op (conv_igemm.rs:79-83). With AIH_VAR_AUTO and no
+ * forced split, a 3x3 conv with dt == wdt, cout <= 64, at most two input
+ * parts whose channel counts, offsets and pixel strides are whole 16-byte
+ * units (4 fp32 / 8 16-bit channels) and at most 8 MFMA steps per tap (64
+ * fp32 / 128 16-bit input channels) runs the direct kernel (plan variant
+ * AIH_VAR_DIRECT, no workspace); <= 3 input channels with 32 or 64 outputs
+ * run the stem kernel; everything else the tiled GEMM (TILE / SPLITK). */
 typedef struct {
   uint32_t n, ih, iw, cin, cout;
   uint32_t k, s, d;
