@@ -262,6 +262,34 @@ def time_launches(torch, stream, fn, reps: int, warm: int = 3) -> float:
     return ts[len(ts) // 2] / 1e3
 
 
+def time_graph(torch, fn, reps: int, warm: int = 3) -> float:
+    """Seconds per launch of fn(r, stream) with no host launch cost between
+    kernels: reps launches (rotating buffer sets) captured once into a HIP
+    graph, the graph replayed three times, the median replay / reps. Short
+    kernels timed one launch at a time also measure the host's launch path
+    (the Python descriptor, the plan call); this is the kernels' own rate."""
+    cap = torch.cuda.Stream()
+    for r in range(warm):
+        fn(r, cap)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        for r in range(reps):
+            fn(r, cap)
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    ts = []
+    for _ in range(3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(cur)
+        g.replay()
+        b.record(cur)
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) / 1e3 / reps)
+    del g
+    return sorted(ts)[1]
+
+
 def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
     res = {}
 
@@ -283,11 +311,14 @@ def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
         wt = rnd(cin * cout, scale=0.05)
         b = rnd(cout, scale=0.01)
         ws = torch.empty(max(plan.ws_bytes // 4, 1), device=dev)
-        t = time_launches(torch, stream, lambda r: spec.run(xs[r % S], wt, b, None, ys[r % S], ws, stream), reps)
+        t1 = time_launches(torch, stream, lambda r: spec.run(xs[r % S], wt, b, None, ys[r % S], ws, stream), reps)
+        t = time_graph(torch, lambda r, st: spec.run(xs[r % S], wt, b, None, ys[r % S], ws, st), reps)
         row = roof(fl, by, t, "f32")
-        row.update(splitk=plan.splitk, bn=plan.bn, grid=plan.grid, buffer_sets=S)
+        row.update(us_one_launch=t1 * 1e6, variant=conv.Variant(plan.variant).name, splitk=plan.splitk, bn=plan.bn,
+                   grid=plan.grid, buffer_sets=S)
         res[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
-        log(f"{name}: {row['us']:.2f} us {row['tflops']:.2f} TF {row['gbs']:.0f} GB/s frac {row['frac']:.3f}")
+        log(f"{name}: {row['us']:.2f} us ({t1 * 1e6:.2f} us one launch at a time) {row['tflops']:.2f} TF "
+            f"{row['gbs']:.0f} GB/s frac {row['frac']:.3f} {row['variant']}")
 
     def ig_case(name, n, ih, iw, cin, cout, s, act, reps=30):
         spec = conv.ConvIgemmSpec(ih=ih, iw=iw, cin=cin, cout=cout, k=3, s=s, pad=(1, 1, 1, 1), act=act, n=n)
@@ -302,11 +333,14 @@ def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
         wt = rnd(9 * cin * cout, scale=0.1)
         b = rnd(cout, scale=0.01)
         ws = torch.empty(max(plan.ws_bytes // 4, 1), device=dev)
-        t = time_launches(torch, stream, lambda r: spec.run([xs[r % S]], wt, b, None, ys[r % S], ws, stream), reps)
+        t1 = time_launches(torch, stream, lambda r: spec.run([xs[r % S]], wt, b, None, ys[r % S], ws, stream), reps)
+        t = time_graph(torch, lambda r, st: spec.run([xs[r % S]], wt, b, None, ys[r % S], ws, st), reps)
         row = roof(fl, by, t, "f32")
-        row.update(splitk=plan.splitk, bn=plan.bn, grid=plan.grid, buffer_sets=S)
+        row.update(us_one_launch=t1 * 1e6, variant=conv.Variant(plan.variant).name, splitk=plan.splitk, bn=plan.bn,
+                   grid=plan.grid, buffer_sets=S)
         res[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
-        log(f"{name}: {row['us']:.2f} us {row['tflops']:.2f} TF {row['gbs']:.0f} GB/s frac {row['frac']:.3f}")
+        log(f"{name}: {row['us']:.2f} us ({t1 * 1e6:.2f} us one launch at a time) {row['tflops']:.2f} TF "
+            f"{row['gbs']:.0f} GB/s frac {row['frac']:.3f} {row['variant']}")
 
     A = conv.Activation
     pw_case("pw_32to64_relu6_80x144", 1, 80, 144, 32, 64, A.RELU6, reps=200)
