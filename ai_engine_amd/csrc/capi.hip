@@ -451,8 +451,14 @@ int aih_conv_igemm_plan(const aih_igemm_desc *d, aih_plan *out) {
     if (!out) return fail("null plan");
     uint32_t oh, ow;
     if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
+    if (igemm_is_stem(d)) {
+      // the stem kernel: 32 pixels per wavefront, 4 wavefronts per workgroup
+      const uint64_t nblocks = ((uint64_t)d->n * oh * ow + 31) / 32;
+      *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->cout, (uint32_t)std::min<uint64_t>((nblocks + 3) / 4, 256u * 8u), 0};
+      return AIH_OK;
+    }
     aih::IgDirectArgs da;
-    if (!igemm_is_stem(d) && ig_direct_plan(d, oh, ow, &da)) {
+    if (ig_direct_plan(d, oh, ow, &da)) {
       *out = aih_plan{AIH_VAR_DIRECT, 1, 32, da.N4 <= 32 ? 32u : 64u, aih::ig_direct_grid(da.nblk, da.nj, da.N4), 0};
       return AIH_OK;
     }

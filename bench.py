@@ -243,7 +243,7 @@ def kernel_key(conv, op, n, dt, dtname) -> str:
         p = conv.ConvIgemmSpec(ih=Lr.ih, iw=Lr.iw, cin=Lr.cin, cout=Lr.cout, k=Lr.k, s=Lr.s, pad=(Lr.pad,) * 4,
                                dt=dt, n=n).plan()
         if p.variant == conv.Variant.DIRECT:
-            return f"conv_igemm_direct_kernel<{dtname}>"
+            return f"conv_stem_kernel<{dtname}>" if Lr.cin <= 3 else f"conv_igemm_direct_kernel<{dtname}>"
     key = f"conv_gemm_kernel<{dtname},{dtname},BN={p.bn},{'igemm' if Lr.k > 1 else 'pw'}>"
     return key + ("+splitk_reduce" if p.splitk > 1 else "")
 

@@ -73,7 +73,8 @@ enum aih_variant {
   AIH_VAR_ROWS = 3,    /* pointwise, ng == 1: one pixel per thread on the VALU */
   AIH_VAR_DIRECT = 4   /* 32 pixels per wavefront, activations from memory into
                           MFMA registers: pointwise with short K and ng <= 16;
-                          3x3 igemm with cout <= 64 (weights resident in LDS) */
+                          3x3 igemm with cout <= 64 (weights resident in LDS);
+                          the 3x3 stem over <= 3 input channels */
 };
 
 /* Pointwise 1x1 conv GEMM: out[M, N] = act(in[M, K] x W[K, N] + bias) (+ res).
@@ -107,8 +108,9 @@ typedef struct {
  * parts whose channel counts, offsets and pixel strides are whole 16-byte
  * units (4 fp32 / 8 16-bit channels) and at most 8 MFMA steps per tap (64
  * fp32 / 128 16-bit input channels) runs the direct kernel (plan variant
- * AIH_VAR_DIRECT, no workspace); <= 3 input channels with 32 or 64 outputs
- * run the stem kernel; everything else the tiled GEMM (TILE / SPLITK). */
+ * AIH_VAR_DIRECT, no workspace); <= 3 input channels of a dense input with
+ * d = 1 and 32 or 64 outputs run the stem kernel (also AIH_VAR_DIRECT);
+ * everything else the tiled GEMM (TILE / SPLITK). */
 typedef struct {
   uint32_t n, ih, iw, cin, cout;
   uint32_t k, s, d;

@@ -146,6 +146,9 @@ def test_igemm_direct_route_limits():
     assert variant(wdt=D.F16) != V.DIRECT
     assert variant(cin=72, srcs=[conv.SrcView(c=48), conv.SrcView(c=24)], dt=D.F16) == V.DIRECT
     assert variant(cin=72, srcs=[conv.SrcView(c=48), conv.SrcView(c=24)]) != V.DIRECT  # 9 fp32 steps per tap
+    # the stem route: <= 3 channels, 32 or 64 outputs (4 wavefronts of 32 pixels per workgroup)
+    stem = conv.ConvIgemmSpec(ih=160, iw=288, cin=3, cout=32, k=3, s=2, pad=(1, 1, 1, 1), n=64).plan()
+    assert stem.variant == V.DIRECT and stem.bn == 32 and stem.grid == 2048 and stem.ws_bytes == 0
 
 
 def _expect_error(fn, fragment):
