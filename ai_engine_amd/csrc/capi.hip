@@ -268,8 +268,8 @@ int plan_igemm(const aih_igemm_desc *d, GemmPlan *g) {
 // false when the call goes to the tiled GEMM: AIH_VAR_AUTO without a forced
 // split, a 3x3 kernel, the same storage for activations and weights, at most
 // 64 output channels, at most two input parts whose kg runs, pixel strides
-// and offsets are whole 16-byte units (two kg for 16-bit storage), at most 8
-// MFMA steps per tap and every part below 2 GiB.
+// and offsets are whole 16-byte units (two kg for 16-bit storage), at most 10
+// MFMA steps per tap, weights within LDS and every part below 2 GiB.
 bool ig_direct_plan(const aih_igemm_desc *d, uint32_t oh, uint32_t ow, aih::IgDirectArgs *a) {
   if (d->variant != AIH_VAR_AUTO || d->splitk != 0 || d->k != 3 || d->dt != d->wdt) return false;
   const uint32_t n4 = div_ceil(d->cout, 4) * 4;

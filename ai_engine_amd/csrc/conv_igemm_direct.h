@@ -32,9 +32,9 @@ struct IgDirectArgs {
 
 // Threads of one workgroup (the weights in LDS are shared by its wavefronts).
 constexpr uint32_t kIgDirectThreads = 512;
-// Most MFMA K steps per tap the kernel takes: 8 units of 16 bytes per lane
-// half (64 fp32 / 128 16-bit input channels).
-constexpr uint32_t kIgDirectMaxSteps = 8;
+// Most MFMA K steps per tap the kernel takes: 10 units of 16 bytes per lane
+// half (80 fp32 / 160 16-bit input channels).
+constexpr uint32_t kIgDirectMaxSteps = 10;
 
 // LDS bytes of a launch: the weights as [9][nj][2][NOB*32] 16-byte units,
 // then NOB*32 fp32 biases.

@@ -264,6 +264,8 @@ hipError_t launch_nob(const IgDirectArgs &a, hipStream_t st) {
     case 6: return launch_inst<DT, NOB, 6, 9>(a, st);
     case 7: return launch_inst<DT, NOB, 7, 9>(a, st);
     case 8: return launch_inst<DT, NOB, 8, 9>(a, st);
+    case 9: return launch_inst<DT, NOB, 9, 9>(a, st);
+    case 10: return launch_inst<DT, NOB, 10, 9>(a, st);
     default: return hipErrorInvalidValue;
   }
 }

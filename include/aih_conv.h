@@ -106,8 +106,9 @@ typedef struct {
  * ConvIgemmSpec::from_op (conv_igemm.rs:79-83). With AIH_VAR_AUTO and no
  * forced split, a 3x3 conv with dt == wdt, cout <= 64, at most two input
  * parts whose channel counts, offsets and pixel strides are whole 16-byte
- * units (4 fp32 / 8 16-bit channels) and at most 8 MFMA steps per tap (64
- * fp32 / 128 16-bit input channels) runs the direct kernel (plan variant
+ * units (4 fp32 / 8 16-bit channels), at most 10 MFMA steps per tap (80
+ * fp32 / 160 16-bit input channels) and 9 * K * N of weights within 160 KB of
+ * LDS runs the direct kernel (plan variant
  * AIH_VAR_DIRECT, no workspace); <= 3 input channels of a dense input with
  * d = 1 and 32 or 64 outputs run the stem kernel (also AIH_VAR_DIRECT);
  * everything else the tiled GEMM (TILE / SPLITK). */

@@ -123,7 +123,8 @@ def test_igemm_policy():
 def test_igemm_direct_route_limits():
     """Shapes the direct route leaves to the tiled GEMM: an odd kg count per
     part at 16-bit storage, more than 64 outputs, a forced variant, a 5x5
-    kernel, more than 8 MFMA steps per tap, mixed storage."""
+    kernel, more than 10 MFMA steps per tap, weights beyond 160 KB of LDS,
+    mixed storage."""
     V, D = conv.Variant, conv.DType
 
     def variant(**kw):
@@ -134,10 +135,11 @@ def test_igemm_direct_route_limits():
     assert variant() == V.DIRECT
     assert variant(cin=12) == V.DIRECT
     assert variant(cin=12, dt=D.F16) != V.DIRECT
-    assert variant(cin=128, dt=D.F16) == V.DIRECT
-    assert variant(cin=136, dt=D.F16) != V.DIRECT
-    assert variant(cin=64) == V.DIRECT
-    assert variant(cin=68) != V.DIRECT
+    assert variant(cin=160, dt=D.F16) == V.DIRECT
+    assert variant(cin=168, dt=D.F16) != V.DIRECT
+    assert variant(cin=80) == V.DIRECT
+    assert variant(cin=84) != V.DIRECT
+    assert variant(cin=72, cout=64) != V.DIRECT  # 9 x 9 x 2 x 64 x 16 B of weights > 160 KB
     assert variant(cout=64) == V.DIRECT
     assert variant(cout=68) != V.DIRECT
     assert variant(variant=V.TILE) == V.TILE
@@ -145,7 +147,7 @@ def test_igemm_direct_route_limits():
     assert variant(k=5, pad=(2, 2, 2, 2)) != V.DIRECT
     assert variant(wdt=D.F16) != V.DIRECT
     assert variant(cin=72, srcs=[conv.SrcView(c=48), conv.SrcView(c=24)], dt=D.F16) == V.DIRECT
-    assert variant(cin=72, srcs=[conv.SrcView(c=48), conv.SrcView(c=24)]) != V.DIRECT  # 9 fp32 steps per tap
+    assert variant(cin=72, srcs=[conv.SrcView(c=48), conv.SrcView(c=24)]) == V.DIRECT  # 6 + 3 fp32 steps per tap
     # the stem route: <= 3 channels, 32 or 64 outputs (4 wavefronts of 32 pixels per workgroup)
     stem = conv.ConvIgemmSpec(ih=160, iw=288, cin=3, cout=32, k=3, s=2, pad=(1, 1, 1, 1), n=64).plan()
     assert stem.variant == V.DIRECT and stem.bn == 32 and stem.grid == 2048 and stem.ws_bytes == 0

@@ -301,6 +301,8 @@ IG_DIRECT = [
     (24, 32, [32, 24], 32, 1, 1, (1, 1, 1, 1), "relu", False, 1, 7505),
     (17, 29, [16, 8], 12, 2, 1, (1, 1, 1, 1), "none", True, 1, 7506),
     (12, 20, 64, 64, 1, 1, (1, 1, 1, 1), "relu", False, 1, 7507),
+    (10, 14, 80, 32, 1, 1, (1, 1, 1, 1), "hardswish", True, 2, 7508),
+    (14, 18, [48, 24], 28, 1, 1, (1, 1, 1, 1), "relu", False, 1, 7509),
 ]
 
 
@@ -316,6 +318,15 @@ def test_igemm_direct(case, dt):
                       parts=parts)
     assert res.plan.variant == G.conv.Variant.DIRECT, res.plan
     check(f"igemm direct dt{dt} {case}", res, dt)
+
+
+@pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
+def test_igemm_direct_10_steps_16bit(dt):
+    """160 16-bit input channels: 10 MFMA steps per tap, the most the direct
+    route takes (fp32 stops at 80 channels)."""
+    res = G.run_igemm(9, 11, 160, 24, 3, 1, [1, 1, 1, 1], "relu", True, dt, 7510)
+    assert res.plan.variant == G.conv.Variant.DIRECT, res.plan
+    check(f"igemm direct 160->24 dt{dt}", res, dt)
 
 
 # ---------------------------------------------------------------- the stem (3x3 over <= 3 channels)
