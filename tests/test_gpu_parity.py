@@ -320,6 +320,30 @@ def test_igemm_direct(case, dt):
     check(f"igemm direct dt{dt} {case}", res, dt)
 
 
+@pytest.mark.parametrize("dt", [F32, F16], ids=["f32", "f16"])
+def test_igemm_direct_channel_view(dt):
+    """One input part that is a channel view (channels 8..31 of a 48-channel
+    tensor, SrcView{c: 24, stride_c: 48, c_off: 8}): the direct route reads the
+    view through its pixel stride and offset; checked against the oracle on
+    the sliced input."""
+    ih, iw, full, c0, c, cout, seed = 15, 21, 48, 8, 24, 20, 7511
+    op = G.orc.conv2d(c, cout, k=3, s=1, pad=[1, 1, 1, 1], act="relu")
+    xf, wts, b = G.stream(seed, ih * iw * full, cout * c * 9, cout)
+    xs = xf.reshape(ih * iw, full)[:, c0:c0 + c].ravel().copy()
+    want = G.orc.conv2d_ref(op, ih, iw, xs, wts, b, None)
+    wp, _ = G.orc.pack_weights_conv(wts, cout, c, 3, 3, 4, dt)
+    spec = G.conv.ConvIgemmSpec(ih=ih, iw=iw, cin=c, cout=cout, k=3, pad=(1, 1, 1, 1), act=G.ACT["relu"],
+                                dt=G.conv.DType(dt), srcs=[G.conv.SrcView(c=c, stride_c=full, c_off=c0)])
+    assert spec.plan().variant == G.conv.Variant.DIRECT
+    yd = G.poisoned(ih * iw * 20, dt)
+    spec.run([G.dev(G.orc.pack_nhwc(xf, 1, ih, iw, full, dt))], G.dev(wp), G.dev(G.orc.pack_bias(b, cout, dt)), None, yd)
+    torch.cuda.synchronize()
+    got = G.orc.unpack_nhwc(G.host(yd, dt), 1, ih, iw, cout, dt)
+    err = G.rel_err(got, want)
+    print(f"igemm direct channel view dt{dt}: max_rel_err={err:.3e}", flush=True)
+    assert err <= (1e-4 if dt == F32 else 2e-2), err
+
+
 @pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
 def test_igemm_direct_10_steps_16bit(dt):
     """160 16-bit input channels: 10 MFMA steps per tap, the most the direct
