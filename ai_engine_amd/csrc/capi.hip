@@ -153,12 +153,53 @@ void fill_plan(const GemmPlan &g, aih_plan *out) {
 // one output channel group goes to the one-pixel-per-thread kernel and short
 // K with at most 64 output channels (same storage for activations and
 // weights) to the direct MFMA kernel; everything else to the tiled GEMM.
-enum { PW_TILED = 0, PW_ROWS = 1, PW_DIRECT = 2 };
+enum { PW_TILED = 0, PW_ROWS = 1, PW_DIRECT = 2, PW_LDS = 3 };
+
+// The pointwise call as a one-tap launch of the direct 3x3 kernel (weights
+// resident in LDS, activations straight into MFMA registers): K beyond the
+// register-operand kernel's reach, <= 64 output channels, a kg count in whole
+// 16-byte units, at most 32 MFMA steps (256 fp32 / 512 16-bit channels), and
+// enough 32-pixel blocks (>= 2048) that the launch fills every CU without
+// splitting K.
+bool pw_lds_plan(const aih_pw_desc *d, aih::IgDirectArgs *a) {
+  const uint32_t ku = d->dt == AIH_F32 ? 1 : 2, es = d->dt == AIH_F32 ? 4 : 2;
+  const uint64_t M = (uint64_t)d->n * d->m;
+  if (d->dt != d->wdt || d->ng < 2 || d->ng * 4 > 64 || d->kg % ku || M < 2048ull * 32 || M > 0xffffff00ull)
+    return false;
+  const uint64_t bytes = M * d->kg * 4 * es;
+  if (bytes >= 0x80000000ull) return false;
+  const uint32_t nu = d->kg / ku, nj = div_ceil(nu, 2);
+  if (aih::pw_lds_steps(nj) == 0 || aih::ig_direct_lds_bytes(1, nj, d->ng * 4) > 160u * 1024u) return false;
+  std::memset(a, 0, sizeof(*a));
+  a->src_bytes[0] = a->src_bytes[1] = (uint32_t)bytes;
+  a->stride_u[0] = a->stride_u[1] = nu;
+  a->nu[0] = nu;
+  a->nj0 = a->nj = nj;
+  a->taps = 1;
+  a->KGP = d->kg_pad;
+  a->N4 = d->ng * 4;
+  a->M = (uint32_t)M;
+  a->OHW = d->m;
+  a->OW = d->m;
+  a->IH = 1;
+  a->IW = d->m;
+  a->S = 1;
+  a->D = 1;
+  a->nblk = (uint32_t)((M + 31) / 32);
+  a->act = d->act;
+  a->has_res = d->residual ? 1 : 0;
+  a->fd_ohw = aih::make_fastdiv(d->m);
+  a->fd_ow = aih::make_fastdiv(d->m);
+  return true;
+}
+
 int pw_route(const aih_pw_desc *d) {
   if (d->variant != AIH_VAR_AUTO || d->splitk != 0) return PW_TILED;
   if (d->ng == 1 && d->kg <= aih::kPwNarrowMaxKG) return PW_ROWS;
   const uint32_t kmax = d->dt == AIH_F32 ? aih::kPwDirectMaxK32 : aih::kPwDirectMaxK16;
   if (d->dt == d->wdt && d->ng >= 2 && d->ng * 4 <= aih::kPwDirectMaxN4 && d->kg * 4 <= kmax) return PW_DIRECT;
+  aih::IgDirectArgs a;
+  if (pw_lds_plan(d, &a)) return PW_LDS;
   return PW_TILED;
 }
 
@@ -299,8 +340,9 @@ bool ig_direct_plan(const aih_igemm_desc *d, uint32_t oh, uint32_t ow, aih::IgDi
     a->src_bytes[1] = a->src_bytes[0];
     a->stride_u[1] = a->stride_u[0];
   }
-  if (nj == 0 || nj > aih::kIgDirectMaxSteps || aih::ig_direct_lds_bytes(nj, n4) > 160u * 1024u) return false;
+  if (nj == 0 || nj > aih::kIgDirectMaxSteps || aih::ig_direct_lds_bytes(9, nj, n4) > 160u * 1024u) return false;
   a->nj = nj;
+  a->taps = 9;
   a->KGP = div_ceil(div_ceil(d->cin, 4), 4) * 4;
   a->N4 = n4;
   a->M = d->n * oh * ow;
@@ -373,6 +415,12 @@ int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out) {
       case PW_ROWS:
         *out = aih_plan{AIH_VAR_ROWS, 1, 256, 4, (uint32_t)std::min<uint64_t>((M + 255) / 256, 4096), 0};
         return AIH_OK;
+      case PW_LDS: {
+        aih::IgDirectArgs a;
+        pw_lds_plan(d, &a);
+        *out = aih_plan{AIH_VAR_DIRECT, 1, 32, a.N4 <= 32 ? 32u : 64u, aih::ig_direct_grid(a.nblk, a.nj, a.N4), 0};
+        return AIH_OK;
+      }
       case PW_DIRECT:
         *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->ng * 4 <= 32 ? 32u : 64u,
                         (uint32_t)std::min<uint64_t>((M + 127) / 128, 256u * 8u), 0};
@@ -403,6 +451,18 @@ int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *
       aih::PwNarrowArgs na{x, w, bias, res, y, (uint32_t)M, d->kg, d->kg, d->act, d->residual ? 1 : 0};
       const hipError_t e = aih::launch_pw_narrow(na, d->dt, d->wdt, static_cast<hipStream_t>(stream));
       return e == hipSuccess ? AIH_OK : fail(std::string("pw narrow launch: ") + hipGetErrorString(e));
+    }
+    if (route == PW_LDS) {
+      // mid-size K, <= 64 output channels: the direct kernel with one tap
+      aih::IgDirectArgs a;
+      pw_lds_plan(d, &a);
+      a.src[0] = a.src[1] = x;
+      a.w = w;
+      a.bias = bias;
+      a.res = res;
+      a.y = y;
+      const hipError_t e = aih::launch_ig_direct(a, d->dt, static_cast<hipStream_t>(stream));
+      return e == hipSuccess ? AIH_OK : fail(std::string("pw lds-direct launch: ") + hipGetErrorString(e));
     }
     if (route == PW_DIRECT) {
       // short K and at most 64 output channels: operands from memory straight

@@ -18,6 +18,7 @@ struct IgDirectArgs {
   uint32_t nu[2];          // 16-byte units of each part per pixel
   uint32_t kg_first[2];    // first kg (of the packed weights) of each part
   uint32_t nj0, nj;        // MFMA K steps per tap: of part 0, of all parts
+  uint32_t taps;           // 9 (3x3) or 1 (1x1: the pointwise route)
   const void *w;           // packed [9][KGP][N4][4]
   const void *bias;        // [N4]
   const void *res;         // like y, or null
@@ -36,11 +37,22 @@ constexpr uint32_t kIgDirectThreads = 512;
 // half (80 fp32 / 160 16-bit input channels).
 constexpr uint32_t kIgDirectMaxSteps = 10;
 
-// LDS bytes of a launch: the weights as [9][nj][2][NOB*32] 16-byte units,
-// then NOB*32 fp32 biases.
-inline uint32_t ig_direct_lds_bytes(uint32_t nj, uint32_t N4) {
+// Step counts of the pointwise (1x1) instantiations: a call runs the
+// smallest one that holds its steps (the extra steps read zero weights and
+// activations).
+constexpr uint32_t kPwLdsSteps[4] = {12, 16, 24, 32};
+inline uint32_t pw_lds_steps(uint32_t nj) {
+  for (uint32_t s : kPwLdsSteps)
+    if (nj <= s) return s;
+  return 0;
+}
+
+// LDS bytes of a launch: the weights as [taps][nj][2][NOB*32] 16-byte units,
+// then NOB*32 fp32 biases (nj: the instantiation's steps per tap).
+inline uint32_t ig_direct_lds_bytes(uint32_t taps, uint32_t nj, uint32_t N4) {
   const uint32_t nob = N4 <= 32 ? 1u : 2u;
-  return 9u * nj * 2u * nob * 32u * 16u + nob * 32u * 4u;
+  if (taps == 1) nj = pw_lds_steps(nj);
+  return taps * nj * 2u * nob * 32u * 16u + nob * 32u * 4u;
 }
 
 // Workgroups of a launch: one per 8 blocks, at most one per CU. A second

@@ -40,21 +40,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t ig_rsrc(const void *base, uint
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
 
-template <int DT, int NOB, int NJ, int D>
+template <int DT, int NOB, int TAPS, int NJ, int D>
 __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgDirectArgs a) {
   constexpr bool F32 = DT == DT_F32;
   constexpr int NC = NOB * 32;  // weight columns in LDS
   extern __shared__ __align__(16) char lds[];
   u32x4 *Wl = reinterpret_cast<u32x4 *>(lds);
   const uint32_t nj0 = a.nj0;
-  float *Bl = reinterpret_cast<float *>(lds + 9 * NJ * 2 * NC * 16);
+  float *Bl = reinterpret_cast<float *>(lds + TAPS * NJ * 2 * NC * 16);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, lh = lane >> 5;
 
   // ---- weights -> LDS as [tap][step][half][column] operands (zero padding) ----
   // every thread issues all of its loads before its first LDS store, so the
   // copy costs one memory latency
-  constexpr int NW = 9 * NJ * 2 * NC;
+  constexpr int NW = TAPS * NJ * 2 * NC;
   constexpr int PER = (NW + kIgDirectThreads - 1) / kIgDirectThreads;
   static_assert(kIgDirectThreads % NC == 0, "column of an entry");
   u32x4 wst[PER];
@@ -157,13 +157,13 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
     for (int o = 0; o < NOB; ++o) w[o] = Wl[wlo + s * 2 * NC + o * 32];
   };
 
-  // Software pipeline over the 9 * NJ MFMA steps of each block: a ring of D
-  // operand registers (D divides 9 * NJ, so step s of every block uses slot
+  // Software pipeline over the TAPS * NJ MFMA steps of each block: a ring of D
+  // operand registers (D divides TAPS * NJ, so step s of every block uses slot
   // s % D); right after step s's MFMAs its slot is refilled with step s + D
   // -- of the next block for the last D steps -- so D - 1 steps of MFMAs
   // cover every load, across block ends too. Within a block the weights of
   // step s + 1 are read from LDS before step s's MFMAs.
-  constexpr int NS = 9 * NJ;
+  constexpr int NS = TAPS * NJ;
   static_assert(NS % D == 0, "operand ring");
   uint32_t blk = b_begin + wave;
   if (blk >= b_end) return;
@@ -239,15 +239,15 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
   }
 }
 
-template <int DT, int NOB, int NJ, int D>
+template <int DT, int NOB, int TAPS, int NJ, int D>
 hipError_t launch_inst(const IgDirectArgs &a, hipStream_t st) {
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void *>(conv_igemm_direct_kernel<DT, NOB, NJ, D>),
+      hipFuncSetAttribute(reinterpret_cast<const void *>(conv_igemm_direct_kernel<DT, NOB, TAPS, NJ, D>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (attr != hipSuccess) return attr;
-  const uint32_t lds = ig_direct_lds_bytes(a.nj, a.N4);
+  const uint32_t lds = ig_direct_lds_bytes(TAPS, a.nj, a.N4);
   const uint32_t grid = ig_direct_grid(a.nblk, a.nj, a.N4);
-  hipLaunchKernelGGL((conv_igemm_direct_kernel<DT, NOB, NJ, D>), dim3(grid), dim3(kIgDirectThreads), lds, st, a);
+  hipLaunchKernelGGL((conv_igemm_direct_kernel<DT, NOB, TAPS, NJ, D>), dim3(grid), dim3(kIgDirectThreads), lds, st, a);
   return hipGetLastError();
 }
 
@@ -255,17 +255,27 @@ template <int DT, int NOB>
 hipError_t launch_nob(const IgDirectArgs &a, hipStream_t st) {
   // operand ring depth D (a divisor of 9 * NJ): 6 / 9 / 12 steps, measured
   // against 3 and 18 on the 16 -> 32 and 32 -> 32 / 64 shapes
+  if (a.taps == 1) {
+    // 1x1: the steps run up to the instantiation's count (ring 12 / 8 deep)
+    switch (pw_lds_steps(a.nj)) {
+      case 12: return launch_inst<DT, NOB, 1, 12, 12>(a, st);
+      case 16: return launch_inst<DT, NOB, 1, 16, 8>(a, st);
+      case 24: return launch_inst<DT, NOB, 1, 24, 12>(a, st);
+      case 32: return launch_inst<DT, NOB, 1, 32, 8>(a, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (a.nj) {
-    case 1: return launch_inst<DT, NOB, 1, 9>(a, st);
-    case 2: return launch_inst<DT, NOB, 2, 6>(a, st);
-    case 3: return launch_inst<DT, NOB, 3, 9>(a, st);
-    case 4: return launch_inst<DT, NOB, 4, 12>(a, st);
-    case 5: return launch_inst<DT, NOB, 5, 9>(a, st);
-    case 6: return launch_inst<DT, NOB, 6, 9>(a, st);
-    case 7: return launch_inst<DT, NOB, 7, 9>(a, st);
-    case 8: return launch_inst<DT, NOB, 8, 9>(a, st);
-    case 9: return launch_inst<DT, NOB, 9, 9>(a, st);
-    case 10: return launch_inst<DT, NOB, 10, 9>(a, st);
+    case 1: return launch_inst<DT, NOB, 9, 1, 9>(a, st);
+    case 2: return launch_inst<DT, NOB, 9, 2, 6>(a, st);
+    case 3: return launch_inst<DT, NOB, 9, 3, 9>(a, st);
+    case 4: return launch_inst<DT, NOB, 9, 4, 12>(a, st);
+    case 5: return launch_inst<DT, NOB, 9, 5, 9>(a, st);
+    case 6: return launch_inst<DT, NOB, 9, 6, 9>(a, st);
+    case 7: return launch_inst<DT, NOB, 9, 7, 9>(a, st);
+    case 8: return launch_inst<DT, NOB, 9, 8, 9>(a, st);
+    case 9: return launch_inst<DT, NOB, 9, 9, 9>(a, st);
+    case 10: return launch_inst<DT, NOB, 9, 10, 9>(a, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -278,8 +288,9 @@ hipError_t launch_dt(const IgDirectArgs &a, hipStream_t st) {
 }  // namespace
 
 hipError_t launch_ig_direct(const IgDirectArgs &a, int dt, hipStream_t st) {
-  if (a.N4 == 0 || a.N4 > 64 || a.N4 % 4 || a.nj == 0 || a.nj > kIgDirectMaxSteps || a.nj0 > a.nj ||
-      ig_direct_lds_bytes(a.nj, a.N4) > 160u * 1024u)
+  if (a.N4 == 0 || a.N4 > 64 || a.N4 % 4 || a.nj == 0 || a.nj0 > a.nj || (a.taps != 1 && a.taps != 9) ||
+      (a.taps == 9 && a.nj > kIgDirectMaxSteps) || (a.taps == 1 && pw_lds_steps(a.nj) == 0) ||
+      ig_direct_lds_bytes(a.taps, a.nj, a.N4) > 160u * 1024u)
     return hipErrorInvalidValue;
   switch (dt) {
     case DT_F32: return launch_dt<DT_F32>(a, st);
