@@ -72,8 +72,10 @@ enum aih_variant {
   AIH_VAR_SPLITK = 2,  /* K cut into chunks, fp32 partials reduced in a fixed order */
   AIH_VAR_ROWS = 3,    /* pointwise, ng == 1: one pixel per thread on the VALU */
   AIH_VAR_DIRECT = 4   /* 32 pixels per wavefront, activations from memory into
-                          MFMA registers: pointwise with short K and ng <= 16;
-                          3x3 igemm with cout <= 64 (weights resident in LDS);
+                          MFMA registers: pointwise with ng <= 16 (short K:
+                          weights in registers; K up to 256 fp32 / 512 16-bit
+                          channels over >= 2048 pixel blocks: weights resident
+                          in LDS); 3x3 igemm with cout <= 64 (weights in LDS);
                           the 3x3 stem over <= 3 input channels */
 };
 
