@@ -156,26 +156,32 @@ void fill_plan(const GemmPlan &g, aih_plan *out) {
 enum { PW_TILED = 0, PW_ROWS = 1, PW_DIRECT = 2, PW_LDS = 3 };
 
 // The pointwise call as a one-tap launch of the direct 3x3 kernel (weights
-// resident in LDS, activations straight into MFMA registers): K beyond the
-// register-operand kernel's reach, <= 64 output channels, a kg count in whole
-// 16-byte units, at most 32 MFMA steps (256 fp32 / 512 16-bit channels), and
-// enough 32-pixel blocks (>= 2048) that the launch fills every CU without
-// splitting K.
+// resident in LDS, activations straight into MFMA registers): what the
+// register-operand kernel does not take, up to 64 output channels (256 at
+// fp32, beyond 64 in groups of 64, one group per work item), a kg count in whole 16-byte
+// units, 4 to 32 MFMA steps (32-256 fp32 / 64-512 16-bit channels), weights
+// within LDS, and enough 32-pixel blocks (>= 2048) that the launch fills every
+// CU without splitting K.
 bool pw_lds_plan(const aih_pw_desc *d, aih::IgDirectArgs *a) {
   const uint32_t ku = d->dt == AIH_F32 ? 1 : 2, es = d->dt == AIH_F32 ? 4 : 2;
   const uint64_t M = (uint64_t)d->n * d->m;
-  if (d->dt != d->wdt || d->ng < 2 || d->ng * 4 > 64 || d->kg % ku || M < 2048ull * 32 || M > 0xffffff00ull)
+  // more than 64 outputs only at fp32: at 16 bit the tiled GEMM is as fast
+  // there (64 -> 256 f16 at 40x72 b64: 51.8 us tiled, 53.4 us here)
+  if (d->dt != d->wdt || d->ng < 2 || d->ng * 4 > (d->dt == AIH_F32 ? 256u : 64u) || d->kg % ku ||
+      M < 2048ull * 32 || M > 0xffffff00ull)
     return false;
   const uint64_t bytes = M * d->kg * 4 * es;
   if (bytes >= 0x80000000ull) return false;
   const uint32_t nu = d->kg / ku, nj = div_ceil(nu, 2);
-  if (aih::pw_lds_steps(nj) == 0 || aih::ig_direct_lds_bytes(1, nj, d->ng * 4) > 160u * 1024u) return false;
+  // at least 4 steps: the shortest instantiation has 8 (padding steps cost MFMAs)
+  if (nj < 4 || aih::pw_lds_steps(nj) == 0 || aih::ig_direct_lds_bytes(1, nj, d->ng * 4) > 160u * 1024u) return false;
   std::memset(a, 0, sizeof(*a));
   a->src_bytes[0] = a->src_bytes[1] = (uint32_t)bytes;
   a->stride_u[0] = a->stride_u[1] = nu;
   a->nu[0] = nu;
   a->nj0 = a->nj = nj;
   a->taps = 1;
+  a->ncg = aih::ig_direct_ncg(d->ng * 4);
   a->KGP = d->kg_pad;
   a->N4 = d->ng * 4;
   a->M = (uint32_t)M;
@@ -343,6 +349,7 @@ bool ig_direct_plan(const aih_igemm_desc *d, uint32_t oh, uint32_t ow, aih::IgDi
   if (nj == 0 || nj > aih::kIgDirectMaxSteps || aih::ig_direct_lds_bytes(9, nj, n4) > 160u * 1024u) return false;
   a->nj = nj;
   a->taps = 9;
+  a->ncg = 1;
   a->KGP = div_ceil(div_ceil(d->cin, 4), 4) * 4;
   a->N4 = n4;
   a->M = d->n * oh * ow;
@@ -418,7 +425,8 @@ int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out) {
       case PW_LDS: {
         aih::IgDirectArgs a;
         pw_lds_plan(d, &a);
-        *out = aih_plan{AIH_VAR_DIRECT, 1, 32, a.N4 <= 32 ? 32u : 64u, aih::ig_direct_grid(a.nblk, a.nj, a.N4), 0};
+        *out = aih_plan{AIH_VAR_DIRECT, 1, 32, aih::ig_direct_nob(a.N4) * 32u, aih::ig_direct_grid(a.nblk, a.nj, a.N4),
+                        0};
         return AIH_OK;
       }
       case PW_DIRECT:

@@ -19,6 +19,7 @@ struct IgDirectArgs {
   uint32_t kg_first[2];    // first kg (of the packed weights) of each part
   uint32_t nj0, nj;        // MFMA K steps per tap: of part 0, of all parts
   uint32_t taps;           // 9 (3x3) or 1 (1x1: the pointwise route)
+  uint32_t ncg;            // column groups of NOB * 32 outputs (work items per block)
   const void *w;           // packed [9][KGP][N4][4]
   const void *bias;        // [N4]
   const void *res;         // like y, or null
@@ -40,30 +41,38 @@ constexpr uint32_t kIgDirectMaxSteps = 10;
 // Step counts of the pointwise (1x1) instantiations: a call runs the
 // smallest one that holds its steps (the extra steps read zero weights and
 // activations).
-constexpr uint32_t kPwLdsSteps[4] = {12, 16, 24, 32};
+constexpr uint32_t kPwLdsSteps[5] = {8, 12, 16, 24, 32};
 inline uint32_t pw_lds_steps(uint32_t nj) {
   for (uint32_t s : kPwLdsSteps)
     if (nj <= s) return s;
   return 0;
 }
 
-// LDS bytes of a launch: the weights as [taps][nj][2][NOB*32] 16-byte units,
-// then NOB*32 fp32 biases (nj: the instantiation's steps per tap).
+// Output columns per wavefront (NOB blocks of 32) and column groups: N4 <=
+// 32 -> one block; <= 64 -> two; beyond (1x1 only, <= 256) -> groups of two
+// blocks, one group per work item.
+inline uint32_t ig_direct_nob(uint32_t N4) { return N4 <= 32 ? 1u : 2u; }
+inline uint32_t ig_direct_ncg(uint32_t N4) { return N4 <= 64 ? 1u : (N4 + 63) / 64; }
+
+// LDS bytes of a launch: the weights as [taps][nj][2][ncg * NOB * 32]
+// 16-byte units, then the fp32 biases of those columns (nj: the
+// instantiation's steps per tap).
 inline uint32_t ig_direct_lds_bytes(uint32_t taps, uint32_t nj, uint32_t N4) {
-  const uint32_t nob = N4 <= 32 ? 1u : 2u;
+  const uint32_t cols = ig_direct_ncg(N4) * ig_direct_nob(N4) * 32u;
   if (taps == 1) nj = pw_lds_steps(nj);
-  return taps * nj * 2u * nob * 32u * 16u + nob * 32u * 4u;
+  return taps * nj * 2u * cols * 16u + cols * 4u;
 }
 
-// Workgroups of a launch: one per 8 blocks, at most one per CU. A second
+// Workgroups of a launch: one per 8 work items (a block of 32 pixels times
+// a column group), at most one per CU. A second
 // resident workgroup per CU (when registers and LDS allow it) measured
 // slower on every shape tried: its extra loads in flight contend for the
 // same caches (3x3 16 -> 32 stride 2 at 160x288 batch 32, fp32: 62.0 us
 // with two per CU, 57.6 us with one).
 inline uint32_t ig_direct_grid(uint32_t nblk, uint32_t nj, uint32_t N4) {
   (void)nj;
-  (void)N4;
-  const uint64_t want = ((uint64_t)nblk + kIgDirectThreads / 64 - 1) / (kIgDirectThreads / 64);
+  const uint64_t items = (uint64_t)nblk * ig_direct_ncg(N4);
+  const uint64_t want = (items + kIgDirectThreads / 64 - 1) / (kIgDirectThreads / 64);
   return (uint32_t)(want < 256ull ? want : 256ull);
 }
 

@@ -47,68 +47,77 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
   extern __shared__ __align__(16) char lds[];
   u32x4 *Wl = reinterpret_cast<u32x4 *>(lds);
   const uint32_t nj0 = a.nj0;
-  float *Bl = reinterpret_cast<float *>(lds + TAPS * NJ * 2 * NC * 16);
+  // LDS row of one (tap, step, half): every column group's NC columns
+  const uint32_t RS = a.ncg * NC;
+  float *Bl = reinterpret_cast<float *>(lds + TAPS * NJ * 2 * RS * 16);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, lh = lane >> 5;
 
   // ---- weights -> LDS as [tap][step][half][column] operands (zero padding) ----
-  // every thread issues all of its loads before its first LDS store, so the
-  // copy costs one memory latency
-  constexpr int NW = TAPS * NJ * 2 * NC;
-  constexpr int PER = (NW + kIgDirectThreads - 1) / kIgDirectThreads;
-  static_assert(kIgDirectThreads % NC == 0, "column of an entry");
-  u32x4 wst[PER];
+  // each thread issues a batch of loads before the batch's LDS stores, so the
+  // copy costs one memory latency per batch (one batch up to 4096 entries)
+  const uint32_t nw = TAPS * NJ * 2 * RS;
+  constexpr int BATCH = 8;
+  for (uint32_t base = 0; base < nw; base += BATCH * kIgDirectThreads) {
+    u32x4 wst[BATCH];
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const uint32_t i = tid + k * kIgDirectThreads;
-    const uint32_t n = i % NC, r = i / NC, h = r & 1, r2 = r >> 1, j = r2 % NJ, tap = r2 / NJ;
-    const uint32_t p = j >= nj0 ? 1 : 0;
-    const uint32_t u = 2 * (j - (p ? nj0 : 0)) + h;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if ((NW % kIgDirectThreads == 0 || i < (uint32_t)NW) && u < a.nu[p] && n < a.N4) {
-      if constexpr (F32) {
-        const uint32_t kg = a.kg_first[p] + u;
-        v = reinterpret_cast<const u32x4 *>(a.w)[(size_t)(tap * a.KGP + kg) * a.N4 + n];
-      } else {
-        const uint32_t kg = a.kg_first[p] + 2 * u;
-        const u32x2 *wp = reinterpret_cast<const u32x2 *>(a.w);
-        const u32x2 lo = wp[(size_t)(tap * a.KGP + kg) * a.N4 + n];
-        const u32x2 hi = wp[(size_t)(tap * a.KGP + kg + 1) * a.N4 + n];
-        v = u32x4{lo.x, lo.y, hi.x, hi.y};
+    for (int k = 0; k < BATCH; ++k) {
+      const uint32_t i = base + tid + k * kIgDirectThreads;
+      const uint32_t n = i % RS, r = i / RS, h = r & 1, r2 = r >> 1, j = r2 % NJ, tap = r2 / NJ;
+      const uint32_t p = j >= nj0 ? 1 : 0;
+      const uint32_t u = 2 * (j - (p ? nj0 : 0)) + h;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (i < nw && u < a.nu[p] && n < a.N4) {
+        if constexpr (F32) {
+          const uint32_t kg = a.kg_first[p] + u;
+          v = reinterpret_cast<const u32x4 *>(a.w)[(size_t)(tap * a.KGP + kg) * a.N4 + n];
+        } else {
+          const uint32_t kg = a.kg_first[p] + 2 * u;
+          const u32x2 *wp = reinterpret_cast<const u32x2 *>(a.w);
+          const u32x2 lo = wp[(size_t)(tap * a.KGP + kg) * a.N4 + n];
+          const u32x2 hi = wp[(size_t)(tap * a.KGP + kg + 1) * a.N4 + n];
+          v = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
       }
+      wst[k] = v;
     }
-    wst[k] = v;
-  }
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const uint32_t i = tid + k * kIgDirectThreads;
-    if (NW % kIgDirectThreads == 0 || i < (uint32_t)NW) Wl[i] = wst[k];
+    for (int k = 0; k < BATCH; ++k) {
+      const uint32_t i = base + tid + k * kIgDirectThreads;
+      if (i < nw) Wl[i] = wst[k];
+    }
   }
-  if (tid < NC) Bl[tid] = (uint32_t)tid < a.N4 ? Vec4IO<DT>::load(a.bias, tid / 4)[tid % 4] : 0.0f;
+  if ((uint32_t)tid < RS) Bl[tid] = (uint32_t)tid < a.N4 ? Vec4IO<DT>::load(a.bias, tid / 4)[tid % 4] : 0.0f;
   __syncthreads();
 
   const __amdgpu_buffer_rsrc_t rs0 = ig_rsrc(a.src[0], a.src_bytes[0]);
   const __amdgpu_buffer_rsrc_t rs1 = ig_rsrc(a.src[1], a.src_bytes[1]);
   const Act actp = act_params(a.act);
 
-  // this workgroup's contiguous range of blocks (ranges go out XCD by XCD so
+  // this workgroup's contiguous range of work items -- item = block * ncg +
+  // column group, so the column groups of one block run back to back and
+  // re-read its activations from the cache (ranges go out XCD by XCD so
   // neighbouring blocks, which share input rows, meet in one L2)
+  const uint32_t nitems = a.nblk * a.ncg;
   const uint32_t g = xcd_remap(blockIdx.x, gridDim.x);
-  const uint32_t b_begin = (uint32_t)(((uint64_t)g * a.nblk) / gridDim.x);
-  const uint32_t b_end = (uint32_t)(((uint64_t)(g + 1) * a.nblk) / gridDim.x);
+  const uint32_t b_begin = (uint32_t)(((uint64_t)g * nitems) / gridDim.x);
+  const uint32_t b_end = (uint32_t)(((uint64_t)(g + 1) * nitems) / gridDim.x);
 
-  // lane's weight operand of (tap, step, column block o) at Wl[wl + (tap*NJ + step)*2*NC + o*32]
-  const uint32_t wl = lh * NC + l32;
+  // lane's weight operand of (tap, step, column group cg, block o) at
+  // Wl[wl + cg*NC + (tap*NJ + step)*2*RS + o*32]
+  const uint32_t wl = lh * RS + l32;
 
   // a block's output pixels decoded: lane pixel, its tap-(0, 0) source row and
   // column, and the unit index (per part) of that source pixel
   struct Blk {
-    uint32_t pix_out, b0, b1;
+    uint32_t pix_out, b0, b1, cg;
     int32_t iy0, ix0;
     bool valid;
   };
-  auto decode = [&](uint32_t blk) {
+  auto decode = [&](uint32_t item) {
     Blk b;
+    const uint32_t blk = item / a.ncg;
+    b.cg = item - blk * a.ncg;
     b.pix_out = blk * 32 + l32;
     b.valid = b.pix_out < a.M;
     const uint32_t pp = b.valid ? b.pix_out : 0;
@@ -154,7 +163,7 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
   uint32_t wlo = wl;
   auto load_w = [&](int s, u32x4 (&w)[NOB]) {
 #pragma unroll
-    for (int o = 0; o < NOB; ++o) w[o] = Wl[wlo + s * 2 * NC + o * 32];
+    for (int o = 0; o < NOB; ++o) w[o] = Wl[wlo + s * 2 * RS + o * 32];
   };
 
   // Software pipeline over the TAPS * NJ MFMA steps of each block: a ring of D
@@ -176,6 +185,7 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
     x[s] = load_step(ts, s % NJ);
   }
   for (;;) {
+    wlo = wl + cur.cg * NC;
     __asm__ volatile("" : "+v"(wlo));
     u32x4 wv[2][NOB];
     load_w(0, wv[0]);
@@ -222,7 +232,7 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
       for (int o = 0; o < NOB; ++o) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const uint32_t c = o * 32 + 8 * q + 4 * lh;
+          const uint32_t c = cur.cg * NC + o * 32 + 8 * q + 4 * lh;
           if (c >= a.N4) continue;
           f32x4 v = f32x4{acc[o][4 * q], acc[o][4 * q + 1], acc[o][4 * q + 2], acc[o][4 * q + 3]} +
                     *reinterpret_cast<const f32x4 *>(Bl + c);
@@ -256,8 +266,9 @@ hipError_t launch_nob(const IgDirectArgs &a, hipStream_t st) {
   // operand ring depth D (a divisor of 9 * NJ): 6 / 9 / 12 steps, measured
   // against 3 and 18 on the 16 -> 32 and 32 -> 32 / 64 shapes
   if (a.taps == 1) {
-    // 1x1: the steps run up to the instantiation's count (ring 12 / 8 deep)
+    // 1x1: the steps run up to the instantiation's count (ring 8 / 12 deep)
     switch (pw_lds_steps(a.nj)) {
+      case 8: return launch_inst<DT, NOB, 1, 8, 8>(a, st);
       case 12: return launch_inst<DT, NOB, 1, 12, 12>(a, st);
       case 16: return launch_inst<DT, NOB, 1, 16, 8>(a, st);
       case 24: return launch_inst<DT, NOB, 1, 24, 12>(a, st);
@@ -288,7 +299,8 @@ hipError_t launch_dt(const IgDirectArgs &a, hipStream_t st) {
 }  // namespace
 
 hipError_t launch_ig_direct(const IgDirectArgs &a, int dt, hipStream_t st) {
-  if (a.N4 == 0 || a.N4 > 64 || a.N4 % 4 || a.nj == 0 || a.nj0 > a.nj || (a.taps != 1 && a.taps != 9) ||
+  if (a.N4 == 0 || a.N4 % 4 || a.N4 > (a.taps == 1 ? 256u : 64u) || a.ncg != ig_direct_ncg(a.N4) || a.nj == 0 ||
+      a.nj0 > a.nj || (a.taps != 1 && a.taps != 9) ||
       (a.taps == 9 && a.nj > kIgDirectMaxSteps) || (a.taps == 1 && pw_lds_steps(a.nj) == 0) ||
       ig_direct_lds_bytes(a.taps, a.nj, a.N4) > 160u * 1024u)
     return hipErrorInvalidValue;

@@ -128,12 +128,14 @@ PW_DIRECT = [((80, 144, 44, 24), "relu", False, 3501), ((13, 19, 32, 12), "none"
              ((7, 11, 8, 8), "sigmoid", True, 3505), ((5, 9, 60, 36), "none", False, 3506)]
 
 
-# K beyond the register-operand kernel, <= 64 outputs, >= 2048 blocks of 32
-# pixels: the direct kernel run with one tap (weights in LDS); a ragged last
-# block, steps padded up to the instantiation (25 -> 32, 13 -> 16), a
-# half-empty last step at 16 bit
+# beyond the register-operand kernel (K, or 65-256 outputs in column groups of
+# 64), >= 2048 blocks of 32 pixels: the direct kernel run with one tap
+# (weights in LDS); a ragged last block, steps padded up to the instantiation
+# (25 -> 32, 13 -> 16), a half-empty last step at 16 bit, 4 and 3 column
+# groups (the last one ragged: 136 = 2 x 64 + 8)
 PW_LDS = [((257, 257, 256, 64), "relu", True, 3601), ((260, 256, 200, 20), "hardswish", False, 3602),
-          ((256, 260, 96, 40), "relu6", True, 3603)]
+          ((256, 260, 96, 40), "relu6", True, 3603), ((257, 256, 64, 256), "relu", False, 3604),
+          ((256, 257, 72, 136), "none", True, 3605)]
 
 
 @pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
@@ -141,7 +143,8 @@ PW_LDS = [((257, 257, 256, 64), "relu", True, 3601), ((260, 256, 200, 20), "hard
 def test_pw_lds_direct(case, dt):
     (h, w, cin, cout), act, res, seed = case
     r = G.run_pw(h, w, cin, cout, act, res, dt, seed)
-    assert r.plan.variant == G.conv.Variant.DIRECT and r.plan.ws_bytes == 0, r.plan
+    if cout <= 64 or dt == F32:  # more than 64 outputs at 16 bit: the tiled GEMM
+        assert r.plan.variant == G.conv.Variant.DIRECT and r.plan.ws_bytes == 0, r.plan
     check(f"pw lds-direct {case} dt{dt} {r.plan}", r, dt)
 
 
