@@ -128,6 +128,13 @@ int plan_gemm(uint32_t M, uint32_t N4, uint32_t KK, int32_t dt, int32_t variant,
     const uint32_t max_s = KK / bkg;
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
+  } else if (variant == AIH_VAR_AUTO && dt == AIH_F32 && tiles < 2 * kCUs && KK >= 128) {
+    // fp32 with long K (>= 512 channels, MFMA-bound) whose tiles fill the CUs
+    // once but not twice: the second, partial round of workgroups idles most
+    // CUs. Four K chunks make each workgroup's range at most 3/4 of a whole
+    // tile's work (960 -> 160 at 10x18 b256: 360 tiles, 236 -> 215 us; two
+    // chunks did not help, six and eight cost more in partial sums).
+    s = 4;
   }
   if (variant == AIH_VAR_TILE && splitk > 1) return fail("AIH_VAR_TILE with splitk > 1");
   uint32_t chunk = div_ceil(KK, s);

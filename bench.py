@@ -11,7 +11,7 @@ TFLOP/s, GB/s and its roofline fraction (t_roof / t_measured,
 t_roof = max(flops / MFMA peak, bytes / 8 TB/s)):
   pw_32to64_relu6_80x144            1x1 32->64 + ReLU6, [1,80,144,32] fp32
   pw_960to160_10x18_b1_splitk{1,4,8} 1x1 960->160, [1,10,18,960] fp32, split-K forced
-  pw_960to160_10x18_b256            the same layer at batch 256 (policy: no split)
+  pw_960to160_10x18_b256            the same layer at batch 256 (policy: four K chunks)
   igemm3x3s2_16to32_relu_160x288_b32 3x3 s2 pad 1 16->32 + ReLU, [32,160,288,16] fp32
   igemm3x3s1_32to64_relu_80x144_b32  3x3 s1 pad 1 32->64 + ReLU, [32,80,144,32] fp32
   ir_block_chain_4x_64c_40x72_b64    4 inverted-residual blocks at [64,40,72,64] fp32

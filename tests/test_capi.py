@@ -67,8 +67,9 @@ def test_pw_policy_splits_small_m_large_k():
     p = pw_plan(1, 180, 960, 160)
     assert p.variant == conv.Variant.SPLITK and p.splitk > 1
     assert p.ws_bytes == p.splitk * 180 * 160 * 4
-    # same layer at batch 256: 360 tiles -> one tile per workgroup over the whole K
-    p = pw_plan(256, 180, 960, 160)
+    # same layer at batch 256: 360 tiles, forced whole -> one tile per
+    # workgroup over the whole K (the policy splits it in four, see below)
+    p = pw_plan(256, 180, 960, 160, variant=conv.Variant.TILE)
     assert p.variant == conv.Variant.TILE and p.splitk == 1 and p.ws_bytes == 0
     assert p.bn == 160 and p.grid == 360
     # 1x1 32 -> 64 at 80x144: short K (32) and 64 output channels -> the
@@ -96,6 +97,16 @@ def test_pw_policy_agrees_with_reference_on_its_splitk_kats(orc):
         assert orc.ref_pw_variant(m, kg, ng) == "Small"
         p = conv.GemmPwSpec(m=m, kg=kg, ng=ng).plan()
         assert p.variant in (conv.Variant.TILE, conv.Variant.DIRECT) and p.splitk == 1, (m, kg, ng, p)
+
+
+def test_pw_policy_splits_long_k_fp32_partial_second_round():
+    """fp32, K >= 512, tiles between one and two per CU: four K chunks
+    (960 -> 160 at 10x18, batch 256: 360 tiles)."""
+    p = pw_plan(256, 180, 960, 160)
+    assert p.variant == conv.Variant.SPLITK and p.splitk == 4 and p.grid == 1440
+    # the same at 16 bit (HBM-bound) and with short K stays whole
+    assert conv.GemmPwSpec(m=180, kg=240, ng=40, n=256, dt=conv.DType.F16).plan().splitk == 1
+    assert pw_plan(256, 180, 256, 160).splitk == 1
 
 
 def test_forced_splitk_factor_is_honoured():
