@@ -1,6 +1,7 @@
 // conv_igemm_direct.h -- launch interface of the 3x3 implicit-GEMM conv with
 // at most 64 output channels whose whole weight tensor fits in LDS (the
-// activations go from memory straight into MFMA operand registers).
+// activations go from memory straight into MFMA operand registers), also
+// launched with one tap for pointwise convs with mid-size K.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -1,6 +1,7 @@
 // conv_igemm_direct.hip -- 3x3 implicit-GEMM conv with at most 64 output
-// channels, the weights resident in LDS and the activations loaded straight
-// into MFMA operand registers.
+// channels (and, as a one-tap launch, pointwise convs with mid-size K), the
+// weights resident in LDS and the activations loaded straight into MFMA
+// operand registers.
 //
 // The tiled GEMM stages A and B through LDS in 16/32-channel steps behind a
 // workgroup barrier each; with 32 or 64 output columns a step holds only 2-8
@@ -12,9 +13,12 @@
 // their source pixels per tap in registers (implicit im2col, no buffer) and
 // loads the tap's input channels as 16-byte buffer loads straight into MFMA B
 // operands -- out-of-image taps and padding units read zeros from the buffer
-// range check. The next tap's loads are in flight while the current tap's
-// MFMAs run. The reference's route for the same layers is
-// conv_igemm_{tiled,direct}.wgsl (crates/ai-gpu/src/kernels/conv_igemm.rs).
+// range check. Loads run a ring of D steps ahead of the MFMAs, across block
+// ends. The reference's route for the same layers is
+// conv_igemm_{tiled,direct}.wgsl (crates/ai-gpu/src/kernels/conv_igemm.rs);
+// for the pointwise launches (TAPS = 1, the pixel row as the image, up to 256
+// fp32 outputs as column groups of 64 that are separate work items) it is
+// gemm_pw_tiled.wgsl (crates/ai-gpu/src/kernels/gemm_pw.rs).
 //
 // K order: tap-major (ky, kx), then the input parts in order, then 16-byte
 // units of each part; MFMA step j of a tap pairs unit 2j (lane half 0) with
