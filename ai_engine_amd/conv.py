@@ -57,6 +57,14 @@ class Activation(enum.IntEnum):
     RECIP = 10
 
 
+class IrWeights(enum.IntEnum):
+    """Where a fused block keeps its expand / project weights (enum aih_ir_weights)."""
+
+    AUTO = 0
+    RESIDENT = 1
+    STREAMED = 2
+
+
 class Variant(enum.IntEnum):
     AUTO = 0
     TILE = 1
@@ -104,7 +112,7 @@ class _IrDesc(C.Structure):
                 ("cexp", C.c_uint32), ("cout", C.c_uint32), ("s", C.c_uint32), ("pad", C.c_uint32 * 4),
                 ("act_expand", C.c_int32), ("act_dw", C.c_int32), ("act_project", C.c_int32),
                 ("residual", C.c_int32), ("dt", C.c_int32), ("tile_h", C.c_uint32), ("tile_w", C.c_uint32),
-                ("ec", C.c_uint32)]
+                ("ec", C.c_uint32), ("weights", C.c_int32)]
 
 
 class IrPlan(C.Structure):
@@ -130,7 +138,7 @@ EXPORTS = (
     "aih_conv_pw", "aih_conv_pw_plan", "aih_conv_igemm", "aih_conv_igemm_plan", "aih_conv_dw", "aih_conv",
     "aih_conv_workspace_size", "aih_nhwc_c4_bytes", "aih_pack_nhwc", "aih_unpack_nhwc",
     "aih_pack_weights_conv", "aih_pack_weights_dw", "aih_pack_bias", "aih_pack_nhwc_device",
-    "aih_ir_block_plan", "aih_ir_block", "aih_last_error", "aih_version", "aih_conv_check",
+    "aih_ir_block_plan", "aih_ir_block", "aih_last_error", "aih_version", "aih_conv_check", "aih_conv_plan",
 )
 
 _lib = None
@@ -153,6 +161,7 @@ def lib() -> C.CDLL:
         "aih_conv_dw": (C.c_int, [C.POINTER(_DwDesc), P, P, P, P, P, P]),
         "aih_conv": (C.c_int, [C.POINTER(_ConvDesc), P, P, P, P, P, P, sz, P]),
         "aih_conv_workspace_size": (sz, [C.POINTER(_ConvDesc)]),
+        "aih_conv_plan": (C.c_int, [C.POINTER(_ConvDesc), C.POINTER(Plan)]),
         "aih_nhwc_c4_bytes": (sz, [u32, u32, u32, u32, i32]),
         "aih_pack_nhwc": (C.c_int, [P, u32, u32, u32, u32, i32, P]),
         "aih_unpack_nhwc": (C.c_int, [P, u32, u32, u32, u32, i32, P]),
@@ -386,6 +395,12 @@ class ConvOp:
     def workspace_bytes(self) -> int:
         return lib().aih_conv_workspace_size(C.byref(self.desc()))
 
+    def plan(self) -> Plan:
+        """The plan of the route aih_conv takes (aih_conv_plan)."""
+        p = Plan()
+        _check(lib().aih_conv_plan(C.byref(self.desc()), C.byref(p)))
+        return p
+
     def run(self, x, w, bias, res, y, ws=None, stream=None):
         nb = self.workspace_bytes()
         ws = _workspace(nb, ws, _device_of(y))
@@ -416,6 +431,7 @@ class IrBlockSpec:
     n: int = 1
     tile: tuple = (0, 0)  # forced output tile (h, w); (0, 0) = plan's choice
     ec: int = 0           # forced expanded channels per chunk; 0 = plan's choice
+    weights: int = 0      # IrWeights: 0 = plan's choice, 1 = resident in LDS, 2 = streamed
 
     def out_hw(self) -> tuple[int, int]:
         return ((self.ih + self.pad[0] + self.pad[2] - 3) // self.s + 1,
@@ -424,7 +440,7 @@ class IrBlockSpec:
     def desc(self) -> _IrDesc:
         return _IrDesc(self.n, self.ih, self.iw, self.cin, self.cexp, self.cout, self.s, (C.c_uint32 * 4)(*self.pad),
                        int(self.act_expand), int(self.act_dw), int(self.act_project), int(bool(self.residual)),
-                       int(self.dt), self.tile[0], self.tile[1], self.ec)
+                       int(self.dt), self.tile[0], self.tile[1], self.ec, int(self.weights))
 
     def plan(self) -> IrPlan:
         p = IrPlan()

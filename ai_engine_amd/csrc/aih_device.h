@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/aih_conv.h"
 
 namespace aih {
@@ -273,15 +275,40 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) {
   return (uint32_t)(((uint64_t)__umulhi(n, f.m) + n) >> f.s);
 }
 
-// MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs,
-// each with a private L2. Remap so that every XCD walks a contiguous range of
-// logical tiles: neighbouring tiles (which share input rows / halos) then hit
-// the same L2. Bijective on [0, n).
-__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n) {
-  constexpr uint32_t XCD = 8;
-  uint32_t per = n / XCD;
-  if (bid >= per * XCD) return bid;
-  return (bid % XCD) * per + bid / XCD;
+// MI355X dispatches consecutive workgroup ids round-robin over its XCDs (8
+// on a whole device), each with a private L2. Remap so that every XCD walks a
+// contiguous range of logical tiles: neighbouring tiles (which share input
+// rows / halos) then hit the same L2. Bijective on [0, n) for any nxcd >= 1.
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n, uint32_t nxcd) {
+  if (nxcd <= 1) return bid;
+  uint32_t per = n / nxcd;
+  if (bid >= per * nxcd) return bid;
+  return (bid % nxcd) * per + bid / nxcd;
 }
+
+// Launch facts of the current device, queried once per device ordinal:
+// compute units (grids and split decisions) and XCDs (xcd_remap). A failed
+// query falls back to a whole MI355X (256 CUs in 8 XCDs).
+struct DeviceInfo {
+  uint32_t cus, xcds;
+};
+
+inline DeviceInfo device_info() {
+  static std::mutex mu;
+  static DeviceInfo cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DeviceInfo{256, 8};
+  std::lock_guard<std::mutex> lock(mu);
+  DeviceInfo &d = cache[dev];
+  if (d.cus == 0) {
+    int cus = 0, xcds = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || xcds <= 0) xcds = 8;
+    d = DeviceInfo{(uint32_t)cus, (uint32_t)xcds};
+  }
+  return d;
+}
+inline uint32_t device_cus() { return device_info().cus; }
+inline uint32_t device_xcds() { return device_info().xcds; }
 
 }  // namespace aih

@@ -8,7 +8,9 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <exception>
 #include <initializer_list>
 #include <string>
@@ -61,7 +63,7 @@ size_t dsize(int32_t dt) { return dt == AIH_F32 ? 4 : 2; }
 // least 16 channel groups (the reference's own kg >= 16 gate), aiming at two
 // workgroups per CU, at most 32 chunks, and at least one full stage per chunk;
 // a grid that splitting cannot bring there takes narrower column tiles first.
-constexpr uint32_t kCUs = 256;
+// The CU count is the current device's (aih::device_cus()).
 
 // kg per K stage of the kernel: 16 channels for fp32, 32 for 16-bit storage.
 int stage_kg(int32_t dt) { return dt == AIH_F32 ? 4 : 8; }
@@ -87,6 +89,7 @@ struct GemmPlan {
 
 int plan_gemm(uint32_t M, uint32_t N4, uint32_t KK, int32_t dt, int32_t variant, int32_t splitk,
               GemmPlan *p) {
+  const uint32_t kCUs = aih::device_cus();
   if (variant != AIH_VAR_AUTO && variant != AIH_VAR_TILE && variant != AIH_VAR_SPLITK)
     return fail("variant must be AIH_VAR_AUTO, AIH_VAR_TILE or AIH_VAR_SPLITK");
   if (splitk < 0 || splitk > 64) return fail("splitk must be in [0, 64]");
@@ -201,6 +204,7 @@ bool pw_lds_plan(const aih_pw_desc *d, aih::IgDirectArgs *a) {
   a->nblk = (uint32_t)((M + 31) / 32);
   a->act = d->act;
   a->has_res = d->residual ? 1 : 0;
+  a->nxcd = aih::device_xcds();
   a->fd_ohw = aih::make_fastdiv(d->m);
   a->fd_ow = aih::make_fastdiv(d->m);
   return true;
@@ -230,6 +234,7 @@ int run_gemm(aih::GemmArgs &a, const GemmPlan &g, int32_t dt, int32_t wdt, bool 
   a.fd_OHW = aih::make_fastdiv(a.OHW);
   a.fd_OW = aih::make_fastdiv(a.OW);
   a.partial = nullptr;
+  a.nxcd = aih::device_xcds();
   if (g.nsplit > 1) {
     if (ws == nullptr || ws_bytes < g.ws)
       return fail("split-K needs a workspace of " + std::to_string(g.ws) + " bytes");
@@ -261,8 +266,44 @@ int check_pw(const aih_pw_desc *d) {
   return AIH_OK;
 }
 
+// Diagnostic overrides of the split-K policy, read once per process (so a
+// plan stays a pure function of its descriptor within a run), as the
+// reference's AI_PW_SPLITK_NG (gemm_pw.rs:112-126) and AI_RT_FORCE_DIRECT
+// (lowering.rs:156-160) are:
+//   AIH_PW_SPLITK=<n>     pointwise convs with AIH_VAR_AUTO and no forced
+//                         split that run the tiled GEMM use n K chunks
+//                         (1 = never split);
+//   AIH_IGEMM_NO_SPLIT=1  KxK convs with AIH_VAR_AUTO and no forced split
+//                         never split K.
+int env_int_once(const char *name, int *slot, std::once_flag *once) {
+  std::call_once(*once, [&] {
+    const char *v = std::getenv(name);
+    *slot = 0;
+    if (v && *v) {
+      char *end = nullptr;
+      const long n = std::strtol(v, &end, 10);
+      if (end && *end == 0 && n > 0 && n <= 64) *slot = (int)n;
+    }
+  });
+  return *slot;
+}
+
+int env_pw_splitk() {
+  static int v;
+  static std::once_flag once;
+  return env_int_once("AIH_PW_SPLITK", &v, &once);
+}
+
+bool env_igemm_no_split() {
+  static int v;
+  static std::once_flag once;
+  return env_int_once("AIH_IGEMM_NO_SPLIT", &v, &once) == 1;
+}
+
 int plan_pw(const aih_pw_desc *d, GemmPlan *g) {
-  return plan_gemm(d->n * d->m, d->ng * 4, d->kg, d->dt, d->variant, d->splitk, g);
+  int32_t sk = d->splitk;
+  if (d->variant == AIH_VAR_AUTO && sk == 0) sk = env_pw_splitk();
+  return plan_gemm(d->n * d->m, d->ng * 4, d->kg, d->dt, d->variant, sk, g);
 }
 
 // ---------------------------------------------------------------- igemm
@@ -314,8 +355,10 @@ bool igemm_is_stem(const aih_igemm_desc *d) {
 int plan_igemm(const aih_igemm_desc *d, GemmPlan *g) {
   uint32_t oh, ow;
   if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
+  int32_t sk = d->splitk;
+  if (d->variant == AIH_VAR_AUTO && sk == 0 && env_igemm_no_split()) sk = 1;
   return plan_gemm(d->n * oh * ow, div_ceil(d->cout, 4) * 4, d->k * d->k * div_ceil(d->cin, 4), d->dt,
-                   d->variant, d->splitk, g);
+                   d->variant, sk, g);
 }
 
 // The 3x3 direct kernel's arguments for an igemm call (buffers aside), or
@@ -371,6 +414,7 @@ bool ig_direct_plan(const aih_igemm_desc *d, uint32_t oh, uint32_t ow, aih::IgDi
   a->nblk = div_ceil(a->M, 32);
   a->act = d->act;
   a->has_res = d->residual ? 1 : 0;
+  a->nxcd = aih::device_xcds();
   a->fd_ohw = aih::make_fastdiv(oh * ow);
   a->fd_ow = aih::make_fastdiv(ow);
   return true;
@@ -407,7 +451,7 @@ bool ir_clamp_acts(const aih_ir_block_desc *d) {
 
 int plan_ir(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, aih::IrPlan *p) {
   const char *why = aih::ir_plan(d->n, d->ih, d->iw, oh, ow, d->cin, d->cexp, d->cout, d->s, d->dt,
-                                 ir_clamp_acts(d), d->tile_h, d->tile_w, d->ec, p);
+                                 ir_clamp_acts(d), d->tile_h, d->tile_w, d->ec, d->weights, p);
   if (why) return fail(std::string("ir_block: ") + why);
   return AIH_OK;
 }
@@ -438,7 +482,7 @@ int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out) {
       }
       case PW_DIRECT:
         *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->ng * 4 <= 32 ? 32u : 64u,
-                        (uint32_t)std::min<uint64_t>((M + 127) / 128, 256u * 8u), 0};
+                        (uint32_t)std::min<uint64_t>((M + 127) / 128, aih::device_cus() * 8u), 0};
         return AIH_OK;
       default:
         break;
@@ -529,7 +573,7 @@ int aih_conv_igemm_plan(const aih_igemm_desc *d, aih_plan *out) {
     if (igemm_is_stem(d)) {
       // the stem kernel: 32 pixels per wavefront, 4 wavefronts per workgroup
       const uint64_t nblocks = ((uint64_t)d->n * oh * ow + 31) / 32;
-      *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->cout, (uint32_t)std::min<uint64_t>((nblocks + 3) / 4, 256u * 8u), 0};
+      *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->cout, (uint32_t)std::min<uint64_t>((nblocks + 3) / 4, aih::device_cus() * 8u), 0};
       return AIH_OK;
     }
     aih::IgDirectArgs da;
@@ -691,6 +735,7 @@ int aih_conv_dw(const aih_dw_desc *d, const void *x, const void *w, const void *
     a.PL = (int32_t)d->pad[1];
     a.act = d->act;
     a.has_res = d->residual ? 1 : 0;
+    a.nxcd = aih::device_xcds();
     if ((uint64_t)a.N * a.IH * a.IW * a.CG > 0xffffffffull || (uint64_t)a.N * a.OH * a.OW * a.CG > 0xffffffffull)
       return fail("dw: tensor too large");
     hipError_t e = aih::launch_conv_dw(a, d->dt, static_cast<hipStream_t>(stream));
@@ -769,6 +814,7 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
     a.mask_e = (d->act_expand == AIH_ACT_SIGMOID || d->act_expand == AIH_ACT_HARDSIGMOID ||
                 d->act_expand == AIH_ACT_RECIP) ? 1 : 0;
     a.clamp_acts = ir_clamp_acts(d) ? 1 : 0;
+    a.nxcd = aih::device_xcds();
     a.lds_x = p.lds_x;
     a.lds_xe = p.lds_xe;
     a.lds_we = p.lds_we;
@@ -826,6 +872,22 @@ int aih_conv_check(const aih_conv_desc *d) {
     if (r == 0) return check_pw(&pw) ? AIH_ERR : plan_pw(&pw, &g);
     if (r == 1) return check_igemm(&ig) ? AIH_ERR : plan_igemm(&ig, &g);
     return check_dw(&dw);
+  });
+}
+
+int aih_conv_plan(const aih_conv_desc *d, aih_plan *out) {
+  return guarded([&] {
+    aih_pw_desc pw;
+    aih_igemm_desc ig;
+    aih_dw_desc dw;
+    const int r = conv_route(d, &pw, &ig, &dw);
+    if (r < 0) return AIH_ERR;
+    if (!out) return fail("null plan");
+    if (r == 0) return aih_conv_pw_plan(&pw, out);
+    if (r == 1) return aih_conv_igemm_plan(&ig, out);
+    if (check_dw(&dw)) return AIH_ERR;
+    *out = aih_plan{AIH_VAR_DIRECT, 1, 0, 0, 0, 0};
+    return AIH_OK;
   });
 }
 

@@ -13,6 +13,7 @@ struct DwArgs {
   uint32_t K, S, D;
   int32_t PT, PL;
   int32_t act, has_res;
+  uint32_t nxcd;  // XCDs of the device (workgroup remap)
 };
 
 hipError_t launch_conv_dw(const DwArgs &a, int dt, hipStream_t st);

@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void conv_dw_strip_kernel(DwArgs a) {
   // Workgroups are dealt round-robin to the 8 XCDs; remapping gives each XCD
   // a contiguous run of output rows, so the input rows shared by vertically
   // adjacent outputs are fetched into one L2 instead of one per XCD.
-  const uint64_t gid = (uint64_t)xcd_remap(blockIdx.x, gridDim.x) * 256 + threadIdx.x;
+  const uint64_t gid = (uint64_t)xcd_remap(blockIdx.x, gridDim.x, a.nxcd) * 256 + threadIdx.x;
   const uint32_t owb = (a.OW + PX - 1) / PX;
   const uint64_t total = (uint64_t)a.N * a.OH * owb * cgv;
   if (gid >= total) return;

@@ -77,6 +77,7 @@ struct GemmArgs {
   uint32_t ntiles_total;  // mtiles * ntiles * nsplit
   int32_t act;
   int32_t has_res;
+  uint32_t nxcd;          // XCDs of the device (workgroup remap)
   // the divisors above the kernel divides by, prepared on the host
   FastDiv fd_ntiles, fd_mtiles, fd_KG, fd_K, fd_OHW, fd_OW;
 };
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void conv_gemm_kernel(GemmArgs a) {
   const int lh = lane >> 5;
 
   // ---- this workgroup's contiguous range of tiles ----
-  const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x, a.nxcd);
   const uint32_t t_begin = (uint32_t)(((uint64_t)blk * a.ntiles_total) / gridDim.x);
   const uint32_t t_end = (uint32_t)(((uint64_t)(blk + 1) * a.ntiles_total) / gridDim.x);
   if (t_begin >= t_end) return;

@@ -12,19 +12,6 @@ namespace aih {
 // Output-channel tile widths that have a kernel instantiation.
 constexpr int kGemmBN[] = {32, 64, 96, 128, 160};
 
-// Compute units of the current device (cached per device ordinal).
-inline int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 // Persistent launch: as many workgroups as fit on the device at once (from
 // the occupancy of this instantiation), capped by the number of tiles.
 template <int DTA, int DTW, int BN, bool IG, bool PAIR>
@@ -35,7 +22,7 @@ hipError_t launch_gemm_inst(const GemmArgs &a, hipStream_t st) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, GEMM_THREADS, 0) != hipSuccess || nb < 1) nb = 1;
     return nb;
   }();
-  const uint32_t slots = (uint32_t)(device_cus() * per_cu);
+  const uint32_t slots = device_cus() * (uint32_t)per_cu;
   const uint32_t grid = std::min(a.ntiles_total, slots);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(GEMM_THREADS), 0, st, a);
   return hipGetLastError();

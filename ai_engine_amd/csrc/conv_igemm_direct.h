@@ -30,6 +30,7 @@ struct IgDirectArgs {
   int32_t PT, PL;
   uint32_t nblk;           // 32-pixel blocks
   int32_t act, has_res;
+  uint32_t nxcd;           // XCDs of the device (workgroup remap)
   FastDiv fd_ohw, fd_ow;
 };
 
@@ -65,7 +66,7 @@ inline uint32_t ig_direct_lds_bytes(uint32_t taps, uint32_t nj, uint32_t N4) {
 }
 
 // Workgroups of a launch: one per 8 work items (a block of 32 pixels times
-// a column group), at most one per CU. A second
+// a column group), at most one per CU of the current device. A second
 // resident workgroup per CU (when registers and LDS allow it) measured
 // slower on every shape tried: its extra loads in flight contend for the
 // same caches (3x3 16 -> 32 stride 2 at 160x288 batch 32, fp32: 62.0 us
@@ -74,7 +75,8 @@ inline uint32_t ig_direct_grid(uint32_t nblk, uint32_t nj, uint32_t N4) {
   (void)nj;
   const uint64_t items = (uint64_t)nblk * ig_direct_ncg(N4);
   const uint64_t want = (items + kIgDirectThreads / 64 - 1) / (kIgDirectThreads / 64);
-  return (uint32_t)(want < 256ull ? want : 256ull);
+  const uint64_t cus = device_cus();
+  return (uint32_t)(want < cus ? want : cus);
 }
 
 hipError_t launch_ig_direct(const IgDirectArgs &a, int dt, hipStream_t st);

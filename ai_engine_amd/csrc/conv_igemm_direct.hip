@@ -103,7 +103,7 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
   // re-read its activations from the cache (ranges go out XCD by XCD so
   // neighbouring blocks, which share input rows, meet in one L2)
   const uint32_t nitems = a.nblk * a.ncg;
-  const uint32_t g = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t g = xcd_remap(blockIdx.x, gridDim.x, a.nxcd);
   const uint32_t b_begin = (uint32_t)(((uint64_t)g * nitems) / gridDim.x);
   const uint32_t b_end = (uint32_t)(((uint64_t)(g + 1) * nitems) / gridDim.x);
 

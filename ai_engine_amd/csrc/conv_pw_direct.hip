@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256) void pw_direct_kernel(PwDirectArgs a) {
 
 template <int DT, int KS, int NOB>
 hipError_t launch_inst(const PwDirectArgs &a, hipStream_t st) {
-  const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblk + 3) / 4, 256u * 8u);
+  const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblk + 3) / 4, device_cus() * 8u);
   hipLaunchKernelGGL((pw_direct_kernel<DT, KS, NOB>), dim3(wgs), dim3(256), 0, st, a);
   return hipGetLastError();
 }

@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
 
 template <int DT, int NOB>
 hipError_t launch_inst(const StemArgs &a, hipStream_t st) {
-  const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblocks + 3) / 4, 256u * 8u);
+  const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblocks + 3) / 4, device_cus() * 8u);
   hipLaunchKernelGGL((conv_stem_kernel<DT, NOB>), dim3(wgs), dim3(256), 0, st, a);
   return hipGetLastError();
 }

@@ -31,6 +31,7 @@ struct IrArgs {
   int32_t act_e, act_d, act_p, has_res;
   int32_t mask_e;        // act_e(0) != 0: expanded halo pixels outside the image are masked to 0
   int32_t clamp_acts;    // all three activations clamp-type (act_is_clamp): branch-free instantiation
+  uint32_t nxcd;         // XCDs of the device (workgroup remap)
   uint32_t lds_x, lds_xe, lds_we, lds_wp, lds_sm, lds_bp;  // LDS byte offsets
   // divisors the kernel uses, prepared on the host
   FastDiv fd_rpx;              // 16-byte items per LDS input row (vectors per pixel + 1)
@@ -49,12 +50,13 @@ struct IrPlan {
 // Chooses the tile and chunk geometry for an inverted-residual block
 // (depthwise 3x3, stride S). Returns nullptr on success, otherwise the reason
 // the block cannot run fused.
-// tile_h / tile_w / ec force that part of the geometry when non-zero.
+// tile_h / tile_w / ec force that part of the geometry when non-zero;
+// weights (enum aih_ir_weights) forces resident or streamed weights.
 // cl: every activation is clamp-type (selects the instantiation whose register
 // use bounds the occupancy).
 const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
                     uint32_t CO, uint32_t S, int dt, bool cl, uint32_t tile_h, uint32_t tile_w, uint32_t ec,
-                    IrPlan *p);
+                    int32_t weights, IrPlan *p);
 
 hipError_t launch_ir_block(const IrArgs &a, int dt, uint32_t lds, uint32_t grid, hipStream_t st);
 

@@ -19,18 +19,6 @@ namespace {
 uint32_t cdiv(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
 
-int cus_of_current_device() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 // Workgroups per CU allowed by registers alone, per instantiation (queried once).
 int reg_occupancy(int dt, uint32_t nob, uint32_t npw, bool cl) {
   static std::mutex mu;
@@ -88,7 +76,7 @@ constexpr uint32_t kMaxLds = 160 * 1024;
 // LDS wins; candidates with a single workgroup per CU pay a latency penalty.
 const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
                     uint32_t CO, uint32_t S, int dt, bool cl, uint32_t tile_h, uint32_t tile_w, uint32_t ec_force,
-                    IrPlan *out) {
+                    int32_t weights, IrPlan *out) {
   if (dt != DT_F32 && dt != DT_F16 && dt != DT_BF16) return "unknown dtype";
   const bool f32 = dt == DT_F32;
   const uint32_t kstep = f32 ? 8 : 16;
@@ -101,14 +89,21 @@ const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t 
   if (ec_force && ec_force != IR_EC) return "the kernel walks E in chunks of 32 channels";
   if ((tile_h && tile_h > OH) || (tile_w && tile_w > OW)) return "forced tile larger than the output";
   if (tile_h && tile_w && (tile_h * tile_w > 256)) return "forced tile above 256 pixels";
+  if (weights != AIH_IR_WEIGHTS_AUTO && weights != AIH_IR_WEIGHTS_RESIDENT && weights != AIH_IR_WEIGHTS_STREAMED)
+    return "unknown weight placement";
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
 
+  // the plan depends on the device (CU count, occupancy) and on the
+  // instantiation (clamp-type activations use fewer registers)
   struct Key {
-    uint32_t v[13];
+    uint32_t v[16];
     bool operator<(const Key &o) const { return std::memcmp(v, o.v, sizeof(v)) < 0; }
   };
   static std::mutex mu;
   static std::map<Key, IrPlan> cache;
-  const Key key{{N, IH, IW, OH, OW, C, E, CO, S, (uint32_t)dt, tile_h, tile_w, ec_force}};
+  const Key key{{N, IH, IW, OH, OW, C, E, CO, S, (uint32_t)dt, tile_h, tile_w, ec_force, (uint32_t)cl,
+                 (uint32_t)weights, (uint32_t)dev}};
   {
     std::lock_guard<std::mutex> lock(mu);
     auto it = cache.find(key);
@@ -118,7 +113,7 @@ const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t 
     }
   }
 
-  const int cus = cus_of_current_device();
+  const int cus = (int)device_cus();
   const uint32_t nob = CO / 32;
   const uint32_t ec = IR_EC, chunks = E / IR_EC;
   // Per-wavefront cycle estimates: one 32-channel chunk of the depthwise +
@@ -134,6 +129,7 @@ const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t 
   double best = 0;
   IrPlan bp{};
   for (uint32_t resident = 0; resident < 2; ++resident) {
+    if ((weights == AIH_IR_WEIGHTS_RESIDENT && !resident) || (weights == AIH_IR_WEIGHTS_STREAMED && resident)) continue;
     for (uint32_t tw = 4; tw <= 64; tw *= 2) {
       const uint32_t twx = tile_w ? tile_w : std::min(tw, OW);
       for (uint32_t th = 1; th <= 32; ++th) {

@@ -217,7 +217,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   const uint32_t WES = EC * a.C * ES, WPS = EC * a.CO * ES;  // bytes of one slot
   const Act act_e = act_params(a.act_e), act_d = act_params(a.act_d), act_p = act_params(a.act_p);
 
-  const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x, a.nxcd);
   const uint32_t t_begin = (uint32_t)(((uint64_t)blk * a.ntiles) / gridDim.x);
   const uint32_t t_end = (uint32_t)(((uint64_t)(blk + 1) * a.ntiles) / gridDim.x);
   if (t_begin >= t_end) return;

@@ -45,7 +45,10 @@ struct Value {
   }
   size_t size() const { return kind == Array ? arr.size() : kind == Object ? obj.size() : 0; }
   uint64_t u64() const {
-    if (kind != Number || num < 0 || num != (double)(uint64_t)num) throw std::runtime_error("json: expected an unsigned integer");
+    // range first: converting a double at or above 2^64 (or NaN) to an
+    // integer is undefined behaviour
+    if (kind != Number || !(num >= 0.0 && num < 18446744073709551616.0) || num != (double)(uint64_t)num)
+      throw std::runtime_error("json: expected an unsigned integer");
     return (uint64_t)num;
   }
   uint32_t u32() const {

@@ -256,6 +256,118 @@ void alloc_tensors(aih_model *m) {
   }
 }
 
+// Every op's geometry against the tensors and weight ranges the file declares,
+// before any device work: the kernels index their buffers by the op's own
+// fields, so a mismatched file must not reach them (the reference's wgpu
+// runtime gets bounds-checked buffers; here the arena and the weight blob are
+// plain device memory). Weight lengths are in the file's element size:
+// dt_weights for the packed std-conv weights, dt_default for depthwise
+// weights, biases and constant channel vectors (format/model.rs:245-254).
+void validate_geometry(const sw::Model &g) {
+  const auto &T = g.tensors;
+  const uint64_t es_d = g.dt_default == sw::F16 ? 2 : 4, es_w = g.dt_weights == sw::F16 ? 2 : 4;
+  auto c4u = [](uint64_t c) { return (c + 3) / 4 * 4; };
+  for (size_t k = 0; k < g.ops.size(); ++k) {
+    const sw::Op &op = g.ops[k];
+    const std::string at = ".sw: op " + std::to_string(k) + ": ";
+    auto shape = [&](uint32_t tid) {
+      return T[tid].name + " " + std::to_string(T[tid].h) + "x" + std::to_string(T[tid].w) + "x" +
+             std::to_string(T[tid].c);
+    };
+    auto same_hw = [&](uint32_t a, uint32_t b) { return T[a].h == T[b].h && T[a].w == T[b].w; };
+    auto parts_c = [&](const std::vector<sw::Part> &ps) {
+      uint64_t c = 0;
+      for (const sw::Part &p : ps) {
+        if (p.c == 0 || p.c > T[p.tid].c) throw sw::Error(at + "part of " + std::to_string(p.c) + " channels in " + shape(p.tid));
+        c += p.c;
+      }
+      return c;
+    };
+    const auto &O = T[op.out];
+    switch (op.kind) {
+      case sw::OP_CONV: {
+        const auto &I = T[op.in];
+        if (!op.groups || !op.kh || !op.kw || !op.sh || !op.sw || !op.d || !op.cin || !op.cout)
+          throw sw::Error(at + "conv with a zero-sized attribute");
+        const uint64_t ekh = (uint64_t)op.d * (op.kh - 1) + 1, ekw = (uint64_t)op.d * (op.kw - 1) + 1;
+        if (I.h + (uint64_t)op.pad[0] + op.pad[2] < ekh || I.w + (uint64_t)op.pad[1] + op.pad[3] < ekw)
+          throw sw::Error(at + "kernel larger than the padded input " + shape(op.in));
+        const uint64_t oh = (I.h + (uint64_t)op.pad[0] + op.pad[2] - ekh) / op.sh + 1;
+        const uint64_t ow = (I.w + (uint64_t)op.pad[1] + op.pad[3] - ekw) / op.sw + 1;
+        if (O.h != oh || O.w != ow || O.c != op.cout)
+          throw sw::Error(at + "output " + shape(op.out) + " but the conv makes " + std::to_string(oh) + "x" +
+                          std::to_string(ow) + "x" + std::to_string(op.cout));
+        if (op.srcs.empty()) {
+          if (I.c != op.cin) throw sw::Error(at + "input " + shape(op.in) + " but cin " + std::to_string(op.cin));
+        } else {
+          if (parts_c(op.srcs) != op.cin) throw sw::Error(at + "concat parts do not add up to cin");
+          for (const sw::Part &p : op.srcs)
+            if (!same_hw(p.tid, op.in)) throw sw::Error(at + "concat part " + shape(p.tid) + " of another size");
+        }
+        if (op.res >= 0 && (T[op.res].h != O.h || T[op.res].w != O.w || T[op.res].c != O.c))
+          throw sw::Error(at + "residual " + shape((uint32_t)op.res) + " is not the output's shape");
+        const uint64_t taps = (uint64_t)op.kh * op.kw;
+        uint64_t wlen;
+        if (op.groups > 1) {
+          wlen = taps * c4u(op.cout) * es_d;
+        } else {
+          if (op.kg_pad < (op.cin + 3) / 4) throw sw::Error(at + "kg_pad below ceil(cin / 4)");
+          wlen = taps * op.kg_pad * c4u(op.cout) * 4 * es_w;
+        }
+        if (op.w.len != wlen)
+          throw sw::Error(at + "weights of " + std::to_string(op.w.len) + " bytes, the packed layout needs " +
+                          std::to_string(wlen));
+        if (op.b.len != c4u(op.cout) * es_d)
+          throw sw::Error(at + "bias of " + std::to_string(op.b.len) + " bytes, needs " +
+                          std::to_string(c4u(op.cout) * es_d));
+        break;
+      }
+      case sw::OP_BINARY: {
+        if (!same_hw(op.in, op.out) || T[op.in].c != O.c)
+          throw sw::Error(at + "binary input " + shape(op.in) + " and output " + shape(op.out) + " differ");
+        const auto *B = op.opnd == sw::OPND_SCALAR || op.opnd == sw::OPND_CVEC ? nullptr : &T[op.b_tid];
+        bool ok = true;
+        switch (op.opnd) {
+          case sw::OPND_TENSOR: ok = B->h == O.h && B->w == O.w && B->c == O.c; break;
+          case sw::OPND_CVEC: ok = op.cvec_c == O.c && op.cvec.len == c4u(O.c) * es_d; break;
+          case sw::OPND_CVEC_TENSOR: ok = B->h == 1 && B->w == 1 && (B->c == 1 || B->c == O.c); break;
+          case sw::OPND_PVEC_TENSOR:
+            ok = (B->c == 1 && B->h == O.h && B->w == O.w) ||
+                 (B->h == 1 && B->w == 1 && (uint64_t)B->c == (uint64_t)O.h * O.w);
+            break;
+          case sw::OPND_TILED_TENSOR: ok = B->h == 1 && B->w == 1 && B->c > 0; break;
+          default: break;
+        }
+        if (!ok) throw sw::Error(at + "binary operand does not fit the output " + shape(op.out));
+        break;
+      }
+      case sw::OP_GPOOL:
+        if (O.h != 1 || O.w != 1 || O.c != T[op.in].c)
+          throw sw::Error(at + "gpool of " + shape(op.in) + " into " + shape(op.out));
+        break;
+      case sw::OP_RESIZE: {
+        if (O.h != op.oh || O.w != op.ow || !op.oh || !op.ow)
+          throw sw::Error(at + "resize to " + std::to_string(op.oh) + "x" + std::to_string(op.ow) + " into " + shape(op.out));
+        if (op.srcs.empty()) {
+          if (T[op.in].c != O.c) throw sw::Error(at + "resize of " + shape(op.in) + " into " + shape(op.out));
+        } else {
+          if (parts_c(op.srcs) != O.c) throw sw::Error(at + "resize parts do not add up to the output channels");
+          for (const sw::Part &p : op.srcs)
+            if (!same_hw(p.tid, op.in)) throw sw::Error(at + "resize part " + shape(p.tid) + " of another size");
+        }
+        break;
+      }
+      case sw::OP_CONCAT: {
+        if (op.srcs.empty() || parts_c(op.srcs) != O.c)
+          throw sw::Error(at + "concat parts do not add up to the output channels");
+        for (const sw::Part &p : op.srcs)
+          if (!same_hw(p.tid, op.out)) throw sw::Error(at + "concat part " + shape(p.tid) + " of another size");
+        break;
+      }
+    }
+  }
+}
+
 void need_dense(const aih_model *m, uint32_t tid, const char *role, size_t op_index) {
   if (!m->dense(tid))
     throw sw::Error(".sw: op " + std::to_string(op_index) + ": " + role + " '" + m->g.tensors[tid].name +
@@ -455,6 +567,7 @@ aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt)
       m->dt = m->wdt = dt;
     }
     if (!m->g.consts.empty()) return api_fail("model_load: constant tensors are not supported");
+    validate_geometry(m->g);
     prepare_weights(m.get(), c);
     alloc_tensors(m.get());
     lower(m.get());
@@ -641,6 +754,7 @@ int aih_sw_describe(const void *bytes, size_t len, char *buf, size_t buflen) {
   return api_guarded([&] {
     sw::Container c = sw::parse_container(bytes, len);
     sw::Model g = sw::parse_model(c.json, c.json_len);
+    validate_geometry(g);
     int counts[5] = {0, 0, 0, 0, 0};
     for (const auto &op : g.ops) ++counts[op.kind];
     int aliases = 0;

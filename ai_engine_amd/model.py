@@ -18,17 +18,24 @@ three launches.
 
 Load-time tuning (tune=True, the default): for every fusable block the
 candidates -- the three separate launches, and the fused launch at the
-planner's tile and at a set of forced tiles -- are timed on the device at
-load, a few launches each, and the fastest is kept (like the reference's
-Model::load, which does its per-model work -- pipeline compilation -- once at
-load). fuse="auto" lets the timing choose between fused and separate; True
-keeps only fused candidates, False never fuses. With tune=False the planner's
-tile is used and "auto" fuses 16-bit models only.
+planner's tile and at a set of forced tiles, each with its weights resident
+in LDS and streamed -- are timed on the device at load, a few launches each,
+and the fastest is kept (like the reference's Model::load, which does its
+per-model work -- pipeline compilation -- once at load). fuse="auto" lets the
+timing choose between fused and separate; True keeps only fused candidates,
+False never fuses. With tune=False the planner's tile is used and "auto"
+fuses 16-bit models only.
+
+The choice per block is recorded (choice_map()) and can be given back
+(choices={block: label}), so a later load runs exactly the same kernels; a
+label is "unfused", "fused THxTW" (streamed weights) or "fused THxTW
+resident" -- fused_candidates() lists the labels a block can take.
 """
 from __future__ import annotations
 
 import ctypes as C
 import dataclasses
+import re
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -90,7 +97,7 @@ class Model:
 
     def __init__(self, layers: list[Layer], weights: Weights, n: int, ih: int, iw: int, cin: int,
                  dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0",
-                 fuse="auto", tune: bool = True):
+                 fuse="auto", tune: bool = True, choices: dict[str, str] | None = None):
         self.layers = layers
         self.n, self.ih, self.iw, self.cin = n, ih, iw, cin
         self.dt = conv.DType(dt)
@@ -125,7 +132,11 @@ class Model:
             fuse = self.dt != conv.DType.F32
         i = 0
         while i < len(layers):
-            blk = self._match_block(layers, i, readers) if fuse else None
+            blk = self._match_block(layers, i, readers) if (fuse or choices) else None
+            if blk is not None and choices is not None:
+                self.ops.extend(self._chosen_block(blk, packed, L, choices))
+                i += 3
+                continue
             if blk is not None:
                 if tune:
                     self.ops.extend(self._tuned_block(blk, packed, L, allow_unfused=fuse == "auto"))
@@ -159,6 +170,66 @@ class Model:
             return None
         return (e, d, p, spec)
 
+    @classmethod
+    def fused_candidates(cls, spec: conv.IrBlockSpec) -> list[tuple[str, conv.IrBlockSpec]]:
+        """The fused launches the tuner times for a block: the planner's tile
+        and every TUNE_TILES entry, each with resident and streamed weights
+        (the ones that fit), as (label, spec with the tile and placement
+        forced); duplicates dropped."""
+        out, seen = [], set()
+        for tile in [(0, 0)] + cls.TUNE_TILES:
+            for w in (conv.IrWeights.RESIDENT, conv.IrWeights.STREAMED):
+                sp = dataclasses.replace(spec, tile=tile, weights=w)
+                if not sp.fusable():
+                    continue
+                pl = sp.plan()
+                key = (pl.th, pl.tw, pl.resident)
+                if key in seen:
+                    continue
+                seen.add(key)
+                out.append((cls.label_of(pl.th, pl.tw, pl.resident),
+                            dataclasses.replace(spec, tile=(pl.th, pl.tw), weights=w)))
+        return out
+
+    @staticmethod
+    def label_of(th: int, tw: int, resident: bool) -> str:
+        return f"fused {th}x{tw}{' resident' if resident else ''}"
+
+    @staticmethod
+    def parse_label(label: str):
+        """"unfused" -> None; "fused THxTW[ resident]" -> ((th, tw), IrWeights)."""
+        if label == "unfused":
+            return None
+        m = re.fullmatch(r"fused (\d+)x(\d+)( resident)?", label)
+        if not m:
+            raise ValueError(f"unknown block choice {label!r}")
+        w = conv.IrWeights.RESIDENT if m.group(3) else conv.IrWeights.STREAMED
+        return (int(m.group(1)), int(m.group(2))), w
+
+    def choice_map(self) -> dict[str, str]:
+        """Block -> the label of the launch it runs (feed back as choices=)."""
+        return {k: v[0] for k, v in self.choices.items()}
+
+    def _block_name(self, p) -> str:
+        return p.name.rsplit(".", 1)[0]
+
+    def _chosen_block(self, blk, packed, L, choices) -> list:
+        """The block as `choices` names it (no timing); a block missing from
+        the map runs unfused."""
+        e, d, p, spec = blk
+        label = choices.get(self._block_name(p), "unfused")
+        forced = self.parse_label(label)
+        self.choices[self._block_name(p)] = (label, float("nan"))
+        if forced is None:
+            return [self._conv_op(Lr, packed, L) for Lr in (e, d, p)]
+        tile, w = forced
+        sp = dataclasses.replace(spec, tile=tile, weights=w)
+        pl = sp.plan()
+        if (pl.th, pl.tw, bool(pl.resident)) != (tile[0], tile[1], w == conv.IrWeights.RESIDENT):
+            raise conv.AihError(f"{self._block_name(p)}: {label!r} planned as "
+                                f"{self.label_of(pl.th, pl.tw, pl.resident)!r}")
+        return [self._fused_op((e, d, p, sp), packed, L)]
+
     def _tuned_block(self, blk, packed, L, allow_unfused: bool) -> list:
         """Times the block's candidates on the device and returns the fastest
         one's ops (an unfused winner keeps its intermediates)."""
@@ -170,21 +241,11 @@ class Model:
             oh, ow = p.out_hw()
             self.tensors[p.name] = self._alloc(oh, ow, p.cout)
         y = self.tensors[p.name]
-        seen = set()
-        for tile in [(0, 0)] + self.TUNE_TILES:
-            sp = dataclasses.replace(spec, tile=tile)
-            if not sp.fusable():
-                continue
-            pl = sp.plan()
-            key = (pl.th, pl.tw, pl.resident)
-            if key in seen:
-                continue
-            seen.add(key)
-            cands.append((f"fused {pl.th}x{pl.tw}{' resident' if pl.resident else ''}",
-                          [self._fused_op((e, d, p, sp), packed, L, y=y)]))
+        for label, sp in self.fused_candidates(spec):
+            cands.append((label, [self._fused_op((e, d, p, sp), packed, L, y=y)]))
         timed = [(self._time_ops(ops), label, ops) for label, ops in cands]
         us, label, ops = min(timed, key=lambda t: t[0])
-        self.choices[p.name.rsplit(".", 1)[0]] = (label, us)
+        self.choices[self._block_name(p)] = (label, us)
         if label != "unfused":
             for nm in (e.name, d.name):
                 self.tensors.pop(nm, None)

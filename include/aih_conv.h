@@ -30,6 +30,13 @@
  *                activation: y = act(acc + bias) + res (reference/conv.rs:53-56).
  * dtypes: AIH_F32 / AIH_F16 as ai-core DType; AIH_BF16 is new. Accumulation
  * is always fp32.
+ *
+ * Diagnostic environment overrides, read once per process (like the
+ * reference's AI_PW_SPLITK_NG, gemm_pw.rs:112-126, and AI_RT_FORCE_DIRECT,
+ * lowering.rs:156-160); they apply to AIH_VAR_AUTO calls without a forced
+ * split only, and the plan functions report their effect:
+ *   AIH_PW_SPLITK=<n>     a pointwise conv on the tiled GEMM uses n K chunks (1 = no split)
+ *   AIH_IGEMM_NO_SPLIT=1  a KxK conv never splits K
  */
 #ifndef AIH_CONV_H
 #define AIH_CONV_H
@@ -172,7 +179,13 @@ typedef struct {
   int32_t dt;
   uint32_t tile_h, tile_w; /* output tile; 0 = chosen by the plan */
   uint32_t ec;             /* expanded channels per chunk; 0 = chosen by the plan */
+  int32_t weights;         /* enum aih_ir_weights: where the expand / project weights live */
 } aih_ir_block_desc;
+
+/* Weight placement of a fused block: chosen by the plan (resident when they
+ * fit), all of them resident in LDS for every tile, or streamed chunk by
+ * chunk through two LDS slots. */
+enum aih_ir_weights { AIH_IR_WEIGHTS_AUTO = 0, AIH_IR_WEIGHTS_RESIDENT = 1, AIH_IR_WEIGHTS_STREAMED = 2 };
 
 /* Geometry aih_ir_block_plan chose: output tile th x tw, expanded channels
  * per chunk, whether all expand/project weights stay resident in LDS, LDS
@@ -215,6 +228,10 @@ int aih_conv_dw(const aih_dw_desc *d, const void *x, const void *w, const void *
 int aih_conv(const aih_conv_desc *d, const void *x, const void *w, const void *bias,
              const void *res, void *y, void *ws, size_t ws_bytes, aih_stream stream);
 size_t aih_conv_workspace_size(const aih_conv_desc *d);
+/* The plan aih_conv would run for d: the pointwise or implicit-GEMM plan of
+ * its route; a depthwise conv reports AIH_VAR_DIRECT with bm = bn = grid = 0
+ * (one kernel, no workspace). */
+int aih_conv_plan(const aih_conv_desc *d, aih_plan *out);
 /* Validates a descriptor as aih_conv would (routing, shapes, dtypes, plan)
  * without launching: AIH_OK, or AIH_ERR with the reason (lower_op's load-time
  * rejection of a conv it cannot run, lowering.rs:136-140). */

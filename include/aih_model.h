@@ -162,9 +162,12 @@ int aih_model_get_info(const aih_model *m, aih_model_info *out);
 const char *aih_model_input_name(const aih_model *m, uint32_t i);
 const char *aih_model_output_name(const aih_model *m, uint32_t i);
 
-/* Parses a .sw container without a device and writes a one-line JSON summary
- * (name, dtypes, tensor / op counts per kind) into buf. Returns the summary's
- * length, or AIH_ERR (the container or graph is invalid or unsupported). */
+/* Parses a .sw container without a device, checks every op's geometry as
+ * aih_model_load does before any device work (output / residual / operand /
+ * part shapes against the op, weight and bias lengths against the packed
+ * layouts), and writes a one-line JSON summary (name, dtypes, tensor / op
+ * counts per kind) into buf. Returns the summary's length, or AIH_ERR (the
+ * container or graph is invalid, inconsistent or unsupported). */
 int aih_sw_describe(const void *bytes, size_t len, char *buf, size_t buflen);
 
 #ifdef __cplusplus

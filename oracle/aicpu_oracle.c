@@ -60,6 +60,10 @@ float orc_act_apply(int32_t act, float x) {
   }
 }
 
+void orc_act_apply_n(int32_t act, const float *x, float *y, size_t n) {
+  for (size_t i = 0; i < n; ++i) y[i] = orc_act_apply(act, x[i]);
+}
+
 /* ai-cpu apply4 -- crates/ai-cpu/src/kernels/mod.rs:21-50.  Differs from the
  * scalar apply for the hard activations: it multiplies by (1/6) instead of
  * dividing by 6, and chains max/min instead of clamp. */

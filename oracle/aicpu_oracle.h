@@ -76,6 +76,8 @@ typedef struct {
 /* ---- ai-core ---- */
 void orc_out_hw(const orc_conv2d *op, uint32_t ih, uint32_t iw, uint32_t *oh, uint32_t *ow);
 float orc_act_apply(int32_t act, float x);
+/* orc_act_apply over n values (y may alias x) */
+void orc_act_apply_n(int32_t act, const float *x, float *y, size_t n);
 void orc_act_apply4(int32_t act, float v[4]);
 
 uint32_t orc_xs32_seed(uint32_t seed);

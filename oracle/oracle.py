@@ -76,6 +76,7 @@ def lib():
             "orc_out_hw": (None, [C.POINTER(Conv2d), u32, u32, C.POINTER(u32), C.POINTER(u32)]),
             "orc_act_apply": (f32, [i32, f32]),
             "orc_act_apply4": (None, [i32, P]),
+            "orc_act_apply_n": (None, [i32, P, P, C.c_size_t]),
             "orc_xs32_seed": (u32, [u32]),
             "orc_xs32_next": (u32, [C.POINTER(u32)]),
             "orc_xs32_next_f32": (f32, [C.POINTER(u32)]),
@@ -146,6 +147,14 @@ def out_hw(op: Conv2d, ih: int, iw: int) -> tuple[int, int]:
 
 def act_apply(act: str | int, x: float) -> float:
     return lib().orc_act_apply(ACT[act] if isinstance(act, str) else act, x)
+
+
+def act_array(act: str | int, x) -> np.ndarray:
+    """Activation::apply (activation.rs:28-43) element-wise over an array."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_act_apply_n(ACT[act] if isinstance(act, str) else act, _p(x), _p(y), x.size)
+    return y
 
 
 def xs32_fill(seed: int, n: int) -> np.ndarray:

@@ -253,3 +253,87 @@ def test_ir_block_rejects_unfusable_shapes():
     L = conv.lib()
     assert L.aih_ir_block(C.byref(d), 16, 16, 16, 16, 16, 16, 16, None, 16, None) == -1
     assert "res must be given" in conv.last_error()
+
+
+# ---------------------------------------------------------------- diagnostic overrides, forced placement
+
+def _plan_in_subprocess(env: dict, code: str) -> str:
+    """Runs `code` (printing its result) in a fresh interpreter with env set:
+    the overrides are read once per process."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    e = dict(os.environ)
+    e.update(env)
+    r = subprocess.run([sys.executable, "-c", "import sys; sys.path.insert(0, %r)\n" % root + code],
+                       capture_output=True, text=True, env=e, timeout=120)
+    assert r.returncode == 0, r.stderr
+    return r.stdout.strip()
+
+
+PW_SPLITK_PROBE = (
+    "from ai_engine_amd import conv\n"
+    "p = conv.GemmPwSpec(m=180, kg=240, ng=40).plan()\n"
+    "q = conv.GemmPwSpec(m=180, kg=240, ng=40, splitk=8).plan()\n"
+    "print(p.splitk, q.splitk)\n")
+IG_SPLIT_PROBE = (
+    "from ai_engine_amd import conv\n"
+    "s = conv.ConvIgemmSpec(ih=9, iw=16, cin=240, cout=96, k=3, pad=(1, 1, 1, 1))\n"
+    "print(s.plan().splitk)\n")
+
+
+def test_env_overrides_of_the_split_policy():
+    # unset: the policy splits the skinny 960 -> 160 layer
+    base = int(_plan_in_subprocess({"AIH_PW_SPLITK": ""}, PW_SPLITK_PROBE).split()[0])
+    assert base > 1
+    # AIH_PW_SPLITK forces the factor of AUTO calls; an explicit split still wins
+    assert _plan_in_subprocess({"AIH_PW_SPLITK": "3"}, PW_SPLITK_PROBE).split() == ["3", "8"]
+    assert _plan_in_subprocess({"AIH_PW_SPLITK": "1"}, PW_SPLITK_PROBE).split() == ["1", "8"]
+    # malformed values are ignored
+    assert int(_plan_in_subprocess({"AIH_PW_SPLITK": "x"}, PW_SPLITK_PROBE).split()[0]) == base
+    # AIH_IGEMM_NO_SPLIT keeps a small-M, long-K 3x3 conv whole
+    assert int(_plan_in_subprocess({"AIH_IGEMM_NO_SPLIT": ""}, IG_SPLIT_PROBE)) > 1
+    assert int(_plan_in_subprocess({"AIH_IGEMM_NO_SPLIT": "1"}, IG_SPLIT_PROBE)) == 1
+
+
+def test_ir_block_forced_weight_placement():
+    base = dict(ih=40, iw=72, cin=64, cexp=256, cout=64, s=1, n=64, dt=conv.DType.F16)
+    for tile in [(0, 0), (8, 8), (4, 16)]:
+        r = conv.IrBlockSpec(tile=tile, weights=conv.IrWeights.RESIDENT, **base).plan()
+        s = conv.IrBlockSpec(tile=tile, weights=conv.IrWeights.STREAMED, **base).plan()
+        assert r.resident == 1 and s.resident == 0, tile
+        if tile != (0, 0):
+            assert (r.th, r.tw) == tile and (s.th, s.tw) == tile
+        # streamed weights take two chunk slots; resident ones all of E
+        assert r.lds_bytes > s.lds_bytes
+    d = conv.IrBlockSpec(weights=7, **base).desc()
+    p = conv.IrPlan()
+    assert conv.lib().aih_ir_block_plan(C.byref(d), C.byref(p)) == -1
+    assert "weight placement" in conv.last_error()
+
+
+def test_ir_block_plan_depends_on_the_activations():
+    """Clamp-type and other activations run different instantiations (with
+    different register use): the plan cache keeps them apart."""
+    A = conv.Activation
+    base = dict(ih=40, iw=72, cin=64, cexp=256, cout=64, s=1, n=64, dt=conv.DType.F16)
+    p1 = conv.IrBlockSpec(act_project=A.NONE, **base).plan()
+    p2 = conv.IrBlockSpec(act_project=A.SIGMOID, **base).plan()
+    p3 = conv.IrBlockSpec(act_project=A.NONE, **base).plan()
+    assert (p1.th, p1.tw, p1.occupancy) == (p3.th, p3.tw, p3.occupancy)
+    assert p1.occupancy >= 1 and p2.occupancy >= 1
+
+
+def test_conv_plan_reports_the_route():
+    A = conv.Activation
+    pw = conv.ConvOp(ih=80, iw=144, cin=32, cout=64, act=A.RELU6)
+    assert pw.plan().variant == conv.Variant.DIRECT
+    assert conv.ConvOp(ih=10, iw=18, cin=960, cout=160).plan().variant == conv.Variant.SPLITK
+    ig = conv.ConvOp(ih=40, iw=72, cin=32, cout=64, kh=3, kw=3, pad=(1, 1, 1, 1))
+    assert ig.plan().variant == conv.Variant.DIRECT
+    dw = conv.ConvOp(ih=40, iw=72, cin=32, cout=32, kh=3, kw=3, pad=(1, 1, 1, 1), groups=32)
+    p = dw.plan()
+    assert p.variant == conv.Variant.DIRECT and p.grid == 0 and p.ws_bytes == 0
+    _expect_error(conv.ConvOp(ih=8, iw=8, cin=8, cout=8, sh=2, sw=2).plan, "stride/pad")

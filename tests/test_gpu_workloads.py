@@ -337,3 +337,114 @@ def test_mnv4_small_encoder_fused(dt):
     assert s_f <= 1.5 * s_u + 2e-3, (s_f, s_u)
     if dt == F16:
         assert e2e <= 3 * ideal + 1e-3, (e2e, ideal)
+
+
+# ---------------------------------------------------------------- the benchmarked routes at full batch
+
+BAR_STORED = {F32: 1e-4, F16: 2e-3, BF16: 8e-3}
+
+
+def image_of(m, name, i, dt):
+    """Image i of model tensor `name` as the GPU stores it, unpacked to logical NHWC fp32."""
+    h, w, c = m.shapes[name]
+    t = m.tensors[name].view(m.n, -1)[i]
+    return orc.unpack_nhwc(G.host(t, dt), 1, h, w, c, dt)
+
+
+def local_op_error(m, op, i, wts, dt):
+    """One launch of a loaded model on image i, against the oracle run of the
+    same ops on the launch's own stored input (and residual) with the weights
+    rounded to dt, every stored intermediate rounded to dt: the kernel's error
+    alone, whatever the layers before it contributed."""
+    rd = (lambda v: v) if dt == F32 else (lambda v: orc.round_to(v, dt))
+    first = op.layers[0]
+    buf = image_of(m, first.src, i, dt)
+    for L in op.layers:
+        cop = orc.conv2d(L.cin, L.cout, k=L.k, s=L.s, pad=L.pad, groups=L.groups, act=L.act)
+        cc = orc.CpuConv(cop, L.ih, L.iw, rd(wts.w[L.name]), rd(wts.b[L.name]), has_res=L.res is not None)
+        buf = rd(cc.run(buf, 1, image_of(m, L.res, i, dt) if L.res else None, threads=8))
+    return G.rel_err(image_of(m, op.layers[-1].name, i, dt), buf)
+
+
+@pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
+def test_encoder_b64_as_benched(dt):
+    """The headline configuration exactly as bench.py loads it: batch 64, the
+    same He-init weights (seed 0), load-time tuning on. Every launch the tuned
+    model runs -- the stem, each block as the tuner chose it (fused at its
+    chosen tile and weight placement, or three launches), the head -- is
+    checked on sampled images against the oracle on its own stored inputs
+    (<= 2e-3 f16, 8e-3 bf16; fp32 arithmetic and storage rounding where the
+    unfused path stores). The choice map is printed; the end-to-end drift
+    from the fp32 chain is printed next to what ideal storage gives."""
+    layers, meta = W.mnv4_small_encoder_160x288(64)
+    wts = W.make_weights(layers, seed=0)
+    n, h, w = 64, meta["h"], meta["w"]
+    x = orc.xs32_fill(6400, n * h * w * 3)
+    m = Model(layers, wts, n, h, w, 3, dt=conv.DType(dt))
+    print(f"encoder b64 dt{dt} choices: {m.choice_map()}", flush=True)
+    m.upload_input(G.dev(x))
+    m.infer()
+    torch.cuda.synchronize()
+    worst = {}
+    for i in sample_images(n):
+        for op in m.ops:
+            worst[op.name] = max(worst.get(op.name, 0.0), local_op_error(m, op, i, wts, dt))
+    print("  local per launch: " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()), flush=True)
+    bad = {k: v for k, v in worst.items() if v > BAR_STORED[dt]}
+    assert not bad, bad
+    img = h * w * 3
+    i = n - 1
+    ref = oracle_chain(layers, wts, x[i * img:(i + 1) * img], h, w)[layers[-1].name]
+    ideal = oracle_chain_stored(layers, wts, x[i * img:(i + 1) * img], dt)[layers[-1].name]
+    got = image_of(m, layers[-1].name, i, dt)
+    print(f"  image {i} end to end vs fp32 chain: {G.rel_err(got, ref):.3e} "
+          f"(ideal {('f16', 'bf16')[dt - 1]} storage {G.rel_err(ideal, ref):.3e}; rms-scaled "
+          f"{scaled_err(got, ref):.3e})", flush=True)
+
+
+def test_ir_chain_b64_as_benched_f32():
+    """The fp32 four-block chain exactly as bench.py loads it (batch 64,
+    load-time tuning between fused and three launches): sampled images end
+    to end within 1e-4 of the oracle's fp32 chain, and every launch locally."""
+    layers, meta = W.ir_chain_40x72(64)
+    wts = oracle_weights(layers, 5)
+    n = 64
+    x = orc.xs32_fill(5002, n * meta["h"] * meta["w"] * meta["c"])
+    m = Model(layers, wts, n, meta["h"], meta["w"], meta["c"], dt=conv.DType.F32)
+    print(f"ir chain b64 f32 choices: {m.choice_map()}", flush=True)
+    m.upload_input(G.dev(x))
+    m.infer()
+    torch.cuda.synchronize()
+    img = meta["h"] * meta["w"] * meta["c"]
+    e2e = local = 0.0
+    for i in sample_images(n):
+        ref = oracle_chain(layers, wts, x[i * img:(i + 1) * img], meta["h"], meta["w"])[layers[-1].name]
+        e2e = max(e2e, G.rel_err(image_of(m, layers[-1].name, i, F32), ref))
+        for op in m.ops:
+            local = max(local, local_op_error(m, op, i, wts, F32))
+    report("ir chain b64 f32 as benched, end to end", e2e, 1e-4)
+    report("ir chain b64 f32 as benched, local", local, 1e-4)
+
+
+def test_ir_chain_b64_unfused_one_tap_route_f32():
+    """The four fp32 blocks as three launches each at batch 64: expand and
+    project take the one-tap direct route (weights in LDS, M >= 2048 blocks
+    of 32 pixels); sampled images within 1e-4 of the oracle's fp32 chain."""
+    layers, meta = W.ir_chain_40x72(64)
+    wts = oracle_weights(layers, 5)
+    n = 64
+    x = orc.xs32_fill(5003, n * meta["h"] * meta["w"] * meta["c"])
+    m = Model(layers, wts, n, meta["h"], meta["w"], meta["c"], dt=conv.DType.F32, fuse=False)
+    for op in m.ops:
+        L = op.layers[0]
+        if not L.depthwise:
+            p = op.spec.plan()
+            assert p.variant == conv.Variant.DIRECT and p.bm == 32, (op.name, p)
+    m.upload_input(G.dev(x))
+    m.infer()
+    torch.cuda.synchronize()
+    img = meta["h"] * meta["w"] * meta["c"]
+    e2e = max(G.rel_err(image_of(m, layers[-1].name, i, F32),
+                        oracle_chain(layers, wts, x[i * img:(i + 1) * img], meta["h"], meta["w"])[layers[-1].name])
+              for i in sample_images(n))
+    report("ir chain b64 f32 unfused (one-tap direct expand / project)", e2e, 1e-4)

@@ -132,6 +132,29 @@ def test_activation_kats(orc):
         assert orc.act_apply("none", x) == x
 
 
+def test_activation_closed_forms_and_array(orc):
+    """Every activation against its closed form (activation.rs:28-43), and the
+    array form (what the GPU activation tests compare with) equal to the
+    scalar one element for element."""
+    import math
+
+    xs = np.array([-30.0, -7.5, -3.0, -1.0, -0.0, 1e-3, 0.25, 1.0, 2.0, 5.999, 6.0, 9.0, 30.0], np.float32)
+    f = {
+        "none": lambda x: x, "relu": lambda x: max(x, 0.0), "sigmoid": lambda x: 1.0 / (1.0 + math.exp(-x)),
+        "tanh": math.tanh, "hardswish": lambda x: x * min(max(x / 6.0 + 0.5, 0.0), 1.0),
+        "hardsigmoid": lambda x: min(max(x / 6.0 + 0.5, 0.0), 1.0), "clamp01": lambda x: min(max(x, 0.0), 1.0),
+        "relu6": lambda x: min(max(x, 0.0), 6.0), "sqrt": lambda x: math.sqrt(max(x, 0.0)), "neg": lambda x: -x,
+        "recip": lambda x: 1.0 / x if x != 0 else math.copysign(math.inf, x),
+    }
+    assert set(f) == set(orc.ACT)
+    for name, fn in f.items():
+        arr = orc.act_array(name, xs)
+        for x, y in zip(xs.tolist(), arr.tolist()):
+            assert y == orc.act_apply(name, x), (name, x)
+            want = fn(x)
+            assert abs(y - want) <= 2e-7 * max(abs(want), 1.0) or (math.isinf(want) and y == want), (name, x, y, want)
+
+
 # ---------------------------------------------------------------- dtype conversion
 
 def test_f16_matches_ieee_rne(orc):

@@ -168,3 +168,55 @@ def test_json_strings_with_escapes():
     g["name"] = "tést \"q\" \\ 中"
     d = json.loads(json.dumps(sw.describe(sw.write_container(g, bytes(544)))))
     assert d["name"] == g["name"]
+
+
+# ---------------------------------------------------------------- load-time geometry checks (no device)
+
+def _edited(segm, edit):
+    from oracle import sw_oracle
+
+    g, blob = sw_oracle.read_container(segm)
+    g = json.loads(json.dumps(g))
+    edit(g)
+    return sw.write_container(g, blob)
+
+
+def _first(g, kind, pred=lambda o: True):
+    return next(o for o in g["ops"] if o["kind"] == kind and pred(o))
+
+
+@pytest.mark.parametrize("what,edit,fragment", [
+    ("conv output height", lambda g: g["tensors"][g["ops"][0]["out"]].__setitem__("h", 81), "but the conv makes"),
+    ("conv output channels", lambda g: g["tensors"][g["ops"][0]["out"]].__setitem__("c", 31), "but the conv makes"),
+    ("conv input channels", lambda g: g["ops"][1].__setitem__("cin", g["ops"][1]["cin"] + 4), "cin"),
+    ("weight length", lambda g: g["ops"][0]["w"].__setitem__("len", g["ops"][0]["w"]["len"] - 256),
+     "packed layout needs"),
+    ("bias length", lambda g: g["ops"][0]["b"].__setitem__("len", 64), "bias of 64 bytes"),
+    ("kg_pad", lambda g: _first(g, "conv", lambda o: o["cin"] > 8 and o["groups"] == 1).__setitem__("kg_pad", 1),
+     "kg_pad"),
+    ("residual shape", lambda g: _first(g, "conv", lambda o: o.get("res") is not None).__setitem__("res", 0),
+     "residual"),
+    ("resize size", lambda g: _first(g, "resize").__setitem__("oh", 7), "resize to"),
+    ("gpool output", lambda g: g["tensors"][_first(g, "gpool")["out"]].__setitem__("h", 2), "gpool"),
+    ("binary operand", lambda g: _first(g, "binary", lambda o: "tensor" in o["b"])["b"]["tensor"]
+     .__setitem__("tid", 0), "binary"),
+    ("concat parts", lambda g: _first(g, "concat")["parts"][0].__setitem__("c", 1), "concat"),
+    ("conv parts", lambda g: _first(g, "conv", lambda o: bool(o.get("srcs")))["srcs"][0].__setitem__("c", 40),
+     "concat parts"),
+])
+def test_describe_rejects_inconsistent_geometry(segm, what, edit, fragment):
+    """A file whose op fields disagree with its tensors or weight ranges is
+    rejected at load (aih_sw_describe runs the same checks as aih_model_load
+    before any device work), with a message naming the op."""
+    bad = _edited(segm, edit)
+    with pytest.raises(conv.AihError) as e:
+        sw.describe(bad)
+    assert fragment in str(e.value) and ".sw: op" in str(e.value), (what, str(e.value))
+
+
+def test_describe_rejects_oversized_integers(segm):
+    """A number beyond 2^64 where an unsigned integer is expected is a clean
+    rejection (its conversion is checked before it happens)."""
+    bad = _edited(segm, lambda g: g["ops"][0]["w"].__setitem__("len", 1e30))
+    with pytest.raises(conv.AihError, match="expected an unsigned integer"):
+        sw.describe(bad)
