@@ -23,6 +23,7 @@
 #include "conv_igemm_direct.h"
 #include "conv_pw_direct.h"
 #include "conv_pw_narrow.h"
+#include "conv_pw_splitk.h"
 #include "conv_stem.h"
 #include "ir_block.h"
 
@@ -101,7 +102,7 @@ int plan_gemm(uint32_t M, uint32_t N4, uint32_t KK, int32_t dt, int32_t variant,
   uint32_t split_cap = 1;
   if (splitk > 0) split_cap = (uint32_t)splitk;
   else if (variant == AIH_VAR_SPLITK) split_cap = 4;
-  else if (variant == AIH_VAR_AUTO && KK >= 16) split_cap = std::min<uint32_t>(32, std::max<uint32_t>(KK / bkg, 1));
+  else if (variant == AIH_VAR_AUTO && KK >= 16) split_cap = std::min<uint32_t>(8, std::max<uint32_t>(KK / bkg, 1));
   if ((uint64_t)p->mtiles * p->ntiles * split_cap < 2 * kCUs) {
     // a grid that splitting K cannot bring to two workgroups per CU: narrower
     // column tiles give more workgroups, as long as the padded columns stay
@@ -126,8 +127,10 @@ int plan_gemm(uint32_t M, uint32_t N4, uint32_t KK, int32_t dt, int32_t variant,
   } else if (variant == AIH_VAR_SPLITK) {
     s = 4;
   } else if (variant == AIH_VAR_AUTO && tiles < kCUs && KK >= 16) {
+    // at most 8 chunks: more only add partial sums to write and reduce
+    // (960 -> 160 at 10x18, batch 1: 15.6 us with 8 chunks, 16.9 us with 30)
     s = (2 * kCUs) / tiles;
-    if (s > 32) s = 32;
+    if (s > 8) s = 8;
     const uint32_t max_s = KK / bkg;
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
@@ -159,11 +162,45 @@ void fill_plan(const GemmPlan &g, aih_plan *out) {
   out->ws_bytes = g.ws;
 }
 
+// Diagnostic overrides of the split-K policy, read once per process (so a
+// plan stays a pure function of its descriptor within a run), as the
+// reference's AI_PW_SPLITK_NG (gemm_pw.rs:112-126) and AI_RT_FORCE_DIRECT
+// (lowering.rs:156-160) are:
+//   AIH_PW_SPLITK=<n>     pointwise convs with AIH_VAR_AUTO and no forced
+//                         split that run the tiled GEMM use n K chunks
+//                         (1 = never split);
+//   AIH_IGEMM_NO_SPLIT=1  KxK convs with AIH_VAR_AUTO and no forced split
+//                         never split K.
+int env_int_once(const char *name, int *slot, std::once_flag *once) {
+  std::call_once(*once, [&] {
+    const char *v = std::getenv(name);
+    *slot = 0;
+    if (v && *v) {
+      char *end = nullptr;
+      const long n = std::strtol(v, &end, 10);
+      if (end && *end == 0 && n > 0 && n <= 64) *slot = (int)n;
+    }
+  });
+  return *slot;
+}
+
+int env_pw_splitk() {
+  static int v;
+  static std::once_flag once;
+  return env_int_once("AIH_PW_SPLITK", &v, &once);
+}
+
+bool env_igemm_no_split() {
+  static int v;
+  static std::once_flag once;
+  return env_int_once("AIH_IGEMM_NO_SPLIT", &v, &once) == 1;
+}
+
 // Which kernel a pointwise call runs: with AIH_VAR_AUTO and no forced split,
 // one output channel group goes to the one-pixel-per-thread kernel and short
 // K with at most 64 output channels (same storage for activations and
 // weights) to the direct MFMA kernel; everything else to the tiled GEMM.
-enum { PW_TILED = 0, PW_ROWS = 1, PW_DIRECT = 2, PW_LDS = 3 };
+enum { PW_TILED = 0, PW_ROWS = 1, PW_DIRECT = 2, PW_LDS = 3, PW_SPLITK = 4 };
 
 // The pointwise call as a one-tap launch of the direct 3x3 kernel (weights
 // resident in LDS, activations straight into MFMA registers): what the
@@ -210,14 +247,74 @@ bool pw_lds_plan(const aih_pw_desc *d, aih::IgDirectArgs *a) {
   return true;
 }
 
+// The split factor of a pointwise call: the descriptor's, else (AUTO only)
+// the AIH_PW_SPLITK override, else 0 (the policy decides).
+int32_t pw_splitk_of(const aih_pw_desc *d) {
+  if (d->splitk != 0 || d->variant != AIH_VAR_AUTO) return d->splitk;
+  return env_pw_splitk();
+}
+
+// Shapes the one-dispatch split-K kernel takes: same storage for activations
+// and weights, whole 16-channel output blocks, at most kPwSplitkMaxM pixels.
+bool pw_splitk_shape(const aih_pw_desc *d) {
+  const uint64_t M = (uint64_t)d->n * d->m;
+  return d->dt == d->wdt && (d->ng * 4) % 16 == 0 && M <= aih::kPwSplitkMaxM;
+}
+
+bool pw_splitk_waves_ok(int32_t w) {
+  for (uint32_t v : aih::kPwSplitkWaves)
+    if ((int32_t)v == w) return true;
+  return false;
+}
+
 int pw_route(const aih_pw_desc *d) {
-  if (d->variant != AIH_VAR_AUTO || d->splitk != 0) return PW_TILED;
+  const int32_t sk = pw_splitk_of(d);
+  if (d->variant == AIH_VAR_AUTO && sk > 0)
+    // a forced factor: one dispatch with that many K chunks where the shape
+    // allows, else the tiled GEMM with that many chunks
+    return pw_splitk_shape(d) && pw_splitk_waves_ok(sk) ? PW_SPLITK : PW_TILED;
+  if (d->variant != AIH_VAR_AUTO) return PW_TILED;
   if (d->ng == 1 && d->kg <= aih::kPwNarrowMaxKG) return PW_ROWS;
   const uint32_t kmax = d->dt == AIH_F32 ? aih::kPwDirectMaxK32 : aih::kPwDirectMaxK16;
-  if (d->dt == d->wdt && d->ng >= 2 && d->ng * 4 <= aih::kPwDirectMaxN4 && d->kg * 4 <= kmax) return PW_DIRECT;
+  if (d->dt == d->wdt && d->ng >= 2 && d->ng * 4 <= aih::kPwDirectMaxN4 && d->kg * 4 <= kmax) {
+    // too few 32-pixel blocks to give every SIMD a wavefront: 16x16 output
+    // blocks, one wavefront each, spread the same work over 4-8x more waves
+    const uint64_t M = (uint64_t)d->n * d->m;
+    if ((d->ng * 4) % 16 == 0 && (M + 31) / 32 < 4ull * aih::device_cus() && M <= 0xffffff00ull) return PW_SPLITK;
+    return PW_DIRECT;
+  }
   aih::IgDirectArgs a;
   if (pw_lds_plan(d, &a)) return PW_LDS;
+  // small M, long K (the reference's kg >= 16 gate, gemm_pw.rs:91-102): the
+  // tiled GEMM's 128-pixel tiles cannot fill the CUs and would split K
+  // through memory; one dispatch with the split on chip instead
+  const uint64_t M = (uint64_t)d->n * d->m;
+  if (pw_splitk_shape(d) && d->kg >= 16 &&
+      ((M + aih::GEMM_BM - 1) / aih::GEMM_BM) * ((d->ng * 4 + 31) / 32) < aih::device_cus())
+    return PW_SPLITK;
   return PW_TILED;
+}
+
+// Arguments of the one-dispatch split-K kernel and its K chunks (waves).
+aih::PwSplitkArgs pw_splitk_args(const aih_pw_desc *d, uint32_t *waves) {
+  aih::PwSplitkArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.M = d->n * d->m;
+  a.KG = d->kg;
+  a.N4 = d->ng * 4;
+  a.mblk = (a.M + 15) / 16;
+  a.nblk = a.N4 / 16;
+  a.steps = aih::pw_splitk_steps(d->kg, d->dt == AIH_F32);
+  const int32_t sk = pw_splitk_of(d);
+  *waves = sk > 0 ? (uint32_t)sk : aih::pw_splitk_waves(a.steps);
+  // short K (the direct route's shapes): one wavefront per 16x16 block
+  const uint32_t kmax = d->dt == AIH_F32 ? aih::kPwDirectMaxK32 : aih::kPwDirectMaxK16;
+  if (sk <= 0 && d->kg * 4 <= kmax) *waves = 1;
+  a.spw = (a.steps + *waves - 1) / *waves;
+  a.act = d->act;
+  a.has_res = d->residual ? 1 : 0;
+  a.nxcd = aih::device_xcds();
+  return a;
 }
 
 int run_gemm(aih::GemmArgs &a, const GemmPlan &g, int32_t dt, int32_t wdt, bool igemm, bool pair, void *ws,
@@ -266,44 +363,8 @@ int check_pw(const aih_pw_desc *d) {
   return AIH_OK;
 }
 
-// Diagnostic overrides of the split-K policy, read once per process (so a
-// plan stays a pure function of its descriptor within a run), as the
-// reference's AI_PW_SPLITK_NG (gemm_pw.rs:112-126) and AI_RT_FORCE_DIRECT
-// (lowering.rs:156-160) are:
-//   AIH_PW_SPLITK=<n>     pointwise convs with AIH_VAR_AUTO and no forced
-//                         split that run the tiled GEMM use n K chunks
-//                         (1 = never split);
-//   AIH_IGEMM_NO_SPLIT=1  KxK convs with AIH_VAR_AUTO and no forced split
-//                         never split K.
-int env_int_once(const char *name, int *slot, std::once_flag *once) {
-  std::call_once(*once, [&] {
-    const char *v = std::getenv(name);
-    *slot = 0;
-    if (v && *v) {
-      char *end = nullptr;
-      const long n = std::strtol(v, &end, 10);
-      if (end && *end == 0 && n > 0 && n <= 64) *slot = (int)n;
-    }
-  });
-  return *slot;
-}
-
-int env_pw_splitk() {
-  static int v;
-  static std::once_flag once;
-  return env_int_once("AIH_PW_SPLITK", &v, &once);
-}
-
-bool env_igemm_no_split() {
-  static int v;
-  static std::once_flag once;
-  return env_int_once("AIH_IGEMM_NO_SPLIT", &v, &once) == 1;
-}
-
 int plan_pw(const aih_pw_desc *d, GemmPlan *g) {
-  int32_t sk = d->splitk;
-  if (d->variant == AIH_VAR_AUTO && sk == 0) sk = env_pw_splitk();
-  return plan_gemm(d->n * d->m, d->ng * 4, d->kg, d->dt, d->variant, sk, g);
+  return plan_gemm(d->n * d->m, d->ng * 4, d->kg, d->dt, d->variant, pw_splitk_of(d), g);
 }
 
 // ---------------------------------------------------------------- igemm
@@ -473,6 +534,14 @@ int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out) {
       case PW_ROWS:
         *out = aih_plan{AIH_VAR_ROWS, 1, 256, 4, (uint32_t)std::min<uint64_t>((M + 255) / 256, 4096), 0};
         return AIH_OK;
+      case PW_SPLITK: {
+        // one dispatch: 16x16 output blocks, K split across `waves`
+        // wavefronts (one wavefront: K whole, reported as a direct launch)
+        uint32_t waves;
+        const aih::PwSplitkArgs a = pw_splitk_args(d, &waves);
+        *out = aih_plan{waves > 1 ? AIH_VAR_SPLITK : AIH_VAR_DIRECT, waves, 16, 16, a.mblk * a.nblk, 0};
+        return AIH_OK;
+      }
       case PW_LDS: {
         aih::IgDirectArgs a;
         pw_lds_plan(d, &a);
@@ -482,7 +551,7 @@ int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out) {
       }
       case PW_DIRECT:
         *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->ng * 4 <= 32 ? 32u : 64u,
-                        (uint32_t)std::min<uint64_t>((M + 127) / 128, aih::device_cus() * 8u), 0};
+                        aih::pw_direct_grid((uint32_t)((M + 31) / 32), aih::device_cus()), 0};
         return AIH_OK;
       default:
         break;
@@ -503,6 +572,19 @@ int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *
     if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16) || !aligned(bias, 8) || (res && !aligned(res, 16)))
       return fail("pw: misaligned buffer (x, w, y, res need 16 bytes, bias 8)");
     const int route = pw_route(d);
+    if (route == PW_SPLITK) {
+      // small M, long K: K split across the wavefronts of one workgroup,
+      // reduced in LDS, one dispatch, no workspace
+      uint32_t waves;
+      aih::PwSplitkArgs a = pw_splitk_args(d, &waves);
+      a.x = x;
+      a.w = w;
+      a.bias = bias;
+      a.res = res;
+      a.y = y;
+      const hipError_t e = aih::launch_pw_splitk(a, d->dt, waves, static_cast<hipStream_t>(stream));
+      return e == hipSuccess ? AIH_OK : fail(std::string("pw split-K launch: ") + hipGetErrorString(e));
+    }
     if (route == PW_ROWS) {
       // at most 4 output channels: one pixel per thread on the VALU
       const uint64_t M = (uint64_t)d->n * d->m;
@@ -897,8 +979,15 @@ size_t aih_conv_workspace_size(const aih_conv_desc *d) {
   aih_dw_desc dw;
   GemmPlan g;
   const int r = conv_route(d, &pw, &ig, &dw);
+  if (r == 0 && !check_pw(&pw) && pw_route(&pw) != PW_TILED) return 0;
   if (r == 0 && !check_pw(&pw) && !plan_pw(&pw, &g)) return g.ws;
-  if (r == 1 && !check_igemm(&ig) && !plan_igemm(&ig, &g)) return g.ws;
+  if (r == 1 && !check_igemm(&ig)) {
+    uint32_t oh, ow;
+    aih::IgDirectArgs da;
+    if (igemm_out_hw(&ig, &oh, &ow)) return 0;
+    if (igemm_is_stem(&ig) || ig_direct_plan(&ig, oh, ow, &da)) return 0;
+    if (!plan_igemm(&ig, &g)) return g.ws;
+  }
   return 0;
 }
 

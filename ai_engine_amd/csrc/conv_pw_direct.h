@@ -22,6 +22,17 @@ struct PwDirectArgs {
 // block stay in registers.
 constexpr uint32_t kPwDirectMaxK16 = 128, kPwDirectMaxK32 = 64, kPwDirectMaxN4 = 64;
 
+// Workgroups of a launch over nblk 32-pixel blocks and their wavefronts:
+// fewer blocks than four per CU run one wavefront (one block) per
+// workgroup, so every CU gets work; otherwise four wavefronts per
+// workgroup, at most 8 workgroups per CU, blocks taken grid-stride.
+inline uint32_t pw_direct_waves_per_group(uint32_t nblk, uint32_t cus) { return nblk < 4u * cus ? 1u : 4u; }
+inline uint32_t pw_direct_grid(uint32_t nblk, uint32_t cus) {
+  if (pw_direct_waves_per_group(nblk, cus) == 1) return nblk;
+  const uint64_t wgs = ((uint64_t)nblk + 3) / 4;
+  return (uint32_t)(wgs < (uint64_t)cus * 8u ? wgs : (uint64_t)cus * 8u);
+}
+
 hipError_t launch_pw_direct(const PwDirectArgs &a, int dt, hipStream_t st);
 
 }  // namespace aih

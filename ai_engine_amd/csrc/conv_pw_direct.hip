@@ -25,8 +25,11 @@ namespace {
 
 // KS: K steps of one MFMA operand (16-bit: 16 channels = 4 kg per step;
 // fp32: 8 channels = 2 kg per step, four v_mfma_f32_32x32x2f32 each).
-template <int DT, int KS, int NOB>
-__global__ __launch_bounds__(256) void pw_direct_kernel(PwDirectArgs a) {
+// WPG: wavefronts per workgroup; the wavefronts share nothing, so a launch
+// with fewer 32-pixel blocks than four per CU takes one-wavefront
+// workgroups, which the dispatcher spreads over every CU.
+template <int DT, int KS, int NOB, int WPG>
+__global__ __launch_bounds__(64 * WPG) void pw_direct_kernel(PwDirectArgs a) {
   constexpr bool F32 = DT == DT_F32;
   const int lane = threadIdx.x & 63, l32 = lane & 31, lh = lane >> 5;
   const Act actp = act_params(a.act);
@@ -67,8 +70,8 @@ __global__ __launch_bounds__(256) void pw_direct_kernel(PwDirectArgs a) {
       bias[ob][q] = c < a.N4 ? Vec4IO<DT>::load(a.bias, c / 4) : f32x4{};
     }
 
-  const uint32_t waves = gridDim.x * 4;
-  for (uint32_t blk = blockIdx.x * 4 + (threadIdx.x >> 6); blk < a.nblk; blk += waves) {
+  const uint32_t waves = gridDim.x * WPG;
+  for (uint32_t blk = blockIdx.x * WPG + (threadIdx.x >> 6); blk < a.nblk; blk += waves) {
     const uint32_t p = blk * 32 + l32;
     const bool valid = p < a.M;
     const size_t xrow = (size_t)(valid ? p : 0) * a.KG;
@@ -125,8 +128,11 @@ __global__ __launch_bounds__(256) void pw_direct_kernel(PwDirectArgs a) {
 
 template <int DT, int KS, int NOB>
 hipError_t launch_inst(const PwDirectArgs &a, hipStream_t st) {
-  const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblk + 3) / 4, device_cus() * 8u);
-  hipLaunchKernelGGL((pw_direct_kernel<DT, KS, NOB>), dim3(wgs), dim3(256), 0, st, a);
+  const uint32_t cus = device_cus(), grid = pw_direct_grid(a.nblk, cus);
+  if (pw_direct_waves_per_group(a.nblk, cus) == 1)
+    hipLaunchKernelGGL((pw_direct_kernel<DT, KS, NOB, 1>), dim3(grid), dim3(64), 0, st, a);
+  else
+    hipLaunchKernelGGL((pw_direct_kernel<DT, KS, NOB, 4>), dim3(grid), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

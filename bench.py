@@ -273,6 +273,8 @@ def kernel_key(conv, op, n, dt, dtname) -> str:
         p = conv.GemmPwSpec(m=Lr.ih * Lr.iw, kg=-(-Lr.cin // 4), ng=-(-Lr.cout // 4), dt=dt, n=n).plan()
         if p.variant == conv.Variant.DIRECT:
             return f"pw_direct_kernel<{dtname}>"
+        if p.variant == conv.Variant.SPLITK and p.bm == 16:
+            return f"pw_splitk_kernel<{dtname}, {p.splitk}>"
     else:
         p = conv.ConvIgemmSpec(ih=Lr.ih, iw=Lr.iw, cin=Lr.cin, cout=Lr.cout, k=Lr.k, s=Lr.s, pad=(Lr.pad,) * 4,
                                dt=dt, n=n).plan()

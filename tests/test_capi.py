@@ -63,19 +63,31 @@ def pw_plan(n, m, cin, cout, dt=0, splitk=0, variant=0):
 
 
 def test_pw_policy_splits_small_m_large_k():
-    # skinny 960 -> 160 at 10x18: 2 pixel tiles cannot fill 256 CUs -> split-K
+    # skinny 960 -> 160 at 10x18: 2 pixel tiles cannot fill 256 CUs -> split-K,
+    # on chip in one dispatch: 16x16 output blocks, K over 16 wavefronts, no
+    # workspace
     p = pw_plan(1, 180, 960, 160)
-    assert p.variant == conv.Variant.SPLITK and p.splitk > 1
-    assert p.ws_bytes == p.splitk * 180 * 160 * 4
+    assert p.variant == conv.Variant.SPLITK and p.splitk == 16 and (p.bm, p.bn) == (16, 16)
+    assert p.grid == 12 * 10 and p.ws_bytes == 0
+    # 100 outputs are not whole 16-channel blocks: the tiled GEMM splits K
+    # through a workspace, at most 8 chunks
+    p = pw_plan(1, 180, 960, 100)
+    assert p.variant == conv.Variant.SPLITK and 1 < p.splitk <= 8 and p.bm == 128
+    assert p.ws_bytes == p.splitk * 180 * 100 * 4
     # same layer at batch 256: 360 tiles, forced whole -> one tile per
     # workgroup over the whole K (the policy splits it in four, see below)
     p = pw_plan(256, 180, 960, 160, variant=conv.Variant.TILE)
     assert p.variant == conv.Variant.TILE and p.splitk == 1 and p.ws_bytes == 0
     assert p.bn == 160 and p.grid == 360
-    # 1x1 32 -> 64 at 80x144: short K (32) and 64 output channels -> the
-    # direct kernel, 32 pixels a wavefront, no workspace
+    # 1x1 32 -> 64 at 80x144: short K (32) and 64 output channels, but 360
+    # blocks of 32 pixels are fewer than four per CU: 16x16 output blocks, one
+    # wavefront each (2880), K whole in each, no workspace
     p = pw_plan(1, 11520, 32, 64)
-    assert p.variant == conv.Variant.DIRECT and p.bm == 32 and p.bn == 64 and p.grid == 90 and p.ws_bytes == 0
+    assert p.variant == conv.Variant.DIRECT and p.splitk == 1 and (p.bm, p.bn) == (16, 16)
+    assert p.grid == 720 * 4 and p.ws_bytes == 0
+    # the same at batch 64: the direct kernel, 32 pixels a wavefront
+    p = pw_plan(64, 11520, 32, 64)
+    assert p.variant == conv.Variant.DIRECT and p.bm == 32 and p.bn == 64 and p.grid == 2048
     # the tiled GEMM forced: K is one stage, nothing to split; 90 pixel tiles
     # cannot fill 256 CUs, so the columns are cut into two 32-wide tiles
     p = pw_plan(1, 11520, 32, 64, variant=conv.Variant.TILE)
@@ -110,9 +122,17 @@ def test_pw_policy_splits_long_k_fp32_partial_second_round():
 
 
 def test_forced_splitk_factor_is_honoured():
+    # AUTO with a forced factor: the one-dispatch kernel with that many K
+    # chunks (a power of two up to 16) where the shape allows it
     for s in (1, 4, 8):
         p = pw_plan(1, 180, 960, 160, splitk=s)
-        assert p.splitk == s
+        assert p.splitk == s and p.bm == 16 and p.ws_bytes == 0
+        assert p.variant == (conv.Variant.SPLITK if s > 1 else conv.Variant.DIRECT)
+    # other factors, or AIH_VAR_SPLITK: the tiled GEMM with a workspace
+    p = pw_plan(1, 180, 960, 160, splitk=3)
+    assert p.splitk == 3 and p.bm == 128 and p.ws_bytes == 3 * 180 * 160 * 4
+    p = pw_plan(1, 180, 960, 160, splitk=4, variant=conv.Variant.SPLITK)
+    assert p.splitk == 4 and p.bm == 128 and p.ws_bytes == 4 * 180 * 160 * 4
     p = pw_plan(1, 180, 960, 160, variant=conv.Variant.TILE)
     assert p.splitk == 1
 
@@ -199,7 +219,7 @@ def test_invalid_descriptors_fail_cleanly():
     ig = conv.ConvIgemmSpec(ih=2, iw=2, cin=4, cout=4, k=5)
     _expect_error(lambda: ig.plan(), "larger than the padded input")
     # split-K without a workspace is an error, not a crash
-    d = conv.GemmPwSpec(m=180, kg=240, ng=40, splitk=4).desc()
+    d = conv.GemmPwSpec(m=180, kg=240, ng=40, splitk=4, variant=conv.Variant.SPLITK).desc()
     assert L.aih_conv_pw(C.byref(d), 16, 16, 16, None, 16, None, 0, None) == -1
     assert "workspace" in conv.last_error()
 
@@ -328,7 +348,7 @@ def test_ir_block_plan_depends_on_the_activations():
 
 def test_conv_plan_reports_the_route():
     A = conv.Activation
-    pw = conv.ConvOp(ih=80, iw=144, cin=32, cout=64, act=A.RELU6)
+    pw = conv.ConvOp(ih=80, iw=144, cin=32, cout=64, act=A.RELU6, n=64)
     assert pw.plan().variant == conv.Variant.DIRECT
     assert conv.ConvOp(ih=10, iw=18, cin=960, cout=160).plan().variant == conv.Variant.SPLITK
     ig = conv.ConvOp(ih=40, iw=72, cin=32, cout=64, kh=3, kw=3, pad=(1, 1, 1, 1))

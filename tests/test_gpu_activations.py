@@ -15,9 +15,11 @@ Activation::apply of z, rounded to the storage dtype:
 
 Equal infinities and NaN in the same place count as equal (recip of an exact
 zero is inf on both sides). The routes are the kernels a conv can land on:
-pointwise one-pixel-per-thread (<= 4 outputs), register-operand direct,
-LDS-weight direct (one tap, large M), tiled GEMM, split-K (the epilogue runs
-in the reduction), implicit-GEMM direct and tiled, the stem, the depthwise
+pointwise one-pixel-per-thread (<= 4 outputs), register-operand direct (32-
+pixel blocks, and 16x16 blocks for small M),
+LDS-weight direct (one tap, large M), tiled GEMM, split-K in one dispatch and
+in two (the epilogue runs in the reduction), implicit-GEMM direct, tiled and
+split-K, the stem, the depthwise
 kernel, and the fused inverted-residual block (its projection epilogue the
 same way; its expand and depthwise activations against the oracle's
 three-op chain with stored-dtype rounding).
@@ -57,15 +59,21 @@ def act_err(got, ref) -> float:
 # route -> (runner(act, dt, seed) -> Result, expected plan variant or None)
 ROUTES = {
     "pw_rows": (lambda a, dt, s: G.run_pw(16, 16, 24, 2, a, False, dt, s, refs=False), V.ROWS),
-    "pw_direct": (lambda a, dt, s: G.run_pw(16, 16, 32, 16, a, False, dt, s, refs=False), V.DIRECT),
+    "pw_direct_16x16": (lambda a, dt, s: G.run_pw(16, 16, 32, 16, a, False, dt, s, refs=False), V.DIRECT),
+    "pw_direct_32px": (lambda a, dt, s: G.run_pw(128, 256, 32, 16, a, False, dt, s, refs=False), V.DIRECT),
     "pw_lds_direct": (lambda a, dt, s: G.run_pw(256, 256, 64 if dt == F32 else 128, 32, a, False, dt, s,
                                                 refs=False), V.DIRECT),
     "pw_tiled": (lambda a, dt, s: G.run_pw(9, 16, 64, 96, a, False, dt, s, variant=1, refs=False), V.TILE),
-    "pw_splitk": (lambda a, dt, s: G.run_pw(9, 16, 256, 64, a, False, dt, s, splitk=4, refs=False), V.SPLITK),
+    "pw_splitk_one_dispatch": (lambda a, dt, s: G.run_pw(9, 16, 256, 64, a, False, dt, s, splitk=4, refs=False),
+                               V.SPLITK),
+    "pw_splitk_two_launch": (lambda a, dt, s: G.run_pw(9, 16, 256, 64, a, False, dt, s, variant=2, splitk=4,
+                                                       refs=False), V.SPLITK),
     "igemm_direct": (lambda a, dt, s: G.run_igemm(12, 20, 16, 32, 3, 1, (1, 1, 1, 1), a, False, dt, s,
                                                   refs=False), V.DIRECT),
     "igemm_tiled": (lambda a, dt, s: G.run_igemm(12, 20, 16, 96, 3, 1, (1, 1, 1, 1), a, False, dt, s,
-                                                 refs=False), V.TILE),
+                                                 variant=1, refs=False), V.TILE),
+    "igemm_splitk": (lambda a, dt, s: G.run_igemm(12, 20, 16, 96, 3, 1, (1, 1, 1, 1), a, False, dt, s,
+                                                  splitk=3, refs=False), V.SPLITK),
     "igemm_stem": (lambda a, dt, s: G.run_igemm(12, 20, 3, 32, 3, 2, (1, 1, 1, 1), a, False, dt, s,
                                                 refs=False), V.DIRECT),
     "dw": (lambda a, dt, s: G.run_dw(12, 20, 32, 3, 1, a, False, dt, s, refs=False), None),

@@ -161,13 +161,15 @@ def test_pw_direct(case, dt):
 @pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
 def test_pw_direct_equals_tiled_gemm(dt):
     # the same short-K shapes with the tiled GEMM forced (AIH_VAR_TILE, one
-    # tile over the whole K): the same MFMA K steps in the same order, so the
-    # outputs agree bit for bit
-    for (h, w, cin, cout, res), seed in [((13, 19, 44, 24, True), 3510), ((40, 72, 32, 64, False), 3511)]:
-        xs = G.stream(seed, 2 * h * w * cin, cout * cin, cout, 2 * h * w * cout if res else 0)
-        a = G.run_pw(h, w, cin, cout, "relu", res, dt, seed, n=2, xs=xs)
-        b = G.run_pw(h, w, cin, cout, "relu", res, dt, seed, n=2, xs=xs, variant=1)
-        assert a.plan.variant == G.conv.Variant.DIRECT and b.plan.variant == G.conv.Variant.TILE
+    # tile over the whole K): the direct kernel's 32-pixel blocks run the same
+    # MFMA K steps in the same order, so the outputs agree bit for bit (the
+    # second shape at batch 16: enough 32-pixel blocks that the 16x16-block
+    # launch for small M does not take it)
+    for (h, w, cin, cout, res, n), seed in [((13, 19, 44, 24, True, 2), 3510), ((40, 72, 32, 64, False, 16), 3511)]:
+        xs = G.stream(seed, n * h * w * cin, cout * cin, cout, n * h * w * cout if res else 0)
+        a = G.run_pw(h, w, cin, cout, "relu", res, dt, seed, n=n, xs=xs)
+        b = G.run_pw(h, w, cin, cout, "relu", res, dt, seed, n=n, xs=xs, variant=1)
+        assert a.plan.variant == G.conv.Variant.DIRECT and a.plan.bm == 32 and b.plan.variant == G.conv.Variant.TILE
         check(f"pw tiled dt{dt}", b, dt)
         assert np.array_equal(np.asarray(a.got), np.asarray(b.got))
 

@@ -351,19 +351,44 @@ def image_of(m, name, i, dt):
     return orc.unpack_nhwc(G.host(t, dt), 1, h, w, c, dt)
 
 
+U = {F16: 2.0 ** -11, BF16: 2.0 ** -8}  # unit roundoff of the storage dtype
+
+
 def local_op_error(m, op, i, wts, dt):
     """One launch of a loaded model on image i, against the oracle run of the
     same ops on the launch's own stored input (and residual) with the weights
     rounded to dt, every stored intermediate rounded to dt: the kernel's error
-    alone, whatever the layers before it contributed."""
+    alone, whatever the layers before it contributed.
+
+    Returns (max |g - c| / max(|c|, 1), worst ratio to the storage bound or
+    None). A fused launch also rounds its two intermediates; where the GPU's
+    fp32 value and the oracle's (summed in another order) straddle a rounding
+    boundary they round one ulp apart, and the next convs carry that on. With
+    the magnitudes m_e = |We||x| + |be|, m_d = |Wd| * m_e + |bd|,
+    m_y = |Wp| m_d (the activations here are 1-Lipschitz) the outputs then
+    differ by at most 4 u m_y + 2 u |c| (u the dtype's unit roundoff): one ulp
+    of each intermediate carried through, one of the output. The ratio to
+    that bound must stay <= 1; a lost term or a wrong index moves outputs by
+    a large fraction of m_y, far beyond it."""
     rd = (lambda v: v) if dt == F32 else (lambda v: orc.round_to(v, dt))
     first = op.layers[0]
     buf = image_of(m, first.src, i, dt)
+    mag = np.abs(buf)
     for L in op.layers:
         cop = orc.conv2d(L.cin, L.cout, k=L.k, s=L.s, pad=L.pad, groups=L.groups, act=L.act)
         cc = orc.CpuConv(cop, L.ih, L.iw, rd(wts.w[L.name]), rd(wts.b[L.name]), has_res=L.res is not None)
         buf = rd(cc.run(buf, 1, image_of(m, L.res, i, dt) if L.res else None, threads=8))
-    return G.rel_err(image_of(m, op.layers[-1].name, i, dt), buf)
+        if dt != F32 and len(op.layers) > 1:
+            aop = orc.conv2d(L.cin, L.cout, k=L.k, s=L.s, pad=L.pad, groups=L.groups, act="none")
+            cm = orc.CpuConv(aop, L.ih, L.iw, np.abs(rd(wts.w[L.name])),
+                             np.abs(rd(wts.b[L.name])) * (L is not op.layers[-1]))
+            mag = cm.run(mag, 1, threads=8)
+    got = image_of(m, op.layers[-1].name, i, dt)
+    ratio = None
+    if dt != F32 and len(op.layers) > 1:
+        bound = 4 * U[dt] * mag + 2 * U[dt] * np.abs(buf) + 1e-5 * (mag + 1.0)
+        ratio = float(np.max(np.abs(got.astype(np.float64) - buf) / bound))
+    return G.rel_err(got, buf), ratio
 
 
 @pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
@@ -373,9 +398,12 @@ def test_encoder_b64_as_benched(dt):
     model runs -- the stem, each block as the tuner chose it (fused at its
     chosen tile and weight placement, or three launches), the head -- is
     checked on sampled images against the oracle on its own stored inputs
-    (<= 2e-3 f16, 8e-3 bf16; fp32 arithmetic and storage rounding where the
-    unfused path stores). The choice map is printed; the end-to-end drift
-    from the fp32 chain is printed next to what ideal storage gives."""
+    (fp32 arithmetic and storage rounding where the unfused path stores):
+    single convs within 2e-3 f16 / 8e-3 bf16, fused blocks within the
+    element-wise storage bound of local_op_error (the same candidates on
+    U[-1,1) inputs meet 2e-3 / 8e-3 in test_gpu_ir_tiles). The choice map is
+    printed; the end-to-end drift from the fp32 chain is printed next to what
+    ideal storage gives."""
     layers, meta = W.mnv4_small_encoder_160x288(64)
     wts = W.make_weights(layers, seed=0)
     n, h, w = 64, meta["h"], meta["w"]
@@ -385,12 +413,22 @@ def test_encoder_b64_as_benched(dt):
     m.upload_input(G.dev(x))
     m.infer()
     torch.cuda.synchronize()
-    worst = {}
+    worst, ratios = {}, {}
     for i in sample_images(n):
         for op in m.ops:
-            worst[op.name] = max(worst.get(op.name, 0.0), local_op_error(m, op, i, wts, dt))
-    print("  local per launch: " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()), flush=True)
-    bad = {k: v for k, v in worst.items() if v > BAR_STORED[dt]}
+            e, r = local_op_error(m, op, i, wts, dt)
+            worst[op.name] = max(worst.get(op.name, 0.0), e)
+            if r is not None:
+                ratios[op.name] = max(ratios.get(op.name, 0.0), r)
+    print("  local per launch (max rel vs stored chain): " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()),
+          flush=True)
+    print("  fused launches, worst ratio to the storage bound: " + ", ".join(f"{k} {v:.2f}" for k, v in ratios.items()),
+          flush=True)
+    # single-conv launches round once: the kernel's bar; fused launches: the
+    # element-wise storage bound (this network's grown activations make one
+    # ulp of an intermediate worth more than the bar)
+    bad = {k: v for k, v in worst.items() if k not in ratios and v > BAR_STORED[dt]}
+    bad.update({k: v for k, v in ratios.items() if v > 1.0})
     assert not bad, bad
     img = h * w * 3
     i = n - 1
@@ -421,7 +459,7 @@ def test_ir_chain_b64_as_benched_f32():
         ref = oracle_chain(layers, wts, x[i * img:(i + 1) * img], meta["h"], meta["w"])[layers[-1].name]
         e2e = max(e2e, G.rel_err(image_of(m, layers[-1].name, i, F32), ref))
         for op in m.ops:
-            local = max(local, local_op_error(m, op, i, wts, F32))
+            local = max(local, local_op_error(m, op, i, wts, F32)[0])
     report("ir chain b64 f32 as benched, end to end", e2e, 1e-4)
     report("ir chain b64 f32 as benched, local", local, 1e-4)
 
