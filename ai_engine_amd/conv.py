@@ -139,6 +139,7 @@ EXPORTS = (
     "aih_conv_workspace_size", "aih_nhwc_c4_bytes", "aih_pack_nhwc", "aih_unpack_nhwc",
     "aih_pack_weights_conv", "aih_pack_weights_dw", "aih_pack_bias", "aih_pack_nhwc_device",
     "aih_ir_block_plan", "aih_ir_block", "aih_last_error", "aih_version", "aih_conv_check", "aih_conv_plan",
+    "aih_conv_noalloc",
 )
 
 _lib = None
@@ -162,6 +163,7 @@ def lib() -> C.CDLL:
         "aih_conv": (C.c_int, [C.POINTER(_ConvDesc), P, P, P, P, P, P, sz, P]),
         "aih_conv_workspace_size": (sz, [C.POINTER(_ConvDesc)]),
         "aih_conv_plan": (C.c_int, [C.POINTER(_ConvDesc), C.POINTER(Plan)]),
+        "aih_conv_noalloc": (C.c_int, [C.POINTER(_ConvDesc), P, P, P, P, P, P]),
         "aih_nhwc_c4_bytes": (sz, [u32, u32, u32, u32, i32]),
         "aih_pack_nhwc": (C.c_int, [P, u32, u32, u32, u32, i32, P]),
         "aih_unpack_nhwc": (C.c_int, [P, u32, u32, u32, u32, i32, P]),

@@ -232,6 +232,19 @@ size_t aih_conv_workspace_size(const aih_conv_desc *d);
  * its route; a depthwise conv reports AIH_VAR_DIRECT with bm = bn = grid = 0
  * (one kernel, no workspace). */
 int aih_conv_plan(const aih_conv_desc *d, aih_plan *out);
+/* aih_conv for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The split-K workspace aih_conv takes from the
+ * caller is instead a static device array of AIH_NOALLOC_SCRATCH_BYTES inside
+ * the library, one per device, set up on the first call from that device and
+ * held until the process ends. A conv whose workspace (aih_conv_workspace_size)
+ * exceeds it fails with AIH_ERR and the size in the message. Calls on one
+ * device share the array: calls that overlap on one device (different
+ * streams, unordered threads) race; calls ordered on one stream do not. The
+ * same kernels as aih_conv, so the same results bit for bit. */
+#define AIH_NOALLOC_SCRATCH_BYTES (16u << 20)
+int aih_conv_noalloc(const aih_conv_desc *d, const void *x, const void *w, const void *bias,
+                     const void *res, void *y, aih_stream stream);
 /* Validates a descriptor as aih_conv would (routing, shapes, dtypes, plan)
  * without launching: AIH_OK, or AIH_ERR with the reason (lower_op's load-time
  * rejection of a conv it cannot run, lowering.rs:136-140). */
