@@ -65,6 +65,14 @@ class IrWeights(enum.IntEnum):
     STREAMED = 2
 
 
+class IrKernel(enum.IntEnum):
+    """Which fused kernel runs a block (enum aih_ir_kernel)."""
+
+    AUTO = 0
+    TILE = 1
+    WAVE = 2
+
+
 class Variant(enum.IntEnum):
     AUTO = 0
     TILE = 1
@@ -112,17 +120,18 @@ class _IrDesc(C.Structure):
                 ("cexp", C.c_uint32), ("cout", C.c_uint32), ("s", C.c_uint32), ("pad", C.c_uint32 * 4),
                 ("act_expand", C.c_int32), ("act_dw", C.c_int32), ("act_project", C.c_int32),
                 ("residual", C.c_int32), ("dt", C.c_int32), ("tile_h", C.c_uint32), ("tile_w", C.c_uint32),
-                ("ec", C.c_uint32), ("weights", C.c_int32)]
+                ("ec", C.c_uint32), ("weights", C.c_int32), ("kernel", C.c_int32)]
 
 
 class IrPlan(C.Structure):
     _fields_ = [("th", C.c_uint32), ("tw", C.c_uint32), ("ec", C.c_uint32), ("chunks", C.c_uint32),
                 ("resident", C.c_uint32), ("tiles", C.c_uint32), ("lds_bytes", C.c_uint32),
-                ("occupancy", C.c_uint32), ("grid", C.c_uint32)]
+                ("occupancy", C.c_uint32), ("grid", C.c_uint32), ("kernel", C.c_uint32), ("waves", C.c_uint32)]
 
     def __repr__(self):
-        return (f"IrPlan(tile={self.th}x{self.tw}, ec={self.ec}, chunks={self.chunks}, resident={self.resident}, "
-                f"tiles={self.tiles}, lds={self.lds_bytes}, occ={self.occupancy}, grid={self.grid})")
+        return (f"IrPlan({IrKernel(self.kernel).name.lower()}, tile={self.th}x{self.tw}, ec={self.ec}, "
+                f"chunks={self.chunks}, resident={self.resident}, tiles={self.tiles}, lds={self.lds_bytes}, "
+                f"occ={self.occupancy}, grid={self.grid}x{self.waves} waves)")
 
 
 class Plan(C.Structure):
@@ -434,6 +443,7 @@ class IrBlockSpec:
     tile: tuple = (0, 0)  # forced output tile (h, w); (0, 0) = plan's choice
     ec: int = 0           # forced expanded channels per chunk; 0 = plan's choice
     weights: int = 0      # IrWeights: 0 = plan's choice, 1 = resident in LDS, 2 = streamed
+    kernel: int = 0       # IrKernel: 0 = plan's choice, 1 = tile kernel, 2 = wave kernel
 
     def out_hw(self) -> tuple[int, int]:
         return ((self.ih + self.pad[0] + self.pad[2] - 3) // self.s + 1,
@@ -442,7 +452,7 @@ class IrBlockSpec:
     def desc(self) -> _IrDesc:
         return _IrDesc(self.n, self.ih, self.iw, self.cin, self.cexp, self.cout, self.s, (C.c_uint32 * 4)(*self.pad),
                        int(self.act_expand), int(self.act_dw), int(self.act_project), int(bool(self.residual)),
-                       int(self.dt), self.tile[0], self.tile[1], self.ec, int(self.weights))
+                       int(self.dt), self.tile[0], self.tile[1], self.ec, int(self.weights), int(self.kernel))
 
     def plan(self) -> IrPlan:
         p = IrPlan()

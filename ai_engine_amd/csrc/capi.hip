@@ -517,6 +517,24 @@ int plan_ir(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, aih::IrPlan *p
   return AIH_OK;
 }
 
+// The wave kernel's plan, when the descriptor selects it (WAVE) or leaves
+// the choice (AUTO) and it applies; false: the tile kernel runs (AUTO) or
+// the call fails (WAVE, with the reason).
+int plan_ir_wave(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, aih::IrWavePlan *p, bool *use) {
+  *use = false;
+  if (d->kernel == AIH_IR_KERNEL_TILE) return AIH_OK;
+  if (d->kernel != AIH_IR_KERNEL_AUTO && d->kernel != AIH_IR_KERNEL_WAVE) return fail("ir_block: unknown kernel");
+  if (d->ec && d->ec != 32) {
+    if (d->kernel == AIH_IR_KERNEL_WAVE) return fail("ir_block: the wave kernel walks E in chunks of 32");
+    return AIH_OK;
+  }
+  const char *why = aih::irw_plan(d->n, d->ih, d->iw, oh, ow, d->cin, d->cexp, d->cout, d->s, d->dt,
+                                  ir_clamp_acts(d), d->tile_h, d->tile_w, d->weights, p);
+  if (why) return d->kernel == AIH_IR_KERNEL_WAVE ? fail(std::string("ir_block: ") + why) : AIH_OK;
+  *use = true;
+  return AIH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -831,9 +849,18 @@ int aih_ir_block_plan(const aih_ir_block_desc *d, aih_ir_plan *out) {
     uint32_t oh, ow;
     if (check_ir(d, &oh, &ow)) return AIH_ERR;
     if (!out) return fail("null plan");
+    aih::IrWavePlan wp;
+    bool wave;
+    if (plan_ir_wave(d, oh, ow, &wp, &wave)) return AIH_ERR;
+    if (wave) {
+      *out = aih_ir_plan{wp.TH, wp.TW, 32, d->cexp / 32, wp.resident, wp.ntiles, wp.lds, wp.occ, wp.grid,
+                         AIH_IR_KERNEL_WAVE, wp.waves};
+      return AIH_OK;
+    }
     aih::IrPlan p;
     if (plan_ir(d, oh, ow, &p)) return AIH_ERR;
-    *out = aih_ir_plan{p.TH, p.TW, p.EC, d->cexp / p.EC, p.resident, p.ntiles, p.lds, p.occ, p.grid};
+    *out = aih_ir_plan{p.TH, p.TW, p.EC, d->cexp / p.EC, p.resident, p.ntiles, p.lds, p.occ, p.grid,
+                       AIH_IR_KERNEL_TILE, 4};
     return AIH_OK;
   });
 }
@@ -852,6 +879,57 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
     for (const void *p : {b_expand, b_dw, b_project})
       if (!aligned(p, 8)) return fail("ir_block: misaligned bias (8 bytes)");
     if (res && !aligned(res, 16)) return fail("ir_block: misaligned residual (16 bytes)");
+    aih::IrWavePlan wp;
+    bool wave;
+    if (plan_ir_wave(d, oh, ow, &wp, &wave)) return AIH_ERR;
+    if (wave) {
+      aih::IrWaveArgs a;
+      std::memset(&a, 0, sizeof(a));
+      a.x = x;
+      a.we = w_expand;
+      a.be = b_expand;
+      a.wd = w_dw;
+      a.bd = b_dw;
+      a.wp = w_project;
+      a.bp = b_project;
+      a.res = res;
+      a.y = y;
+      a.N = d->n;
+      a.IH = d->ih;
+      a.IW = d->iw;
+      a.OH = oh;
+      a.OW = ow;
+      a.C = d->cin;
+      a.E = d->cexp;
+      a.CO = d->cout;
+      a.S = d->s;
+      a.PT = (int32_t)d->pad[0];
+      a.PL = (int32_t)d->pad[1];
+      a.TH = wp.TH;
+      a.TW = wp.TW;
+      a.HH = wp.HH;
+      a.HW = wp.HW;
+      a.tiles_y = wp.tiles_y;
+      a.tiles_x = wp.tiles_x;
+      a.ntiles = wp.ntiles;
+      a.resident = wp.resident;
+      a.act_e = d->act_expand;
+      a.act_d = d->act_dw;
+      a.act_p = d->act_project;
+      a.has_res = d->residual ? 1 : 0;
+      a.nxcd = aih::device_xcds();
+      a.lds_w = wp.lds_w;
+      a.lds_bp = wp.lds_bp;
+      a.lds_xe = wp.lds_xe;
+      a.fd_hw = aih::make_fastdiv(wp.HW);
+      a.fd_tw = aih::make_fastdiv(wp.TW);
+      a.fd_tx = aih::make_fastdiv(wp.tiles_x);
+      a.fd_pi = aih::make_fastdiv(wp.tiles_x * wp.tiles_y);
+      const hipError_t e =
+          aih::launch_ir_wave(a, d->dt, wp.NPI, wp.waves, wp.lds, wp.grid, static_cast<hipStream_t>(stream));
+      if (e != hipSuccess) return fail(std::string("ir_block wave launch: ") + hipGetErrorString(e));
+      return AIH_OK;
+    }
     aih::IrPlan p;
     if (plan_ir(d, oh, ow, &p)) return AIH_ERR;
     aih::IrArgs a;

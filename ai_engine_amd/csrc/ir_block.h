@@ -60,4 +60,54 @@ const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t 
 
 hipError_t launch_ir_block(const IrArgs &a, int dt, uint32_t lds, uint32_t grid, hipStream_t st);
 
+// ---- the one-tile-per-wavefront kernel (ir_wave_impl.h) ----
+
+constexpr int IRW_THREADS = 512;              // the most threads a workgroup has (8 wavefronts)
+constexpr uint32_t IRW_RPE = 32 * 2 + 16;     // expanded-chunk LDS row pitch: 32 16-bit channels + 16 bytes
+constexpr uint32_t IRW_SMB = 11 * 32 * 2;     // per chunk: 9 depthwise taps, depthwise bias, expand bias
+
+struct IrWaveArgs {
+  const void *x;         // [N][IH][IW][C]
+  const void *we, *be;   // expand weights [C/4][E][4], bias [E]
+  const void *wd, *bd;   // depthwise weights [9][E/4][4], bias [E]
+  const void *wp, *bp;   // project weights [E/4][CO][4], bias [CO]
+  const void *res;       // [N][OH][OW][CO] or null
+  void *y;               // [N][OH][OW][CO]
+  uint32_t N, IH, IW, OH, OW;
+  uint32_t C, E, CO, S;
+  int32_t PT, PL;
+  uint32_t TH, TW, HH, HW;  // output tile (<= 32 pixels), input (halo) tile
+  uint32_t tiles_y, tiles_x, ntiles;
+  uint32_t resident;        // 1: every chunk's weights stay in LDS; 0: two streamed slots
+  int32_t act_e, act_d, act_p, has_res;
+  uint32_t nxcd;            // XCDs of the device (workgroup remap)
+  uint32_t lds_w, lds_bp, lds_xe;  // LDS byte offsets: weight slots, fp32 projection bias, expanded regions
+  FastDiv fd_hw, fd_tw, fd_tx, fd_pi;
+};
+
+// Bytes of one chunk's weight slot: expand [C/4][32][4], project [8][CO][4],
+// then IRW_SMB bytes of depthwise taps and biases (16-bit elements).
+__host__ __device__ inline uint32_t irw_slot_bytes(uint32_t C, uint32_t CO) { return 64 * C + 64 * CO + IRW_SMB; }
+
+// Tile, weight placement and LDS layout of one launch of the wave kernel.
+struct IrWavePlan {
+  uint32_t TH, TW, HH, HW, NPI, resident;
+  uint32_t waves;                       // wavefronts per workgroup (2, 4 or 8)
+  uint32_t tiles_y, tiles_x, ntiles;
+  uint32_t lds_w, lds_bp, lds_xe, lds;  // LDS byte offsets and total
+  uint32_t occ, grid;                   // workgroups per CU, launched workgroups
+};
+
+// Chooses the wave kernel's tile (<= 32 output pixels, halo within NPI
+// blocks of an instantiation) and weight placement (resident when all
+// chunks fit in LDS next to the eight wavefronts' expanded regions).
+// Returns nullptr, or the reason the block cannot run on this kernel
+// (dtype, activations, widths without an instantiation, LDS).
+const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
+                     uint32_t CO, uint32_t S, int dt, bool cl, uint32_t tile_h, uint32_t tile_w, int32_t weights,
+                     IrWavePlan *p);
+
+hipError_t launch_ir_wave(const IrWaveArgs &a, int dt, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
+                          hipStream_t st);
+
 }  // namespace aih

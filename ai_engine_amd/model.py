@@ -28,8 +28,9 @@ fuses 16-bit models only.
 
 The choice per block is recorded (choice_map()) and can be given back
 (choices={block: label}), so a later load runs exactly the same kernels; a
-label is "unfused", "fused THxTW" (streamed weights) or "fused THxTW
-resident" -- fused_candidates() lists the labels a block can take.
+label is "unfused", "fused THxTW" (the tile kernel, streamed weights),
+"fused THxTW resident", or "wave THxTW[ resident]" (the wave kernel) --
+fused_candidates() lists the labels a block can take.
 """
 from __future__ import annotations
 
@@ -91,9 +92,12 @@ class ModelOp:
 
 
 class Model:
-    # forced output tiles (h, w) tried for a fused block besides the planner's
+    # forced output tiles (h, w) tried for a fused block besides the planner's:
+    # for the tile kernel (a workgroup per tile) and the wave kernel (a
+    # wavefront per tile of at most 32 pixels)
     TUNE_TILES = [(2, 8), (4, 4), (4, 8), (8, 4), (4, 16), (8, 8), (16, 4), (2, 32), (4, 32), (8, 16), (16, 8),
                   (8, 32), (16, 16)]
+    WAVE_TILES = [(4, 8), (8, 4), (5, 6), (6, 5), (2, 16), (16, 2), (3, 10)]
 
     def __init__(self, layers: list[Layer], weights: Weights, n: int, ih: int, iw: int, cin: int,
                  dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0",
@@ -172,39 +176,43 @@ class Model:
 
     @classmethod
     def fused_candidates(cls, spec: conv.IrBlockSpec) -> list[tuple[str, conv.IrBlockSpec]]:
-        """The fused launches the tuner times for a block: the planner's tile
-        and every TUNE_TILES entry, each with resident and streamed weights
-        (the ones that fit), as (label, spec with the tile and placement
-        forced); duplicates dropped."""
+        """The fused launches the tuner times for a block: on the tile kernel
+        the planner's tile and every TUNE_TILES entry, on the wave kernel the
+        planner's tile and every WAVE_TILES entry, each with resident and
+        streamed weights (the ones that fit), as (label, spec with kernel,
+        tile and placement forced); duplicates dropped."""
         out, seen = [], set()
-        for tile in [(0, 0)] + cls.TUNE_TILES:
-            for w in (conv.IrWeights.RESIDENT, conv.IrWeights.STREAMED):
-                sp = dataclasses.replace(spec, tile=tile, weights=w)
-                if not sp.fusable():
-                    continue
-                pl = sp.plan()
-                key = (pl.th, pl.tw, pl.resident)
-                if key in seen:
-                    continue
-                seen.add(key)
-                out.append((cls.label_of(pl.th, pl.tw, pl.resident),
-                            dataclasses.replace(spec, tile=(pl.th, pl.tw), weights=w)))
+        for kernel, tiles in ((conv.IrKernel.TILE, cls.TUNE_TILES), (conv.IrKernel.WAVE, cls.WAVE_TILES)):
+            for tile in [(0, 0)] + tiles:
+                for w in (conv.IrWeights.RESIDENT, conv.IrWeights.STREAMED):
+                    sp = dataclasses.replace(spec, tile=tile, weights=w, kernel=kernel)
+                    if not sp.fusable():
+                        continue
+                    pl = sp.plan()
+                    key = (int(kernel), pl.th, pl.tw, pl.resident)
+                    if key in seen:
+                        continue
+                    seen.add(key)
+                    out.append((cls.label_of(kernel, pl.th, pl.tw, pl.resident),
+                                dataclasses.replace(spec, tile=(pl.th, pl.tw), weights=w, kernel=kernel)))
         return out
 
     @staticmethod
-    def label_of(th: int, tw: int, resident: bool) -> str:
-        return f"fused {th}x{tw}{' resident' if resident else ''}"
+    def label_of(kernel, th: int, tw: int, resident: bool) -> str:
+        name = "wave" if conv.IrKernel(kernel) == conv.IrKernel.WAVE else "fused"
+        return f"{name} {th}x{tw}{' resident' if resident else ''}"
 
     @staticmethod
     def parse_label(label: str):
-        """"unfused" -> None; "fused THxTW[ resident]" -> ((th, tw), IrWeights)."""
+        """"unfused" -> None; "fused|wave THxTW[ resident]" -> (IrKernel, (th, tw), IrWeights)."""
         if label == "unfused":
             return None
-        m = re.fullmatch(r"fused (\d+)x(\d+)( resident)?", label)
+        m = re.fullmatch(r"(fused|wave) (\d+)x(\d+)( resident)?", label)
         if not m:
             raise ValueError(f"unknown block choice {label!r}")
-        w = conv.IrWeights.RESIDENT if m.group(3) else conv.IrWeights.STREAMED
-        return (int(m.group(1)), int(m.group(2))), w
+        k = conv.IrKernel.WAVE if m.group(1) == "wave" else conv.IrKernel.TILE
+        w = conv.IrWeights.RESIDENT if m.group(4) else conv.IrWeights.STREAMED
+        return k, (int(m.group(2)), int(m.group(3))), w
 
     def choice_map(self) -> dict[str, str]:
         """Block -> the label of the launch it runs (feed back as choices=)."""
@@ -222,12 +230,12 @@ class Model:
         self.choices[self._block_name(p)] = (label, float("nan"))
         if forced is None:
             return [self._conv_op(Lr, packed, L) for Lr in (e, d, p)]
-        tile, w = forced
-        sp = dataclasses.replace(spec, tile=tile, weights=w)
+        kernel, tile, w = forced
+        sp = dataclasses.replace(spec, tile=tile, weights=w, kernel=kernel)
         pl = sp.plan()
-        if (pl.th, pl.tw, bool(pl.resident)) != (tile[0], tile[1], w == conv.IrWeights.RESIDENT):
+        if (pl.kernel, pl.th, pl.tw, bool(pl.resident)) != (int(kernel), tile[0], tile[1], w == conv.IrWeights.RESIDENT):
             raise conv.AihError(f"{self._block_name(p)}: {label!r} planned as "
-                                f"{self.label_of(pl.th, pl.tw, pl.resident)!r}")
+                                f"{self.label_of(pl.kernel, pl.th, pl.tw, pl.resident)!r}")
         return [self._fused_op((e, d, p, sp), packed, L)]
 
     def _tuned_block(self, blk, packed, L, allow_unfused: bool) -> list:

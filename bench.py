@@ -151,7 +151,9 @@ def main() -> int:
         g = groups.setdefault(key, dict(launches=0, secs=0.0, flops=0, bytes=0, grids=[]))
         g["launches"] += 1
         if op.kind == "ir_block":
-            g["grids"].append(op.spec.plan().grid * 256)  # dispatch size in threads, as rocprofv3 lists it
+            pl = op.spec.plan()
+            # dispatch size in threads, as rocprofv3 lists it
+            g["grids"].append(pl.grid * 64 * pl.waves)
         g["secs"] += t
         g["flops"] += fl
         g["bytes"] += by
@@ -259,6 +261,10 @@ def kernel_key(conv, op, n, dt, dtname) -> str:
     trace names it for the fused block; descriptive for the conv kernels)."""
     if op.kind == "ir_block":
         p = op.spec.plan()
+        if p.kernel == conv.IrKernel.WAVE:
+            s = op.spec.s
+            npi = 2 if ((p.th - 1) * s + 3) * ((p.tw - 1) * s + 3) <= 64 else 5
+            return f"ir_wave_kernel<{int(dt)}, {op.spec.cin // 16}, {npi}, {op.spec.cout // 32}>"
         npw = -(-(-(-p.th * p.tw // 32)) // 4)
         A = conv.Activation
         clamp = all(int(x) in (A.NONE, A.RELU, A.RELU6, A.CLAMP01)

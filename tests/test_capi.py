@@ -238,8 +238,10 @@ ENCODER_BLOCKS = [  # (n, ih, iw, cin, cexp, cout, s) of the 160x288 encoder's t
 @pytest.mark.parametrize("blk", ENCODER_BLOCKS, ids=lambda b: "x".join(map(str, b)))
 def test_ir_block_plan_covers_the_output_and_fits_lds(blk, dt):
     n, ih, iw, cin, cexp, cout, s = blk
-    spec = conv.IrBlockSpec(ih=ih, iw=iw, cin=cin, cexp=cexp, cout=cout, s=s, n=n, dt=conv.DType(dt))
+    spec = conv.IrBlockSpec(ih=ih, iw=iw, cin=cin, cexp=cexp, cout=cout, s=s, n=n, dt=conv.DType(dt),
+                            kernel=conv.IrKernel.TILE)
     p = spec.plan()
+    assert p.kernel == conv.IrKernel.TILE
     oh, ow = spec.out_hw()
     tiles_y, tiles_x = -(-oh // p.th), -(-ow // p.tw)
     assert p.tiles == n * tiles_y * tiles_x
@@ -257,6 +259,33 @@ def test_ir_block_plan_covers_the_output_and_fits_lds(blk, dt):
     need = halo * (cin * es + 16) + halo * (p.ec * es + 16) + wn * cin * es + wn * cout * es
     need += 11 * wn * es + cout * 4
     assert p.lds_bytes >= need
+
+
+@pytest.mark.parametrize("dt", [1, 2], ids=["f16", "bf16"])
+@pytest.mark.parametrize("blk", ENCODER_BLOCKS, ids=lambda b: "x".join(map(str, b)))
+def test_ir_wave_plan_covers_the_output_and_fits_lds(blk, dt):
+    """The wave kernel: tiles of at most 32 output pixels whose halo fits the
+    instantiation's blocks, every tile covered, and the LDS it addresses --
+    weight slots (all chunks or two), the fp32 projection bias, one expanded
+    region of NPI x 32 pixels x 80 bytes per wavefront."""
+    n, ih, iw, cin, cexp, cout, s = blk
+    spec = conv.IrBlockSpec(ih=ih, iw=iw, cin=cin, cexp=cexp, cout=cout, s=s, n=n, dt=conv.DType(dt),
+                            kernel=conv.IrKernel.WAVE)
+    if not spec.fusable():
+        _expect_error(spec.plan, "wave")
+        return
+    p = spec.plan()
+    oh, ow = spec.out_hw()
+    assert p.kernel == conv.IrKernel.WAVE and p.ec == 32 and p.chunks == cexp // 32
+    assert p.th * p.tw <= 32 and p.th <= oh and p.tw <= ow
+    assert p.tiles == n * -(-oh // p.th) * -(-ow // p.tw)
+    halo = ((p.th - 1) * s + 3) * ((p.tw - 1) * s + 3)
+    npi = 2 if halo <= 64 else 5
+    assert halo <= npi * 32
+    slot = 64 * cin + 64 * cout + 11 * 32 * 2
+    weights = (cexp // 32 if p.resident else 2) * slot
+    assert p.lds_bytes >= weights + cout * 4 + 2 * npi * 32 * 80 and p.lds_bytes <= 160 * 1024
+    assert 1 <= p.grid <= p.tiles
 
 
 def test_ir_block_rejects_unfusable_shapes():
