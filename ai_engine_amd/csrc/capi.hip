@@ -529,7 +529,8 @@ int plan_ir_wave(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, aih::IrWa
     return AIH_OK;
   }
   const char *why = aih::irw_plan(d->n, d->ih, d->iw, oh, ow, d->cin, d->cexp, d->cout, d->s, d->dt,
-                                  ir_clamp_acts(d), d->tile_h, d->tile_w, d->weights, p);
+                                  ir_clamp_acts(d), d->act_expand == AIH_ACT_RELU && d->act_dw == AIH_ACT_RELU,
+                                  d->tile_h, d->tile_w, d->weights, p);
   if (why) return d->kernel == AIH_IR_KERNEL_WAVE ? fail(std::string("ir_block: ") + why) : AIH_OK;
   *use = true;
   return AIH_OK;

@@ -103,9 +103,11 @@ struct IrWavePlan {
 // chunks fit in LDS next to the eight wavefronts' expanded regions).
 // Returns nullptr, or the reason the block cannot run on this kernel
 // (dtype, activations, widths without an instantiation, LDS).
+// rl: the expand and depthwise activations are both ReLU (selects the
+// instantiation whose register use bounds the occupancy).
 const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
-                     uint32_t CO, uint32_t S, int dt, bool cl, uint32_t tile_h, uint32_t tile_w, int32_t weights,
-                     IrWavePlan *p);
+                     uint32_t CO, uint32_t S, int dt, bool cl, bool rl, uint32_t tile_h, uint32_t tile_w,
+                     int32_t weights, IrWavePlan *p);
 
 hipError_t launch_ir_wave(const IrWaveArgs &a, int dt, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
                           hipStream_t st);

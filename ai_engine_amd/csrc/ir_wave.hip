@@ -18,16 +18,17 @@ namespace {
 uint32_t cdiv(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
 
-int irw_occupancy(int dt, uint32_t ke, uint32_t npi, uint32_t nob, uint32_t waves, uint32_t lds) {
+int irw_occupancy(int dt, uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves, uint32_t lds) {
   static std::mutex mu;
-  static std::map<std::tuple<int, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, int>, int> cache;
+  static std::map<std::tuple<int, uint32_t, uint32_t, uint32_t, bool, uint32_t, uint32_t, int>, int> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = -1;
   std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_tuple(dt, ke, npi, nob, waves, lds, dev);
+  const auto key = std::make_tuple(dt, ke, npi, nob, rl, waves, lds, dev);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
-  int occ = dt == DT_F16 ? ir_wave_occ_f16(ke, npi, nob, waves, lds) : ir_wave_occ_bf16(ke, npi, nob, waves, lds);
+  int occ = dt == DT_F16 ? ir_wave_occ_f16(ke, npi, nob, rl, waves, lds)
+                         : ir_wave_occ_bf16(ke, npi, nob, rl, waves, lds);
   // without a device the runtime cannot answer: plan for one workgroup per CU
   if (occ <= 0) occ = 1;
   cache[key] = occ;
@@ -41,8 +42,8 @@ constexpr uint32_t kTiles[][2] = {{4, 8}, {8, 4}, {5, 6}, {6, 5}, {2, 16}, {16, 
 }  // namespace
 
 const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
-                     uint32_t CO, uint32_t S, int dt, bool cl, uint32_t tile_h, uint32_t tile_w, int32_t weights,
-                     IrWavePlan *out) {
+                     uint32_t CO, uint32_t S, int dt, bool cl, bool rl, uint32_t tile_h, uint32_t tile_w,
+                     int32_t weights, IrWavePlan *out) {
   if (dt != DT_F16 && dt != DT_BF16) return "the wave kernel takes f16 / bf16 storage";
   if (!cl) return "the wave kernel takes clamp-type activations (identity, ReLU, ReLU6, clamp01)";
   if (C % 16 || E % 32 || CO % 32 || C == 0 || E == 0 || CO == 0) return "cin % 16, cexp % 32 and cout % 32 needed";
@@ -63,7 +64,8 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
   };
   static std::mutex mu;
   static std::map<Key, IrWavePlan> cache;
-  const Key key{{N, IH, IW, OH, OW, C, E, CO, S, (uint32_t)dt, tile_h, tile_w, (uint32_t)weights, (uint32_t)dev, 1u}};
+  const Key key{{N, IH, IW, OH, OW, C, E, CO, S, (uint32_t)dt, tile_h, tile_w, (uint32_t)weights, (uint32_t)dev,
+                 rl ? 1u : 0u}};
   {
     std::lock_guard<std::mutex> lock(mu);
     auto it = cache.find(key);
@@ -105,7 +107,7 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
         p.lds_xe = align16(p.lds_bp + CO * 4);
         p.lds = p.lds_xe + waves * npi * 32 * IRW_RPE;
         if (p.lds > 160u * 1024u) continue;
-        const int occ = irw_occupancy(dt, ke, npi, nob, waves, p.lds);
+        const int occ = irw_occupancy(dt, ke, npi, nob, rl, waves, p.lds);
         p.tiles_y = cdiv(OH, th);
         p.tiles_x = cdiv(OW, tw);
         const uint64_t nt = (uint64_t)N * p.tiles_y * p.tiles_x;

@@ -8,8 +8,8 @@ hipError_t launch_ir_wave_f16(const IrWaveArgs &a, uint32_t npi, uint32_t waves,
   return irw_launch_dt<DT_F16>(a, npi, waves, lds, grid, st);
 }
 
-int ir_wave_occ_f16(uint32_t ke, uint32_t npi, uint32_t nob, uint32_t waves, uint32_t lds) {
-  return irw_occ_dt<DT_F16>(ke, npi, nob, waves, lds);
+int ir_wave_occ_f16(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves, uint32_t lds) {
+  return irw_occ_dt<DT_F16>(ke, npi, nob, rl, waves, lds);
 }
 
 }  // namespace aih

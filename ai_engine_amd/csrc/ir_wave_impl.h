@@ -55,6 +55,30 @@ __device__ __forceinline__ void irw_dma(char *dst, uint32_t n, __amdgpu_buffer_r
   }
 }
 
+// ReLU of two 16-bit floats packed in 32 bits, as 16-bit signed integers:
+// every negative float (and -0) has its sign bit set, so max(bits, 0) is 0
+// exactly where max(x, 0) is, and a non-negative float keeps its bits (one
+// v_pk_max_i16 for two values). Rounding is monotone and keeps the sign, so
+// relu(round(x)) == round(relu(x)) bit for bit: packing first is exact.
+__device__ __forceinline__ uint32_t irw_relu2(uint32_t v) {
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(s16x2, v), s16x2{0, 0}));
+}
+
+// act(v) rounded to the storage dtype, 4 values -> 8 bytes: ReLU after the
+// conversion on packed 16-bit integers; other clamp-type activations before
+// it (one v_med3_f32 each).
+template <int DT, bool RELU>
+__device__ __forceinline__ u32x2 irw_act_pack4(const Act &p, f32x4 v) {
+  if constexpr (RELU) {
+    const u32x2 b = pack4<DT>(v);
+    return u32x2{irw_relu2(b.x), irw_relu2(b.y)};
+  }
+  float t[4] = {v.x, v.y, v.z, v.w};
+  ir_act<true, 4>(p, t);
+  return pack4<DT>(f32x4{t[0], t[1], t[2], t[3]});
+}
+
 // Orders this wavefront's LDS accesses on either side (its lanes write the
 // expanded chunk that other lanes of the same wavefront read next; a
 // wavefront's LDS operations complete in issue order, so only the compiler
@@ -65,8 +89,9 @@ __device__ __forceinline__ void irw_wave_order() {
 }
 
 // KE: expand K steps (C / 16); NPI: 32-pixel blocks of the halo tile; NOB:
-// projection blocks of 32 output channels.
-template <int DT, int KE, int NPI, int NOB>
+// projection blocks of 32 output channels; RL: the expand and depthwise
+// activations are both ReLU (applied to the packed 16-bit results).
+template <int DT, int KE, int NPI, int NOB, bool RL>
 __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   static_assert(DT == DT_F16 || DT == DT_BF16, "16-bit storage");
   extern __shared__ __align__(16) char lds[];
@@ -74,6 +99,16 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   constexpr uint32_t GB = 4 * ES;  // one packed group: 4 K of one channel
   constexpr uint32_t C = KE * KSTEP;
   constexpr uint32_t WES = EC * C * ES;  // expand weights of one chunk
+  // depthwise taps whose operands are read in one batch: all nine when the
+  // registers held across a chunk (input halo, expand A operands, projection
+  // accumulators) leave room for 72 more, else one row of three. The
+  // narrowest shape (HELD <= 64) fits four waves per SIMD in 128 VGPRs only
+  // with the short batch and the unpacked ReLU; four waves beat both there.
+  constexpr int HELD = 4 * NPI * KE + 4 * KE + 16 * NOB;
+  constexpr int TB = HELD > 64 && HELD <= 120 ? 9 : 3;
+  // packed ReLU where the registers allow it (it keeps the packed results
+  // live longer; the widest instantiations would spill)
+  constexpr bool RLP = RL && HELD > 64 && HELD <= 130;
   const int tid = threadIdx.x;
   const int lane = tid & 63, l32 = lane & 31, lh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -194,11 +229,9 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
       for (int k = 0; k < KE; ++k) e = ir_mma<DT>(aw[k], xop[b][k], e);
       char *row = XeL + (b * 32 + l32) * IRW_RPE;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float v[4] = {e[4 * q], e[4 * q + 1], e[4 * q + 2], e[4 * q + 3]};
-        ir_act<true, 4>(act_e, v);
-        *reinterpret_cast<u32x2 *>(row + (8 * q + 4 * lh) * ES) = pack4<DT>(f32x4{v[0], v[1], v[2], v[3]});
-      }
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<u32x2 *>(row + (8 * q + 4 * lh) * ES) =
+            irw_act_pack4<DT, RLP>(act_e, f32x4{e[4 * q], e[4 * q + 1], e[4 * q + 2], e[4 * q + 3]});
     }
     irw_wave_order();
 
@@ -208,17 +241,30 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
     const uint32_t wp_ks = KSTEP / 4 * a.CO * GB, wp_next = a.CO * GB;
 #pragma unroll 1
     for (int ks = 0; ks < NKS; ++ks) {
-      u32x4 wv[9];
-#pragma unroll
-      for (int t = 0; t < 9; ++t) wv[t] = *reinterpret_cast<const u32x4 *>(wdp + t * (EC * ES) + ks * 32);
+      // the operands of TB taps go out together (2 * TB reads in flight),
+      // then their FMAs; all nine at once where the registers allow
       float d[HK];
       ir_unpack<DT, HK>(*reinterpret_cast<const u32x4 *>(bdp + ks * 32), d);
 #pragma unroll
-      for (int t = 0; t < 9; ++t)
-        ir_fma_taps<DT, HK>(*reinterpret_cast<const u32x4 *>(XeL + rowo[t / 3] + (t % 3) * IRW_RPE + ks * 32), wv[t],
-                            d);
-      ir_act<true, HK>(act_d, d);
-      const u32x4 bop = ir_pack<DT, HK>(d);
+      for (int t0 = 0; t0 < 9; t0 += TB) {
+        u32x4 wv[TB], xv[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) wv[t] = *reinterpret_cast<const u32x4 *>(wdp + (t0 + t) * (EC * ES) + ks * 32);
+#pragma unroll
+        for (int t = 0; t < TB; ++t)
+          xv[t] = *reinterpret_cast<const u32x4 *>(XeL + rowo[(t0 + t) / 3] + ((t0 + t) % 3) * IRW_RPE + ks * 32);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
+      }
+      u32x4 bop;
+      if constexpr (RLP) {
+        bop = ir_pack<DT, HK>(d);
+        bop = u32x4{irw_relu2(bop.x), irw_relu2(bop.y), irw_relu2(bop.z), irw_relu2(bop.w)};
+      } else {
+        ir_act<true, HK>(act_d, d);
+        bop = ir_pack<DT, HK>(d);
+      }
 #pragma unroll
       for (int o = 0; o < NOB; ++o)
         acc[o] = ir_mma<DT>(ir_ld_w<DT>(wpp + o * (32 * GB) + ks * wp_ks, wp_next), bop, acc[o]);
@@ -280,26 +326,26 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   ir_dma_wait();
 }
 
-template <int DT, int KE, int NPI, int NOB>
+template <int DT, int KE, int NPI, int NOB, bool RL>
 inline hipError_t irw_prepare_inst() {
-  static const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(ir_wave_kernel<DT, KE, NPI, NOB>),
+  static const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(ir_wave_kernel<DT, KE, NPI, NOB, RL>),
                                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   return e;
 }
 
-template <int DT, int KE, int NPI, int NOB>
+template <int DT, int KE, int NPI, int NOB, bool RL>
 inline hipError_t irw_launch_inst(const IrWaveArgs &a, uint32_t waves, uint32_t lds, uint32_t grid, hipStream_t st) {
-  const hipError_t e = irw_prepare_inst<DT, KE, NPI, NOB>();
+  const hipError_t e = irw_prepare_inst<DT, KE, NPI, NOB, RL>();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((ir_wave_kernel<DT, KE, NPI, NOB>), dim3(grid), dim3(64 * waves), lds, st, a);
+  hipLaunchKernelGGL((ir_wave_kernel<DT, KE, NPI, NOB, RL>), dim3(grid), dim3(64 * waves), lds, st, a);
   return hipGetLastError();
 }
 
-template <int DT, int KE, int NPI, int NOB>
+template <int DT, int KE, int NPI, int NOB, bool RL>
 inline int irw_occ_inst(uint32_t waves, uint32_t lds) {
-  if (irw_prepare_inst<DT, KE, NPI, NOB>() != hipSuccess) return 0;
+  if (irw_prepare_inst<DT, KE, NPI, NOB, RL>() != hipSuccess) return 0;
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_wave_kernel<DT, KE, NPI, NOB>, (int)(64 * waves),
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_wave_kernel<DT, KE, NPI, NOB, RL>, (int)(64 * waves),
                                                    lds) != hipSuccess)
     return 0;
   return per_cu;
@@ -318,21 +364,28 @@ inline bool irw_has_shape(uint32_t ke, uint32_t npi, uint32_t nob) {
   return false;
 }
 
+// Both inner activations ReLU: the instantiation that applies them to packed results.
+inline bool irw_relu_inner(int act_e, int act_d) { return act_e == AIH_ACT_RELU && act_d == AIH_ACT_RELU; }
+
 template <int DT>
 inline hipError_t irw_launch_dt(const IrWaveArgs &a, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
                                 hipStream_t st) {
   const uint32_t ke = a.C / 16, nob = a.CO / 32;
-#define AIH_IRW_LAUNCH(KE, NPI, NOB) \
-  if (ke == KE && npi == NPI && nob == NOB) return irw_launch_inst<DT, KE, NPI, NOB>(a, waves, lds, grid, st);
+  const bool rl = irw_relu_inner(a.act_e, a.act_d);
+#define AIH_IRW_LAUNCH(KE, NPI, NOB)                                                          \
+  if (ke == KE && npi == NPI && nob == NOB)                                                   \
+    return rl ? irw_launch_inst<DT, KE, NPI, NOB, true>(a, waves, lds, grid, st)             \
+              : irw_launch_inst<DT, KE, NPI, NOB, false>(a, waves, lds, grid, st);
   AIH_IRW_SHAPES(AIH_IRW_LAUNCH)
 #undef AIH_IRW_LAUNCH
   return hipErrorInvalidValue;
 }
 
 template <int DT>
-inline int irw_occ_dt(uint32_t ke, uint32_t npi, uint32_t nob, uint32_t waves, uint32_t lds) {
-#define AIH_IRW_OCC(KE, NPI, NOB) \
-  if (ke == KE && npi == NPI && nob == NOB) return irw_occ_inst<DT, KE, NPI, NOB>(waves, lds);
+inline int irw_occ_dt(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves, uint32_t lds) {
+#define AIH_IRW_OCC(KE, NPI, NOB)                                                                        \
+  if (ke == KE && npi == NPI && nob == NOB)                                                              \
+    return rl ? irw_occ_inst<DT, KE, NPI, NOB, true>(waves, lds) : irw_occ_inst<DT, KE, NPI, NOB, false>(waves, lds);
   AIH_IRW_SHAPES(AIH_IRW_OCC)
 #undef AIH_IRW_OCC
   return 0;
@@ -342,7 +395,7 @@ hipError_t launch_ir_wave_f16(const IrWaveArgs &a, uint32_t npi, uint32_t waves,
                               hipStream_t st);
 hipError_t launch_ir_wave_bf16(const IrWaveArgs &a, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
                                hipStream_t st);
-int ir_wave_occ_f16(uint32_t ke, uint32_t npi, uint32_t nob, uint32_t waves, uint32_t lds);
-int ir_wave_occ_bf16(uint32_t ke, uint32_t npi, uint32_t nob, uint32_t waves, uint32_t lds);
+int ir_wave_occ_f16(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves, uint32_t lds);
+int ir_wave_occ_bf16(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves, uint32_t lds);
 
 }  // namespace aih
