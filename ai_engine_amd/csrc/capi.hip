@@ -903,6 +903,7 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
       a.C = d->cin;
       a.E = d->cexp;
       a.CO = d->cout;
+      a.COP = aih::ir_cop(d->cout);
       a.S = d->s;
       a.PT = (int32_t)d->pad[0];
       a.PL = (int32_t)d->pad[1];
@@ -952,6 +953,7 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
     a.C = d->cin;
     a.E = d->cexp;
     a.CO = d->cout;
+    a.COP = aih::ir_cop(d->cout);
     a.S = d->s;
     a.PT = (int32_t)d->pad[0];
     a.PL = (int32_t)d->pad[1];

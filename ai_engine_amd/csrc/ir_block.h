@@ -20,6 +20,7 @@ struct IrArgs {
   void *y;               // [N][OH][OW][CO]
   uint32_t N, IH, IW, OH, OW;
   uint32_t C, E, CO;
+  uint32_t COP;          // CO rounded up to 32: the projection's MFMA width and LDS weight pitch
   uint32_t S;
   int32_t PT, PL;
   uint32_t TH, TW;       // output tile
@@ -75,6 +76,7 @@ struct IrWaveArgs {
   void *y;               // [N][OH][OW][CO]
   uint32_t N, IH, IW, OH, OW;
   uint32_t C, E, CO, S;
+  uint32_t COP;             // CO rounded up to 32: the projection's MFMA width and LDS weight pitch
   int32_t PT, PL;
   uint32_t TH, TW, HH, HW;  // output tile (<= 32 pixels), input (halo) tile
   uint32_t tiles_y, tiles_x, ntiles;
@@ -85,9 +87,14 @@ struct IrWaveArgs {
   FastDiv fd_hw, fd_tw, fd_tx, fd_pi;
 };
 
-// Bytes of one chunk's weight slot: expand [C/4][32][4], project [8][CO][4],
-// then IRW_SMB bytes of depthwise taps and biases (16-bit elements).
-__host__ __device__ inline uint32_t irw_slot_bytes(uint32_t C, uint32_t CO) { return 64 * C + 64 * CO + IRW_SMB; }
+// Bytes of one chunk's weight slot: expand [C/4][32][4], project [8][COP][4]
+// (channels CO..COP zero), then IRW_SMB bytes of depthwise taps and biases
+// (16-bit elements).
+__host__ __device__ inline uint32_t irw_slot_bytes(uint32_t C, uint32_t COP) { return 64 * C + 64 * COP + IRW_SMB; }
+
+// The projection width the kernels compute: cout (a multiple of 16) rounded
+// up to whole 32-channel MFMA blocks.
+__host__ __device__ inline uint32_t ir_cop(uint32_t CO) { return (CO + 31) / 32 * 32; }
 
 // Tile, weight placement and LDS layout of one launch of the wave kernel.
 struct IrWavePlan {

@@ -41,10 +41,11 @@ int reg_occupancy(int dt, uint32_t nob, uint32_t npw, bool cl) {
 }
 
 // LDS regions of the kernel: input tile, the expanded chunk, and WR/32 weight
-// slots, each holding one 32-channel chunk's expand, project and depthwise
-// weights and biases in their packed layouts (all of E when the weights are
-// resident, else two slots), and the fp32 projection bias.
-void lds_layout(uint32_t C, uint32_t CO, uint32_t WR, uint32_t NPI, int dt, IrPlan *p) {
+// slots, each holding one 32-channel chunk's expand, project (rows of COP
+// channels) and depthwise weights and biases in their packed layouts (all of
+// E when the weights are resident, else two slots), and the fp32 projection
+// bias.
+void lds_layout(uint32_t C, uint32_t COP, uint32_t CO, uint32_t WR, uint32_t NPI, int dt, IrPlan *p) {
   const uint32_t es = dt == DT_F32 ? 4 : 2;
   const uint32_t rpx = C * es + 16, rpe = IR_EC * es + 16;
   uint32_t off = 0;
@@ -55,7 +56,7 @@ void lds_layout(uint32_t C, uint32_t CO, uint32_t WR, uint32_t NPI, int dt, IrPl
   p->lds_we = off;
   off = align16(off + WR * C * es);
   p->lds_wp = off;
-  off = align16(off + WR * CO * es);
+  off = align16(off + WR * COP * es);
   p->lds_sm = off;
   off = align16(off + WR * 11 * es);
   p->lds_bp = off;
@@ -84,7 +85,7 @@ const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t 
   if (C % kstep) return f32 ? "expand input channels must be a multiple of 8" : "expand input channels must be a multiple of 16";
   if (C > 128) return "expand input channels must be at most 128";
   if (E % 32) return "expanded channels must be a multiple of 32";
-  if (CO % 32 || CO > 128) return "project output channels must be a multiple of 32 and at most 128";
+  if (CO % 16 || CO > 128) return "project output channels must be a multiple of 16 and at most 128";
   if (S != 1 && S != 2) return "depthwise stride must be 1 or 2";
   if (ec_force && ec_force != IR_EC) return "the kernel walks E in chunks of 32 channels";
   if ((tile_h && tile_h > OH) || (tile_w && tile_w > OW)) return "forced tile larger than the output";
@@ -114,7 +115,7 @@ const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t 
   }
 
   const int cus = (int)device_cus();
-  const uint32_t nob = CO / 32;
+  const uint32_t COP = ir_cop(CO), nob = COP / 32;
   const uint32_t ec = IR_EC, chunks = E / IR_EC;
   // Per-wavefront cycle estimates: one 32-channel chunk of the depthwise +
   // projection for a 32-pixel block (VALU-bound: 9 FMAs per channel and ~50%
@@ -149,7 +150,7 @@ const char *ir_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t 
         p.NPB = npb;
         p.EC = ec;
         p.resident = resident;
-        lds_layout(C, CO, resident ? E : 2 * ec, npi, dt, &p);
+        lds_layout(C, COP, CO, resident ? E : 2 * ec, npi, dt, &p);
         if (p.lds > kMaxLds) continue;
         const uint32_t npw = cdiv(npb, 4);
         const int occ_r = reg_occupancy(dt, nob, npw, cl);

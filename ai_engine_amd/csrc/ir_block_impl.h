@@ -200,7 +200,8 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   // chunk c in slot c & 1. Every slot holds the chunk's weights byte for byte
   // as packed by the converter:
   //   WeL [slot][C/4 groups][32 channels][GB]    expand, group kq of channel e
-  //   WpL [slot][EC/4 groups][CO][GB]            project (one contiguous range)
+  //   WpL [slot][EC/4 groups][COP][GB]           project (one contiguous range;
+  //                                              channels CO..COP zero)
   //   SmL [slot][11][32] x ES                    depthwise taps 0..8, depthwise bias, expand bias
   char *XL = lds + a.lds_x;    // [NPI*32][RPX]   input tile
   char *XeL = lds + a.lds_xe;  // [NPI*32][RPE]   expanded chunk
@@ -214,7 +215,8 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   const uint32_t nks_e = a.C / KSTEP;
   const uint32_t HPIX = a.HH * a.HW;
   const uint32_t TPIX = a.TH * a.TW;
-  const uint32_t WES = EC * a.C * ES, WPS = EC * a.CO * ES;  // bytes of one slot
+  const uint32_t WES = EC * a.C * ES, WPS = EC * a.COP * ES;  // bytes of one slot
+  const uint32_t WPG = EC * a.CO * ES;                        // a chunk's project weights in memory
   const Act act_e = act_params(a.act_e), act_d = act_params(a.act_d), act_p = act_params(a.act_p);
 
   const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x, a.nxcd);
@@ -232,14 +234,23 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
   // ---- weights of chunk c (expanded channels [32c, 32c + 32)) -> slot s ----
   // Packed 1x1 weights hold element (k, n) at (k/4 * Nn + n) * 4 + k%4
   // (pack.rs:95 with one tap): the chunk's expand weights are C/4 runs of
-  // 32 * GB bytes, its project weights one run of WPS bytes; depthwise
-  // weights [tap][E/4][4] give 9 runs of 32 * ES bytes.
+  // 32 * GB bytes, its project weights one run of WPG bytes (EC/4 runs of CO
+  // channels, each to a COP-channel row when CO < COP); depthwise weights
+  // [tap][E/4][4] give 9 runs of 32 * ES bytes.
   auto dma_chunk = [&](uint32_t c, uint32_t s) {
     constexpr uint32_t GR = EC * GB / 16;  // 16-byte items per expand run
     ir_dma<16>(WeL + s * WES, (a.C / 4) * GR, rs_we, wave, lane, 0, [&](uint32_t g) -> uint32_t {
       return ((g / GR) * a.E + EC * c) * GB + (g % GR) * 16;
     });
-    ir_dma<16>(WpL + s * WPS, WPS / 16, rs_wp, wave, lane, 1, [&](uint32_t g) -> uint32_t { return c * WPS + g * 16; });
+    if (a.COP == a.CO) {
+      ir_dma<16>(WpL + s * WPS, WPS / 16, rs_wp, wave, lane, 1,
+                 [&](uint32_t g) -> uint32_t { return c * WPG + g * 16; });
+    } else {
+      const uint32_t rb = a.CO * GB;  // bytes of one K group's run
+      for (uint32_t q = 0; q < EC / 4; ++q)
+        ir_dma<16>(WpL + s * WPS + q * (a.COP * GB), rb / 16, rs_wp, wave, lane, (int)(q & 3),
+                   [&](uint32_t g) -> uint32_t { return c * WPG + q * rb + g * 16; });
+    }
     constexpr uint32_t TR = EC * ES / 16;  // 16-byte items per depthwise tap run
     char *sm = SmL + s * SMB;
     ir_dma<16>(sm, 9 * TR, rs_wd, wave, lane, 2, [&](uint32_t g) -> uint32_t {
@@ -254,6 +265,15 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
 
   for (uint32_t i = tid; i < a.CO / 4; i += 256)
     *reinterpret_cast<f32x4 *>(BpL + 4 * i) = Vec4IO<DT>::load(a.bp, i);
+  if (a.COP != a.CO) {
+    // project weights of channels CO..COP: zero in every slot, for good (the
+    // copies write only channels below CO)
+    const uint32_t nslots = a.resident ? nchunks : 2u, pad16 = (a.COP - a.CO) * GB / 16;
+    for (uint32_t i = tid; i < nslots * (EC / 4) * pad16; i += 256) {
+      const uint32_t sq = i / pad16, v = i - sq * pad16;
+      *reinterpret_cast<u32x4 *>(WpL + sq * (a.COP * GB) + a.CO * GB + v * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
   if (a.resident)
     for (uint32_t c = 0; c < nchunks; ++c) dma_chunk(c, c);
 
@@ -421,8 +441,8 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
         const char *wdp = SmL + s * SMB + lh * 16;            // tap t at + t * EC * ES
         const char *bdp = SmL + s * SMB + 9 * EC * ES + lh * 16;
         // lane: output channel l32 of block o, K groups as in the expand
-        const char *wpp = WpL + s * WPS + ((uint32_t)lh * (HK / 4) * a.CO + l32) * GB;
-        const uint32_t wp_ks = KSTEP / 4 * a.CO * GB, wp_next = a.CO * GB;
+        const char *wpp = WpL + s * WPS + ((uint32_t)lh * (HK / 4) * a.COP + l32) * GB;
+        const uint32_t wp_ks = KSTEP / 4 * a.COP * GB, wp_next = a.COP * GB;
         // one K step at a time (unrolled, so that every LDS offset is an
         // immediate; the scheduling barrier keeps the next step's 18 operand
         // reads below this one, which would double the live registers)
@@ -476,6 +496,7 @@ __global__ __launch_bounds__(256) void ir_block_kernel(IrArgs a) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t oc = o * 32 + 8 * q + 4 * lh;
+          if (o == NOB - 1 && oc >= a.CO) continue;  // padding channels of the last block
           f32x4 v = f32x4{acc[i][o][4 * q], acc[i][o][4 * q + 1], acc[i][o][4 * q + 2], acc[i][o][4 * q + 3]} +
                     *reinterpret_cast<const f32x4 *>(BpL + oc);
           {
@@ -520,12 +541,12 @@ inline int ir_occ_inst(uint32_t lds) {
   return per_cu;
 }
 
-// Dispatch on the projection width (NOB = CO / 32 output-channel blocks), the
+// Dispatch on the projection width (NOB = COP / 32 output-channel blocks), the
 // output pixel blocks per wavefront (NPW) and whether every activation is
 // clamp-type.
 template <int DT, bool CL>
 inline hipError_t ir_launch_cl(const IrArgs &a, uint32_t lds, uint32_t grid, hipStream_t st) {
-  const uint32_t nob = a.CO / 32, npw = (a.NPB + 3) / 4;
+  const uint32_t nob = a.COP / 32, npw = (a.NPB + 3) / 4;
   switch (nob * 4 + npw) {
     case 1 * 4 + 1: return ir_launch_inst<DT, 1, 1, CL>(a, lds, grid, st);
     case 1 * 4 + 2: return ir_launch_inst<DT, 1, 2, CL>(a, lds, grid, st);

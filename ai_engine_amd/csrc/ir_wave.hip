@@ -46,11 +46,11 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
                      int32_t weights, IrWavePlan *out) {
   if (dt != DT_F16 && dt != DT_BF16) return "the wave kernel takes f16 / bf16 storage";
   if (!cl) return "the wave kernel takes clamp-type activations (identity, ReLU, ReLU6, clamp01)";
-  if (C % 16 || E % 32 || CO % 32 || C == 0 || E == 0 || CO == 0) return "cin % 16, cexp % 32 and cout % 32 needed";
+  if (C % 16 || E % 32 || CO % 16 || C == 0 || E == 0 || CO == 0) return "cin % 16, cexp % 32 and cout % 16 needed";
   if (S != 1 && S != 2) return "depthwise stride must be 1 or 2";
   if (weights != AIH_IR_WEIGHTS_AUTO && weights != AIH_IR_WEIGHTS_RESIDENT && weights != AIH_IR_WEIGHTS_STREAMED)
     return "unknown weight placement";
-  const uint32_t ke = C / 16, nob = CO / 32;
+  const uint32_t ke = C / 16, COP = ir_cop(CO), nob = COP / 32;
   if (!irw_has_shape(ke, 2, nob) && !irw_has_shape(ke, 5, nob)) return "no wave-kernel instantiation for this width";
   if ((tile_h && tile_h > OH) || (tile_w && tile_w > OW)) return "forced tile larger than the output";
   if (tile_h && tile_w && tile_h * tile_w > 32) return "the wave kernel's tiles hold at most 32 pixels";
@@ -76,7 +76,7 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
   }
 
   const uint32_t cus = device_cus();
-  const uint32_t nchunks = E / 32, slot = irw_slot_bytes(C, CO);
+  const uint32_t nchunks = E / 32, slot = irw_slot_bytes(C, COP);
   bool found = false;
   double best = 0;
   IrWavePlan bp{};

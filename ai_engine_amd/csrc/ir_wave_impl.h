@@ -115,8 +115,9 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   // wavefronts of this workgroup (2, 4 or 8, chosen by the plan)
   const uint32_t nthr = blockDim.x, nwaves = nthr >> 6;
 
-  const uint32_t WPS = EC * a.CO * ES;         // project weights of one chunk
-  const uint32_t SLOT = WES + WPS + IRW_SMB;   // 16-byte multiple (C, CO multiples of 16 / 32)
+  const uint32_t WPG = EC * a.CO * ES;         // project weights of one chunk in memory
+  const uint32_t WPS = EC * a.COP * ES;        // ... in a slot, rows padded to COP channels
+  const uint32_t SLOT = WES + WPS + IRW_SMB;   // 16-byte multiple (C, COP multiples of 16 / 32)
   const uint32_t nchunks = a.E / EC;
   char *WL = lds + a.lds_w;
   float *BpL = reinterpret_cast<float *>(lds + a.lds_bp);
@@ -132,13 +133,22 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   // chunk c's weights (expanded channels [32c, 32c + 32)) -> slot s, byte
   // for byte in the packed layouts: expand element (k, e) at (k/4 * E + e) * 4
   // + k%4 gives C/4 runs of 32 channels; the project weights of K rows
-  // [32c, 32c + 32) are one contiguous run; depthwise taps 9 runs of 32.
+  // [32c, 32c + 32) are one contiguous run (EC/4 runs of CO channels, each
+  // to a COP-channel row when CO < COP); depthwise taps 9 runs of 32.
   auto dma_chunk = [&](uint32_t c, uint32_t s) {
     char *slot = WL + s * SLOT;
     constexpr uint32_t GR = EC * GB / 16;  // 16-byte items per expand run
     irw_dma<16>(slot, (C / 4) * GR, rs_we, wave, lane, nthr,
                 [&](uint32_t g) -> uint32_t { return ((g / GR) * a.E + EC * c) * GB + (g % GR) * 16; });
-    irw_dma<16>(slot + WES, WPS / 16, rs_wp, wave, lane, nthr, [&](uint32_t g) -> uint32_t { return c * WPS + g * 16; });
+    if (a.COP == a.CO) {
+      irw_dma<16>(slot + WES, WPS / 16, rs_wp, wave, lane, nthr,
+                  [&](uint32_t g) -> uint32_t { return c * WPG + g * 16; });
+    } else {
+      const uint32_t rb = a.CO * GB;  // bytes of one K group's run
+      for (uint32_t q = 0; q < EC / 4; ++q)
+        irw_dma<16>(slot + WES + q * (a.COP * GB), rb / 16, rs_wp, (wave + q) % nwaves, lane, nthr,
+                    [&](uint32_t g) -> uint32_t { return c * WPG + q * rb + g * 16; });
+    }
     constexpr uint32_t TR = EC * ES / 16;  // 16-byte items per depthwise tap run
     char *sm = slot + WES + WPS;
     irw_dma<16>(sm, 9 * TR, rs_wd, wave, lane, nthr,
@@ -151,6 +161,16 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
 
   for (uint32_t i = tid; i < a.CO / 4; i += nthr)
     *reinterpret_cast<f32x4 *>(BpL + 4 * i) = Vec4IO<DT>::load(a.bp, i);
+  if (a.COP != a.CO) {
+    // project weights of channels CO..COP: zero in every slot, for good (the
+    // copies write only channels below CO)
+    const uint32_t nslots = a.resident ? nchunks : 2u, pad16 = (a.COP - a.CO) * GB / 16;
+    for (uint32_t i = tid; i < nslots * (EC / 4) * pad16; i += nthr) {
+      const uint32_t sq = i / pad16, v = i - sq * pad16;
+      *reinterpret_cast<u32x4 *>(WL + (sq / (EC / 4)) * SLOT + WES + (sq % (EC / 4)) * (a.COP * GB) + a.CO * GB +
+                                 v * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
   if (a.resident) {
     for (uint32_t c = 0; c < nchunks; ++c) dma_chunk(c, c);
   } else {
@@ -237,8 +257,8 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
 
     const char *wdp = sm + lh * 16;                 // tap t at + t * EC * ES
     const char *bdp = sm + 9 * EC * ES + lh * 16;
-    const char *wpp = slot + WES + ((uint32_t)lh * (HK / 4) * a.CO + l32) * GB;
-    const uint32_t wp_ks = KSTEP / 4 * a.CO * GB, wp_next = a.CO * GB;
+    const char *wpp = slot + WES + ((uint32_t)lh * (HK / 4) * a.COP + l32) * GB;
+    const uint32_t wp_ks = KSTEP / 4 * a.COP * GB, wp_next = a.COP * GB;
 #pragma unroll 1
     for (int ks = 0; ks < NKS; ++ks) {
       // the operands of TB taps go out together (2 * TB reads in flight),
@@ -281,6 +301,7 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const uint32_t oc = o * 32 + 8 * q + 4 * lh;
+        if (o == NOB - 1 && oc >= a.CO) continue;  // padding channels of the last block
         f32x4 v = f32x4{acc[o][4 * q], acc[o][4 * q + 1], acc[o][4 * q + 2], acc[o][4 * q + 3]} +
                   *reinterpret_cast<const f32x4 *>(BpL + oc);
         float t4[4] = {v.x, v.y, v.z, v.w};
@@ -353,8 +374,9 @@ inline int irw_occ_inst(uint32_t waves, uint32_t lds) {
 
 // The (KE, NPI, NOB) combinations with an instantiation: the inverted-residual
 // blocks of the MobileNet-style encoders (C = 16 KE input channels, NPI halo
-// blocks: 2 for a stride-1 tile of <= 32 pixels, 5 for stride 2, NOB = CO / 32).
-#define AIH_IRW_SHAPES(X) X(2, 2, 1) X(2, 5, 2) X(4, 2, 2) X(4, 5, 3) X(6, 2, 3) X(8, 2, 4)
+// blocks: 2 for a stride-1 tile of <= 32 pixels, 5 for stride 2, NOB = COP /
+// 32) and the 48 -> 96 -> 48 blocks of the converter's segmentation model.
+#define AIH_IRW_SHAPES(X) X(2, 2, 1) X(2, 5, 2) X(3, 2, 2) X(4, 2, 2) X(4, 5, 3) X(6, 2, 3) X(8, 2, 4)
 
 inline bool irw_has_shape(uint32_t ke, uint32_t npi, uint32_t nob) {
 #define AIH_IRW_HAS(KE, NPI, NOB) \
@@ -370,7 +392,7 @@ inline bool irw_relu_inner(int act_e, int act_d) { return act_e == AIH_ACT_RELU 
 template <int DT>
 inline hipError_t irw_launch_dt(const IrWaveArgs &a, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
                                 hipStream_t st) {
-  const uint32_t ke = a.C / 16, nob = a.CO / 32;
+  const uint32_t ke = a.C / 16, nob = a.COP / 32;
   const bool rl = irw_relu_inner(a.act_e, a.act_d);
 #define AIH_IRW_LAUNCH(KE, NPI, NOB)                                                          \
   if (ke == KE && npi == NPI && nob == NOB)                                                   \

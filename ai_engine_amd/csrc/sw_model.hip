@@ -9,9 +9,12 @@
 // with its descriptor built once (lower_op, lowering.rs:88-516). Conv ops go
 // through the conv entry points of aih_conv.h exactly as the op-level boundary
 // routes them; the other op kinds through aih_model.h's op entry points.
-// The converter has already decided fusion, topological order and liveness
-// (format/model.rs:1-9); the runtime keeps one buffer per tensor (HBM is not
-// the constraint at these sizes) and does no graph analysis.
+// The converter has already decided its fusions (conv + act + residual),
+// topological order and liveness (format/model.rs:1-9); the runtime keeps one
+// buffer per tensor (HBM is not the constraint at these sizes). On top of
+// that, one graph rewrite of its own: each inverted-residual block (1x1
+// expand -> depthwise 3x3 -> 1x1 project whose intermediates nothing else
+// reads) becomes one aih_ir_block launch, its intermediates never stored.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -21,6 +24,7 @@
 #include <functional>
 #include <map>
 #include <memory>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -142,8 +146,17 @@ struct aih_model {
   size_t ws_bytes = 0;
   float *staging = nullptr;
   size_t staging_floats = 0;
-  std::vector<std::function<int(hipStream_t)>> launches;
+  std::vector<std::function<int(hipStream_t)>> launches;  // per op; empty for a fused block's 2nd and 3rd op
   size_t device_bytes = 0;
+  uint32_t flags = 0;
+  struct Fused {
+    uint32_t first;  // ops first .. first + 2
+    aih_ir_block_desc d;
+    aih_ir_plan plan;
+  };
+  std::vector<Fused> fused;
+  std::vector<int32_t> block_of;  // per op: its fused block, or -1
+  std::vector<int32_t> internal;  // per tensor: first op of the fused block it stays inside, or -1
 
   ~aih_model() {
     for (void *p : allocs) (void)hipFree(p);
@@ -178,6 +191,13 @@ struct aih_model {
   aih_src src_of(uint32_t tid, uint32_t c) const {
     const View &v = views[tid];
     return aih_src{c, v.stride_c, v.c_off};
+  }
+  // fails for a tensor that stays inside a fused block (never stored)
+  void need_stored(uint32_t tid, const char *what) const {
+    if (internal[tid] >= 0)
+      throw std::runtime_error(std::string(what) + ": tensor '" + g.tensors[tid].name +
+                               "' stays inside the fused block of ops " + std::to_string(internal[tid]) + ".." +
+                               std::to_string(internal[tid] + 2) + " (load with AIH_MODEL_NO_FUSE to keep it)");
   }
 };
 
@@ -233,7 +253,7 @@ void alloc_tensors(aih_model *m) {
   size_t total = 0;
   std::vector<size_t> off(T.size(), 0);
   for (size_t i = 0; i < T.size(); ++i) {
-    if (T[i].alias_of >= 0) continue;
+    if (T[i].alias_of >= 0 || m->internal[i] >= 0) continue;
     off[i] = total;
     total += ((size_t)m->n * T[i].h * T[i].w * c4(T[i].c) * es + 255) / 256 * 256;
   }
@@ -241,7 +261,7 @@ void alloc_tensors(aih_model *m) {
   const hipError_t e = hipMemset(arena, 0, total ? total : 16);
   if (e != hipSuccess) throw std::runtime_error(std::string("tensor arena clear: ") + hipGetErrorString(e));
   for (size_t i = 0; i < T.size(); ++i) {
-    if (T[i].alias_of >= 0) continue;
+    if (T[i].alias_of >= 0 || m->internal[i] >= 0) continue;
     m->views[i] = aih_model::View{arena + off[i], (size_t)m->n * T[i].h * T[i].w * c4(T[i].c) * es, c4(T[i].c), 0};
   }
   for (size_t i = 0; i < T.size(); ++i) {
@@ -374,11 +394,121 @@ void need_dense(const aih_model *m, uint32_t tid, const char *role, size_t op_in
                     "' is a channel view; this op needs a whole tensor");
 }
 
+// A tensor a kernel can take as a whole NHWC-C4 buffer: its own, or an alias
+// covering all of its backing tensor's channel groups from the first.
+bool dense_tid(const sw::Model &g, uint32_t tid) {
+  const auto r = g.resolve(tid);
+  return r.second == 0 && c4(g.tensors[r.first].c) == c4(g.tensors[tid].c);
+}
+
+// The tensors each op reads.
+std::set<uint32_t> reads_of(const sw::Op &op) {
+  std::set<uint32_t> r;
+  for (const sw::Part &p : op.srcs) r.insert(p.tid);
+  switch (op.kind) {
+    case sw::OP_CONV:
+      r.insert(op.in);
+      if (op.res >= 0) r.insert((uint32_t)op.res);
+      break;
+    case sw::OP_BINARY:
+      r.insert(op.in);
+      if (op.opnd != sw::OPND_SCALAR && op.opnd != sw::OPND_CVEC) r.insert(op.b_tid);
+      break;
+    case sw::OP_GPOOL:
+    case sw::OP_RESIZE: r.insert(op.in); break;
+    case sw::OP_CONCAT: break;
+  }
+  return r;
+}
+
+bool is_pw(const sw::Op &o) {
+  return o.kind == sw::OP_CONV && o.groups == 1 && o.kh == 1 && o.kw == 1 && o.sh == 1 && o.sw == 1 && o.d == 1 &&
+         !o.pad[0] && !o.pad[1] && !o.pad[2] && !o.pad[3] && o.srcs.empty();
+}
+
+// Inverted-residual blocks that run as one aih_ir_block launch: ops k, k+1,
+// k+2 = 1x1 expand (no residual), depthwise 3x3 (d = 1, square stride) on the
+// expand's output, 1x1 project on the depthwise's output (residual allowed);
+// both intermediates read by exactly that next op and by nothing else (no
+// other op, alias, graph output or state); weights in the activation dtype at
+// the alignment aih_ir_block needs; and a plan that aih_ir_block_plan accepts.
+// The fused kernels take the converter's packed layouts as they are (the
+// 1x1 weights' K groups past cin / 4 and the pitch of kg_pad are never read).
+void find_fusions(aih_model *m) {
+  const auto &ops = m->g.ops;
+  const auto &T = m->g.tensors;
+  m->block_of.assign(ops.size(), -1);
+  m->internal.assign(T.size(), -1);
+  if ((m->flags & AIH_MODEL_NO_FUSE) || m->wdt != m->dt) return;
+  std::vector<uint32_t> readers(T.size(), 0);
+  for (const sw::Op &op : ops)
+    for (uint32_t t : reads_of(op)) ++readers[t];
+  std::vector<bool> pinned(T.size(), false);
+  for (uint32_t t : m->g.outputs) pinned[t] = true;
+  for (const auto &st : m->g.states) pinned[st.first] = pinned[st.second] = true;
+  for (size_t i = 0; i < T.size(); ++i)
+    if (T[i].alias_of >= 0) pinned[i] = pinned[(size_t)T[i].alias_of] = true;
+  auto aligned = [&](const sw::WRef &r, uintptr_t a) { return (reinterpret_cast<uintptr_t>(m->wptr(r)) % a) == 0; };
+  for (size_t k = 0; k + 2 < ops.size();) {
+    const sw::Op &A = ops[k], &B = ops[k + 1], &P = ops[k + 2];
+    bool ok = is_pw(A) && A.res < 0 && B.kind == sw::OP_CONV && B.kh == 3 && B.kw == 3 && B.sh == B.sw &&
+              B.d == 1 && B.groups == B.cin && B.cin == B.cout && B.cout == A.cout && B.in == A.out &&
+              B.srcs.empty() && B.res < 0 && is_pw(P) && P.in == B.out && P.cin == B.cout;
+    ok = ok && readers[A.out] == 1 && readers[B.out] == 1 && !pinned[A.out] && !pinned[B.out] &&
+         dense_tid(m->g, A.in) && dense_tid(m->g, P.out) && (P.res < 0 || dense_tid(m->g, (uint32_t)P.res));
+    ok = ok && aligned(A.w, 16) && aligned(B.w, 16) && aligned(P.w, 16) && aligned(A.b, 8) && aligned(B.b, 8) &&
+         aligned(P.b, 8);
+    if (ok) {
+      aih_ir_block_desc d{};
+      d.n = m->n;
+      d.ih = T[A.in].h;
+      d.iw = T[A.in].w;
+      d.cin = A.cin;
+      d.cexp = A.cout;
+      d.cout = P.cout;
+      d.s = B.sh;
+      std::memcpy(d.pad, B.pad, sizeof(d.pad));
+      d.act_expand = A.act;
+      d.act_dw = B.act;
+      d.act_project = P.act;
+      d.residual = P.res >= 0 ? 1 : 0;
+      d.dt = m->dt;
+      aih_ir_plan plan;
+      if (aih_ir_block_plan(&d, &plan) == AIH_OK) {
+        const int32_t bi = (int32_t)m->fused.size();
+        m->fused.push_back(aih_model::Fused{(uint32_t)k, d, plan});
+        m->block_of[k] = m->block_of[k + 1] = m->block_of[k + 2] = bi;
+        m->internal[A.out] = m->internal[B.out] = (int32_t)k;
+        k += 3;
+        continue;
+      }
+    }
+    ++k;
+  }
+}
+
 void lower(aih_model *m) {
   const auto &T = m->g.tensors;
   for (size_t k = 0; k < m->g.ops.size(); ++k) {
     const sw::Op &op = m->g.ops[k];
     const auto &O = T[op.out];
+    if (m->block_of[k] >= 0) {
+      const aih_model::Fused &f = m->fused[(size_t)m->block_of[k]];
+      if (f.first != k) {
+        m->launches.emplace_back();  // runs in the block's first op
+        continue;
+      }
+      const sw::Op &B = m->g.ops[k + 1], &P = m->g.ops[k + 2];
+      const aih_ir_block_desc d = f.d;
+      const void *x = m->ptr(op.in), *we = m->wptr(op.w), *be = m->wptr(op.b), *wd = m->wptr(B.w),
+                 *bd = m->wptr(B.b), *wp = m->wptr(P.w), *bp = m->wptr(P.b);
+      const void *res = P.res >= 0 ? m->ptr((uint32_t)P.res) : nullptr;
+      void *y = m->ptr(P.out);
+      m->launches.push_back([d, x, we, be, wd, bd, wp, bp, res, y](hipStream_t s) {
+        return aih_ir_block(&d, x, we, be, wd, bd, wp, bp, res, y, s);
+      });
+      continue;
+    }
     need_dense(m, op.out, "output", k);
     void *y = m->ptr(op.out);
     switch (op.kind) {
@@ -545,14 +675,20 @@ void lower(aih_model *m) {
 extern "C" {
 
 aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt) {
+  return aih_model_load_ex(bytes, len, n, dt, 0);
+}
+
+aih_model *aih_model_load_ex(const void *bytes, size_t len, uint32_t n, int32_t dt, uint32_t flags) {
   aih_model *out = nullptr;
   const int rc = api_guarded([&] {
     if (n == 0) return api_fail("model_load: n must be >= 1");
+    if (flags & ~(uint32_t)AIH_MODEL_NO_FUSE) return api_fail("model_load: unknown flags");
     if (dt != -1 && dt != AIH_F32 && dt != AIH_F16 && dt != AIH_BF16) return api_fail("model_load: unknown dtype");
     sw::Container c = sw::parse_container(bytes, len);
     std::unique_ptr<aih_model> m(new aih_model);
     m->g = sw::parse_model(c.json, c.json_len);
     m->n = n;
+    m->flags = flags;
     m->blob_dt = m->g.dt_default == sw::F16 ? AIH_F16 : AIH_F32;
     for (const auto &t : m->g.tensors)
       if (t.dt != m->g.dt_default)
@@ -569,6 +705,7 @@ aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt)
     if (!m->g.consts.empty()) return api_fail("model_load: constant tensors are not supported");
     validate_geometry(m->g);
     prepare_weights(m.get(), c);
+    find_fusions(m.get());
     alloc_tensors(m.get());
     lower(m.get());
     if (m->ws_bytes) m->ws = m->dalloc(m->ws_bytes);
@@ -623,7 +760,8 @@ int aih_model_infer(aih_model *m, aih_stream stream) {
     if (!m) return api_fail("infer: null model");
     hipStream_t s = static_cast<hipStream_t>(stream);
     for (size_t i = 0; i < m->launches.size(); ++i)
-      if (m->launches[i](s) != AIH_OK) return api_fail("infer: op " + std::to_string(i) + ": " + aih_last_error());
+      if (m->launches[i] && m->launches[i](s) != AIH_OK)
+        return api_fail("infer: op " + std::to_string(i) + ": " + aih_last_error());
     return AIH_OK;
   });
 }
@@ -632,9 +770,14 @@ int aih_model_infer_range(aih_model *m, uint32_t first, uint32_t last, aih_strea
   return api_guarded([&] {
     if (!m) return api_fail("infer_range: null model");
     if (first > last || last > m->launches.size()) return api_fail("infer_range: bad op range");
+    for (uint32_t e : {first, last})
+      if (e < m->block_of.size() && m->block_of[e] >= 0 && m->fused[(size_t)m->block_of[e]].first != e)
+        return api_fail("infer_range: op " + std::to_string(e) + " is inside the fused block of ops " +
+                        std::to_string(m->fused[(size_t)m->block_of[e]].first) + "..; a range holds all of it or none");
     hipStream_t s = static_cast<hipStream_t>(stream);
     for (uint32_t i = first; i < last; ++i)
-      if (m->launches[i](s) != AIH_OK) return api_fail("infer: op " + std::to_string(i) + ": " + aih_last_error());
+      if (m->launches[i] && m->launches[i](s) != AIH_OK)
+        return api_fail("infer: op " + std::to_string(i) + ": " + aih_last_error());
     return AIH_OK;
   });
 }
@@ -644,6 +787,7 @@ int aih_model_read_output(aih_model *m, const char *name, float *host_nhwc, size
     if (!m || !host_nhwc) return api_fail("read_output: null argument");
     const int64_t tid = m->find(name);
     if (tid < 0) return api_fail(std::string("read_output: no tensor named '") + (name ? name : "") + "'");
+    m->need_stored((uint32_t)tid, "read_output");
     const auto &t = m->g.tensors[tid];
     const size_t want = (size_t)m->n * t.h * t.w * t.c;
     if (count != want) return api_fail("read_output: expected " + std::to_string(want) + " floats");
@@ -678,6 +822,7 @@ int aih_model_write_tensor(aih_model *m, const char *name, const float *host_nhw
     if (!m || !host_nhwc) return api_fail("write_tensor: null argument");
     const int64_t tid = m->find(name);
     if (tid < 0) return api_fail(std::string("write_tensor: no tensor named '") + (name ? name : "") + "'");
+    m->need_stored((uint32_t)tid, "write_tensor");
     const auto &t = m->g.tensors[tid];
     const size_t want = (size_t)m->n * t.h * t.w * t.c;
     if (count != want) return api_fail("write_tensor: expected " + std::to_string(want) + " floats");
@@ -724,6 +869,7 @@ int aih_model_tensor(const aih_model *m, const char *name, aih_tensor_info *out)
     if (!m || !out) return api_fail("tensor: null argument");
     const int64_t tid = m->find(name);
     if (tid < 0) return api_fail(std::string("tensor: no tensor named '") + (name ? name : "") + "'");
+    m->need_stored((uint32_t)tid, "tensor");
     const auto &t = m->g.tensors[tid];
     const aih_model::View &v = m->views[tid];
     const size_t skip = (size_t)v.c_off * es_of(m->dt);
@@ -735,9 +881,20 @@ int aih_model_tensor(const aih_model *m, const char *name, aih_tensor_info *out)
 int aih_model_get_info(const aih_model *m, aih_model_info *out) {
   return api_guarded([&] {
     if (!m || !out) return api_fail("info: null argument");
+    uint32_t nl = 0;
+    for (const auto &f : m->launches) nl += f ? 1u : 0u;
     *out = aih_model_info{(uint32_t)m->g.tensors.size(), (uint32_t)m->g.ops.size(), (uint32_t)m->g.inputs.size(),
-                          (uint32_t)m->g.outputs.size(), (uint32_t)m->launches.size(), m->dt, m->wdt,
+                          (uint32_t)m->g.outputs.size(), nl, (uint32_t)m->fused.size(), m->dt, m->wdt,
                           m->device_bytes};
+    return AIH_OK;
+  });
+}
+
+int aih_model_fused_block(const aih_model *m, uint32_t i, aih_model_fused_info *out) {
+  return api_guarded([&] {
+    if (!m || !out) return api_fail("fused_block: null argument");
+    if (i >= m->fused.size()) return api_fail("fused_block: no fused block " + std::to_string(i));
+    *out = aih_model_fused_info{m->fused[i].first, m->fused[i].plan};
     return AIH_OK;
   });
 }

@@ -50,15 +50,22 @@ class TensorInfo(C.Structure):
 
 class ModelInfo(C.Structure):
     _fields_ = [("n_tensors", C.c_uint32), ("n_ops", C.c_uint32), ("n_inputs", C.c_uint32),
-                ("n_outputs", C.c_uint32), ("n_launches", C.c_uint32), ("dt", C.c_int32), ("wdt", C.c_int32),
-                ("device_bytes", C.c_size_t)]
+                ("n_outputs", C.c_uint32), ("n_launches", C.c_uint32), ("n_fused", C.c_uint32),
+                ("dt", C.c_int32), ("wdt", C.c_int32), ("device_bytes", C.c_size_t)]
+
+
+class FusedInfo(C.Structure):
+    _fields_ = [("first_op", C.c_uint32), ("plan", conv.IrPlan)]
+
+
+NO_FUSE = 1  # aih_model_flags
 
 
 EXPORTS = (
-    "aih_resize", "aih_gpool", "aih_binary", "aih_concat", "aih_model_load", "aih_model_free",
+    "aih_resize", "aih_gpool", "aih_binary", "aih_concat", "aih_model_load", "aih_model_load_ex", "aih_model_free",
     "aih_model_upload_input", "aih_model_upload_input_device", "aih_model_infer", "aih_model_infer_range",
     "aih_model_read_output", "aih_model_write_tensor", "aih_model_reset", "aih_model_tensor", "aih_model_get_info", "aih_model_input_name", "aih_model_output_name",
-    "aih_sw_describe",
+    "aih_sw_describe", "aih_model_fused_block",
 )
 
 COORD = {"half_pixel": 0, "asymmetric": 1}
@@ -81,6 +88,8 @@ def lib() -> C.CDLL:
         "aih_binary": (C.c_int, [C.POINTER(_Binary), P, P, P, P]),
         "aih_concat": (C.c_int, [C.POINTER(_Concat), C.POINTER(P), P, P]),
         "aih_model_load": (P, [C.c_char_p, sz, u32, i32]),
+        "aih_model_load_ex": (P, [C.c_char_p, sz, u32, i32, u32]),
+        "aih_model_fused_block": (C.c_int, [P, u32, C.POINTER(FusedInfo)]),
         "aih_model_free": (None, [P]),
         "aih_model_upload_input": (C.c_int, [P, C.c_char_p, P, sz, P]),
         "aih_model_upload_input_device": (C.c_int, [P, C.c_char_p, P, sz, P]),
@@ -159,11 +168,14 @@ def concat(parts, n, h, w, dt, y, stream=None):
 # ---------------------------------------------------------------- model
 
 class SwModel:
-    """A .sw model resident on the current HIP device (batch n, outermost)."""
+    """A .sw model resident on the current HIP device (batch n, outermost).
+    fuse=False lowers every op on its own (AIH_MODEL_NO_FUSE); by default each
+    inverted-residual block runs as one fused launch."""
 
-    def __init__(self, data: bytes, n: int = 1, dt: conv.DType | None = None):
+    def __init__(self, data: bytes, n: int = 1, dt: conv.DType | None = None, fuse: bool = True):
         L = lib()
-        self._h = L.aih_model_load(bytes(data), len(data), n, -1 if dt is None else int(dt))
+        self._h = L.aih_model_load_ex(bytes(data), len(data), n, -1 if dt is None else int(dt),
+                                      0 if fuse else NO_FUSE)
         if not self._h:
             raise conv.AihError(conv.last_error())
         self.n = n
@@ -184,6 +196,14 @@ class SwModel:
             self.close()
         except Exception:  # interpreter shutdown
             pass
+
+    def fused_blocks(self) -> list[FusedInfo]:
+        out = []
+        for i in range(self.info.n_fused):
+            f = FusedInfo()
+            conv._check(lib().aih_model_fused_block(self._h, i, C.byref(f)))
+            out.append(f)
+        return out
 
     def tensor(self, name: str) -> TensorInfo:
         t = TensorInfo()

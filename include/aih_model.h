@@ -118,6 +118,21 @@ typedef struct aih_model aih_model;
  * every activation in it. Returns NULL on failure (aih_last_error). The model
  * uses the current HIP device. */
 aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt);
+
+/* aih_model_load with load flags. By default (flags 0, and aih_model_load)
+ * every inverted-residual block of the graph runs as one fused launch
+ * (aih_ir_block): a 1x1 expand, a 3x3 depthwise reading only the expand's
+ * output and a 1x1 projection reading only the depthwise's output,
+ * consecutive in the file's op order, whose two intermediate tensors no other
+ * op, alias, graph output or state uses, and that aih_ir_block_plan accepts
+ * (the plan's deterministic choice of kernel, tile and weight placement).
+ * The intermediates are then never stored: reading, writing or querying them
+ * fails, and aih_model_infer_range may not split a fused block. The reference
+ * runtime dispatches the three convs separately (lowering.rs:122-152); this
+ * fusion has no counterpart there and keeps each conv's arithmetic and
+ * rounding points. AIH_MODEL_NO_FUSE lowers every op on its own. */
+enum aih_model_flags { AIH_MODEL_NO_FUSE = 1 };
+aih_model *aih_model_load_ex(const void *bytes, size_t len, uint32_t n, int32_t dt, uint32_t flags);
 void aih_model_free(aih_model *m);
 
 /* Logical NHWC fp32 (n*h*w*c floats) of an input -> its NHWC-C4 tensor. host
@@ -130,7 +145,9 @@ int aih_model_upload_input_device(aih_model *m, const char *name, const float *d
 /* Runs every op in order on `stream` (asynchronous). */
 int aih_model_infer(aih_model *m, aih_stream stream);
 /* Runs ops [first, last) only (per-op timing and parity; the reference's
- * ai-cpu profiler times op by op, crates/ai-cpu/src/model.rs:241-272). */
+ * ai-cpu profiler times op by op, crates/ai-cpu/src/model.rs:241-272). A
+ * fused block's three ops run together: a range must hold all of them or
+ * none. */
 int aih_model_infer_range(aih_model *m, uint32_t first, uint32_t last, aih_stream stream);
 /* A tensor (by name; outputs and any other tensor) as logical NHWC fp32,
  * n*h*w*c floats; waits for `stream`. */
@@ -153,11 +170,21 @@ typedef struct {
 int aih_model_tensor(const aih_model *m, const char *name, aih_tensor_info *out);
 
 typedef struct {
-  uint32_t n_tensors, n_ops, n_inputs, n_outputs, n_launches;
+  uint32_t n_tensors, n_ops, n_inputs, n_outputs;
+  uint32_t n_launches; /* kernel launches of one aih_model_infer: ops, less two per fused block */
+  uint32_t n_fused;    /* fused inverted-residual blocks */
   int32_t dt, wdt;
   size_t device_bytes; /* weights + tensors + workspace */
 } aih_model_info;
 int aih_model_get_info(const aih_model *m, aih_model_info *out);
+
+/* Fused block i (0 <= i < n_fused): its first op (it covers ops first_op ..
+ * first_op + 2) and the plan aih_ir_block runs it with. */
+typedef struct {
+  uint32_t first_op;
+  aih_ir_plan plan;
+} aih_model_fused_info;
+int aih_model_fused_block(const aih_model *m, uint32_t i, aih_model_fused_info *out);
 /* Name of input / output i (valid while m lives). */
 const char *aih_model_input_name(const aih_model *m, uint32_t i);
 const char *aih_model_output_name(const aih_model *m, uint32_t i);

@@ -16,7 +16,9 @@ chain against the fp32 chain) plus the kernel's bar, and f16 to 2e-2, bf16 to
 
 Shapes cover both strides, residual on/off, odd sizes (tiles overhanging the
 image), images smaller than a tile, one- and multi-chunk expansions, every
-projection width (32..128) and asymmetric padding. Outputs start as NaN.
+projection width (32..128, and 16, 48, 80: part of the last 32-channel MFMA
+block unused) and asymmetric padding. Outputs start as NaN, so a store into a
+padding channel, or a missing one, shows.
 """
 import pytest
 
@@ -49,6 +51,12 @@ CASES = [
     # (act(0) != 0: the border mask, generic activations)
     (2, 11, 19, 32, 128, 32, 1, (1, 1, 1, 1), True, "none/relu6/relu"),
     (2, 12, 20, 32, 128, 64, 2, (1, 1, 1, 1), False, "sigmoid/relu6/none"),
+    # projection widths that are not whole 32-channel MFMA blocks: the
+    # converter's segmentation model's 48 -> 96 -> 48 block (its shape and
+    # activations), 16 and 80 channels
+    (2, 10, 18, 48, 96, 48, 1, (1, 1, 1, 1), True, "relu/relu/none"),
+    (1, 9, 17, 32, 64, 16, 2, (1, 1, 1, 1), False, "relu"),
+    (2, 12, 20, 32, 128, 80, 1, (1, 1, 1, 1), True, "relu6"),
 ]
 
 
@@ -88,3 +96,23 @@ def test_ir_block_matches_oracle_chain(case, dt):
     else:
         # bf16's 8-bit mantissa: ideal storage alone is 0.9e-2 .. 2.3e-2 on these cases
         assert e <= 4e-2, e
+
+
+@pytest.mark.parametrize("kernel", ["tile", "wave"])
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
+def test_ir_block_48_channel_projection_both_kernels(kernel, dt):
+    """The 48 -> 96 -> 48 block (two 32-channel MFMA blocks, the second half
+    zero-weighted and never stored) on each kernel that takes it, weights
+    resident and streamed."""
+    from ai_engine_amd import conv
+    if kernel == "wave" and dt == F32:
+        pytest.skip("the wave kernel takes 16-bit storage")
+    c = G.IrCase(2, 10, 18, 48, 96, 48, 1, (1, 1, 1, 1), True, ("relu", "relu", "none"), dt, seed=7600 + dt)
+    k = conv.IrKernel.TILE if kernel == "tile" else conv.IrKernel.WAVE
+    for w in (conv.IrWeights.RESIDENT, conv.IrWeights.STREAMED):
+        spec = c.spec(kernel=k, weights=w)
+        p = spec.plan()
+        assert p.kernel == k and p.resident == (w == conv.IrWeights.RESIDENT), p
+        e = G.rel_err(c.run(spec), c.want_stored)
+        print(f"{kernel} dt{dt} {w.name}: {p} vs stored-dtype chain {e:.3e}", flush=True)
+        assert e <= BAR_STORED[dt], (w, e)

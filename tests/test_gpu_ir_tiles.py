@@ -1,6 +1,7 @@
 """Every fused launch the load-time tuner can choose, checked: for each of the
 ten inverted-residual blocks of the 160x288 encoder (the headline workload's
-shapes, two images), every candidate the tuner times -- the planner's tile
+shapes, two images) and the 48 -> 96 -> 48 block of the converter's
+segmentation model, every candidate the tuner times -- the planner's tile
 and every forced tile, each with its weights resident in LDS and streamed
 (Model.fused_candidates) -- runs through the C ABI and is compared with the
 oracle's three-op chain (the convs the reference dispatches separately,
@@ -35,6 +36,9 @@ def encoder_blocks():
         e, d, p = layers[i:i + 3]
         out.append((e.name.split(".")[0], (e.ih, e.iw, e.cin, e.cout, p.cout, d.s, p.res is not None)))
     assert len(out) == 10
+    # the four 48 -> 96 -> 48 blocks of the converter's segmentation model
+    # (ops 12-23 of segm_r11_160x288.sw), which the native loader fuses
+    out.append(("segm_ir48", (10, 18, 48, 96, 48, 1, True)))
     return out
 
 

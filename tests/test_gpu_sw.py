@@ -12,6 +12,10 @@
   chained ops); f16 / bf16 (weights converted at load): every op within
   2e-2 of the oracle with the same storage rounding, the end-to-end mask
   agreeing with fp32 on >= 99% of pixels;
+  The model runs both as loaded by default -- its four 48 -> 96 -> 48
+  inverted-residual blocks (ops 12-23) fused into one aih_ir_block launch
+  each, checked block by block against the oracle's three ops -- and with
+  AIH_MODEL_NO_FUSE, op by op;
 * a synthetic conv chain written as a .sw the way the converter writes one,
   through the native loader.
 Outputs of the op tests start as NaN.
@@ -182,33 +186,70 @@ def _op_inputs(op):
     return sorted({t for t in ins if isinstance(t, int)})
 
 
+SEGM_FUSED = [12, 15, 18, 21]  # first ops of the real model's inverted-residual blocks
+
+
+def _launch_steps(m, graph):
+    """(first op, last op + 1) of each launch the model makes: one op, or a
+    fused block's three."""
+    firsts = {f.first_op for f in m.fused_blocks()}
+    k, out = 0, []
+    while k < len(graph.g["ops"]):
+        step = 3 if k in firsts else 1
+        out.append((k, k + step))
+        k += step
+    return out
+
+
+def _stored(m, graph, name):
+    """Tensors a fused model keeps (every one but a fused block's intermediates)."""
+    internal = set()
+    for f in m.fused_blocks():
+        for k in (f.first_op, f.first_op + 1):
+            internal.add(graph.T[graph.g["ops"][k]["out"]]["name"])
+    return name not in internal
+
+
+def _check_launches(m, graph, ref, bar):
+    """Every launch fed the reference values of its inputs, its output against
+    the reference's; the worst error."""
+    T, ops = graph.T, graph.g["ops"]
+    worst = 0.0
+    for a, b in _launch_steps(m, graph):
+        for k in range(a, b):
+            for tid in _op_inputs(ops[k]):
+                if any(ops[j]["out"] == tid for j in range(a, k)):
+                    continue  # made inside the block
+                m.write_tensor(T[tid]["name"], ref[T[tid]["name"]])
+        m.infer_range(a, b)
+        name = T[ops[b - 1]["out"]]["name"]
+        e = G.rel_err(m.read_output(name), ref[name])
+        worst = max(worst, e)
+        assert e <= bar, (a, b, ops[b - 1]["kind"], name, e)
+    return worst
+
+
+@pytest.mark.parametrize("fuse", [True, False], ids=["fused", "unfused"])
 @pytest.mark.parametrize("n", [1, 2])
-def test_real_model_fp32_every_op_matches_oracle(segm, n):
-    """Each of the 44 ops, fed the oracle's values of its inputs, matches the
-    oracle's output to 1e-4 (the per-op bar); the whole graph run end to end
-    stays within 1e-3 of the oracle on every tensor (the per-op rounding
-    differences accumulate through up to 44 chained ops)."""
+def test_real_model_fp32_every_op_matches_oracle(segm, n, fuse):
+    """Each of the 44 ops (each fused block as one launch), fed the oracle's
+    values of its inputs, matches the oracle's output to 1e-4 (the per-op bar);
+    the whole graph run end to end stays within 1e-3 of the oracle on every
+    stored tensor (the per-op rounding differences accumulate through up to
+    44 chained ops)."""
     data, graph = segm
     x = rnd(50 + n, n, 160, 288, 3)
     want = graph.run({"input_1": x}, n=n, keep_all=True)
-    T = graph.T
-    m = sw.SwModel(data, n=n)
+    m = sw.SwModel(data, n=n, fuse=fuse)
     assert m.inputs == ["input_1"] and m.outputs == ["segment"]
-    worst_op = 0.0
-    for k, op in enumerate(graph.g["ops"]):
-        for tid in _op_inputs(op):
-            m.write_tensor(T[tid]["name"], want[T[tid]["name"]])
-        m.infer_range(k, k + 1)
-        name = T[op["out"]]["name"]
-        e = G.rel_err(m.read_output(name), want[name])
-        worst_op = max(worst_op, e)
-        assert e <= 1e-4, (k, op["kind"], name, e)
+    assert [f.first_op for f in m.fused_blocks()] == (SEGM_FUSED if fuse else [])
+    worst_op = _check_launches(m, graph, want, 1e-4)
     m.upload_input("input_1", x)
     m.infer()
-    worst = max(G.rel_err(m.read_output(nm), w) for nm, w in want.items())
+    worst = max(G.rel_err(m.read_output(nm), w) for nm, w in want.items() if _stored(m, graph, nm))
     e_out = G.rel_err(m.read_output(), want["segment"])
-    print(f"segm n={n}: worst per-op {worst_op:.2e}, end to end: output {e_out:.2e}, worst tensor {worst:.2e}",
-          flush=True)
+    print(f"segm n={n} fuse={fuse}: worst per-op {worst_op:.2e}, end to end: output {e_out:.2e}, "
+          f"worst tensor {worst:.2e}", flush=True)
     assert worst <= 1e-3 and e_out <= 1e-3
     # a second frame through the device upload path reuses every buffer
     x2 = rnd(60 + n, n, 160, 288, 3)
@@ -218,31 +259,28 @@ def test_real_model_fp32_every_op_matches_oracle(segm, n):
     m.close()
 
 
+@pytest.mark.parametrize("fuse", [True, False], ids=["fused", "unfused"])
 @pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
-def test_real_model_16bit_every_op_matches_stored_dtype_oracle(segm, dt):
-    """16-bit storage (weights converted at load): each op, fed the values of
-    the oracle run with the same storage rounding (weights, input and every op
-    output rounded to dt), within 2e-2 of that run's output. End to end, 44
-    ops of 16-bit rounding accumulate (bf16 keeps 8 mantissa bits): the
-    segmentation mask (argmax of the two logits) agrees with the fp32 run on
-    >= 99% of pixels, f16's logits stay within 1e-1; both distances are
-    printed."""
+def test_real_model_16bit_every_op_matches_stored_dtype_oracle(segm, dt, fuse):
+    """16-bit storage (weights converted at load): each op (each fused block
+    as one launch), fed the values of the oracle run with the same storage
+    rounding (weights, input and every op output rounded to dt), within 2e-2
+    of that run's output. End to end, 44 ops of 16-bit rounding accumulate
+    (bf16 keeps 8 mantissa bits): the segmentation mask (argmax of the two
+    logits) agrees with the fp32 run on >= 99% of pixels, f16's logits stay
+    within 1e-1; both distances are printed."""
     data, graph = segm
     n = 2
     x = rnd(70, n, 160, 288, 3)
-    m = sw.SwModel(data, n=n, dt=conv.DType(dt))
+    m = sw.SwModel(data, n=n, dt=conv.DType(dt), fuse=fuse)
     assert m.dt == dt
+    blocks = m.fused_blocks()
+    assert [f.first_op for f in blocks] == (SEGM_FUSED if fuse else [])
+    if fuse:
+        print(f"segm dt{dt} fused blocks: " + ", ".join(f"ops {f.first_op}-{f.first_op + 2} {f.plan}" for f in blocks),
+              flush=True)
     stored = so.SwGraph(data, round_dt=dt).run({"input_1": x}, n=n, keep_all=True)
-    T = graph.T
-    worst = 0.0
-    for k, op in enumerate(graph.g["ops"]):
-        for tid in _op_inputs(op):
-            m.write_tensor(T[tid]["name"], stored[T[tid]["name"]])
-        m.infer_range(k, k + 1)
-        name = T[op["out"]]["name"]
-        e = G.rel_err(m.read_output(name), stored[name])
-        worst = max(worst, e)
-        assert e <= 2e-2, (k, op["kind"], name, e)
+    worst = _check_launches(m, graph, stored, 2e-2)
     m.upload_input("input_1", x)
     m.infer()
     got = m.read_output("segment")
@@ -251,7 +289,7 @@ def test_real_model_16bit_every_op_matches_stored_dtype_oracle(segm, dt):
     e32 = G.rel_err(got, want32)
     # what the model delivers: the per-pixel class (argmax of the 2 logits)
     agree = float(np.mean(got.argmax(-1) == want32.argmax(-1)))
-    print(f"segm dt{dt}: worst per-op {worst:.2e}; end to end vs stored-dtype oracle {e_st:.2e}, "
+    print(f"segm dt{dt} fuse={fuse}: worst per-op {worst:.2e}; end to end vs stored-dtype oracle {e_st:.2e}, "
           f"vs fp32 {e32:.2e}, mask agreement {agree:.5f}", flush=True)
     assert agree >= 0.99
     if dt == F16:
@@ -259,14 +297,29 @@ def test_real_model_16bit_every_op_matches_stored_dtype_oracle(segm, dt):
 
 
 def test_tensor_storage_and_info(segm):
-    data, _ = segm
+    data, graph = segm
     m = sw.SwModel(data, n=3)
     t = m.tensor("input_1")
     assert (t.n, t.h, t.w, t.c, t.stride_c, t.dt) == (3, 160, 288, 3, 4, 0)
     assert t.bytes == 3 * 160 * 288 * 4 * 4 and t.data
     seg = m.tensor("segment")  # an alias of the last resize's output
     assert (seg.h, seg.w, seg.c, seg.stride_c) == (160, 288, 2, 4)
-    assert m.info.n_ops == 44 and m.info.n_launches == 44 and m.info.device_bytes > 0
+    # four fused blocks: 44 ops in 36 launches
+    assert m.info.n_ops == 44 and m.info.n_fused == 4 and m.info.n_launches == 36 and m.info.device_bytes > 0
+    # a fused block's intermediates are never stored; ranges keep blocks whole
+    inner = graph.T[graph.g["ops"][12]["out"]]["name"]
+    for call in (lambda: m.read_output(inner), lambda: m.tensor(inner),
+                 lambda: m.write_tensor(inner, np.zeros(3 * 10 * 18 * 96, np.float32))):
+        with pytest.raises(conv.AihError, match="stays inside the fused block of ops 12..14"):
+            call()
+    for a, b in [(13, 15), (12, 13), (0, 14)]:
+        with pytest.raises(conv.AihError, match="inside the fused block"):
+            m.infer_range(a, b)
+    unfused = sw.SwModel(data, n=3, fuse=False)
+    assert unfused.info.n_fused == 0 and unfused.info.n_launches == 44
+    assert unfused.tensor(inner).c == 96
+    assert unfused.info.device_bytes > m.info.device_bytes  # the intermediates are not allocated
+    unfused.close()
     with pytest.raises(conv.AihError, match="no input named"):
         m.upload_input("nope", np.zeros(3, np.float32))
     with pytest.raises(conv.AihError, match="expected"):
@@ -287,10 +340,38 @@ def test_synthetic_chain_through_the_native_loader(orc):
     n = 3
     x = rnd(80, n, 40, 72, 3)
     want = so.SwGraph(data).run({"input": x}, n=n)["head"]
+    for fuse, blocks in [(True, [1, 4]), (False, [])]:
+        m = sw.SwModel(data, n=n, fuse=fuse)
+        assert [f.first_op for f in m.fused_blocks()] == blocks
+        m.upload_input("input", x)
+        m.infer()
+        assert G.rel_err(m.read_output(), want) <= 1e-4
+        m.close()
+
+
+def test_fusion_needs_single_readers(orc):
+    """An expand output that a second op also reads keeps its block unfused
+    (the tensor must be stored); the next block still fuses. Results as the
+    oracle's either way."""
+    from ai_engine_amd.workloads import Layer, _chain, make_weights
+
+    layers = _chain([Layer("stem", 3, 32, k=3, s=2, act="relu"), Layer("e", 32, 128, act="relu"),
+                     Layer("d", 128, 128, k=3, groups=128, act="relu"), Layer("p", 128, 32, res="stem"),
+                     Layer("side", 128, 32, src="e", res="p"),
+                     Layer("e2", 32, 64, act="relu6"), Layer("d2", 64, 64, k=3, groups=64, act="relu6"),
+                     Layer("p2", 64, 32, res="side"), Layer("head", 32, 2)], 24, 40)
+    wts = make_weights(layers, seed=11)
+    data = sw.conv_graph_to_sw("side", layers, wts, 24, 40, 3)
+    n = 2
+    x = rnd(81, n, 24, 40, 3)
+    want = so.SwGraph(data).run({"input": x}, n=n)["head"]
     m = sw.SwModel(data, n=n)
+    assert [f.first_op for f in m.fused_blocks()] == [5]
+    assert m.tensor("e").c == 128  # stored: "side" reads it
     m.upload_input("input", x)
     m.infer()
     assert G.rel_err(m.read_output(), want) <= 1e-4
+    m.close()
 
 
 def test_model_load_rejects_what_it_cannot_run(segm):
