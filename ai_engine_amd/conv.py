@@ -71,6 +71,7 @@ class IrKernel(enum.IntEnum):
     AUTO = 0
     TILE = 1
     WAVE = 2
+    SPLIT = 3
 
 
 class Variant(enum.IntEnum):
@@ -120,7 +121,7 @@ class _IrDesc(C.Structure):
                 ("cexp", C.c_uint32), ("cout", C.c_uint32), ("s", C.c_uint32), ("pad", C.c_uint32 * 4),
                 ("act_expand", C.c_int32), ("act_dw", C.c_int32), ("act_project", C.c_int32),
                 ("residual", C.c_int32), ("dt", C.c_int32), ("tile_h", C.c_uint32), ("tile_w", C.c_uint32),
-                ("ec", C.c_uint32), ("weights", C.c_int32), ("kernel", C.c_int32)]
+                ("ec", C.c_uint32), ("weights", C.c_int32), ("kernel", C.c_int32), ("waves", C.c_uint32)]
 
 
 class IrPlan(C.Structure):
@@ -443,7 +444,8 @@ class IrBlockSpec:
     tile: tuple = (0, 0)  # forced output tile (h, w); (0, 0) = plan's choice
     ec: int = 0           # forced expanded channels per chunk; 0 = plan's choice
     weights: int = 0      # IrWeights: 0 = plan's choice, 1 = resident in LDS, 2 = streamed
-    kernel: int = 0       # IrKernel: 0 = plan's choice, 1 = tile kernel, 2 = wave kernel
+    kernel: int = 0       # IrKernel: 0 = plan's choice, 1 = tile, 2 = wave, 3 = split kernel
+    waves: int = 0        # wavefronts per workgroup (wave / split kernel); 0 = plan's choice
 
     def out_hw(self) -> tuple[int, int]:
         return ((self.ih + self.pad[0] + self.pad[2] - 3) // self.s + 1,
@@ -452,7 +454,8 @@ class IrBlockSpec:
     def desc(self) -> _IrDesc:
         return _IrDesc(self.n, self.ih, self.iw, self.cin, self.cexp, self.cout, self.s, (C.c_uint32 * 4)(*self.pad),
                        int(self.act_expand), int(self.act_dw), int(self.act_project), int(bool(self.residual)),
-                       int(self.dt), self.tile[0], self.tile[1], self.ec, int(self.weights), int(self.kernel))
+                       int(self.dt), self.tile[0], self.tile[1], self.ec, int(self.weights), int(self.kernel),
+                       self.waves)
 
     def plan(self) -> IrPlan:
         p = IrPlan()

@@ -517,21 +517,23 @@ int plan_ir(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, aih::IrPlan *p
   return AIH_OK;
 }
 
-// The wave kernel's plan, when the descriptor selects it (WAVE) or leaves
-// the choice (AUTO) and it applies; false: the tile kernel runs (AUTO) or
-// the call fails (WAVE, with the reason).
+// The wave or split kernel's plan, when the descriptor selects one (WAVE,
+// SPLIT) or leaves the choice (AUTO) and one applies; false: the tile kernel
+// runs (AUTO) or the call fails (WAVE / SPLIT, with the reason).
 int plan_ir_wave(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, aih::IrWavePlan *p, bool *use) {
   *use = false;
   if (d->kernel == AIH_IR_KERNEL_TILE) return AIH_OK;
-  if (d->kernel != AIH_IR_KERNEL_AUTO && d->kernel != AIH_IR_KERNEL_WAVE) return fail("ir_block: unknown kernel");
+  if (d->kernel != AIH_IR_KERNEL_AUTO && d->kernel != AIH_IR_KERNEL_WAVE && d->kernel != AIH_IR_KERNEL_SPLIT)
+    return fail("ir_block: unknown kernel");
+  const bool forced = d->kernel != AIH_IR_KERNEL_AUTO;
   if (d->ec && d->ec != 32) {
-    if (d->kernel == AIH_IR_KERNEL_WAVE) return fail("ir_block: the wave kernel walks E in chunks of 32");
+    if (forced) return fail("ir_block: the wave and split kernels walk E in chunks of 32");
     return AIH_OK;
   }
   const char *why = aih::irw_plan(d->n, d->ih, d->iw, oh, ow, d->cin, d->cexp, d->cout, d->s, d->dt,
                                   ir_clamp_acts(d), d->act_expand == AIH_ACT_RELU && d->act_dw == AIH_ACT_RELU,
-                                  d->tile_h, d->tile_w, d->weights, p);
-  if (why) return d->kernel == AIH_IR_KERNEL_WAVE ? fail(std::string("ir_block: ") + why) : AIH_OK;
+                                  d->tile_h, d->tile_w, d->weights, d->kernel, d->waves, p);
+  if (why) return forced || d->waves ? fail(std::string("ir_block: ") + why) : AIH_OK;
   *use = true;
   return AIH_OK;
 }
@@ -855,9 +857,10 @@ int aih_ir_block_plan(const aih_ir_block_desc *d, aih_ir_plan *out) {
     if (plan_ir_wave(d, oh, ow, &wp, &wave)) return AIH_ERR;
     if (wave) {
       *out = aih_ir_plan{wp.TH, wp.TW, 32, d->cexp / 32, wp.resident, wp.ntiles, wp.lds, wp.occ, wp.grid,
-                         AIH_IR_KERNEL_WAVE, wp.waves};
+                         wp.split ? AIH_IR_KERNEL_SPLIT : AIH_IR_KERNEL_WAVE, wp.waves};
       return AIH_OK;
     }
+    if (d->waves) return fail("ir_block: the tile kernel's workgroups have 4 wavefronts (waves must be 0)");
     aih::IrPlan p;
     if (plan_ir(d, oh, ow, &p)) return AIH_ERR;
     *out = aih_ir_plan{p.TH, p.TW, p.EC, d->cexp / p.EC, p.resident, p.ntiles, p.lds, p.occ, p.grid,
@@ -923,15 +926,17 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
       a.lds_w = wp.lds_w;
       a.lds_bp = wp.lds_bp;
       a.lds_xe = wp.lds_xe;
+      a.lds_red = wp.lds_red;
+      a.lds_x = wp.lds_x;
       a.fd_hw = aih::make_fastdiv(wp.HW);
       a.fd_tw = aih::make_fastdiv(wp.TW);
       a.fd_tx = aih::make_fastdiv(wp.tiles_x);
       a.fd_pi = aih::make_fastdiv(wp.tiles_x * wp.tiles_y);
-      const hipError_t e =
-          aih::launch_ir_wave(a, d->dt, wp.NPI, wp.waves, wp.lds, wp.grid, static_cast<hipStream_t>(stream));
+      const hipError_t e = aih::launch_ir_wave(a, d->dt, wp, static_cast<hipStream_t>(stream));
       if (e != hipSuccess) return fail(std::string("ir_block wave launch: ") + hipGetErrorString(e));
       return AIH_OK;
     }
+    if (d->waves) return fail("ir_block: the tile kernel's workgroups have 4 wavefronts (waves must be 0)");
     aih::IrPlan p;
     if (plan_ir(d, oh, ow, &p)) return AIH_ERR;
     aih::IrArgs a;

@@ -84,6 +84,8 @@ struct IrWaveArgs {
   int32_t act_e, act_d, act_p, has_res;
   uint32_t nxcd;            // XCDs of the device (workgroup remap)
   uint32_t lds_w, lds_bp, lds_xe;  // LDS byte offsets: weight slots, fp32 projection bias, expanded regions
+  uint32_t lds_red;                // split kernel: projection partial sums (over the regions below)
+  uint32_t lds_x;                  // split kernel: the tile's input halo
   FastDiv fd_hw, fd_tw, fd_tx, fd_pi;
 };
 
@@ -96,27 +98,38 @@ __host__ __device__ inline uint32_t irw_slot_bytes(uint32_t C, uint32_t COP) { r
 // up to whole 32-channel MFMA blocks.
 __host__ __device__ inline uint32_t ir_cop(uint32_t CO) { return (CO + 31) / 32 * 32; }
 
-// Tile, weight placement and LDS layout of one launch of the wave kernel.
+// Tile, weight placement and LDS layout of one launch of the wave kernel
+// (split = 0: a tile per wavefront) or of the split kernel (split = 1: a
+// tile per workgroup, its chunks divided among the wavefronts).
 struct IrWavePlan {
+  uint32_t split;
   uint32_t TH, TW, HH, HW, NPI, resident;
-  uint32_t waves;                       // wavefronts per workgroup (2, 4 or 8)
+  uint32_t waves;                       // wavefronts per workgroup (wave: 2, 4 or 8; split: 1, 2, 4 or 8)
   uint32_t tiles_y, tiles_x, ntiles;
-  uint32_t lds_w, lds_bp, lds_xe, lds;  // LDS byte offsets and total
+  uint32_t lds_w, lds_bp, lds_xe, lds_red, lds_x, lds;  // LDS byte offsets and total
   uint32_t occ, grid;                   // workgroups per CU, launched workgroups
 };
 
-// Chooses the wave kernel's tile (<= 32 output pixels, halo within NPI
-// blocks of an instantiation) and weight placement (resident when all
-// chunks fit in LDS next to the eight wavefronts' expanded regions).
-// Returns nullptr, or the reason the block cannot run on this kernel
-// (dtype, activations, widths without an instantiation, LDS).
+// Split kernel LDS: the tile's halo (NPI x 32 rows of C channels + 16
+// bytes), per wavefront its expanded chunk and its two-slot ring of
+// depthwise taps and biases; partial sums: NOB blocks of 32 x 32 fp32 per
+// wavefront, over the rest once it is done with.
+constexpr uint32_t IRS_RING = 2 * IRW_SMB;
+constexpr uint32_t IRS_RED_BLOCK = 32 * 32 * 4;
+
+// Chooses between the wave kernel and the split kernel (kernel: enum
+// aih_ir_kernel, AUTO for the cheaper estimate), the tile (<= 32 output
+// pixels, halo within NPI blocks of an instantiation), the wave kernel's
+// weight placement (resident when all chunks fit in LDS next to the
+// wavefronts' expanded regions) and the wavefronts per workgroup (waves: 0 =
+// the plan's choice). Returns nullptr, or the reason the block cannot run on
+// these kernels (dtype, activations, widths without an instantiation, LDS).
 // rl: the expand and depthwise activations are both ReLU (selects the
 // instantiation whose register use bounds the occupancy).
 const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
                      uint32_t CO, uint32_t S, int dt, bool cl, bool rl, uint32_t tile_h, uint32_t tile_w,
-                     int32_t weights, IrWavePlan *p);
+                     int32_t weights, int32_t kernel, uint32_t waves, IrWavePlan *p);
 
-hipError_t launch_ir_wave(const IrWaveArgs &a, int dt, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
-                          hipStream_t st);
+hipError_t launch_ir_wave(const IrWaveArgs &a, int dt, const IrWavePlan &p, hipStream_t st);
 
 }  // namespace aih

@@ -29,7 +29,8 @@ fuses 16-bit models only.
 The choice per block is recorded (choice_map()) and can be given back
 (choices={block: label}), so a later load runs exactly the same kernels; a
 label is "unfused", "fused THxTW" (the tile kernel, streamed weights),
-"fused THxTW resident", or "wave THxTW[ resident]" (the wave kernel) --
+"fused THxTW resident", "wave THxTW[ resident]" (the wave kernel) or
+"split THxTW wN" (the split kernel, N wavefronts per tile) --
 fused_candidates() lists the labels a block can take.
 """
 from __future__ import annotations
@@ -98,6 +99,7 @@ class Model:
     TUNE_TILES = [(2, 8), (4, 4), (4, 8), (8, 4), (4, 16), (8, 8), (16, 4), (2, 32), (4, 32), (8, 16), (16, 8),
                   (8, 32), (16, 16)]
     WAVE_TILES = [(4, 8), (8, 4), (5, 6), (6, 5), (2, 16), (16, 2), (3, 10)]
+    SPLIT_WAVES = [2, 4, 8]
 
     def __init__(self, layers: list[Layer], weights: Weights, n: int, ih: int, iw: int, cin: int,
                  dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0",
@@ -179,40 +181,51 @@ class Model:
         """The fused launches the tuner times for a block: on the tile kernel
         the planner's tile and every TUNE_TILES entry, on the wave kernel the
         planner's tile and every WAVE_TILES entry, each with resident and
-        streamed weights (the ones that fit), as (label, spec with kernel,
-        tile and placement forced); duplicates dropped."""
+        streamed weights (the ones that fit), on the split kernel the planner's
+        tile and every WAVE_TILES entry with each of SPLIT_WAVES wavefronts,
+        as (label, spec with kernel, tile, placement and wavefronts forced);
+        duplicates dropped."""
         out, seen = [], set()
-        for kernel, tiles in ((conv.IrKernel.TILE, cls.TUNE_TILES), (conv.IrKernel.WAVE, cls.WAVE_TILES)):
-            for tile in [(0, 0)] + tiles:
-                for w in (conv.IrWeights.RESIDENT, conv.IrWeights.STREAMED):
-                    sp = dataclasses.replace(spec, tile=tile, weights=w, kernel=kernel)
-                    if not sp.fusable():
-                        continue
-                    pl = sp.plan()
-                    key = (int(kernel), pl.th, pl.tw, pl.resident)
-                    if key in seen:
-                        continue
-                    seen.add(key)
-                    out.append((cls.label_of(kernel, pl.th, pl.tw, pl.resident),
-                                dataclasses.replace(spec, tile=(pl.th, pl.tw), weights=w, kernel=kernel)))
+        K, Wt = conv.IrKernel, conv.IrWeights
+        opts = [(K.TILE, t, w, 0) for t in [(0, 0)] + cls.TUNE_TILES for w in (Wt.RESIDENT, Wt.STREAMED)]
+        opts += [(K.WAVE, t, w, 0) for t in [(0, 0)] + cls.WAVE_TILES for w in (Wt.RESIDENT, Wt.STREAMED)]
+        opts += [(K.SPLIT, t, Wt.AUTO, n) for t in [(0, 0)] + cls.WAVE_TILES for n in cls.SPLIT_WAVES]
+        for kernel, tile, w, waves in opts:
+            sp = dataclasses.replace(spec, tile=tile, weights=w, kernel=kernel, waves=waves)
+            if not sp.fusable():
+                continue
+            pl = sp.plan()
+            key = (int(kernel), pl.th, pl.tw, pl.resident, pl.waves if kernel == K.SPLIT else 0)
+            if key in seen:
+                continue
+            seen.add(key)
+            out.append((cls.label_of(kernel, pl.th, pl.tw, pl.resident, pl.waves),
+                        dataclasses.replace(spec, tile=(pl.th, pl.tw), weights=w, kernel=kernel, waves=waves)))
         return out
 
     @staticmethod
-    def label_of(kernel, th: int, tw: int, resident: bool) -> str:
-        name = "wave" if conv.IrKernel(kernel) == conv.IrKernel.WAVE else "fused"
+    def label_of(kernel, th: int, tw: int, resident: bool, waves: int = 0) -> str:
+        k = conv.IrKernel(kernel)
+        if k == conv.IrKernel.SPLIT:
+            return f"split {th}x{tw} w{waves}"
+        name = "wave" if k == conv.IrKernel.WAVE else "fused"
         return f"{name} {th}x{tw}{' resident' if resident else ''}"
 
     @staticmethod
     def parse_label(label: str):
-        """"unfused" -> None; "fused|wave THxTW[ resident]" -> (IrKernel, (th, tw), IrWeights)."""
+        """"unfused" -> None; "fused|wave THxTW[ resident]" or "split THxTW wN"
+        -> (IrKernel, (th, tw), IrWeights, wavefronts or 0)."""
         if label == "unfused":
             return None
+        m = re.fullmatch(r"split (\d+)x(\d+) w(\d+)", label)
+        if m:
+            return conv.IrKernel.SPLIT, (int(m.group(1)), int(m.group(2))), conv.IrWeights.AUTO, int(m.group(3))
         m = re.fullmatch(r"(fused|wave) (\d+)x(\d+)( resident)?", label)
         if not m:
             raise ValueError(f"unknown block choice {label!r}")
         k = conv.IrKernel.WAVE if m.group(1) == "wave" else conv.IrKernel.TILE
         w = conv.IrWeights.RESIDENT if m.group(4) else conv.IrWeights.STREAMED
-        return k, (int(m.group(2)), int(m.group(3))), w
+        return k, (int(m.group(2)), int(m.group(3))), w, 0
 
     def choice_map(self) -> dict[str, str]:
         """Block -> the label of the launch it runs (feed back as choices=)."""
@@ -230,12 +243,12 @@ class Model:
         self.choices[self._block_name(p)] = (label, float("nan"))
         if forced is None:
             return [self._conv_op(Lr, packed, L) for Lr in (e, d, p)]
-        kernel, tile, w = forced
-        sp = dataclasses.replace(spec, tile=tile, weights=w, kernel=kernel)
+        kernel, tile, w, waves = forced
+        sp = dataclasses.replace(spec, tile=tile, weights=w, kernel=kernel, waves=waves)
         pl = sp.plan()
-        if (pl.kernel, pl.th, pl.tw, bool(pl.resident)) != (int(kernel), tile[0], tile[1], w == conv.IrWeights.RESIDENT):
+        if self.label_of(pl.kernel, pl.th, pl.tw, pl.resident, pl.waves) != label:
             raise conv.AihError(f"{self._block_name(p)}: {label!r} planned as "
-                                f"{self.label_of(pl.kernel, pl.th, pl.tw, pl.resident)!r}")
+                                f"{self.label_of(pl.kernel, pl.th, pl.tw, pl.resident, pl.waves)!r}")
         return [self._fused_op((e, d, p, sp), packed, L)]
 
     def _tuned_block(self, blk, packed, L, allow_unfused: bool) -> list:

@@ -261,15 +261,16 @@ def kernel_key(conv, op, n, dt, dtname) -> str:
     trace names it for the fused block; descriptive for the conv kernels)."""
     if op.kind == "ir_block":
         p = op.spec.plan()
-        if p.kernel == conv.IrKernel.WAVE:
+        if p.kernel in (conv.IrKernel.WAVE, conv.IrKernel.SPLIT):
             s = op.spec.s
             npi = 2 if ((p.th - 1) * s + 3) * ((p.tw - 1) * s + 3) <= 64 else 5
-            return f"ir_wave_kernel<{int(dt)}, {op.spec.cin // 16}, {npi}, {op.spec.cout // 32}>"
+            name = "ir_wave_kernel" if p.kernel == conv.IrKernel.WAVE else "ir_split_kernel"
+            return f"{name}<{int(dt)}, {op.spec.cin // 16}, {npi}, {-(-op.spec.cout // 32)}>"
         npw = -(-(-(-p.th * p.tw // 32)) // 4)
         A = conv.Activation
         clamp = all(int(x) in (A.NONE, A.RELU, A.RELU6, A.CLAMP01)
                     for x in (op.spec.act_expand, op.spec.act_dw, op.spec.act_project))
-        return f"ir_block_kernel<{int(dt)}, {op.spec.cout // 32}, {npw}, {'true' if clamp else 'false'}>"
+        return f"ir_block_kernel<{int(dt)}, {-(-op.spec.cout // 32)}, {npw}, {'true' if clamp else 'false'}>"
     Lr = op.layers[0]
     if Lr.depthwise:
         return f"conv_dw_strip_kernel<{dtname}>"

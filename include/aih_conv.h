@@ -181,15 +181,20 @@ typedef struct {
   uint32_t ec;             /* expanded channels per chunk; 0 = chosen by the plan */
   int32_t weights;         /* enum aih_ir_weights: where the expand / project weights live */
   int32_t kernel;          /* enum aih_ir_kernel */
+  uint32_t waves;          /* wavefronts per workgroup of the wave / split kernel; 0 = chosen by the plan */
 } aih_ir_block_desc;
 
-/* Which fused kernel runs a block: chosen by the plan (the wave kernel where
- * it applies, else the tile kernel), the tile kernel (a workgroup shares one
- * output tile of up to 256 pixels and its halo through LDS, any clamp or
- * other activation, f32 / f16 / bf16), or the wave kernel (every wavefront
- * owns a tile of up to 32 pixels with a private expanded chunk in LDS; f16 /
- * bf16 storage, clamp-type activations, the instantiated widths). */
-enum aih_ir_kernel { AIH_IR_KERNEL_AUTO = 0, AIH_IR_KERNEL_TILE = 1, AIH_IR_KERNEL_WAVE = 2 };
+/* Which fused kernel runs a block: chosen by the plan (the cheaper estimate
+ * of the wave and split kernels where they apply, else the tile kernel), the
+ * tile kernel (a workgroup shares one output tile of up to 256 pixels and its
+ * halo through LDS, any clamp or other activation, f32 / f16 / bf16), the
+ * wave kernel (every wavefront owns a tile of up to 32 pixels with a private
+ * expanded chunk in LDS, weights shared through LDS; f16 / bf16 storage,
+ * clamp-type activations, the instantiated widths), or the split kernel
+ * (as the wave kernel, but the 1..8 wavefronts of a workgroup share one tile
+ * and divide its expanded channels, weights read from memory, the partial
+ * projections added in a fixed order: for launches with few tiles). */
+enum aih_ir_kernel { AIH_IR_KERNEL_AUTO = 0, AIH_IR_KERNEL_TILE = 1, AIH_IR_KERNEL_WAVE = 2, AIH_IR_KERNEL_SPLIT = 3 };
 
 /* Weight placement of a fused block: chosen by the plan (resident when they
  * fit), all of them resident in LDS for every tile, or streamed chunk by
@@ -202,7 +207,7 @@ enum aih_ir_weights { AIH_IR_WEIGHTS_AUTO = 0, AIH_IR_WEIGHTS_RESIDENT = 1, AIH_
 typedef struct {
   uint32_t th, tw, ec, chunks, resident;
   uint32_t tiles, lds_bytes, occupancy, grid;
-  uint32_t kernel; /* enum aih_ir_kernel: AIH_IR_KERNEL_TILE or AIH_IR_KERNEL_WAVE */
+  uint32_t kernel; /* enum aih_ir_kernel: AIH_IR_KERNEL_TILE, _WAVE or _SPLIT */
   uint32_t waves;  /* wavefronts per workgroup */
 } aih_ir_plan;
 

@@ -116,3 +116,29 @@ def test_ir_block_48_channel_projection_both_kernels(kernel, dt):
         e = G.rel_err(c.run(spec), c.want_stored)
         print(f"{kernel} dt{dt} {w.name}: {p} vs stored-dtype chain {e:.3e}", flush=True)
         assert e <= BAR_STORED[dt], (w, e)
+
+
+@pytest.mark.parametrize("case", CASES, ids=_id)
+@pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
+def test_ir_block_split_kernel_every_wave_count(case, dt):
+    """The split kernel (a tile per workgroup, its chunks divided among 1, 2,
+    4 or 8 wavefronts, partial projections added in wavefront order) on every
+    case it takes, against the stored-dtype chain; two runs of one launch
+    give the same bits (the order of the partial sums is fixed)."""
+    from ai_engine_amd import conv
+    c = make_case(case, dt, 7800 + 10 * CASES.index(case))
+    ran = 0
+    for waves in (1, 2, 4, 8):
+        spec = c.spec(kernel=conv.IrKernel.SPLIT, waves=waves)
+        if not spec.fusable():
+            continue
+        p = spec.plan()
+        assert p.kernel == conv.IrKernel.SPLIT and p.waves == waves and p.grid == p.tiles, p
+        got = c.run(spec)
+        e = G.rel_err(got, c.want_stored)
+        print(f"case {_id(case)} dt{dt} split w{waves}: {p} vs stored-dtype chain {e:.3e}", flush=True)
+        assert e <= BAR_STORED[dt], (waves, e)
+        assert (c.run(spec) == got).all()
+        ran += 1
+    if not ran:
+        pytest.skip("not a split-kernel shape (activation, width or instantiation)")
