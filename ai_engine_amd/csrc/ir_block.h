@@ -103,6 +103,7 @@ __host__ __device__ inline uint32_t ir_cop(uint32_t CO) { return (CO + 31) / 32 
 // tile per workgroup, its chunks divided among the wavefronts).
 struct IrWavePlan {
   uint32_t split;
+  uint32_t deep;                        // split kernel: operands prefetched a whole chunk ahead
   uint32_t TH, TW, HH, HW, NPI, resident;
   uint32_t waves;                       // wavefronts per workgroup (wave: 2, 4 or 8; split: 1, 2, 4 or 8)
   uint32_t tiles_y, tiles_x, ntiles;

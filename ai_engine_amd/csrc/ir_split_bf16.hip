@@ -3,13 +3,13 @@
 
 namespace aih {
 
-hipError_t launch_ir_split_bf16(const IrWaveArgs &a, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
-                              hipStream_t st) {
-  return irs_launch_dt<DT_BF16>(a, npi, waves, lds, grid, st);
+hipError_t launch_ir_split_bf16(const IrWaveArgs &a, uint32_t npi, bool deep, uint32_t waves, uint32_t lds,
+                              uint32_t grid, hipStream_t st) {
+  return irs_launch_dt<DT_BF16>(a, npi, deep, waves, lds, grid, st);
 }
 
-int ir_split_occ_bf16(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves, uint32_t lds) {
-  return irs_occ_dt<DT_BF16>(ke, npi, nob, rl, waves, lds);
+int ir_split_occ_bf16(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, bool deep, uint32_t waves, uint32_t lds) {
+  return irs_occ_dt<DT_BF16>(ke, npi, nob, rl, deep, waves, lds);
 }
 
 }  // namespace aih

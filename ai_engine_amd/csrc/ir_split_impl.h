@@ -38,7 +38,7 @@
 
 namespace aih {
 
-template <int DT, int KE, int NPI, int NOB, bool RL>
+template <int DT, int KE, int NPI, int NOB, bool RL, bool DP>
 __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
   static_assert(DT == DT_F16 || DT == DT_BF16, "16-bit storage");
   extern __shared__ __align__(16) char lds[];
@@ -49,11 +49,12 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
   // both K steps' projection operands. Depthwise taps are read in batches of
   // three; the projection operands go out before the expand where the shape
   // stays within 128 VGPRs (four wavefronts per SIMD), else before each K
-  // step's depthwise. No packed ReLU: it keeps the packed results live longer
-  // and costs a wavefront per SIMD on the wider shapes.
+  // step's depthwise. The packed ReLU on the expand's epilogue only: on the
+  // depthwise result it keeps the packed values live longer and costs a
+  // wavefront per SIMD on the wider shapes.
   constexpr int HELD = 4 * KE + 16 * NOB + 8 * NOB;
   constexpr int TB = 3;
-  constexpr bool RLP = false;
+  constexpr bool RLE = RL, RLD = false;
   constexpr bool WP_EARLY = HELD <= 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63, l32 = lane & 31, lh = lane >> 5;
@@ -121,28 +122,30 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
   const size_t out_pix = ((size_t)img * a.OH + ty0 + oy) * a.OW + tx0 + ox;
 
   // ---- weights of chunk c ----
+  // Every weight offset is a lane part (held) plus a wavefront-uniform part
+  // that goes into the buffer load's scalar offset (no per-chunk address
+  // arithmetic on the vector unit).
   // expand A operands: channel 32c + l32, K groups 4k + 2 lh and the next
   // (packed element (k, e) at (k/4 * E + e) * 4 + k%4)
+  const uint32_t vo_aw = ((uint32_t)lh * 2 * a.E + l32) * GB;
   auto load_aw = [&](uint32_t c, u32x4 (&aw)[KE]) {
-    const uint32_t base = ((uint32_t)lh * 2 * a.E + EC * c + l32) * GB;
 #pragma unroll
     for (int k = 0; k < KE; ++k) {
-      const uint32_t off = base + (uint32_t)k * 4 * a.E * GB;
-      const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_we, off, 0, 0));
-      const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_we, off + a.E * GB, 0, 0));
+      const uint32_t so = (EC * c + (uint32_t)k * 4 * a.E) * GB;
+      const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_we, vo_aw, so, 0));
+      const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_we, vo_aw, so + a.E * GB, 0));
       aw[k] = u32x4{lo.x, lo.y, hi.x, hi.y};
     }
   };
   // projection A operand of block o, K step ks: output channel 32o + l32, K
   // rows 32c + 16ks + 8lh .. + 8 (groups 8c + 4ks + 2lh and the next); zeros
-  // for channels CO..COP
+  // for channels CO..COP (a lane offset past every buffer)
   auto load_wp = [&](uint32_t c, int ks, int o) -> u32x4 {
     const uint32_t ch = (uint32_t)o * 32 + l32;
-    const uint32_t g = 8 * c + 4 * (uint32_t)ks + 2 * (uint32_t)lh;
-    const uint32_t off = ch < a.CO ? (g * a.CO + ch) * GB : IR_OOB;
-    const uint32_t off2 = ch < a.CO ? off + a.CO * GB : IR_OOB;
-    const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_wp, off, 0, 0));
-    const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_wp, off2, 0, 0));
+    const uint32_t vo = ch < a.CO ? (2 * (uint32_t)lh * a.CO + ch) * GB : IR_OOB;
+    const uint32_t so = (8 * c + 4 * (uint32_t)ks) * a.CO * GB;
+    const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_wp, vo, so, 0));
+    const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_wp, vo, so + a.CO * GB, 0));
     return u32x4{lo.x, lo.y, hi.x, hi.y};
   };
   // depthwise taps, depthwise bias, expand bias of chunk c -> ring slot s
@@ -152,101 +155,198 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
     char *sm = SmL + s * IRW_SMB;
     constexpr uint32_t TR = EC * ES / 16;  // 16-byte items per tap run
     irw_dma<16>(sm, 9 * TR, rs_wd, 0, lane, 64,
-                [&](uint32_t g) -> uint32_t { return ((g / TR) * a.E + EC * c) * ES + (g % TR) * 16; });
-    irw_dma<4>(sm + 9 * EC * ES, EC * ES / 4, rs_bd, 0, lane, 64,
-               [&](uint32_t g) -> uint32_t { return EC * c * ES + g * 4; });
-    irw_dma<4>(sm + 10 * EC * ES, EC * ES / 4, rs_be, 0, lane, 64,
-               [&](uint32_t g) -> uint32_t { return EC * c * ES + g * 4; });
+                [&](uint32_t g) -> uint32_t { return (g / TR) * a.E * ES + (g % TR) * 16; }, EC * c * ES);
+    irw_dma<4>(sm + 9 * EC * ES, EC * ES / 4, rs_bd, 0, lane, 64, [&](uint32_t g) -> uint32_t { return g * 4; },
+               EC * c * ES);
+    irw_dma<4>(sm + 10 * EC * ES, EC * ES / 4, rs_be, 0, lane, 64, [&](uint32_t g) -> uint32_t { return g * 4; },
+               EC * c * ES);
   };
 
   f32x16 acc[NOB];
 #pragma unroll
   for (int o = 0; o < NOB; ++o) acc[o] = f32x16{};
 
-  u32x4 aw[KE];
-  if (c_begin < c_end) {
-    load_aw(c_begin, aw);
-    load_small(c_begin, 0);
-  }
-  // the halo (every wavefront's share of the copy) and the projection bias
-  ir_dma_wait();
-  __syncthreads();
-  for (uint32_t c = c_begin; c < c_end; ++c) {
-    const uint32_t s = (c - c_begin) & 1;
-    const char *sm = SmL + s * IRW_SMB;
-    // chunk c's small tensors have landed (and every earlier load)
+  auto load_wp_all = [&](uint32_t c, u32x4 (&wp)[NKS][NOB]) {
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+      for (int o = 0; o < NOB; ++o) wp[ks][o] = load_wp(c, ks, o);
+  };
+  // expand of the chunk whose small tensors are at sm, over the halo tile ->
+  // XeL, each K step's B operands read from LDS one step ahead. With the deep
+  // prefetch (registers to spare) the halo blocks go two at a time with their
+  // MFMA chains interleaved (two accumulators), so an MFMA does not wait for
+  // the one before it.
+  constexpr int G = DP ? 2 : 1;
+  auto expand = [&](const char *sm, const u32x4 (&aw)[KE]) {
+    const uint32_t bw = lh == 0 ? (uint32_t)*reinterpret_cast<const uint16_t *>(sm + 10 * EC * ES + l32 * 2) : 0u;
+#pragma unroll
+    for (int b0 = 0; b0 < NPI; b0 += G) {
+      const int ng = NPI - b0 < G ? NPI - b0 : G;
+      f32x16 e[G];
+      u32x4 xb[G][2];
+      const char *xr[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        if (g >= ng) continue;
+        xr[g] = XL + ((b0 + g) * 32 + l32) * RPX + lh * 16;
+        xb[g][0] = *reinterpret_cast<const u32x4 *>(xr[g]);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        if (g >= ng) continue;
+        const u32x4 bx = {(lh == 0 && inside[b0 + g]) ? ONE : 0u, 0u, 0u, 0u};
+        e[g] = ir_mma<DT>(u32x4{bw, 0u, 0u, 0u}, bx, f32x16{});
+      }
+#pragma unroll
+      for (int k = 0; k < KE; ++k) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          if (g < ng && k + 1 < KE) xb[g][(k + 1) & 1] = *reinterpret_cast<const u32x4 *>(xr[g] + (k + 1) * 32);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          if (g < ng) e[g] = ir_mma<DT>(aw[k], xb[g][k & 1], e[g]);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        if (g >= ng) continue;
+        char *row = XeL + ((b0 + g) * 32 + l32) * IRW_RPE;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<u32x2 *>(row + (8 * q + 4 * lh) * ES) = irw_act_pack4<DT, RLE>(
+              act_e, f32x4{e[g][4 * q], e[g][4 * q + 1], e[g][4 * q + 2], e[g][4 * q + 3]});
+      }
+    }
+  };
+
+  if constexpr (!DP) {
+    u32x4 aw[KE];
+    if (c_begin < c_end) {
+      load_aw(c_begin, aw);
+      load_small(c_begin, 0);
+    }
+    // the halo (every wavefront's share of the copy) and the projection bias
     ir_dma_wait();
-    irw_wave_order();
-    // the projection operands (both K steps' in flight during the expand)
-    u32x4 wpv[NKS][NOB];
-    if constexpr (WP_EARLY) {
+    __syncthreads();
+    for (uint32_t c = c_begin; c < c_end; ++c) {
+      const uint32_t s = (c - c_begin) & 1;
+      const char *sm = SmL + s * IRW_SMB;
+      // chunk c's small tensors have landed (and every earlier load)
+      ir_dma_wait();
+      irw_wave_order();
+      // the projection operands (both K steps' in flight during the expand)
+      u32x4 wpv[NKS][NOB];
+      if constexpr (WP_EARLY) load_wp_all(c, wpv);
+
+      expand(sm, aw);
+      irw_wave_order();
+      // the next chunk's operands go out now: its expand weights into the
+      // registers this expand has finished with, its small tensors into the
+      // other ring slot (last read by the previous chunk, whose reads are done)
+      if (c + 1 < c_end) {
+        load_aw(c + 1, aw);
+        load_small(c + 1, s ^ 1u);
+      }
+
+      // depthwise of the lane's K slice straight into the projection's B operand
+      const char *wdp = sm + lh * 16;
+      const char *bdp = sm + 9 * EC * ES + lh * 16;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        if constexpr (!WP_EARLY) {
+#pragma unroll
+          for (int o = 0; o < NOB; ++o) wpv[ks][o] = load_wp(c, ks, o);
+        }
+        float d[HK];
+        ir_unpack<DT, HK>(*reinterpret_cast<const u32x4 *>(bdp + ks * 32), d);
+#pragma unroll
+        for (int t0 = 0; t0 < 9; t0 += TB) {
+          u32x4 wv[TB], xv[TB];
+#pragma unroll
+          for (int t = 0; t < TB; ++t) wv[t] = *reinterpret_cast<const u32x4 *>(wdp + (t0 + t) * (EC * ES) + ks * 32);
+#pragma unroll
+          for (int t = 0; t < TB; ++t)
+            xv[t] = *reinterpret_cast<const u32x4 *>(XeL + rowo[(t0 + t) / 3] + ((t0 + t) % 3) * IRW_RPE + ks * 32);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
+        }
+        u32x4 bop;
+        if constexpr (RLD) {
+          bop = ir_pack<DT, HK>(d);
+          bop = u32x4{irw_relu2(bop.x), irw_relu2(bop.y), irw_relu2(bop.z), irw_relu2(bop.w)};
+        } else {
+          ir_act<true, HK>(act_d, d);
+          bop = ir_pack<DT, HK>(d);
+        }
+#pragma unroll
+        for (int o = 0; o < NOB; ++o) acc[o] = ir_mma<DT>(wpv[ks][o], bop, acc[o]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // the next chunk's expand overwrites XeL after these reads
+      irw_wave_order();
+    }
+  } else {
+    // Deep prefetch, for launches with few wavefronts per SIMD (the
+    // registers are there; other wavefronts do not hide the latency): two
+    // sets of expand operands (A for the even chunks of this wavefront's run,
+    // B for the odd ones) and two ring slots, so a chunk's expand weights and
+    // small tensors go out at the start of the chunk before it; its
+    // projection operands go out at its own start, ahead of its expand.
+    u32x4 awA[KE], awB[KE];
+    if (c_begin < c_end) {
+      load_aw(c_begin, awA);
+      load_small(c_begin, 0);
+    }
+    ir_dma_wait();
+    __syncthreads();
+    // chunk c from ring slot s with expand operands `cur`; the next chunk's
+    // into `nxt` and the other slot
+    auto step = [&](uint32_t c, uint32_t s, u32x4 (&cur)[KE], u32x4 (&nxt)[KE]) {
+      const char *sm = SmL + s * IRW_SMB;
+      ir_dma_wait();
+      irw_wave_order();
+      u32x4 wpv[NKS][NOB];
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
         for (int o = 0; o < NOB; ++o) wpv[ks][o] = load_wp(c, ks, o);
-    }
-
-    // expand over the halo tile -> XeL
-    const uint32_t bw = lh == 0 ? (uint32_t)*reinterpret_cast<const uint16_t *>(sm + 10 * EC * ES + l32 * 2) : 0u;
-#pragma unroll
-    for (int b = 0; b < NPI; ++b) {
-      const u32x4 bx = {(lh == 0 && inside[b]) ? ONE : 0u, 0u, 0u, 0u};
-      f32x16 e = ir_mma<DT>(u32x4{bw, 0u, 0u, 0u}, bx, f32x16{});
-      const char *xr = XL + (b * 32 + l32) * RPX + lh * 16;
-#pragma unroll
-      for (int k = 0; k < KE; ++k) e = ir_mma<DT>(aw[k], *reinterpret_cast<const u32x4 *>(xr + k * 32), e);
-      char *row = XeL + (b * 32 + l32) * IRW_RPE;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<u32x2 *>(row + (8 * q + 4 * lh) * ES) =
-            irw_act_pack4<DT, RLP>(act_e, f32x4{e[4 * q], e[4 * q + 1], e[4 * q + 2], e[4 * q + 3]});
-    }
-    irw_wave_order();
-    // the next chunk's operands go out now: its expand weights into the
-    // registers this expand has finished with, its small tensors into the
-    // other ring slot (last read by the previous chunk, whose reads are done)
-    if (c + 1 < c_end) {
-      load_aw(c + 1, aw);
-      load_small(c + 1, s ^ 1u);
-    }
-
-    // depthwise of the lane's K slice straight into the projection's B operand
-    const char *wdp = sm + lh * 16;
-    const char *bdp = sm + 9 * EC * ES + lh * 16;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      if constexpr (!WP_EARLY) {
-#pragma unroll
-        for (int o = 0; o < NOB; ++o) wpv[ks][o] = load_wp(c, ks, o);
+      if (c + 1 < c_end) {
+        load_aw(c + 1, nxt);
+        load_small(c + 1, s ^ 1u);
       }
-      float d[HK];
-      ir_unpack<DT, HK>(*reinterpret_cast<const u32x4 *>(bdp + ks * 32), d);
+      expand(sm, cur);
+      irw_wave_order();
+      const char *wdp = sm + lh * 16;
+      const char *bdp = sm + 9 * EC * ES + lh * 16;
 #pragma unroll
-      for (int t0 = 0; t0 < 9; t0 += TB) {
-        u32x4 wv[TB], xv[TB];
+      for (int ks = 0; ks < NKS; ++ks) {
+        float d[HK];
+        ir_unpack<DT, HK>(*reinterpret_cast<const u32x4 *>(bdp + ks * 32), d);
 #pragma unroll
-        for (int t = 0; t < TB; ++t) wv[t] = *reinterpret_cast<const u32x4 *>(wdp + (t0 + t) * (EC * ES) + ks * 32);
+        for (int t0 = 0; t0 < 9; t0 += TB) {
+          u32x4 wv[TB], xv[TB];
 #pragma unroll
-        for (int t = 0; t < TB; ++t)
-          xv[t] = *reinterpret_cast<const u32x4 *>(XeL + rowo[(t0 + t) / 3] + ((t0 + t) % 3) * IRW_RPE + ks * 32);
-        __builtin_amdgcn_sched_barrier(0);
+          for (int t = 0; t < TB; ++t) wv[t] = *reinterpret_cast<const u32x4 *>(wdp + (t0 + t) * (EC * ES) + ks * 32);
 #pragma unroll
-        for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
-      }
-      u32x4 bop;
-      if constexpr (RLP) {
-        bop = ir_pack<DT, HK>(d);
-        bop = u32x4{irw_relu2(bop.x), irw_relu2(bop.y), irw_relu2(bop.z), irw_relu2(bop.w)};
-      } else {
+          for (int t = 0; t < TB; ++t)
+            xv[t] = *reinterpret_cast<const u32x4 *>(XeL + rowo[(t0 + t) / 3] + ((t0 + t) % 3) * IRW_RPE + ks * 32);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
+        }
         ir_act<true, HK>(act_d, d);
-        bop = ir_pack<DT, HK>(d);
-      }
+        const u32x4 bop = ir_pack<DT, HK>(d);
 #pragma unroll
-      for (int o = 0; o < NOB; ++o) acc[o] = ir_mma<DT>(wpv[ks][o], bop, acc[o]);
-      __builtin_amdgcn_sched_barrier(0);
+        for (int o = 0; o < NOB; ++o) acc[o] = ir_mma<DT>(wpv[ks][o], bop, acc[o]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      irw_wave_order();
+    };
+    for (uint32_t c = c_begin; c < c_end; c += 2) {
+      step(c, 0, awA, awB);
+      if (c + 1 < c_end) step(c + 1, 1, awB, awA);
     }
-    // the next chunk's expand overwrites XeL after these reads
-    irw_wave_order();
   }
 
   // ---- partial sums: wavefront w's block o at [w][o][q][lane] (f32x4) ----
@@ -282,31 +382,44 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
   }
 }
 
-template <int DT, int KE, int NPI, int NOB, bool RL>
+template <int DT, int KE, int NPI, int NOB, bool RL, bool DP>
 inline hipError_t irs_prepare_inst() {
   static const hipError_t e = hipFuncSetAttribute(
-      reinterpret_cast<const void *>(ir_split_kernel<DT, KE, NPI, NOB, RL>),
+      reinterpret_cast<const void *>(ir_split_kernel<DT, KE, NPI, NOB, RL, DP>),
       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   return e;
 }
 
-template <int DT, int KE, int NPI, int NOB, bool RL>
+template <int DT, int KE, int NPI, int NOB, bool RL, bool DP>
 inline hipError_t irs_launch_inst(const IrWaveArgs &a, uint32_t waves, uint32_t lds, uint32_t grid,
                                   hipStream_t st) {
-  const hipError_t e = irs_prepare_inst<DT, KE, NPI, NOB, RL>();
+  const hipError_t e = irs_prepare_inst<DT, KE, NPI, NOB, RL, DP>();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((ir_split_kernel<DT, KE, NPI, NOB, RL>), dim3(grid), dim3(64 * waves), lds, st, a);
+  hipLaunchKernelGGL((ir_split_kernel<DT, KE, NPI, NOB, RL, DP>), dim3(grid), dim3(64 * waves), lds, st, a);
   return hipGetLastError();
 }
 
-template <int DT, int KE, int NPI, int NOB, bool RL>
+template <int DT, int KE, int NPI, int NOB, bool RL, bool DP>
 inline int irs_occ_inst(uint32_t waves, uint32_t lds) {
-  if (irs_prepare_inst<DT, KE, NPI, NOB, RL>() != hipSuccess) return 0;
+  if (irs_prepare_inst<DT, KE, NPI, NOB, RL, DP>() != hipSuccess) return 0;
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_split_kernel<DT, KE, NPI, NOB, RL>,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_split_kernel<DT, KE, NPI, NOB, RL, DP>,
                                                    (int)(64 * waves), lds) != hipSuccess)
     return 0;
   return per_cu;
+}
+
+template <int DT, int KE, int NPI, int NOB, bool RL>
+inline hipError_t irs_launch_rl(const IrWaveArgs &a, bool deep, uint32_t waves, uint32_t lds, uint32_t grid,
+                                hipStream_t st) {
+  return deep ? irs_launch_inst<DT, KE, NPI, NOB, RL, true>(a, waves, lds, grid, st)
+              : irs_launch_inst<DT, KE, NPI, NOB, RL, false>(a, waves, lds, grid, st);
+}
+
+template <int DT, int KE, int NPI, int NOB, bool RL>
+inline int irs_occ_rl(bool deep, uint32_t waves, uint32_t lds) {
+  return deep ? irs_occ_inst<DT, KE, NPI, NOB, RL, true>(waves, lds)
+              : irs_occ_inst<DT, KE, NPI, NOB, RL, false>(waves, lds);
 }
 
 // The split kernel's instantiations: the wave kernel's, and the stride-2
@@ -323,34 +436,35 @@ inline bool irs_has_shape(uint32_t ke, uint32_t npi, uint32_t nob) {
 }
 
 template <int DT>
-inline hipError_t irs_launch_dt(const IrWaveArgs &a, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
-                                hipStream_t st) {
+inline hipError_t irs_launch_dt(const IrWaveArgs &a, uint32_t npi, bool deep, uint32_t waves, uint32_t lds,
+                                uint32_t grid, hipStream_t st) {
   const uint32_t ke = a.C / 16, nob = a.COP / 32;
   const bool rl = irw_relu_inner(a.act_e, a.act_d);
 #define AIH_IRS_LAUNCH(KE, NPI, NOB)                                                          \
   if (ke == KE && npi == NPI && nob == NOB)                                                   \
-    return rl ? irs_launch_inst<DT, KE, NPI, NOB, true>(a, waves, lds, grid, st)             \
-              : irs_launch_inst<DT, KE, NPI, NOB, false>(a, waves, lds, grid, st);
+    return rl ? irs_launch_rl<DT, KE, NPI, NOB, true>(a, deep, waves, lds, grid, st)         \
+              : irs_launch_rl<DT, KE, NPI, NOB, false>(a, deep, waves, lds, grid, st);
   AIH_IRS_SHAPES(AIH_IRS_LAUNCH)
 #undef AIH_IRS_LAUNCH
   return hipErrorInvalidValue;
 }
 
 template <int DT>
-inline int irs_occ_dt(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves, uint32_t lds) {
-#define AIH_IRS_OCC(KE, NPI, NOB)                                                                        \
-  if (ke == KE && npi == NPI && nob == NOB)                                                              \
-    return rl ? irs_occ_inst<DT, KE, NPI, NOB, true>(waves, lds) : irs_occ_inst<DT, KE, NPI, NOB, false>(waves, lds);
+inline int irs_occ_dt(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, bool deep, uint32_t waves, uint32_t lds) {
+#define AIH_IRS_OCC(KE, NPI, NOB)                                                           \
+  if (ke == KE && npi == NPI && nob == NOB)                                                 \
+    return rl ? irs_occ_rl<DT, KE, NPI, NOB, true>(deep, waves, lds)                        \
+              : irs_occ_rl<DT, KE, NPI, NOB, false>(deep, waves, lds);
   AIH_IRS_SHAPES(AIH_IRS_OCC)
 #undef AIH_IRS_OCC
   return 0;
 }
 
-hipError_t launch_ir_split_f16(const IrWaveArgs &a, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
-                               hipStream_t st);
-hipError_t launch_ir_split_bf16(const IrWaveArgs &a, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
-                                hipStream_t st);
-int ir_split_occ_f16(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves, uint32_t lds);
-int ir_split_occ_bf16(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves, uint32_t lds);
+hipError_t launch_ir_split_f16(const IrWaveArgs &a, uint32_t npi, bool deep, uint32_t waves, uint32_t lds,
+                               uint32_t grid, hipStream_t st);
+hipError_t launch_ir_split_bf16(const IrWaveArgs &a, uint32_t npi, bool deep, uint32_t waves, uint32_t lds,
+                                uint32_t grid, hipStream_t st);
+int ir_split_occ_f16(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, bool deep, uint32_t waves, uint32_t lds);
+int ir_split_occ_bf16(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, bool deep, uint32_t waves, uint32_t lds);
 
 }  // namespace aih

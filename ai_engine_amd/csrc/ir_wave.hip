@@ -23,10 +23,11 @@ uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
 
 // Workgroups per CU of an instantiation at a workgroup size and LDS size
 // (queried once per device).
-int irw_occupancy(bool split, int dt, uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves,
+// split: 0 = wave kernel, 1 = split kernel, 2 = split kernel with the deep prefetch
+int irw_occupancy(int split, int dt, uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves,
                   uint32_t lds) {
   static std::mutex mu;
-  static std::map<std::tuple<bool, int, uint32_t, uint32_t, uint32_t, bool, uint32_t, uint32_t, int>, int> cache;
+  static std::map<std::tuple<int, int, uint32_t, uint32_t, uint32_t, bool, uint32_t, uint32_t, int>, int> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = -1;
   std::lock_guard<std::mutex> lock(mu);
@@ -35,7 +36,8 @@ int irw_occupancy(bool split, int dt, uint32_t ke, uint32_t npi, uint32_t nob, b
   if (it != cache.end()) return it->second;
   int occ;
   if (split)
-    occ = dt == DT_F16 ? ir_split_occ_f16(ke, npi, nob, rl, waves, lds) : ir_split_occ_bf16(ke, npi, nob, rl, waves, lds);
+    occ = dt == DT_F16 ? ir_split_occ_f16(ke, npi, nob, rl, split == 2, waves, lds)
+                       : ir_split_occ_bf16(ke, npi, nob, rl, split == 2, waves, lds);
   else
     occ = dt == DT_F16 ? ir_wave_occ_f16(ke, npi, nob, rl, waves, lds) : ir_wave_occ_bf16(ke, npi, nob, rl, waves, lds);
   // without a device the runtime cannot answer: plan for one workgroup per CU
@@ -151,7 +153,7 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
           p.lds_red = 0;
           p.lds = p.lds_xe + waves * npi * 32 * IRW_RPE;
           if (p.lds > 160u * 1024u) continue;
-          p.occ = (uint32_t)irw_occupancy(false, dt, ke, npi, nob, rl, waves, p.lds);
+          p.occ = (uint32_t)irw_occupancy(0, dt, ke, npi, nob, rl, waves, p.lds);
           p.tiles_y = tiles_y;
           p.tiles_x = tiles_x;
           p.ntiles = nt;
@@ -188,7 +190,12 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
         p.lds_red = p.lds_x;
         p.lds = p.lds_x + std::max(p.lds_w + w * IRS_RING - p.lds_x, w * nob * IRS_RED_BLOCK);
         if (p.lds > 160u * 1024u) continue;
-        p.occ = (uint32_t)irw_occupancy(true, dt, ke, npi, nob, rl, w, p.lds);
+        p.occ = (uint32_t)irw_occupancy(1, dt, ke, npi, nob, rl, w, p.lds);
+        // the deep prefetch where its registers cost no workgroup this
+        // launch would have resident
+        const uint32_t occ_deep = (uint32_t)irw_occupancy(2, dt, ke, npi, nob, rl, w, p.lds);
+        p.deep = occ_deep >= std::min(p.occ, cdiv(nt, cus)) ? 1u : 0u;
+        if (p.deep) p.occ = occ_deep;
         p.tiles_y = tiles_y;
         p.tiles_x = tiles_x;
         p.ntiles = nt;
@@ -228,8 +235,8 @@ hipError_t launch_ir_wave(const IrWaveArgs &a, int dt, const IrWavePlan &p, hipS
   if (p.split) {
     if (p.waves != 1 && p.waves != 2 && p.waves != 4 && p.waves != 8) return hipErrorInvalidValue;
     switch (dt) {
-      case DT_F16: return launch_ir_split_f16(a, p.NPI, p.waves, p.lds, p.grid, st);
-      case DT_BF16: return launch_ir_split_bf16(a, p.NPI, p.waves, p.lds, p.grid, st);
+      case DT_F16: return launch_ir_split_f16(a, p.NPI, p.deep != 0, p.waves, p.lds, p.grid, st);
+      case DT_BF16: return launch_ir_split_bf16(a, p.NPI, p.deep != 0, p.waves, p.lds, p.grid, st);
       default: return hipErrorInvalidValue;
     }
   }

@@ -38,20 +38,21 @@
 namespace aih {
 
 // Global -> LDS copy of n items of SZ bytes (LDS-direct loads, no
-// registers): item g from byte offset src(g); the workgroup's `threads`
+// registers): item g from byte offset src(g) + soff (soff: a wavefront-
+// uniform part, added in the scalar offset); the workgroup's `threads`
 // take 64-item rows in turn, a row per wavefront. Asynchronous until
 // ir_dma_wait() and a barrier.
 template <int SZ, class F>
 __device__ __forceinline__ void irw_dma(char *dst, uint32_t n, __amdgpu_buffer_rsrc_t rs, int wave, int lane,
-                                        uint32_t threads, F src) {
+                                        uint32_t threads, F src, uint32_t soff = 0) {
   for (uint32_t g0 = (uint32_t)wave * 64; g0 < n; g0 += threads) {
     const uint32_t g = g0 + lane;
     if (g >= n) continue;
     ir_lds_void *d = (ir_lds_void *)(dst + g0 * SZ);
     if constexpr (SZ == 16)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, d, 16, src(g), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, d, 16, src(g), (int)soff, 0, 0);
     else
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, d, 4, src(g), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, d, 4, src(g), (int)soff, 0, 0);
   }
 }
 
@@ -103,12 +104,15 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   // registers held across a chunk (input halo, expand A operands, projection
   // accumulators) leave room for 72 more, else one row of three. The
   // narrowest shape (HELD <= 64) fits four waves per SIMD in 128 VGPRs only
-  // with the short batch and the unpacked ReLU; four waves beat both there.
+  // with the short batch; four waves beat the long one there.
   constexpr int HELD = 4 * NPI * KE + 4 * KE + 16 * NOB;
   constexpr int TB = HELD > 64 && HELD <= 120 ? 9 : 3;
   // packed ReLU where the registers allow it (it keeps the packed results
-  // live longer; the widest instantiations would spill)
-  constexpr bool RLP = RL && HELD > 64 && HELD <= 130;
+  // live longer; the widest instantiations would spill): on the expand's
+  // epilogue (RLE) and the depthwise result (RLD) -- on the narrowest shape
+  // only the former keeps it within 128 VGPRs
+  constexpr bool RLE = RL && HELD <= 130;
+  constexpr bool RLD = RL && HELD > 64 && HELD <= 130;
   const int tid = threadIdx.x;
   const int lane = tid & 63, l32 = lane & 31, lh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -251,7 +255,7 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         *reinterpret_cast<u32x2 *>(row + (8 * q + 4 * lh) * ES) =
-            irw_act_pack4<DT, RLP>(act_e, f32x4{e[4 * q], e[4 * q + 1], e[4 * q + 2], e[4 * q + 3]});
+            irw_act_pack4<DT, RLE>(act_e, f32x4{e[4 * q], e[4 * q + 1], e[4 * q + 2], e[4 * q + 3]});
     }
     irw_wave_order();
 
@@ -278,7 +282,7 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
         for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
       }
       u32x4 bop;
-      if constexpr (RLP) {
+      if constexpr (RLD) {
         bop = ir_pack<DT, HK>(d);
         bop = u32x4{irw_relu2(bop.x), irw_relu2(bop.y), irw_relu2(bop.z), irw_relu2(bop.w)};
       } else {
