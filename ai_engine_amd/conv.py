@@ -127,12 +127,13 @@ class _IrDesc(C.Structure):
 class IrPlan(C.Structure):
     _fields_ = [("th", C.c_uint32), ("tw", C.c_uint32), ("ec", C.c_uint32), ("chunks", C.c_uint32),
                 ("resident", C.c_uint32), ("tiles", C.c_uint32), ("lds_bytes", C.c_uint32),
-                ("occupancy", C.c_uint32), ("grid", C.c_uint32), ("kernel", C.c_uint32), ("waves", C.c_uint32)]
+                ("occupancy", C.c_uint32), ("grid", C.c_uint32), ("kernel", C.c_uint32), ("waves", C.c_uint32),
+                ("deep", C.c_uint32)]
 
     def __repr__(self):
         return (f"IrPlan({IrKernel(self.kernel).name.lower()}, tile={self.th}x{self.tw}, ec={self.ec}, "
                 f"chunks={self.chunks}, resident={self.resident}, tiles={self.tiles}, lds={self.lds_bytes}, "
-                f"occ={self.occupancy}, grid={self.grid}x{self.waves} waves)")
+                f"occ={self.occupancy}, grid={self.grid}x{self.waves} waves{', deep' if self.deep else ''})")
 
 
 class Plan(C.Structure):

@@ -857,14 +857,14 @@ int aih_ir_block_plan(const aih_ir_block_desc *d, aih_ir_plan *out) {
     if (plan_ir_wave(d, oh, ow, &wp, &wave)) return AIH_ERR;
     if (wave) {
       *out = aih_ir_plan{wp.TH, wp.TW, 32, d->cexp / 32, wp.resident, wp.ntiles, wp.lds, wp.occ, wp.grid,
-                         wp.split ? AIH_IR_KERNEL_SPLIT : AIH_IR_KERNEL_WAVE, wp.waves};
+                         wp.split ? AIH_IR_KERNEL_SPLIT : AIH_IR_KERNEL_WAVE, wp.waves, wp.deep};
       return AIH_OK;
     }
     if (d->waves) return fail("ir_block: the tile kernel's workgroups have 4 wavefronts (waves must be 0)");
     aih::IrPlan p;
     if (plan_ir(d, oh, ow, &p)) return AIH_ERR;
     *out = aih_ir_plan{p.TH, p.TW, p.EC, d->cexp / p.EC, p.resident, p.ntiles, p.lds, p.occ, p.grid,
-                       AIH_IR_KERNEL_TILE, 4};
+                       AIH_IR_KERNEL_TILE, 4, 0};
     return AIH_OK;
   });
 }

@@ -69,6 +69,10 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--choices", default=None,
                     help="JSON map block -> launch label (as printed in block_choices) to load without tuning")
+    ap.add_argument("--profile-config", default=None, choices=sorted(PROFILE_CONFIGS),
+                    help="run only this workload's launches, --profile-reps times, and print no JSON line "
+                         "(the command rocprofv3 counter passes run)")
+    ap.add_argument("--profile-reps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -86,6 +90,8 @@ def main() -> int:
     conv.lib()
     torch.manual_seed(0)
     DT = {"f32": conv.DType.F32, "f16": conv.DType.F16, "bf16": conv.DType.BF16}
+    if args.profile_config:
+        return profile_config(args, torch, conv, W, Model, dev, DT)
 
     # ------------------------------------------------------------ headline: encoder, batch 64
     layers, meta = W.mnv4_small_encoder_160x288(64)
@@ -241,6 +247,71 @@ def main() -> int:
     return 0
 
 
+# Workloads --profile-config can run alone: (kind, n, h, w, cin, cout, stride, activation)
+PROFILE_CONFIGS = {
+    "pw_32to64_relu6_80x144": ("pw", 1, 80, 144, 32, 64, 1, "RELU6"),
+    "pw_960to160_10x18_b1": ("pw", 1, 10, 18, 960, 160, 1, "NONE"),
+    "pw_960to160_10x18_b256": ("pw", 256, 10, 18, 960, 160, 1, "NONE"),
+    "igemm3x3s2_16to32_relu_160x288_b32": ("ig", 32, 160, 288, 16, 32, 2, "RELU"),
+    "igemm3x3s1_32to64_relu_80x144_b32": ("ig", 32, 80, 144, 32, 64, 1, "RELU"),
+    "ir_block_chain_4x_64c_40x72_b64": ("chain",),
+    "encoder_160x288_b64": ("encoder",),
+    "copy_1gib": ("copy",),  # calibration: reads and writes 1 GiB
+}
+
+
+def profile_config(args, torch, conv, W, Model, dev, DT) -> int:
+    """--profile-config: the launches of one workload only (fp32 configs as in
+    the kernel table, the encoder in --dtype with --choices), so that a
+    rocprofv3 counter pass sees that workload's kernels and nothing else
+    (besides torch's input fills)."""
+    cfg = PROFILE_CONFIGS[args.profile_config]
+    reps = args.profile_reps
+    rnd = lambda nel, scale=1.0: (torch.rand(nel, device=dev) * 2 - 1) * scale
+    A = conv.Activation
+    if cfg[0] in ("pw", "ig"):
+        _, n, h, w, cin, cout, s, act = cfg
+        if cfg[0] == "pw":
+            spec = conv.GemmPwSpec(m=h * w, kg=cin // 4, ng=cout // 4, act=A[act], n=n)
+            m = n * h * w
+            x, wt = rnd(m * cin), rnd(cin * cout, 0.05)
+            run = lambda y, ws: spec.run(x, wt, b, None, y, ws)
+        else:
+            spec = conv.ConvIgemmSpec(ih=h, iw=w, cin=cin, cout=cout, k=3, s=s, pad=(1, 1, 1, 1), act=A[act], n=n)
+            oh, ow = spec.out_hw()
+            m = n * oh * ow
+            x, wt = rnd(n * h * w * cin), rnd(9 * cin * cout, 0.1)
+            run = lambda y, ws: spec.run([x], wt, b, None, y, ws)
+        b = rnd(cout, 0.01)
+        y = torch.empty(m * cout, device=dev)
+        ws = torch.empty(max(spec.plan().ws_bytes // 4, 1), device=dev)
+        for _ in range(reps):
+            run(y, ws)
+    elif cfg[0] == "chain":
+        layers, meta = W.ir_chain_40x72(64)
+        m4 = Model(layers, W.make_weights(layers, seed=1), meta["n"], meta["h"], meta["w"], meta["c"], dt=DT["f32"],
+                   tune=False)
+        m4.tensors["input"].uniform_(-1, 1)
+        for _ in range(reps):
+            m4.infer()
+    elif cfg[0] == "copy":
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(reps):
+            dst.copy_(src)
+    else:
+        layers, meta = W.mnv4_small_encoder_160x288(64)
+        model = Model(layers, W.make_weights(layers, seed=0), meta["n"], meta["h"], meta["w"], 3, dt=DT[args.dtype],
+                      choices=json.loads(args.choices) if args.choices else None)
+        x = (torch.rand(meta["n"], meta["h"], meta["w"], 3, device=dev) * 2 - 1).contiguous()
+        for _ in range(reps):
+            model.upload_input(x)
+            model.infer()
+    torch.cuda.synchronize()
+    log(f"profiled {args.profile_config}: {reps} repetitions")
+    return 0
+
+
 def measured_traffic(key: str):
     """HBM bytes per launch of kernel `key` as the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary under profiles/ reports it (calibrated against a 1 GiB
@@ -264,8 +335,12 @@ def kernel_key(conv, op, n, dt, dtname) -> str:
         if p.kernel in (conv.IrKernel.WAVE, conv.IrKernel.SPLIT):
             s = op.spec.s
             npi = 2 if ((p.th - 1) * s + 3) * ((p.tw - 1) * s + 3) <= 64 else 5
-            name = "ir_wave_kernel" if p.kernel == conv.IrKernel.WAVE else "ir_split_kernel"
-            return f"{name}<{int(dt)}, {op.spec.cin // 16}, {npi}, {-(-op.spec.cout // 32)}>"
+            A = conv.Activation
+            rl = "true" if int(op.spec.act_expand) == A.RELU and int(op.spec.act_dw) == A.RELU else "false"
+            head = f"<{int(dt)}, {op.spec.cin // 16}, {npi}, {-(-op.spec.cout // 32)}, {rl}"
+            if p.kernel == conv.IrKernel.WAVE:
+                return f"ir_wave_kernel{head}>"
+            return f"ir_split_kernel{head}, {'true' if p.deep else 'false'}>"
         npw = -(-(-(-p.th * p.tw // 32)) // 4)
         A = conv.Activation
         clamp = all(int(x) in (A.NONE, A.RELU, A.RELU6, A.CLAMP01)

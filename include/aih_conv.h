@@ -209,6 +209,7 @@ typedef struct {
   uint32_t tiles, lds_bytes, occupancy, grid;
   uint32_t kernel; /* enum aih_ir_kernel: AIH_IR_KERNEL_TILE, _WAVE or _SPLIT */
   uint32_t waves;  /* wavefronts per workgroup */
+  uint32_t deep;   /* split kernel: operands prefetched a whole chunk ahead (1) or one phase ahead (0) */
 } aih_ir_plan;
 
 /* ---- op entry points (asynchronous on `stream`) ---- */
