@@ -24,6 +24,7 @@
 #include "conv_pw_direct.h"
 #include "conv_pw_narrow.h"
 #include "conv_pw_splitk.h"
+#include "conv_pw_stream.h"
 #include "conv_stem.h"
 #include "ir_block.h"
 
@@ -200,7 +201,7 @@ bool env_igemm_no_split() {
 // one output channel group goes to the one-pixel-per-thread kernel and short
 // K with at most 64 output channels (same storage for activations and
 // weights) to the direct MFMA kernel; everything else to the tiled GEMM.
-enum { PW_TILED = 0, PW_ROWS = 1, PW_DIRECT = 2, PW_LDS = 3, PW_SPLITK = 4 };
+enum { PW_TILED = 0, PW_ROWS = 1, PW_DIRECT = 2, PW_LDS = 3, PW_SPLITK = 4, PW_STREAM = 5 };
 
 // The pointwise call as a one-tap launch of the direct 3x3 kernel (weights
 // resident in LDS, activations straight into MFMA registers): what the
@@ -247,6 +248,44 @@ bool pw_lds_plan(const aih_pw_desc *d, aih::IgDirectArgs *a) {
   return true;
 }
 
+// The fp32 pointwise call on the LDS-streamed GEMM (conv_pw_stream.hip): long
+// K (>= 256 channels, MFMA-bound), whole buffers within 32-bit offsets, and
+// at least 8 wavefront units (32 pixels x 32 channels or two such) per CU,
+// so the fine-grained grid evens out without splitting K. The tile width is
+// the instantiation that pads the output channels least (the wider on ties).
+bool pw_stream_plan(const aih_pw_desc *d, aih::PwStreamArgs *a, aih::PwStreamShape *shape) {
+  if (d->dt != AIH_F32 || d->wdt != AIH_F32 || d->kg < 64) return false;
+  const uint64_t M = (uint64_t)d->n * d->m, N4 = (uint64_t)d->ng * 4;
+  const uint64_t xb = M * d->kg * 16, wb = (uint64_t)d->kg_pad * N4 * 16;
+  if (xb >= 0x80000000ull || wb >= 0x80000000ull) return false;
+  const aih::PwStreamShape *best = nullptr;
+  uint64_t best_cols = 0;
+  for (const aih::PwStreamShape &sh : aih::kPwStreamShapes) {
+    const uint64_t cols = (N4 + aih::pw_stream_bn(sh) - 1) / aih::pw_stream_bn(sh) * aih::pw_stream_bn(sh);
+    if (!best || cols < best_cols || (cols == best_cols && aih::pw_stream_bn(sh) > aih::pw_stream_bn(*best))) {
+      best = &sh;
+      best_cols = cols;
+    }
+  }
+  const uint64_t mtiles = (M + aih::pw_stream_bm(*best) - 1) / aih::pw_stream_bm(*best);
+  const uint64_t ntiles = best_cols / aih::pw_stream_bn(*best);
+  if (mtiles * ntiles * best->wm * best->wn < 8ull * aih::device_cus() || mtiles * ntiles > 0x7fffffffull)
+    return false;
+  std::memset(a, 0, sizeof(*a));
+  a->x_bytes = (uint32_t)xb;
+  a->w_bytes = (uint32_t)wb;
+  a->M = (uint32_t)M;
+  a->KG = d->kg;
+  a->N4 = (uint32_t)N4;
+  a->mtiles = (uint32_t)mtiles;
+  a->ntiles = (uint32_t)ntiles;
+  a->act = d->act;
+  a->has_res = d->residual ? 1 : 0;
+  a->nxcd = aih::device_xcds();
+  *shape = *best;
+  return true;
+}
+
 // The split factor of a pointwise call: the descriptor's, else (AUTO only)
 // the AIH_PW_SPLITK override, else 0 (the policy decides).
 int32_t pw_splitk_of(const aih_pw_desc *d) {
@@ -285,6 +324,9 @@ int pw_route(const aih_pw_desc *d) {
   }
   aih::IgDirectArgs a;
   if (pw_lds_plan(d, &a)) return PW_LDS;
+  aih::PwStreamArgs sa;
+  aih::PwStreamShape ss;
+  if (pw_stream_plan(d, &sa, &ss)) return PW_STREAM;
   // small M, long K (the reference's kg >= 16 gate, gemm_pw.rs:91-102): the
   // tiled GEMM's 128-pixel tiles cannot fill the CUs and would split K
   // through memory; one dispatch with the split on chip instead
@@ -570,6 +612,14 @@ int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out) {
                         0};
         return AIH_OK;
       }
+      case PW_STREAM: {
+        // a tiled GEMM over the whole K (operands streamed through LDS)
+        aih::PwStreamArgs a;
+        aih::PwStreamShape sh;
+        pw_stream_plan(d, &a, &sh);
+        *out = aih_plan{AIH_VAR_TILE, 1, aih::pw_stream_bm(sh), aih::pw_stream_bn(sh), a.mtiles * a.ntiles, 0};
+        return AIH_OK;
+      }
       case PW_DIRECT:
         *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->ng * 4 <= 32 ? 32u : 64u,
                         aih::pw_direct_grid((uint32_t)((M + 31) / 32), aih::device_cus()), 0};
@@ -625,6 +675,19 @@ int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *
       a.y = y;
       const hipError_t e = aih::launch_ig_direct(a, d->dt, static_cast<hipStream_t>(stream));
       return e == hipSuccess ? AIH_OK : fail(std::string("pw lds-direct launch: ") + hipGetErrorString(e));
+    }
+    if (route == PW_STREAM) {
+      // fp32, long K, many pixels: operands streamed through LDS by DMA
+      aih::PwStreamArgs a;
+      aih::PwStreamShape sh;
+      pw_stream_plan(d, &a, &sh);
+      a.x = x;
+      a.w = w;
+      a.bias = bias;
+      a.res = res;
+      a.y = y;
+      const hipError_t e = aih::launch_pw_stream(a, sh, static_cast<hipStream_t>(stream));
+      return e == hipSuccess ? AIH_OK : fail(std::string("pw stream launch: ") + hipGetErrorString(e));
     }
     if (route == PW_DIRECT) {
       // short K and at most 64 output channels: operands from memory straight

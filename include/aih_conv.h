@@ -221,7 +221,10 @@ typedef struct {
  * no workspace: ng == 1 (at most 4 output channels) runs a VALU kernel (one
  * pixel per thread, the reference's Gemv role); dt == wdt, 2 <= ng <= 16 and
  * at most 128 (16-bit) / 64 (fp32) input channels run a direct MFMA kernel
- * (32 pixels per wavefront, operands from memory into registers). */
+ * (32 pixels per wavefront, operands from memory into registers); fp32 with
+ * at least 256 input channels and enough pixels for eight 32 x 32 wavefront
+ * units per CU runs a GEMM whose operands stream through LDS by DMA over
+ * the whole K (reported as AIH_VAR_TILE with bm = 96, no workspace). */
 int aih_conv_pw(const aih_pw_desc *d, const void *x, const void *w, const void *bias,
                 const void *res, void *y, void *ws, size_t ws_bytes, aih_stream stream);
 int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out);

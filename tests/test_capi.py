@@ -111,14 +111,28 @@ def test_pw_policy_agrees_with_reference_on_its_splitk_kats(orc):
         assert p.variant in (conv.Variant.TILE, conv.Variant.DIRECT) and p.splitk == 1, (m, kg, ng, p)
 
 
-def test_pw_policy_splits_long_k_fp32_partial_second_round():
-    """fp32, K >= 512, tiles between one and two per CU: four K chunks
-    (960 -> 160 at 10x18, batch 256: 360 tiles)."""
+def test_pw_policy_long_k_fp32_many_pixels():
+    """fp32, K >= 256 and at least 8 wavefront units per CU: the LDS-streamed
+    GEMM over the whole K (960 -> 160 at 10x18, batch 256: 480 tiles of
+    96 x 160, no workspace)."""
     p = pw_plan(256, 180, 960, 160)
+    assert p.variant == conv.Variant.TILE and p.splitk == 1 and (p.bm, p.bn, p.grid, p.ws_bytes) == (96, 160, 480, 0)
+    p = pw_plan(256, 180, 256, 160)
+    assert p.splitk == 1 and p.bm == 96
+    # at 16 bit (HBM-bound) the tiled GEMM keeps K whole
+    p = conv.GemmPwSpec(m=180, kg=240, ng=40, n=256, dt=conv.DType.F16).plan()
+    assert p.splitk == 1 and p.bm == 128
+    # too few pixels for eight units per CU: the tiled GEMM's policy decides
+    assert pw_plan(8, 180, 960, 160).bm != 96
+
+
+def test_tiled_policy_splits_long_k_fp32_partial_second_round():
+    """The tiled GEMM with fp32, long K and tiles between one and two per CU
+    takes four K chunks: a 3x3 256 -> 160 conv at 10x18, batch 256 (360
+    tiles of 128 x 160)."""
+    op = conv.ConvOp(ih=10, iw=18, cin=256, cout=160, kh=3, kw=3, pad=(1, 1, 1, 1), n=256)
+    p = op.plan()
     assert p.variant == conv.Variant.SPLITK and p.splitk == 4 and p.grid == 1440
-    # the same at 16 bit (HBM-bound) and with short K stays whole
-    assert conv.GemmPwSpec(m=180, kg=240, ng=40, n=256, dt=conv.DType.F16).plan().splitk == 1
-    assert pw_plan(256, 180, 256, 160).splitk == 1
 
 
 def test_forced_splitk_factor_is_honoured():

@@ -195,6 +195,34 @@ def test_pw_tail_tiles():
     check("pw tails", res, F32)
 
 
+# fp32, K >= 256 channels and enough 32-pixel x 32-channel wavefront units to
+# fill every CU eight times over: the LDS-streamed GEMM (96-pixel tiles over
+# the whole K, reported as TILE with bm = 96 and no workspace). The cases
+# take a ragged last pixel tile, a K tail inside the last 16-channel stage,
+# columns padded inside a 128-wide tile, two column tiles, and the 960 -> 160
+# layer at batch 80.
+PW_STREAM = [((1, 13250, 260, 160, 1), "relu6", True, 3601),
+             ((1, 16400, 256, 100, 1), "hardswish", False, 3602),
+             ((1, 16400, 272, 256, 1), "none", True, 3603),
+             ((10, 18, 960, 160, 80), "none", False, 3604)]
+
+
+@pytest.mark.parametrize("case", PW_STREAM, ids=str)
+def test_pw_stream(case):
+    (h, w, cin, cout, n), act, res, seed = case
+    r = G.run_pw(h, w, cin, cout, act, res, F32, seed, n=n)
+    assert r.plan.variant == G.conv.Variant.TILE and r.plan.bm == 96 and r.plan.ws_bytes == 0, r.plan
+    check(f"pw stream {case} {r.plan}", r, F32)
+
+
+def test_pw_stream_is_deterministic():
+    xs = G.stream(3605, 80 * 180 * 960, 160 * 960, 160, 80 * 180 * 160)
+    a = G.run_pw(10, 18, 960, 160, "relu", True, F32, 3605, n=80, xs=xs, refs=False)
+    b = G.run_pw(10, 18, 960, 160, "relu", True, F32, 3605, n=80, xs=xs, refs=False)
+    assert a.plan.bm == 96
+    assert np.array_equal(np.asarray(a.got), np.asarray(b.got))
+
+
 # ---------------------------------------------------------------- depthwise (testsuite.rs:466-496)
 
 DW_SHAPES = [(72, 128, 64, 3, 1), (36, 64, 96, 5, 2), (33, 17, 6, 3, 2), (16, 16, 10, 5, 1)]

@@ -90,7 +90,9 @@ def test_noalloc_split_igemm_and_plain_conv():
 
 def test_noalloc_rejects_workspace_beyond_scratch():
     L = lib()
-    op = conv.ConvOp(ih=10, iw=18, cin=960, cout=160, n=256, dt=conv.DType.F32)
+    # a 3x3 256 -> 160 fp32 conv at 10x18, batch 256: four K chunks on the
+    # tiled implicit GEMM, 118 MB of partial sums
+    op = conv.ConvOp(ih=10, iw=18, cin=256, cout=160, kh=3, kw=3, pad=(1, 1, 1, 1), n=256, dt=conv.DType.F32)
     need = op.workspace_bytes()
     assert need > SCRATCH, need
     d = op.desc()
