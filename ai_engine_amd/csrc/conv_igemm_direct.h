@@ -32,6 +32,7 @@ struct IgDirectArgs {
   int32_t act, has_res;
   uint32_t nxcd;           // XCDs of the device (workgroup remap)
   FastDiv fd_ohw, fd_ow;
+  uint32_t st_off;         // LDS byte offset of the output staging rows, 0: none (set by the launch)
 };
 
 // Threads of one workgroup (the weights in LDS are shared by its wavefronts).

@@ -39,6 +39,11 @@ namespace {
 
 constexpr uint32_t kOob = 0x80000000u;  // a byte offset past every part's buffer
 constexpr int kWaves = kIgDirectThreads / 64;
+// Output staging rows: 32 pixels x 32 fp32 channels per wavefront, the row
+// pitch 4 floats wider so the MFMA-layout writes (8 pixels, one 16-byte piece
+// each, per LDS cycle) fall in distinct banks.
+constexpr uint32_t kStPitch = 36;
+constexpr uint32_t kStBytes = kWaves * 32 * kStPitch * 4;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ig_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
@@ -55,7 +60,10 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
   const uint32_t RS = a.ncg * NC;
   float *Bl = reinterpret_cast<float *>(lds + TAPS * NJ * 2 * RS * 16);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, lh = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, lh = lane >> 5;
+  // the wavefront index in a scalar register: block indices and the loop's
+  // exit test stay uniform (scalar branches, no exec-mask regions)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   // ---- weights -> LDS as [tap][step][half][column] operands (zero padding) ----
   // each thread issues a batch of loads before the batch's LDS stores, so the
@@ -111,14 +119,16 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
   // Wl[wl + cg*NC + (tap*NJ + step)*2*RS + o*32]
   const uint32_t wl = lh * RS + l32;
 
-  // a block's output pixels decoded: lane pixel, its tap-(0, 0) source row and
-  // column, and the unit index (per part) of that source pixel
+  // a block's output pixels decoded: lane pixel, the unit index (per part)
+  // of its tap-(0, 0) source pixel, and which kernel rows / columns of the
+  // taps fall inside the image (bit k: row / column k; no bits for a lane
+  // without a pixel, or a block past the range)
   struct Blk {
     uint32_t pix_out, b0, b1, cg;
-    int32_t iy0, ix0;
+    uint32_t rows, cols;
     bool valid;
   };
-  auto decode = [&](uint32_t item) {
+  auto decode = [&](uint32_t item, bool in_range) {
     Blk b;
     const uint32_t blk = item / a.ncg;
     b.cg = item - blk * a.ncg;
@@ -129,11 +139,20 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
     const uint32_t rem = pp - img * a.OHW;
     const uint32_t oy = fdiv(rem, a.fd_ow);
     const uint32_t ox = rem - oy * a.OW;
-    b.iy0 = (int32_t)(oy * a.S) - a.PT;
-    b.ix0 = (int32_t)(ox * a.S) - a.PL;
+    const int32_t iy0 = (int32_t)(oy * a.S) - a.PT;
+    const int32_t ix0 = (int32_t)(ox * a.S) - a.PL;
+    constexpr int KS = TAPS == 9 ? 3 : 1;
+    uint32_t rows = 0, cols = 0;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      rows |= (uint32_t)((uint32_t)(iy0 + k * (int32_t)a.D) < a.IH) << k;
+      cols |= (uint32_t)((uint32_t)(ix0 + k * (int32_t)a.D) < a.IW) << k;
+    }
+    b.rows = (b.valid & in_range) ? rows : 0u;
+    b.cols = cols;
     // wraps (unsigned) when the tap-(0, 0) pixel lies above or left of the
     // image; tap offsets bring in-image taps back, the others are not read
-    const uint32_t pix = (img * a.IH + (uint32_t)b.iy0) * a.IW + (uint32_t)b.ix0;
+    const uint32_t pix = (img * a.IH + (uint32_t)iy0) * a.IW + (uint32_t)ix0;
     b.b0 = pix * a.stride_u[0] + a.off_u[0];
     b.b1 = pix * a.stride_u[1] + a.off_u[1];
     return b;
@@ -146,9 +165,9 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
   };
   auto tap_src = [&](const Blk &b, int tap) {
     TapSrc t;
-    const uint32_t dy = (tap / 3) * a.D, dx = (tap % 3) * a.D;
-    t.ok = b.valid && (uint32_t)(b.iy0 + (int32_t)dy) < a.IH && (uint32_t)(b.ix0 + (int32_t)dx) < a.IW;
-    const uint32_t dpix = dy * a.IW + dx;
+    const int ky = tap / 3, kx = tap % 3;
+    t.ok = ((b.rows >> ky) & (b.cols >> kx) & 1u) != 0;
+    const uint32_t dpix = (uint32_t)ky * a.D * a.IW + (uint32_t)kx * a.D;
     t.b0 = b.b0 + dpix * a.stride_u[0];
     t.b1 = b.b1 + dpix * a.stride_u[1];
     return t;
@@ -157,7 +176,7 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
   auto load_step = [&](const TapSrc &t, int j) {
     const bool p1 = (uint32_t)j >= nj0;
     const uint32_t u = 2 * ((uint32_t)j - (p1 ? nj0 : 0u)) + lh;
-    const bool in = t.ok && u < (p1 ? a.nu[1] : a.nu[0]);
+    const bool in = t.ok & (u < (p1 ? a.nu[1] : a.nu[0]));
     const uint32_t off = in ? ((p1 ? t.b1 : t.b0) + u) * 16u : kOob;
     return __builtin_amdgcn_raw_buffer_load_b128(p1 ? rs1 : rs0, off, 0, 0);
   };
@@ -180,7 +199,7 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
   static_assert(NS % D == 0, "operand ring");
   uint32_t blk = b_begin + wave;
   if (blk >= b_end) return;
-  Blk cur = decode(blk);
+  Blk cur = decode(blk, true);
   u32x4 x[D];
   TapSrc ts = tap_src(cur, 0);
 #pragma unroll
@@ -195,7 +214,10 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
     load_w(0, wv[0]);
     const uint32_t blk_next = blk + kWaves;
     const bool more = blk_next < b_end;
-    const Blk nxt = decode(more ? blk_next : blk);
+    // past the range the next block reads zeros (offsets outside the
+    // buffers): the ring's loads are issued unconditionally, so the block
+    // loop has no divergent branch and never drains the ring
+    const Blk nxt = decode(more ? blk_next : blk, more);
     f32x16 acc[NOB];
 #pragma unroll
     for (int o = 0; o < NOB; ++o) acc[o] = f32x16{};
@@ -223,7 +245,7 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
       if (sl < NS) {
         if (sl % NJ == 0) ts = tap_src(cur, sl / NJ);
         x[s % D] = load_step(ts, sl % NJ);
-      } else if (more) {
+      } else {
         if ((sl - NS) % NJ == 0) ts = tap_src(nxt, (sl - NS) / NJ);
         x[s % D] = load_step(ts, (sl - NS) % NJ);
       }
@@ -231,7 +253,38 @@ __global__ __launch_bounds__(kIgDirectThreads) void conv_igemm_direct_kernel(IgD
       __builtin_amdgcn_sched_barrier(0);
     }
 
-    if (cur.valid) {
+    if (a.st_off) {
+      // through the wavefront's LDS rows: act(acc + bias) in the MFMA
+      // layout, then 8 pixels x 8 four-channel pieces per store, so a store
+      // instruction writes whole contiguous rows (one 4 KB run for 32 fp32
+      // channels) instead of 16 bytes at each of 64 pixels
+      float *rows = reinterpret_cast<float *>(lds + a.st_off) + wave * 32 * kStPitch;
+      const uint32_t pix0 = cur.pix_out - l32;
+#pragma unroll
+      for (int o = 0; o < NOB; ++o) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t cl = 8 * q + 4 * lh;
+          const uint32_t c = cur.cg * NC + o * 32 + cl;
+          f32x4 v = f32x4{acc[o][4 * q], acc[o][4 * q + 1], acc[o][4 * q + 2], acc[o][4 * q + 3]} +
+                    *reinterpret_cast<const f32x4 *>(Bl + c);
+          *reinterpret_cast<f32x4 *>(rows + l32 * kStPitch + cl) = act4(actp, v);
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t px = 8 * i + (lane >> 3), pc = 4 * (lane & 7);
+          const uint32_t m = pix0 + px, c = cur.cg * NC + o * 32 + pc;
+          f32x4 v = *reinterpret_cast<const f32x4 *>(rows + px * kStPitch + pc);
+          if (m < a.M && c < a.N4) {
+            const size_t vi = (size_t)m * (a.N4 / 4) + c / 4;
+            if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
+            Vec4IO<DT>::store(a.y, vi, v);
+          }
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
+    } else if (cur.valid) {
 #pragma unroll
       for (int o = 0; o < NOB; ++o) {
 #pragma unroll
@@ -259,9 +312,13 @@ hipError_t launch_inst(const IgDirectArgs &a, hipStream_t st) {
       hipFuncSetAttribute(reinterpret_cast<const void *>(conv_igemm_direct_kernel<DT, NOB, TAPS, NJ, D>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (attr != hipSuccess) return attr;
-  const uint32_t lds = ig_direct_lds_bytes(TAPS, a.nj, a.N4);
+  // the output staging rows go after the weights and biases where LDS has room
+  IgDirectArgs b = a;
+  const uint32_t base = ig_direct_lds_bytes(TAPS, a.nj, a.N4);
+  b.st_off = base + kStBytes <= 160u * 1024u ? base : 0u;
+  const uint32_t lds = base + (b.st_off ? kStBytes : 0u);
   const uint32_t grid = ig_direct_grid(a.nblk, a.nj, a.N4);
-  hipLaunchKernelGGL((conv_igemm_direct_kernel<DT, NOB, TAPS, NJ, D>), dim3(grid), dim3(kIgDirectThreads), lds, st, a);
+  hipLaunchKernelGGL((conv_igemm_direct_kernel<DT, NOB, TAPS, NJ, D>), dim3(grid), dim3(kIgDirectThreads), lds, st, b);
   return hipGetLastError();
 }
 
