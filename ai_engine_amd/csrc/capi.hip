@@ -594,9 +594,12 @@ int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out) {
     if (!out) return fail("null plan");
     const uint64_t M = (uint64_t)d->n * d->m;
     switch (pw_route(d)) {
-      case PW_ROWS:
-        *out = aih_plan{AIH_VAR_ROWS, 1, 256, 4, (uint32_t)std::min<uint64_t>((M + 255) / 256, 4096), 0};
+      case PW_ROWS: {
+        // pw_narrow_group(kg) lanes per pixel: 256 / that many pixels per workgroup
+        const uint32_t ppb = 256 / aih::pw_narrow_group(d->kg);
+        *out = aih_plan{AIH_VAR_ROWS, 1, ppb, 4, (uint32_t)std::min<uint64_t>((M + ppb - 1) / ppb, 65535), 0};
         return AIH_OK;
+      }
       case PW_SPLITK: {
         // one dispatch: 16x16 output blocks, K split across `waves`
         // wavefronts (one wavefront: K whole, reported as a direct launch)

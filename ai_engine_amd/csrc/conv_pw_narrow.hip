@@ -1,10 +1,13 @@
 // conv_pw_narrow.hip -- pointwise conv with at most 4 output channels (one
 // NHWC-C4 vector per pixel): the segmentation heads (24 -> 2, 128 -> 2). A
 // 128-pixel x 32-channel MFMA tile would compute 28 zero channels of every 32;
-// here one thread owns one pixel, reads its K channels once (16-byte loads),
-// and does the 4 dot products on the VALU against weights staged in LDS. It
-// is HBM-bound: (K + 4 (+4 res)) * storage bytes per pixel. The role of the
-// reference's Gemv variant (gemm_pw.rs:91-102) and ai-cpu's pw_dot
+// here a group of G lanes owns one pixel: lane g reads input channel
+// groups g, g + G, ... (so the group's loads cover the pixel's
+// contiguous channels, one coalesced run per step), does the 4 dot products
+// on the VALU against weights staged in LDS, and the group adds its partial
+// sums by butterfly shuffles (a fixed order). It is HBM-bound: (K + 4 (+4
+// res)) * storage bytes per pixel. The role of the reference's Gemv variant
+// (gemm_pw.rs:91-102) and ai-cpu's pw_dot
 // (crates/ai-cpu/src/kernels/pw_dot.rs:32-61); the epilogue order is
 // act(acc + bias) (+ residual) as everywhere.
 #include <hip/hip_runtime.h>
@@ -23,7 +26,10 @@ __device__ __forceinline__ f32x4 ld_w4(const void *w, size_t vi) {
   else return unpack4<DTW>(reinterpret_cast<const u32x2 *>(w)[vi]);
 }
 
-template <int DTA, int DTW>
+// Lanes per pixel G: 16 for at least 16 kg (a 128-channel head takes two
+// steps of 64 channels), 4 for 4-15 kg (24 channels: two steps, the second
+// half full), 1 below.
+template <int DTA, int DTW, int G>
 __global__ __launch_bounds__(256) void pw_narrow_kernel(PwNarrowArgs a) {
   extern __shared__ f32x4 wl[];  // [KG][4]: input channels 4kg..4kg+3 of output channel j
   // packed weights with one column group (NG = 1): vector (kg, j) at kg * 4 + j (pack.rs:95)
@@ -31,17 +37,28 @@ __global__ __launch_bounds__(256) void pw_narrow_kernel(PwNarrowArgs a) {
   __syncthreads();
   const f32x4 bias = Vec4IO<DTA>::load(a.bias, 0);
   const Act ap = act_params(a.act);
-  for (uint32_t m = blockIdx.x * 256 + threadIdx.x; m < a.M; m += gridDim.x * 256) {
+  const uint32_t g = threadIdx.x % G;
+  const uint32_t per_block = 256 / G;
+  for (uint32_t m0 = blockIdx.x * per_block; m0 < a.M; m0 += gridDim.x * per_block) {
+    const uint32_t m = m0 + threadIdx.x / G;
+    const bool pv = m < a.M;
     f32x4 acc = {};
-    const size_t xrow = (size_t)m * a.KGX;
-    for (uint32_t kg = 0; kg < a.KG; ++kg) {
-      const f32x4 xv = Vec4IO<DTA>::load(a.x, xrow + kg);
+    const size_t xrow = (size_t)(pv ? m : 0) * a.KGX;
+    for (uint32_t kg = g; kg < a.KG; kg += G) {
+      const f32x4 xv = pv ? Vec4IO<DTA>::load(a.x, xrow + kg) : f32x4{};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f32x4 wv = wl[kg * 4 + j];
         acc[j] += xv.x * wv.x + xv.y * wv.y + xv.z * wv.z + xv.w * wv.w;
       }
     }
+    // the group's partial sums, added by butterfly (every lane ends with the total)
+#pragma unroll
+    for (int off = G / 2; off > 0; off /= 2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] += __shfl_xor(acc[j], off, G);
+    }
+    if (!pv || g != 0) continue;
     float v[4] = {acc.x + bias.x, acc.y + bias.y, acc.z + bias.z, acc.w + bias.w};
     act_array<4>(ap, v);
     f32x4 o = f32x4{v[0], v[1], v[2], v[3]};
@@ -50,11 +67,20 @@ __global__ __launch_bounds__(256) void pw_narrow_kernel(PwNarrowArgs a) {
   }
 }
 
+template <int DTA, int DTW, int G>
+hipError_t launch_g(const PwNarrowArgs &a, hipStream_t st) {
+  const uint32_t per_block = 256 / G;
+  const uint32_t blocks = (uint32_t)std::min<uint64_t>((a.M + per_block - 1) / per_block, 65535);
+  hipLaunchKernelGGL((pw_narrow_kernel<DTA, DTW, G>), dim3(blocks), dim3(256), a.KG * 4 * sizeof(f32x4), st, a);
+  return hipGetLastError();
+}
+
 template <int DTA, int DTW>
 hipError_t launch_inst(const PwNarrowArgs &a, hipStream_t st) {
-  const uint32_t blocks = (uint32_t)std::min<uint64_t>((a.M + 255) / 256, 4096);
-  hipLaunchKernelGGL((pw_narrow_kernel<DTA, DTW>), dim3(blocks), dim3(256), a.KG * 4 * sizeof(f32x4), st, a);
-  return hipGetLastError();
+  const uint32_t g = pw_narrow_group(a.KG);
+  if (g == 16) return launch_g<DTA, DTW, 16>(a, st);
+  if (g == 4) return launch_g<DTA, DTW, 4>(a, st);
+  return launch_g<DTA, DTW, 1>(a, st);
 }
 
 }  // namespace
