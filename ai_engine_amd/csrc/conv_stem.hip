@@ -11,8 +11,8 @@
 // or 16 MFMAs (fp32, K 2 each). A wavefront owns 32 output pixels at a time
 // (grid-stride over the blocks); the 9 input pixels of a lane are 9 vector
 // loads of its image row neighbourhood (cached); the weights sit in registers
-// for the whole launch. The epilogue is act(acc + bias) (+ residual) in the
-// MFMA layout, stored as one vector of 4 channels per lane and group.
+// for the whole launch. The epilogue is act(acc + bias) in the MFMA layout,
+// then through LDS rows (+ residual) to stores of whole pixel rows.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -29,10 +29,16 @@ __device__ __forceinline__ uint32_t h16(u32x2 v, int c) {
 }
 __device__ __forceinline__ uint32_t pk(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
 
+// Output staging rows: 32 pixels x 32 fp32 channels per wavefront, pitch 4
+// floats wider than the row so the MFMA-layout writes spread over the banks.
+constexpr uint32_t kStPitch = 36;
+
 template <int DT, int NOB>
 __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
   constexpr bool F32 = DT == DT_F32;
+  __shared__ float stg[4][32 * kStPitch];
   const int lane = threadIdx.x & 63, l32 = lane & 31, lh = lane >> 5;
+  float *rows = stg[threadIdx.x >> 6];
   const uint32_t NG = a.CO / 4;
 
   // ---- weights of output channel row ob*32 + l32, in K order tap*3 + ic ----
@@ -133,18 +139,30 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
         }
       }
     }
-    if (!valid) continue;
-    // lane: pixel p, channels ob*32 + 8q + 4lh + (0..3) in acc[ob][4q..4q+3]
+    // lane: pixel p, channels ob*32 + 8q + 4lh + (0..3) in acc[ob][4q..4q+3];
+    // act(acc + bias) goes through the wavefront's LDS rows so each store
+    // instruction writes 8 whole pixel rows of the block (contiguous)
 #pragma unroll
-    for (int ob = 0; ob < NOB; ++ob)
+    for (int ob = 0; ob < NOB; ++ob) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        f32x4 o = f32x4{acc[ob][4 * q], acc[ob][4 * q + 1], acc[ob][4 * q + 2], acc[ob][4 * q + 3]} + bias[ob][q];
-        o = act4(actp, o);
-        const size_t vi = (size_t)p * NG + (ob * 32 + 8 * q + 4 * lh) / 4;
-        if (a.has_res) o += Vec4IO<DT>::load(a.res, vi);
-        Vec4IO<DT>::store(a.y, vi, o);
+        const f32x4 o = f32x4{acc[ob][4 * q], acc[ob][4 * q + 1], acc[ob][4 * q + 2], acc[ob][4 * q + 3]} + bias[ob][q];
+        *reinterpret_cast<f32x4 *>(rows + l32 * kStPitch + 8 * q + 4 * lh) = act4(actp, o);
       }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t px = 8 * i + (lane >> 3), pc = 4 * (lane & 7);
+        const uint32_t m = blk * 32 + px;
+        f32x4 o = *reinterpret_cast<const f32x4 *>(rows + px * kStPitch + pc);
+        if (m < a.M) {
+          const size_t vi = (size_t)m * NG + (ob * 32 + pc) / 4;
+          if (a.has_res) o += Vec4IO<DT>::load(a.res, vi);
+          Vec4IO<DT>::store(a.y, vi, o);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
   }
 }
 
