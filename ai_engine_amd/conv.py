@@ -150,7 +150,7 @@ EXPORTS = (
     "aih_conv_workspace_size", "aih_nhwc_c4_bytes", "aih_pack_nhwc", "aih_unpack_nhwc",
     "aih_pack_weights_conv", "aih_pack_weights_dw", "aih_pack_bias", "aih_pack_nhwc_device",
     "aih_ir_block_plan", "aih_ir_block", "aih_last_error", "aih_version", "aih_conv_check", "aih_conv_plan",
-    "aih_conv_noalloc",
+    "aih_conv_noalloc", "aih_conv_stem_f32in",
 )
 
 _lib = None
@@ -182,6 +182,7 @@ def lib() -> C.CDLL:
         "aih_pack_weights_dw": (C.c_int, [P, u32, u32, u32, i32, P]),
         "aih_pack_bias": (C.c_int, [P, u32, i32, P]),
         "aih_pack_nhwc_device": (C.c_int, [P, u32, u32, u32, u32, i32, P, P]),
+        "aih_conv_stem_f32in": (C.c_int, [C.POINTER(_IgemmDesc), P, P, P, P, P, P]),
         "aih_ir_block_plan": (C.c_int, [C.POINTER(_IrDesc), C.POINTER(IrPlan)]),
         "aih_ir_block": (C.c_int, [C.POINTER(_IrDesc), P, P, P, P, P, P, P, P, P, P]),
         "aih_last_error": (C.c_char_p, []),
@@ -335,6 +336,13 @@ class ConvIgemmSpec:
         arr = (C.c_void_p * 3)(*[_ptr(t) for t in inputs])
         _check(lib().aih_conv_igemm(C.byref(d), arr, _ptr(w), _ptr(bias), _ptr(res), _ptr(y), _ptr(ws),
                                     p.ws_bytes if ws is not None else 0, _stream(stream)))
+        return y
+
+    def run_f32_input(self, x, w, bias, res, y, stream=None):
+        """The stem route from a logical NHWC fp32 input (aih_conv_stem_f32in):
+        equal to pack_nhwc_device followed by run(), without the packed copy."""
+        _check(lib().aih_conv_stem_f32in(C.byref(self.desc()), _ptr(x), _ptr(w), _ptr(bias), _ptr(res), _ptr(y),
+                                         _stream(stream)))
         return y
 
 

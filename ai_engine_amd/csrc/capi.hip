@@ -448,6 +448,29 @@ int check_igemm(const aih_igemm_desc *d) {
   return AIH_OK;
 }
 
+// The stem kernel's arguments for a stem-route descriptor (buffers unset).
+int stem_args(const aih_igemm_desc *d, uint32_t oh, uint32_t ow, aih::StemArgs *sa) {
+  const uint64_t M = (uint64_t)d->n * oh * ow;
+  if (M > 0xffffff00ull) return fail("igemm: too many output pixels");
+  std::memset(sa, 0, sizeof(*sa));
+  sa->IH = d->ih;
+  sa->IW = d->iw;
+  sa->OHW = oh * ow;
+  sa->OW = ow;
+  sa->S = d->s;
+  sa->PT = (int32_t)d->pad[0];
+  sa->PL = (int32_t)d->pad[1];
+  sa->CO = d->cout;
+  sa->KGP = 4;
+  sa->M = (uint32_t)M;
+  sa->nblocks = (uint32_t)((M + 31) / 32);
+  sa->act = d->act;
+  sa->has_res = d->residual ? 1 : 0;
+  sa->fd_ohw = aih::make_fastdiv(oh * ow);
+  sa->fd_ow = aih::make_fastdiv(ow);
+  return AIH_OK;
+}
+
 // The stem route: <= 3 input channels of a dense input, 3x3, 32 or 64 outputs.
 bool igemm_is_stem(const aih_igemm_desc *d) {
   const bool dense_in = d->nsrcs == 0 || (d->nsrcs == 1 && d->srcs[0].c_off == 0 && d->srcs[0].stride_c == 4);
@@ -775,30 +798,13 @@ int aih_conv_igemm(const aih_igemm_desc *d, const void *const *inputs, const voi
     if (igemm_is_stem(d)) {
       // the stem: <= 3 input channels, every (tap, channel) gathered into one
       // 32-deep MFMA operand
-      const uint64_t M = (uint64_t)d->n * oh * ow;
-      if (M > 0xffffff00ull) return fail("igemm: too many output pixels");
       aih::StemArgs sa;
-      std::memset(&sa, 0, sizeof(sa));
+      if (stem_args(d, oh, ow, &sa)) return AIH_ERR;
       sa.x = inputs[0];
       sa.w = w;
       sa.bias = bias;
       sa.res = res;
       sa.y = y;
-      sa.IH = d->ih;
-      sa.IW = d->iw;
-      sa.OHW = oh * ow;
-      sa.OW = ow;
-      sa.S = d->s;
-      sa.PT = (int32_t)d->pad[0];
-      sa.PL = (int32_t)d->pad[1];
-      sa.CO = d->cout;
-      sa.KGP = 4;
-      sa.M = (uint32_t)M;
-      sa.nblocks = (uint32_t)((M + 31) / 32);
-      sa.act = d->act;
-      sa.has_res = d->residual ? 1 : 0;
-      sa.fd_ohw = aih::make_fastdiv(oh * ow);
-      sa.fd_ow = aih::make_fastdiv(ow);
       const hipError_t e = aih::launch_conv_stem(sa, d->dt, static_cast<hipStream_t>(stream));
       return e == hipSuccess ? AIH_OK : fail(std::string("conv stem launch: ") + hipGetErrorString(e));
     }
@@ -1283,6 +1289,35 @@ int aih_pack_nhwc_device(const float *x, uint32_t n, uint32_t h, uint32_t w, uin
     hipError_t e = aih::launch_pack_nhwc(x, (uint64_t)n * h * w, c, dt, y, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(std::string("pack_nhwc launch: ") + hipGetErrorString(e));
     return AIH_OK;
+  });
+}
+
+int aih_conv_stem_f32in(const aih_igemm_desc *d, const float *x, const void *w, const void *bias,
+                        const void *res, void *y, aih_stream stream) {
+  return guarded([&] {
+    if (check_igemm(d)) return AIH_ERR;
+    if (!igemm_is_stem(d) || d->nsrcs != 0)
+      return fail("stem_f32in: the descriptor is not on the stem route (k 3, d 1, cin <= 3, cout 32 / 64, "
+                  "one dense input, AUTO, splitk 0, dt == wdt)");
+    if (!x || !w || !bias || !y) return fail("stem_f32in: null buffer");
+    if ((d->residual != 0) != (res != nullptr)) return fail("stem_f32in: res must be given iff residual");
+    if (!aligned(x, 4) || !aligned(w, 16) || !aligned(y, 16) || !aligned(bias, 8) || (res && !aligned(res, 16)))
+      return fail("stem_f32in: misaligned buffer (x needs 4 bytes, w, y, res 16, bias 8)");
+    const uint64_t xb = (uint64_t)d->n * d->ih * d->iw * d->cin * 4;
+    if (xb >= 0x80000000ull) return fail("stem_f32in: input of 2 GiB or more");
+    uint32_t oh, ow;
+    if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
+    aih::StemArgs sa;
+    if (stem_args(d, oh, ow, &sa)) return AIH_ERR;
+    sa.x = x;
+    sa.cin_f32 = d->cin;
+    sa.x_bytes = (uint32_t)xb;
+    sa.w = w;
+    sa.bias = bias;
+    sa.res = res;
+    sa.y = y;
+    const hipError_t e = aih::launch_conv_stem(sa, d->dt, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? AIH_OK : fail(std::string("conv stem launch: ") + hipGetErrorString(e));
   });
 }
 

@@ -20,6 +20,9 @@ struct StemArgs {
   uint32_t M, nblocks;  // output pixels over the batch, 32-pixel blocks
   int32_t act, has_res;
   FastDiv fd_ohw, fd_ow;
+  uint32_t cin_f32;  // 0: x is NHWC-C4 in the dtype; 1..3: x is logical NHWC fp32 with
+                     // that many channels per pixel, rounded to the dtype as it is read
+  uint32_t x_bytes;  // bytes of x when cin_f32 != 0 (< 2 GiB)
 };
 
 hipError_t launch_conv_stem(const StemArgs &a, int dt, hipStream_t st);

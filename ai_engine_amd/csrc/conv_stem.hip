@@ -33,7 +33,11 @@ __device__ __forceinline__ uint32_t pk(uint32_t lo, uint32_t hi) { return lo | (
 // floats wider than the row so the MFMA-layout writes spread over the banks.
 constexpr uint32_t kStPitch = 36;
 
-template <int DT, int NOB>
+// F32IN: the input is the model's logical NHWC fp32 image (cin_f32 channels
+// per pixel, no padding), each pixel read as one 12-byte (or narrower) load
+// and rounded to the storage dtype exactly as pack_nhwc rounds it, so the
+// result equals pack-then-stem bit for bit without the packed copy.
+template <int DT, int NOB, bool F32IN>
 __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
   constexpr bool F32 = DT == DT_F32;
   __shared__ float stg[4][32 * kStPitch];
@@ -75,6 +79,9 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) bias[ob][q] = Vec4IO<DT>::load(a.bias, (ob * 32 + 8 * q + 4 * lh) / 4);
   const Act actp = act_params(a.act);
+  // fp32 input: the whole image batch as one buffer (the host keeps it below 2 GiB)
+  const __amdgpu_buffer_rsrc_t rs_x =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), 0, (int)a.x_bytes, 0x00020000);
 
   const uint32_t waves = gridDim.x * 4;
   for (uint32_t blk = blockIdx.x * 4 + (threadIdx.x >> 6); blk < a.nblocks; blk += waves) {
@@ -95,7 +102,21 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
       const int32_t iy = iy0 + t / 3, ix = ix0 + t % 3;
       const bool in = valid && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
       const size_t vi = ibase + (size_t)(in ? iy : 0) * a.IW + (in ? ix : 0);
-      if constexpr (F32) {
+      if constexpr (F32IN) {
+        f32x4 v = {};
+        if (a.cin_f32 == 3) {
+          // one 12-byte buffer load; taps outside the image read zeros
+          typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+          const u32x3 t3 = __builtin_amdgcn_raw_buffer_load_b96(rs_x, in ? (uint32_t)vi * 12u : 0x80000000u, 0, 0);
+          v = f32x4{__uint_as_float(t3.x), __uint_as_float(t3.y), __uint_as_float(t3.z), 0.0f};
+        } else if (in) {
+          const float *xp = reinterpret_cast<const float *>(a.x) + vi * a.cin_f32;
+          v.x = xp[0];
+          if (a.cin_f32 > 1) v.y = xp[1];
+        }
+        if constexpr (F32) tf[t] = v;
+        else th[t] = pack4<DT>(v);
+      } else if constexpr (F32) {
         tf[t] = in ? reinterpret_cast<const f32x4 *>(a.x)[vi] : f32x4{};
       } else {
         th[t] = in ? reinterpret_cast<const u32x2 *>(a.x)[vi] : u32x2{0u, 0u};
@@ -166,11 +187,27 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
   }
 }
 
+// Grid-stride launch of one instantiation: as many workgroups as the CUs
+// hold at once (registers and LDS), so every workgroup starts in the first
+// round and they all walk the blocks in step.
+template <int DT, int NOB, bool F32IN>
+hipError_t launch_one(const StemArgs &a, hipStream_t st) {
+  static int per_cu = -1;
+  if (per_cu < 0) {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, conv_stem_kernel<DT, NOB, F32IN>, 256, 0) != hipSuccess ||
+        v < 1)
+      v = 1;
+    per_cu = v;
+  }
+  const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblocks + 3) / 4, (uint64_t)device_cus() * per_cu);
+  hipLaunchKernelGGL((conv_stem_kernel<DT, NOB, F32IN>), dim3(wgs), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
 template <int DT, int NOB>
 hipError_t launch_inst(const StemArgs &a, hipStream_t st) {
-  const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblocks + 3) / 4, device_cus() * 8u);
-  hipLaunchKernelGGL((conv_stem_kernel<DT, NOB>), dim3(wgs), dim3(256), 0, st, a);
-  return hipGetLastError();
+  return a.cin_f32 ? launch_one<DT, NOB, true>(a, st) : launch_one<DT, NOB, false>(a, st);
 }
 
 template <int DT>
@@ -185,6 +222,7 @@ hipError_t launch_dt(const StemArgs &a, hipStream_t st) {
 }  // namespace
 
 hipError_t launch_conv_stem(const StemArgs &a, int dt, hipStream_t st) {
+  if (a.cin_f32 > 3) return hipErrorInvalidValue;
   switch (dt) {
     case DT_F32: return launch_dt<DT_F32>(a, st);
     case DT_F16: return launch_dt<DT_F16>(a, st);

@@ -152,6 +152,10 @@ class Model:
                 continue
             self.ops.append(self._conv_op(layers[i], packed, L))
             i += 1
+        # a stem that is the input's only reader reads the fp32 input itself
+        self._x_f32 = None        # the uploaded fp32 input, held until the next upload
+        self._input_packed = True  # tensors["input"] holds the last upload
+        self._stem_in = self._stem_input_op(layers, readers, packed, L)
 
     # ------------------------------------------------------------ graph building
 
@@ -325,22 +329,76 @@ class Model:
                 ws.data_ptr() if ws is not None else None, nb)
         return ModelOp(Lr.name, "conv", [Lr], L.aih_conv, args, op, [desc, wd, bd, ws])
 
+    def _stem_input_op(self, layers, readers, packed, L) -> ModelOp | None:
+        """The first op as a stem launch on the logical NHWC fp32 input
+        (aih_conv_stem_f32in): the pack of upload_input and the stem in one
+        kernel, bit for bit the same result. Only for a first layer on the
+        stem route whose input nothing else reads."""
+        if not self.ops or self.ops[0].kind != "conv":
+            return None
+        Lr = layers[0]
+        if (Lr.src != "input" or readers.get("input", 0) != 1 or Lr.depthwise or Lr.groups != 1 or Lr.k != 3
+                or Lr.cin > 3 or Lr.cout not in (32, 64) or self.wdt != self.dt):
+            return None
+        spec = conv.ConvIgemmSpec(ih=Lr.ih, iw=Lr.iw, cin=Lr.cin, cout=Lr.cout, k=3, s=Lr.s, pad=(Lr.pad,) * 4,
+                                  act=ACT[Lr.act], residual=Lr.res is not None, dt=self.dt, wdt=self.wdt, n=self.n)
+        desc = spec.desc()
+        wd, bd = packed[Lr.name]
+        res = self.tensors[Lr.res] if Lr.res else None
+        y = self.tensors[Lr.name]
+        args = (C.byref(desc), None, wd.data_ptr(), bd.data_ptr(), res.data_ptr() if res is not None else None,
+                y.data_ptr())
+        return ModelOp(Lr.name, "conv", [Lr], L.aih_conv_stem_f32in, args, spec, [desc, wd, bd])
+
     def _alloc(self, h: int, w: int, c: int) -> torch.Tensor:
         return torch.empty(self.n * h * w * (-(-c // 4)) * 4, dtype=_storage_torch(self.dt), device=self.device)
 
     # ------------------------------------------------------------ runtime verbs
 
     def upload_input(self, x_nhwc_f32: torch.Tensor, stream=None):
-        conv.pack_nhwc_device(x_nhwc_f32, self.n, self.ih, self.iw, self.cin, self.dt, self.tensors["input"], stream)
+        """The next infer()'s input. With a stem as the first op the fp32
+        tensor itself is the stem's input (no packed copy; the model holds
+        it until the next upload, and it must not change before infer()
+        has run); otherwise it is packed into the input slot now."""
+        if self._stem_in is None:
+            conv.pack_nhwc_device(x_nhwc_f32, self.n, self.ih, self.iw, self.cin, self.dt, self.tensors["input"],
+                                  stream)
+            return
+        x = x_nhwc_f32
+        if (not isinstance(x, torch.Tensor) or x.device != self.device or x.dtype != torch.float32
+                or not x.is_contiguous() or x.numel() != self.n * self.ih * self.iw * self.cin):
+            raise conv.AihError(f"upload_input: expected a contiguous float32 tensor of "
+                                f"{self.n * self.ih * self.iw * self.cin} values on {self.device}")
+        self._x_f32 = x
+        self._input_packed = False
+        a = self._stem_in.args
+        self._stem_in.args = (a[0], x.data_ptr()) + a[2:]
+
+    def sync_input(self):
+        """Fills tensors["input"] with the last upload when the stem read the
+        fp32 tensor directly (for inspecting the stored input; later infer()
+        calls then read the slot)."""
+        if not self._input_packed:
+            conv.pack_nhwc_device(self._x_f32, self.n, self.ih, self.iw, self.cin, self.dt, self.tensors["input"])
+            torch.cuda.synchronize(self.device)
+            self._input_packed = True
+
+    def _op(self, i: int) -> ModelOp:
+        # op 0 reads the fp32 upload while it has not been packed into the
+        # input slot; otherwise (no upload yet, or the slot written) the slot
+        if i == 0 and self._stem_in is not None and not self._input_packed:
+            return self._stem_in
+        return self.ops[i]
 
     def infer(self, stream=None):
         s = conv._stream(stream)
-        for op in self.ops:
+        for i in range(len(self.ops)):
+            op = self._op(i)
             if op.fn(*op.args, s) != 0:
                 raise conv.AihError(f"{op.name}: {conv.last_error()}")
 
     def launch_op(self, i: int, stream=None):
-        op = self.ops[i]
+        op = self._op(i)
         if op.fn(*op.args, conv._stream(stream)) != 0:
             raise conv.AihError(f"{op.name}: {conv.last_error()}")
 
@@ -348,6 +406,8 @@ class Model:
         """Unpacked logical NHWC fp32 of a tensor (default: the graph output)."""
         name = name or self.output
         h, w, c = self.shapes[name]
+        if name == "input":
+            self.sync_input()
         a = self.tensors[name].detach().cpu().numpy()
         if a.dtype == np.int16:
             a = a.view(np.uint16)

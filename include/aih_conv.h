@@ -300,6 +300,18 @@ int aih_pack_bias(const float *b, uint32_t cout, int32_t dt, void *out);
 int aih_pack_nhwc_device(const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
                          int32_t dt, void *y, aih_stream stream);
 
+/* The stem conv straight from the model's input: x is logical NHWC fp32
+ * (n*ih*iw*cin floats, the layout Model::upload_input takes,
+ * crates/ai-gpu-runtime/src/model.rs:387-399), rounded to d->dt as it is
+ * read, so y equals aih_pack_nhwc_device into NHWC-C4 followed by
+ * aih_conv_igemm bit for bit, without the packed copy. It replaces that
+ * pair -- the runtime's input pack and the first Conv's dispatch
+ * (lowering.rs:122-168) -- for a descriptor on the stem route (k = 3,
+ * d = 1, cin <= 3, cout 32 or 64, one dense input, AIH_VAR_AUTO, splitk 0,
+ * dt == wdt); x must stay below 2 GiB and 4-byte aligned. */
+int aih_conv_stem_f32in(const aih_igemm_desc *d, const float *x, const void *w, const void *bias,
+                        const void *res, void *y, aih_stream stream);
+
 /* ---- errors / info ---- */
 const char *aih_last_error(void);
 const char *aih_version(void);

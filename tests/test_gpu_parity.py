@@ -420,3 +420,29 @@ def test_stem_kernel(case, dt):
     (ih, iw, cin, cout, s, pad), act, with_res, seed, n = case
     res = G.run_igemm(ih, iw, cin, cout, 3, s, pad, act, with_res, dt, seed, n=n)
     check(f"stem dt{dt} {case}", res, dt)
+
+
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("case", STEM, ids=str)
+def test_stem_from_f32_input_equals_pack_then_stem(case, dt):
+    """aih_conv_stem_f32in reads the logical NHWC fp32 input and rounds it
+    to dt as it loads: its output equals aih_pack_nhwc_device followed by
+    aih_conv_igemm bit for bit (the same stored input, the same kernel)."""
+    (ih, iw, cin, cout, s, pad), act, with_res, seed, n = case
+    spec = G.conv.ConvIgemmSpec(ih=ih, iw=iw, cin=cin, cout=cout, k=3, s=s, pad=pad, act=G.ACT[act],
+                                residual=with_res, dt=G.conv.DType(dt), n=n)
+    oh, ow = spec.out_hw()
+    x, wts, b, r = G.stream(seed, n * ih * iw * cin, cout * cin * 9, cout, n * oh * ow * cout if with_res else 0)
+    xf = G.dev(np.asarray(x, np.float32))
+    wp, _ = G.orc.pack_weights_conv(wts, cout, cin, 3, 3, 4, dt)
+    wd, bd = G.dev(wp), G.dev(G.orc.pack_bias(b, cout, dt))
+    rd = G.dev(G.orc.pack_nhwc(r, n, oh, ow, cout, dt)) if with_res else None
+    n4 = -(-cout // 4) * 4
+    xp = G.poisoned(n * ih * iw * 4, dt)
+    G.conv.pack_nhwc_device(xf, n, ih, iw, cin, G.conv.DType(dt), xp)
+    want = G.poisoned(n * oh * ow * n4, dt)
+    spec.run([xp], wd, bd, rd, want)
+    got = G.poisoned(n * oh * ow * n4, dt)
+    spec.run_f32_input(xf, wd, bd, rd, got)
+    G.torch.cuda.synchronize()
+    assert G.torch.equal(got.view(-1), want.view(-1))

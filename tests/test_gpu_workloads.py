@@ -346,6 +346,8 @@ BAR_STORED = {F32: 1e-4, F16: 2e-3, BF16: 8e-3}
 
 def image_of(m, name, i, dt):
     """Image i of model tensor `name` as the GPU stores it, unpacked to logical NHWC fp32."""
+    if name == "input":
+        m.sync_input()  # the stem may have read the fp32 upload directly
     h, w, c = m.shapes[name]
     t = m.tensors[name].view(m.n, -1)[i]
     return orc.unpack_nhwc(G.host(t, dt), 1, h, w, c, dt)
