@@ -646,10 +646,14 @@ int aih_conv_pw_plan(const aih_pw_desc *d, aih_plan *out) {
         *out = aih_plan{AIH_VAR_TILE, 1, aih::pw_stream_bm(sh), aih::pw_stream_bn(sh), a.mtiles * a.ntiles, 0};
         return AIH_OK;
       }
-      case PW_DIRECT:
-        *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->ng * 4 <= 32 ? 32u : 64u,
-                        aih::pw_direct_grid((uint32_t)((M + 31) / 32), aih::device_cus()), 0};
+      case PW_DIRECT: {
+        aih::PwDirectArgs da{nullptr, nullptr, nullptr, nullptr, nullptr, (uint32_t)M, d->kg, d->ng * 4,
+                             (uint32_t)((M + 31) / 32), d->act, d->residual ? 1 : 0};
+        uint32_t grid = 0;
+        if (aih::launch_pw_direct(da, d->dt, nullptr, &grid) != hipSuccess) return fail("pw: no direct instantiation");
+        *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->ng * 4 <= 32 ? 32u : 64u, grid, 0};
         return AIH_OK;
+      }
       default:
         break;
     }
@@ -764,8 +768,11 @@ int aih_conv_igemm_plan(const aih_igemm_desc *d, aih_plan *out) {
     if (igemm_out_hw(d, &oh, &ow)) return AIH_ERR;
     if (igemm_is_stem(d)) {
       // the stem kernel: 32 pixels per wavefront, 4 wavefronts per workgroup
-      const uint64_t nblocks = ((uint64_t)d->n * oh * ow + 31) / 32;
-      *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->cout, (uint32_t)std::min<uint64_t>((nblocks + 3) / 4, aih::device_cus() * 8u), 0};
+      aih::StemArgs sa;
+      if (stem_args(d, oh, ow, &sa)) return AIH_ERR;
+      uint32_t grid = 0;
+      if (aih::launch_conv_stem(sa, d->dt, nullptr, &grid) != hipSuccess) return fail("igemm: no stem instantiation");
+      *out = aih_plan{AIH_VAR_DIRECT, 1, 32, d->cout, grid, 0};
       return AIH_OK;
     }
     aih::IgDirectArgs da;

@@ -27,12 +27,8 @@ constexpr uint32_t kPwDirectMaxK16 = 128, kPwDirectMaxK32 = 64, kPwDirectMaxN4 =
 // workgroup, so every CU gets work; otherwise four wavefronts per
 // workgroup, at most 8 workgroups per CU, blocks taken grid-stride.
 inline uint32_t pw_direct_waves_per_group(uint32_t nblk, uint32_t cus) { return nblk < 4u * cus ? 1u : 4u; }
-inline uint32_t pw_direct_grid(uint32_t nblk, uint32_t cus) {
-  if (pw_direct_waves_per_group(nblk, cus) == 1) return nblk;
-  const uint64_t wgs = ((uint64_t)nblk + 3) / 4;
-  return (uint32_t)(wgs < (uint64_t)cus * 8u ? wgs : (uint64_t)cus * 8u);
-}
 
-hipError_t launch_pw_direct(const PwDirectArgs &a, int dt, hipStream_t st);
+// grid_out non-null: only the launch's workgroup count is computed (plans).
+hipError_t launch_pw_direct(const PwDirectArgs &a, int dt, hipStream_t st, uint32_t *grid_out = nullptr);
 
 }  // namespace aih

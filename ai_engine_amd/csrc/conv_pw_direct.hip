@@ -126,10 +126,32 @@ __global__ __launch_bounds__(64 * WPG) void pw_direct_kernel(PwDirectArgs a) {
   }
 }
 
+// Launch (or, with grid_out, only size) one instantiation. Small launches
+// take one wavefront per block; larger ones are grid-stride with 4
+// wavefronts per workgroup and as many workgroups as the CUs hold at once
+// (the instantiation's occupancy), so none waits for a second round.
 template <int DT, int KS, int NOB>
-hipError_t launch_inst(const PwDirectArgs &a, hipStream_t st) {
-  const uint32_t cus = device_cus(), grid = pw_direct_grid(a.nblk, cus);
-  if (pw_direct_waves_per_group(a.nblk, cus) == 1)
+hipError_t launch_inst(const PwDirectArgs &a, hipStream_t st, uint32_t *grid_out) {
+  const uint32_t cus = device_cus();
+  const bool one = pw_direct_waves_per_group(a.nblk, cus) == 1;
+  uint32_t grid = a.nblk;
+  if (!one) {
+    static int per_cu = -1;
+    if (per_cu < 0) {
+      int v = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, pw_direct_kernel<DT, KS, NOB, 4>, 256, 0) != hipSuccess ||
+          v < 1)
+        v = 8;  // no device to ask: eight workgroups per CU
+      per_cu = v;
+    }
+    const uint64_t wgs = ((uint64_t)a.nblk + 3) / 4, cap = (uint64_t)cus * per_cu;
+    grid = (uint32_t)(wgs < cap ? wgs : cap);
+  }
+  if (grid_out) {
+    *grid_out = grid;
+    return hipSuccess;
+  }
+  if (one)
     hipLaunchKernelGGL((pw_direct_kernel<DT, KS, NOB, 1>), dim3(grid), dim3(64), 0, st, a);
   else
     hipLaunchKernelGGL((pw_direct_kernel<DT, KS, NOB, 4>), dim3(grid), dim3(256), 0, st, a);
@@ -137,28 +159,28 @@ hipError_t launch_inst(const PwDirectArgs &a, hipStream_t st) {
 }
 
 template <int DT, int KS>
-hipError_t launch_ks(const PwDirectArgs &a, hipStream_t st) {
-  return a.N4 <= 32 ? launch_inst<DT, KS, 1>(a, st) : launch_inst<DT, KS, 2>(a, st);
+hipError_t launch_ks(const PwDirectArgs &a, hipStream_t st, uint32_t *grid_out) {
+  return a.N4 <= 32 ? launch_inst<DT, KS, 1>(a, st, grid_out) : launch_inst<DT, KS, 2>(a, st, grid_out);
 }
 
 template <int DT>
-hipError_t launch_dt(const PwDirectArgs &a, hipStream_t st) {
+hipError_t launch_dt(const PwDirectArgs &a, hipStream_t st, uint32_t *grid_out) {
   // K steps: fp32 8 channels, 16-bit 16 channels
   const uint32_t ks = DT == DT_F32 ? (a.KG + 1) / 2 : (a.KG + 3) / 4;
-  if (ks <= 2) return launch_ks<DT, 2>(a, st);
-  if (ks <= 4) return launch_ks<DT, 4>(a, st);
-  if (ks <= 8) return launch_ks<DT, 8>(a, st);
+  if (ks <= 2) return launch_ks<DT, 2>(a, st, grid_out);
+  if (ks <= 4) return launch_ks<DT, 4>(a, st, grid_out);
+  if (ks <= 8) return launch_ks<DT, 8>(a, st, grid_out);
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-hipError_t launch_pw_direct(const PwDirectArgs &a, int dt, hipStream_t st) {
+hipError_t launch_pw_direct(const PwDirectArgs &a, int dt, hipStream_t st, uint32_t *grid_out) {
   if (a.N4 > kPwDirectMaxN4 || a.N4 % 4) return hipErrorInvalidValue;
   switch (dt) {
-    case DT_F32: return launch_dt<DT_F32>(a, st);
-    case DT_F16: return launch_dt<DT_F16>(a, st);
-    case DT_BF16: return launch_dt<DT_BF16>(a, st);
+    case DT_F32: return launch_dt<DT_F32>(a, st, grid_out);
+    case DT_F16: return launch_dt<DT_F16>(a, st, grid_out);
+    case DT_BF16: return launch_dt<DT_BF16>(a, st, grid_out);
     default: return hipErrorInvalidValue;
   }
 }

@@ -25,6 +25,7 @@ struct StemArgs {
   uint32_t x_bytes;  // bytes of x when cin_f32 != 0 (< 2 GiB)
 };
 
-hipError_t launch_conv_stem(const StemArgs &a, int dt, hipStream_t st);
+// grid_out non-null: only the launch's workgroup count is computed (plans).
+hipError_t launch_conv_stem(const StemArgs &a, int dt, hipStream_t st, uint32_t *grid_out = nullptr);
 
 }  // namespace aih

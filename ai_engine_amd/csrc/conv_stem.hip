@@ -191,42 +191,46 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
 // hold at once (registers and LDS), so every workgroup starts in the first
 // round and they all walk the blocks in step.
 template <int DT, int NOB, bool F32IN>
-hipError_t launch_one(const StemArgs &a, hipStream_t st) {
+hipError_t launch_one(const StemArgs &a, hipStream_t st, uint32_t *grid_out) {
   static int per_cu = -1;
   if (per_cu < 0) {
     int v = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, conv_stem_kernel<DT, NOB, F32IN>, 256, 0) != hipSuccess ||
         v < 1)
-      v = 1;
+      v = 8;  // no device to ask: eight workgroups per CU
     per_cu = v;
   }
   const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblocks + 3) / 4, (uint64_t)device_cus() * per_cu);
+  if (grid_out) {
+    *grid_out = wgs;
+    return hipSuccess;
+  }
   hipLaunchKernelGGL((conv_stem_kernel<DT, NOB, F32IN>), dim3(wgs), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
 template <int DT, int NOB>
-hipError_t launch_inst(const StemArgs &a, hipStream_t st) {
-  return a.cin_f32 ? launch_one<DT, NOB, true>(a, st) : launch_one<DT, NOB, false>(a, st);
+hipError_t launch_inst(const StemArgs &a, hipStream_t st, uint32_t *grid_out) {
+  return a.cin_f32 ? launch_one<DT, NOB, true>(a, st, grid_out) : launch_one<DT, NOB, false>(a, st, grid_out);
 }
 
 template <int DT>
-hipError_t launch_dt(const StemArgs &a, hipStream_t st) {
+hipError_t launch_dt(const StemArgs &a, hipStream_t st, uint32_t *grid_out) {
   switch (a.CO / 32) {
-    case 1: return launch_inst<DT, 1>(a, st);
-    case 2: return launch_inst<DT, 2>(a, st);
+    case 1: return launch_inst<DT, 1>(a, st, grid_out);
+    case 2: return launch_inst<DT, 2>(a, st, grid_out);
     default: return hipErrorInvalidValue;
   }
 }
 
 }  // namespace
 
-hipError_t launch_conv_stem(const StemArgs &a, int dt, hipStream_t st) {
+hipError_t launch_conv_stem(const StemArgs &a, int dt, hipStream_t st, uint32_t *grid_out) {
   if (a.cin_f32 > 3) return hipErrorInvalidValue;
   switch (dt) {
-    case DT_F32: return launch_dt<DT_F32>(a, st);
-    case DT_F16: return launch_dt<DT_F16>(a, st);
-    case DT_BF16: return launch_dt<DT_BF16>(a, st);
+    case DT_F32: return launch_dt<DT_F32>(a, st, grid_out);
+    case DT_F16: return launch_dt<DT_F16>(a, st, grid_out);
+    case DT_BF16: return launch_dt<DT_BF16>(a, st, grid_out);
     default: return hipErrorInvalidValue;
   }
 }
