@@ -224,7 +224,7 @@ def main() -> int:
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": args.dtype, "data": "synthetic",
         "config": {"workload": meta["name"], "batch": n, "height": H, "width": Wd, "convs": len(layers),
-                   "storage": args.dtype, "accumulate": "f32", "step": "device pack + 32 convs"},
+                   "storage": args.dtype, "accumulate": "f32", "step": "32 convs from the resident fp32 NHWC input (the stem rounds it to the storage dtype as it reads)"},
         "gpu_ms_per_step": round(gpu_ms, 4),
         "step_stats": step_stats,
         "step_roofline": {"tflops": round(step_roof["tflops"], 2), "gbs": round(step_roof["gbs"], 1),
