@@ -20,7 +20,9 @@
 // the oldest buffer. Pixel rows sit in LDS as 4 16-byte units per pixel with
 // the unit index XORed by bits 1-2 of the pixel, so the MFMA operand reads
 // (8 pixels, one unit each, per LDS cycle) touch 8 distinct bank groups; the
-// DMA lanes still read each pixel's 64 bytes as one contiguous run.
+// DMA lanes still read each pixel's 64 bytes as one contiguous run. Weight
+// rows of odd kg hold column n at n ^ 4, so the lanes of the two lane halves
+// (kg 2q and 2q + 1 of the same columns) also fall in different banks.
 //
 // MFMA mapping (v_mfma_f32_32x32x2f32, operands swapped so the result is
 // channel-major): A = weights (32 channels x K), B = activations (K x 32
@@ -42,6 +44,13 @@ constexpr uint32_t kOob = 0x80000000u;  // a byte offset past both buffers
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ps_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
+
+// LDS slot of unit u of tile pixel p is 4p + (u ^ ps_swz(p)): bits 1 and 2
+// of p swapped into a 2-bit XOR. The 8 pixels an LDS cycle serves (8
+// consecutive lanes, one unit each) land in 8 distinct 16-byte bank groups,
+// and so do 4 consecutive lanes together with the 4 lanes 32 above them
+// (the same pixels, the neighbouring unit).
+__device__ __forceinline__ uint32_t ps_swz(uint32_t p) { return (((p >> 1) & 1) << 1) | ((p >> 2) & 1); }
 
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited for).
 template <int N>
@@ -106,7 +115,7 @@ __global__ __launch_bounds__(64 * WM * WN) void pw_stream_kernel(PwStreamArgs a)
     d_ok[k] = false;
     if (i < A_INS) {
       const uint32_t p = 16 * i + (lane >> 2);
-      const uint32_t u = (uint32_t)(lane & 3) ^ ((p >> 1) & 3);
+      const uint32_t u = (uint32_t)(lane & 3) ^ ps_swz(p);
       const uint32_t m = m0 + p;
       d_ok[k] = m < a.M;
       d_off[k] = (m * a.KG + u) * 16;
@@ -115,7 +124,7 @@ __global__ __launch_bounds__(64 * WM * WN) void pw_stream_kernel(PwStreamArgs a)
       ++nmine;
     } else if (i < NI) {
       const uint32_t e = 64 * (i - A_INS) + lane;
-      const uint32_t kgl = e / BN, n = e - kgl * BN;
+      const uint32_t kgl = e / BN, n = (e - kgl * BN) ^ (4 * (kgl & 1));
       d_ok[k] = n0 + n < a.N4;
       d_off[k] = (kgl * a.N4 + n0 + n) * 16;
       d_step[k] = 64 * a.N4;
@@ -144,9 +153,10 @@ __global__ __launch_bounds__(64 * WM * WN) void pw_stream_kernel(PwStreamArgs a)
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const uint32_t u = 2 * q + lh;
-    a_off[q] = (4 * p + (u ^ ((p >> 1) & 3))) * 16;
+    a_off[q] = (4 * p + (u ^ ps_swz(p))) * 16;
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) w_off[q][tn] = A_BYTES + (u * BN + 32 * TN * wn + 32 * tn + l32) * 16;
+    for (int tn = 0; tn < TN; ++tn)
+      w_off[q][tn] = A_BYTES + (u * BN + ((32 * TN * wn + 32 * tn + l32) ^ (4 * lh))) * 16;
   }
 
   f32x16 acc[TN];
