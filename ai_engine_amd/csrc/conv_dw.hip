@@ -173,13 +173,25 @@ __global__ __launch_bounds__(256) void conv_dw_strip_kernel(DwArgs a) {
   }
 }
 
-template <int DT, int CV, int K, int S>
-static hipError_t launch_strip(const DwArgs &a, hipStream_t st) {
-  constexpr int PX = 4;
+template <int DT, int CV, int K, int S, int PX>
+static hipError_t launch_strip_px(const DwArgs &a, hipStream_t st) {
   const uint64_t total = (uint64_t)a.N * a.OH * ((a.OW + PX - 1) / PX) * (a.CG * 4 / CV);
   const dim3 grid((unsigned)((total + 255) / 256));
   hipLaunchKernelGGL((conv_dw_strip_kernel<DT, CV, K, S, PX>), grid, dim3(256), 0, st, a);
   return hipGetLastError();
+}
+
+// Strips of 4 output pixels where that still gives every SIMD four
+// wavefronts (64 lanes x 4 x 4 SIMDs per CU); small late layers (10x18 or
+// 20x36 outputs) take strips of 2 or 1 pixels instead, so their launches fill
+// the GPU rather than leaving most CUs idle with long per-thread tap loops.
+template <int DT, int CV, int K, int S>
+static hipError_t launch_strip(const DwArgs &a, hipStream_t st) {
+  const uint64_t want = (uint64_t)device_cus() * 4 * 4 * 64;
+  const uint64_t per_px = (uint64_t)a.N * a.OH * (a.CG * 4 / CV);
+  if (per_px * ((a.OW + 3) / 4) >= want) return launch_strip_px<DT, CV, K, S, 4>(a, st);
+  if (per_px * ((a.OW + 1) / 2) >= want) return launch_strip_px<DT, CV, K, S, 2>(a, st);
+  return launch_strip_px<DT, CV, K, S, 1>(a, st);
 }
 
 template <int DT, int CV>
@@ -190,7 +202,11 @@ static hipError_t launch_strip_ks(const DwArgs &a, hipStream_t st) {
 
 hipError_t launch_conv_dw(const DwArgs &a, int dt, hipStream_t st) {
   if (a.D == 1 && (a.K == 3 || a.K == 5) && (a.S == 1 || a.S == 2)) {
-    const bool cv8 = a.CG % 2 == 0;  // two 4-channel groups per 16-byte vector
+    // two 4-channel groups per 16-byte vector, unless one-pixel strips of
+    // 8-channel vectors still leave the GPU short of threads (small late
+    // layers): then 4-channel vectors, twice the threads
+    const uint64_t one_px8 = (uint64_t)a.N * a.OH * a.OW * (a.CG / 2);
+    const bool cv8 = a.CG % 2 == 0 && one_px8 >= (uint64_t)device_cus() * 4 * 4 * 64;
     switch (dt) {
       case DT_F32: return launch_strip_ks<DT_F32, 4>(a, st);
       case DT_F16: return cv8 ? launch_strip_ks<DT_F16, 8>(a, st) : launch_strip_ks<DT_F16, 4>(a, st);
