@@ -136,6 +136,22 @@ class IrPlan(C.Structure):
                 f"occ={self.occupancy}, grid={self.grid}x{self.waves} waves{', deep' if self.deep else ''})")
 
 
+class _DwPwDesc(C.Structure):
+    _fields_ = [("n", C.c_uint32), ("ih", C.c_uint32), ("iw", C.c_uint32), ("c", C.c_uint32),
+                ("k", C.c_uint32), ("s", C.c_uint32), ("pad", C.c_uint32 * 4), ("cout", C.c_uint32),
+                ("kg_pad", C.c_uint32), ("act_dw", C.c_int32), ("act_pw", C.c_int32), ("residual", C.c_int32),
+                ("dt", C.c_int32), ("tile_h", C.c_uint32), ("tile_w", C.c_uint32)]
+
+
+class DwPwPlan(C.Structure):
+    _fields_ = [("th", C.c_uint32), ("tw", C.c_uint32), ("waves", C.c_uint32), ("chunks", C.c_uint32),
+                ("tiles", C.c_uint32), ("lds_bytes", C.c_uint32), ("occupancy", C.c_uint32), ("grid", C.c_uint32)]
+
+    def __repr__(self):
+        return (f"DwPwPlan(tile={self.th}x{self.tw}, waves={self.waves}, chunks={self.chunks}, "
+                f"tiles={self.tiles}, lds={self.lds_bytes}, occ={self.occupancy}, grid={self.grid})")
+
+
 class Plan(C.Structure):
     _fields_ = [("variant", C.c_int32), ("splitk", C.c_uint32), ("bm", C.c_uint32), ("bn", C.c_uint32),
                 ("grid", C.c_uint32), ("ws_bytes", C.c_size_t)]
@@ -150,7 +166,7 @@ EXPORTS = (
     "aih_conv_workspace_size", "aih_nhwc_c4_bytes", "aih_pack_nhwc", "aih_unpack_nhwc",
     "aih_pack_weights_conv", "aih_pack_weights_dw", "aih_pack_bias", "aih_pack_nhwc_device",
     "aih_ir_block_plan", "aih_ir_block", "aih_last_error", "aih_version", "aih_conv_check", "aih_conv_plan",
-    "aih_conv_noalloc", "aih_conv_stem_f32in",
+    "aih_conv_noalloc", "aih_conv_stem_f32in", "aih_conv_dwpw_plan", "aih_conv_dwpw",
 )
 
 _lib = None
@@ -185,6 +201,8 @@ def lib() -> C.CDLL:
         "aih_conv_stem_f32in": (C.c_int, [C.POINTER(_IgemmDesc), P, P, P, P, P, P]),
         "aih_ir_block_plan": (C.c_int, [C.POINTER(_IrDesc), C.POINTER(IrPlan)]),
         "aih_ir_block": (C.c_int, [C.POINTER(_IrDesc), P, P, P, P, P, P, P, P, P, P]),
+        "aih_conv_dwpw_plan": (C.c_int, [C.POINTER(_DwPwDesc), C.POINTER(DwPwPlan)]),
+        "aih_conv_dwpw": (C.c_int, [C.POINTER(_DwPwDesc), P, P, P, P, P, P, P, P]),
         "aih_last_error": (C.c_char_p, []),
         "aih_version": (C.c_char_p, []),
     }
@@ -479,6 +497,55 @@ class IrBlockSpec:
         _check(lib().aih_ir_block(C.byref(self.desc()), _ptr(x), _ptr(w_expand), _ptr(b_expand), _ptr(w_dw),
                                   _ptr(b_dw), _ptr(w_project), _ptr(b_project), _ptr(res), _ptr(y),
                                   _stream(stream)))
+        return y
+
+
+@dataclass
+class DwPwSpec:
+    """Fused depthwise 3x3 + pointwise 1x1: a depthwise conv and the 1x1 conv
+    that is its output's only reader, in one launch (the depthwise output
+    never reaches memory). The reference dispatches them separately
+    (ConvDwSpec, then GemmPwSpec; crates/ai-gpu-runtime/src/lowering.rs:122-168).
+    Weights in the unfused ops' layouts: depthwise as pack_weights_dw, the
+    pointwise as pack_weights_conv (kg_align 4, kg_pad groups)."""
+
+    ih: int
+    iw: int
+    c: int
+    cout: int
+    k: int = 3
+    s: int = 1
+    pad: tuple = (1, 1, 1, 1)
+    act_dw: Activation = Activation.RELU
+    act_pw: Activation = Activation.NONE
+    residual: bool = False
+    dt: DType = DType.F32
+    n: int = 1
+    kg_pad: int = 0       # 0: ceil(c / 4) rounded up to a multiple of 4 (pack_weights_conv's kg_align 4)
+    tile: tuple = (0, 0)  # forced output tile (h, w); (0, 0) = plan's choice
+
+    def out_hw(self) -> tuple[int, int]:
+        return ((self.ih + self.pad[0] + self.pad[2] - self.k) // self.s + 1,
+                (self.iw + self.pad[1] + self.pad[3] - self.k) // self.s + 1)
+
+    def desc(self) -> _DwPwDesc:
+        kgp = self.kg_pad or ((self.c + 3) // 4 + 3) // 4 * 4
+        return _DwPwDesc(self.n, self.ih, self.iw, self.c, self.k, self.s, (C.c_uint32 * 4)(*self.pad), self.cout,
+                         kgp, int(self.act_dw), int(self.act_pw), int(bool(self.residual)), int(self.dt),
+                         self.tile[0], self.tile[1])
+
+    def plan(self) -> DwPwPlan:
+        p = DwPwPlan()
+        _check(lib().aih_conv_dwpw_plan(C.byref(self.desc()), C.byref(p)))
+        return p
+
+    def fusable(self) -> bool:
+        p = DwPwPlan()
+        return lib().aih_conv_dwpw_plan(C.byref(self.desc()), C.byref(p)) == 0
+
+    def run(self, x, w_dw, b_dw, w_pw, b_pw, res, y, stream=None):
+        _check(lib().aih_conv_dwpw(C.byref(self.desc()), _ptr(x), _ptr(w_dw), _ptr(b_dw), _ptr(w_pw), _ptr(b_pw),
+                                   _ptr(res), _ptr(y), _stream(stream)))
         return y
 
 

@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "../../include/aih_model.h"
+#include "aih_device.h"
 #include "capi_util.h"
 #include "sw_format.h"
 
@@ -146,13 +147,16 @@ struct aih_model {
   size_t ws_bytes = 0;
   float *staging = nullptr;
   size_t staging_floats = 0;
-  std::vector<std::function<int(hipStream_t)>> launches;  // per op; empty for a fused block's 2nd and 3rd op
+  std::vector<std::function<int(hipStream_t)>> launches;  // per op; empty for a fused block's later ops
   size_t device_bytes = 0;
   uint32_t flags = 0;
   struct Fused {
-    uint32_t first;  // ops first .. first + 2
+    uint32_t first;  // ops first .. first + nops - 1
+    uint32_t nops;   // 3: inverted-residual block (d, plan); 2: depthwise -> pointwise pair (dp, dpp)
     aih_ir_block_desc d;
     aih_ir_plan plan;
+    aih_dwpw_desc dp;
+    aih_dwpw_plan dpp;
   };
   std::vector<Fused> fused;
   std::vector<int32_t> block_of;  // per op: its fused block, or -1
@@ -194,10 +198,12 @@ struct aih_model {
   }
   // fails for a tensor that stays inside a fused block (never stored)
   void need_stored(uint32_t tid, const char *what) const {
-    if (internal[tid] >= 0)
+    if (internal[tid] >= 0) {
+      const Fused &f = fused[(size_t)block_of[(size_t)internal[tid]]];
       throw std::runtime_error(std::string(what) + ": tensor '" + g.tensors[tid].name +
-                               "' stays inside the fused block of ops " + std::to_string(internal[tid]) + ".." +
-                               std::to_string(internal[tid] + 2) + " (load with AIH_MODEL_NO_FUSE to keep it)");
+                               "' stays inside the fused block of ops " + std::to_string(f.first) + ".." +
+                               std::to_string(f.first + f.nops - 1) + " (load with AIH_MODEL_NO_FUSE to keep it)");
+    }
   }
 };
 
@@ -426,6 +432,44 @@ bool is_pw(const sw::Op &o) {
          !o.pad[0] && !o.pad[1] && !o.pad[2] && !o.pad[3] && o.srcs.empty();
 }
 
+// Ops k, k + 1 as one aih_conv_dwpw launch, by the rule in find_fusions'
+// comment (op k a depthwise conv: never the first op of an inverted-residual
+// block).
+bool fuse_pair(aih_model *m, size_t k, const std::vector<uint32_t> &readers, const std::vector<bool> &pinned) {
+  const auto &ops = m->g.ops;
+  const auto &T = m->g.tensors;
+  if (m->dt != AIH_F32 || m->wdt != AIH_F32 || k + 1 >= ops.size()) return false;
+  const sw::Op &B = ops[k], &P = ops[k + 1];
+  const bool ok = B.kind == sw::OP_CONV && B.kh == 3 && B.kw == 3 && B.sh == B.sw && B.d == 1 &&
+                  B.groups == B.cin && B.cin == B.cout && B.srcs.empty() && B.res < 0 && is_pw(P) &&
+                  P.in == B.out && P.cin == B.cout && readers[B.out] == 1 && !pinned[B.out] &&
+                  dense_tid(m->g, B.in) && dense_tid(m->g, P.out) && (P.res < 0 || dense_tid(m->g, (uint32_t)P.res));
+  if (!ok) return false;
+  for (const sw::WRef *r : {&B.w, &B.b, &P.w, &P.b})
+    if (reinterpret_cast<uintptr_t>(m->wptr(*r)) % 16 != 0) return false;
+  aih_dwpw_desc d{};
+  d.n = m->n;
+  d.ih = T[B.in].h;
+  d.iw = T[B.in].w;
+  d.c = B.cin;
+  d.k = 3;
+  d.s = B.sh;
+  std::memcpy(d.pad, B.pad, sizeof(d.pad));
+  d.cout = P.cout;
+  d.kg_pad = P.kg_pad;
+  d.act_dw = B.act;
+  d.act_pw = P.act;
+  d.residual = P.res >= 0 ? 1 : 0;
+  d.dt = m->dt;
+  aih_dwpw_plan plan;
+  if (aih_conv_dwpw_plan(&d, &plan) != AIH_OK || plan.tiles < 2 * aih::device_cus()) return false;
+  const int32_t bi = (int32_t)m->fused.size();
+  m->fused.push_back(aih_model::Fused{(uint32_t)k, 2, aih_ir_block_desc{}, aih_ir_plan{}, d, plan});
+  m->block_of[k] = m->block_of[k + 1] = bi;
+  m->internal[B.out] = (int32_t)k;
+  return true;
+}
+
 // Inverted-residual blocks that run as one aih_ir_block launch: ops k, k+1,
 // k+2 = 1x1 expand (no residual), depthwise 3x3 (d = 1, square stride) on the
 // expand's output, 1x1 project on the depthwise's output (residual allowed);
@@ -434,6 +478,13 @@ bool is_pw(const sw::Op &o) {
 // the alignment aih_ir_block needs; and a plan that aih_ir_block_plan accepts.
 // The fused kernels take the converter's packed layouts as they are (the
 // 1x1 weights' K groups past cin / 4 and the pitch of kg_pad are never read).
+//
+// Where no such block starts, an fp32 depthwise 3x3 (d = 1, square stride)
+// whose output only the next op, a 1x1 conv, reads runs with it as one
+// aih_conv_dwpw launch, when its plan has at least two tiles per CU (with
+// fewer, each CU walks one tile's channel chunks alone, and the fused launch
+// measured slower than the two: 20x36 stride 2, 96 -> 48 at batch 64, 24 vs
+// 22 us; at 80x144, 44 -> 24, 83 vs 100 us).
 void find_fusions(aih_model *m) {
   const auto &ops = m->g.ops;
   const auto &T = m->g.tensors;
@@ -449,7 +500,12 @@ void find_fusions(aih_model *m) {
   for (size_t i = 0; i < T.size(); ++i)
     if (T[i].alias_of >= 0) pinned[i] = pinned[(size_t)T[i].alias_of] = true;
   auto aligned = [&](const sw::WRef &r, uintptr_t a) { return (reinterpret_cast<uintptr_t>(m->wptr(r)) % a) == 0; };
-  for (size_t k = 0; k + 2 < ops.size();) {
+  for (size_t k = 0; k + 1 < ops.size();) {
+    if (fuse_pair(m, k, readers, pinned)) {
+      k += 2;
+      continue;
+    }
+    if (k + 2 >= ops.size()) break;
     const sw::Op &A = ops[k], &B = ops[k + 1], &P = ops[k + 2];
     bool ok = is_pw(A) && A.res < 0 && B.kind == sw::OP_CONV && B.kh == 3 && B.kw == 3 && B.sh == B.sw &&
               B.d == 1 && B.groups == B.cin && B.cin == B.cout && B.cout == A.cout && B.in == A.out &&
@@ -476,7 +532,7 @@ void find_fusions(aih_model *m) {
       aih_ir_plan plan;
       if (aih_ir_block_plan(&d, &plan) == AIH_OK) {
         const int32_t bi = (int32_t)m->fused.size();
-        m->fused.push_back(aih_model::Fused{(uint32_t)k, d, plan});
+        m->fused.push_back(aih_model::Fused{(uint32_t)k, 3, d, plan, aih_dwpw_desc{}, aih_dwpw_plan{}});
         m->block_of[k] = m->block_of[k + 1] = m->block_of[k + 2] = bi;
         m->internal[A.out] = m->internal[B.out] = (int32_t)k;
         k += 3;
@@ -496,6 +552,18 @@ void lower(aih_model *m) {
       const aih_model::Fused &f = m->fused[(size_t)m->block_of[k]];
       if (f.first != k) {
         m->launches.emplace_back();  // runs in the block's first op
+        continue;
+      }
+      if (f.nops == 2) {
+        const sw::Op &P = m->g.ops[k + 1];
+        const aih_dwpw_desc d = f.dp;
+        const void *x = m->ptr(op.in), *wd = m->wptr(op.w), *bd = m->wptr(op.b), *wp = m->wptr(P.w),
+                   *bp = m->wptr(P.b);
+        const void *res = P.res >= 0 ? m->ptr((uint32_t)P.res) : nullptr;
+        void *y = m->ptr(P.out);
+        m->launches.push_back([d, x, wd, bd, wp, bp, res, y](hipStream_t s) {
+          return aih_conv_dwpw(&d, x, wd, bd, wp, bp, res, y, s);
+        });
         continue;
       }
       const sw::Op &B = m->g.ops[k + 1], &P = m->g.ops[k + 2];
@@ -894,7 +962,8 @@ int aih_model_fused_block(const aih_model *m, uint32_t i, aih_model_fused_info *
   return api_guarded([&] {
     if (!m || !out) return api_fail("fused_block: null argument");
     if (i >= m->fused.size()) return api_fail("fused_block: no fused block " + std::to_string(i));
-    *out = aih_model_fused_info{m->fused[i].first, m->fused[i].plan};
+    const aih_model::Fused &f = m->fused[i];
+    *out = aih_model_fused_info{f.first, f.nops, f.plan, f.dpp};
     return AIH_OK;
   });
 }

@@ -17,9 +17,11 @@ weights; blocks the fused kernel cannot run (aih_ir_block_plan fails) stay
 three launches.
 
 Load-time tuning (tune=True, the default): for every fusable block the
-candidates -- the three separate launches, and the fused launch at the
-planner's tile and at a set of forced tiles, each with its weights resident
-in LDS and streamed -- are timed on the device at load, a few launches each,
+candidates -- the three separate launches, the fused launch at the planner's
+tile and at a set of forced tiles, each with its weights resident in LDS and
+streamed, and (fp32) the expand conv followed by one aih_conv_dwpw launch for
+the depthwise and projection at each of its tiles -- are timed on the device
+at load, a few launches each,
 and the fastest is kept (like the reference's Model::load, which does its
 per-model work -- pipeline compilation -- once at load). fuse="auto" lets the
 timing choose between fused and separate; True keeps only fused candidates,
@@ -29,9 +31,10 @@ fuses 16-bit models only.
 The choice per block is recorded (choice_map()) and can be given back
 (choices={block: label}), so a later load runs exactly the same kernels; a
 label is "unfused", "fused THxTW" (the tile kernel, streamed weights),
-"fused THxTW resident", "wave THxTW[ resident]" (the wave kernel) or
-"split THxTW wN" (the split kernel, N wavefronts per tile) --
-fused_candidates() lists the labels a block can take.
+"fused THxTW resident", "wave THxTW[ resident]" (the wave kernel),
+"split THxTW wN" (the split kernel, N wavefronts per tile) or "dwpw THxTW"
+(expand, then the fused depthwise + projection at that tile) --
+fused_candidates() and dwpw_candidates() list the labels a block can take.
 """
 from __future__ import annotations
 
@@ -143,7 +146,7 @@ class Model:
                 self.ops.extend(self._chosen_block(blk, packed, L, choices))
                 i += 3
                 continue
-            if blk is not None:
+            if blk is not None and (tune and fuse == "auto" or blk[3].fusable()):
                 if tune:
                     self.ops.extend(self._tuned_block(blk, packed, L, allow_unfused=fuse == "auto"))
                 else:
@@ -176,9 +179,28 @@ class Model:
         spec = conv.IrBlockSpec(ih=e.ih, iw=e.iw, cin=e.cin, cexp=e.cout, cout=p.cout, s=d.s, pad=(d.pad,) * 4,
                                 act_expand=ACT[e.act], act_dw=ACT[d.act], act_project=ACT[p.act],
                                 residual=p.res is not None, dt=self.dt, n=self.n)
-        if not spec.fusable():
+        if not spec.fusable() and not self.dwpw_candidates(self._dwpw_spec(d, p)):
             return None
         return (e, d, p, spec)
+
+    def _dwpw_spec(self, d, p) -> conv.DwPwSpec:
+        return conv.DwPwSpec(ih=d.ih, iw=d.iw, c=d.cin, cout=p.cout, k=d.k, s=d.s, pad=(d.pad,) * 4,
+                             act_dw=ACT[d.act], act_pw=ACT[p.act], residual=p.res is not None, dt=self.dt,
+                             n=self.n)
+
+    DWPW_TILES = [(4, 16), (8, 16), (4, 32), (16, 16), (8, 32), (4, 64)]
+
+    @classmethod
+    def dwpw_candidates(cls, spec: conv.DwPwSpec) -> list[tuple[str, conv.DwPwSpec]]:
+        """The fused depthwise + projection launches the tuner times after the
+        expand conv: every DWPW_TILES entry that fits, as (label, spec with the
+        tile forced); none for a pair aih_conv_dwpw cannot run."""
+        out = []
+        for t in cls.DWPW_TILES:
+            sp = dataclasses.replace(spec, tile=t)
+            if sp.fusable():
+                out.append((f"dwpw {t[0]}x{t[1]}", sp))
+        return out
 
     @classmethod
     def fused_candidates(cls, spec: conv.IrBlockSpec) -> list[tuple[str, conv.IrBlockSpec]]:
@@ -218,9 +240,13 @@ class Model:
     @staticmethod
     def parse_label(label: str):
         """"unfused" -> None; "fused|wave THxTW[ resident]" or "split THxTW wN"
-        -> (IrKernel, (th, tw), IrWeights, wavefronts or 0)."""
+        -> (IrKernel, (th, tw), IrWeights, wavefronts or 0); "dwpw THxTW" ->
+        ("dwpw", (th, tw), None, 0)."""
         if label == "unfused":
             return None
+        m = re.fullmatch(r"dwpw (\d+)x(\d+)", label)
+        if m:
+            return "dwpw", (int(m.group(1)), int(m.group(2))), None, 0
         m = re.fullmatch(r"split (\d+)x(\d+) w(\d+)", label)
         if m:
             return conv.IrKernel.SPLIT, (int(m.group(1)), int(m.group(2))), conv.IrWeights.AUTO, int(m.group(3))
@@ -248,6 +274,11 @@ class Model:
         if forced is None:
             return [self._conv_op(Lr, packed, L) for Lr in (e, d, p)]
         kernel, tile, w, waves = forced
+        if kernel == "dwpw":
+            sp = dataclasses.replace(self._dwpw_spec(d, p), tile=tile)
+            if not sp.fusable():
+                raise conv.AihError(f"{self._block_name(p)}: {label!r}: {conv.last_error()}")
+            return [self._conv_op(e, packed, L), self._dwpw_op(d, p, sp, packed, L)]
         sp = dataclasses.replace(spec, tile=tile, weights=w, kernel=kernel, waves=waves)
         pl = sp.plan()
         if self.label_of(pl.kernel, pl.th, pl.tw, pl.resident, pl.waves) != label:
@@ -266,13 +297,18 @@ class Model:
             oh, ow = p.out_hw()
             self.tensors[p.name] = self._alloc(oh, ow, p.cout)
         y = self.tensors[p.name]
-        for label, sp in self.fused_candidates(spec):
-            cands.append((label, [self._fused_op((e, d, p, sp), packed, L, y=y)]))
+        if spec.fusable():
+            for label, sp in self.fused_candidates(spec):
+                cands.append((label, [self._fused_op((e, d, p, sp), packed, L, y=y)]))
+        if allow_unfused:
+            expand = cands[0][1][0]
+            for label, sp in self.dwpw_candidates(self._dwpw_spec(d, p)):
+                cands.append((label, [expand, self._dwpw_op(d, p, sp, packed, L, y=y)]))
         timed = [(self._time_ops(ops), label, ops) for label, ops in cands]
         us, label, ops = min(timed, key=lambda t: t[0])
         self.choices[self._block_name(p)] = (label, us)
         if label != "unfused":
-            for nm in (e.name, d.name):
+            for nm in ((d.name,) if label.startswith("dwpw") else (e.name, d.name)):
                 self.tensors.pop(nm, None)
         return ops
 
@@ -310,6 +346,20 @@ class Model:
                 res.data_ptr() if res is not None else None, y.data_ptr())
         keep = [desc] + [t for nm in (e.name, d.name, p.name) for t in packed[nm]]
         return ModelOp(p.name.rsplit(".", 1)[0], "ir_block", [e, d, p], L.aih_ir_block, args, spec, keep)
+
+    def _dwpw_op(self, d, p, spec: conv.DwPwSpec, packed, L, y=None) -> ModelOp:
+        """The depthwise conv d and the projection p as one aih_conv_dwpw launch."""
+        oh, ow = p.out_hw()
+        if y is None:
+            y = self._alloc(oh, ow, p.cout)
+        self.tensors[p.name] = y
+        desc = spec.desc()
+        res = self.tensors[p.res] if p.res else None
+        args = (C.byref(desc), self.tensors[d.src].data_ptr(), packed[d.name][0].data_ptr(),
+                packed[d.name][1].data_ptr(), packed[p.name][0].data_ptr(), packed[p.name][1].data_ptr(),
+                res.data_ptr() if res is not None else None, y.data_ptr())
+        keep = [desc] + [t for nm in (d.name, p.name) for t in packed[nm]]
+        return ModelOp(p.name.rsplit(".", 1)[0] + ".dwpw", "dw_pw", [d, p], L.aih_conv_dwpw, args, spec, keep)
 
     def _conv_op(self, Lr, packed, L) -> ModelOp:
         oh, ow = Lr.out_hw()

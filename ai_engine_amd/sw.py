@@ -55,7 +55,7 @@ class ModelInfo(C.Structure):
 
 
 class FusedInfo(C.Structure):
-    _fields_ = [("first_op", C.c_uint32), ("plan", conv.IrPlan)]
+    _fields_ = [("first_op", C.c_uint32), ("n_ops", C.c_uint32), ("plan", conv.IrPlan), ("dwpw", conv.DwPwPlan)]
 
 
 NO_FUSE = 1  # aih_model_flags

@@ -531,7 +531,8 @@ def real_model(torch, conv, dev, stream) -> dict:
         key = f"segm_r11_real_160x288_b{n}_{dt}" + ("" if fuse else "_unfused")
         out[key] = dict(us=round(t * 1e6, 1), frames_per_s=round(n / t, 1), tflops=round(2 * macs * n / t / 1e12, 2),
                         gflop_per_frame=round(2 * macs / 1e9, 3), ops=len(g["ops"]), launches=m.info.n_launches,
-                        fused_blocks=[f"ops {f.first_op}-{f.first_op + 2}: {f.plan}" for f in m.fused_blocks()])
+                        fused_blocks=[f"ops {f.first_op}-{f.first_op + f.n_ops - 1}: "
+                                      f"{f.plan if f.n_ops == 3 else f.dwpw}" for f in m.fused_blocks()])
         log(f"real segm model {dt} b{n} {'fused' if fuse else 'unfused'}: {t * 1e3:.3f} ms {n / t:.0f} frames/s "
             f"({m.info.n_launches} launches)")
         m.close()

@@ -280,6 +280,42 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
                  const void *w_dw, const void *b_dw, const void *w_project, const void *b_project,
                  const void *res, void *y, aih_stream stream);
 
+/* Fused depthwise + pointwise: a depthwise 3x3 conv (groups = c, stride s,
+ * d = 1) + act_dw and the 1x1 conv that is its output's only reader (c ->
+ * cout) + act_pw (+ residual) -- two SwOp::Conv that lower_op dispatches
+ * separately (lowering.rs:122-168: conv_dw.rs:21-216, then gemm_pw.rs:129-297)
+ * -- as one kernel; the depthwise output never goes to memory. No
+ * counterpart op in the reference (a fusion of those two dispatches). Each
+ * stage keeps its unfused arithmetic (fp32 accumulation, depthwise sum from
+ * the bias over the taps in (ky, kx) order, y = act(acc + bias) (+ res)).
+ * Buffers in the unfused ops' layouts: x [n][ih][iw][c] NHWC-C4, w_dw / b_dw
+ * as aih_conv_dw takes them, w_pw / b_pw as aih_conv_pw takes them (packed
+ * kg_align 4, kg_pad groups), res / y [n][oh][ow][cout] NHWC-C4; every buffer
+ * 16-byte aligned. fp32 storage only; cout 1..64; fails with a message
+ * otherwise (the caller then runs the two ops). */
+typedef struct {
+  uint32_t n, ih, iw, c;   /* depthwise input: n images, c channels */
+  uint32_t k, s;           /* depthwise kernel (3) and stride (1 or 2) */
+  uint32_t pad[4];         /* depthwise padding: top, left, bottom, right (< k) */
+  uint32_t cout;           /* pointwise output channels */
+  uint32_t kg_pad;         /* kg of the packed pointwise weights (>= ceil(c / 4)) */
+  int32_t act_dw, act_pw;  /* enum aih_act */
+  int32_t residual;        /* 0 or 1: y = act_pw(...) + res */
+  int32_t dt;              /* AIH_F32 */
+  uint32_t tile_h, tile_w; /* output tile: 4 x 16 multiples of at most 4 wavefronts; 0 = chosen by the plan */
+} aih_dwpw_desc;
+
+/* Geometry aih_conv_dwpw_plan chose: output tile th x tw (a wavefront per 4
+ * rows x 16 columns), channel chunks of 16, tiles (one workgroup each), LDS
+ * bytes and resident workgroups per CU, launched workgroups. */
+typedef struct {
+  uint32_t th, tw, waves, chunks, tiles, lds_bytes, occupancy, grid;
+} aih_dwpw_plan;
+
+int aih_conv_dwpw_plan(const aih_dwpw_desc *d, aih_dwpw_plan *out);
+int aih_conv_dwpw(const aih_dwpw_desc *d, const void *x, const void *w_dw, const void *b_dw, const void *w_pw,
+                  const void *b_pw, const void *res, void *y, aih_stream stream);
+
 /* ---- host-side packing (ai-core pack.rs; plain host memory) ---- */
 /* Output bytes = n*h*w*ceil(c/4)*4*sizeof(dt). */
 size_t aih_nhwc_c4_bytes(uint32_t n, uint32_t h, uint32_t w, uint32_t c, int32_t dt);

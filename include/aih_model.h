@@ -126,11 +126,14 @@ aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt)
  * consecutive in the file's op order, whose two intermediate tensors no other
  * op, alias, graph output or state uses, and that aih_ir_block_plan accepts
  * (the plan's deterministic choice of kernel, tile and weight placement).
- * The intermediates are then never stored: reading, writing or querying them
- * fails, and aih_model_infer_range may not split a fused block. The reference
- * runtime dispatches the three convs separately (lowering.rs:122-152); this
- * fusion has no counterpart there and keeps each conv's arithmetic and
- * rounding points. AIH_MODEL_NO_FUSE lowers every op on its own. */
+ * Elsewhere, in an fp32 model, a 3x3 depthwise and the 1x1 conv after it that
+ * alone reads its output run as one aih_conv_dwpw launch when its plan has
+ * at least two tiles per CU. The intermediates are then never stored:
+ * reading, writing or querying them fails, and aih_model_infer_range may not
+ * split a fused block. The reference runtime dispatches the convs separately
+ * (lowering.rs:122-152); this fusion has no counterpart there and keeps each
+ * conv's arithmetic and rounding points. AIH_MODEL_NO_FUSE lowers every op on
+ * its own. */
 enum aih_model_flags { AIH_MODEL_NO_FUSE = 1 };
 aih_model *aih_model_load_ex(const void *bytes, size_t len, uint32_t n, int32_t dt, uint32_t flags);
 void aih_model_free(aih_model *m);
@@ -146,8 +149,7 @@ int aih_model_upload_input_device(aih_model *m, const char *name, const float *d
 int aih_model_infer(aih_model *m, aih_stream stream);
 /* Runs ops [first, last) only (per-op timing and parity; the reference's
  * ai-cpu profiler times op by op, crates/ai-cpu/src/model.rs:241-272). A
- * fused block's three ops run together: a range must hold all of them or
- * none. */
+ * fused block's ops run together: a range must hold all of them or none. */
 int aih_model_infer_range(aih_model *m, uint32_t first, uint32_t last, aih_stream stream);
 /* A tensor (by name; outputs and any other tensor) as logical NHWC fp32,
  * n*h*w*c floats; waits for `stream`. */
@@ -171,18 +173,22 @@ int aih_model_tensor(const aih_model *m, const char *name, aih_tensor_info *out)
 
 typedef struct {
   uint32_t n_tensors, n_ops, n_inputs, n_outputs;
-  uint32_t n_launches; /* kernel launches of one aih_model_infer: ops, less two per fused block */
-  uint32_t n_fused;    /* fused inverted-residual blocks */
+  uint32_t n_launches; /* kernel launches of one aih_model_infer: ops, less n_ops - 1 per fused block */
+  uint32_t n_fused;    /* fused blocks (inverted-residual blocks and depthwise -> pointwise pairs) */
   int32_t dt, wdt;
   size_t device_bytes; /* weights + tensors + workspace */
 } aih_model_info;
 int aih_model_get_info(const aih_model *m, aih_model_info *out);
 
-/* Fused block i (0 <= i < n_fused): its first op (it covers ops first_op ..
- * first_op + 2) and the plan aih_ir_block runs it with. */
+/* Fused block i (0 <= i < n_fused): its first op and op count (it covers
+ * ops first_op .. first_op + n_ops - 1); for an inverted-residual block
+ * (n_ops 3) the plan aih_ir_block runs it with, for a depthwise -> pointwise
+ * pair (n_ops 2) the plan of aih_conv_dwpw. */
 typedef struct {
   uint32_t first_op;
+  uint32_t n_ops;
   aih_ir_plan plan;
+  aih_dwpw_plan dwpw;
 } aih_model_fused_info;
 int aih_model_fused_block(const aih_model *m, uint32_t i, aih_model_fused_info *out);
 /* Name of input / output i (valid while m lives). */

@@ -191,11 +191,11 @@ SEGM_FUSED = [12, 15, 18, 21]  # first ops of the real model's inverted-residual
 
 def _launch_steps(m, graph):
     """(first op, last op + 1) of each launch the model makes: one op, or a
-    fused block's three."""
-    firsts = {f.first_op for f in m.fused_blocks()}
+    fused block's two or three."""
+    firsts = {f.first_op: f.n_ops for f in m.fused_blocks()}
     k, out = 0, []
     while k < len(graph.g["ops"]):
-        step = 3 if k in firsts else 1
+        step = firsts.get(k, 1)
         out.append((k, k + step))
         k += step
     return out
@@ -205,7 +205,7 @@ def _stored(m, graph, name):
     """Tensors a fused model keeps (every one but a fused block's intermediates)."""
     internal = set()
     for f in m.fused_blocks():
-        for k in (f.first_op, f.first_op + 1):
+        for k in range(f.first_op, f.first_op + f.n_ops - 1):
             internal.add(graph.T[graph.g["ops"][k]["out"]]["name"])
     return name not in internal
 
@@ -347,6 +347,44 @@ def test_synthetic_chain_through_the_native_loader(orc):
         m.infer()
         assert G.rel_err(m.read_output(), want) <= 1e-4
         m.close()
+
+
+def test_depthwise_pointwise_pair_through_the_native_loader(orc):
+    """An fp32 depthwise 3x3 whose output only the next 1x1 conv reads runs
+    with it as one aih_conv_dwpw launch when the plan has >= 2 tiles per CU
+    (80x144 at batch 12: 540 tiles of 16x16), and not at batch 2; the
+    depthwise output is then never stored; results within 1e-4 of the
+    oracle's graph run either way, each launch and end to end; a 16-bit load
+    of the same file keeps the two ops."""
+    from ai_engine_amd.workloads import Layer, _chain, make_weights
+
+    layers = _chain([Layer("stem", 3, 32, k=3, s=2, act="relu"), Layer("d", 32, 32, k=3, groups=32, act="relu"),
+                     Layer("p", 32, 24, act="relu"), Layer("head", 24, 2)], 160, 288)
+    wts = make_weights(layers, seed=12)
+    data = sw.conv_graph_to_sw("pair", layers, wts, 160, 288, 3)
+    graph = so.SwGraph(data)
+    for n, pairs in [(12, [(1, 2)]), (2, [])]:
+        x = rnd(82 + n, n, 160, 288, 3)
+        want = graph.run({"input": x}, n=n, keep_all=True)
+        m = sw.SwModel(data, n=n)
+        blocks = m.fused_blocks()
+        assert [(f.first_op, f.n_ops) for f in blocks] == pairs
+        if pairs:
+            assert blocks[0].dwpw.tiles == 12 * 45 and m.info.n_launches == 3
+            with pytest.raises(conv.AihError, match="stays inside the fused block of ops 1..2"):
+                m.read_output("d")
+            with pytest.raises(conv.AihError, match="inside the fused block"):
+                m.infer_range(2, 4)
+        worst = _check_launches(m, graph, want, 1e-4)
+        m.upload_input("input", x)
+        m.infer()
+        e = G.rel_err(m.read_output(), want["head"])
+        print(f"dw->pw pair n={n} fused={bool(pairs)}: per launch {worst:.2e}, end to end {e:.2e}", flush=True)
+        assert e <= 1e-4
+        m.close()
+    m16 = sw.SwModel(data, n=12, dt=conv.DType.F16)
+    assert m16.fused_blocks() == []
+    m16.close()
 
 
 def test_fusion_needs_single_readers(orc):
