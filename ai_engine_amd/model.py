@@ -66,7 +66,8 @@ def _to_device(a: np.ndarray, device) -> torch.Tensor:
 
 @dataclass
 class ModelOp:
-    """One launch of the graph: a single conv ("conv") or a fused block ("ir_block")."""
+    """One launch of the graph: a single conv ("conv"), a fused block
+    ("ir_block") or a fused depthwise + pointwise pair ("dw_pw")."""
 
     name: str
     kind: str
@@ -84,9 +85,17 @@ class ModelOp:
         write once (a fused block's intermediates never reach HBM)."""
         if self.kind == "conv":
             return self.layers[0].bytes(n, act_bytes, w_bytes)
+        c4 = lambda c: -(-c // 4) * 4
+        if self.kind == "dw_pw":
+            d, p = self.layers
+            oh, ow = p.out_hw()
+            x = n * d.ih * d.iw * c4(d.cin) * act_bytes
+            y = n * oh * ow * p.cout * act_bytes
+            r = y if p.res else 0
+            w = (d.k * d.k * d.cout + p.cin * p.cout) * w_bytes + (d.cout + p.cout) * act_bytes
+            return x + y + r + w
         e, d, p = self.layers
         oh, ow = p.out_hw()
-        c4 = lambda c: -(-c // 4) * 4
         x = n * e.ih * e.iw * c4(e.cin) * act_bytes
         y = n * oh * ow * p.cout * act_bytes
         r = y if p.res else 0

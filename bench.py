@@ -493,6 +493,13 @@ def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
     row["per_layer_roofline_sum_us"] = sum(
         max(L.flops(meta["n"]) / (PEAK_TF["f32"] * 1e12), L.bytes(meta["n"], 4, 4) / (HBM_GBS * 1e9))
         for L in layers) * 1e6
+    row["frac_basis"] = "per layer: the unfused layers' bytes (the depthwise outputs included)"
+    own_s = sum(max(op.flops(meta["n"]) / (PEAK_TF["f32"] * 1e12), op.bytes(meta["n"], 4, 4) / (HBM_GBS * 1e9))
+                for op in m4.ops)
+    row["own_roofline_us"] = own_s * 1e6
+    row["own_frac"] = own_s / t
+    row["own_note"] = ("sum over the launches run of max(flops / MFMA peak, bytes / 8 TB/s), a fused "
+                       "launch counting only the tensors it reads and writes")
     res["ir_block_chain_4x_64c_40x72_b64"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
     log(f"ir chain: {row['us']:.1f} us frac {row['frac']:.3f}; blocks: " +
         ", ".join(f"{k} {v[0]} ({v[1]:.0f} us)" for k, v in m4.choices.items()))
@@ -548,7 +555,12 @@ def encoder_other(torch, W, Model, layers, wts, x, n, H, Wd, dtname, DT, stream)
 
     t = time_launches(torch, stream, step, 10)
     fl, by = W.totals(layers, n, 2, 2)
-    row = roof(fl, by, t, dtname)
+    row = roof(fl, sum(op.bytes(n, 2, 2) for op in m.ops), t, dtname)
+    row["frac"] = sum(max(op.flops(n) / (PEAK_TF[dtname] * 1e12), op.bytes(n, 2, 2) / (HBM_GBS * 1e9))
+                      for op in m.ops) / t
+    row["frac_basis"] = ("the step's own roofline: sum over the launches run of max(flops / MFMA peak, "
+                         "bytes / 8 TB/s), a fused block counting its input, output, residual and weights")
+    row["per_layer_frac"] = roof(fl, by, t, dtname)["frac"]
     row["frames_per_s"] = n / t
     log(f"encoder {dtname}: {t * 1e3:.3f} ms {n / t:.0f} frames/s")
     return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
