@@ -140,15 +140,17 @@ class _DwPwDesc(C.Structure):
     _fields_ = [("n", C.c_uint32), ("ih", C.c_uint32), ("iw", C.c_uint32), ("c", C.c_uint32),
                 ("k", C.c_uint32), ("s", C.c_uint32), ("pad", C.c_uint32 * 4), ("cout", C.c_uint32),
                 ("kg_pad", C.c_uint32), ("act_dw", C.c_int32), ("act_pw", C.c_int32), ("residual", C.c_int32),
-                ("dt", C.c_int32), ("tile_h", C.c_uint32), ("tile_w", C.c_uint32)]
+                ("dt", C.c_int32), ("tile_h", C.c_uint32), ("tile_w", C.c_uint32),
+                ("wave_rows", C.c_uint32)]
 
 
 class DwPwPlan(C.Structure):
-    _fields_ = [("th", C.c_uint32), ("tw", C.c_uint32), ("waves", C.c_uint32), ("chunks", C.c_uint32),
+    _fields_ = [("th", C.c_uint32), ("tw", C.c_uint32), ("waves", C.c_uint32), ("wave_rows", C.c_uint32),
+                ("chunks", C.c_uint32),
                 ("tiles", C.c_uint32), ("lds_bytes", C.c_uint32), ("occupancy", C.c_uint32), ("grid", C.c_uint32)]
 
     def __repr__(self):
-        return (f"DwPwPlan(tile={self.th}x{self.tw}, waves={self.waves}, chunks={self.chunks}, "
+        return (f"DwPwPlan(tile={self.th}x{self.tw}, waves={self.waves}x{self.wave_rows} rows, chunks={self.chunks}, "
                 f"tiles={self.tiles}, lds={self.lds_bytes}, occ={self.occupancy}, grid={self.grid})")
 
 
@@ -469,6 +471,7 @@ class IrBlockSpec:
     dt: DType = DType.F32
     n: int = 1
     tile: tuple = (0, 0)  # forced output tile (h, w); (0, 0) = plan's choice
+    rows: int = 0         # forced output rows per wavefront (2 or 4); 0 = plan's choice
     ec: int = 0           # forced expanded channels per chunk; 0 = plan's choice
     weights: int = 0      # IrWeights: 0 = plan's choice, 1 = resident in LDS, 2 = streamed
     kernel: int = 0       # IrKernel: 0 = plan's choice, 1 = tile, 2 = wave, 3 = split kernel
@@ -523,6 +526,7 @@ class DwPwSpec:
     n: int = 1
     kg_pad: int = 0       # 0: ceil(c / 4) rounded up to a multiple of 4 (pack_weights_conv's kg_align 4)
     tile: tuple = (0, 0)  # forced output tile (h, w); (0, 0) = plan's choice
+    rows: int = 0         # forced output rows per wavefront (2 or 4); 0 = plan's choice
 
     def out_hw(self) -> tuple[int, int]:
         return ((self.ih + self.pad[0] + self.pad[2] - self.k) // self.s + 1,
@@ -532,7 +536,7 @@ class DwPwSpec:
         kgp = self.kg_pad or ((self.c + 3) // 4 + 3) // 4 * 4
         return _DwPwDesc(self.n, self.ih, self.iw, self.c, self.k, self.s, (C.c_uint32 * 4)(*self.pad), self.cout,
                          kgp, int(self.act_dw), int(self.act_pw), int(bool(self.residual)), int(self.dt),
-                         self.tile[0], self.tile[1])
+                         self.tile[0], self.tile[1], self.rows)
 
     def plan(self) -> DwPwPlan:
         p = DwPwPlan()

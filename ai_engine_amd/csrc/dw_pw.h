@@ -10,8 +10,6 @@
 
 namespace aih {
 
-// Output rows of one wavefront (a vertical strip of 16-pixel row blocks).
-constexpr uint32_t kDpRows = 4;
 // 16-byte units (4 fp32 channels) of one chunk per halo pixel: 4, i.e. 16
 // channels (32-channel chunks, whole 128-byte lines, measured slower: twice
 // the LDS per buffer halves the resident workgroups, and a channel count
@@ -19,8 +17,10 @@ constexpr uint32_t kDpRows = 4;
 // more unit, the pad: an odd number of units puts the 16 consecutive pixels
 // one ds_read_b128 reads in distinct banks.
 constexpr int dwpw_units(int s) { return s > 0 ? 4 : 4; }
-// Most 64-slot rows of the halo region one wavefront copies per chunk.
-constexpr uint32_t kDpSlotsPerThread = 24;
+// Most 64-slot rows of the halo region one wavefront copies per chunk (its
+// slot offsets stay in registers for the whole launch): 10 at stride 1 (the
+// shapes the planner tries need at most 9), 24 at stride 2.
+constexpr uint32_t dwpw_slots(uint32_t s) { return s == 1 ? 10u : 24u; }
 
 struct DwPwArgs {
   const void *x;    // depthwise input [N][IH][IW][C] (C a multiple of 4)
@@ -33,7 +33,7 @@ struct DwPwArgs {
   uint32_t img_bytes;  // bytes of one input image
   uint32_t IH, IW, C, OH, OW, CO4, KGP;
   int32_t PT, PL;
-  uint32_t TH, TW;   // output tile: wy * kDpRows rows, wx * 16 columns
+  uint32_t TH, TW;   // output tile: wy * nb rows (nb per wavefront), wx * 16 columns
   uint32_t wx;       // wavefronts across the tile
   uint32_t HH, HW;   // halo rows / columns of the tile
   uint32_t HWE;      // stride 2: columns of the even half (ceil(HW / 2)); halo columns are stored even first
@@ -48,7 +48,7 @@ struct DwPwArgs {
 };
 
 struct DwPwPlan {
-  uint32_t wx, wy, TH, TW, HH, HW, HWE;
+  uint32_t wx, wy, nb, TH, TW, HH, HW, HWE;
   uint32_t tiles_x, tiles_y, ntiles;
   uint32_t xrows, buf_bytes, lds, occ, grid;
 };
@@ -68,8 +68,11 @@ inline uint32_t dwpw_buf_bytes(uint32_t k, uint32_t s, uint32_t hh, uint32_t hw,
   return dwpw_xrows(s, hh, hw) * 1024 + (k * k * u + u + u * cop) * 16;
 }
 
-hipError_t launch_dw_pw(const DwPwArgs &a, int dt, uint32_t k, uint32_t s, uint32_t waves, uint32_t lds,
-                        uint32_t grid, hipStream_t st);
-int dw_pw_occupancy(int dt, uint32_t k, uint32_t s, uint32_t cout, uint32_t waves, uint32_t lds);
+// rows: output rows per wavefront (2 or 4).
+hipError_t launch_dw_pw(const DwPwArgs &a, int dt, uint32_t k, uint32_t s, uint32_t rows, uint32_t waves,
+                        uint32_t lds, uint32_t grid, hipStream_t st);
+// cl: both activations clamp-type (the instantiation launch_dw_pw runs for them).
+int dw_pw_occupancy(int dt, uint32_t k, uint32_t s, uint32_t cout, uint32_t rows, bool cl, uint32_t waves,
+                    uint32_t lds);
 
 }  // namespace aih

@@ -15,15 +15,16 @@
 // crates/ai-cpu/src/kernels/dw.rs:40-204), the pointwise sum is the MFMA's,
 // the epilogue act(acc + bias) + res (common/epilogue.rs:13-30).
 //
-// Decomposition (MI355X): a workgroup owns an output tile of wy * 4 rows x
-// wx * 16 columns of one image and walks the depthwise channels in chunks of
+// Decomposition (MI355X): a workgroup owns an output tile of wy * NB rows x
+// wx * 16 columns of one image (NB = 4 or 2 rows per wavefront, up to 8
+// wavefronts) and walks the depthwise channels in chunks of
 // 16. Per chunk the tile's input halo (the chunk's 64 bytes of every pixel)
 // and the chunk's weights are copied global -> LDS by LDS-direct buffer loads
 // (no registers; zeros outside the image from the range check) into one of
 // two buffers, the next chunk's copy overlapping the current chunk's compute,
 // one workgroup barrier per chunk (three or four buffers, more chunks in
 // flight, measured 1.4-1.9x slower: their LDS costs resident workgroups).
-// A wavefront owns a vertical strip of four 16-pixel row blocks; lane l
+// A wavefront owns a vertical strip of NB 16-pixel row blocks; lane l
 // computes the depthwise result of pixel l % 16 of each block for the four
 // channels of 16-byte unit l / 16, reading every
 // halo row once for the up to K blocks that use it (row reuse), and that
@@ -61,14 +62,14 @@ __device__ __forceinline__ void dp_load16(__amdgpu_buffer_rsrc_t rs, char *dst, 
 }
 
 // K: depthwise kernel size; S: stride; NO: blocks of 16 output channels;
-// U: 16-byte units (4 fp32 channels) per chunk and halo pixel; CL: both
-// activations are clamp-type (one v_med3 each, no mode switch).
-template <int K, int S, int NO, int U, bool CL>
-__global__ __launch_bounds__(256) void dw_pw_kernel(DwPwArgs a) {
+// U: 16-byte units (4 fp32 channels) per chunk and halo pixel; NB: output
+// rows (16-pixel row blocks) per wavefront, 4 or 2; CL: both activations are
+// clamp-type (one v_med3 each, no mode switch).
+template <int K, int S, int NO, int U, int NB, bool CL>
+__global__ __launch_bounds__(512) void dw_pw_kernel(DwPwArgs a) {
   constexpr uint32_t ES = 4, EC = 4 * U, COP = 16 * NO, PITCH = (U + 1) * 16;
-  constexpr int NB = kDpRows;
   constexpr int HR = (NB - 1) * S + K;  // halo rows one wavefront reads
-  constexpr int XS = kDpSlotsPerThread;
+  constexpr int XS = dwpw_slots(S);
   constexpr uint32_t NWD = K * K * U, NWP = U * COP;  // weight slots of a chunk
   extern __shared__ __align__(16) char lds[];
   const uint32_t tid = threadIdx.x, lane = tid & 63, p16 = lane & 15, kq = lane >> 4;
@@ -256,28 +257,27 @@ __global__ __launch_bounds__(256) void dw_pw_kernel(DwPwArgs a) {
   }
 }
 
-template <int K, int S, int NO, bool CL>
+template <int K, int S, int NO, int NB, bool CL>
 hipError_t prepare_inst() {
   static const hipError_t e =
-      hipFuncSetAttribute(reinterpret_cast<const void *>(dw_pw_kernel<K, S, NO, dwpw_units(S), CL>),
+      hipFuncSetAttribute(reinterpret_cast<const void *>(dw_pw_kernel<K, S, NO, dwpw_units(S), NB, CL>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   return e;
 }
 
-template <int K, int S, int NO, bool CL>
+template <int K, int S, int NO, int NB, bool CL>
 hipError_t launch_inst(const DwPwArgs &a, uint32_t waves, uint32_t lds, uint32_t grid, hipStream_t st) {
-  const hipError_t e = prepare_inst<K, S, NO, CL>();
+  const hipError_t e = prepare_inst<K, S, NO, NB, CL>();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((dw_pw_kernel<K, S, NO, dwpw_units(S), CL>), dim3(grid), dim3(64 * waves), lds, st, a);
+  hipLaunchKernelGGL((dw_pw_kernel<K, S, NO, dwpw_units(S), NB, CL>), dim3(grid), dim3(64 * waves), lds, st, a);
   return hipGetLastError();
 }
 
-template <int K, int S, int NO>
+template <int K, int S, int NO, int NB, bool CL>
 int occ_inst(uint32_t waves, uint32_t lds) {
-  // the clamp and generic instantiations take the same registers or fewer: plan by the generic one
-  if (prepare_inst<K, S, NO, false>() != hipSuccess) return 0;
+  if (prepare_inst<K, S, NO, NB, CL>() != hipSuccess) return 0;
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, dw_pw_kernel<K, S, NO, dwpw_units(S), false>,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, dw_pw_kernel<K, S, NO, dwpw_units(S), NB, CL>,
                                                    (int)(64 * waves), lds) != hipSuccess)
     return 0;
   return per_cu;
@@ -288,15 +288,20 @@ int occ_inst(uint32_t waves, uint32_t lds) {
 
 }  // namespace
 
-hipError_t launch_dw_pw(const DwPwArgs &a, int dt, uint32_t k, uint32_t s, uint32_t waves, uint32_t lds,
-                        uint32_t grid, hipStream_t st) {
+hipError_t launch_dw_pw(const DwPwArgs &a, int dt, uint32_t k, uint32_t s, uint32_t rows, uint32_t waves,
+                        uint32_t lds, uint32_t grid, hipStream_t st) {
   if (dt != DT_F32) return hipErrorInvalidValue;
   const uint32_t no = dwpw_no(a.CO4);
   const bool cl = act_is_clamp(a.act_d) && act_is_clamp(a.act_p);
-#define AIH_DP_LAUNCH(K_, S_, NO_)                                                          \
-  if (k == K_ && s == S_ && no == NO_)                                                      \
-    return cl ? launch_inst<K_, S_, NO_, true>(a, waves, lds, grid, st)                     \
-              : launch_inst<K_, S_, NO_, false>(a, waves, lds, grid, st);
+#define AIH_DP_LAUNCH(K_, S_, NO_)                                                                  \
+  if (k == K_ && s == S_ && no == NO_) {                                                            \
+    if (rows == 2)                                                                                  \
+      return cl ? launch_inst<K_, S_, NO_, 2, true>(a, waves, lds, grid, st)                        \
+                : launch_inst<K_, S_, NO_, 2, false>(a, waves, lds, grid, st);                      \
+    if (rows == 4)                                                                                  \
+      return cl ? launch_inst<K_, S_, NO_, 4, true>(a, waves, lds, grid, st)                        \
+                : launch_inst<K_, S_, NO_, 4, false>(a, waves, lds, grid, st);                      \
+  }
   AIH_DP_SHAPES(AIH_DP_LAUNCH)
 #undef AIH_DP_LAUNCH
   return hipErrorInvalidValue;
@@ -304,20 +309,23 @@ hipError_t launch_dw_pw(const DwPwArgs &a, int dt, uint32_t k, uint32_t s, uint3
 
 // Workgroups per CU of an instantiation at a workgroup size and LDS size,
 // queried once per device; 0 for a shape without an instantiation.
-int dw_pw_occupancy(int dt, uint32_t k, uint32_t s, uint32_t cout, uint32_t waves, uint32_t lds) {
-  if (dt != DT_F32) return 0;
+int dw_pw_occupancy(int dt, uint32_t k, uint32_t s, uint32_t cout, uint32_t rows, bool cl, uint32_t waves,
+                    uint32_t lds) {
+  if (dt != DT_F32 || (rows != 2 && rows != 4)) return 0;
   const uint32_t no = dwpw_no(cout);
   static std::mutex mu;
-  static std::map<std::tuple<uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, int>, int> cache;
+  static std::map<std::tuple<uint32_t, uint32_t, uint32_t, uint32_t, bool, uint32_t, uint32_t, int>, int> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = -1;
   std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_tuple(k, s, no, waves, lds, dev);
+  const auto key = std::make_tuple(k, s, no, rows, cl, waves, lds, dev);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int occ = -1;
-#define AIH_DP_OCC(K_, S_, NO_) \
-  if (k == K_ && s == S_ && no == NO_) occ = occ_inst<K_, S_, NO_>(waves, lds);
+#define AIH_DP_OCC(K_, S_, NO_)                                                                           \
+  if (k == K_ && s == S_ && no == NO_)                                                                      \
+    occ = rows == 2 ? (cl ? occ_inst<K_, S_, NO_, 2, true>(waves, lds) : occ_inst<K_, S_, NO_, 2, false>(waves, lds)) \
+                    : (cl ? occ_inst<K_, S_, NO_, 4, true>(waves, lds) : occ_inst<K_, S_, NO_, 4, false>(waves, lds));
   AIH_DP_SHAPES(AIH_DP_OCC)
 #undef AIH_DP_OCC
   if (occ < 0) return 0;
@@ -359,35 +367,45 @@ bool dp_check(const aih_dwpw_desc *d, uint32_t *oh, uint32_t *ow) {
   return true;
 }
 
-// Tile shape (wy x wx wavefronts, each 4 output rows x 16 columns): forced
-// by tile_h / tile_w, else the shape with the most wavefronts whose tiles
-// still give every CU one (a tile's wavefronts share its halo and overlap one
-// another's MFMA and depthwise phases; the more resident, the better the
-// copies are hidden), among those the least halo copied over all tiles
-// (partial edge tiles included); with fewer tiles than CUs for every shape,
-// the most tiles. Two LDS chunk buffers.
+// Tile shape (wy x wx wavefronts, each nb = 4 or 2 output rows x 16
+// columns): forced by tile_h / tile_w (and wave_rows), else, among the shapes
+// whose tiles give every CU one (or, when none does, the most tiles), the one
+// keeping the most wavefronts resident per CU (workgroups resident x
+// wavefronts, up to 16, or fewer when the launch has fewer tiles: the MFMA
+// and depthwise phases of one wavefront and the copies of another overlap),
+// then the fewest wavefronts per workgroup (a shorter barrier), the least
+// halo copied over all tiles, four rows per wavefront. Measured at batch 64
+// (us): 256 -> 64 at 40x72, 8x16 with 2 rows 109, 16x16 with 2 rows (8
+// wavefronts) 119, 16x16 with 4 rows 132; 44 -> 24 at 80x144 56 / 65 / 74.
+// Two LDS chunk buffers.
 bool dp_plan(const aih_dwpw_desc *d, uint32_t oh, uint32_t ow, DwPwPlan *out) {
-  static const uint32_t shapes[][2] = {{1, 1}, {2, 1}, {1, 2}, {4, 1}, {2, 2}, {1, 4}};
+  // {wx, wy, nb}: 1-8 wavefronts, at most 64 columns and 16 rows
+  static const uint32_t shapes[][3] = {{1, 1, 4}, {2, 1, 4}, {1, 2, 4}, {4, 1, 4}, {2, 2, 4}, {1, 4, 4},
+                                       {1, 2, 2}, {2, 2, 2}, {1, 4, 2}, {4, 2, 2}, {2, 4, 2}, {1, 8, 2}};
   const uint32_t cus = aih::device_cus();
   bool found = false;
   uint64_t best_halo = 0;
+  double best_eff = 0.0;
   for (const auto &sh : shapes) {
     DwPwPlan p{};
     p.wx = sh[0];
     p.wy = sh[1];
-    if ((d->tile_h || d->tile_w) && (d->tile_h != p.wy * aih::kDpRows || d->tile_w != p.wx * 16)) continue;
+    p.nb = sh[2];
+    if ((d->tile_h || d->tile_w) && (d->tile_h != p.wy * p.nb || d->tile_w != p.wx * 16)) continue;
+    if (d->wave_rows && d->wave_rows != p.nb) continue;
     const uint32_t waves = p.wx * p.wy;
-    p.TH = p.wy * aih::kDpRows;
+    p.TH = p.wy * p.nb;
     p.TW = p.wx * 16;
     p.HH = (p.TH - 1) * d->s + d->k;
     p.HW = (p.TW - 1) * d->s + d->k;
     p.HWE = d->s == 2 ? (p.HW + 1) / 2 : 0;
     p.xrows = aih::dwpw_xrows(d->s, p.HH, p.HW);
-    if (p.xrows > waves * aih::kDpSlotsPerThread) continue;
+    if (p.xrows > waves * aih::dwpw_slots(d->s)) continue;
     p.buf_bytes = aih::dwpw_buf_bytes(d->k, d->s, p.HH, p.HW, d->cout);
     p.lds = 2 * p.buf_bytes;
     if (p.lds > 160u * 1024u) continue;
-    p.occ = (uint32_t)aih::dw_pw_occupancy(d->dt, d->k, d->s, d->cout, waves, p.lds);
+    p.occ = (uint32_t)aih::dw_pw_occupancy(d->dt, d->k, d->s, d->cout, p.nb,
+                                           aih::act_is_clamp(d->act_dw) && aih::act_is_clamp(d->act_pw), waves, p.lds);
     if (p.occ == 0) continue;
     p.tiles_x = (ow + p.TW - 1) / p.TW;
     p.tiles_y = (oh + p.TH - 1) / p.TH;
@@ -396,28 +414,35 @@ bool dp_plan(const aih_dwpw_desc *d, uint32_t oh, uint32_t ow, DwPwPlan *out) {
     p.ntiles = (uint32_t)nt;
     p.grid = p.ntiles;
     const uint64_t halo = nt * p.HH * p.HW;
+    const double eff = std::min({(double)(waves * p.occ), 16.0, (double)nt * waves / cus});
     bool better = !found;
     if (found) {
       const bool fills = p.ntiles >= cus, best_fills = out->ntiles >= cus;
       const uint32_t best_waves = out->wx * out->wy;
       if (fills != best_fills)
         better = fills;
-      else if (!fills)
+      else if (!fills && p.ntiles != out->ntiles)
         better = p.ntiles > out->ntiles;
+      else if (std::fabs(eff - best_eff) > 1e-9)
+        better = eff > best_eff;
       else if (waves != best_waves)
-        better = waves > best_waves;
-      else
+        better = waves < best_waves;
+      else if (halo != best_halo)
         better = halo < best_halo;
+      else
+        better = p.nb > out->nb;
     }
     if (better) {
       *out = p;
       best_halo = halo;
+      best_eff = eff;
       found = true;
     }
   }
   if (!found) {
-    dp_fail(d->tile_h || d->tile_w ? "dwpw: the forced tile is no 4 x 16 multiple of at most 4 wavefronts that fits"
-                                   : "dwpw: no tile fits");
+    dp_fail(d->tile_h || d->tile_w || d->wave_rows
+                ? "dwpw: the forced tile / wave rows are no shape of 1-8 wavefronts of 2 or 4 rows x 16 columns that fits"
+                : "dwpw: no tile fits");
     return false;
   }
   return true;
@@ -437,7 +462,7 @@ int aih_conv_dwpw_plan(const aih_dwpw_desc *d, aih_dwpw_plan *out) {
     DwPwPlan p;
     if (!dp_plan(d, oh, ow, &p)) return AIH_ERR;
     const uint32_t ec = 4 * aih::dwpw_units(d->s);
-    *out = aih_dwpw_plan{p.TH, p.TW, p.wx * p.wy, (d->c + ec - 1) / ec, p.ntiles, p.lds, p.occ, p.grid};
+    *out = aih_dwpw_plan{p.TH, p.TW, p.wx * p.wy, p.nb, (d->c + ec - 1) / ec, p.ntiles, p.lds, p.occ, p.grid};
     return AIH_OK;
   });
 }
@@ -492,7 +517,7 @@ int aih_conv_dwpw(const aih_dwpw_desc *d, const void *x, const void *w_dw, const
     a.act_p = d->act_pw;
     a.has_res = d->residual ? 1 : 0;
     a.nxcd = aih::device_xcds();
-    const hipError_t e = aih::launch_dw_pw(a, d->dt, d->k, d->s, p.wx * p.wy, p.lds, p.grid,
+    const hipError_t e = aih::launch_dw_pw(a, d->dt, d->k, d->s, p.nb, p.wx * p.wy, p.lds, p.grid,
                                            static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return dp_fail(std::string("dwpw launch: ") + hipGetErrorString(e));
     return AIH_OK;

@@ -462,7 +462,7 @@ bool fuse_pair(aih_model *m, size_t k, const std::vector<uint32_t> &readers, con
   d.residual = P.res >= 0 ? 1 : 0;
   d.dt = m->dt;
   aih_dwpw_plan plan;
-  if (aih_conv_dwpw_plan(&d, &plan) != AIH_OK || plan.tiles < 2 * aih::device_cus()) return false;
+  if (aih_conv_dwpw_plan(&d, &plan) != AIH_OK || plan.tiles < aih::device_cus()) return false;
   const int32_t bi = (int32_t)m->fused.size();
   m->fused.push_back(aih_model::Fused{(uint32_t)k, 2, aih_ir_block_desc{}, aih_ir_plan{}, d, plan});
   m->block_of[k] = m->block_of[k + 1] = bi;
@@ -481,10 +481,10 @@ bool fuse_pair(aih_model *m, size_t k, const std::vector<uint32_t> &readers, con
 //
 // Where no such block starts, an fp32 depthwise 3x3 (d = 1, square stride)
 // whose output only the next op, a 1x1 conv, reads runs with it as one
-// aih_conv_dwpw launch, when its plan has at least two tiles per CU (with
-// fewer, each CU walks one tile's channel chunks alone, and the fused launch
-// measured slower than the two: 20x36 stride 2, 96 -> 48 at batch 64, 24 vs
-// 22 us; at 80x144, 44 -> 24, 83 vs 100 us).
+// aih_conv_dwpw launch, when its plan has a tile for every CU (with fewer,
+// part of the GPU idles through the whole channel walk). Measured at batch
+// 64, fused against the two launches: 96 -> 48 stride 2 at 20x36 15 vs 22 us
+// (256 tiles), 44 -> 24 at 80x144 56 vs 89 us.
 void find_fusions(aih_model *m) {
   const auto &ops = m->g.ops;
   const auto &T = m->g.tensors;

@@ -32,8 +32,9 @@ The choice per block is recorded (choice_map()) and can be given back
 (choices={block: label}), so a later load runs exactly the same kernels; a
 label is "unfused", "fused THxTW" (the tile kernel, streamed weights),
 "fused THxTW resident", "wave THxTW[ resident]" (the wave kernel),
-"split THxTW wN" (the split kernel, N wavefronts per tile) or "dwpw THxTW"
-(expand, then the fused depthwise + projection at that tile) --
+"split THxTW wN" (the split kernel, N wavefronts per tile) or "dwpw THxTW rR"
+(expand, then the fused depthwise + projection at that tile, R output rows
+per wavefront) --
 fused_candidates() and dwpw_candidates() list the labels a block can take.
 """
 from __future__ import annotations
@@ -202,13 +203,15 @@ class Model:
     @classmethod
     def dwpw_candidates(cls, spec: conv.DwPwSpec) -> list[tuple[str, conv.DwPwSpec]]:
         """The fused depthwise + projection launches the tuner times after the
-        expand conv: every DWPW_TILES entry that fits, as (label, spec with the
-        tile forced); none for a pair aih_conv_dwpw cannot run."""
+        expand conv: every DWPW_TILES entry with 4 and with 2 output rows per
+        wavefront that fits, as (label, spec with tile and rows forced); none
+        for a pair aih_conv_dwpw cannot run."""
         out = []
         for t in cls.DWPW_TILES:
-            sp = dataclasses.replace(spec, tile=t)
-            if sp.fusable():
-                out.append((f"dwpw {t[0]}x{t[1]}", sp))
+            for rows in (4, 2):
+                sp = dataclasses.replace(spec, tile=t, rows=rows)
+                if sp.fusable():
+                    out.append((f"dwpw {t[0]}x{t[1]} r{rows}", sp))
         return out
 
     @classmethod
@@ -250,12 +253,12 @@ class Model:
     def parse_label(label: str):
         """"unfused" -> None; "fused|wave THxTW[ resident]" or "split THxTW wN"
         -> (IrKernel, (th, tw), IrWeights, wavefronts or 0); "dwpw THxTW" ->
-        ("dwpw", (th, tw), None, 0)."""
+        ("dwpw", (th, tw), None, rows per wavefront)."""
         if label == "unfused":
             return None
-        m = re.fullmatch(r"dwpw (\d+)x(\d+)", label)
+        m = re.fullmatch(r"dwpw (\d+)x(\d+) r([24])", label)
         if m:
-            return "dwpw", (int(m.group(1)), int(m.group(2))), None, 0
+            return "dwpw", (int(m.group(1)), int(m.group(2))), None, int(m.group(3))
         m = re.fullmatch(r"split (\d+)x(\d+) w(\d+)", label)
         if m:
             return conv.IrKernel.SPLIT, (int(m.group(1)), int(m.group(2))), conv.IrWeights.AUTO, int(m.group(3))
@@ -284,7 +287,7 @@ class Model:
             return [self._conv_op(Lr, packed, L) for Lr in (e, d, p)]
         kernel, tile, w, waves = forced
         if kernel == "dwpw":
-            sp = dataclasses.replace(self._dwpw_spec(d, p), tile=tile)
+            sp = dataclasses.replace(self._dwpw_spec(d, p), tile=tile, rows=waves)
             if not sp.fusable():
                 raise conv.AihError(f"{self._block_name(p)}: {label!r}: {conv.last_error()}")
             return [self._conv_op(e, packed, L), self._dwpw_op(d, p, sp, packed, L)]

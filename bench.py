@@ -289,7 +289,7 @@ def profile_config(args, torch, conv, W, Model, dev, DT) -> int:
             run(y, ws)
     elif cfg[0] == "chain":
         layers, meta = W.ir_chain_40x72(64)
-        # --choices as the bench's block_choices (e.g. "dwpw 16x16" per block), else three launches per block
+        # --choices as the bench's block_choices (e.g. "dwpw 16x16 r4" per block), else three launches per block
         m4 = Model(layers, W.make_weights(layers, seed=1), meta["n"], meta["h"], meta["w"], meta["c"], dt=DT["f32"],
                    tune=False, choices=json.loads(args.choices) if args.choices else None)
         m4.tensors["input"].uniform_(-1, 1)

@@ -302,14 +302,15 @@ typedef struct {
   int32_t act_dw, act_pw;  /* enum aih_act */
   int32_t residual;        /* 0 or 1: y = act_pw(...) + res */
   int32_t dt;              /* AIH_F32 */
-  uint32_t tile_h, tile_w; /* output tile: 4 x 16 multiples of at most 4 wavefronts; 0 = chosen by the plan */
+  uint32_t tile_h, tile_w; /* output tile (16-column multiples, 1-8 wavefronts); 0 = chosen by the plan */
+  uint32_t wave_rows;      /* output rows per wavefront, 2 or 4; 0 = chosen by the plan */
 } aih_dwpw_desc;
 
-/* Geometry aih_conv_dwpw_plan chose: output tile th x tw (a wavefront per 4
- * rows x 16 columns), channel chunks of 16, tiles (one workgroup each), LDS
- * bytes and resident workgroups per CU, launched workgroups. */
+/* Geometry aih_conv_dwpw_plan chose: output tile th x tw (a wavefront per
+ * wave_rows rows x 16 columns), channel chunks of 16, tiles (one workgroup
+ * each), LDS bytes and resident workgroups per CU, launched workgroups. */
 typedef struct {
-  uint32_t th, tw, waves, chunks, tiles, lds_bytes, occupancy, grid;
+  uint32_t th, tw, waves, wave_rows, chunks, tiles, lds_bytes, occupancy, grid;
 } aih_dwpw_plan;
 
 int aih_conv_dwpw_plan(const aih_dwpw_desc *d, aih_dwpw_plan *out);

@@ -82,19 +82,22 @@ def test_dwpw_matches_two_ops(case):
     assert err <= TOL, (cs.spec().plan(), err)
 
 
-TILES = [(4, 16), (4, 32), (8, 16), (4, 64), (8, 32), (16, 16)]
+# (tile, output rows per wavefront): every shape the planner can choose
+TILES = [((4, 16), 4), ((4, 32), 4), ((8, 16), 4), ((4, 64), 4), ((8, 32), 4), ((16, 16), 4),
+         ((4, 16), 2), ((4, 32), 2), ((8, 16), 2), ((4, 64), 2), ((8, 32), 2), ((16, 16), 2)]
 
 
-@pytest.mark.parametrize("tile", TILES, ids=lambda t: f"{t[0]}x{t[1]}")
+@pytest.mark.parametrize("tile", TILES, ids=lambda t: f"{t[0][0]}x{t[0][1]}r{t[1]}")
 @pytest.mark.parametrize("s", [1, 2])
 def test_dwpw_every_tile(tile, s):
     """Every tile shape the planner can choose, forced, on one case per stride."""
+    (th, tw), rows = tile
     cs = DwPwCase(2, 19, 43, 52, 36, s, (1, 1, 1, 1), True, "relu", "relu6", seed=7 + s)
-    spec = cs.spec(tile=tile)
+    spec = cs.spec(tile=(th, tw), rows=rows)
     if not spec.fusable():
-        pytest.skip(f"tile {tile} does not fit at stride {s}: {conv.last_error()}")
+        pytest.skip(f"tile {th}x{tw} r{rows} does not fit at stride {s}: {conv.last_error()}")
     p = spec.plan()
-    assert (p.th, p.tw) == tile
+    assert (p.th, p.tw, p.wave_rows, p.waves) == (th, tw, rows, th // rows * (tw // 16))
     err = rel_err(cs.run(spec), cs.want)
     assert err <= TOL, (p, err)
 
