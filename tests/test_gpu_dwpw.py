@@ -70,6 +70,8 @@ CASES = [
     (1, 16, 16, 16, 64, 2, (1, 1, 1, 1), False, "none", "none"),      # one chunk, four output blocks
     (2, 13, 29, 64, 40, 1, (0, 1, 2, 1), True, "relu", "relu"),       # asymmetric padding
     (1, 12, 20, 32, 2, 1, (1, 1, 1, 1), False, "relu", "none"),       # two outputs (c4 padding)
+    (2, 17, 23, 42, 20, 1, (1, 1, 1, 1), True, "relu6", "relu"),      # channels no multiple of 4 (c4 padding)
+    (1, 18, 26, 42, 36, 2, (1, 1, 1, 1), False, "relu", "none"),      # the same at stride 2
 ]
 
 

@@ -41,6 +41,21 @@ def _poison(y, dt):
         y.fill_(0x7e00 if dt == D.F16 else 0x7fc0)
 
 
+def _diff(y, ref, dt):
+    """Where a replay's output differs from the eager one: how many elements,
+    how many of them still hold the NaN poison (never written), the largest
+    difference among the written ones and the first differing index."""
+    f = y.float() if dt == D.F32 else (y.view(torch.float16) if dt == D.F16 else y.view(torch.bfloat16)).float()
+    g = ref.float() if dt == D.F32 else (ref.view(torch.float16) if dt == D.F16 else ref.view(torch.bfloat16)).float()
+    bad = (f != g) & ~(torch.isnan(f) & torch.isnan(g))
+    nan = bad & torch.isnan(f)
+    written = bad & ~torch.isnan(f)
+    idx = torch.nonzero(bad)
+    md = float((f[written] - g[written]).abs().max()) if written.any() else 0.0
+    return (f"{int(bad.sum())} of {f.numel()} elements differ, {int(nan.sum())} unwritten (NaN), "
+            f"max |diff| of the written {md:.3e}, first at {int(idx[0]) if len(idx) else -1}")
+
+
 def _cases(gen):
     """(name, spec, launch(stream), output buffer, its dtype, expected plan variant)"""
     out = []
@@ -108,8 +123,8 @@ def test_graph_replays_match_eager():
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
-        for (name, _, _, y, _, _), ref in zip(cases, want):
+        for (name, _, _, y, dt, _), ref in zip(cases, want):
             same = torch.equal(y, ref)
             print(f"replay {rep} {name}: {'bit-identical' if same else 'DIFFERS'}", flush=True)
-            assert same, f"replay {rep}: {name} differs from the eager launch"
+            assert same, f"replay {rep}: {name} differs from the eager launch: {_diff(y, ref, dt)}"
             assert not torch.isnan(ref if ref.dtype == torch.float32 else ref.view(torch.float16)).any(), name
