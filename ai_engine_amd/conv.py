@@ -471,7 +471,6 @@ class IrBlockSpec:
     dt: DType = DType.F32
     n: int = 1
     tile: tuple = (0, 0)  # forced output tile (h, w); (0, 0) = plan's choice
-    rows: int = 0         # forced output rows per wavefront (2 or 4); 0 = plan's choice
     ec: int = 0           # forced expanded channels per chunk; 0 = plan's choice
     weights: int = 0      # IrWeights: 0 = plan's choice, 1 = resident in LDS, 2 = streamed
     kernel: int = 0       # IrKernel: 0 = plan's choice, 1 = tile, 2 = wave, 3 = split kernel

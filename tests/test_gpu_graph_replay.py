@@ -77,7 +77,8 @@ def _cases(gen):
     sp = conv.ConvIgemmSpec(ih=40, iw=72, cin=72, cout=32, k=3, pad=(1, 1, 1, 1), act=A.RELU, residual=True,
                             dt=D.F16, n=2, srcs=[conv.SrcView(c=48), conv.SrcView(c=24)])
     xs = [_rnd(gen, 2 * 40 * 72 * 48, D.F16), _rnd(gen, 2 * 40 * 72 * 24, D.F16)]
-    w, b = _rnd(gen, 9 * 72 * 32, D.F16, 0.1), _rnd(gen, 32, D.F16, 0.01)
+    # packed weights [tap][kg_pad][32 outputs][4]: 72 channels = 18 groups, padded to 20
+    w, b = _rnd(gen, 9 * 20 * 32 * 4, D.F16, 0.1), _rnd(gen, 32, D.F16, 0.01)
     r = _rnd(gen, 2 * 40 * 72 * 32, D.F16)
     y = _nan(2 * 40 * 72 * 32, D.F16)
     out.append(("igemm direct", sp, lambda st, sp=sp, xs=xs, w=w, b=b, r=r, y=y: sp.run(xs, w, b, r, y, None, st), y,
