@@ -16,7 +16,7 @@ namespace aih {
 // such as 44 pads its last chunk by a third). In LDS a halo pixel takes one
 // more unit, the pad: an odd number of units puts the 16 consecutive pixels
 // one ds_read_b128 reads in distinct banks.
-constexpr int dwpw_units(int s) { return s > 0 ? 4 : 4; }
+constexpr int kDpUnits = 4;
 // Most 64-slot rows of the halo region one wavefront copies per chunk (its
 // slot offsets stay in registers for the whole launch): 10 at stride 1 (the
 // shapes the planner tries need at most 9), 24 at stride 2.
@@ -39,7 +39,7 @@ struct DwPwArgs {
   uint32_t HWE;      // stride 2: columns of the even half (ceil(HW / 2)); halo columns are stored even first
   uint32_t tiles_x, per_img, ntiles;
   FastDiv fd_pi, fd_tx, fd_hw;
-  uint32_t nchunks;    // chunks of 4 * dwpw_units(S) channels of C
+  uint32_t nchunks;    // chunks of 4 * kDpUnits channels of C
   uint32_t xrows;      // 64-slot rows (1 KB) of the halo region: HH * HW * (U + 1) slots rounded up
   uint32_t buf_bytes;  // one LDS chunk buffer
   uint32_t off_wd;     // inside a buffer: depthwise weights [K*K][U units], bias [U], pointwise weights [U][COP][4]
@@ -58,14 +58,14 @@ inline bool dwpw_has_cout(uint32_t cout) { return cout >= 1 && cout <= 64; }
 inline uint32_t dwpw_no(uint32_t cout) { return (cout + 15) / 16; }
 
 // 64-slot rows of the halo region of a chunk buffer for a halo of hh x hw pixels.
-inline uint32_t dwpw_xrows(uint32_t s, uint32_t hh, uint32_t hw) {
-  return (hh * hw * (dwpw_units((int)s) + 1) + 63) / 64;
+inline uint32_t dwpw_xrows(uint32_t hh, uint32_t hw) {
+  return (hh * hw * (kDpUnits + 1) + 63) / 64;
 }
 
 // LDS bytes of one chunk buffer: the halo region, then the weights.
 inline uint32_t dwpw_buf_bytes(uint32_t k, uint32_t s, uint32_t hh, uint32_t hw, uint32_t cout) {
-  const uint32_t u = dwpw_units((int)s), cop = dwpw_no(cout) * 16;
-  return dwpw_xrows(s, hh, hw) * 1024 + (k * k * u + u + u * cop) * 16;
+  const uint32_t u = kDpUnits, cop = dwpw_no(cout) * 16;
+  return dwpw_xrows(hh, hw) * 1024 + (k * k * u + u + u * cop) * 16;
 }
 
 // rows: output rows per wavefront (2 or 4).

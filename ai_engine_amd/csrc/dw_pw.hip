@@ -17,8 +17,8 @@
 //
 // Decomposition (MI355X): a workgroup owns an output tile of wy * NB rows x
 // wx * 16 columns of one image (NB = 4 or 2 rows per wavefront, up to 8
-// wavefronts) and walks the depthwise channels in chunks of
-// 16. Per chunk the tile's input halo (the chunk's 64 bytes of every pixel)
+// wavefronts) and walks the depthwise channels in chunks of 16. Per chunk
+// the tile's input halo (the chunk's 64 bytes of every pixel)
 // and the chunk's weights are copied global -> LDS by LDS-direct buffer loads
 // (no registers; zeros outside the image from the range check) into one of
 // two buffers, the next chunk's copy overlapping the current chunk's compute,
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(512) void dw_pw_kernel(DwPwArgs a) {
     const uint32_t cur = c & 1;
     const char *B = lds + cur * a.buf_bytes;
     const char *W = B + a.off_wd;
-    // lane group kq takes units kq and kq + 4 (U = 8) of the chunk
+    // lane group kq takes unit kq of the chunk (and kq + 4, ... for U > 4)
 #pragma unroll
     for (int h = 0; h < U / 4; ++h) {
       const uint32_t u = 4 * h + kq;
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(512) void dw_pw_kernel(DwPwArgs a) {
 template <int K, int S, int NO, int NB, bool CL>
 hipError_t prepare_inst() {
   static const hipError_t e =
-      hipFuncSetAttribute(reinterpret_cast<const void *>(dw_pw_kernel<K, S, NO, dwpw_units(S), NB, CL>),
+      hipFuncSetAttribute(reinterpret_cast<const void *>(dw_pw_kernel<K, S, NO, kDpUnits, NB, CL>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   return e;
 }
@@ -269,7 +269,7 @@ template <int K, int S, int NO, int NB, bool CL>
 hipError_t launch_inst(const DwPwArgs &a, uint32_t waves, uint32_t lds, uint32_t grid, hipStream_t st) {
   const hipError_t e = prepare_inst<K, S, NO, NB, CL>();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((dw_pw_kernel<K, S, NO, dwpw_units(S), NB, CL>), dim3(grid), dim3(64 * waves), lds, st, a);
+  hipLaunchKernelGGL((dw_pw_kernel<K, S, NO, kDpUnits, NB, CL>), dim3(grid), dim3(64 * waves), lds, st, a);
   return hipGetLastError();
 }
 
@@ -277,7 +277,7 @@ template <int K, int S, int NO, int NB, bool CL>
 int occ_inst(uint32_t waves, uint32_t lds) {
   if (prepare_inst<K, S, NO, NB, CL>() != hipSuccess) return 0;
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, dw_pw_kernel<K, S, NO, dwpw_units(S), NB, CL>,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, dw_pw_kernel<K, S, NO, kDpUnits, NB, CL>,
                                                    (int)(64 * waves), lds) != hipSuccess)
     return 0;
   return per_cu;
@@ -399,7 +399,7 @@ bool dp_plan(const aih_dwpw_desc *d, uint32_t oh, uint32_t ow, DwPwPlan *out) {
     p.HH = (p.TH - 1) * d->s + d->k;
     p.HW = (p.TW - 1) * d->s + d->k;
     p.HWE = d->s == 2 ? (p.HW + 1) / 2 : 0;
-    p.xrows = aih::dwpw_xrows(d->s, p.HH, p.HW);
+    p.xrows = aih::dwpw_xrows(p.HH, p.HW);
     if (p.xrows > waves * aih::dwpw_slots(d->s)) continue;
     p.buf_bytes = aih::dwpw_buf_bytes(d->k, d->s, p.HH, p.HW, d->cout);
     p.lds = 2 * p.buf_bytes;
@@ -461,7 +461,7 @@ int aih_conv_dwpw_plan(const aih_dwpw_desc *d, aih_dwpw_plan *out) {
     if (!out) return dp_fail("dwpw: null plan");
     DwPwPlan p;
     if (!dp_plan(d, oh, ow, &p)) return AIH_ERR;
-    const uint32_t ec = 4 * aih::dwpw_units(d->s);
+    const uint32_t ec = 4 * aih::kDpUnits;
     *out = aih_dwpw_plan{p.TH, p.TW, p.wx * p.wy, p.nb, (d->c + ec - 1) / ec, p.ntiles, p.lds, p.occ, p.grid};
     return AIH_OK;
   });
@@ -509,7 +509,7 @@ int aih_conv_dwpw(const aih_dwpw_desc *d, const void *x, const void *w_dw, const
     a.fd_pi = aih::make_fastdiv(a.per_img);
     a.fd_tx = aih::make_fastdiv(p.tiles_x);
     a.fd_hw = aih::make_fastdiv(p.HW);
-    a.nchunks = (a.C + 4 * aih::dwpw_units(d->s) - 1) / (4 * aih::dwpw_units(d->s));
+    a.nchunks = (a.C + 4 * aih::kDpUnits - 1) / (4 * aih::kDpUnits);
     a.xrows = p.xrows;
     a.buf_bytes = p.buf_bytes;
     a.off_wd = p.xrows * 1024;
