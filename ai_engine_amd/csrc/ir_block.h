@@ -66,6 +66,17 @@ hipError_t launch_ir_block(const IrArgs &a, int dt, uint32_t lds, uint32_t grid,
 constexpr int IRW_THREADS = 512;              // the most threads a workgroup has (8 wavefronts)
 constexpr uint32_t IRW_RPE = 32 * 2 + 16;     // expanded-chunk LDS row pitch: 32 16-bit channels + 16 bytes
 constexpr uint32_t IRW_SMB = 11 * 32 * 2;     // per chunk: 9 depthwise taps, depthwise bias, expand bias
+// bf16 with resident weights: per chunk, the 9 depthwise taps' odd channels
+// as 32-bit words with the even half zeroed (the taps in the slot keep the
+// even channels, odd half zeroed): v_dot2 operands without per-use masking
+constexpr uint32_t IRW_HI_BYTES = 9 * 32 * 2;
+// The wave kernel instantiations that split the bf16 taps: where the
+// registers held across a chunk (halo operands, expand operands,
+// projection accumulators: 4 NPI KE + 4 KE + 16 NOB) leave room for the odd
+// taps beside the even ones (the wider shapes would spill).
+__host__ __device__ constexpr bool irw_bf16_split(uint32_t ke, uint32_t npi, uint32_t nob) {
+  return 4 * npi * ke + 4 * ke + 16 * nob <= 64;
+}
 
 struct IrWaveArgs {
   const void *x;         // [N][IH][IW][C]
@@ -84,6 +95,7 @@ struct IrWaveArgs {
   int32_t act_e, act_d, act_p, has_res;
   uint32_t nxcd;            // XCDs of the device (workgroup remap)
   uint32_t lds_w, lds_bp, lds_xe;  // LDS byte offsets: weight slots, fp32 projection bias, expanded regions
+  uint32_t lds_hi;                 // wave kernel, bf16, resident weights: odd-channel depthwise taps (IRW_HI_BYTES a chunk)
   uint32_t lds_red;                // split kernel: projection partial sums (over the regions below)
   uint32_t lds_x;                  // split kernel: the tile's input halo
   FastDiv fd_hw, fd_tw, fd_tx, fd_pi;
@@ -107,7 +119,7 @@ struct IrWavePlan {
   uint32_t TH, TW, HH, HW, NPI, resident;
   uint32_t waves;                       // wavefronts per workgroup (wave: 2, 4 or 8; split: 1, 2, 4 or 8)
   uint32_t tiles_y, tiles_x, ntiles;
-  uint32_t lds_w, lds_bp, lds_xe, lds_red, lds_x, lds;  // LDS byte offsets and total
+  uint32_t lds_w, lds_bp, lds_xe, lds_red, lds_x, lds_hi, lds;  // LDS byte offsets and total
   uint32_t occ, grid;                   // workgroups per CU, launched workgroups
 };
 

@@ -148,7 +148,8 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
           p.resident = resident;
           p.waves = waves;
           p.lds_w = 0;
-          p.lds_bp = align16((resident ? nchunks : 2u) * slot);
+          p.lds_hi = dt == DT_BF16 && resident && irw_bf16_split(ke, npi, nob) ? align16(nchunks * slot) : 0u;
+          p.lds_bp = align16(p.lds_hi ? p.lds_hi + nchunks * IRW_HI_BYTES : (resident ? nchunks : 2u) * slot);
           p.lds_xe = align16(p.lds_bp + CO * 4);
           p.lds_red = 0;
           p.lds = p.lds_xe + waves * npi * 32 * IRW_RPE;

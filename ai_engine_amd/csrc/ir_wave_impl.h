@@ -182,6 +182,23 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   }
   ir_dma_wait();
   __syncthreads();
+  constexpr bool BSPLIT = DT == DT_BF16 && irw_bf16_split(KE, NPI, NOB);
+  if constexpr (BSPLIT) {
+    if (a.resident) {
+      // every chunk's depthwise taps split by channel parity, once: the
+      // slot keeps the even channels (odd halves zeroed), lds_hi gets the
+      // odd ones (even halves zeroed)
+      constexpr uint32_t TW = 9 * EC / 2;  // 32-bit words of one chunk's taps
+      for (uint32_t i = tid; i < nchunks * TW; i += nthr) {
+        const uint32_t c = i / TW, r = i - c * TW;
+        uint32_t *wlo = reinterpret_cast<uint32_t *>(WL + c * SLOT + WES + WPS) + r;
+        const uint32_t w = *wlo;
+        *wlo = w & 0x0000ffffu;
+        reinterpret_cast<uint32_t *>(lds + a.lds_hi + c * IRW_HI_BYTES)[r] = w & 0xffff0000u;
+      }
+      __syncthreads();
+    }
+  }
 
   // this workgroup's contiguous range of tiles (handed out XCD by XCD)
   const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x, a.nxcd);
@@ -235,8 +252,10 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   };
 
   // expand of chunk `slot` over the halo tile -> this wavefront's XeL, then
-  // its depthwise + projection into acc
-  auto run_chunk = [&](const char *slot) {
+  // its depthwise + projection into acc; hi: the chunk's odd-channel taps
+  // (bf16 with resident weights, the slot's taps then hold the even ones),
+  // else null
+  auto run_chunk = [&](const char *slot, const char *hi) {
     // expand A operands of the chunk: channel l32, K groups from 2 * lh; a K
     // step advances 4 groups of 32 channels (1024 bytes)
     const char *ap = slot + ((uint32_t)lh * (HK / 4) * EC + l32) * GB;
@@ -277,6 +296,18 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
 #pragma unroll
         for (int t = 0; t < TB; ++t)
           xv[t] = *reinterpret_cast<const u32x4 *>(XeL + rowo[(t0 + t) / 3] + ((t0 + t) % 3) * IRW_RPE + ks * 32);
+        if constexpr (BSPLIT) {
+          if (hi) {
+            u32x4 wh[TB];
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+              wh[t] = *reinterpret_cast<const u32x4 *>(hi + lh * 16 + (t0 + t) * (EC * ES) + ks * 32);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < TB; ++t) ir_fma_taps_bf16_split<HK>(xv[t], wv[t], wh[t], d);
+            continue;
+          }
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
@@ -322,7 +353,8 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
     // every chunk in LDS: the wavefronts run their tiles independently
     for (uint32_t T = t_begin + wave; T < t_end; T += nwaves) {
       begin_tile(T);
-      for (uint32_t c = 0; c < nchunks; ++c) run_chunk(WL + c * SLOT);
+      for (uint32_t c = 0; c < nchunks; ++c)
+        run_chunk(WL + c * SLOT, BSPLIT ? lds + a.lds_hi + c * IRW_HI_BYTES : nullptr);
       end_tile();
     }
     return;
@@ -344,7 +376,7 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
       __syncthreads();
       const bool last = c + 1 == nchunks;
       if (!last || more) dma_chunk(last ? 0 : c + 1, (gc + 1) & 1);
-      if (active) run_chunk(WL + (gc & 1) * SLOT);
+      if (active) run_chunk(WL + (gc & 1) * SLOT, nullptr);
     }
     if (active) end_tile();
   }
