@@ -128,6 +128,16 @@ struct IrWavePlan {
 // depthwise taps and biases; partial sums: NOB blocks of 32 x 32 fp32 per
 // wavefront, over the rest once it is done with.
 constexpr uint32_t IRS_RING = 2 * IRW_SMB;
+// bf16 on the shapes with 2 halo blocks and at most 64 input channels: a
+// ring slot also holds its taps' odd-channel halves (the slot's own taps
+// then keep the even ones), split by the wavefront when they land. The wider
+// shapes keep masking per use: the extra operand registers cost them a
+// wavefront per SIMD (96 -> 384 -> 96 at 20x36 b64 bf16: 32 -> 41 us).
+constexpr uint32_t IRS_SLOT_BF16 = IRW_SMB + IRW_HI_BYTES;
+__host__ __device__ constexpr bool irs_bf16_split(uint32_t ke, uint32_t npi) { return ke <= 4 && npi == 2; }
+__host__ __device__ constexpr uint32_t irs_ring_bytes(int dt, uint32_t ke, uint32_t npi) {
+  return dt == 2 && irs_bf16_split(ke, npi) ? 2 * IRS_SLOT_BF16 : IRS_RING;
+}
 constexpr uint32_t IRS_RED_BLOCK = 32 * 32 * 4;
 
 // Chooses between the wave kernel and the split kernel (kernel: enum

@@ -67,7 +67,12 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
   constexpr uint32_t RPX = C * ES + 16;  // halo row pitch: the pixel's C channels + 16 bytes
   const char *XL = lds + a.lds_x;
   char *XeL = lds + a.lds_xe + wave * (NPI * 32 * IRW_RPE);
-  char *SmL = lds + a.lds_w + wave * (2 * IRW_SMB);
+  // ring slot s of this wavefront at SmL + s * SMS; BS (bf16 on the narrow
+  // shapes): the slot's taps split by channel parity (split_taps), the odd
+  // halves IRW_SMB bytes in
+  constexpr bool BS = DT == DT_BF16 && irs_bf16_split(KE, NPI);
+  constexpr uint32_t SMS = BS ? IRS_SLOT_BF16 : IRW_SMB;
+  char *SmL = lds + a.lds_w + wave * (2 * SMS);
   const Act act_e = act_params(a.act_e), act_d = act_params(a.act_d), act_p = act_params(a.act_p);
 
   const __amdgpu_buffer_rsrc_t rs_we = ir_rsrc(a.we, C * a.E * ES);
@@ -152,7 +157,7 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
   // (9 runs of 32 channels, then the two biases: the slot layout of the wave
   // kernel); this wavefront's LDS-direct loads, landed at its next ir_dma_wait
   auto load_small = [&](uint32_t c, uint32_t s) {
-    char *sm = SmL + s * IRW_SMB;
+    char *sm = SmL + s * SMS;
     constexpr uint32_t TR = EC * ES / 16;  // 16-byte items per tap run
     irw_dma<16>(sm, 9 * TR, rs_wd, 0, lane, 64,
                 [&](uint32_t g) -> uint32_t { return (g / TR) * a.E * ES + (g % TR) * 16; }, EC * c * ES);
@@ -160,6 +165,24 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
                EC * c * ES);
     irw_dma<4>(sm + 10 * EC * ES, EC * ES / 4, rs_be, 0, lane, 64, [&](uint32_t g) -> uint32_t { return g * 4; },
                EC * c * ES);
+  };
+
+  // BS: ring slot sm's taps (landed, this wavefront's own) split by
+  // channel parity -- even halves kept in place, odd halves IRW_SMB bytes
+  // in -- so each tap is two v_dot2c with no per-use masking; the
+  // wavefront's LDS accesses stay in issue order, no barrier
+  auto split_taps = [&](char *sm) {
+    if constexpr (BS) {
+      constexpr uint32_t TW = 9 * EC / 2;  // 32-bit words of one chunk's taps
+      uint32_t *lo = reinterpret_cast<uint32_t *>(sm), *hi = reinterpret_cast<uint32_t *>(sm + IRW_SMB);
+#pragma unroll
+      for (uint32_t i = (uint32_t)lane; i < TW; i += 64) {
+        const uint32_t w = lo[i];
+        lo[i] = w & 0x0000ffffu;
+        hi[i] = w & 0xffff0000u;
+      }
+      irw_wave_order();
+    }
   };
 
   f32x16 acc[NOB];
@@ -230,10 +253,11 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
     __syncthreads();
     for (uint32_t c = c_begin; c < c_end; ++c) {
       const uint32_t s = (c - c_begin) & 1;
-      const char *sm = SmL + s * IRW_SMB;
+      char *sm = SmL + s * SMS;
       // chunk c's small tensors have landed (and every earlier load)
       ir_dma_wait();
       irw_wave_order();
+      split_taps(sm);
       // the projection operands (both K steps' in flight during the expand)
       u32x4 wpv[NKS][NOB];
       if constexpr (WP_EARLY) load_wp_all(c, wpv);
@@ -267,9 +291,19 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
 #pragma unroll
           for (int t = 0; t < TB; ++t)
             xv[t] = *reinterpret_cast<const u32x4 *>(XeL + rowo[(t0 + t) / 3] + ((t0 + t) % 3) * IRW_RPE + ks * 32);
-          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (BS) {
+            u32x4 wh[TB];
 #pragma unroll
-          for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
+            for (int t = 0; t < TB; ++t)
+              wh[t] = *reinterpret_cast<const u32x4 *>(wdp + IRW_SMB + (t0 + t) * (EC * ES) + ks * 32);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < TB; ++t) ir_fma_taps_bf16_split<HK>(xv[t], wv[t], wh[t], d);
+          } else {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
+          }
         }
         u32x4 bop;
         if constexpr (RLD) {
@@ -303,9 +337,10 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
     // chunk c from ring slot s with expand operands `cur`; the next chunk's
     // into `nxt` and the other slot
     auto step = [&](uint32_t c, uint32_t s, u32x4 (&cur)[KE], u32x4 (&nxt)[KE]) {
-      const char *sm = SmL + s * IRW_SMB;
+      char *sm = SmL + s * SMS;
       ir_dma_wait();
       irw_wave_order();
+      split_taps(sm);
       u32x4 wpv[NKS][NOB];
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks)
@@ -331,9 +366,19 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
 #pragma unroll
           for (int t = 0; t < TB; ++t)
             xv[t] = *reinterpret_cast<const u32x4 *>(XeL + rowo[(t0 + t) / 3] + ((t0 + t) % 3) * IRW_RPE + ks * 32);
-          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (BS) {
+            u32x4 wh[TB];
 #pragma unroll
-          for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
+            for (int t = 0; t < TB; ++t)
+              wh[t] = *reinterpret_cast<const u32x4 *>(wdp + IRW_SMB + (t0 + t) * (EC * ES) + ks * 32);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < TB; ++t) ir_fma_taps_bf16_split<HK>(xv[t], wv[t], wh[t], d);
+          } else {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
+          }
         }
         ir_act<true, HK>(act_d, d);
         const u32x4 bop = ir_pack<DT, HK>(d);
