@@ -118,3 +118,43 @@ def test_dwpw_repeat_is_bit_identical():
     a = cs.run(cs.spec())
     b = cs.run(cs.spec())
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("case", [(40, 72, 256, 64, True, "relu", "none"), (80, 144, 44, 24, False, "relu", "relu")],
+                         ids=["ir_chain_256to64_40x72", "segm_head_44to24_80x144"])
+def test_dwpw_benched_routes_b64(case):
+    """The two pairs the bench times at batch 64 (the fp32 inverted-residual
+    chain's depthwise + projection, the real model's 44 -> 24 head pair),
+    launched over the whole batch with the planner's tile -- 8x16 tiles of
+    2-row wavefronts, the tuner's choice there -- and checked on sampled
+    images against the oracle's two ops (1e-4)."""
+    ih, iw, c, cout, res, act_d, act_p = case
+    n = 64
+    op_d = orc.conv2d(c, c, k=3, s=1, pad=[1, 1, 1, 1], groups=c, act=act_d)
+    op_p = orc.conv2d(c, cout, act=act_p)
+    oh, ow = orc.out_hw(op_d, ih, iw)
+    x = orc.xs32_fill(900 + c, n * ih * iw * c)
+    wd = orc.gauss_fill(901, 0.0, float(np.sqrt(2.0 / 9)), c * 9)
+    bd = orc.gauss_fill(902, 0.0, 0.01, c)
+    wp = orc.gauss_fill(903, 0.0, float(np.sqrt(2.0 / c)), cout * c)
+    bp = orc.gauss_fill(904, 0.0, 0.01, cout)
+    r = orc.xs32_fill(905, n * oh * ow * cout) if res else None
+    wpp, kgp = orc.pack_weights_conv(wp, cout, c, 1, 1, 4, 0)
+    spec = conv.DwPwSpec(ih=ih, iw=iw, c=c, cout=cout, act_dw=ACT[act_d], act_pw=ACT[act_p], residual=res, n=n,
+                         kg_pad=kgp)
+    p = spec.plan()
+    assert (p.th, p.tw, p.wave_rows) == (8, 16, 2), p
+    y = poisoned(n * oh * ow * (-(-cout // 4)) * 4, 0)
+    spec.run(dev(orc.pack_nhwc(x, n, ih, iw, c, 0)), dev(orc.pack_weights_dw(wd, c, 3, 3, 0)),
+             dev(orc.pack_bias(bd, c, 0)), dev(wpp), dev(orc.pack_bias(bp, cout, 0)),
+             dev(orc.pack_nhwc(r, n, oh, ow, cout, 0)) if res else None, y)
+    torch.cuda.synchronize()
+    got = orc.unpack_nhwc(host(y, 0), n, oh, ow, cout, 0).reshape(n, -1)
+    img_in, img_out = ih * iw * c, oh * ow * cout
+    worst = 0.0
+    for i in (0, 21, 42, 63):
+        d = orc.CpuConv(op_d, ih, iw, wd, bd).run(x[i * img_in:(i + 1) * img_in], 1, threads=8)
+        ri = r[i * img_out:(i + 1) * img_out] if res else None
+        want = orc.CpuConv(op_p, oh, ow, wp, bp, has_res=res).run(d, 1, ri, threads=8)
+        worst = max(worst, rel_err(got[i], want.reshape(-1)))
+    assert worst <= TOL, (p, worst)
