@@ -400,3 +400,34 @@ def test_conv_plan_reports_the_route():
     p = dw.plan()
     assert p.variant == conv.Variant.DIRECT and p.grid == 0 and p.ws_bytes == 0
     _expect_error(conv.ConvOp(ih=8, iw=8, cin=8, cout=8, sh=2, sw=2).plan, "stride/pad")
+
+
+# ---------------------------------------------------------------- fused depthwise -> pointwise (host side)
+
+@pytest.mark.parametrize("shape", [(40, 72, 256, 64, 1, 64), (80, 144, 44, 24, 1, 64), (20, 36, 96, 48, 2, 64),
+                                   (7, 5, 20, 12, 1, 1), (19, 43, 52, 36, 2, 2)])
+def test_dwpw_plan_covers_the_output_and_fits_lds(shape):
+    """aih_conv_dwpw_plan's tiles cover the output, its LDS fits the CU, and
+    the tile is a 16-column multiple of 2- or 4-row wavefronts (host only)."""
+    ih, iw, c, cout, s, n = shape
+    spec = conv.DwPwSpec(ih=ih, iw=iw, c=c, cout=cout, s=s, n=n)
+    p = spec.plan()
+    oh, ow = spec.out_hw()
+    assert p.wave_rows in (2, 4) and p.tw % 16 == 0 and p.th % p.wave_rows == 0
+    assert p.waves == (p.th // p.wave_rows) * (p.tw // 16) <= 8
+    assert p.tiles == n * -(-oh // p.th) * -(-ow // p.tw) == p.grid
+    assert p.chunks == -(-(-(-c // 4) * 4) // 16) and 0 < p.lds_bytes <= 160 * 1024
+
+
+def test_dwpw_rejects_what_it_cannot_run():
+    base = dict(ih=16, iw=16, c=32, cout=32)
+    for kw, msg in [(dict(dt=conv.DType.F16), "fp32"), (dict(k=5), "3x3"), (dict(cout=80), "cout"),
+                    (dict(s=3), "stride"), (dict(pad=(3, 1, 1, 1)), "padding"), (dict(kg_pad=4), "kg_pad"),
+                    (dict(tile=(4, 48)), "forced tile"), (dict(tile=(6, 16)), "forced tile"),
+                    (dict(rows=3), "forced tile")]:
+        spec = conv.DwPwSpec(**{**base, **kw})
+        assert not spec.fusable(), kw
+        _expect_error(spec.plan, msg)
+    d = conv.DwPwSpec(residual=True, **base).desc()
+    assert conv.lib().aih_conv_dwpw(C.byref(d), 16, 16, 16, 16, 16, None, 16, None) == -1
+    assert "res must be given" in conv.last_error()
