@@ -167,9 +167,12 @@ void fill_plan(const GemmPlan &g, aih_plan *out) {
 // plan stays a pure function of its descriptor within a run), as the
 // reference's AI_PW_SPLITK_NG (gemm_pw.rs:112-126) and AI_RT_FORCE_DIRECT
 // (lowering.rs:156-160) are:
-//   AIH_PW_SPLITK=<n>     pointwise convs with AIH_VAR_AUTO and no forced
-//                         split that run the tiled GEMM use n K chunks
-//                         (1 = never split);
+//   AIH_PW_SPLITK=<n>     every pointwise conv with AIH_VAR_AUTO and no
+//                         forced split is given n K chunks, as a forced split
+//                         is: the one-dispatch split-K kernel where its shape
+//                         allows, else the tiled GEMM (1 = no split); the
+//                         narrow, direct, LDS one-tap and streamed routes are
+//                         bypassed while it is set;
 //   AIH_IGEMM_NO_SPLIT=1  KxK convs with AIH_VAR_AUTO and no forced split
 //                         never split K.
 int env_int_once(const char *name, int *slot, std::once_flag *once) {

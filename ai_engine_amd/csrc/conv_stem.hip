@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "aih_device.h"
 #include "conv_stem.h"
@@ -192,15 +193,21 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
 // round and they all walk the blocks in step.
 template <int DT, int NOB, bool F32IN>
 hipError_t launch_one(const StemArgs &a, hipStream_t st, uint32_t *grid_out) {
-  static int per_cu = -1;
-  if (per_cu < 0) {
+  // workgroups per CU, asked once per process; a failed query (no device to
+  // ask) plans for eight and is not kept, so a later call asks again
+  static std::atomic<int> per_cu{-1};
+  int pc = per_cu.load(std::memory_order_relaxed);
+  if (pc < 0) {
     int v = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, conv_stem_kernel<DT, NOB, F32IN>, 256, 0) != hipSuccess ||
-        v < 1)
-      v = 8;  // no device to ask: eight workgroups per CU
-    per_cu = v;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, conv_stem_kernel<DT, NOB, F32IN>, 256, 0) == hipSuccess &&
+        v >= 1) {
+      per_cu.store(v, std::memory_order_relaxed);
+      pc = v;
+    } else {
+      pc = 8;
+    }
   }
-  const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblocks + 3) / 4, (uint64_t)device_cus() * per_cu);
+  const uint32_t wgs = (uint32_t)std::min<uint64_t>((a.nblocks + 3) / 4, (uint64_t)device_cus() * pc);
   if (grid_out) {
     *grid_out = wgs;
     return hipSuccess;

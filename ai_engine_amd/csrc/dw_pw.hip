@@ -275,11 +275,11 @@ hipError_t launch_inst(const DwPwArgs &a, uint32_t waves, uint32_t lds, uint32_t
 
 template <int K, int S, int NO, int NB, bool CL>
 int occ_inst(uint32_t waves, uint32_t lds) {
-  if (prepare_inst<K, S, NO, NB, CL>() != hipSuccess) return 0;
+  if (prepare_inst<K, S, NO, NB, CL>() != hipSuccess) return -1;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, dw_pw_kernel<K, S, NO, kDpUnits, NB, CL>,
                                                    (int)(64 * waves), lds) != hipSuccess)
-    return 0;
+    return -1;
   return per_cu;
 }
 
@@ -321,16 +321,17 @@ int dw_pw_occupancy(int dt, uint32_t k, uint32_t s, uint32_t cout, uint32_t rows
   const auto key = std::make_tuple(k, s, no, rows, cl, waves, lds, dev);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
-  int occ = -1;
+  int occ = -2;
 #define AIH_DP_OCC(K_, S_, NO_)                                                                           \
   if (k == K_ && s == S_ && no == NO_)                                                                      \
     occ = rows == 2 ? (cl ? occ_inst<K_, S_, NO_, 2, true>(waves, lds) : occ_inst<K_, S_, NO_, 2, false>(waves, lds)) \
                     : (cl ? occ_inst<K_, S_, NO_, 4, true>(waves, lds) : occ_inst<K_, S_, NO_, 4, false>(waves, lds));
   AIH_DP_SHAPES(AIH_DP_OCC)
 #undef AIH_DP_OCC
-  if (occ < 0) return 0;
-  // without a device the runtime cannot answer: plan for one workgroup per CU
-  if (occ == 0) occ = 1;
+  if (occ == -2) return 0;  // no instantiation
+  // a failed query (no device to ask): plan for one workgroup per CU, and
+  // ask again next time; a real answer, 0 included, is kept
+  if (occ < 0) return 1;
   cache[key] = occ;
   return occ;
 }

@@ -34,8 +34,10 @@ int reg_occupancy(int dt, uint32_t nob, uint32_t npw, bool cl) {
     case DT_BF16: occ = ir_occ_bf16(nob, npw, cl, 0); break;
     default: break;
   }
-  // Without a device the runtime cannot answer; plan for one workgroup per CU.
-  if (occ <= 0) occ = 1;
+  // A failed query (no device to ask): plan for one workgroup per CU, and
+  // ask again next time; a real answer, 0 included, is kept (the planner
+  // then skips the shape).
+  if (occ < 0) return 1;
   cache[key] = occ;
   return occ;
 }

@@ -549,11 +549,11 @@ inline hipError_t ir_launch_inst(const IrArgs &a, uint32_t lds, uint32_t grid, h
 // (registers and LDS both counted by the runtime).
 template <int DT, int NOB, int NPW, bool CL>
 inline int ir_occ_inst(uint32_t lds) {
-  if (ir_prepare_inst<DT, NOB, NPW, CL>() != hipSuccess) return 0;
+  if (ir_prepare_inst<DT, NOB, NPW, CL>() != hipSuccess) return -1;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_block_kernel<DT, NOB, NPW, CL>, 256, lds) !=
       hipSuccess)
-    return 0;
+    return -1;
   return per_cu;
 }
 

@@ -446,11 +446,11 @@ inline hipError_t irs_launch_inst(const IrWaveArgs &a, uint32_t waves, uint32_t 
 
 template <int DT, int KE, int NPI, int NOB, bool RL, bool DP>
 inline int irs_occ_inst(uint32_t waves, uint32_t lds) {
-  if (irs_prepare_inst<DT, KE, NPI, NOB, RL, DP>() != hipSuccess) return 0;
+  if (irs_prepare_inst<DT, KE, NPI, NOB, RL, DP>() != hipSuccess) return -1;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_split_kernel<DT, KE, NPI, NOB, RL, DP>,
                                                    (int)(64 * waves), lds) != hipSuccess)
-    return 0;
+    return -1;
   return per_cu;
 }
 

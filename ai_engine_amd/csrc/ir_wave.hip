@@ -40,8 +40,9 @@ int irw_occupancy(int split, int dt, uint32_t ke, uint32_t npi, uint32_t nob, bo
                        : ir_split_occ_bf16(ke, npi, nob, rl, split == 2, waves, lds);
   else
     occ = dt == DT_F16 ? ir_wave_occ_f16(ke, npi, nob, rl, waves, lds) : ir_wave_occ_bf16(ke, npi, nob, rl, waves, lds);
-  // without a device the runtime cannot answer: plan for one workgroup per CU
-  if (occ <= 0) occ = 1;
+  // a failed query (no device to ask): plan for one workgroup per CU, and
+  // ask again next time; a real answer, 0 included, is kept
+  if (occ < 0) return 1;
   cache[key] = occ;
   return occ;
 }
@@ -155,6 +156,7 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
           p.lds = p.lds_xe + waves * npi * 32 * IRW_RPE;
           if (p.lds > 160u * 1024u) continue;
           p.occ = (uint32_t)irw_occupancy(0, dt, ke, npi, nob, rl, waves, p.lds);
+          if (p.occ == 0) continue;  // not resident at this size
           p.tiles_y = tiles_y;
           p.tiles_x = tiles_x;
           p.ntiles = nt;
@@ -192,10 +194,11 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
         p.lds = p.lds_x + std::max(p.lds_w + w * irs_ring_bytes(dt, ke, npi) - p.lds_x, w * nob * IRS_RED_BLOCK);
         if (p.lds > 160u * 1024u) continue;
         p.occ = (uint32_t)irw_occupancy(1, dt, ke, npi, nob, rl, w, p.lds);
+        if (p.occ == 0) continue;  // not resident at this size
         // the deep prefetch where its registers cost no workgroup this
         // launch would have resident
         const uint32_t occ_deep = (uint32_t)irw_occupancy(2, dt, ke, npi, nob, rl, w, p.lds);
-        p.deep = occ_deep >= std::min(p.occ, cdiv(nt, cus)) ? 1u : 0u;
+        p.deep = occ_deep > 0 && occ_deep >= std::min(p.occ, cdiv(nt, cus)) ? 1u : 0u;
         if (p.deep) p.occ = occ_deep;
         p.tiles_y = tiles_y;
         p.tiles_x = tiles_x;

@@ -400,11 +400,11 @@ inline hipError_t irw_launch_inst(const IrWaveArgs &a, uint32_t waves, uint32_t 
 
 template <int DT, int KE, int NPI, int NOB, bool RL>
 inline int irw_occ_inst(uint32_t waves, uint32_t lds) {
-  if (irw_prepare_inst<DT, KE, NPI, NOB, RL>() != hipSuccess) return 0;
+  if (irw_prepare_inst<DT, KE, NPI, NOB, RL>() != hipSuccess) return -1;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_wave_kernel<DT, KE, NPI, NOB, RL>, (int)(64 * waves),
                                                    lds) != hipSuccess)
-    return 0;
+    return -1;
   return per_cu;
 }
 

@@ -24,7 +24,6 @@
 #include <functional>
 #include <map>
 #include <memory>
-#include <set>
 #include <string>
 #include <vector>
 
@@ -407,21 +406,24 @@ bool dense_tid(const sw::Model &g, uint32_t tid) {
   return r.second == 0 && c4(g.tensors[r.first].c) == c4(g.tensors[tid].c);
 }
 
-// The tensors each op reads.
-std::set<uint32_t> reads_of(const sw::Op &op) {
-  std::set<uint32_t> r;
-  for (const sw::Part &p : op.srcs) r.insert(p.tid);
+// The tensors each op reads, one entry per operand slot: an op that reads a
+// tensor through two slots (a conv whose residual is its own input, a binary
+// op of a tensor with itself) counts as two readers of it, so no fusion rule
+// that asks for a single reader can drop a tensor the op still needs.
+std::vector<uint32_t> reads_of(const sw::Op &op) {
+  std::vector<uint32_t> r;
+  for (const sw::Part &p : op.srcs) r.push_back(p.tid);
   switch (op.kind) {
     case sw::OP_CONV:
-      r.insert(op.in);
-      if (op.res >= 0) r.insert((uint32_t)op.res);
+      r.push_back(op.in);
+      if (op.res >= 0) r.push_back((uint32_t)op.res);
       break;
     case sw::OP_BINARY:
-      r.insert(op.in);
-      if (op.opnd != sw::OPND_SCALAR && op.opnd != sw::OPND_CVEC) r.insert(op.b_tid);
+      r.push_back(op.in);
+      if (op.opnd != sw::OPND_SCALAR && op.opnd != sw::OPND_CVEC) r.push_back(op.b_tid);
       break;
     case sw::OP_GPOOL:
-    case sw::OP_RESIZE: r.insert(op.in); break;
+    case sw::OP_RESIZE: r.push_back(op.in); break;
     case sw::OP_CONCAT: break;
   }
   return r;

@@ -99,7 +99,9 @@ class ModelOp:
         oh, ow = p.out_hw()
         x = n * e.ih * e.iw * c4(e.cin) * act_bytes
         y = n * oh * ow * p.cout * act_bytes
-        r = y if p.res else 0
+        # a residual that is the block's own input is the tensor already
+        # counted in x: each tensor once (crates/ai-cpu/src/model.rs:241-272)
+        r = y if p.res and p.res != e.src else 0
         w = (e.cin * e.cout + d.k * d.k * d.cout + p.cin * p.cout) * w_bytes
         b = (e.cout + d.cout + p.cout) * act_bytes
         return x + y + r + w + b
@@ -167,6 +169,7 @@ class Model:
             i += 1
         # a stem that is the input's only reader reads the fp32 input itself
         self._x_f32 = None        # the uploaded fp32 input, held until the next upload
+        self._x_version = 0       # its version counter at the upload
         self._input_packed = True  # tensors["input"] holds the last upload
         self._stem_in = self._stem_input_op(layers, readers, packed, L)
 
@@ -421,7 +424,11 @@ class Model:
         """The next infer()'s input. With a stem as the first op the fp32
         tensor itself is the stem's input (no packed copy; the model holds
         it until the next upload, and it must not change before infer()
-        has run); otherwise it is packed into the input slot now."""
+        has run: an in-place torch write to it after the upload -- which
+        bumps the tensor's version counter -- makes infer() raise instead of
+        reading the new values; writes torch does not see, through its raw
+        pointer, are the caller's to order); otherwise it is packed into the
+        input slot now."""
         if self._stem_in is None:
             conv.pack_nhwc_device(x_nhwc_f32, self.n, self.ih, self.iw, self.cin, self.dt, self.tensors["input"],
                                   stream)
@@ -432,6 +439,7 @@ class Model:
             raise conv.AihError(f"upload_input: expected a contiguous float32 tensor of "
                                 f"{self.n * self.ih * self.iw * self.cin} values on {self.device}")
         self._x_f32 = x
+        self._x_version = x._version
         self._input_packed = False
         a = self._stem_in.args
         self._stem_in.args = (a[0], x.data_ptr()) + a[2:]
@@ -449,6 +457,9 @@ class Model:
         # op 0 reads the fp32 upload while it has not been packed into the
         # input slot; otherwise (no upload yet, or the slot written) the slot
         if i == 0 and self._stem_in is not None and not self._input_packed:
+            if self._x_f32._version != self._x_version:
+                raise conv.AihError("infer: the tensor given to upload_input was modified in place after the "
+                                    "upload; call upload_input again")
             return self._stem_in
         return self.ops[i]
 

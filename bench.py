@@ -4,14 +4,17 @@ Headline workload (value, frames/s): the MobileNetV4-small-width segmentation
 encoder at 160x288, batch 64, f16 storage with fp32 accumulation -- 32 convs
 (stem 3x3 s2 3->32, ten inverted-residual blocks, 1x1 head 128->2) with
 random He-init weights and U[-1,1) synthetic input already resident in HBM.
-One step = pack the fp32 NHWC input to NHWC-C4 on the device + all 32 convs.
+One step = all 32 convs from the resident logical NHWC fp32 input: the stem
+reads it directly and rounds each value to the storage dtype as it loads it
+(no separate pack launch).
 
 Also measured in the same run (the "kernels" object), each with absolute
 TFLOP/s, GB/s and its roofline fraction (t_roof / t_measured,
 t_roof = max(flops / MFMA peak, bytes / 8 TB/s)):
   pw_32to64_relu6_80x144            1x1 32->64 + ReLU6, [1,80,144,32] fp32
   pw_960to160_10x18_b1_splitk{1,4,8} 1x1 960->160, [1,10,18,960] fp32, split-K forced
-  pw_960to160_10x18_b256            the same layer at batch 256 (policy: four K chunks)
+  pw_960to160_10x18_b256[_splitk{1,4,8}] the same layer at batch 256 (policy: the
+                                     LDS-streamed GEMM, no split; forced 1/4/8)
   igemm3x3s2_16to32_relu_160x288_b32 3x3 s2 pad 1 16->32 + ReLU, [32,160,288,16] fp32
   igemm3x3s1_32to64_relu_80x144_b32  3x3 s1 pad 1 32->64 + ReLU, [32,80,144,32] fp32
   ir_block_chain_4x_64c_40x72_b64    4 inverted-residual blocks at [64,40,72,64] fp32
@@ -135,23 +138,24 @@ def main() -> int:
                   "max_ms": round(st[-1], 4), "frames_per_s_at_median": round(n / (st[NS // 2] / 1e3), 1)}
     log(f"per-step (events, {NS} steps): min {st[0]:.3f} median {st[NS // 2]:.3f} max {st[-1]:.3f} ms")
 
-    # per-op timing (HIP events on the launch stream), grouped by kernel instantiation
-    R = 5
+    # per-op timing, grouped by kernel instantiation: each launch of the step
+    # repeated R times back to back in a HIP graph on a capture stream, the
+    # graph replayed between HIP events (time_graph): no host launch cost and
+    # no event between the launches, so the figure is the kernel's own
+    # duration as a kernel trace of the step reports it. Every op reads its
+    # inputs and writes a separate output, so a repeat recomputes the same
+    # values from the same (L2 / Infinity-Cache-warm) inputs as in the step.
+    R = 10
     nops = len(model.ops)
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nops)]
-           for _ in range(R)]
-    for r in range(R):
-        model.upload_input(x)
-        for i in range(nops):
-            evs[r][i][0].record(stream)
-            model.launch_op(i)
-            evs[r][i][1].record(stream)
+    model.upload_input(x)
+    model.infer()
     torch.cuda.synchronize()
+    op_secs = [time_graph(torch, lambda r, st, i=i: model.launch_op(i, st), R) for i in range(nops)]
     act_b = 2 if args.dtype != "f32" else 4
     groups: dict[str, dict] = {}
     layer_rows = []
     for i, op in enumerate(model.ops):
-        t = sorted(evs[r][i][0].elapsed_time(evs[r][i][1]) for r in range(R))[R // 2] / 1e3
+        t = op_secs[i]
         fl, by = op.flops(n), op.bytes(n, act_b, act_b)
         key = kernel_key(conv, op, n, DT[args.dtype], args.dtype)
         g = groups.setdefault(key, dict(launches=0, secs=0.0, flops=0, bytes=0, grids=[]))
@@ -183,11 +187,15 @@ def main() -> int:
     roofline["traffic"] = measured_traffic(dom_key)
     roofline.update(kernel=dom_key, launches_per_step=dom["launches"], dispatch_threads=sorted(dom["grids"]),
                     avg_launch_us=round(dom["secs"] / dom["launches"] * 1e6, 2),
+                    timing=f"each launch {R} times back to back in a HIP graph, replayed between HIP events "
+                           "(the kernel's own duration, as rocprofv3's kernel trace of --profile-config "
+                           "encoder_160x288_b64 reports it)",
                     algorithmic_bytes_per_launch=int(dom["bytes"] / dom["launches"]),
                     algorithmic_flops_per_launch=int(dom["flops"] / dom["launches"]),
                     share_of_step=round(dom["secs"] / step_secs, 3))
     tot_fl, tot_by = W.totals(layers, n, act_b, act_b)
-    step_roof = roof(tot_fl, tot_by, gpu_ms / 1e3, args.dtype)
+    unfused_roof_s = sum(max(L.flops(n) / (PEAK_TF[args.dtype] * 1e12), L.bytes(n, act_b, act_b) / (HBM_GBS * 1e9))
+                         for L in layers)
     log(f"dominant kernel {dom_key}: {roofline}")
 
     # plain device copy of 1 GiB (the calibration kernel for HBM counters and
@@ -227,16 +235,17 @@ def main() -> int:
                    "storage": args.dtype, "accumulate": "f32", "step": "32 convs from the resident fp32 NHWC input (the stem rounds it to the storage dtype as it reads)"},
         "gpu_ms_per_step": round(gpu_ms, 4),
         "step_stats": step_stats,
-        "step_roofline": {"tflops": round(step_roof["tflops"], 2), "gbs": round(step_roof["gbs"], 1),
-                          "bound": step_roof["bound"], "frac": round(step_roof["frac"], 4),
-                          "algorithmic_flops": tot_fl, "algorithmic_bytes": tot_by,
-                          "note": "bytes of the unfused layers (expanded tensors included): a per-layer "
-                                  "roofline the fused blocks do not move; step_roofline_fused is the step's own"},
         "step_roofline_fused": {"roof_us": round(fused_roof_s * 1e6, 1), "bytes": fused_bytes,
+                                "flops": sum(op.flops(n) for op in model.ops),
                                 "frac": round(fused_roof_s / (gpu_ms / 1e3), 4),
-                                "note": "sum over the launches the step runs of max(flops / MFMA peak, "
-                                        "bytes / 8 TB/s), a fused block counting its input, output, residual "
-                                        "and weights only"},
+                                "note": "the step's own roofline: sum over the launches it runs of max(flops / "
+                                        "MFMA peak, bytes / 8 TB/s), each launch counting every tensor it reads "
+                                        "or writes once (a fused block: its input -- which is also its residual "
+                                        "-- its output and its weights; the expanded tensors never reach HBM)"},
+        "unfused_layers_reference": {"roof_us": round(unfused_roof_s * 1e6, 1), "bytes": tot_by, "flops": tot_fl,
+                                     "note": "the same sum over the 32 convs as separate layers (expanded "
+                                             "tensors written and read): bytes the fused step does not move, "
+                                             "a reference only, no fraction"},
         "block_choices": model.choice_map(),
         "roofline": roofline,
         "hbm_copy_gbs": round(copy_gbs, 1),
@@ -487,20 +496,22 @@ def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
     m4 = Model(layers, wts, meta["n"], meta["h"], meta["w"], meta["c"], dt=DT["f32"])
     m4.tensors["input"].uniform_(-1, 1)
     t = time_launches(torch, stream, lambda r: m4.infer(stream), 10)
-    fl, by = W.totals(layers, meta["n"], 4, 4)
+    fl = sum(op.flops(meta["n"]) for op in m4.ops)
+    by = sum(op.bytes(meta["n"], 4, 4) for op in m4.ops)
     row = roof(fl, by, t, "f32")
     row["launches"] = len(m4.ops)
     row["block_choices"] = {k: {"choice": v[0], "us": round(v[1], 2)} for k, v in m4.choices.items()}
-    row["per_layer_roofline_sum_us"] = sum(
-        max(L.flops(meta["n"]) / (PEAK_TF["f32"] * 1e12), L.bytes(meta["n"], 4, 4) / (HBM_GBS * 1e9))
-        for L in layers) * 1e6
-    row["frac_basis"] = "per layer: the unfused layers' bytes (the depthwise outputs included)"
     own_s = sum(max(op.flops(meta["n"]) / (PEAK_TF["f32"] * 1e12), op.bytes(meta["n"], 4, 4) / (HBM_GBS * 1e9))
                 for op in m4.ops)
+    row["frac"] = own_s / t
     row["own_roofline_us"] = own_s * 1e6
-    row["own_frac"] = own_s / t
-    row["own_note"] = ("sum over the launches run of max(flops / MFMA peak, bytes / 8 TB/s), a fused "
-                       "launch counting only the tensors it reads and writes")
+    row["frac_basis"] = ("the launches' own roofline: sum over the launches run of max(flops / MFMA peak, "
+                         "bytes / 8 TB/s), each launch counting every tensor it reads or writes once (the "
+                         "fused depthwise + projection never writes the depthwise output); bytes and gbs "
+                         "are those launches' bytes")
+    row["unfused_layers_roof_us"] = sum(
+        max(L.flops(meta["n"]) / (PEAK_TF["f32"] * 1e12), L.bytes(meta["n"], 4, 4) / (HBM_GBS * 1e9))
+        for L in layers) * 1e6
     res["ir_block_chain_4x_64c_40x72_b64"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
     log(f"ir chain: {row['us']:.1f} us frac {row['frac']:.3f}; blocks: " +
         ", ".join(f"{k} {v[0]} ({v[1]:.0f} us)" for k, v in m4.choices.items()))
@@ -561,7 +572,8 @@ def encoder_other(torch, W, Model, layers, wts, x, n, H, Wd, dtname, DT, stream)
                       for op in m.ops) / t
     row["frac_basis"] = ("the step's own roofline: sum over the launches run of max(flops / MFMA peak, "
                          "bytes / 8 TB/s), a fused block counting its input, output, residual and weights")
-    row["per_layer_frac"] = roof(fl, by, t, dtname)["frac"]
+    row["unfused_layers_roof_us"] = sum(
+        max(L.flops(n) / (PEAK_TF[dtname] * 1e12), L.bytes(n, 2, 2) / (HBM_GBS * 1e9)) for L in layers) * 1e6
     row["frames_per_s"] = n / t
     log(f"encoder {dtname}: {t * 1e3:.3f} ms {n / t:.0f} frames/s")
     return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}

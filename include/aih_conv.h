@@ -35,7 +35,10 @@
  * reference's AI_PW_SPLITK_NG, gemm_pw.rs:112-126, and AI_RT_FORCE_DIRECT,
  * lowering.rs:156-160); they apply to AIH_VAR_AUTO calls without a forced
  * split only, and the plan functions report their effect:
- *   AIH_PW_SPLITK=<n>     a pointwise conv on the tiled GEMM uses n K chunks (1 = no split)
+ *   AIH_PW_SPLITK=<n>     every AUTO pointwise conv gets n K chunks as a forced split does
+ *                         (the one-dispatch split-K kernel where the shape allows, else the
+ *                         tiled GEMM; 1 = no split): the narrow, direct, LDS one-tap and
+ *                         streamed routes are bypassed while it is set
  *   AIH_IGEMM_NO_SPLIT=1  a KxK conv never splits K
  */
 #ifndef AIH_CONV_H

@@ -356,6 +356,14 @@ def test_env_overrides_of_the_split_policy():
     assert _plan_in_subprocess({"AIH_PW_SPLITK": "1"}, PW_SPLITK_PROBE).split() == ["1", "8"]
     # malformed values are ignored
     assert int(_plan_in_subprocess({"AIH_PW_SPLITK": "x"}, PW_SPLITK_PROBE).split()[0]) == base
+    # the override applies to every AUTO pointwise call, routed as a forced
+    # split: a narrow head (one channel group) leaves its row kernel for the
+    # tiled GEMM while it is set (the header documents this)
+    narrow = ("from ai_engine_amd import conv\n"
+              "p = conv.GemmPwSpec(m=180, kg=32, ng=1).plan()\n"
+              "print(conv.Variant(p.variant).name, p.splitk)\n")
+    assert _plan_in_subprocess({"AIH_PW_SPLITK": ""}, narrow).split()[0] == "ROWS"
+    assert _plan_in_subprocess({"AIH_PW_SPLITK": "2"}, narrow).split() == ["SPLITK", "2"]
     # AIH_IGEMM_NO_SPLIT keeps a small-M, long-K 3x3 conv whole
     assert int(_plan_in_subprocess({"AIH_IGEMM_NO_SPLIT": ""}, IG_SPLIT_PROBE)) > 1
     assert int(_plan_in_subprocess({"AIH_IGEMM_NO_SPLIT": "1"}, IG_SPLIT_PROBE)) == 1
@@ -431,3 +439,16 @@ def test_dwpw_rejects_what_it_cannot_run():
     d = conv.DwPwSpec(residual=True, **base).desc()
     assert conv.lib().aih_conv_dwpw(C.byref(d), 16, 16, 16, 16, 16, None, 16, None) == -1
     assert "res must be given" in conv.last_error()
+
+
+def test_noalloc_rejects_workspace_beyond_scratch_on_the_host():
+    # the size check of aih_conv_noalloc comes before any device call: on a
+    # machine without a GPU the call still fails with the size in the message
+    # (a 3x3 256 -> 160 fp32 conv at 10x18 batch 256: 118 MB of partial sums)
+    L = conv.lib()
+    op = conv.ConvOp(ih=10, iw=18, cin=256, cout=160, kh=3, kw=3, pad=(1, 1, 1, 1), n=256, dt=conv.DType.F32)
+    need = op.workspace_bytes()
+    assert need > 16 << 20, need
+    d = op.desc()
+    assert L.aih_conv_noalloc(C.byref(d), None, None, None, None, None, None) == -1
+    assert str(need) in conv.last_error() and "scratch" in conv.last_error()

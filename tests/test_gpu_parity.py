@@ -183,6 +183,29 @@ def test_pw_splitk_factors(splitk, n):
     check(f"pw splitk={splitk} n={n}", res, F32)
 
 
+@pytest.mark.parametrize("splitk", [1, 4, 8])
+def test_pw_splitk_factors_at_batch_256(splitk):
+    """The skinny 960 -> 160 layer at 10x18, batch 256 (46080 pixels), with
+    split-K forced to 1 / 4 / 8: the rows the bench times as
+    pw_960to160_10x18_b256_splitk{1,4,8}. A forced factor takes the tiled GEMM
+    (160-channel tiles) and, above 1, its fp32 partials and the reduction
+    launch. Images of a batch never interact, so sampled images are checked
+    against the oracle run of each image alone (fp32 bar 1e-4)."""
+    n, h, w, cin, cout = 256, 10, 18, 960, 160
+    xs = G.stream(3600 + splitk, n * h * w * cin, cout * cin, cout, 0)
+    res = G.run_pw(h, w, cin, cout, "none", False, F32, 3600 + splitk, n=n, splitk=splitk, xs=xs, refs=False)
+    assert res.plan.splitk == splitk and res.plan.bn == 160, res.plan
+    x, wts, b, _ = xs
+    op = G.orc.conv2d(cin, cout, act="none")
+    got = np.asarray(res.got).reshape(n, -1)
+    worst = 0.0
+    for i in (0, 1, 97, 200, 255):
+        want = G.orc.conv2d_ref(op, h, w, x.reshape(n, -1)[i], wts, b, None, n=1)
+        worst = max(worst, G.rel_err(got[i], want))
+    print(f"pw 960->160 b256 splitk={splitk} ({res.plan}): sampled images max_rel_err={worst:.3e}", flush=True)
+    assert worst <= 1e-4
+
+
 def test_pw_splitk_is_deterministic():
     a = G.run_pw(9, 16, 960, 160, "relu", True, F32, 3401, splitk=8).got
     b = G.run_pw(9, 16, 960, 160, "relu", True, F32, 3401, splitk=8).got

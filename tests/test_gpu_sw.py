@@ -310,6 +310,45 @@ def test_real_model_16bit_every_op_matches_stored_dtype_oracle(segm, dt, fuse):
         assert e32 <= 1e-1
 
 
+def _tile_batch(ref, reps):
+    """A batch of `reps` copies of each reference tensor's images, in order
+    (image i of the tiled batch is image i % n of the reference)."""
+    return {k: np.concatenate([v] * reps) for k, v in ref.items()}
+
+
+@pytest.mark.parametrize("dt", [F32, F16], ids=["f32", "f16"])
+def test_real_model_batch64_every_launch(segm, dt):
+    """The real model at batch 64 through aih_model_load, as the bench times
+    it: fused as loaded by default -- at fp32 also the depthwise -> pointwise
+    pairs that batch 64 fuses (ops 33-34 and 40-41) -- and every launch fed
+    the oracle's values of its inputs against the oracle's output (fp32: 1e-4
+    against the fp32 graph; f16: 2e-2 against the graph run with the same
+    storage rounding). The batch is two oracle images repeated 32 times
+    (images never interact), so all 64 are checked at the cost of two."""
+    data, graph = segm
+    n, base = 64, 2
+    x2 = rnd(90, base, 160, 288, 3)
+    x = np.concatenate([x2] * (n // base))
+    m = sw.SwModel(data, n=n, dt=None if dt == F32 else conv.DType(dt))
+    pairs = _check_fused(m, True)
+    if dt == F32:
+        assert sorted(pairs) == sorted(SEGM_PAIRS), pairs
+        for f in m.fused_blocks():
+            if f.n_ops == 2:
+                print(f"segm b64 f32 pair ops {f.first_op}-{f.first_op + 1}: {f.dwpw}", flush=True)
+    ref = graph if dt == F32 else so.SwGraph(data, round_dt=dt)
+    want = _tile_batch(ref.run({"input_1": x2}, n=base, keep_all=True), n // base)
+    worst = _check_launches(m, graph, want, 1e-4 if dt == F32 else 2e-2)
+    m.upload_input("input_1", x)
+    m.infer()
+    e_out = G.rel_err(m.read_output(), want["segment"])
+    print(f"segm b64 dt{dt}: {m.info.n_launches} launches, worst per launch {worst:.2e}, end to end {e_out:.2e}",
+          flush=True)
+    if dt == F32:
+        assert e_out <= 1e-3
+    m.close()
+
+
 def test_tensor_storage_and_info(segm):
     data, graph = segm
     m = sw.SwModel(data, n=3)
@@ -427,6 +466,34 @@ def test_fusion_needs_single_readers(orc):
     m.infer()
     assert G.rel_err(m.read_output(), want) <= 1e-4
     m.close()
+
+
+def test_projection_reading_its_input_twice_stays_unfused(orc):
+    """A projection whose residual is its own input (the depthwise output,
+    cin == cout) reads that tensor through two slots: it counts as two
+    readers, so neither the inverted-residual rule nor the depthwise ->
+    pointwise rule may fuse it away (the residual would have no buffer).
+    The graph loads unfused and matches the oracle."""
+    from ai_engine_amd.workloads import Layer, _chain, make_weights
+
+    layers = _chain([Layer("stem", 3, 32, k=3, s=2, act="relu"), Layer("e", 32, 128, act="relu"),
+                     Layer("d", 128, 128, k=3, groups=128, act="relu"), Layer("p", 128, 128, res="d"),
+                     Layer("head", 128, 2)], 48, 80)
+    wts = make_weights(layers, seed=13)
+    data = sw.conv_graph_to_sw("selfres", layers, wts, 48, 80, 3)
+    n = 2
+    x = rnd(84, n, 48, 80, 3)
+    want = so.SwGraph(data).run({"input": x}, n=n)["head"]
+    for dt in (None, conv.DType.F16):
+        m = sw.SwModel(data, n=n, dt=dt)
+        assert m.fused_blocks() == []
+        assert m.tensor("d").c == 128
+        m.upload_input("input", x)
+        m.infer()
+        e = G.rel_err(m.read_output(), want)
+        print(f"self-residual projection dt={dt}: {e:.2e}", flush=True)
+        assert e <= (1e-4 if dt is None else 5e-2)
+        m.close()
 
 
 def test_model_load_rejects_what_it_cannot_run(segm):

@@ -96,5 +96,17 @@ def test_noalloc_rejects_workspace_beyond_scratch():
     need = op.workspace_bytes()
     assert need > SCRATCH, need
     d = op.desc()
-    assert L.aih_conv_noalloc(C.byref(d), 16, 16, 16, None, 16, None) == -1
+    # real device buffers of the conv's own sizes: were the call accepted,
+    # its kernels would read and write inside them (and aih_conv itself
+    # rejects a workspace below the plan's), so a regression in the host-side
+    # rejection fails the assertion below rather than touching a bad address
+    x = torch.zeros(256 * 10 * 18 * 256, dtype=torch.float32, device=G.DEV)
+    w = torch.zeros(9 * 256 * 160, dtype=torch.float32, device=G.DEV)
+    b = torch.zeros(160, dtype=torch.float32, device=G.DEV)
+    y = G.poisoned(256 * 10 * 18 * 160, 0)
+    rc = L.aih_conv_noalloc(C.byref(d), x.data_ptr(), w.data_ptr(), b.data_ptr(), None, y.data_ptr(), None)
+    torch.cuda.synchronize()
+    assert rc == -1
     assert str(need) in conv.last_error() and "scratch" in conv.last_error()
+    # nothing was written
+    assert bool(torch.isnan(y).all())
