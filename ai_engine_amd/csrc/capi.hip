@@ -1008,7 +1008,6 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
       a.lds_w = wp.lds_w;
       a.lds_bp = wp.lds_bp;
       a.lds_xe = wp.lds_xe;
-      a.lds_hi = wp.lds_hi;
       a.lds_red = wp.lds_red;
       a.lds_x = wp.lds_x;
       a.fd_hw = aih::make_fastdiv(wp.HW);

@@ -64,19 +64,19 @@ hipError_t launch_ir_block(const IrArgs &a, int dt, uint32_t lds, uint32_t grid,
 // ---- the one-tile-per-wavefront kernel (ir_wave_impl.h) ----
 
 constexpr int IRW_THREADS = 512;              // the most threads a workgroup has (8 wavefronts)
-constexpr uint32_t IRW_RPE = 32 * 2 + 16;     // expanded-chunk LDS row pitch: 32 16-bit channels + 16 bytes
-constexpr uint32_t IRW_SMB = 11 * 32 * 2;     // per chunk: 9 depthwise taps, depthwise bias, expand bias
-// bf16 with resident weights: per chunk, the 9 depthwise taps' odd channels
-// as 32-bit words with the even half zeroed (the taps in the slot keep the
-// even channels, odd half zeroed): v_dot2 operands without per-use masking
-constexpr uint32_t IRW_HI_BYTES = 9 * 32 * 2;
-// The wave kernel instantiations that split the bf16 taps: where the
-// registers held across a chunk (halo operands, expand operands,
-// projection accumulators: 4 NPI KE + 4 KE + 16 NOB) leave room for the odd
-// taps beside the even ones (the wider shapes would spill).
-__host__ __device__ constexpr bool irw_bf16_split(uint32_t ke, uint32_t npi, uint32_t nob) {
-  return 4 * npi * ke + 4 * ke + 16 * nob <= 64;
-}
+// A wavefront's expanded chunk in LDS: four planes of 8 channels (16 bytes a
+// halo pixel), plane h holding channels 8h .. 8h + 7 of every halo pixel in
+// turn -- 64 bytes a pixel. (The depthwise reads 16-pixel groups of one
+// plane; measured on gfx950, these reads cost 6.5 LDS cycles per wavefront
+// instruction against 8.8 - 9.6 for rows of 64 + 16 bytes a pixel.)
+constexpr uint32_t IRW_XPIX = 32 * 2;         // bytes of one halo pixel over the four planes
+// Per chunk, after the expand and project weights: the 9 depthwise taps
+// (32 16-bit channels each), a run of 32 zeros (the partner of the ninth tap
+// in the depthwise MFMAs), the depthwise bias and the expand bias.
+constexpr uint32_t IRW_TAPS_ZERO = 9 * 32 * 2;
+constexpr uint32_t IRW_BD = 10 * 32 * 2;
+constexpr uint32_t IRW_BE = 11 * 32 * 2;
+constexpr uint32_t IRW_SMB = 12 * 32 * 2;
 
 struct IrWaveArgs {
   const void *x;         // [N][IH][IW][C]
@@ -95,7 +95,6 @@ struct IrWaveArgs {
   int32_t act_e, act_d, act_p, has_res;
   uint32_t nxcd;            // XCDs of the device (workgroup remap)
   uint32_t lds_w, lds_bp, lds_xe;  // LDS byte offsets: weight slots, fp32 projection bias, expanded regions
-  uint32_t lds_hi;                 // wave kernel, bf16, resident weights: odd-channel depthwise taps (IRW_HI_BYTES a chunk)
   uint32_t lds_red;                // split kernel: projection partial sums (over the regions below)
   uint32_t lds_x;                  // split kernel: the tile's input halo
   FastDiv fd_hw, fd_tw, fd_tx, fd_pi;
@@ -119,7 +118,7 @@ struct IrWavePlan {
   uint32_t TH, TW, HH, HW, NPI, resident;
   uint32_t waves;                       // wavefronts per workgroup (wave: 2, 4 or 8; split: 1, 2, 4 or 8)
   uint32_t tiles_y, tiles_x, ntiles;
-  uint32_t lds_w, lds_bp, lds_xe, lds_red, lds_x, lds_hi, lds;  // LDS byte offsets and total
+  uint32_t lds_w, lds_bp, lds_xe, lds_red, lds_x, lds;  // LDS byte offsets and total
   uint32_t occ, grid;                   // workgroups per CU, launched workgroups
 };
 
@@ -128,16 +127,6 @@ struct IrWavePlan {
 // depthwise taps and biases; partial sums: NOB blocks of 32 x 32 fp32 per
 // wavefront, over the rest once it is done with.
 constexpr uint32_t IRS_RING = 2 * IRW_SMB;
-// bf16 on the shapes with 2 halo blocks and at most 64 input channels: a
-// ring slot also holds its taps' odd-channel halves (the slot's own taps
-// then keep the even ones), split by the wavefront when they land. The wider
-// shapes keep masking per use: the extra operand registers cost them a
-// wavefront per SIMD (96 -> 384 -> 96 at 20x36 b64 bf16: 32 -> 41 us).
-constexpr uint32_t IRS_SLOT_BF16 = IRW_SMB + IRW_HI_BYTES;
-__host__ __device__ constexpr bool irs_bf16_split(uint32_t ke, uint32_t npi) { return ke <= 4 && npi == 2; }
-__host__ __device__ constexpr uint32_t irs_ring_bytes(int dt, uint32_t ke, uint32_t npi) {
-  return dt == 2 && irs_bf16_split(ke, npi) ? 2 * IRS_SLOT_BF16 : IRS_RING;
-}
 constexpr uint32_t IRS_RED_BLOCK = 32 * 32 * 4;
 
 // Chooses between the wave kernel and the split kernel (kernel: enum

@@ -119,22 +119,6 @@ __device__ __forceinline__ void ir_fma_taps(u32x4 xv, u32x4 wv, float (&d)[HK]) 
   }
 }
 
-// bf16 depthwise taps from weights already split by channel parity: wlo
-// holds each word's even channel (odd half zero), whi its odd channel (even
-// half zero), so each product is one v_dot2c with no masking -- the same
-// arithmetic as ir_fma_taps (x.lo * w.lo + x.hi * 0 + d), bit for bit.
-template <int HK>
-__device__ __forceinline__ void ir_fma_taps_bf16_split(u32x4 xv, u32x4 wlo, u32x4 whi, float (&d)[HK]) {
-  const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w}, ls[4] = {wlo.x, wlo.y, wlo.z, wlo.w},
-                 hs[4] = {whi.x, whi.y, whi.z, whi.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bf16x2 x2 = __builtin_bit_cast(bf16x2, xs[j]);
-    d[2 * j] = __builtin_amdgcn_fdot2_f32_bf16(x2, __builtin_bit_cast(bf16x2, ls[j]), d[2 * j], false);
-    d[2 * j + 1] = __builtin_amdgcn_fdot2_f32_bf16(x2, __builtin_bit_cast(bf16x2, hs[j]), d[2 * j + 1], false);
-  }
-}
-
 // Global -> LDS copies without registers: buffer_load_dword{,x4} ... lds
 // writes lane i's SZ bytes to LDS at a wavefront-uniform base + SZ * i.
 // A lane whose offset lies at or past the buffer's size writes zeros.

@@ -42,22 +42,19 @@ template <int DT, int KE, int NPI, int NOB, bool RL, bool DP>
 __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
   static_assert(DT == DT_F16 || DT == DT_BF16, "16-bit storage");
   extern __shared__ __align__(16) char lds[];
-  constexpr int ES = 2, KSTEP = 16, HK = 8, EC = 32, NKS = EC / KSTEP;
+  constexpr int ES = 2, EC = 32, NOG = 2 * NOB;
   constexpr uint32_t GB = 4 * ES;  // one packed group: 4 K of one channel
-  constexpr uint32_t C = KE * KSTEP;
+  constexpr uint32_t C = KE * 16;
   // Registers held across a chunk: the expand operands, the accumulators and
-  // both K steps' projection operands. Depthwise taps are read in batches of
-  // three; the projection operands go out before the expand where the shape
-  // stays within 128 VGPRs (four wavefronts per SIMD), else before each K
-  // step's depthwise. The packed ReLU on the expand's epilogue only: on the
-  // depthwise result it keeps the packed values live longer and costs a
-  // wavefront per SIMD on the wider shapes.
+  // the projection operands. The projection operands go out before the
+  // expand where the shape stays within 128 VGPRs (four wavefronts per
+  // SIMD), else after it. The packed ReLU on the expand's epilogue and on
+  // the depthwise result.
   constexpr int HELD = 4 * KE + 16 * NOB + 8 * NOB;
-  constexpr int TB = 3;
-  constexpr bool RLE = RL, RLD = false;
+  constexpr bool RLE = RL, RLD = RL;
   constexpr bool WP_EARLY = HELD <= 64;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, l32 = lane & 31, lh = lane >> 5;
+  const int lane = tid & 63, l32 = lane & 31, lh = lane >> 5, l16 = lane & 15, q = lane >> 4;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t nw = blockDim.x >> 6;
   const uint32_t nchunks = a.E / EC;
@@ -66,14 +63,13 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
   float *BpL = reinterpret_cast<float *>(lds + a.lds_bp);
   constexpr uint32_t RPX = C * ES + 16;  // halo row pitch: the pixel's C channels + 16 bytes
   const char *XL = lds + a.lds_x;
-  char *XeL = lds + a.lds_xe + wave * (NPI * 32 * IRW_RPE);
-  // ring slot s of this wavefront at SmL + s * SMS; BS (bf16 on the narrow
-  // shapes): the slot's taps split by channel parity (split_taps), the odd
-  // halves IRW_SMB bytes in
-  constexpr bool BS = DT == DT_BF16 && irs_bf16_split(KE, NPI);
-  constexpr uint32_t SMS = BS ? IRS_SLOT_BF16 : IRW_SMB;
-  char *SmL = lds + a.lds_w + wave * (2 * SMS);
+  constexpr uint32_t PLANE = NPI * 32 * 16;  // one 8-channel plane of the expanded chunk
+  char *XeL = lds + a.lds_xe + wave * (4 * PLANE);
+  // ring slot s of this wavefront at SmL + s * IRW_SMB (the slot layout of
+  // the wave kernel: 9 taps, zero run, depthwise bias, expand bias)
+  char *SmL = lds + a.lds_w + wave * (2 * IRW_SMB);
   const Act act_e = act_params(a.act_e), act_d = act_params(a.act_d), act_p = act_params(a.act_p);
+  const IrDwLane DL = irdw_lane(lane);
 
   const __amdgpu_buffer_rsrc_t rs_we = ir_rsrc(a.we, C * a.E * ES);
   const __amdgpu_buffer_rsrc_t rs_wp = ir_rsrc(a.wp, a.E * a.CO * ES);
@@ -83,6 +79,10 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
 
   for (uint32_t i = tid; i < a.CO / 4; i += blockDim.x)
     *reinterpret_cast<f32x4 *>(BpL + 4 * i) = Vec4IO<DT>::load(a.bp, i);
+  // the zero run of this wavefront's two ring slots (its copies never write it)
+  if (lane < 8)
+    *reinterpret_cast<u32x4 *>(SmL + (lane >> 2) * IRW_SMB + IRW_TAPS_ZERO + (lane & 3) * 16) =
+        u32x4{0u, 0u, 0u, 0u};
 
   // ---- the tile: its input halo -> XL, row r = halo pixel r ----
   const uint32_t T = xcd_remap(blockIdx.x, gridDim.x, a.nxcd);
@@ -117,14 +117,18 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
     const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
     inside[b] = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
   }
-  // this lane's output pixel and its three depthwise tap rows in XeL
-  const bool in_tile = (uint32_t)l32 < TPIX;
-  const uint32_t oy = in_tile ? fdiv(l32, a.fd_tw) : 0, ox = in_tile ? l32 - oy * a.TW : 0;
-  uint32_t rowo[3];
+  // this lane's output pixel of each 16-pixel group and its depthwise B offsets in XeL
+  uint32_t bc[2][3], br[2], pix[2];
+  bool ok[2];
 #pragma unroll
-  for (int dy = 0; dy < 3; ++dy) rowo[dy] = ((oy * a.S + dy) * a.HW + ox * a.S) * IRW_RPE + lh * 16;
-  const bool out_ok = in_tile && ty0 + oy < a.OH && tx0 + ox < a.OW;
-  const size_t out_pix = ((size_t)img * a.OH + ty0 + oy) * a.OW + tx0 + ox;
+  for (int pg = 0; pg < 2; ++pg) {
+    const uint32_t op = pg * 16 + l16;
+    const bool in_tile = op < TPIX;
+    const uint32_t oy = in_tile ? fdiv(op, a.fd_tw) : 0, ox = in_tile ? op - oy * a.TW : 0;
+    irdw_rows(oy * a.S * a.HW + ox * a.S, a.HW, q, PLANE, bc[pg], br[pg]);
+    ok[pg] = in_tile && ty0 + oy < a.OH && tx0 + ox < a.OW;
+    pix[pg] = (img * a.OH + ty0 + oy) * a.OW + tx0 + ox;
+  }
 
   // ---- weights of chunk c ----
   // Every weight offset is a lane part (held) plus a wavefront-uniform part
@@ -142,59 +146,37 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
       aw[k] = u32x4{lo.x, lo.y, hi.x, hi.y};
     }
   };
-  // projection A operand of block o, K step ks: output channel 32o + l32, K
-  // rows 32c + 16ks + 8lh .. + 8 (groups 8c + 4ks + 2lh and the next); zeros
-  // for channels CO..COP (a lane offset past every buffer)
-  auto load_wp = [&](uint32_t c, int ks, int o) -> u32x4 {
-    const uint32_t ch = (uint32_t)o * 32 + l32;
-    const uint32_t vo = ch < a.CO ? (2 * (uint32_t)lh * a.CO + ch) * GB : IR_OOB;
-    const uint32_t so = (8 * c + 4 * (uint32_t)ks) * a.CO * GB;
-    const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_wp, vo, so, 0));
-    const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_wp, vo, so + a.CO * GB, 0));
-    return u32x4{lo.x, lo.y, hi.x, hi.y};
+  // projection A operands of chunk c: block og, output channel 16 og + l16,
+  // K slice q = packed groups 8c + q and 8c + q + 4 (the depthwise result's
+  // K order); zeros for channels CO..COP (a lane offset past every buffer)
+  auto load_wp = [&](uint32_t c, u32x4 (&wp)[NOG]) {
+    const uint32_t so = 8 * c * a.CO * GB;
+#pragma unroll
+    for (int og = 0; og < NOG; ++og) {
+      const uint32_t ch = (uint32_t)og * 16 + l16;
+      const uint32_t vo = ch < a.CO ? ((uint32_t)q * a.CO + ch) * GB : IR_OOB;
+      const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_wp, vo, so, 0));
+      const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_wp, vo, so + 4 * a.CO * GB, 0));
+      wp[og] = u32x4{lo.x, lo.y, hi.x, hi.y};
+    }
   };
-  // depthwise taps, depthwise bias, expand bias of chunk c -> ring slot s
-  // (9 runs of 32 channels, then the two biases: the slot layout of the wave
-  // kernel); this wavefront's LDS-direct loads, landed at its next ir_dma_wait
+  // depthwise taps, depthwise bias, expand bias of chunk c -> ring slot s;
+  // this wavefront's LDS-direct loads, landed at its next ir_dma_wait
   auto load_small = [&](uint32_t c, uint32_t s) {
-    char *sm = SmL + s * SMS;
+    char *sm = SmL + s * IRW_SMB;
     constexpr uint32_t TR = EC * ES / 16;  // 16-byte items per tap run
     irw_dma<16>(sm, 9 * TR, rs_wd, 0, lane, 64,
                 [&](uint32_t g) -> uint32_t { return (g / TR) * a.E * ES + (g % TR) * 16; }, EC * c * ES);
-    irw_dma<4>(sm + 9 * EC * ES, EC * ES / 4, rs_bd, 0, lane, 64, [&](uint32_t g) -> uint32_t { return g * 4; },
+    irw_dma<4>(sm + IRW_BD, EC * ES / 4, rs_bd, 0, lane, 64, [&](uint32_t g) -> uint32_t { return g * 4; },
                EC * c * ES);
-    irw_dma<4>(sm + 10 * EC * ES, EC * ES / 4, rs_be, 0, lane, 64, [&](uint32_t g) -> uint32_t { return g * 4; },
+    irw_dma<4>(sm + IRW_BE, EC * ES / 4, rs_be, 0, lane, 64, [&](uint32_t g) -> uint32_t { return g * 4; },
                EC * c * ES);
   };
 
-  // BS: ring slot sm's taps (landed, this wavefront's own) split by
-  // channel parity -- even halves kept in place, odd halves IRW_SMB bytes
-  // in -- so each tap is two v_dot2c with no per-use masking; the
-  // wavefront's LDS accesses stay in issue order, no barrier
-  auto split_taps = [&](char *sm) {
-    if constexpr (BS) {
-      constexpr uint32_t TW = 9 * EC / 2;  // 32-bit words of one chunk's taps
-      uint32_t *lo = reinterpret_cast<uint32_t *>(sm), *hi = reinterpret_cast<uint32_t *>(sm + IRW_SMB);
+  f32x4 acc[NOG][2];
 #pragma unroll
-      for (uint32_t i = (uint32_t)lane; i < TW; i += 64) {
-        const uint32_t w = lo[i];
-        lo[i] = w & 0x0000ffffu;
-        hi[i] = w & 0xffff0000u;
-      }
-      irw_wave_order();
-    }
-  };
+  for (int og = 0; og < NOG; ++og) acc[og][0] = acc[og][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  f32x16 acc[NOB];
-#pragma unroll
-  for (int o = 0; o < NOB; ++o) acc[o] = f32x16{};
-
-  auto load_wp_all = [&](uint32_t c, u32x4 (&wp)[NKS][NOB]) {
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-      for (int o = 0; o < NOB; ++o) wp[ks][o] = load_wp(c, ks, o);
-  };
   // expand of the chunk whose small tensors are at sm, over the halo tile ->
   // XeL, each K step's B operands read from LDS one step ahead. With the deep
   // prefetch (registers to spare) the halo blocks go two at a time with their
@@ -202,7 +184,7 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
   // the one before it.
   constexpr int G = DP ? 2 : 1;
   auto expand = [&](const char *sm, const u32x4 (&aw)[KE]) {
-    const uint32_t bw = lh == 0 ? (uint32_t)*reinterpret_cast<const uint16_t *>(sm + 10 * EC * ES + l32 * 2) : 0u;
+    const uint32_t bw = lh == 0 ? (uint32_t)*reinterpret_cast<const uint16_t *>(sm + IRW_BE + l32 * 2) : 0u;
 #pragma unroll
     for (int b0 = 0; b0 < NPI; b0 += G) {
       const int ng = NPI - b0 < G ? NPI - b0 : G;
@@ -233,12 +215,25 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         if (g >= ng) continue;
-        char *row = XeL + ((b0 + g) * 32 + l32) * IRW_RPE;
+        // channels 8 qq + 4 lh .. + 3: plane qq, the pixel's 16 bytes at 8 lh
+        char *px = XeL + ((b0 + g) * 32 + l32) * 16 + lh * 8;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          *reinterpret_cast<u32x2 *>(row + (8 * q + 4 * lh) * ES) = irw_act_pack4<DT, RLE>(
-              act_e, f32x4{e[g][4 * q], e[g][4 * q + 1], e[g][4 * q + 2], e[g][4 * q + 3]});
+        for (int qq = 0; qq < 4; ++qq)
+          *reinterpret_cast<u32x2 *>(px + qq * PLANE) = irw_act_pack4<DT, RLE>(
+              act_e, f32x4{e[g][4 * qq], e[g][4 * qq + 1], e[g][4 * qq + 2], e[g][4 * qq + 3]});
       }
+    }
+  };
+  // depthwise of the chunk at sm (expanded rows in XeL) and its projection
+  // into acc with operands wpv
+  auto dw_project = [&](const char *sm, const u32x4 (&wpv)[NOG]) {
+    u32x4 bop[2];
+    irdw_chunk<DT, RLD, PLANE>(XeL, sm, DL, bc, br, q, act_d, bop);
+#pragma unroll
+    for (int og = 0; og < NOG; ++og) {
+      if (og * 16 >= (int)a.CO) continue;
+#pragma unroll
+      for (int pg = 0; pg < 2; ++pg) acc[og][pg] = ir_mma16<DT>(wpv[og], bop[pg], acc[og][pg]);
     }
   };
 
@@ -253,14 +248,13 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
     __syncthreads();
     for (uint32_t c = c_begin; c < c_end; ++c) {
       const uint32_t s = (c - c_begin) & 1;
-      char *sm = SmL + s * SMS;
+      char *sm = SmL + s * IRW_SMB;
       // chunk c's small tensors have landed (and every earlier load)
       ir_dma_wait();
       irw_wave_order();
-      split_taps(sm);
-      // the projection operands (both K steps' in flight during the expand)
-      u32x4 wpv[NKS][NOB];
-      if constexpr (WP_EARLY) load_wp_all(c, wpv);
+      // the projection operands (in flight during the expand where registers allow)
+      u32x4 wpv[NOG];
+      if constexpr (WP_EARLY) load_wp(c, wpv);
 
       expand(sm, aw);
       irw_wave_order();
@@ -271,52 +265,8 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
         load_aw(c + 1, aw);
         load_small(c + 1, s ^ 1u);
       }
-
-      // depthwise of the lane's K slice straight into the projection's B operand
-      const char *wdp = sm + lh * 16;
-      const char *bdp = sm + 9 * EC * ES + lh * 16;
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        if constexpr (!WP_EARLY) {
-#pragma unroll
-          for (int o = 0; o < NOB; ++o) wpv[ks][o] = load_wp(c, ks, o);
-        }
-        float d[HK];
-        ir_unpack<DT, HK>(*reinterpret_cast<const u32x4 *>(bdp + ks * 32), d);
-#pragma unroll
-        for (int t0 = 0; t0 < 9; t0 += TB) {
-          u32x4 wv[TB], xv[TB];
-#pragma unroll
-          for (int t = 0; t < TB; ++t) wv[t] = *reinterpret_cast<const u32x4 *>(wdp + (t0 + t) * (EC * ES) + ks * 32);
-#pragma unroll
-          for (int t = 0; t < TB; ++t)
-            xv[t] = *reinterpret_cast<const u32x4 *>(XeL + rowo[(t0 + t) / 3] + ((t0 + t) % 3) * IRW_RPE + ks * 32);
-          if constexpr (BS) {
-            u32x4 wh[TB];
-#pragma unroll
-            for (int t = 0; t < TB; ++t)
-              wh[t] = *reinterpret_cast<const u32x4 *>(wdp + IRW_SMB + (t0 + t) * (EC * ES) + ks * 32);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int t = 0; t < TB; ++t) ir_fma_taps_bf16_split<HK>(xv[t], wv[t], wh[t], d);
-          } else {
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
-          }
-        }
-        u32x4 bop;
-        if constexpr (RLD) {
-          bop = ir_pack<DT, HK>(d);
-          bop = u32x4{irw_relu2(bop.x), irw_relu2(bop.y), irw_relu2(bop.z), irw_relu2(bop.w)};
-        } else {
-          ir_act<true, HK>(act_d, d);
-          bop = ir_pack<DT, HK>(d);
-        }
-#pragma unroll
-        for (int o = 0; o < NOB; ++o) acc[o] = ir_mma<DT>(wpv[ks][o], bop, acc[o]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      if constexpr (!WP_EARLY) load_wp(c, wpv);
+      dw_project(sm, wpv);
       // the next chunk's expand overwrites XeL after these reads
       irw_wave_order();
     }
@@ -337,55 +287,18 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
     // chunk c from ring slot s with expand operands `cur`; the next chunk's
     // into `nxt` and the other slot
     auto step = [&](uint32_t c, uint32_t s, u32x4 (&cur)[KE], u32x4 (&nxt)[KE]) {
-      char *sm = SmL + s * SMS;
+      char *sm = SmL + s * IRW_SMB;
       ir_dma_wait();
       irw_wave_order();
-      split_taps(sm);
-      u32x4 wpv[NKS][NOB];
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-        for (int o = 0; o < NOB; ++o) wpv[ks][o] = load_wp(c, ks, o);
+      u32x4 wpv[NOG];
+      load_wp(c, wpv);
       if (c + 1 < c_end) {
         load_aw(c + 1, nxt);
         load_small(c + 1, s ^ 1u);
       }
       expand(sm, cur);
       irw_wave_order();
-      const char *wdp = sm + lh * 16;
-      const char *bdp = sm + 9 * EC * ES + lh * 16;
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        float d[HK];
-        ir_unpack<DT, HK>(*reinterpret_cast<const u32x4 *>(bdp + ks * 32), d);
-#pragma unroll
-        for (int t0 = 0; t0 < 9; t0 += TB) {
-          u32x4 wv[TB], xv[TB];
-#pragma unroll
-          for (int t = 0; t < TB; ++t) wv[t] = *reinterpret_cast<const u32x4 *>(wdp + (t0 + t) * (EC * ES) + ks * 32);
-#pragma unroll
-          for (int t = 0; t < TB; ++t)
-            xv[t] = *reinterpret_cast<const u32x4 *>(XeL + rowo[(t0 + t) / 3] + ((t0 + t) % 3) * IRW_RPE + ks * 32);
-          if constexpr (BS) {
-            u32x4 wh[TB];
-#pragma unroll
-            for (int t = 0; t < TB; ++t)
-              wh[t] = *reinterpret_cast<const u32x4 *>(wdp + IRW_SMB + (t0 + t) * (EC * ES) + ks * 32);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int t = 0; t < TB; ++t) ir_fma_taps_bf16_split<HK>(xv[t], wv[t], wh[t], d);
-          } else {
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
-          }
-        }
-        ir_act<true, HK>(act_d, d);
-        const u32x4 bop = ir_pack<DT, HK>(d);
-#pragma unroll
-        for (int o = 0; o < NOB; ++o) acc[o] = ir_mma<DT>(wpv[ks][o], bop, acc[o]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      dw_project(sm, wpv);
       irw_wave_order();
     };
     for (uint32_t c = c_begin; c < c_end; c += 2) {
@@ -394,36 +307,34 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
     }
   }
 
-  // ---- partial sums: wavefront w's block o at [w][o][q][lane] (f32x4) ----
+  // ---- partial sums: wavefront w's unit (og, pg) at [w][og][pg][lane] (f32x4) ----
   // The region overlaps the halo, the wavefronts' XeL and rings: every
   // wavefront must be done with them first.
   __syncthreads();
   f32x4 *red = reinterpret_cast<f32x4 *>(lds + a.lds_red);
 #pragma unroll
-  for (int o = 0; o < NOB; ++o)
+  for (int og = 0; og < NOG; ++og)
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      red[((wave * NOB + o) * 4 + q) * 64 + lane] =
-          f32x4{acc[o][4 * q], acc[o][4 * q + 1], acc[o][4 * q + 2], acc[o][4 * q + 3]};
+    for (int pg = 0; pg < 2; ++pg) red[((wave * NOG + og) * 2 + pg) * 64 + lane] = acc[og][pg];
   __syncthreads();
-  if (!out_ok) return;
-  // block o belongs to wavefront o % W: the sum over wavefronts 0..W-1 in
-  // order, then bias -> act -> (+ residual) -> store
-  for (uint32_t o = wave; o < (uint32_t)NOB; o += nw) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t oc = o * 32 + 8 * q + 4 * lh;
-      if (oc >= a.CO) continue;  // padding channels of the last block
-      f32x4 v = red[((0 * NOB + o) * 4 + q) * 64 + lane];
-      for (uint32_t w = 1; w < nw; ++w) v += red[((w * NOB + o) * 4 + q) * 64 + lane];
-      v += *reinterpret_cast<const f32x4 *>(BpL + oc);
-      float t4[4] = {v.x, v.y, v.z, v.w};
-      ir_act<true, 4>(act_p, t4);
-      v = f32x4{t4[0], t4[1], t4[2], t4[3]};
-      const size_t vi = out_pix * (a.CO / 4) + oc / 4;
-      if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
-      Vec4IO<DT>::store(a.y, vi, v);
-    }
+  // unit u = (og, pg) belongs to wavefront u % W: the sum over wavefronts
+  // 0..W-1 in order, then bias -> act -> (+ residual) -> store
+  for (uint32_t u = wave; u < (uint32_t)(2 * NOG); u += nw) {
+    const uint32_t og = u >> 1, pg = u & 1;
+    const uint32_t oc = og * 16 + 4 * q;
+    // (selects, not a register array indexed at run time)
+    const bool okp = pg ? ok[1] : ok[0];
+    const uint32_t pixp = pg ? pix[1] : pix[0];
+    if (og * 16 >= a.CO || !okp) continue;  // padding channels of the last block; pixels outside
+    f32x4 v = red[((0 * NOG + og) * 2 + pg) * 64 + lane];
+    for (uint32_t w = 1; w < nw; ++w) v += red[((w * NOG + og) * 2 + pg) * 64 + lane];
+    v += *reinterpret_cast<const f32x4 *>(BpL + oc);
+    float t4[4] = {v.x, v.y, v.z, v.w};
+    ir_act<true, 4>(act_p, t4);
+    v = f32x4{t4[0], t4[1], t4[2], t4[3]};
+    const size_t vi = (size_t)pixp * (a.CO / 4) + oc / 4;
+    if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
+    Vec4IO<DT>::store(a.y, vi, v);
   }
 }
 

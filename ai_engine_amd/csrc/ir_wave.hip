@@ -81,6 +81,7 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
   if ((tile_h && tile_h > OH) || (tile_w && tile_w > OW)) return "forced tile larger than the output";
   if (tile_h && tile_w && tile_h * tile_w > 32) return "the wave kernels' tiles hold at most 32 pixels";
   if ((uint64_t)IH * IW * C * 2 >= 0x80000000ull) return "image of 2 GiB or more";
+  if ((uint64_t)N * OH * OW >= 0xffffffffull) return "2^32 or more output pixels";
 
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = -1;
@@ -128,9 +129,9 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
     if (nt64 > 0x7fffffffull) return;
     const uint32_t nt = (uint32_t)nt64;
     // one chunk of one tile: expand (NPI blocks of KE + 1 MFMAs, their
-    // epilogue), the depthwise of 32 pixels x 32 channels on the VALU, the
-    // projection
-    auto chunk_cost = [&](uint32_t npi) { return npi * (ke + 1) * 32.0 + npi * 120.0 + 800.0 + nob * 64.0; };
+    // epilogue), the depthwise of 32 pixels x 32 channels (20 16x16x32
+    // MFMAs and the operand masking), the projection
+    auto chunk_cost = [&](uint32_t npi) { return npi * (ke + 1) * 32.0 + npi * 120.0 + 420.0 + nob * 64.0; };
     if (kernel != AIH_IR_KERNEL_SPLIT && npi_w) {
       const uint32_t npi = npi_w;
       const double chunk = chunk_cost(npi);
@@ -149,11 +150,10 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
           p.resident = resident;
           p.waves = waves;
           p.lds_w = 0;
-          p.lds_hi = dt == DT_BF16 && resident && irw_bf16_split(ke, npi, nob) ? align16(nchunks * slot) : 0u;
-          p.lds_bp = align16(p.lds_hi ? p.lds_hi + nchunks * IRW_HI_BYTES : (resident ? nchunks : 2u) * slot);
+          p.lds_bp = align16((resident ? nchunks : 2u) * slot);
           p.lds_xe = align16(p.lds_bp + CO * 4);
           p.lds_red = 0;
-          p.lds = p.lds_xe + waves * npi * 32 * IRW_RPE;
+          p.lds = p.lds_xe + waves * npi * 32 * IRW_XPIX;
           if (p.lds > 160u * 1024u) continue;
           p.occ = (uint32_t)irw_occupancy(0, dt, ke, npi, nob, rl, waves, p.lds);
           if (p.occ == 0) continue;  // not resident at this size
@@ -189,9 +189,9 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
         p.lds_bp = 0;
         p.lds_x = align16(CO * 4);
         p.lds_xe = p.lds_x + npi * 32 * (C * 2 + 16);
-        p.lds_w = p.lds_xe + w * npi * 32 * IRW_RPE;
+        p.lds_w = p.lds_xe + w * npi * 32 * IRW_XPIX;
         p.lds_red = p.lds_x;
-        p.lds = p.lds_x + std::max(p.lds_w + w * irs_ring_bytes(dt, ke, npi) - p.lds_x, w * nob * IRS_RED_BLOCK);
+        p.lds = p.lds_x + std::max(p.lds_w + w * IRS_RING - p.lds_x, w * nob * IRS_RED_BLOCK);
         if (p.lds > 160u * 1024u) continue;
         p.occ = (uint32_t)irw_occupancy(1, dt, ke, npi, nob, rl, w, p.lds);
         if (p.occ == 0) continue;  // not resident at this size

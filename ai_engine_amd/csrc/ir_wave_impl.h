@@ -89,32 +89,179 @@ __device__ __forceinline__ void irw_wave_order() {
   asm volatile("" ::: "memory");
 }
 
+// ---- depthwise 3x3 and projection on 16x16x32 MFMAs ----
+//
+// Lane l: l16 = l % 16 is a pixel (B column, result column) or a channel (A
+// row); q = l / 16 its K slice of 8 elements. The depthwise of a chunk runs
+// as matrix products whose K = 32 holds two taps of 16 channels: slice q is
+// channels 8 (q % 2) .. + 7 of tap ta (q < 2) or of its partner tb (q >= 2),
+// read as 16 bytes of the expanded chunk (B) and of the tap weights (A). A is
+// diagonal -- row c holds w[t][c] at channel c's K position of each tap and
+// zeros elsewhere, a lane's 16 weight bytes masked to its own element -- so
+// result row c, column p is w[ta][c] x[p + ta][c] + w[tb][c] x[p + tb][c]
+// (+ the accumulator): two taps of a 16-channel x 16-pixel depthwise per
+// MFMA, fp32 accumulation of exact 16-bit products, the bias entering as the
+// first MFMA's accumulator. Nine taps are four pairs and one single whose
+// partner is a zero run in the weight slot. The 32 channels of a chunk are
+// two 16-channel groups (cg), the 32 output pixels of a tile two 16-pixel
+// groups (pg). The result lane (pixel p, slice q) holds rows 4q .. 4q + 3 of
+// each group; packed after act_d, group 0's four then group 1's four are
+// exactly the projection's B operand for K slice q when the projection's K
+// order is channels {4q .. 4q+3, 16+4q .. 16+4q+3}: packed weight groups q and
+// q + 4 of the chunk (ir_ld_w with a stride of four groups).
+//
+// Pairs, taps t = 3 dy + dx:            A (tap weights)      B (expanded chunk)
+//   (0, 1) (3, 4) (6+1, 6+2) along a row    wa1 + 64 ta          bc[dy] (+ one pixel for (7, 8))
+//   (2, 5) down a column                    wa3 + 64 * 2         br + two pixels
+//   (6, zero run)                           wa3 + 64 * 6         bc[2] (partner lanes read tap 7, times 0)
+// wa1 / wa3: the lane's 8-channel half, + one / three taps for q >= 2;
+// bc[dy] = pixel row + dy rows (+ one pixel for q >= 2); br = pixel row (+ one
+// row for q >= 2). Every read stays inside the tile's halo rows. (Reads of the
+// expanded chunk: plane 2 cg + q % 2, 16 bytes at the halo pixel.)
+
+template <int DT>
+__device__ __forceinline__ f32x4 ir_mma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == DT_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+// Lane constants of the depthwise MFMAs.
+struct IrDwLane {
+  u32x4 mask;         // the lane's diagonal element in its 16 weight bytes (0xffff in its half), or zero
+  uint32_t wa1, wa3;  // tap-weight byte offsets in a slot: the 8-channel half, + 1 / 3 taps for q >= 2
+};
+
+__device__ __forceinline__ IrDwLane irdw_lane(int lane) {
+  const uint32_t l16 = lane & 15, q = lane >> 4, qh = q & 1, qt = q >> 1;
+  const uint32_t e = l16 & 7, j = e >> 1;
+  const uint32_t hm = (l16 >> 3) == qh ? ((e & 1) ? 0xffff0000u : 0x0000ffffu) : 0u;
+  IrDwLane L;
+  L.mask = u32x4{j == 0 ? hm : 0u, j == 1 ? hm : 0u, j == 2 ? hm : 0u, j == 3 ? hm : 0u};
+  L.wa1 = qh * 16 + qt * 64;
+  L.wa3 = qh * 16 + qt * 192;
+  return L;
+}
+
+// B-operand byte offsets (within the wavefront's expanded chunk, planes of
+// PLANE bytes) of the output pixel whose top-left halo pixel is rp, for lane
+// slice q: bc[dy] and br as in the table above (plane q % 2 of the channel
+// group; the group's plane offset and the tap column are immediates).
+__device__ __forceinline__ void irdw_rows(uint32_t rp, uint32_t hw, int q, uint32_t plane, uint32_t (&bc)[3],
+                                          uint32_t &br) {
+  const uint32_t qh = q & 1, qt = q >> 1;
+  const uint32_t lo = qh * plane + rp * 16;
+#pragma unroll
+  for (int dy = 0; dy < 3; ++dy) bc[dy] = lo + (dy * hw + qt) * 16;
+  br = lo + qt * hw * 16;
+}
+
+// The depthwise of one chunk for the wavefront's two 16-pixel groups: tap
+// weights and biases of the chunk at sm (slot layout: 9 taps, zero run, bd,
+// be), its expanded planes (PLANE bytes each) at xe. Returns the projection
+// B operand of each pixel group: act_d of the result in the storage dtype,
+// rows 4q .. 4q + 3 of channel group 0, then of group 1.
+template <int DT, bool RLD, uint32_t PLANE>
+__device__ __forceinline__ void irdw_chunk(const char *xe, const char *sm, const IrDwLane &L,
+                                          const uint32_t (&bc)[2][3], const uint32_t (&br)[2], int q,
+                                          const Act &act_d, u32x4 (&bop)[2]) {
+  // Ten steps s = 5 cg + P: channel group cg (one after the other: half the
+  // accumulators live at a time), tap pair P; in each, the two pixel groups'
+  // MFMA chains interleave. The operands of step s + 1 are read before the
+  // MFMAs of step s, so an MFMA does not wait on the LDS read just issued.
+  auto aoff = [&](int P) -> uint32_t {
+    return P == 0 ? L.wa1 : P == 1 ? L.wa1 + 3 * 64 : P == 2 ? L.wa1 + 7 * 64 : P == 3 ? L.wa3 + 2 * 64
+                                                                                         : L.wa3 + 6 * 64;
+  };
+  auto boff = [&](int P, int pg) -> uint32_t {
+    return P == 0 ? bc[pg][0] : P == 1 ? bc[pg][1] : P == 2 ? bc[pg][2] + 16 : P == 3 ? br[pg] + 32 : bc[pg][2];
+  };
+  u32x4 A[2], B[2][2];
+  auto load = [&](int s, int slot) {
+    const int cg = s / 5, P = s % 5;
+    A[slot] = *reinterpret_cast<const u32x4 *>(sm + aoff(P) + 32 * cg);
+#pragma unroll
+    for (int pg = 0; pg < 2; ++pg)
+      B[slot][pg] = *reinterpret_cast<const u32x4 *>(xe + boff(P, pg) + 2 * cg * PLANE);
+  };
+  u32x2 h[2][2];  // [cg][pg]: act_d of the result, packed
+  f32x4 d[2], bias;
+  load(0, 0);
+#pragma unroll
+  for (int s = 0; s < 10; ++s) {
+    const int cg = s / 5, P = s % 5, cur = s & 1;
+    if (P == 0)  // bias of rows 4q..4q+3: the first MFMA's accumulator
+      bias = unpack4<DT>(*reinterpret_cast<const u32x2 *>(sm + IRW_BD + (16 * cg + 4 * q) * 2));
+    if (s + 1 < 10) load(s + 1, cur ^ 1);
+    const u32x4 Am = A[cur] & L.mask;
+#pragma unroll
+    for (int pg = 0; pg < 2; ++pg) d[pg] = ir_mma16<DT>(Am, B[cur][pg], P == 0 ? bias : d[pg]);
+    if (P == 4) {
+#pragma unroll
+      for (int pg = 0; pg < 2; ++pg) {
+        if constexpr (RLD) {
+          const u32x2 b = pack4<DT>(d[pg]);
+          h[cg][pg] = u32x2{irw_relu2(b.x), irw_relu2(b.y)};
+        } else {
+          float t[4] = {d[pg].x, d[pg].y, d[pg].z, d[pg].w};
+          ir_act<true, 4>(act_d, t);
+          h[cg][pg] = pack4<DT>(f32x4{t[0], t[1], t[2], t[3]});
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int pg = 0; pg < 2; ++pg) bop[pg] = u32x4{h[0][pg].x, h[0][pg].y, h[1][pg].x, h[1][pg].y};
+}
+
+// Bias, act_p, residual and the store of a wavefront's projection results:
+// block og (16 output channels) of pixel group pg, lane rows 4q .. 4q + 3 =
+// output channels 16 og + 4q .. + 3 of pixel pix[pg].
+template <int DT, int NOG>
+__device__ __forceinline__ void irdw_store(const IrWaveArgs &a, const float *BpL, const f32x4 (&acc)[NOG][2],
+                                          const bool (&ok)[2], const uint32_t (&pix)[2], int q, const Act &act_p) {
+#pragma unroll
+  for (int og = 0; og < NOG; ++og) {
+    const uint32_t oc = og * 16 + 4 * q;
+    if (og * 16 >= (int)a.CO) continue;  // padding channels of the last 32-channel block
+#pragma unroll
+    for (int pg = 0; pg < 2; ++pg) {
+      if (!ok[pg]) continue;
+      f32x4 v = acc[og][pg] + *reinterpret_cast<const f32x4 *>(BpL + oc);
+      float t4[4] = {v.x, v.y, v.z, v.w};
+      ir_act<true, 4>(act_p, t4);
+      v = f32x4{t4[0], t4[1], t4[2], t4[3]};
+      const size_t vi = (size_t)pix[pg] * (a.CO / 4) + oc / 4;
+      if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
+      Vec4IO<DT>::store(a.y, vi, v);
+    }
+  }
+}
+
 // KE: expand K steps (C / 16); NPI: 32-pixel blocks of the halo tile; NOB:
 // projection blocks of 32 output channels; RL: the expand and depthwise
 // activations are both ReLU (applied to the packed 16-bit results).
+// Wavefronts per SIMD the register allocation aims for: four on the
+// narrowest shape (its operands fit 128 VGPRs), else what the shape needs.
+__host__ __device__ constexpr int irw_waves_per_simd(int ke, int npi, int nob) {
+  return ke == 2 && npi == 2 && nob == 1 ? 4 : 1;
+}
+
 template <int DT, int KE, int NPI, int NOB, bool RL>
-__global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
+__global__ __launch_bounds__(IRW_THREADS) __attribute__((amdgpu_waves_per_eu(irw_waves_per_simd(KE, NPI, NOB))))
+void ir_wave_kernel(IrWaveArgs a) {
   static_assert(DT == DT_F16 || DT == DT_BF16, "16-bit storage");
   extern __shared__ __align__(16) char lds[];
-  constexpr int ES = 2, KSTEP = 16, HK = 8, EC = 32, NKS = EC / KSTEP;
+  constexpr int ES = 2, KSTEP = 16, HK = 8, EC = 32, NOG = 2 * NOB;
   constexpr uint32_t GB = 4 * ES;  // one packed group: 4 K of one channel
   constexpr uint32_t C = KE * KSTEP;
   constexpr uint32_t WES = EC * C * ES;  // expand weights of one chunk
-  // depthwise taps whose operands are read in one batch: all nine when the
-  // registers held across a chunk (input halo, expand A operands, projection
-  // accumulators) leave room for 72 more, else one row of three. The
-  // narrowest shape (HELD <= 64) fits four waves per SIMD in 128 VGPRs only
-  // with the short batch; four waves beat the long one there.
-  constexpr int HELD = 4 * NPI * KE + 4 * KE + 16 * NOB;
-  constexpr int TB = HELD > 64 && HELD <= 120 ? 9 : 3;
-  // packed ReLU where the registers allow it (it keeps the packed results
-  // live longer; the widest instantiations would spill): on the expand's
-  // epilogue (RLE) and the depthwise result (RLD) -- on the narrowest shape
-  // only the former keeps it within 128 VGPRs
-  constexpr bool RLE = RL && HELD <= 130;
-  constexpr bool RLD = RL && HELD > 64 && HELD <= 130;
+  constexpr bool RLE = RL, RLD = RL;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, l32 = lane & 31, lh = lane >> 5;
+  const int lane = tid & 63, l32 = lane & 31, lh = lane >> 5, l16 = lane & 15, q = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // wavefronts of this workgroup (2, 4 or 8, chosen by the plan)
   const uint32_t nthr = blockDim.x, nwaves = nthr >> 6;
@@ -125,8 +272,10 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   const uint32_t nchunks = a.E / EC;
   char *WL = lds + a.lds_w;
   float *BpL = reinterpret_cast<float *>(lds + a.lds_bp);
-  char *XeL = lds + a.lds_xe + (uint32_t)wave * (NPI * 32 * IRW_RPE);
+  constexpr uint32_t PLANE = NPI * 32 * 16;  // one 8-channel plane of the expanded chunk
+  char *XeL = lds + a.lds_xe + (uint32_t)wave * (4 * PLANE);
   const Act act_e = act_params(a.act_e), act_d = act_params(a.act_d), act_p = act_params(a.act_p);
+  const IrDwLane DL = irdw_lane(lane);
 
   const __amdgpu_buffer_rsrc_t rs_we = ir_rsrc(a.we, C * a.E * ES);
   const __amdgpu_buffer_rsrc_t rs_wp = ir_rsrc(a.wp, a.E * a.CO * ES);
@@ -149,32 +298,37 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
                   [&](uint32_t g) -> uint32_t { return c * WPG + g * 16; });
     } else {
       const uint32_t rb = a.CO * GB;  // bytes of one K group's run
-      for (uint32_t q = 0; q < EC / 4; ++q)
-        irw_dma<16>(slot + WES + q * (a.COP * GB), rb / 16, rs_wp, (wave + q) % nwaves, lane, nthr,
-                    [&](uint32_t g) -> uint32_t { return c * WPG + q * rb + g * 16; });
+      for (uint32_t qq = 0; qq < EC / 4; ++qq)
+        irw_dma<16>(slot + WES + qq * (a.COP * GB), rb / 16, rs_wp, (wave + qq) % nwaves, lane, nthr,
+                    [&](uint32_t g) -> uint32_t { return c * WPG + qq * rb + g * 16; });
     }
     constexpr uint32_t TR = EC * ES / 16;  // 16-byte items per depthwise tap run
     char *sm = slot + WES + WPS;
     irw_dma<16>(sm, 9 * TR, rs_wd, wave, lane, nthr,
                 [&](uint32_t g) -> uint32_t { return ((g / TR) * a.E + EC * c) * ES + (g % TR) * 16; });
-    irw_dma<4>(sm + 9 * EC * ES, EC * ES / 4, rs_bd, wave, lane, nthr,
+    irw_dma<4>(sm + IRW_BD, EC * ES / 4, rs_bd, wave, lane, nthr,
                [&](uint32_t g) -> uint32_t { return EC * c * ES + g * 4; });
-    irw_dma<4>(sm + 10 * EC * ES, EC * ES / 4, rs_be, wave, lane, nthr,
+    irw_dma<4>(sm + IRW_BE, EC * ES / 4, rs_be, wave, lane, nthr,
                [&](uint32_t g) -> uint32_t { return EC * c * ES + g * 4; });
   };
 
   for (uint32_t i = tid; i < a.CO / 4; i += nthr)
     *reinterpret_cast<f32x4 *>(BpL + 4 * i) = Vec4IO<DT>::load(a.bp, i);
+  const uint32_t nslots = a.resident ? nchunks : 2u;
   if (a.COP != a.CO) {
     // project weights of channels CO..COP: zero in every slot, for good (the
     // copies write only channels below CO)
-    const uint32_t nslots = a.resident ? nchunks : 2u, pad16 = (a.COP - a.CO) * GB / 16;
+    const uint32_t pad16 = (a.COP - a.CO) * GB / 16;
     for (uint32_t i = tid; i < nslots * (EC / 4) * pad16; i += nthr) {
       const uint32_t sq = i / pad16, v = i - sq * pad16;
       *reinterpret_cast<u32x4 *>(WL + (sq / (EC / 4)) * SLOT + WES + (sq % (EC / 4)) * (a.COP * GB) + a.CO * GB +
                                  v * 16) = u32x4{0u, 0u, 0u, 0u};
     }
   }
+  // the zero run after each slot's taps (the copies never write it)
+  for (uint32_t i = tid; i < nslots * 4; i += nthr)
+    *reinterpret_cast<u32x4 *>(WL + (i >> 2) * SLOT + WES + WPS + IRW_TAPS_ZERO + (i & 3) * 16) =
+        u32x4{0u, 0u, 0u, 0u};
   if (a.resident) {
     for (uint32_t c = 0; c < nchunks; ++c) dma_chunk(c, c);
   } else {
@@ -182,23 +336,6 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   }
   ir_dma_wait();
   __syncthreads();
-  constexpr bool BSPLIT = DT == DT_BF16 && irw_bf16_split(KE, NPI, NOB);
-  if constexpr (BSPLIT) {
-    if (a.resident) {
-      // every chunk's depthwise taps split by channel parity, once: the
-      // slot keeps the even channels (odd halves zeroed), lds_hi gets the
-      // odd ones (even halves zeroed)
-      constexpr uint32_t TW = 9 * EC / 2;  // 32-bit words of one chunk's taps
-      for (uint32_t i = tid; i < nchunks * TW; i += nthr) {
-        const uint32_t c = i / TW, r = i - c * TW;
-        uint32_t *wlo = reinterpret_cast<uint32_t *>(WL + c * SLOT + WES + WPS) + r;
-        const uint32_t w = *wlo;
-        *wlo = w & 0x0000ffffu;
-        reinterpret_cast<uint32_t *>(lds + a.lds_hi + c * IRW_HI_BYTES)[r] = w & 0xffff0000u;
-      }
-      __syncthreads();
-    }
-  }
 
   // this workgroup's contiguous range of tiles (handed out XCD by XCD)
   const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x, a.nxcd);
@@ -214,10 +351,10 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
   // ---- per-tile state of this wavefront ----
   u32x4 xop[NPI][KE];  // input halo pixels as expand B operands
   bool inside[NPI];    // this lane's halo pixel of block b lies in the image
-  uint32_t rowo[3];    // LDS byte offsets of this lane's three depthwise tap rows
-  size_t out_pix = 0;  // this lane's output pixel
-  bool out_ok = false;
-  f32x16 acc[NOB];
+  uint32_t bc[2][3], br[2];  // depthwise B offsets per 16-pixel group
+  uint32_t pix[2];     // this lane's output pixel of each group
+  bool ok[2];
+  f32x4 acc[NOG][2];
 
   auto begin_tile = [&](uint32_t T) {
     const uint32_t img = fdiv(T, a.fd_pi);
@@ -238,24 +375,23 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
         xop[b][k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_x, off + k * 32, 0, 0));
       inside[b] = in;
     }
-    const uint32_t op = l32;
-    const bool in_tile = op < TPIX;
-    const uint32_t oy = in_tile ? fdiv(op, a.fd_tw) : 0, ox = in_tile ? op - oy * a.TW : 0;
-    const uint32_t base = oy * a.S * a.HW + ox * a.S;
 #pragma unroll
-    for (int dy = 0; dy < 3; ++dy) rowo[dy] = (base + dy * a.HW) * IRW_RPE + lh * 16;
-    const uint32_t gy = ty0 + oy, gx = tx0 + ox;
-    out_ok = in_tile && gy < a.OH && gx < a.OW;
-    out_pix = ((size_t)img * a.OH + gy) * a.OW + gx;
+    for (int pg = 0; pg < 2; ++pg) {
+      const uint32_t op = pg * 16 + l16;
+      const bool in_tile = op < TPIX;
+      const uint32_t oy = in_tile ? fdiv(op, a.fd_tw) : 0, ox = in_tile ? op - oy * a.TW : 0;
+      irdw_rows(oy * a.S * a.HW + ox * a.S, a.HW, q, PLANE, bc[pg], br[pg]);
+      const uint32_t gy = ty0 + oy, gx = tx0 + ox;
+      ok[pg] = in_tile && gy < a.OH && gx < a.OW;
+      pix[pg] = (img * a.OH + gy) * a.OW + gx;
+    }
 #pragma unroll
-    for (int o = 0; o < NOB; ++o) acc[o] = f32x16{};
+    for (int og = 0; og < NOG; ++og) acc[og][0] = acc[og][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   };
 
   // expand of chunk `slot` over the halo tile -> this wavefront's XeL, then
-  // its depthwise + projection into acc; hi: the chunk's odd-channel taps
-  // (bf16 with resident weights, the slot's taps then hold the even ones),
-  // else null
-  auto run_chunk = [&](const char *slot, const char *hi) {
+  // its depthwise and projection into acc
+  auto run_chunk = [&](const char *slot) {
     // expand A operands of the chunk: channel l32, K groups from 2 * lh; a K
     // step advances 4 groups of 32 channels (1024 bytes)
     const char *ap = slot + ((uint32_t)lh * (HK / 4) * EC + l32) * GB;
@@ -263,99 +399,43 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
 #pragma unroll
     for (int k = 0; k < KE; ++k) aw[k] = ir_ld_w<DT>(ap + k * (KSTEP * EC * ES), EC * GB);
     const char *sm = slot + WES + WPS;
-    const uint32_t bw = lh == 0 ? (uint32_t)*reinterpret_cast<const uint16_t *>(sm + 10 * EC * ES + l32 * 2) : 0u;
+    const uint32_t bw = lh == 0 ? (uint32_t)*reinterpret_cast<const uint16_t *>(sm + IRW_BE + l32 * 2) : 0u;
 #pragma unroll
     for (int b = 0; b < NPI; ++b) {
       const u32x4 bx = {(lh == 0 && inside[b]) ? ONE : 0u, 0u, 0u, 0u};
       f32x16 e = ir_mma<DT>(u32x4{bw, 0u, 0u, 0u}, bx, f32x16{});
 #pragma unroll
       for (int k = 0; k < KE; ++k) e = ir_mma<DT>(aw[k], xop[b][k], e);
-      char *row = XeL + (b * 32 + l32) * IRW_RPE;
+      // channels 8 qq + 4 lh .. + 3: plane qq, the pixel's 16 bytes at 8 lh
+      char *px = XeL + (b * 32 + l32) * 16 + lh * 8;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<u32x2 *>(row + (8 * q + 4 * lh) * ES) =
-            irw_act_pack4<DT, RLE>(act_e, f32x4{e[4 * q], e[4 * q + 1], e[4 * q + 2], e[4 * q + 3]});
+      for (int qq = 0; qq < 4; ++qq)
+        *reinterpret_cast<u32x2 *>(px + qq * PLANE) =
+            irw_act_pack4<DT, RLE>(act_e, f32x4{e[4 * qq], e[4 * qq + 1], e[4 * qq + 2], e[4 * qq + 3]});
     }
     irw_wave_order();
 
-    const char *wdp = sm + lh * 16;                 // tap t at + t * EC * ES
-    const char *bdp = sm + 9 * EC * ES + lh * 16;
-    const char *wpp = slot + WES + ((uint32_t)lh * (HK / 4) * a.COP + l32) * GB;
-    const uint32_t wp_ks = KSTEP / 4 * a.COP * GB, wp_next = a.COP * GB;
-#pragma unroll 1
-    for (int ks = 0; ks < NKS; ++ks) {
-      // the operands of TB taps go out together (2 * TB reads in flight),
-      // then their FMAs; all nine at once where the registers allow
-      float d[HK];
-      ir_unpack<DT, HK>(*reinterpret_cast<const u32x4 *>(bdp + ks * 32), d);
+    u32x4 bop[2];
+    irdw_chunk<DT, RLD, PLANE>(XeL, sm, DL, bc, br, q, act_d, bop);
+    // projection: K slice q = packed groups q and q + 4 of the chunk
+    const char *wpp = slot + WES + ((uint32_t)q * a.COP + l16) * GB;
 #pragma unroll
-      for (int t0 = 0; t0 < 9; t0 += TB) {
-        u32x4 wv[TB], xv[TB];
+    for (int og = 0; og < NOG; ++og) {
+      if (og * 16 >= (int)a.CO) continue;
+      const u32x4 wv = ir_ld_w<DT>(wpp + og * (16 * GB), 4 * a.COP * GB);
 #pragma unroll
-        for (int t = 0; t < TB; ++t) wv[t] = *reinterpret_cast<const u32x4 *>(wdp + (t0 + t) * (EC * ES) + ks * 32);
-#pragma unroll
-        for (int t = 0; t < TB; ++t)
-          xv[t] = *reinterpret_cast<const u32x4 *>(XeL + rowo[(t0 + t) / 3] + ((t0 + t) % 3) * IRW_RPE + ks * 32);
-        if constexpr (BSPLIT) {
-          if (hi) {
-            u32x4 wh[TB];
-#pragma unroll
-            for (int t = 0; t < TB; ++t)
-              wh[t] = *reinterpret_cast<const u32x4 *>(hi + lh * 16 + (t0 + t) * (EC * ES) + ks * 32);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int t = 0; t < TB; ++t) ir_fma_taps_bf16_split<HK>(xv[t], wv[t], wh[t], d);
-            continue;
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int t = 0; t < TB; ++t) ir_fma_taps<DT, HK>(xv[t], wv[t], d);
-      }
-      u32x4 bop;
-      if constexpr (RLD) {
-        bop = ir_pack<DT, HK>(d);
-        bop = u32x4{irw_relu2(bop.x), irw_relu2(bop.y), irw_relu2(bop.z), irw_relu2(bop.w)};
-      } else {
-        ir_act<true, HK>(act_d, d);
-        bop = ir_pack<DT, HK>(d);
-      }
-#pragma unroll
-      for (int o = 0; o < NOB; ++o)
-        acc[o] = ir_mma<DT>(ir_ld_w<DT>(wpp + o * (32 * GB) + ks * wp_ks, wp_next), bop, acc[o]);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int pg = 0; pg < 2; ++pg) acc[og][pg] = ir_mma16<DT>(wv, bop[pg], acc[og][pg]);
     }
     // the next chunk's expand overwrites XeL after these reads
     irw_wave_order();
-  };
-
-  auto end_tile = [&]() {
-    if (!out_ok) return;
-#pragma unroll
-    for (int o = 0; o < NOB; ++o) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t oc = o * 32 + 8 * q + 4 * lh;
-        if (o == NOB - 1 && oc >= a.CO) continue;  // padding channels of the last block
-        f32x4 v = f32x4{acc[o][4 * q], acc[o][4 * q + 1], acc[o][4 * q + 2], acc[o][4 * q + 3]} +
-                  *reinterpret_cast<const f32x4 *>(BpL + oc);
-        float t4[4] = {v.x, v.y, v.z, v.w};
-        ir_act<true, 4>(act_p, t4);
-        v = f32x4{t4[0], t4[1], t4[2], t4[3]};
-        const size_t vi = out_pix * (a.CO / 4) + oc / 4;
-        if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
-        Vec4IO<DT>::store(a.y, vi, v);
-      }
-    }
   };
 
   if (a.resident) {
     // every chunk in LDS: the wavefronts run their tiles independently
     for (uint32_t T = t_begin + wave; T < t_end; T += nwaves) {
       begin_tile(T);
-      for (uint32_t c = 0; c < nchunks; ++c)
-        run_chunk(WL + c * SLOT, BSPLIT ? lds + a.lds_hi + c * IRW_HI_BYTES : nullptr);
-      end_tile();
+      for (uint32_t c = 0; c < nchunks; ++c) run_chunk(WL + c * SLOT);
+      irdw_store<DT, NOG>(a, BpL, acc, ok, pix, q, act_p);
     }
     return;
   }
@@ -376,9 +456,9 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_wave_kernel(IrWaveArgs a) {
       __syncthreads();
       const bool last = c + 1 == nchunks;
       if (!last || more) dma_chunk(last ? 0 : c + 1, (gc + 1) & 1);
-      if (active) run_chunk(WL + (gc & 1) * SLOT, nullptr);
+      if (active) run_chunk(WL + (gc & 1) * SLOT);
     }
-    if (active) end_tile();
+    if (active) irdw_store<DT, NOG>(a, BpL, acc, ok, pix, q, act_p);
   }
   ir_dma_wait();
 }
