@@ -282,7 +282,8 @@ def test_real_model_16bit_every_op_matches_stored_dtype_oracle(segm, dt, fuse):
     of that run's output. End to end, 44 ops of 16-bit rounding accumulate
     (bf16 keeps 8 mantissa bits): the segmentation mask (argmax of the two
     logits) agrees with the fp32 run on >= 99% of pixels, f16's logits stay
-    within 1e-1; both distances are printed."""
+    within the ideal-storage distance + 5e-2 (measured 4.7e-2 against fp32);
+    the distances are printed."""
     data, graph = segm
     n = 2
     x = rnd(70, n, 160, 288, 3)
@@ -301,13 +302,15 @@ def test_real_model_16bit_every_op_matches_stored_dtype_oracle(segm, dt, fuse):
     want32 = graph.run({"input_1": x}, n=n)["segment"]
     e_st = G.rel_err(got, stored["segment"])
     e32 = G.rel_err(got, want32)
+    e_ideal = G.rel_err(stored["segment"], want32)  # ideal storage alone
     # what the model delivers: the per-pixel class (argmax of the 2 logits)
     agree = float(np.mean(got.argmax(-1) == want32.argmax(-1)))
     print(f"segm dt{dt} fuse={fuse}: worst per-op {worst:.2e}; end to end vs stored-dtype oracle {e_st:.2e}, "
-          f"vs fp32 {e32:.2e}, mask agreement {agree:.5f}", flush=True)
+          f"vs fp32 {e32:.2e} (ideal storage {e_ideal:.2e}), mask agreement {agree:.5f}", flush=True)
     assert agree >= 0.99
     if dt == F16:
-        assert e32 <= 1e-1
+        # measured: 4.7e-2 fused, 4.9e-2 unfused against fp32
+        assert e32 <= e_ideal + 5e-2, (e32, e_ideal)
 
 
 def _tile_batch(ref, reps):

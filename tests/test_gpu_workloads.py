@@ -251,11 +251,11 @@ def test_mnv4_small_encoder_160x288(dt):
         within 2e-2 once normalised by the tensor's rms (bf16's 8-bit mantissa
         puts even ideal storage at ~7e-2 on the depthwise layers, so bf16 only
         gets a 0.1 sanity bound); the literal metric is printed;
-      * end to end: drift within 3x the ideal-storage drift (f16); bf16's
-        ideal storage alone already drifts ~0.3, a regime where rounding ties
-        flipped by a different fp32 summation order (one full-K MFMA chain
-        against split-K partials, for instance) move single outputs by O(1),
-        so bf16 gets 5x."""
+      * end to end: drift within the ideal-storage drift + 0.15 (f16; measured
+        0.239 against 0.179); bf16's ideal storage alone already drifts ~0.3,
+        a regime where rounding ties flipped by a different fp32 summation
+        order move single outputs by O(1) (measured 1.26), so bf16 gets
+        + 1.2."""
     layers, meta = W.mnv4_small_encoder_160x288(2)
     wts = oracle_weights(layers, 6)
     n, h, w = 2, meta["h"], meta["w"]
@@ -270,7 +270,10 @@ def test_mnv4_small_encoder_160x288(dt):
     ideal = max(G.rel_err(oracle_chain_stored(layers, wts, x[i * img:(i + 1) * img], dt)[layers[-1].name],
                           refs[i][layers[-1].name]) for i in range(n))
     print(f"encoder dt{dt}: end-to-end drift {e2e:.3e}, ideal-storage drift {ideal:.3e}", flush=True)
-    assert e2e <= (3 if dt == F16 else 5) * ideal + 1e-3, (e2e, ideal)
+    # measured: f16 0.239 against ideal 0.179, bf16 1.258 against 0.321 (one-ulp
+    # rounding differences amplified by the network; test_encoder_16bit_drift_by_launch
+    # places them launch by launch); bound: ideal + the measured excess + a margin
+    assert e2e <= ideal + (0.15 if dt == F16 else 1.2), (e2e, ideal)
     m = Model(layers, wts, n, h, w, 3, dt=conv.DType(dt), fuse=False)
     worst_scaled = 0.0
     for i, L in enumerate(layers):
@@ -312,7 +315,7 @@ def test_mnv4_small_encoder_fused(dt):
     (The literal max |g-c|/max(|c|,1) of this ill-conditioned random network
     is dominated by a few near-zero outputs after cancellation and swings
     between runs that differ only in rounding order; it is printed, and for
-    f16 held to 3x the ideal-storage drift as in the unfused test.)"""
+    f16 held to the ideal-storage drift + 0.15 as in the unfused test.)"""
     layers, meta = W.mnv4_small_encoder_160x288(2)
     wts = oracle_weights(layers, 6)
     n, h, w = 2, meta["h"], meta["w"]
@@ -336,7 +339,105 @@ def test_mnv4_small_encoder_fused(dt):
           f"rms-scaled fused {s_f:.3e} unfused {s_u:.3e}", flush=True)
     assert s_f <= 1.5 * s_u + 2e-3, (s_f, s_u)
     if dt == F16:
-        assert e2e <= 3 * ideal + 1e-3, (e2e, ideal)
+        # measured: fused 0.114, unfused 0.239, ideal storage 0.179
+        assert e2e <= ideal + 0.15, (e2e, ideal)
+
+
+def ideal_continue(layers, wts, bufs, start, dt):
+    """The oracle chain with every stored tensor rounded to dt (exact fp32
+    arithmetic in between) from layer index `start` on, over a copy of bufs
+    (tensor name -> stored values of image 0): what ideal 16-bit storage
+    gives downstream of the tensors in bufs."""
+    bufs = dict(bufs)
+    for L in layers[start:]:
+        op = orc.conv2d(L.cin, L.cout, k=L.k, s=L.s, pad=L.pad, groups=L.groups, act=L.act)
+        cc = orc.CpuConv(op, L.ih, L.iw, orc.round_to(wts.w[L.name], dt), orc.round_to(wts.b[L.name], dt),
+                         has_res=L.res is not None)
+        bufs[L.name] = orc.round_to(cc.run(bufs[L.src], 1, bufs[L.res] if L.res else None, threads=8), dt)
+    return bufs
+
+
+@pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
+def test_encoder_16bit_drift_by_launch(dt):
+    """Where the 16-bit encoder's end-to-end drift from the fp32 chain comes
+    from (the headline's weights, seed 0; image 0 of a batch of 2; the fused
+    model with the planner's choices, as the native loader runs it).
+
+    * ideal: the oracle chain with ideal storage (every stored tensor rounded
+      to dt, exact fp32 arithmetic in between);
+    * gpu: the GPU model end to end;
+    * per launch j: the ideal chain with launch j alone run on the GPU (fed the
+      ideal chain's stored inputs, its output carried on by the ideal chain):
+      how much that one launch's own rounding -- fp32 sums in another order
+      that round to a neighbouring 16-bit value -- moves the end result.
+
+    * ideal64: ideal storage again with the arithmetic in fp64 -- the same
+      rounding points, only which way a few values round differs.
+
+    Printed as a table. Measured, f16: gpu 0.316, ideal 0.179, ideal64 0.256;
+    one launch on the GPU moves the end result by -0.09 (the stem) to +0.21
+    (b0) while its own output is within 1-2 ulps of ideal storage: the
+    network amplifies one-ulp rounding differences to tenths of the literal
+    metric, as the two exact-arithmetic references already differ by 0.08.
+    bf16 (8-bit mantissa): gpu 2.01, ideal 1.76, ideal64 1.28, single
+    launches -0.39 .. +0.32. Asserted (measured plus a margin): no single
+    launch moves it by more than 0.3 f16 / 0.6 bf16 (a lost term or a wrong
+    index moves it by O(1)), and the end-to-end drift stays within 0.45 f16 /
+    3.0 bf16."""
+    layers, meta = W.mnv4_small_encoder_160x288(2)
+    wts = W.make_weights(layers, seed=0)
+    n, h, w = 2, meta["h"], meta["w"]
+    x0 = orc.xs32_fill(6500, h * w * 3)
+    x = np.concatenate([x0, x0])
+    ref = oracle_chain(layers, wts, x0, h, w)
+    out = layers[-1].name
+    ideal = ideal_continue(layers, wts, {"input": orc.round_to(x0, dt)}, 0, dt)
+    e_ideal = G.rel_err(ideal[out], ref[out])
+    m = Model(layers, wts, n, h, w, 3, dt=conv.DType(dt), tune=False)
+    m.upload_input(G.dev(x))
+    m.infer()
+    torch.cuda.synchronize()
+    e_gpu = G.rel_err(m.read_output().reshape(n, -1)[0], ref[out])
+    index = {L.name: k for k, L in enumerate(layers)}
+    rows = []
+    for op in m.ops:
+        for L in op.layers[:1]:
+            for name in {L.src} | ({op.layers[-1].res} if op.layers[-1].res else set()):
+                hh, ww, cc = m.shapes[name]
+                m.tensors[name].copy_(G.dev(orc.pack_nhwc(np.concatenate([ideal[name]] * n), n, hh, ww, cc, dt)))
+        m._input_packed = True  # the stem reads the stored input just written
+        m.launch_op(m.ops.index(op))
+        torch.cuda.synchronize()
+        last = op.layers[-1].name
+        got = image_of(m, last, 0, dt)
+        cont = ideal_continue(layers, wts, {**ideal, last: got}, index[last] + 1, dt)
+        e_j = G.rel_err(cont[out], ref[out])
+        rows.append((op.name, G.rel_err(got, ideal[last]), e_j))
+    print(f"encoder dt{dt} drift from the fp32 chain: gpu {e_gpu:.4f}, ideal storage {e_ideal:.4f}", flush=True)
+    print("  launch       local vs ideal   end result with this launch on the GPU (change vs ideal)", flush=True)
+    for name, loc, e_j in rows:
+        print(f"  {name:10s}   {loc:.3e}        {e_j:.4f} ({e_j - e_ideal:+.4f})", flush=True)
+    # the same ideal storage with the arithmetic in fp64 (torch, CPU) instead
+    # of the oracle's fp32 sums: another exact-arithmetic reference whose only
+    # difference is which way a few values round
+    b64 = {"input": orc.round_to(x0, dt).astype(np.float64)}
+    for L in layers:
+        xin = torch.from_numpy(b64[L.src].reshape(1, L.ih, L.iw, L.cin)).permute(0, 3, 1, 2)
+        wt = torch.from_numpy(orc.round_to(wts.w[L.name], dt).astype(np.float64)).reshape(
+            L.cout, 1 if L.depthwise else L.cin, L.k, L.k)
+        bt = torch.from_numpy(orc.round_to(wts.b[L.name], dt).astype(np.float64))
+        y = torch.nn.functional.conv2d(xin, wt, bt, stride=L.s, padding=L.pad, groups=L.groups)
+        y = y.clamp_min(0) if L.act == "relu" else y
+        y = y.permute(0, 2, 3, 1).reshape(-1).numpy()
+        if L.res:
+            y = y + b64[L.res]
+        b64[L.name] = orc.round_to(y.astype(np.float32), dt).astype(np.float64)
+    e_ideal64 = G.rel_err(b64[out], ref[out])
+    print(f"  ideal storage with fp64 arithmetic: {e_ideal64:.4f} ({e_ideal64 - e_ideal:+.4f} against fp32 "
+          f"arithmetic)", flush=True)
+    worst_shift = max(abs(e_j - e_ideal) for _, _, e_j in rows)
+    assert worst_shift <= (0.3 if dt == F16 else 0.6), worst_shift
+    assert e_gpu <= (0.45 if dt == F16 else 3.0), e_gpu
 
 
 # ---------------------------------------------------------------- the benchmarked routes at full batch
