@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
+#include <set>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -160,6 +162,14 @@ struct aih_model {
   std::vector<Fused> fused;
   std::vector<int32_t> block_of;  // per op: its fused block, or -1
   std::vector<int32_t> internal;  // per tensor: first op of the fused block it stays inside, or -1
+  // A stem conv that is the graph's single input's only reader reads the
+  // uploaded logical NHWC fp32 values from `staging` itself
+  // (aih_conv_stem_f32in: the pack and the conv in one launch, the same
+  // result bit for bit). staged: the input's values sit in staging and its
+  // NHWC-C4 slot is stale until settle_input packs it.
+  int64_t stem_op = -1;
+  uint32_t stem_tid = 0;
+  bool staged = false;
 
   ~aih_model() {
     for (void *p : allocs) (void)hipFree(p);
@@ -545,6 +555,145 @@ void find_fusions(aih_model *m) {
   }
 }
 
+// Load-time tuning (AIH_MODEL_TUNE): every fused inverted-residual block's
+// launch options -- the plan's own choice, and the wave kernel (weights
+// resident and streamed), the split kernel (2 / 4 / 8 wavefronts a tile) and
+// the tile kernel at a set of forced output tiles -- are timed on the device
+// with the model's own buffers, two warm-up launches and five timed ones each
+// (the median), and the fastest is kept. The reference's Model::load does its
+// per-model device work -- pipeline compilation -- once at load
+// (crates/ai-gpu-runtime/src/model.rs:56-366); this is the same kind of
+// one-time cost, a few milliseconds a block. The kernels' arithmetic does not
+// depend on the choice beyond the fp32 summation order.
+constexpr uint32_t kTuneWaveTiles[][2] = {{0, 0}, {4, 8}, {8, 4}, {5, 6}, {6, 5}, {2, 16}, {16, 2}, {3, 10}};
+constexpr uint32_t kTuneTileTiles[][2] = {{0, 0}, {4, 8}, {8, 4}, {8, 8}, {4, 16}, {16, 4}, {8, 16}, {16, 8}};
+
+void tune_blocks(aih_model *m) {
+  hipStream_t st = nullptr;
+  if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) throw std::runtime_error("tune: hipStreamCreate");
+  hipEvent_t ev[12];
+  for (auto &e : ev)
+    if (hipEventCreate(&e) != hipSuccess) throw std::runtime_error("tune: hipEventCreate");
+  struct Cleanup {
+    hipStream_t st;
+    hipEvent_t *ev;
+    ~Cleanup() {
+      for (int i = 0; i < 12; ++i) (void)hipEventDestroy(ev[i]);
+      (void)hipStreamDestroy(st);
+    }
+  } cleanup{st, ev};
+  for (aih_model::Fused &f : m->fused) {
+    if (f.nops != 3) continue;
+    const sw::Op &A = m->g.ops[f.first], &B = m->g.ops[f.first + 1], &P = m->g.ops[f.first + 2];
+    const void *x = m->ptr(A.in), *we = m->wptr(A.w), *be = m->wptr(A.b), *wd = m->wptr(B.w), *bd = m->wptr(B.b),
+               *wp = m->wptr(P.w), *bp = m->wptr(P.b);
+    const void *res = P.res >= 0 ? m->ptr((uint32_t)P.res) : nullptr;
+    void *y = m->ptr(P.out);
+    std::vector<aih_ir_block_desc> cands;
+    auto add = [&](int32_t kernel, const uint32_t (&t)[2], int32_t weights, uint32_t waves) {
+      aih_ir_block_desc d = f.d;
+      d.tile_h = t[0];
+      d.tile_w = t[1];
+      d.kernel = kernel;
+      d.weights = weights;
+      d.waves = waves;
+      cands.push_back(d);
+    };
+    cands.push_back(f.d);
+    for (const auto &t : kTuneWaveTiles) {
+      add(AIH_IR_KERNEL_WAVE, t, AIH_IR_WEIGHTS_RESIDENT, 0);
+      add(AIH_IR_KERNEL_WAVE, t, AIH_IR_WEIGHTS_STREAMED, 0);
+      for (uint32_t w : {2u, 4u, 8u}) add(AIH_IR_KERNEL_SPLIT, t, AIH_IR_WEIGHTS_AUTO, w);
+    }
+    for (const auto &t : kTuneTileTiles) {
+      add(AIH_IR_KERNEL_TILE, t, AIH_IR_WEIGHTS_RESIDENT, 0);
+      add(AIH_IR_KERNEL_TILE, t, AIH_IR_WEIGHTS_STREAMED, 0);
+    }
+    std::set<std::array<uint32_t, 5>> seen;
+    float best = -1.0f;
+    for (const aih_ir_block_desc &d : cands) {
+      aih_ir_plan plan;
+      if (aih_ir_block_plan(&d, &plan) != AIH_OK) continue;  // a forced option this block cannot run
+      const std::array<uint32_t, 5> key{plan.kernel, plan.th, plan.tw, plan.resident,
+                                        plan.kernel == AIH_IR_KERNEL_SPLIT ? plan.waves : 0u};
+      if (!seen.insert(key).second) continue;
+      // the plan's choice, made explicit, so later calls run exactly it
+      aih_ir_block_desc dd = d;
+      dd.tile_h = plan.th;
+      dd.tile_w = plan.tw;
+      dd.kernel = (int32_t)plan.kernel;
+      if (plan.kernel != AIH_IR_KERNEL_SPLIT)
+        dd.weights = plan.resident ? AIH_IR_WEIGHTS_RESIDENT : AIH_IR_WEIGHTS_STREAMED;
+      else
+        dd.waves = plan.waves;
+      for (int w = 0; w < 2; ++w)
+        if (aih_ir_block(&dd, x, we, be, wd, bd, wp, bp, res, y, st) != AIH_OK)
+          throw std::runtime_error(std::string("tune: ") + aih_last_error());
+      float t[5];
+      for (int r = 0; r < 5; ++r) {
+        if (hipEventRecord(ev[2 * r], st) != hipSuccess ||
+            aih_ir_block(&dd, x, we, be, wd, bd, wp, bp, res, y, st) != AIH_OK ||
+            hipEventRecord(ev[2 * r + 1], st) != hipSuccess)
+          throw std::runtime_error("tune: launch");
+      }
+      if (hipEventSynchronize(ev[9]) != hipSuccess) throw std::runtime_error("tune: hipEventSynchronize");
+      for (int r = 0; r < 5; ++r)
+        if (hipEventElapsedTime(&t[r], ev[2 * r], ev[2 * r + 1]) != hipSuccess)
+          throw std::runtime_error("tune: hipEventElapsedTime");
+      std::sort(t, t + 5);
+      if (best < 0 || t[2] < best) {
+        best = t[2];
+        f.d = dd;
+        f.plan = plan;
+      }
+    }
+  }
+  if (hipStreamSynchronize(st) != hipSuccess) throw std::runtime_error("tune: hipStreamSynchronize");
+}
+
+// The stem-from-fp32 route for the graph's input (see aih_model::stem_op):
+// one input, read only by op k, a dense 3x3 conv on the stem route (d = 1,
+// cin <= 3, cout 32 or 64, weights in the activation dtype), not a graph
+// output, state or alias; not under AIH_MODEL_NO_FUSE (every op on its own).
+void find_stem_input(aih_model *m) {
+  const auto &ops = m->g.ops;
+  if ((m->flags & AIH_MODEL_NO_FUSE) || m->g.inputs.size() != 1 || m->dt != m->wdt) return;
+  const uint32_t t = m->g.inputs[0];
+  if (m->g.tensors[t].alias_of >= 0) return;
+  for (uint32_t o : m->g.outputs)
+    if (o == t) return;
+  for (const auto &st : m->g.states)
+    if (st.first == t || st.second == t) return;
+  for (const auto &tt : m->g.tensors)
+    if (tt.alias_of == (int64_t)t) return;
+  int64_t reader = -1;
+  size_t nreads = 0;
+  for (size_t k = 0; k < ops.size(); ++k)
+    for (uint32_t r : reads_of(ops[k]))
+      if (r == t) {
+        ++nreads;
+        reader = (int64_t)k;
+      }
+  if (nreads != 1 || m->block_of[(size_t)reader] >= 0) return;
+  const sw::Op &op = ops[(size_t)reader];
+  if (op.kind != sw::OP_CONV || op.in != t || !op.srcs.empty() || op.groups != 1 || op.kh != 3 || op.kw != 3 ||
+      op.sh != op.sw || op.d != 1 || op.cin > 3 || (op.cout != 32 && op.cout != 64) || !m->dense(t))
+    return;
+  m->stem_op = reader;
+  m->stem_tid = t;
+}
+
+// Packs the staged fp32 input into its NHWC-C4 slot (for a reader of the
+// slot other than the stem: read_output, tensor storage).
+int settle_input(const aih_model *cm, aih_stream stream) {
+  aih_model *m = const_cast<aih_model *>(cm);
+  if (!m->staged) return AIH_OK;
+  const auto &t = m->g.tensors[m->stem_tid];
+  if (aih_pack_nhwc_device(m->staging, m->n, t.h, t.w, t.c, m->dt, m->ptr(m->stem_tid), stream)) return AIH_ERR;
+  m->staged = false;
+  return AIH_OK;
+}
+
 void lower(aih_model *m) {
   const auto &T = m->g.tensors;
   for (size_t k = 0; k < m->g.ops.size(); ++k) {
@@ -660,6 +809,28 @@ void lower(aih_model *m) {
           m->ws_bytes = std::max(m->ws_bytes, ws);
           const void *x = m->ptr(op.in);
           aih_model *mm = m;
+          if ((int64_t)k == m->stem_op) {
+            aih_igemm_desc sd{};
+            sd.n = m->n;
+            sd.ih = I.h;
+            sd.iw = I.w;
+            sd.cin = op.cin;
+            sd.cout = op.cout;
+            sd.k = 3;
+            sd.s = op.sh;
+            sd.d = 1;
+            std::memcpy(sd.pad, op.pad, sizeof(sd.pad));
+            sd.act = op.act;
+            sd.residual = res ? 1 : 0;
+            sd.dt = m->dt;
+            sd.wdt = wdt;  // one dense input: no parts (nsrcs 0)
+            m->launches.push_back([mm, d, sd, x, w, b, res, y](hipStream_t s) {
+              // the staged fp32 upload, read by the stem itself; else the slot
+              return mm->staged ? aih_conv_stem_f32in(&sd, mm->staging, w, b, res, y, s)
+                                : aih_conv(&d, x, w, b, res, y, mm->ws, mm->ws_bytes, s);
+            });
+            break;
+          }
           m->launches.push_back([mm, d, x, w, b, res, y](hipStream_t s) {
             return aih_conv(&d, x, w, b, res, y, mm->ws, mm->ws_bytes, s);
           });
@@ -752,7 +923,7 @@ aih_model *aih_model_load_ex(const void *bytes, size_t len, uint32_t n, int32_t 
   aih_model *out = nullptr;
   const int rc = api_guarded([&] {
     if (n == 0) return api_fail("model_load: n must be >= 1");
-    if (flags & ~(uint32_t)AIH_MODEL_NO_FUSE) return api_fail("model_load: unknown flags");
+    if (flags & ~(uint32_t)(AIH_MODEL_NO_FUSE | AIH_MODEL_TUNE)) return api_fail("model_load: unknown flags");
     if (dt != -1 && dt != AIH_F32 && dt != AIH_F16 && dt != AIH_BF16) return api_fail("model_load: unknown dtype");
     sw::Container c = sw::parse_container(bytes, len);
     std::unique_ptr<aih_model> m(new aih_model);
@@ -777,6 +948,8 @@ aih_model *aih_model_load_ex(const void *bytes, size_t len, uint32_t n, int32_t 
     prepare_weights(m.get(), c);
     find_fusions(m.get());
     alloc_tensors(m.get());
+    if (flags & AIH_MODEL_TUNE) tune_blocks(m.get());
+    find_stem_input(m.get());
     lower(m.get());
     if (m->ws_bytes) m->ws = m->dalloc(m->ws_bytes);
     for (uint32_t t : m->g.inputs)
@@ -802,12 +975,21 @@ static int upload(aih_model *m, const char *name, const float *src, size_t count
     if (!m->dense((uint32_t)tid)) return api_fail("upload_input: input is a channel view");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const float *x = src;
-    if (host) {
-      const hipError_t e = hipMemcpyAsync(m->staging, src, count * 4, hipMemcpyHostToDevice, s);
+    if (m->stem_op >= 0 && (uint32_t)tid == m->stem_tid) {
+      // the stem reads the fp32 values from staging at infer (a copy, as
+      // Model::upload_input copies: the caller's buffer is free afterwards)
+      const hipError_t e = hipMemcpyAsync(m->staging, src, count * 4,
+                                          host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice, s);
       if (e != hipSuccess) return hip_fail("upload_input copy", e);
-      x = m->staging;
+      m->staged = true;
+    } else {
+      if (host) {
+        const hipError_t e = hipMemcpyAsync(m->staging, src, count * 4, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) return hip_fail("upload_input copy", e);
+        x = m->staging;
+      }
+      if (aih_pack_nhwc_device(x, m->n, t.h, t.w, t.c, m->dt, m->ptr((uint32_t)tid), stream)) return AIH_ERR;
     }
-    if (aih_pack_nhwc_device(x, m->n, t.h, t.w, t.c, m->dt, m->ptr((uint32_t)tid), stream)) return AIH_ERR;
     if (host) {
       const hipError_t e = hipStreamSynchronize(s);
       if (e != hipSuccess) return hip_fail("upload_input", e);
@@ -858,6 +1040,7 @@ int aih_model_read_output(aih_model *m, const char *name, float *host_nhwc, size
     const int64_t tid = m->find(name);
     if (tid < 0) return api_fail(std::string("read_output: no tensor named '") + (name ? name : "") + "'");
     m->need_stored((uint32_t)tid, "read_output");
+    if ((uint32_t)tid == m->stem_tid && settle_input(m, stream)) return AIH_ERR;
     const auto &t = m->g.tensors[tid];
     const size_t want = (size_t)m->n * t.h * t.w * t.c;
     if (count != want) return api_fail("read_output: expected " + std::to_string(want) + " floats");
@@ -893,6 +1076,7 @@ int aih_model_write_tensor(aih_model *m, const char *name, const float *host_nhw
     const int64_t tid = m->find(name);
     if (tid < 0) return api_fail(std::string("write_tensor: no tensor named '") + (name ? name : "") + "'");
     m->need_stored((uint32_t)tid, "write_tensor");
+    if ((uint32_t)tid == m->stem_tid && settle_input(m, stream)) return AIH_ERR;
     const auto &t = m->g.tensors[tid];
     const size_t want = (size_t)m->n * t.h * t.w * t.c;
     if (count != want) return api_fail("write_tensor: expected " + std::to_string(want) + " floats");
@@ -940,6 +1124,13 @@ int aih_model_tensor(const aih_model *m, const char *name, aih_tensor_info *out)
     const int64_t tid = m->find(name);
     if (tid < 0) return api_fail(std::string("tensor: no tensor named '") + (name ? name : "") + "'");
     m->need_stored((uint32_t)tid, "tensor");
+    if ((uint32_t)tid == m->stem_tid && m->staged) {
+      // the caller may read or write the slot directly from now on: it holds
+      // the last upload, and infer reads it
+      if (settle_input(m, nullptr)) return AIH_ERR;
+      const hipError_t e = hipStreamSynchronize(nullptr);
+      if (e != hipSuccess) return hip_fail("tensor", e);
+    }
     const auto &t = m->g.tensors[tid];
     const aih_model::View &v = m->views[tid];
     const size_t skip = (size_t)v.c_off * es_of(m->dt);

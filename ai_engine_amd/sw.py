@@ -58,7 +58,7 @@ class FusedInfo(C.Structure):
     _fields_ = [("first_op", C.c_uint32), ("n_ops", C.c_uint32), ("plan", conv.IrPlan), ("dwpw", conv.DwPwPlan)]
 
 
-NO_FUSE = 1  # aih_model_flags
+NO_FUSE, TUNE = 1, 2  # aih_model_flags
 
 
 EXPORTS = (
@@ -170,12 +170,15 @@ def concat(parts, n, h, w, dt, y, stream=None):
 class SwModel:
     """A .sw model resident on the current HIP device (batch n, outermost).
     fuse=False lowers every op on its own (AIH_MODEL_NO_FUSE); by default each
-    inverted-residual block runs as one fused launch."""
+    inverted-residual block runs as one fused launch. tune=True times each
+    fused block's launch options at load and keeps the fastest
+    (AIH_MODEL_TUNE)."""
 
-    def __init__(self, data: bytes, n: int = 1, dt: conv.DType | None = None, fuse: bool = True):
+    def __init__(self, data: bytes, n: int = 1, dt: conv.DType | None = None, fuse: bool = True,
+                 tune: bool = False):
         L = lib()
         self._h = L.aih_model_load_ex(bytes(data), len(data), n, -1 if dt is None else int(dt),
-                                      0 if fuse else NO_FUSE)
+                                      (0 if fuse else NO_FUSE) | (TUNE if tune else 0))
         if not self._h:
             raise conv.AihError(conv.last_error())
         self.n = n

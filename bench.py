@@ -238,6 +238,8 @@ def main() -> int:
         kernels["encoder_f16" if args.dtype == "bf16" else "encoder_bf16"] = encoder_other(
             torch, W, Model, layers, wts, x, n, H, Wd, "f16" if args.dtype == "bf16" else "bf16", DT, stream)
     kernels["encoder_layers"] = layer_rows
+    kernels["encoder_via_aih_model"] = encoder_native(torch, W, layers, wts, x, n, H, Wd, DT[args.dtype], stream,
+                                                      fps)
     kernels["encoder_block_choices"] = {k: {"choice": v[0], "us": round(v[1], 2)} for k, v in model.choices.items()}
 
     # ------------------------------------------------------------ CPU baseline (oracle ai-cpu restatement)
@@ -579,6 +581,40 @@ def real_model(torch, conv, dev, stream) -> dict:
             f"({m.info.n_launches} launches)")
         m.close()
     return out
+
+
+def encoder_native(torch, W, layers, wts, x, n, H, Wd, dt, stream, headline_fps) -> dict:
+    """The headline step through the graph-level C ABI: the same encoder and
+    weights written as the reference converter's .sw container, loaded by
+    aih_model_load_ex with load-time tuning (AIH_MODEL_TUNE) and 16-bit
+    storage; one step = aih_model_upload_input_device of the resident fp32
+    input + aih_model_infer, timed as the headline is."""
+    from ai_engine_amd import sw
+
+    data = sw.conv_graph_to_sw("mnv4_small_encoder_160x288", layers, wts, H, Wd, 3)
+    m = sw.SwModel(data, n=n, dt=dt, tune=True)
+    out = m.outputs[0]
+
+    def step(_):
+        m.upload_input("input", x, stream)
+        m.infer(stream)
+
+    for _ in range(5):
+        step(0)
+    torch.cuda.synchronize()
+    K = 50
+    t0 = time.perf_counter()
+    for _ in range(K):
+        step(0)
+    torch.cuda.synchronize()
+    t = (time.perf_counter() - t0) / K
+    row = dict(us=round(t * 1e6, 1), frames_per_s=round(n / t, 1), ratio_to_headline=round(n / t / headline_fps, 4),
+               launches=m.info.n_launches, output=out,
+               fused_blocks=[f"ops {f.first_op}-{f.first_op + f.n_ops - 1}: {f.plan}" for f in m.fused_blocks()])
+    log(f"encoder via aih_model_* ({m.info.n_launches} launches): {t * 1e3:.3f} ms {n / t:.0f} frames/s "
+        f"({row['ratio_to_headline']:.3f} of the headline)")
+    m.close()
+    return row
 
 
 def encoder_other(torch, W, Model, layers, wts, x, n, H, Wd, dtname, DT, stream) -> dict:

@@ -133,8 +133,13 @@ aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt)
  * split a fused block. The reference runtime dispatches the convs separately
  * (lowering.rs:122-152); this fusion has no counterpart there and keeps each
  * conv's arithmetic and rounding points. AIH_MODEL_NO_FUSE lowers every op on
- * its own. */
-enum aih_model_flags { AIH_MODEL_NO_FUSE = 1 };
+ * its own. AIH_MODEL_TUNE times each fused inverted-residual block's launch
+ * options at load (the plan's choice; the wave, split and tile kernels at a
+ * set of forced tiles, weight placements and wavefront counts; a few
+ * launches each on the model's own buffers) and keeps the fastest, as the
+ * reference's Model::load does its per-model device work once
+ * (model.rs:56-366); aih_model_fused_block reports the choice. */
+enum aih_model_flags { AIH_MODEL_NO_FUSE = 1, AIH_MODEL_TUNE = 2 };
 aih_model *aih_model_load_ex(const void *bytes, size_t len, uint32_t n, int32_t dt, uint32_t flags);
 void aih_model_free(aih_model *m);
 

@@ -471,6 +471,41 @@ def test_fusion_needs_single_readers(orc):
     m.close()
 
 
+@pytest.mark.parametrize("dt", [F16, BF16], ids=["f16", "bf16"])
+def test_encoder_through_the_native_loader_tuned(dt):
+    """The headline encoder written as the converter's .sw and loaded by
+    aih_model_load_ex with AIH_MODEL_TUNE (each fused block's launch options
+    timed at load): all ten inverted-residual blocks fuse, the stem reads the
+    staged fp32 upload, and the output equals bit for bit that of the op-level
+    Model (ai_engine_amd.model) told to run the same kernels -- whose launches
+    the oracle checks in test_gpu_workloads / test_gpu_ir_tiles. Batch 8."""
+    from ai_engine_amd import workloads as W
+    from ai_engine_amd.model import Model
+
+    n = 8
+    layers, meta = W.mnv4_small_encoder_160x288(n)
+    wts = W.make_weights(layers, seed=0)
+    data = sw.conv_graph_to_sw("mnv4_small_encoder_160x288", layers, wts, meta["h"], meta["w"], 3)
+    x = torch.from_numpy(rnd(91, n, meta["h"], meta["w"], 3)).cuda()
+    m = sw.SwModel(data, n=n, dt=conv.DType(dt), tune=True)
+    blocks = m.fused_blocks()
+    assert [f.n_ops for f in blocks] == [3] * 10 and m.info.n_launches == 12
+    choices = {f"b{i}": Model.label_of(f.plan.kernel, f.plan.th, f.plan.tw, bool(f.plan.resident), f.plan.waves)
+               for i, f in enumerate(blocks)}
+    print(f"native tuned choices dt{dt}: {choices}", flush=True)
+    m.upload_input("input", x)
+    m.infer()
+    got = np.ravel(m.read_output())
+    ref = Model(layers, wts, n, meta["h"], meta["w"], 3, dt=conv.DType(dt), choices=choices)
+    ref.upload_input(x)
+    ref.infer()
+    want = np.ravel(ref.read_output())
+    assert np.array_equal(got, want), float(np.max(np.abs(got - want)))
+    # the stored input slot, packed on demand, equals the op-level model's
+    assert np.array_equal(np.ravel(m.read_output("input")), np.ravel(ref.read_output("input")))
+    m.close()
+
+
 def test_projection_reading_its_input_twice_stays_unfused(orc):
     """A projection whose residual is its own input (the depthwise output,
     cin == cout) reads that tensor through two slots: it counts as two
