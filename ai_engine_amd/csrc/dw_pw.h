@@ -10,10 +10,10 @@
 
 namespace aih {
 
-// 16-byte units (4 fp32 channels) of one chunk per halo pixel: 4, i.e. 16
-// channels (32-channel chunks, whole 128-byte lines, measured slower: twice
-// the LDS per buffer halves the resident workgroups, and a channel count
-// such as 44 pads its last chunk by a third). In LDS a halo pixel takes one
+// 16-byte units of one chunk per halo pixel: 4, i.e. 16 fp32 channels or 32
+// 16-bit ones (fp32: 32-channel chunks, whole 128-byte lines, measured
+// slower: twice the LDS per buffer halves the resident workgroups, and a
+// channel count such as 44 pads its last chunk by a third). In LDS a halo pixel takes one
 // more unit, the pad: an odd number of units puts the 16 consecutive pixels
 // one ds_read_b128 reads in distinct banks.
 constexpr int kDpUnits = 4;
@@ -39,7 +39,7 @@ struct DwPwArgs {
   uint32_t HWE;      // stride 2: columns of the even half (ceil(HW / 2)); halo columns are stored even first
   uint32_t tiles_x, per_img, ntiles;
   FastDiv fd_pi, fd_tx, fd_hw;
-  uint32_t nchunks;    // chunks of 4 * kDpUnits channels of C
+  uint32_t nchunks;    // chunks of kDpUnits 16-byte units (4 fp32 / 8 16-bit channels each) of C
   uint32_t xrows;      // 64-slot rows (1 KB) of the halo region: HH * HW * (U + 1) slots rounded up
   uint32_t buf_bytes;  // one LDS chunk buffer
   uint32_t off_wd;     // inside a buffer: depthwise weights [K*K][U units], bias [U], pointwise weights [U][COP][4]
@@ -71,6 +71,14 @@ inline uint32_t dwpw_buf_bytes(uint32_t k, uint32_t s, uint32_t hh, uint32_t hw,
 // rows: output rows per wavefront (2 or 4).
 hipError_t launch_dw_pw(const DwPwArgs &a, int dt, uint32_t k, uint32_t s, uint32_t rows, uint32_t waves,
                         uint32_t lds, uint32_t grid, hipStream_t st);
+// The 16-bit instantiations (dw_pw_f16.hip, dw_pw_bf16.hip). occ: -2 no
+// instantiation, -1 no device to ask, else workgroups per CU.
+hipError_t launch_dw_pw_f16(const DwPwArgs &a, uint32_t k, uint32_t s, uint32_t rows, uint32_t waves, uint32_t lds,
+                            uint32_t grid, hipStream_t st);
+hipError_t launch_dw_pw_bf16(const DwPwArgs &a, uint32_t k, uint32_t s, uint32_t rows, uint32_t waves, uint32_t lds,
+                             uint32_t grid, hipStream_t st);
+int dw_pw_occ_f16(uint32_t k, uint32_t s, uint32_t no, uint32_t rows, bool cl, uint32_t waves, uint32_t lds);
+int dw_pw_occ_bf16(uint32_t k, uint32_t s, uint32_t no, uint32_t rows, bool cl, uint32_t waves, uint32_t lds);
 // cl: both activations clamp-type (the instantiation launch_dw_pw runs for them).
 int dw_pw_occupancy(int dt, uint32_t k, uint32_t s, uint32_t cout, uint32_t rows, bool cl, uint32_t waves,
                     uint32_t lds);

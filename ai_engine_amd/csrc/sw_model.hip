@@ -450,7 +450,7 @@ bool is_pw(const sw::Op &o) {
 bool fuse_pair(aih_model *m, size_t k, const std::vector<uint32_t> &readers, const std::vector<bool> &pinned) {
   const auto &ops = m->g.ops;
   const auto &T = m->g.tensors;
-  if (m->dt != AIH_F32 || m->wdt != AIH_F32 || k + 1 >= ops.size()) return false;
+  if (m->dt != m->wdt || k + 1 >= ops.size()) return false;
   const sw::Op &B = ops[k], &P = ops[k + 1];
   const bool ok = B.kind == sw::OP_CONV && B.kh == 3 && B.kw == 3 && B.sh == B.sw && B.d == 1 &&
                   B.groups == B.cin && B.cin == B.cout && B.srcs.empty() && B.res < 0 && is_pw(P) &&

@@ -290,12 +290,14 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
  * -- as one kernel; the depthwise output never goes to memory. No
  * counterpart op in the reference (a fusion of those two dispatches). Each
  * stage keeps its unfused arithmetic (fp32 accumulation, depthwise sum from
- * the bias over the taps in (ky, kx) order, y = act(acc + bias) (+ res)).
+ * the bias over the taps in (ky, kx) order, y = act(acc + bias) (+ res)),
+ * and at 16 bit its rounding point: the depthwise result is rounded to dt
+ * where the unfused depthwise stores it.
  * Buffers in the unfused ops' layouts: x [n][ih][iw][c] NHWC-C4, w_dw / b_dw
  * as aih_conv_dw takes them, w_pw / b_pw as aih_conv_pw takes them (packed
  * kg_align 4, kg_pad groups), res / y [n][oh][ow][cout] NHWC-C4; every buffer
- * 16-byte aligned. fp32 storage only; cout 1..64; fails with a message
- * otherwise (the caller then runs the two ops). */
+ * 16-byte aligned. Storage f32, f16 or bf16 (every buffer in dt); cout
+ * 1..64; fails with a message otherwise (the caller then runs the two ops). */
 typedef struct {
   uint32_t n, ih, iw, c;   /* depthwise input: n images, c channels */
   uint32_t k, s;           /* depthwise kernel (3) and stride (1 or 2) */
@@ -304,14 +306,15 @@ typedef struct {
   uint32_t kg_pad;         /* kg of the packed pointwise weights (>= ceil(c / 4)) */
   int32_t act_dw, act_pw;  /* enum aih_act */
   int32_t residual;        /* 0 or 1: y = act_pw(...) + res */
-  int32_t dt;              /* AIH_F32 */
+  int32_t dt;              /* enum aih_dtype: AIH_F32, AIH_F16 or AIH_BF16 */
   uint32_t tile_h, tile_w; /* output tile (16-column multiples, 1-8 wavefronts); 0 = chosen by the plan */
   uint32_t wave_rows;      /* output rows per wavefront, 2 or 4; 0 = chosen by the plan */
 } aih_dwpw_desc;
 
 /* Geometry aih_conv_dwpw_plan chose: output tile th x tw (a wavefront per
- * wave_rows rows x 16 columns), channel chunks of 16, tiles (one workgroup
- * each), LDS bytes and resident workgroups per CU, launched workgroups. */
+ * wave_rows rows x 16 columns), channel chunks of 16 (fp32) or 32 (16-bit),
+ * tiles (one workgroup each), LDS bytes and resident workgroups per CU,
+ * launched workgroups. */
 typedef struct {
   uint32_t th, tw, waves, wave_rows, chunks, tiles, lds_bytes, occupancy, grid;
 } aih_dwpw_plan;

@@ -126,9 +126,9 @@ aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt)
  * consecutive in the file's op order, whose two intermediate tensors no other
  * op, alias, graph output or state uses, and that aih_ir_block_plan accepts
  * (the plan's deterministic choice of kernel, tile and weight placement).
- * Elsewhere, in an fp32 model, a 3x3 depthwise and the 1x1 conv after it that
- * alone reads its output run as one aih_conv_dwpw launch when its plan has
- * a tile for every CU. The intermediates are then never stored:
+ * Elsewhere, a 3x3 depthwise and the 1x1 conv after it that alone reads its
+ * output run as one aih_conv_dwpw launch when its plan has a tile for every
+ * CU (weights in the activation dtype). The intermediates are then never stored:
  * reading, writing or querying them fails, and aih_model_infer_range may not
  * split a fused block. The reference runtime dispatches the convs separately
  * (lowering.rs:122-152); this fusion has no counterpart there and keeps each

@@ -429,7 +429,7 @@ def test_dwpw_plan_covers_the_output_and_fits_lds(shape):
 
 def test_dwpw_rejects_what_it_cannot_run():
     base = dict(ih=16, iw=16, c=32, cout=32)
-    for kw, msg in [(dict(dt=conv.DType.F16), "fp32"), (dict(k=5), "3x3"), (dict(cout=80), "cout"),
+    for kw, msg in [(dict(k=5), "3x3"), (dict(cout=80), "cout"),
                     (dict(s=3), "stride"), (dict(pad=(3, 1, 1, 1)), "padding"), (dict(kg_pad=4), "kg_pad"),
                     (dict(tile=(4, 48)), "forced tile"), (dict(tile=(6, 16)), "forced tile"),
                     (dict(rows=3), "forced tile")]:
@@ -439,6 +439,12 @@ def test_dwpw_rejects_what_it_cannot_run():
     d = conv.DwPwSpec(residual=True, **base).desc()
     assert conv.lib().aih_conv_dwpw(C.byref(d), 16, 16, 16, 16, 16, None, 16, None) == -1
     assert "res must be given" in conv.last_error()
+    # 16-bit storage plans like fp32 (the same tiles and LDS bytes), with
+    # 32-channel chunks
+    for dt in (conv.DType.F16, conv.DType.BF16):
+        p16, p32 = conv.DwPwSpec(dt=dt, **base).plan(), conv.DwPwSpec(**base).plan()
+        assert (p16.th, p16.tw, p16.lds_bytes) == (p32.th, p32.tw, p32.lds_bytes)
+        assert p16.chunks == 1 and p32.chunks == 2
 
 
 def test_noalloc_rejects_workspace_beyond_scratch_on_the_host():

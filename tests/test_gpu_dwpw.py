@@ -6,7 +6,10 @@ storage, max relative error <= 1e-4 (the reference's metric,
 crates/ai-cpu/tests/synthetic_e2e.rs:113-116). Cases cover both strides,
 channel counts with a partial last 16-channel chunk, every output block
 count, widths and heights that leave partial tiles, asymmetric padding,
-batches, every forced tile shape and the non-clamp activations."""
+batches, every forced tile shape and the non-clamp activations. 16-bit
+storage (f16, bf16): the same cases against the oracle's two ops with the
+same storage rounding (inputs, weights, the depthwise output and the result
+rounded to the dtype, fp32 arithmetic) within 2e-3 f16 / 8e-3 bf16."""
 import numpy as np
 import pytest
 
@@ -27,8 +30,8 @@ class DwPwCase:
     """Seeded depthwise + pointwise pair: the oracle's separate ops on the
     host and the packed device buffers in the unfused ops' layouts."""
 
-    def __init__(self, n, ih, iw, c, cout, s, pad, residual, act_d, act_p, seed):
-        self.n, self.ih, self.iw, self.c, self.cout, self.s = n, ih, iw, c, cout, s
+    def __init__(self, n, ih, iw, c, cout, s, pad, residual, act_d, act_p, seed, dt=0):
+        self.n, self.ih, self.iw, self.c, self.cout, self.s, self.dt = n, ih, iw, c, cout, s, dt
         self.pad, self.residual, self.act_d, self.act_p = tuple(pad), residual, act_d, act_p
         op_d = orc.conv2d(c, c, k=3, s=s, pad=list(pad), groups=c, act=act_d)
         op_p = orc.conv2d(c, cout, act=act_p)
@@ -39,23 +42,27 @@ class DwPwCase:
         wp = orc.gauss_fill(seed + 3, 0.0, float(np.sqrt(2.0 / c)), cout * c)
         bp = orc.gauss_fill(seed + 4, 0.0, 0.01, cout)
         r = orc.xs32_fill(seed + 5, n * self.oh * self.ow * cout) if residual else None
-        d = orc.CpuConv(op_d, ih, iw, wd, bd).run(x, n, threads=8)
-        self.want = orc.CpuConv(op_p, self.oh, self.ow, wp, bp, has_res=residual).run(d, n, r, threads=8)
-        wpp, self.kgp = orc.pack_weights_conv(wp, cout, c, 1, 1, 4, 0)
-        self.bufs = (dev(orc.pack_nhwc(x, n, ih, iw, c, 0)), dev(orc.pack_weights_dw(wd, c, 3, 3, 0)),
-                     dev(orc.pack_bias(bd, c, 0)), dev(wpp), dev(orc.pack_bias(bp, cout, 0)),
-                     dev(orc.pack_nhwc(r, n, self.oh, self.ow, cout, 0)) if residual else None)
+        # 16-bit: the oracle on the stored values, its depthwise output and
+        # result rounded where the unfused ops store them
+        rd = (lambda v: v) if dt == 0 else (lambda v: orc.round_to(v, dt))
+        d = rd(orc.CpuConv(op_d, ih, iw, rd(wd), rd(bd)).run(rd(x), n, threads=8))
+        self.want = rd(orc.CpuConv(op_p, self.oh, self.ow, rd(wp), rd(bp), has_res=residual).run(
+            d, n, rd(r) if residual else None, threads=8))
+        wpp, self.kgp = orc.pack_weights_conv(wp, cout, c, 1, 1, 4, dt)
+        self.bufs = (dev(orc.pack_nhwc(x, n, ih, iw, c, dt)), dev(orc.pack_weights_dw(wd, c, 3, 3, dt)),
+                     dev(orc.pack_bias(bd, c, dt)), dev(wpp), dev(orc.pack_bias(bp, cout, dt)),
+                     dev(orc.pack_nhwc(r, n, self.oh, self.ow, cout, dt)) if residual else None)
 
     def spec(self, **kw):
         return conv.DwPwSpec(ih=self.ih, iw=self.iw, c=self.c, cout=self.cout, s=self.s, pad=self.pad,
                              act_dw=ACT[self.act_d], act_pw=ACT[self.act_p], residual=self.residual, n=self.n,
-                             kg_pad=self.kgp, **kw)
+                             kg_pad=self.kgp, dt=conv.DType(self.dt), **kw)
 
     def run(self, spec) -> np.ndarray:
-        yd = poisoned(self.n * self.oh * self.ow * (-(-self.cout // 4)) * 4, 0)
+        yd = poisoned(self.n * self.oh * self.ow * (-(-self.cout // 4)) * 4, self.dt)
         spec.run(*self.bufs, yd)
         torch.cuda.synchronize()
-        return orc.unpack_nhwc(host(yd, 0), self.n, self.oh, self.ow, self.cout, 0)
+        return orc.unpack_nhwc(host(yd, self.dt), self.n, self.oh, self.ow, self.cout, self.dt)
 
 
 CASES = [
@@ -158,3 +165,17 @@ def test_dwpw_benched_routes_b64(case):
         want = orc.CpuConv(op_p, oh, ow, wp, bp, has_res=res).run(d, 1, ri, threads=8)
         worst = max(worst, rel_err(got[i], want.reshape(-1)))
     assert worst <= TOL, (p, worst)
+
+
+@pytest.mark.parametrize("dt", [1, 2], ids=["f16", "bf16"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(str(v) for v in c[:6]) + f"_{c[8]}_{c[9]}")
+def test_dwpw_16bit_matches_two_ops_with_storage_rounding(case, dt):
+    n, ih, iw, c, cout, s, pad, res, act_d, act_p = case
+    cs = DwPwCase(n, ih, iw, c, cout, s, pad, res, act_d, act_p, 7700 + c + cout, dt=dt)
+    spec = cs.spec()
+    if not spec.fusable():
+        pytest.skip(f"not fusable: {conv.last_error()}")
+    got = cs.run(spec)
+    err = rel_err(got, cs.want)
+    print(f"dwpw dt{dt} {case}: plan {spec.plan()}, max_rel_err {err:.3e}", flush=True)
+    assert err <= (2e-3 if dt == 1 else 8e-3), err
