@@ -114,7 +114,7 @@ __device__ __forceinline__ void irw_wave_order() {
 //   (0, 1) (3, 4) (6+1, 6+2) along a row    wa1 + 64 ta          bc[dy] (+ one pixel for (7, 8))
 //   (2, 5) down a column                    wa3 + 64 * 2         br + two pixels
 //   (6, zero run)                           wa3 + 64 * 6         bc[2] (partner lanes read tap 7, times 0)
-// wa1 / wa3: the lane's 8-channel half, + one / three taps for q >= 2;
+// wa1 / wa3: the word of the lane's row channel, + one / three taps for q >= 2;
 // bc[dy] = pixel row + dy rows (+ one pixel for q >= 2); br = pixel row (+ one
 // row for q >= 2). Every read stays inside the tile's halo rows. (Reads of the
 // expanded chunk: plane 2 cg + q % 2, 16 bytes at the halo pixel.)
@@ -129,10 +129,13 @@ __device__ __forceinline__ f32x4 ir_mma16(u32x4 a, u32x4 b, f32x4 c) {
                                                    0, 0, 0);
 }
 
-// Lane constants of the depthwise MFMAs.
+// Lane constants of the depthwise MFMAs. The A operand of lane (row c, slice
+// q) is zero but for w[t][c] in its own element: the lane reads just the
+// 32-bit word holding channel c's weight (and its neighbour's) and masks it
+// into the dword of its element.
 struct IrDwLane {
-  u32x4 mask;         // the lane's diagonal element in its 16 weight bytes (0xffff in its half), or zero
-  uint32_t wa1, wa3;  // tap-weight byte offsets in a slot: the 8-channel half, + 1 / 3 taps for q >= 2
+  u32x4 mask;         // the lane's diagonal element (0xffff in its half of its dword), or zero
+  uint32_t wa1, wa3;  // tap-weight word offsets in a slot: channel c's word, + 1 / 3 taps for q >= 2
 };
 
 __device__ __forceinline__ IrDwLane irdw_lane(int lane) {
@@ -141,8 +144,8 @@ __device__ __forceinline__ IrDwLane irdw_lane(int lane) {
   const uint32_t hm = (l16 >> 3) == qh ? ((e & 1) ? 0xffff0000u : 0x0000ffffu) : 0u;
   IrDwLane L;
   L.mask = u32x4{j == 0 ? hm : 0u, j == 1 ? hm : 0u, j == 2 ? hm : 0u, j == 3 ? hm : 0u};
-  L.wa1 = qh * 16 + qt * 64;
-  L.wa3 = qh * 16 + qt * 192;
+  L.wa1 = (l16 & ~1u) * 2 + qt * 64;
+  L.wa3 = (l16 & ~1u) * 2 + qt * 192;
   return L;
 }
 
@@ -179,10 +182,11 @@ __device__ __forceinline__ void irdw_chunk(const char *xe, const char *sm, const
   auto boff = [&](int P, int pg) -> uint32_t {
     return P == 0 ? bc[pg][0] : P == 1 ? bc[pg][1] : P == 2 ? bc[pg][2] + 16 : P == 3 ? br[pg] + 32 : bc[pg][2];
   };
-  u32x4 A[2], B[2][2];
+  uint32_t A[2];
+  u32x4 B[2][2];
   auto load = [&](int s, int slot) {
     const int cg = s / 5, P = s % 5;
-    A[slot] = *reinterpret_cast<const u32x4 *>(sm + aoff(P) + 32 * cg);
+    A[slot] = *reinterpret_cast<const uint32_t *>(sm + aoff(P) + 32 * cg);
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg)
       B[slot][pg] = *reinterpret_cast<const u32x4 *>(xe + boff(P, pg) + 2 * cg * PLANE);
@@ -196,7 +200,7 @@ __device__ __forceinline__ void irdw_chunk(const char *xe, const char *sm, const
     if (P == 0)  // bias of rows 4q..4q+3: the first MFMA's accumulator
       bias = unpack4<DT>(*reinterpret_cast<const u32x2 *>(sm + IRW_BD + (16 * cg + 4 * q) * 2));
     if (s + 1 < 10) load(s + 1, cur ^ 1);
-    const u32x4 Am = A[cur] & L.mask;
+    const u32x4 Am = u32x4{A[cur], A[cur], A[cur], A[cur]} & L.mask;
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg) d[pg] = ir_mma16<DT>(Am, B[cur][pg], P == 0 ? bias : d[pg]);
     if (P == 4) {
