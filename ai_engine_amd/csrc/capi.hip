@@ -471,6 +471,7 @@ int stem_args(const aih_igemm_desc *d, uint32_t oh, uint32_t ow, aih::StemArgs *
   sa->has_res = d->residual ? 1 : 0;
   sa->fd_ohw = aih::make_fastdiv(oh * ow);
   sa->fd_ow = aih::make_fastdiv(ow);
+  sa->nxcd = aih::device_xcds();
   return AIH_OK;
 }
 

@@ -23,6 +23,7 @@ struct StemArgs {
   uint32_t cin_f32;  // 0: x is NHWC-C4 in the dtype; 1..3: x is logical NHWC fp32 with
                      // that many channels per pixel, rounded to the dtype as it is read
   uint32_t x_bytes;  // bytes of x when cin_f32 != 0 (< 2 GiB)
+  uint32_t nxcd;     // XCDs of the device (workgroup remap)
 };
 
 // grid_out non-null: only the launch's workgroup count is computed (plans).
