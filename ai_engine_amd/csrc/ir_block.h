@@ -63,7 +63,14 @@ hipError_t launch_ir_block(const IrArgs &a, int dt, uint32_t lds, uint32_t grid,
 
 // ---- the one-tile-per-wavefront kernel (ir_wave_impl.h) ----
 
-constexpr int IRW_THREADS = 512;              // the most threads a workgroup has (8 wavefronts)
+constexpr int IRW_THREADS = 512;              // the most threads a split-kernel workgroup has (8 wavefronts)
+// The most wavefronts a wave-kernel workgroup of a shape (KE = C / 16, NPI
+// halo blocks, NOB = COP / 32) has: 12 -- three per SIMD, one workgroup a
+// CU sharing one resident copy of the weights -- where the shape's registers
+// fit 168 VGPRs (the stride-1 tiles of 48- and 64-channel blocks), else 8.
+__host__ __device__ constexpr uint32_t irw_max_waves(uint32_t ke, uint32_t npi, uint32_t nob) {
+  return npi == 2 && nob == 2 && (ke == 3 || ke == 4) ? 12u : 8u;
+}
 // A wavefront's expanded chunk in LDS: four planes of 8 channels (16 bytes a
 // halo pixel), plane h holding channels 8h .. 8h + 7 of every halo pixel in
 // turn -- 64 bytes a pixel. (The depthwise reads 16-pixel groups of one
@@ -116,7 +123,7 @@ struct IrWavePlan {
   uint32_t split;
   uint32_t deep;                        // split kernel: operands prefetched a whole chunk ahead
   uint32_t TH, TW, HH, HW, NPI, resident;
-  uint32_t waves;                       // wavefronts per workgroup (wave: 2, 4 or 8; split: 1, 2, 4 or 8)
+  uint32_t waves;                       // wavefronts per workgroup (wave: 2, 4, 8 or 12; split: 1, 2, 4 or 8)
   uint32_t tiles_y, tiles_x, ntiles;
   uint32_t lds_w, lds_bp, lds_xe, lds_red, lds_x, lds;  // LDS byte offsets and total
   uint32_t occ, grid;                   // workgroups per CU, launched workgroups

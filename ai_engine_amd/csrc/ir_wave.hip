@@ -71,8 +71,9 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
     return "not a wave-family kernel";
   if (kernel == AIH_IR_KERNEL_SPLIT && weights != AIH_IR_WEIGHTS_AUTO)
     return "the split kernel reads its weights from memory (no placement to choose)";
-  if (waves_force && waves_force != 1 && waves_force != 2 && waves_force != 4 && waves_force != 8)
-    return "wavefronts per workgroup must be 1, 2, 4 or 8";
+  if (waves_force && waves_force != 1 && waves_force != 2 && waves_force != 4 && waves_force != 8 &&
+      waves_force != 12)
+    return "wavefronts per workgroup must be 1, 2, 4, 8 or 12 (12: the wave kernel, where its shape allows)";
   const uint32_t ke = C / 16, COP = ir_cop(CO), nob = COP / 32;
   const bool any_wave = irw_has_shape(ke, 2, nob) || irw_has_shape(ke, 5, nob);
   const bool any_split = irs_has_shape(ke, 2, nob) || irs_has_shape(ke, 5, nob);
@@ -135,9 +136,10 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
     if (kernel != AIH_IR_KERNEL_SPLIT && npi_w) {
       const uint32_t npi = npi_w;
       const double chunk = chunk_cost(npi);
-      for (uint32_t waves : {8u, 4u, 2u})
+      for (uint32_t waves : {12u, 8u, 4u, 2u})
         for (uint32_t resident = 0; resident < 2; ++resident) {
           if (waves_force && waves != waves_force) continue;
+          if (waves > irw_max_waves(ke, npi, nob)) continue;
           if ((weights == AIH_IR_WEIGHTS_RESIDENT && !resident) || (weights == AIH_IR_WEIGHTS_STREAMED && resident))
             continue;
           IrWavePlan p{};
@@ -244,7 +246,9 @@ hipError_t launch_ir_wave(const IrWaveArgs &a, int dt, const IrWavePlan &p, hipS
       default: return hipErrorInvalidValue;
     }
   }
-  if (p.waves != 2 && p.waves != 4 && p.waves != 8) return hipErrorInvalidValue;
+  if ((p.waves != 2 && p.waves != 4 && p.waves != 8 && p.waves != 12) ||
+      p.waves > irw_max_waves(a.C / 16, p.NPI, a.COP / 32))
+    return hipErrorInvalidValue;
   switch (dt) {
     case DT_F16: return launch_ir_wave_f16(a, p.NPI, p.waves, p.lds, p.grid, st);
     case DT_BF16: return launch_ir_wave_bf16(a, p.NPI, p.waves, p.lds, p.grid, st);

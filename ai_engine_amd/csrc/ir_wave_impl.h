@@ -249,13 +249,15 @@ __device__ __forceinline__ void irdw_store(const IrWaveArgs &a, const float *BpL
 // projection blocks of 32 output channels; RL: the expand and depthwise
 // activations are both ReLU (applied to the packed 16-bit results).
 // Wavefronts per SIMD the register allocation aims for: four on the
-// narrowest shape (its operands fit 128 VGPRs), else what the shape needs.
+// narrowest shape (its operands fit 128 VGPRs), three where a workgroup may
+// have 12 wavefronts (168 VGPRs), else what the shape needs.
 __host__ __device__ constexpr int irw_waves_per_simd(int ke, int npi, int nob) {
-  return ke == 2 && npi == 2 && nob == 1 ? 4 : 1;
+  return ke == 2 && npi == 2 && nob == 1 ? 4 : irw_max_waves(ke, npi, nob) == 12 ? 3 : 1;
 }
 
 template <int DT, int KE, int NPI, int NOB, bool RL>
-__global__ __launch_bounds__(IRW_THREADS) __attribute__((amdgpu_waves_per_eu(irw_waves_per_simd(KE, NPI, NOB))))
+__global__ __launch_bounds__(64 * irw_max_waves(KE, NPI, NOB))
+__attribute__((amdgpu_waves_per_eu(irw_waves_per_simd(KE, NPI, NOB))))
 void ir_wave_kernel(IrWaveArgs a) {
   static_assert(DT == DT_F16 || DT == DT_BF16, "16-bit storage");
   extern __shared__ __align__(16) char lds[];
@@ -267,7 +269,7 @@ void ir_wave_kernel(IrWaveArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, l32 = lane & 31, lh = lane >> 5, l16 = lane & 15, q = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // wavefronts of this workgroup (2, 4 or 8, chosen by the plan)
+  // wavefronts of this workgroup (2, 4, 8 or 12, chosen by the plan)
   const uint32_t nthr = blockDim.x, nwaves = nthr >> 6;
 
   const uint32_t WPG = EC * a.CO * ES;         // project weights of one chunk in memory

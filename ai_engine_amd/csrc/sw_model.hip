@@ -601,8 +601,10 @@ void tune_blocks(aih_model *m) {
     };
     cands.push_back(f.d);
     for (const auto &t : kTuneWaveTiles) {
-      add(AIH_IR_KERNEL_WAVE, t, AIH_IR_WEIGHTS_RESIDENT, 0);
-      add(AIH_IR_KERNEL_WAVE, t, AIH_IR_WEIGHTS_STREAMED, 0);
+      for (uint32_t w : {0u, 12u}) {  // the plan's wavefronts per workgroup, and 12 where the shape allows
+        add(AIH_IR_KERNEL_WAVE, t, AIH_IR_WEIGHTS_RESIDENT, w);
+        add(AIH_IR_KERNEL_WAVE, t, AIH_IR_WEIGHTS_STREAMED, w);
+      }
       for (uint32_t w : {2u, 4u, 8u}) add(AIH_IR_KERNEL_SPLIT, t, AIH_IR_WEIGHTS_AUTO, w);
     }
     for (const auto &t : kTuneTileTiles) {
@@ -615,17 +617,15 @@ void tune_blocks(aih_model *m) {
       aih_ir_plan plan;
       if (aih_ir_block_plan(&d, &plan) != AIH_OK) continue;  // a forced option this block cannot run
       const std::array<uint32_t, 5> key{plan.kernel, plan.th, plan.tw, plan.resident,
-                                        plan.kernel == AIH_IR_KERNEL_SPLIT ? plan.waves : 0u};
+                                        plan.kernel == AIH_IR_KERNEL_TILE ? 0u : plan.waves};
       if (!seen.insert(key).second) continue;
       // the plan's choice, made explicit, so later calls run exactly it
       aih_ir_block_desc dd = d;
       dd.tile_h = plan.th;
       dd.tile_w = plan.tw;
       dd.kernel = (int32_t)plan.kernel;
-      if (plan.kernel != AIH_IR_KERNEL_SPLIT)
-        dd.weights = plan.resident ? AIH_IR_WEIGHTS_RESIDENT : AIH_IR_WEIGHTS_STREAMED;
-      else
-        dd.waves = plan.waves;
+      if (plan.kernel != AIH_IR_KERNEL_SPLIT) dd.weights = plan.resident ? AIH_IR_WEIGHTS_RESIDENT : AIH_IR_WEIGHTS_STREAMED;
+      if (plan.kernel != AIH_IR_KERNEL_TILE) dd.waves = plan.waves;
       for (int w = 0; w < 2; ++w)
         if (aih_ir_block(&dd, x, we, be, wd, bd, wp, bp, res, y, st) != AIH_OK)
           throw std::runtime_error(std::string("tune: ") + aih_last_error());

@@ -115,6 +115,7 @@ class Model:
                   (8, 32), (16, 16)]
     WAVE_TILES = [(4, 8), (8, 4), (5, 6), (6, 5), (2, 16), (16, 2), (3, 10)]
     SPLIT_WAVES = [2, 4, 8]
+    WAVE_WIDE = 12  # wave-kernel workgroups of 12 wavefronts (the shapes that allow them)
 
     def __init__(self, layers: list[Layer], weights: Weights, n: int, ih: int, iw: int, cin: int,
                  dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0",
@@ -222,21 +223,23 @@ class Model:
         """The fused launches the tuner times for a block: on the tile kernel
         the planner's tile and every TUNE_TILES entry, on the wave kernel the
         planner's tile and every WAVE_TILES entry, each with resident and
-        streamed weights (the ones that fit), on the split kernel the planner's
+        streamed weights (the ones that fit) and with the planner's or
+        WAVE_WIDE wavefronts per workgroup, on the split kernel the planner's
         tile and every WAVE_TILES entry with each of SPLIT_WAVES wavefronts,
         as (label, spec with kernel, tile, placement and wavefronts forced);
         duplicates dropped."""
         out, seen = [], set()
         K, Wt = conv.IrKernel, conv.IrWeights
         opts = [(K.TILE, t, w, 0) for t in [(0, 0)] + cls.TUNE_TILES for w in (Wt.RESIDENT, Wt.STREAMED)]
-        opts += [(K.WAVE, t, w, 0) for t in [(0, 0)] + cls.WAVE_TILES for w in (Wt.RESIDENT, Wt.STREAMED)]
+        opts += [(K.WAVE, t, w, n) for t in [(0, 0)] + cls.WAVE_TILES for w in (Wt.RESIDENT, Wt.STREAMED)
+                 for n in (0, cls.WAVE_WIDE)]
         opts += [(K.SPLIT, t, Wt.AUTO, n) for t in [(0, 0)] + cls.WAVE_TILES for n in cls.SPLIT_WAVES]
         for kernel, tile, w, waves in opts:
             sp = dataclasses.replace(spec, tile=tile, weights=w, kernel=kernel, waves=waves)
             if not sp.fusable():
                 continue
             pl = sp.plan()
-            key = (int(kernel), pl.th, pl.tw, pl.resident, pl.waves if kernel == K.SPLIT else 0)
+            key = (int(kernel), pl.th, pl.tw, pl.resident, pl.waves if kernel in (K.SPLIT, K.WAVE) else 0)
             if key in seen:
                 continue
             seen.add(key)
@@ -249,14 +252,16 @@ class Model:
         k = conv.IrKernel(kernel)
         if k == conv.IrKernel.SPLIT:
             return f"split {th}x{tw} w{waves}"
-        name = "wave" if k == conv.IrKernel.WAVE else "fused"
-        return f"{name} {th}x{tw}{' resident' if resident else ''}"
+        if k == conv.IrKernel.WAVE:
+            return f"wave {th}x{tw}{' resident' if resident else ''} w{waves}"
+        return f"fused {th}x{tw}{' resident' if resident else ''}"
 
     @staticmethod
     def parse_label(label: str):
-        """"unfused" -> None; "fused|wave THxTW[ resident]" or "split THxTW wN"
-        -> (IrKernel, (th, tw), IrWeights, wavefronts or 0); "dwpw THxTW" ->
-        ("dwpw", (th, tw), None, rows per wavefront)."""
+        """"unfused" -> None; "fused THxTW[ resident]", "wave THxTW[ resident][ wN]"
+        or "split THxTW wN" -> (IrKernel, (th, tw), IrWeights, wavefronts or 0
+        for the plan's choice); "dwpw THxTW rN" -> ("dwpw", (th, tw), None,
+        rows per wavefront)."""
         if label == "unfused":
             return None
         m = re.fullmatch(r"dwpw (\d+)x(\d+) r([24])", label)
@@ -265,12 +270,15 @@ class Model:
         m = re.fullmatch(r"split (\d+)x(\d+) w(\d+)", label)
         if m:
             return conv.IrKernel.SPLIT, (int(m.group(1)), int(m.group(2))), conv.IrWeights.AUTO, int(m.group(3))
-        m = re.fullmatch(r"(fused|wave) (\d+)x(\d+)( resident)?", label)
+        m = re.fullmatch(r"wave (\d+)x(\d+)( resident)?(?: w(\d+))?", label)
+        if m:
+            w = conv.IrWeights.RESIDENT if m.group(3) else conv.IrWeights.STREAMED
+            return conv.IrKernel.WAVE, (int(m.group(1)), int(m.group(2))), w, int(m.group(4) or 0)
+        m = re.fullmatch(r"fused (\d+)x(\d+)( resident)?", label)
         if not m:
             raise ValueError(f"unknown block choice {label!r}")
-        k = conv.IrKernel.WAVE if m.group(1) == "wave" else conv.IrKernel.TILE
-        w = conv.IrWeights.RESIDENT if m.group(4) else conv.IrWeights.STREAMED
-        return k, (int(m.group(2)), int(m.group(3))), w, 0
+        w = conv.IrWeights.RESIDENT if m.group(3) else conv.IrWeights.STREAMED
+        return conv.IrKernel.TILE, (int(m.group(1)), int(m.group(2))), w, 0
 
     def choice_map(self) -> dict[str, str]:
         """Block -> the label of the launch it runs (feed back as choices=)."""
@@ -296,7 +304,10 @@ class Model:
             return [self._conv_op(e, packed, L), self._dwpw_op(d, p, sp, packed, L)]
         sp = dataclasses.replace(spec, tile=tile, weights=w, kernel=kernel, waves=waves)
         pl = sp.plan()
-        if self.label_of(pl.kernel, pl.th, pl.tw, pl.resident, pl.waves) != label:
+        planned = self.label_of(pl.kernel, pl.th, pl.tw, pl.resident, pl.waves)
+        if kernel == conv.IrKernel.WAVE and not waves:
+            planned = planned.rsplit(" w", 1)[0]  # a label without a count takes the plan's
+        if planned != label:
             raise conv.AihError(f"{self._block_name(p)}: {label!r} planned as "
                                 f"{self.label_of(pl.kernel, pl.th, pl.tw, pl.resident, pl.waves)!r}")
         return [self._fused_op((e, d, p, sp), packed, L)]

@@ -184,7 +184,10 @@ typedef struct {
   uint32_t ec;             /* expanded channels per chunk; 0 = chosen by the plan */
   int32_t weights;         /* enum aih_ir_weights: where the expand / project weights live */
   int32_t kernel;          /* enum aih_ir_kernel */
-  uint32_t waves;          /* wavefronts per workgroup of the wave / split kernel; 0 = chosen by the plan */
+  uint32_t waves;          /* wavefronts per workgroup; 0 = chosen by the plan. The split kernel takes
+                              1, 2, 4 or 8; the wave kernel 2, 4, 8, or 12 for the stride-1 tiles of
+                              48- and 64-channel blocks (three wavefronts per SIMD sharing one copy
+                              of the weights) */
 } aih_ir_block_desc;
 
 /* Which fused kernel runs a block: chosen by the plan (the cheaper estimate
