@@ -15,7 +15,8 @@ struct PwNarrowArgs {
   int32_t act, has_res;
 };
 
-// Largest K (in kg) the kernel stages in LDS.
+// Largest K (in kg) the narrow route takes (one group of G lanes sums a
+// pixel's whole K).
 constexpr uint32_t kPwNarrowMaxKG = 2048;
 
 // Lanes per pixel for kg input channel groups: 16, 4 or 1.

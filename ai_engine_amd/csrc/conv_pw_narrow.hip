@@ -4,8 +4,10 @@
 // here a group of G lanes owns one pixel: lane g reads input channel
 // groups g, g + G, ... (so the group's loads cover the pixel's
 // contiguous channels, one coalesced run per step), does the 4 dot products
-// on the VALU against weights staged in LDS, and the group adds its partial
-// sums by butterfly shuffles (a fixed order). It is HBM-bound: (K + 4 (+4
+// on the VALU against its weight vectors (read straight from memory, where
+// every workgroup finds them in the caches: no LDS staging, no barrier, so
+// the activation and weight loads are in flight together), and the group
+// adds its partial sums by butterfly shuffles (a fixed order). It is HBM-bound: (K + 4 (+4
 // res)) * storage bytes per pixel. The role of the reference's Gemv variant
 // (gemm_pw.rs:91-102) and ai-cpu's pw_dot
 // (crates/ai-cpu/src/kernels/pw_dot.rs:32-61); the epilogue order is
@@ -31,10 +33,8 @@ __device__ __forceinline__ f32x4 ld_w4(const void *w, size_t vi) {
 // half full), 1 below.
 template <int DTA, int DTW, int G>
 __global__ __launch_bounds__(256) void pw_narrow_kernel(PwNarrowArgs a) {
-  extern __shared__ f32x4 wl[];  // [KG][4]: input channels 4kg..4kg+3 of output channel j
-  // packed weights with one column group (NG = 1): vector (kg, j) at kg * 4 + j (pack.rs:95)
-  for (uint32_t i = threadIdx.x; i < a.KG * 4; i += 256) wl[i] = ld_w4<DTA, DTW>(a.w, i);
-  __syncthreads();
+  // packed weights with one column group (NG = 1): vector (kg, j) -- input
+  // channels 4kg..4kg+3 of output channel j -- at kg * 4 + j (pack.rs:95)
   const f32x4 bias = Vec4IO<DTA>::load(a.bias, 0);
   const Act ap = act_params(a.act);
   const uint32_t g = threadIdx.x % G;
@@ -44,13 +44,15 @@ __global__ __launch_bounds__(256) void pw_narrow_kernel(PwNarrowArgs a) {
     const bool pv = m < a.M;
     f32x4 acc = {};
     const size_t xrow = (size_t)(pv ? m : 0) * a.KGX;
+#pragma unroll 2
     for (uint32_t kg = g; kg < a.KG; kg += G) {
-      const f32x4 xv = pv ? Vec4IO<DTA>::load(a.x, xrow + kg) : f32x4{};
+      const f32x4 xl = Vec4IO<DTA>::load(a.x, xrow + kg);
+      const f32x4 xv = pv ? xl : f32x4{};
+      f32x4 wv[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 wv = wl[kg * 4 + j];
-        acc[j] += xv.x * wv.x + xv.y * wv.y + xv.z * wv.z + xv.w * wv.w;
-      }
+      for (int j = 0; j < 4; ++j) wv[j] = ld_w4<DTA, DTW>(a.w, (size_t)kg * 4 + j);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] += xv.x * wv[j].x + xv.y * wv[j].y + xv.z * wv[j].z + xv.w * wv[j].w;
     }
     // the group's partial sums, added by butterfly (every lane ends with the total)
 #pragma unroll
@@ -71,7 +73,7 @@ template <int DTA, int DTW, int G>
 hipError_t launch_g(const PwNarrowArgs &a, hipStream_t st) {
   const uint32_t per_block = 256 / G;
   const uint32_t blocks = (uint32_t)std::min<uint64_t>((a.M + per_block - 1) / per_block, 65535);
-  hipLaunchKernelGGL((pw_narrow_kernel<DTA, DTW, G>), dim3(blocks), dim3(256), a.KG * 4 * sizeof(f32x4), st, a);
+  hipLaunchKernelGGL((pw_narrow_kernel<DTA, DTW, G>), dim3(blocks), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -601,7 +601,7 @@ void tune_blocks(aih_model *m) {
     };
     cands.push_back(f.d);
     for (const auto &t : kTuneWaveTiles) {
-      for (uint32_t w : {0u, 12u}) {  // the plan's wavefronts per workgroup, and 12 where the shape allows
+      for (uint32_t w : {0u, 4u, 8u, 12u}) {  // the plan's wavefronts per workgroup, then forced (12 where allowed)
         add(AIH_IR_KERNEL_WAVE, t, AIH_IR_WEIGHTS_RESIDENT, w);
         add(AIH_IR_KERNEL_WAVE, t, AIH_IR_WEIGHTS_STREAMED, w);
       }

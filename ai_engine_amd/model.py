@@ -115,7 +115,7 @@ class Model:
                   (8, 32), (16, 16)]
     WAVE_TILES = [(4, 8), (8, 4), (5, 6), (6, 5), (2, 16), (16, 2), (3, 10)]
     SPLIT_WAVES = [2, 4, 8]
-    WAVE_WIDE = 12  # wave-kernel workgroups of 12 wavefronts (the shapes that allow them)
+    WAVE_WAVES = [4, 8, 12]  # wave-kernel workgroup sizes (12: the shapes that allow it)
 
     def __init__(self, layers: list[Layer], weights: Weights, n: int, ih: int, iw: int, cin: int,
                  dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0",
@@ -223,8 +223,8 @@ class Model:
         """The fused launches the tuner times for a block: on the tile kernel
         the planner's tile and every TUNE_TILES entry, on the wave kernel the
         planner's tile and every WAVE_TILES entry, each with resident and
-        streamed weights (the ones that fit) and with the planner's or
-        WAVE_WIDE wavefronts per workgroup, on the split kernel the planner's
+        streamed weights (the ones that fit) and with the planner's or each
+        of WAVE_WAVES wavefronts per workgroup, on the split kernel the planner's
         tile and every WAVE_TILES entry with each of SPLIT_WAVES wavefronts,
         as (label, spec with kernel, tile, placement and wavefronts forced);
         duplicates dropped."""
@@ -232,7 +232,7 @@ class Model:
         K, Wt = conv.IrKernel, conv.IrWeights
         opts = [(K.TILE, t, w, 0) for t in [(0, 0)] + cls.TUNE_TILES for w in (Wt.RESIDENT, Wt.STREAMED)]
         opts += [(K.WAVE, t, w, n) for t in [(0, 0)] + cls.WAVE_TILES for w in (Wt.RESIDENT, Wt.STREAMED)
-                 for n in (0, cls.WAVE_WIDE)]
+                 for n in [0] + cls.WAVE_WAVES]
         opts += [(K.SPLIT, t, Wt.AUTO, n) for t in [(0, 0)] + cls.WAVE_TILES for n in cls.SPLIT_WAVES]
         for kernel, tile, w, waves in opts:
             sp = dataclasses.replace(spec, tile=tile, weights=w, kernel=kernel, waves=waves)

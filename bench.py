@@ -110,6 +110,21 @@ def main() -> int:
         model.upload_input(x)
         model.infer()
 
+    # per-step distribution first (untimed for the headline): max(100, K)
+    # steps, each bracketed by HIP events
+    NS = max(100, args.steps)
+    sev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(NS)]
+    for a, b in sev:
+        a.record(stream)
+        step()
+        b.record(stream)
+    torch.cuda.synchronize()
+    st = sorted(a.elapsed_time(b) for a, b in sev)
+    step_stats = {"steps": NS, "min_ms": round(st[0], 4), "median_ms": round(st[NS // 2], 4),
+                  "max_ms": round(st[-1], 4), "frames_per_s_at_median": round(n / (st[NS // 2] / 1e3), 1)}
+    log(f"per-step (events, {NS} steps): min {st[0]:.3f} median {st[NS // 2]:.3f} max {st[-1]:.3f} ms")
+    # the headline: W warm-up steps, then exactly K steps between a
+    # synchronize on either side
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -125,18 +140,6 @@ def main() -> int:
     ms_per_step = wall * 1e3 / args.steps
     fps = n / (ms_per_step / 1e3)
     log(f"encoder {args.dtype} b{n}: {ms_per_step:.3f} ms/step wall, {gpu_ms:.3f} ms/step gpu, {fps:.0f} frames/s")
-    # per-step distribution: max(100, K) steps, each bracketed by HIP events
-    NS = max(100, args.steps)
-    sev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(NS)]
-    for a, b in sev:
-        a.record(stream)
-        step()
-        b.record(stream)
-    torch.cuda.synchronize()
-    st = sorted(a.elapsed_time(b) for a, b in sev)
-    step_stats = {"steps": NS, "min_ms": round(st[0], 4), "median_ms": round(st[NS // 2], 4),
-                  "max_ms": round(st[-1], 4), "frames_per_s_at_median": round(n / (st[NS // 2] / 1e3), 1)}
-    log(f"per-step (events, {NS} steps): min {st[0]:.3f} median {st[NS // 2]:.3f} max {st[-1]:.3f} ms")
 
     # per-op timing, grouped by kernel instantiation: R passes over the step,
     # HIP events on the launch stream around every launch (each median over
@@ -610,9 +613,29 @@ def encoder_native(torch, W, layers, wts, x, n, H, Wd, dt, stream, headline_fps)
 
     t_up = timed(lambda: m.upload_input("input", x, stream))
     m.upload_input("input", x, stream)
+    timed(lambda: m.infer(stream), 100)  # untimed: the steady state first, as for the headline
     t = timed(lambda: m.infer(stream))
+    # per launch: op ranges (a fused block's ops together), HIP events around
+    # each, median of 5 passes
+    fb = {f.first_op: f.n_ops for f in m.fused_blocks()}
+    ranges, i = [], 0
+    while i < m.info.n_ops:
+        ranges.append((i, i + fb.get(i, 1)))
+        i += fb.get(i, 1)
+    R = 5
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in ranges]
+           for _ in range(R)]
+    for r in range(R):
+        for (a, b), (e0, e1) in zip(ranges, evs[r]):
+            e0.record(stream)
+            m.infer_range(a, b, stream)
+            e1.record(stream)
+    torch.cuda.synchronize()
+    per_launch = [dict(ops=f"{a}-{b - 1}", us=round(sorted(evs[r][j][0].elapsed_time(evs[r][j][1])
+                                                           for r in range(R))[R // 2] * 1e3, 2))
+                  for j, (a, b) in enumerate(ranges)]
     row = dict(us=round(t * 1e6, 1), frames_per_s=round(n / t, 1), ratio_to_headline=round(n / t / headline_fps, 4),
-               upload_us=round(t_up * 1e6, 1), launches=m.info.n_launches, output=out,
+               upload_us=round(t_up * 1e6, 1), launches=m.info.n_launches, per_launch=per_launch, output=out,
                fused_blocks=[f"ops {f.first_op}-{f.first_op + f.n_ops - 1}: {f.plan}" for f in m.fused_blocks()])
     log(f"encoder via aih_model_* ({m.info.n_launches} launches): {t * 1e3:.3f} ms {n / t:.0f} frames/s "
         f"({row['ratio_to_headline']:.3f} of the headline)")
