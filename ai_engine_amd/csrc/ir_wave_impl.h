@@ -10,7 +10,7 @@
 //     MFMA column block) and runs expand -> depthwise -> project for it
 //     alone; its expanded chunk lives in a private LDS region, so the
 //     wavefronts of a workgroup never wait for each other between phases --
-//     while one is in its MFMA expand another runs its VALU depthwise;
+//     while one packs its expand results another runs its depthwise MFMAs;
 //   * the input tile (with its halo, NPI blocks of 32 pixels) goes from
 //     memory straight into MFMA operand registers once per tile (16-byte
 //     buffer loads, zeros outside the image through the range check) and
@@ -28,9 +28,9 @@
 // expand bias enters as one extra K step against a column that is 1.0 for
 // pixels inside the image and 0 outside, so outside pixels expand to exactly
 // 0 (the depthwise zero padding; the activations here are all clamp-type,
-// act(0) = 0). The depthwise of the K slice a lane feeds to the projection
-// is computed by that lane (fp32 accumulation, v_fma_mix / v_dot2c), so its
-// result is the projection's B operand without an LDS round trip.
+// act(0) = 0). The depthwise runs on 16x16x32 MFMAs with diagonal weight
+// operands (below); its result lane holds exactly the K slice it feeds to
+// the projection's MFMAs, so it is their B operand without an LDS round trip.
 #pragma once
 
 #include "ir_block_impl.h"
