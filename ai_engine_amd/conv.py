@@ -169,6 +169,7 @@ EXPORTS = (
     "aih_pack_weights_conv", "aih_pack_weights_dw", "aih_pack_bias", "aih_pack_nhwc_device",
     "aih_ir_block_plan", "aih_ir_block", "aih_last_error", "aih_version", "aih_conv_check", "aih_conv_plan",
     "aih_conv_noalloc", "aih_conv_stem_f32in", "aih_conv_dwpw_plan", "aih_conv_dwpw",
+    "aih_ir_block_stem_plan", "aih_ir_block_stem",
 )
 
 _lib = None
@@ -203,6 +204,8 @@ def lib() -> C.CDLL:
         "aih_conv_stem_f32in": (C.c_int, [C.POINTER(_IgemmDesc), P, P, P, P, P, P]),
         "aih_ir_block_plan": (C.c_int, [C.POINTER(_IrDesc), C.POINTER(IrPlan)]),
         "aih_ir_block": (C.c_int, [C.POINTER(_IrDesc), P, P, P, P, P, P, P, P, P, P]),
+        "aih_ir_block_stem_plan": (C.c_int, [C.POINTER(_IgemmDesc), C.POINTER(_IrDesc), C.POINTER(IrPlan)]),
+        "aih_ir_block_stem": (C.c_int, [C.POINTER(_IgemmDesc), C.POINTER(_IrDesc)] + [P] * 11),
         "aih_conv_dwpw_plan": (C.c_int, [C.POINTER(_DwPwDesc), C.POINTER(DwPwPlan)]),
         "aih_conv_dwpw": (C.c_int, [C.POINTER(_DwPwDesc), P, P, P, P, P, P, P, P]),
         "aih_last_error": (C.c_char_p, []),
@@ -499,6 +502,34 @@ class IrBlockSpec:
         _check(lib().aih_ir_block(C.byref(self.desc()), _ptr(x), _ptr(w_expand), _ptr(b_expand), _ptr(w_dw),
                                   _ptr(b_dw), _ptr(w_project), _ptr(b_project), _ptr(res), _ptr(y),
                                   _stream(stream)))
+        return y
+
+
+@dataclass
+class StemIrBlockSpec:
+    """The stem conv (a ConvIgemmSpec on the stem route, 3 -> 32, read from
+    the logical NHWC fp32 image) fused into the inverted-residual block that
+    reads its output as input and residual (aih_ir_block_stem): one launch,
+    the stem's output never stored; bit for bit aih_conv_stem_f32in followed
+    by aih_ir_block on the same plan. The reference dispatches the four convs
+    separately (crates/ai-gpu-runtime/src/lowering.rs:122-168)."""
+
+    stem: "ConvIgemmSpec"
+    block: IrBlockSpec
+
+    def plan(self) -> IrPlan:
+        p = IrPlan()
+        _check(lib().aih_ir_block_stem_plan(C.byref(self.stem.desc()), C.byref(self.block.desc()), C.byref(p)))
+        return p
+
+    def fusable(self) -> bool:
+        p = IrPlan()
+        return lib().aih_ir_block_stem_plan(C.byref(self.stem.desc()), C.byref(self.block.desc()), C.byref(p)) == 0
+
+    def run(self, image, w_stem, b_stem, w_expand, b_expand, w_dw, b_dw, w_project, b_project, y, stream=None):
+        _check(lib().aih_ir_block_stem(C.byref(self.stem.desc()), C.byref(self.block.desc()), _ptr(image),
+                                       _ptr(w_stem), _ptr(b_stem), _ptr(w_expand), _ptr(b_expand), _ptr(w_dw),
+                                       _ptr(b_dw), _ptr(w_project), _ptr(b_project), _ptr(y), _stream(stream)))
         return y
 
 

@@ -607,6 +607,79 @@ int plan_ir_wave(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, aih::IrWa
   return AIH_OK;
 }
 
+// The wave / split kernels' arguments from a block descriptor and its plan
+// (buffers aside).
+aih::IrWaveArgs wave_args(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, const aih::IrWavePlan &wp) {
+  aih::IrWaveArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.N = d->n;
+  a.IH = d->ih;
+  a.IW = d->iw;
+  a.OH = oh;
+  a.OW = ow;
+  a.C = d->cin;
+  a.E = d->cexp;
+  a.CO = d->cout;
+  a.COP = aih::ir_cop(d->cout);
+  a.S = d->s;
+  a.PT = (int32_t)d->pad[0];
+  a.PL = (int32_t)d->pad[1];
+  a.TH = wp.TH;
+  a.TW = wp.TW;
+  a.HH = wp.HH;
+  a.HW = wp.HW;
+  a.tiles_y = wp.tiles_y;
+  a.tiles_x = wp.tiles_x;
+  a.ntiles = wp.ntiles;
+  a.resident = wp.resident;
+  a.act_e = d->act_expand;
+  a.act_d = d->act_dw;
+  a.act_p = d->act_project;
+  a.has_res = d->residual ? 1 : 0;
+  a.nxcd = aih::device_xcds();
+  a.lds_w = wp.lds_w;
+  a.lds_bp = wp.lds_bp;
+  a.lds_xe = wp.lds_xe;
+  a.lds_red = wp.lds_red;
+  a.lds_x = wp.lds_x;
+  a.lds_stem = wp.lds_stem;
+  a.lds_res = wp.lds_res;
+  a.fd_hw = aih::make_fastdiv(wp.HW);
+  a.fd_tw = aih::make_fastdiv(wp.TW);
+  a.fd_tx = aih::make_fastdiv(wp.tiles_x);
+  a.fd_pi = aih::make_fastdiv(wp.tiles_x * wp.tiles_y);
+  return a;
+}
+
+// The stem-fused block: both descriptors checked against each other and the
+// block planned on the stem kernel (aih_ir_block_stem_plan / _stem).
+int plan_ir_stem(const aih_igemm_desc *sd, const aih_ir_block_desc *d, uint32_t *oh, uint32_t *ow,
+                 aih::StemArgs *sa, aih::IrWavePlan *wp) {
+  if (!sd || !d) return fail("ir_block_stem: null descriptor");
+  if (check_igemm(sd) || check_ir(d, oh, ow)) return AIH_ERR;
+  if (!igemm_is_stem(sd) || sd->nsrcs != 0 || sd->cin != 3 || sd->cout != 32 || sd->residual)
+    return fail("ir_block_stem: the stem must be on the stem route (k 3, d 1, AUTO, splitk 0, dt == wdt) with 3 "
+                "input and 32 output channels, one dense fp32 input and no residual");
+  if (!aih::act_is_clamp(sd->act))
+    return fail("ir_block_stem: the stem's activation must be clamp-type (none, relu, relu6, clamp01)");
+  if (sd->dt != d->dt || (d->dt != AIH_F16 && d->dt != AIH_BF16))
+    return fail("ir_block_stem: the stem and the block must both have f16 or both bf16 storage");
+  uint32_t soh, sow;
+  if (igemm_out_hw(sd, &soh, &sow)) return AIH_ERR;
+  if (sd->n != d->n || soh != d->ih || sow != d->iw || d->cin != 32 || d->cout != 32 || d->s != 1 || !d->residual)
+    return fail("ir_block_stem: the block must be 32 -> cexp -> 32 with a stride-1 depthwise and its input as "
+                "residual, on the stem's output (same n and size)");
+  if ((uint64_t)sd->n * sd->ih * sd->iw * 3 * 4 >= 0x80000000ull) return fail("ir_block_stem: image of 2 GiB or more");
+  if (d->kernel != AIH_IR_KERNEL_AUTO && d->kernel != AIH_IR_KERNEL_WAVE)
+    return fail("ir_block_stem: the stem-fused block runs the wave kernel");
+  if (d->ec && d->ec != 32) return fail("ir_block_stem: the wave kernel walks E in chunks of 32");
+  const char *why = aih::irw_plan(d->n, d->ih, d->iw, *oh, *ow, d->cin, d->cexp, d->cout, d->s, d->dt,
+                                  ir_clamp_acts(d), d->act_expand == AIH_ACT_RELU && d->act_dw == AIH_ACT_RELU,
+                                  d->tile_h, d->tile_w, d->weights, AIH_IR_KERNEL_WAVE, d->waves, wp, true);
+  if (why) return fail(std::string("ir_block_stem: ") + why);
+  return stem_args(sd, soh, sow, sa);
+}
+
 }  // namespace
 
 extern "C" {
@@ -970,8 +1043,7 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
     bool wave;
     if (plan_ir_wave(d, oh, ow, &wp, &wave)) return AIH_ERR;
     if (wave) {
-      aih::IrWaveArgs a;
-      std::memset(&a, 0, sizeof(a));
+      aih::IrWaveArgs a = wave_args(d, oh, ow, wp);
       a.x = x;
       a.we = w_expand;
       a.be = b_expand;
@@ -981,40 +1053,6 @@ int aih_ir_block(const aih_ir_block_desc *d, const void *x, const void *w_expand
       a.bp = b_project;
       a.res = res;
       a.y = y;
-      a.N = d->n;
-      a.IH = d->ih;
-      a.IW = d->iw;
-      a.OH = oh;
-      a.OW = ow;
-      a.C = d->cin;
-      a.E = d->cexp;
-      a.CO = d->cout;
-      a.COP = aih::ir_cop(d->cout);
-      a.S = d->s;
-      a.PT = (int32_t)d->pad[0];
-      a.PL = (int32_t)d->pad[1];
-      a.TH = wp.TH;
-      a.TW = wp.TW;
-      a.HH = wp.HH;
-      a.HW = wp.HW;
-      a.tiles_y = wp.tiles_y;
-      a.tiles_x = wp.tiles_x;
-      a.ntiles = wp.ntiles;
-      a.resident = wp.resident;
-      a.act_e = d->act_expand;
-      a.act_d = d->act_dw;
-      a.act_p = d->act_project;
-      a.has_res = d->residual ? 1 : 0;
-      a.nxcd = aih::device_xcds();
-      a.lds_w = wp.lds_w;
-      a.lds_bp = wp.lds_bp;
-      a.lds_xe = wp.lds_xe;
-      a.lds_red = wp.lds_red;
-      a.lds_x = wp.lds_x;
-      a.fd_hw = aih::make_fastdiv(wp.HW);
-      a.fd_tw = aih::make_fastdiv(wp.TW);
-      a.fd_tx = aih::make_fastdiv(wp.tiles_x);
-      a.fd_pi = aih::make_fastdiv(wp.tiles_x * wp.tiles_y);
       const hipError_t e = aih::launch_ir_wave(a, d->dt, wp, static_cast<hipStream_t>(stream));
       if (e != hipSuccess) return fail(std::string("ir_block wave launch: ") + hipGetErrorString(e));
       return AIH_OK;
@@ -1329,6 +1367,58 @@ int aih_conv_stem_f32in(const aih_igemm_desc *d, const float *x, const void *w, 
     sa.y = y;
     const hipError_t e = aih::launch_conv_stem(sa, d->dt, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? AIH_OK : fail(std::string("conv stem launch: ") + hipGetErrorString(e));
+  });
+}
+
+int aih_ir_block_stem_plan(const aih_igemm_desc *stem, const aih_ir_block_desc *blk, aih_ir_plan *out) {
+  return guarded([&] {
+    uint32_t oh, ow;
+    aih::StemArgs sa;
+    aih::IrWavePlan wp;
+    if (plan_ir_stem(stem, blk, &oh, &ow, &sa, &wp)) return AIH_ERR;
+    if (!out) return fail("null plan");
+    *out = aih_ir_plan{wp.TH, wp.TW, 32, blk->cexp / 32, wp.resident, wp.ntiles, wp.lds, wp.occ, wp.grid,
+                       AIH_IR_KERNEL_WAVE, wp.waves, 0};
+    return AIH_OK;
+  });
+}
+
+int aih_ir_block_stem(const aih_igemm_desc *stem, const aih_ir_block_desc *blk, const float *image,
+                      const void *w_stem, const void *b_stem, const void *w_expand, const void *b_expand,
+                      const void *w_dw, const void *b_dw, const void *w_project, const void *b_project, void *y,
+                      aih_stream stream) {
+  return guarded([&] {
+    uint32_t oh, ow;
+    aih::StemArgs sa;
+    aih::IrWavePlan wp;
+    if (plan_ir_stem(stem, blk, &oh, &ow, &sa, &wp)) return AIH_ERR;
+    if (!image || !w_stem || !b_stem || !w_expand || !b_expand || !w_dw || !b_dw || !w_project || !b_project || !y)
+      return fail("ir_block_stem: null buffer");
+    if (!aligned(image, 4)) return fail("ir_block_stem: misaligned image (4 bytes)");
+    for (const void *p : {w_stem, w_expand, w_dw, w_project, (const void *)y})
+      if (!aligned(p, 16)) return fail("ir_block_stem: misaligned buffer (y and weights need 16 bytes)");
+    for (const void *p : {b_stem, b_expand, b_dw, b_project})
+      if (!aligned(p, 8)) return fail("ir_block_stem: misaligned bias (8 bytes)");
+    aih::IrWaveArgs a = wave_args(blk, oh, ow, wp);
+    a.we = w_expand;
+    a.be = b_expand;
+    a.wd = w_dw;
+    a.bd = b_dw;
+    a.wp = w_project;
+    a.bp = b_project;
+    a.y = y;
+    a.sx = image;
+    a.sw = w_stem;
+    a.sb = b_stem;
+    a.SIH = stem->ih;
+    a.SIW = stem->iw;
+    a.SS = stem->s;
+    a.SPT = sa.PT;
+    a.SPL = sa.PL;
+    a.act_s = stem->act;
+    a.sx_bytes = (uint32_t)((uint64_t)stem->n * stem->ih * stem->iw * 3 * 4);
+    const hipError_t e = aih::launch_ir_wave_stem(a, blk->dt, wp, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? AIH_OK : fail(std::string("ir_block_stem launch: ") + hipGetErrorString(e));
   });
 }
 

@@ -29,4 +29,33 @@ struct StemArgs {
 // grid_out non-null: only the launch's workgroup count is computed (plans).
 hipError_t launch_conv_stem(const StemArgs &a, int dt, hipStream_t st, uint32_t *grid_out = nullptr);
 
+// ---- the 16-bit stem's MFMA operands, shared with the block kernel that
+// computes the stem inside its halo loads (ir_wave_impl.h) ----
+//
+// 4 K per tap (the fourth channel zero), 3 steps of v_mfma_f32_32x32x16;
+// the two lane halves hold different taps: load slot i of lane half h holds
+// tap stem_slot_tap(h, i) (ky*3 + kx; 9 = none). Both halves of a slot read
+// the same input row at neighbouring columns but one (slot 3), so one load
+// instruction touches about as many cache lines as a single tap would; slots
+// 2s and 2s + 1 of a half feed MFMA step s.
+__host__ __device__ constexpr int stem_slot_tap(int h, int i) {
+  constexpr int t[2][6] = {{0, 3, 6, 2, 8, 9}, {1, 4, 7, 5, 9, 9}};
+  return t[h][i];
+}
+
+// A operand of output channel o (lane row), lane half lh, step s: K =
+// s*16 + lh*8 + j, j < 4 the channels (ic 3 zero) of tap stem_slot_tap(lh,
+// 2s), j >= 4 those of stem_slot_tap(lh, 2s + 1), from the packed weights:
+// element (tap, kg 0, n = o, comp = ic) at ((tap*KGP)*NG + o/4)*16 + (o%4)*4
+// + ic (pack.rs:95), 16-bit storage bits.
+__device__ __forceinline__ u32x4 stem_a16(const void *w, uint32_t KGP, uint32_t NG, uint32_t o, int lh, int s) {
+  auto wt = [&](int tap, int ic) -> uint32_t {
+    if (tap >= 9 || ic >= 3) return 0u;
+    return reinterpret_cast<const uint16_t *>(w)[((size_t)tap * KGP * NG + o / 4) * 16 + (o % 4) * 4 + ic];
+  };
+  const int t = lh ? stem_slot_tap(1, 2 * s) : stem_slot_tap(0, 2 * s);
+  const int u = lh ? stem_slot_tap(1, 2 * s + 1) : stem_slot_tap(0, 2 * s + 1);
+  return u32x4{wt(t, 0) | (wt(t, 1) << 16), wt(t, 2), wt(u, 0) | (wt(u, 1) << 16), wt(u, 2)};
+}
+
 }  // namespace aih

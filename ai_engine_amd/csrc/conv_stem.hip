@@ -33,14 +33,6 @@
 namespace aih {
 namespace {
 
-__device__ __forceinline__ uint32_t pk(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
-
-// 16-bit: the tap (ky*3 + kx; 9 = none) in load slot i of lane half h. Both
-// halves of a slot read the same input row at neighbouring columns but one
-// (slot 3), so one load instruction touches about as many cache lines as a
-// single tap would; slots 2s and 2s + 1 of a half feed MFMA step s.
-__device__ constexpr int kSlotTap[2][6] = {{0, 3, 6, 2, 8, 9}, {1, 4, 7, 5, 9, 9}};
-
 // Output staging rows: 32 pixels x 32 fp32 channels per wavefront, pitch 4
 // floats wider than the row so the MFMA-layout writes spread over the banks.
 constexpr uint32_t kStPitch = 36;
@@ -72,9 +64,8 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
     if constexpr (F32) return reinterpret_cast<const uint32_t *>(a.w)[idx];
     else return reinterpret_cast<const uint16_t *>(a.w)[idx];
   };
-  // 16-bit: 3 steps of K 16; A[ob][s] holds K = s*16 + lh*8 + j, j < 4 the
-  //   channels (ic 3 zero) of tap kSlotTap[lh][2s], j >= 4 those of kSlotTap[lh][2s + 1].
-  // fp32: K = tap*3 + ic (27, padded to 32); Af[ob][s] holds K = 2s + lh.
+  // 16-bit: 3 steps of K 16 (stem_a16); fp32: K = tap*3 + ic (27, padded to
+  // 32), Af[ob][s] holding K = 2s + lh.
   u32x4 A[F32 ? 1 : NOB][3];
   float Af[F32 ? NOB : 1][16];
 #pragma unroll
@@ -88,11 +79,7 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
       }
     } else {
 #pragma unroll
-      for (int s = 0; s < 3; ++s) {
-        const int t = lh ? kSlotTap[1][2 * s] : kSlotTap[0][2 * s];
-        const int u = lh ? kSlotTap[1][2 * s + 1] : kSlotTap[0][2 * s + 1];
-        A[ob][s] = u32x4{pk(wtap(o, t, 0), wtap(o, t, 1)), wtap(o, t, 2), pk(wtap(o, u, 0), wtap(o, u, 1)), wtap(o, u, 2)};
-      }
+      for (int s = 0; s < 3; ++s) A[ob][s] = stem_a16(a.w, a.KGP, NG, o, lh, s);
     }
   }
   // bias of the lane's 16 channels per output block: groups 8q + 4lh
@@ -108,14 +95,14 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
 
   // The input pixels a lane loads per output pixel. fp32: all 9 taps (each
   // lane half feeds every tap). 16-bit: 5 slots, slot i holding tap
-  // kSlotTap[lh][i], so the two halves split the loads and each slot pair
-  // is one B operand.
+  // stem_slot_tap(lh, i), so the two halves split the loads and each slot
+  // pair is one B operand.
   constexpr int NT = F32 ? 9 : 5;
   int32_t tdy[NT], tdx[NT], toff[NT];
   bool tok[NT];
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
-    const int t0 = F32 ? i : kSlotTap[0][i], t1 = F32 ? i : kSlotTap[1][i];
+    const int t0 = F32 ? i : stem_slot_tap(0, i), t1 = F32 ? i : stem_slot_tap(1, i);
     tdy[i] = lh ? t1 / 3 : t0 / 3;
     tdx[i] = lh ? t1 % 3 : t0 % 3;
     tok[i] = lh ? t1 < 9 : t0 < 9;

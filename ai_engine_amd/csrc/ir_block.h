@@ -105,7 +105,22 @@ struct IrWaveArgs {
   uint32_t lds_red;                // split kernel: projection partial sums (over the regions below)
   uint32_t lds_x;                  // split kernel: the tile's input halo
   FastDiv fd_hw, fd_tw, fd_tx, fd_pi;
+  // ir_wave_stem_kernel only: the block's input (and residual) is the output
+  // of a 3x3 stem conv over a 3-channel fp32 image, computed per halo pixel
+  // instead of read (x and res unused)
+  const void *sx;                  // the image [N][SIH][SIW][3], fp32, < 2 GiB
+  const void *sw, *sb;             // stem weights (packed, the storage dtype) and bias [C]
+  uint32_t SIH, SIW, SS, sx_bytes; // image size, stem stride, bytes of sx
+  int32_t SPT, SPL, act_s;         // stem padding (top, left), activation (clamp-type)
+  uint32_t lds_stem, lds_res;      // LDS: stem A operands + fp32 bias; per-wavefront residual stashes
 };
+
+// LDS of the stem-fused launch beyond the block's own: the stem's A operands
+// (3 MFMA steps x 64 lanes x 16 bytes) and fp32 bias (32 channels), and per
+// wavefront the tile's stem outputs (<= 32 pixels x 32 16-bit channels),
+// the block's residual.
+constexpr uint32_t IRW_STEM_LDS = 3 * 64 * 16 + 32 * 4;
+constexpr uint32_t IRW_RES_STASH = 32 * 32 * 2;
 
 // Bytes of one chunk's weight slot: expand [C/4][32][4], project [8][COP][4]
 // (channels CO..COP zero), then IRW_SMB bytes of depthwise taps and biases
@@ -126,6 +141,7 @@ struct IrWavePlan {
   uint32_t waves;                       // wavefronts per workgroup (wave: 2, 4, 8 or 12; split: 1, 2, 4 or 8)
   uint32_t tiles_y, tiles_x, ntiles;
   uint32_t lds_w, lds_bp, lds_xe, lds_red, lds_x, lds;  // LDS byte offsets and total
+  uint32_t lds_stem, lds_res;           // stem-fused launch: stem tables, residual stashes
   uint32_t occ, grid;                   // workgroups per CU, launched workgroups
 };
 
@@ -144,11 +160,15 @@ constexpr uint32_t IRS_RED_BLOCK = 32 * 32 * 4;
 // the plan's choice). Returns nullptr, or the reason the block cannot run on
 // these kernels (dtype, activations, widths without an instantiation, LDS).
 // rl: the expand and depthwise activations are both ReLU (selects the
-// instantiation whose register use bounds the occupancy).
+// instantiation whose register use bounds the occupancy). stem: the plan of
+// the stem-fused launch (ir_wave_stem_kernel: the wave kernel's 32 -> E -> 32
+// stride-1 shape with ReLU inside, its LDS grown by the stem tables and the
+// wavefronts' residual stashes).
 const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
                      uint32_t CO, uint32_t S, int dt, bool cl, bool rl, uint32_t tile_h, uint32_t tile_w,
-                     int32_t weights, int32_t kernel, uint32_t waves, IrWavePlan *p);
+                     int32_t weights, int32_t kernel, uint32_t waves, IrWavePlan *p, bool stem = false);
 
 hipError_t launch_ir_wave(const IrWaveArgs &a, int dt, const IrWavePlan &p, hipStream_t st);
+hipError_t launch_ir_wave_stem(const IrWaveArgs &a, int dt, const IrWavePlan &p, hipStream_t st);
 
 }  // namespace aih

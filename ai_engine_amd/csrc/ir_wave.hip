@@ -23,7 +23,8 @@ uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
 
 // Workgroups per CU of an instantiation at a workgroup size and LDS size
 // (queried once per device).
-// split: 0 = wave kernel, 1 = split kernel, 2 = split kernel with the deep prefetch
+// split: 0 = wave kernel, 1 = split kernel, 2 = split kernel with the deep
+// prefetch, 3 = the stem-fused wave kernel
 int irw_occupancy(int split, int dt, uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves,
                   uint32_t lds) {
   static std::mutex mu;
@@ -35,7 +36,9 @@ int irw_occupancy(int split, int dt, uint32_t ke, uint32_t npi, uint32_t nob, bo
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int occ;
-  if (split)
+  if (split == 3)
+    occ = dt == DT_F16 ? ir_wave_stem_occ_f16(waves, lds) : ir_wave_stem_occ_bf16(waves, lds);
+  else if (split)
     occ = dt == DT_F16 ? ir_split_occ_f16(ke, npi, nob, rl, split == 2, waves, lds)
                        : ir_split_occ_bf16(ke, npi, nob, rl, split == 2, waves, lds);
   else
@@ -60,7 +63,13 @@ double simd_eff(uint32_t n) { return n <= 1 ? 0.45 : n == 2 ? 0.7 : n == 3 ? 0.8
 
 const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
                      uint32_t CO, uint32_t S, int dt, bool cl, bool rl, uint32_t tile_h, uint32_t tile_w,
-                     int32_t weights, int32_t kernel, uint32_t waves_force, IrWavePlan *out) {
+                     int32_t weights, int32_t kernel, uint32_t waves_force, IrWavePlan *out, bool stem) {
+  if (stem) {
+    if (C != 32 || CO != 32 || S != 1) return "the stem-fused block is 32 -> E -> 32 with a stride-1 depthwise";
+    if (!rl) return "the stem-fused block takes ReLU after its expand and its depthwise";
+    if (kernel != AIH_IR_KERNEL_AUTO && kernel != AIH_IR_KERNEL_WAVE) return "the stem-fused block runs the wave kernel";
+    kernel = AIH_IR_KERNEL_WAVE;
+  }
   if (dt != DT_F16 && dt != DT_BF16) return "the wave kernels take f16 / bf16 storage";
   if (!cl) return "the wave kernels take clamp-type activations (identity, ReLU, ReLU6, clamp01)";
   if (C % 16 || E % 32 || CO % 16 || C == 0 || E == 0 || CO == 0) return "cin % 16, cexp % 32 and cout % 16 needed";
@@ -87,13 +96,13 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = -1;
   struct Key {
-    uint32_t v[17];
+    uint32_t v[18];
     bool operator<(const Key &o) const { return std::memcmp(v, o.v, sizeof(v)) < 0; }
   };
   static std::mutex mu;
   static std::map<Key, IrWavePlan> cache;
   const Key key{{N, IH, IW, OH, OW, C, E, CO, S, (uint32_t)dt, tile_h, tile_w, (uint32_t)weights, (uint32_t)dev,
-                 rl ? 1u : 0u, (uint32_t)kernel, waves_force}};
+                 rl ? 1u : 0u, (uint32_t)kernel, waves_force, stem ? 1u : 0u}};
   {
     std::lock_guard<std::mutex> lock(mu);
     auto it = cache.find(key);
@@ -156,8 +165,14 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
           p.lds_xe = align16(p.lds_bp + CO * 4);
           p.lds_red = 0;
           p.lds = p.lds_xe + waves * npi * 32 * IRW_XPIX;
+          if (stem) {
+            if (npi != 2) continue;
+            p.lds_stem = p.lds;
+            p.lds_res = p.lds_stem + IRW_STEM_LDS;
+            p.lds = p.lds_res + waves * IRW_RES_STASH;
+          }
           if (p.lds > 160u * 1024u) continue;
-          p.occ = (uint32_t)irw_occupancy(0, dt, ke, npi, nob, rl, waves, p.lds);
+          p.occ = (uint32_t)irw_occupancy(stem ? 3 : 0, dt, ke, npi, nob, rl, waves, p.lds);
           if (p.occ == 0) continue;  // not resident at this size
           p.tiles_y = tiles_y;
           p.tiles_x = tiles_x;
@@ -174,7 +189,7 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
           keep(p, (rounds + 1e-3 * (double)nt / (cus * 4.0)) * per_tile / simd_eff(per_simd));
         }
     }
-    if (kernel != AIH_IR_KERNEL_WAVE && weights == AIH_IR_WEIGHTS_AUTO && npi_s) {
+    if (!stem && kernel != AIH_IR_KERNEL_WAVE && weights == AIH_IR_WEIGHTS_AUTO && npi_s) {
       const uint32_t npi = npi_s;
       const double chunk = chunk_cost(npi);
       for (uint32_t w : {1u, 2u, 4u, 8u}) {
@@ -234,6 +249,17 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
   }
   *out = bp;
   return nullptr;
+}
+
+hipError_t launch_ir_wave_stem(const IrWaveArgs &a, int dt, const IrWavePlan &p, hipStream_t st) {
+  if (p.lds > 160u * 1024u || p.grid == 0 || p.split || p.NPI != 2 || a.C != 32 || a.COP != 32 ||
+      (p.waves != 2 && p.waves != 4 && p.waves != 8))
+    return hipErrorInvalidValue;
+  switch (dt) {
+    case DT_F16: return launch_ir_wave_stem_f16(a, p.waves, p.lds, p.grid, st);
+    case DT_BF16: return launch_ir_wave_stem_bf16(a, p.waves, p.lds, p.grid, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_ir_wave(const IrWaveArgs &a, int dt, const IrWavePlan &p, hipStream_t st) {

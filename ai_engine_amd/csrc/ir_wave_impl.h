@@ -33,6 +33,7 @@
 // the projection's MFMAs, so it is their B operand without an LDS round trip.
 #pragma once
 
+#include "conv_stem.h"
 #include "ir_block_impl.h"
 
 namespace aih {
@@ -223,10 +224,13 @@ __device__ __forceinline__ void irdw_chunk(const char *xe, const char *sm, const
 
 // Bias, act_p, residual and the store of a wavefront's projection results:
 // block og (16 output channels) of pixel group pg, lane rows 4q .. 4q + 3 =
-// output channels 16 og + 4q .. + 3 of pixel pix[pg].
-template <int DT, int NOG>
+// output channels 16 og + 4q .. + 3 of pixel pix[pg]. STEM: the residual
+// comes from the wavefront's stash (32 16-bit channels per tile pixel, tile
+// pixel pg * 16 + l16), not from memory.
+template <int DT, int NOG, bool STEM = false>
 __device__ __forceinline__ void irdw_store(const IrWaveArgs &a, const float *BpL, const f32x4 (&acc)[NOG][2],
-                                          const bool (&ok)[2], const uint32_t (&pix)[2], int q, const Act &act_p) {
+                                          const bool (&ok)[2], const uint32_t (&pix)[2], int q, const Act &act_p,
+                                          const char *ResL = nullptr, int l16 = 0) {
 #pragma unroll
   for (int og = 0; og < NOG; ++og) {
     const uint32_t oc = og * 16 + 4 * q;
@@ -239,7 +243,10 @@ __device__ __forceinline__ void irdw_store(const IrWaveArgs &a, const float *BpL
       ir_act<true, 4>(act_p, t4);
       v = f32x4{t4[0], t4[1], t4[2], t4[3]};
       const size_t vi = (size_t)pix[pg] * (a.CO / 4) + oc / 4;
-      if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
+      if constexpr (STEM)
+        v += unpack4<DT>(*reinterpret_cast<const u32x2 *>(ResL + ((pg * 16 + l16) * 32 + oc) * 2));
+      else if (a.has_res)
+        v += Vec4IO<DT>::load(a.res, vi);
       Vec4IO<DT>::store(a.y, vi, v);
     }
   }
@@ -255,11 +262,18 @@ __host__ __device__ constexpr int irw_waves_per_simd(int ke, int npi, int nob) {
   return ke == 2 && npi == 2 && nob == 1 ? 4 : irw_max_waves(ke, npi, nob) == 12 ? 3 : 1;
 }
 
-template <int DT, int KE, int NPI, int NOB, bool RL>
-__global__ __launch_bounds__(64 * irw_max_waves(KE, NPI, NOB))
-__attribute__((amdgpu_waves_per_eu(irw_waves_per_simd(KE, NPI, NOB))))
-void ir_wave_kernel(IrWaveArgs a) {
+// The kernel body. STEM: the block's input is computed, not read -- each halo
+// pixel's 32 channels are the stem conv's output at that pixel (the 3x3
+// conv over the 3-channel fp32 image, with the stem kernel's operands,
+// MFMA steps, bias, activation and rounding: bit for bit what the stem
+// kernel stores), held as the expand's B operands, and the tile's own
+// pixels of it stashed in LDS as the projection's residual. The expand's
+// operands are the unfused block's, in its K order, so the block's sums are
+// the same.
+template <int DT, int KE, int NPI, int NOB, bool RL, bool STEM>
+__device__ __forceinline__ void ir_wave_body(const IrWaveArgs &a) {
   static_assert(DT == DT_F16 || DT == DT_BF16, "16-bit storage");
+  static_assert(!STEM || (KE == 2 && NOB == 1), "the stem feeds a 32-channel block");
   extern __shared__ __align__(16) char lds[];
   constexpr int ES = 2, KSTEP = 16, HK = 8, EC = 32, NOG = 2 * NOB;
   constexpr uint32_t GB = 4 * ES;  // one packed group: 4 K of one channel
@@ -340,6 +354,18 @@ void ir_wave_kernel(IrWaveArgs a) {
   } else {
     dma_chunk(0, 0);
   }
+  if constexpr (STEM) {
+    // the stem's A operands as the stem kernel builds them (lane (channel
+    // l32, half lh), steps 0..2) and its bias in fp32, once per workgroup
+    if (tid < 64) {
+#pragma unroll
+      for (int s = 0; s < 3; ++s)
+        *reinterpret_cast<u32x4 *>(lds + a.lds_stem + (s * 64 + lane) * 16) = stem_a16(a.sw, 4, C / 4, l32, lh, s);
+    } else if (tid < 64 + (int)C / 4) {
+      const int g = tid - 64;
+      *reinterpret_cast<f32x4 *>(lds + a.lds_stem + 3 * 64 * 16 + g * 16) = Vec4IO<DT>::load(a.sb, g);
+    }
+  }
   ir_dma_wait();
   __syncthreads();
 
@@ -350,6 +376,11 @@ void ir_wave_kernel(IrWaveArgs a) {
 
   const char *xg = reinterpret_cast<const char *>(a.x);
   const uint32_t img_bytes = a.IH * a.IW * C * ES;
+  // STEM: the whole fp32 image batch as one buffer (below 2 GiB), and this
+  // wavefront's residual stash
+  const __amdgpu_buffer_rsrc_t rs_sx = STEM ? ir_rsrc(a.sx, a.sx_bytes) : ir_rsrc(a.we, 0);
+  char *ResL = lds + a.lds_res + (uint32_t)wave * IRW_RES_STASH;
+  const Act act_s = act_params(a.act_s);
   const uint32_t per_img = a.tiles_y * a.tiles_x;
   const uint32_t HPIX = a.HH * a.HW, TPIX = a.TH * a.TW;
   constexpr uint32_t ONE = DT == DT_F16 ? 0x3C00u : 0x3F80u;
@@ -368,18 +399,72 @@ void ir_wave_kernel(IrWaveArgs a) {
     const uint32_t tyi = fdiv(trem, a.fd_tx);
     const uint32_t ty0 = tyi * a.TH, tx0 = (trem - tyi * a.tiles_x) * a.TW;
     const int32_t iy0 = (int32_t)(ty0 * a.S) - a.PT, ix0 = (int32_t)(tx0 * a.S) - a.PL;
-    const __amdgpu_buffer_rsrc_t rs_x = ir_rsrc(xg + (size_t)img * img_bytes, img_bytes);
+    const __amdgpu_buffer_rsrc_t rs_x = ir_rsrc(xg + (size_t)img * img_bytes, STEM ? 0u : img_bytes);
 #pragma unroll
     for (int b = 0; b < NPI; ++b) {
       const uint32_t r = b * 32 + l32;
       const uint32_t hy = fdiv(r, a.fd_hw), hx = r - hy * a.HW;
       const int32_t iy = iy0 + (int32_t)hy, ix = ix0 + (int32_t)hx;
       const bool in = r < HPIX && (uint32_t)iy < a.IH && (uint32_t)ix < a.IW;
-      const uint32_t off = in ? ((uint32_t)iy * a.IW + (uint32_t)ix) * (C * ES) + lh * 16 : IR_OOB;
-#pragma unroll
-      for (int k = 0; k < KE; ++k)
-        xop[b][k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_x, off + k * 32, 0, 0));
       inside[b] = in;
+      if constexpr (!STEM) {
+        const uint32_t off = in ? ((uint32_t)iy * a.IW + (uint32_t)ix) * (C * ES) + lh * 16 : IR_OOB;
+#pragma unroll
+        for (int k = 0; k < KE; ++k)
+          xop[b][k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_x, off + k * 32, 0, 0));
+      } else {
+        // the stem at block input pixel (iy, ix): its 5 input-pixel slots of
+        // this lane half (zeros outside the image, or for a halo pixel
+        // outside the block's input), 3 MFMAs, act(acc + bias), rounded
+        const int32_t sy0 = iy * (int32_t)a.SS - a.SPT, sx0 = ix * (int32_t)a.SS - a.SPL;
+        const uint32_t v0 = ((uint32_t)img * a.SIH + (uint32_t)sy0) * a.SIW + (uint32_t)sx0;
+        u32x2 th[6];
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+          const int t0 = stem_slot_tap(0, i), t1 = stem_slot_tap(1, i);
+          const int32_t dy = lh ? t1 / 3 : t0 / 3, dx = lh ? t1 % 3 : t0 % 3;
+          const bool tok = lh ? t1 < 9 : t0 < 9;
+          const bool sin = in && tok && (uint32_t)(sy0 + dy) < a.SIH && (uint32_t)(sx0 + dx) < a.SIW;
+          typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+          const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(
+              rs_sx, sin ? (v0 + (uint32_t)(dy * (int32_t)a.SIW + dx)) * 12u : IR_OOB, 0, 0);
+          th[i] = pack4<DT>(f32x4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), 0.0f});
+        }
+        th[5] = u32x2{0u, 0u};
+        f32x16 sa = {};
+#pragma unroll
+        for (int s = 0; s < 3; ++s)
+          sa = ir_mma<DT>(*reinterpret_cast<const u32x4 *>(lds + a.lds_stem + (s * 64 + lane) * 16),
+                          u32x4{th[2 * s].x, th[2 * s].y, th[2 * s + 1].x, th[2 * s + 1].y}, sa);
+        // lane: pixel r, channels 8 qq + 4 lh .. + 3 in sa[4 qq .. 4 qq + 3]
+        u32x2 h[4];
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const f32x4 o = f32x4{sa[4 * qq], sa[4 * qq + 1], sa[4 * qq + 2], sa[4 * qq + 3]} +
+                          *reinterpret_cast<const f32x4 *>(lds + a.lds_stem + 3 * 64 * 16 + (8 * qq + 4 * lh) * 4);
+          const u32x2 p = pack4<DT>(f32x4{act_clamp_any(act_s, o.x), act_clamp_any(act_s, o.y),
+                                          act_clamp_any(act_s, o.z), act_clamp_any(act_s, o.w)});
+          h[qq] = in ? p : u32x2{0u, 0u};
+        }
+        // the expand's B operand of step k, lane half lh: channels 16k + 8lh
+        // .. + 7, as the unfused block loads them (the same K order, so the
+        // same MFMA sums); half 0 holds groups 8q + 0..3, half 1 8q + 4..7:
+        // each half passes the other the two groups it lacks
+        const u32x2 sa0 = lh ? h[0] : h[1], sb0 = lh ? h[2] : h[3];
+        const u32x2 ra = u32x2{(uint32_t)__shfl_xor((int)sa0.x, 32), (uint32_t)__shfl_xor((int)sa0.y, 32)};
+        const u32x2 rb = u32x2{(uint32_t)__shfl_xor((int)sb0.x, 32), (uint32_t)__shfl_xor((int)sb0.y, 32)};
+        xop[b][0] = lh ? u32x4{ra.x, ra.y, h[1].x, h[1].y} : u32x4{h[0].x, h[0].y, ra.x, ra.y};
+        xop[b][1] = lh ? u32x4{rb.x, rb.y, h[3].x, h[3].y} : u32x4{h[2].x, h[2].y, rb.x, rb.y};
+        // the tile's own pixels: the projection's residual (stride 1, the
+        // block's input pixel (iy, ix) = output pixel (iy0 + hy, ix0 + hx)
+        // less the padding)
+        const uint32_t ry = hy - (uint32_t)a.PT, rx = hx - (uint32_t)a.PL;
+        if (r < HPIX && ry < a.TH && rx < a.TW) {
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq)
+            *reinterpret_cast<u32x2 *>(ResL + ((ry * a.TW + rx) * 32 + 8 * qq + 4 * lh) * 2) = h[qq];
+        }
+      }
     }
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg) {
@@ -441,7 +526,7 @@ void ir_wave_kernel(IrWaveArgs a) {
     for (uint32_t T = t_begin + wave; T < t_end; T += nwaves) {
       begin_tile(T);
       for (uint32_t c = 0; c < nchunks; ++c) run_chunk(WL + c * SLOT);
-      irdw_store<DT, NOG>(a, BpL, acc, ok, pix, q, act_p);
+      irdw_store<DT, NOG, STEM>(a, BpL, acc, ok, pix, q, act_p, ResL, l16);
     }
     return;
   }
@@ -464,9 +549,25 @@ void ir_wave_kernel(IrWaveArgs a) {
       if (!last || more) dma_chunk(last ? 0 : c + 1, (gc + 1) & 1);
       if (active) run_chunk(WL + (gc & 1) * SLOT);
     }
-    if (active) irdw_store<DT, NOG>(a, BpL, acc, ok, pix, q, act_p);
+    if (active) irdw_store<DT, NOG, STEM>(a, BpL, acc, ok, pix, q, act_p, ResL, l16);
   }
   ir_dma_wait();
+}
+
+template <int DT, int KE, int NPI, int NOB, bool RL>
+__global__ __launch_bounds__(64 * irw_max_waves(KE, NPI, NOB))
+__attribute__((amdgpu_waves_per_eu(irw_waves_per_simd(KE, NPI, NOB))))
+void ir_wave_kernel(IrWaveArgs a) {
+  ir_wave_body<DT, KE, NPI, NOB, RL, false>(a);
+}
+
+// The stem conv fused into the first inverted-residual block after it: the
+// 32 -> 128 -> 32 stride-1 block (ReLU inside) reading the stem's output as
+// its input and residual. The stem's output is never stored.
+template <int DT>
+__global__ __launch_bounds__(64 * irw_max_waves(2, 2, 1)) __attribute__((amdgpu_waves_per_eu(irw_waves_per_simd(2, 2, 1))))
+void ir_wave_stem_kernel(IrWaveArgs a) {
+  ir_wave_body<DT, 2, 2, 1, true, true>(a);
 }
 
 template <int DT, int KE, int NPI, int NOB, bool RL>
@@ -535,8 +636,37 @@ inline int irw_occ_dt(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t
   return 0;
 }
 
+template <int DT>
+inline hipError_t irw_stem_prepare() {
+  static const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(ir_wave_stem_kernel<DT>),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  return e;
+}
+
+template <int DT>
+inline hipError_t irw_stem_launch(const IrWaveArgs &a, uint32_t waves, uint32_t lds, uint32_t grid, hipStream_t st) {
+  const hipError_t e = irw_stem_prepare<DT>();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((ir_wave_stem_kernel<DT>), dim3(grid), dim3(64 * waves), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int DT>
+inline int irw_stem_occ(uint32_t waves, uint32_t lds) {
+  if (irw_stem_prepare<DT>() != hipSuccess) return -1;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ir_wave_stem_kernel<DT>, (int)(64 * waves), lds) !=
+      hipSuccess)
+    return -1;
+  return per_cu;
+}
+
 hipError_t launch_ir_wave_f16(const IrWaveArgs &a, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
                               hipStream_t st);
+hipError_t launch_ir_wave_stem_f16(const IrWaveArgs &a, uint32_t waves, uint32_t lds, uint32_t grid, hipStream_t st);
+hipError_t launch_ir_wave_stem_bf16(const IrWaveArgs &a, uint32_t waves, uint32_t lds, uint32_t grid, hipStream_t st);
+int ir_wave_stem_occ_f16(uint32_t waves, uint32_t lds);
+int ir_wave_stem_occ_bf16(uint32_t waves, uint32_t lds);
 hipError_t launch_ir_wave_bf16(const IrWaveArgs &a, uint32_t npi, uint32_t waves, uint32_t lds, uint32_t grid,
                                hipStream_t st);
 int ir_wave_occ_f16(uint32_t ke, uint32_t npi, uint32_t nob, bool rl, uint32_t waves, uint32_t lds);

@@ -153,11 +153,13 @@ struct aih_model {
   uint32_t flags = 0;
   struct Fused {
     uint32_t first;  // ops first .. first + nops - 1
-    uint32_t nops;   // 3: inverted-residual block (d, plan); 2: depthwise -> pointwise pair (dp, dpp)
+    uint32_t nops;   // 3: inverted-residual block (d, plan); 2: depthwise -> pointwise pair (dp, dpp);
+                     // 4: the stem conv and the block after it (sd, d, plan: aih_ir_block_stem)
     aih_ir_block_desc d;
     aih_ir_plan plan;
     aih_dwpw_desc dp;
     aih_dwpw_plan dpp;
+    aih_igemm_desc sd;
   };
   std::vector<Fused> fused;
   std::vector<int32_t> block_of;  // per op: its fused block, or -1
@@ -694,6 +696,162 @@ int settle_input(const aih_model *cm, aih_stream stream) {
   return AIH_OK;
 }
 
+// The stem conv fused into the inverted-residual block after it
+// (aih_ir_block_stem): the stem-from-fp32 route's conv (stem_op) whose
+// output only that fused block reads -- as its expand input and its
+// residual, two reads -- and that is no graph output, state or alias. Runs
+// after lower(): op k's launch becomes one aih_ir_block_stem from the
+// staged fp32 input, falling back to the stem and the block as two
+// launches (the stem's output keeps its slot for that) when the input slot
+// holds the input instead; the block's record then covers the stem op
+// (n_ops 4) and the stem's output counts as the block's intermediate. With
+// AIH_MODEL_TUNE the two launches and the fused one at the tune tiles,
+// placements and 4 / 8 wavefronts are timed on the model's buffers (the
+// staged input zeroed), the fastest kept; else the fused launch on the
+// block's own tile and placement where it plans. Not under AIH_MODEL_NO_FUSE.
+void fuse_stem_launch(aih_model *m) {
+  if (m->stem_op < 0 || (m->flags & AIH_MODEL_NO_FUSE)) return;
+  const size_t k = (size_t)m->stem_op;
+  const auto &ops = m->g.ops;
+  if (k + 3 >= ops.size() || m->block_of[k + 1] < 0) return;
+  const int32_t bi = m->block_of[k + 1];
+  aih_model::Fused &f = m->fused[(size_t)bi];
+  if (f.first != k + 1 || f.nops != 3) return;
+  const sw::Op &S = ops[k], &A = ops[k + 1], &B = ops[k + 2], &P = ops[k + 3];
+  const uint32_t t = S.out;
+  if (S.res >= 0 || A.in != t || P.res != (int64_t)t || m->g.tensors[t].alias_of >= 0) return;
+  for (uint32_t o : m->g.outputs)
+    if (o == t) return;
+  for (const auto &st : m->g.states)
+    if (st.first == t || st.second == t) return;
+  for (const auto &tt : m->g.tensors)
+    if (tt.alias_of == (int64_t)t) return;
+  size_t nreads = 0;
+  for (const auto &op : ops)
+    for (uint32_t r : reads_of(op)) nreads += r == t;
+  if (nreads != 2) return;
+  const auto &I = m->g.tensors[S.in];
+  aih_igemm_desc sd{};
+  sd.n = m->n;
+  sd.ih = I.h;
+  sd.iw = I.w;
+  sd.cin = S.cin;
+  sd.cout = S.cout;
+  sd.k = 3;
+  sd.s = S.sh;
+  sd.d = 1;
+  std::memcpy(sd.pad, S.pad, sizeof(sd.pad));
+  sd.act = S.act;
+  sd.dt = m->dt;
+  sd.wdt = m->wdt;
+  const float *img = m->staging;
+  const void *ws = m->wptr(S.w), *bs = m->wptr(S.b), *we = m->wptr(A.w), *be = m->wptr(A.b), *wd = m->wptr(B.w),
+             *bd = m->wptr(B.b), *wp = m->wptr(P.w), *bp = m->wptr(P.b);
+  void *y = m->ptr(P.out);
+  // the candidates: the block's own tile and placement, then (tuning) the tune set
+  std::vector<aih_ir_block_desc> cands;
+  {
+    aih_ir_block_desc d = f.d;
+    if (d.kernel != AIH_IR_KERNEL_WAVE) d.kernel = AIH_IR_KERNEL_AUTO, d.tile_h = d.tile_w = 0, d.waves = 0;
+    cands.push_back(d);
+  }
+  const bool tune = (m->flags & AIH_MODEL_TUNE) != 0;
+  if (tune)
+    for (const auto &tt : kTuneWaveTiles)
+      for (int32_t w : {AIH_IR_WEIGHTS_RESIDENT, AIH_IR_WEIGHTS_STREAMED})
+        for (uint32_t wv : {0u, 4u, 8u}) {
+          aih_ir_block_desc d = f.d;
+          d.kernel = AIH_IR_KERNEL_WAVE;
+          d.tile_h = tt[0];
+          d.tile_w = tt[1];
+          d.weights = w;
+          d.waves = wv;
+          cands.push_back(d);
+        }
+  std::function<int(hipStream_t)> sep_stem = m->launches[k], sep_blk = m->launches[k + 1];
+  aih_ir_block_desc best{};
+  aih_ir_plan best_plan{};
+  bool found = false;
+  if (!tune) {
+    for (const auto &d : cands)
+      if (aih_ir_block_stem_plan(&sd, &d, &best_plan) == AIH_OK) {
+        best = d;
+        found = true;
+        break;
+      }
+  } else {
+    hipStream_t st = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) throw std::runtime_error("tune: hipStreamCreate");
+    hipEvent_t ev[10];
+    for (auto &e : ev)
+      if (hipEventCreate(&e) != hipSuccess) throw std::runtime_error("tune: hipEventCreate");
+    struct Cleanup {
+      hipStream_t st;
+      hipEvent_t *ev;
+      ~Cleanup() {
+        for (int i = 0; i < 10; ++i) (void)hipEventDestroy(ev[i]);
+        (void)hipStreamDestroy(st);
+      }
+    } cleanup{st, ev};
+    if (hipMemsetAsync(m->staging, 0, m->staging_floats * 4, st) != hipSuccess) throw std::runtime_error("tune: memset");
+    const bool staged0 = m->staged;
+    m->staged = true;
+    auto time = [&](const std::function<int(hipStream_t)> &fn) -> float {
+      for (int w = 0; w < 2; ++w)
+        if (fn(st) != AIH_OK) throw std::runtime_error(std::string("tune: ") + aih_last_error());
+      for (int r = 0; r < 5; ++r)
+        if (hipEventRecord(ev[2 * r], st) != hipSuccess || fn(st) != AIH_OK || hipEventRecord(ev[2 * r + 1], st) != hipSuccess)
+          throw std::runtime_error("tune: launch");
+      if (hipEventSynchronize(ev[9]) != hipSuccess) throw std::runtime_error("tune: hipEventSynchronize");
+      float ts[5];
+      for (int r = 0; r < 5; ++r)
+        if (hipEventElapsedTime(&ts[r], ev[2 * r], ev[2 * r + 1]) != hipSuccess) throw std::runtime_error("tune: elapsed");
+      std::sort(ts, ts + 5);
+      return ts[2];
+    };
+    float best_ms = time([&](hipStream_t s) { return sep_stem(s) != AIH_OK ? AIH_ERR : sep_blk(s); });
+    std::set<std::array<uint32_t, 4>> seen;
+    for (const auto &d : cands) {
+      aih_ir_plan plan;
+      if (aih_ir_block_stem_plan(&sd, &d, &plan) != AIH_OK) continue;
+      if (!seen.insert({plan.th, plan.tw, plan.resident, plan.waves}).second) continue;
+      aih_ir_block_desc dd = d;
+      dd.kernel = AIH_IR_KERNEL_WAVE;
+      dd.tile_h = plan.th;
+      dd.tile_w = plan.tw;
+      dd.weights = plan.resident ? AIH_IR_WEIGHTS_RESIDENT : AIH_IR_WEIGHTS_STREAMED;
+      dd.waves = plan.waves;
+      const float ms = time([&](hipStream_t s) {
+        return aih_ir_block_stem(&sd, &dd, img, ws, bs, we, be, wd, bd, wp, bp, y, s);
+      });
+      if (ms < best_ms) {
+        best_ms = ms;
+        best = dd;
+        best_plan = plan;
+        found = true;
+      }
+    }
+    m->staged = staged0;
+    if (hipStreamSynchronize(st) != hipSuccess) throw std::runtime_error("tune: hipStreamSynchronize");
+  }
+  if (!found) return;
+  aih_model *mm = m;
+  const aih_ir_block_desc d = best;
+  m->launches[k] = [mm, sd, d, ws, bs, we, be, wd, bd, wp, bp, y, sep_stem, sep_blk](hipStream_t s) {
+    // the staged fp32 upload: one launch; else the stem from the input slot, then the block
+    if (mm->staged) return aih_ir_block_stem(&sd, &d, mm->staging, ws, bs, we, be, wd, bd, wp, bp, y, s);
+    return sep_stem(s) != AIH_OK ? AIH_ERR : sep_blk(s);
+  };
+  m->launches[k + 1] = {};
+  f.first = (uint32_t)k;
+  f.nops = 4;
+  f.sd = sd;
+  f.d = best;
+  f.plan = best_plan;
+  m->block_of[k] = bi;
+  m->internal[t] = (int32_t)k;
+}
+
 void lower(aih_model *m) {
   const auto &T = m->g.tensors;
   for (size_t k = 0; k < m->g.ops.size(); ++k) {
@@ -950,11 +1108,12 @@ aih_model *aih_model_load_ex(const void *bytes, size_t len, uint32_t n, int32_t 
     alloc_tensors(m.get());
     if (flags & AIH_MODEL_TUNE) tune_blocks(m.get());
     find_stem_input(m.get());
-    lower(m.get());
-    if (m->ws_bytes) m->ws = m->dalloc(m->ws_bytes);
     for (uint32_t t : m->g.inputs)
       m->staging_floats = std::max(m->staging_floats, (size_t)n * m->g.tensors[t].h * m->g.tensors[t].w * m->g.tensors[t].c);
     if (m->staging_floats) m->staging = static_cast<float *>(m->dalloc(m->staging_floats * 4));
+    lower(m.get());
+    if (m->ws_bytes) m->ws = m->dalloc(m->ws_bytes);
+    fuse_stem_launch(m.get());
     out = m.release();
     return AIH_OK;
   });

@@ -68,7 +68,8 @@ def _to_device(a: np.ndarray, device) -> torch.Tensor:
 @dataclass
 class ModelOp:
     """One launch of the graph: a single conv ("conv"), a fused block
-    ("ir_block") or a fused depthwise + pointwise pair ("dw_pw")."""
+    ("ir_block"), a fused depthwise + pointwise pair ("dw_pw") or the stem
+    conv fused into the block after it ("stem_ir_block")."""
 
     name: str
     kind: str
@@ -95,6 +96,16 @@ class ModelOp:
             r = y if p.res else 0
             w = (d.k * d.k * d.cout + p.cin * p.cout) * w_bytes + (d.cout + p.cout) * act_bytes
             return x + y + r + w
+        if self.kind == "stem_ir_block":
+            # the fp32 image in, the block's output out, weights once: the
+            # stem's output (the block's input and residual) is never stored
+            S, e, d, p = self.layers
+            oh, ow = p.out_hw()
+            x = n * S.ih * S.iw * S.cin * 4
+            y = n * oh * ow * p.cout * act_bytes
+            w = (S.k * S.k * S.cin * S.cout + e.cin * e.cout + d.k * d.k * d.cout + p.cin * p.cout) * w_bytes
+            b = (S.cout + e.cout + d.cout + p.cout) * act_bytes
+            return x + y + w + b
         e, d, p = self.layers
         oh, ow = p.out_hw()
         x = n * e.ih * e.iw * c4(e.cin) * act_bytes
@@ -116,6 +127,10 @@ class Model:
     WAVE_TILES = [(4, 8), (8, 4), (5, 6), (6, 5), (2, 16), (16, 2), (3, 10)]
     SPLIT_WAVES = [2, 4, 8]
     WAVE_WAVES = [4, 8, 12]  # wave-kernel workgroup sizes (12: the shapes that allow it)
+    # a block's label with this prefix: the stem conv before it fused into its
+    # launch (aih_ir_block_stem), the rest naming the block's wave-kernel plan
+    STEM_PREFIX = "stem+"
+    STEM_WAVES = [4, 8]
 
     def __init__(self, layers: list[Layer], weights: Weights, n: int, ih: int, iw: int, cin: int,
                  dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0",
@@ -173,6 +188,8 @@ class Model:
         self._x_version = 0       # its version counter at the upload
         self._input_packed = True  # tensors["input"] holds the last upload
         self._stem_in = self._stem_input_op(layers, readers, packed, L)
+        # the stem fused into the block after it: op 0 reads the fp32 upload
+        self._stem_fused = self._fuse_stem(layers, readers, packed, L, tune, choices)
 
     # ------------------------------------------------------------ graph building
 
@@ -264,6 +281,8 @@ class Model:
         rows per wavefront)."""
         if label == "unfused":
             return None
+        if label.startswith(Model.STEM_PREFIX):  # the block fused with the stem before it: the block's part
+            label = label[len(Model.STEM_PREFIX):]
         m = re.fullmatch(r"dwpw (\d+)x(\d+) r([24])", label)
         if m:
             return "dwpw", (int(m.group(1)), int(m.group(2))), None, int(m.group(3))
@@ -307,7 +326,7 @@ class Model:
         planned = self.label_of(pl.kernel, pl.th, pl.tw, pl.resident, pl.waves)
         if kernel == conv.IrKernel.WAVE and not waves:
             planned = planned.rsplit(" w", 1)[0]  # a label without a count takes the plan's
-        if planned != label:
+        if planned != label.removeprefix(self.STEM_PREFIX):
             raise conv.AihError(f"{self._block_name(p)}: {label!r} planned as "
                                 f"{self.label_of(pl.kernel, pl.th, pl.tw, pl.resident, pl.waves)!r}")
         return [self._fused_op((e, d, p, sp), packed, L)]
@@ -426,6 +445,84 @@ class Model:
                 y.data_ptr())
         return ModelOp(Lr.name, "conv", [Lr], L.aih_conv_stem_f32in, args, spec, [desc, wd, bd])
 
+    def _stem_block_op(self, blk, sp: conv.StemIrBlockSpec, packed, L, y, image=None) -> ModelOp:
+        """The stem conv (op 0) and the block after it (blk) as one
+        aih_ir_block_stem launch reading the fp32 image."""
+        S = self._stem_in.layers[0]
+        e, d, p = blk.layers
+        self.tensors[p.name] = y
+        sd, bd = sp.stem.desc(), sp.block.desc()
+        args = (C.byref(sd), C.byref(bd), image.data_ptr() if image is not None else None,
+                packed[S.name][0].data_ptr(), packed[S.name][1].data_ptr()) + tuple(
+            packed[nm][k].data_ptr() for nm in (e.name, d.name, p.name) for k in (0, 1)) + (y.data_ptr(),)
+        keep = [sd, bd] + [t for nm in (S.name, e.name, d.name, p.name) for t in packed[nm]]
+        return ModelOp(f"{S.name}+{blk.name}", "stem_ir_block", [S, e, d, p], L.aih_ir_block_stem, args, sp, keep)
+
+    def _fuse_stem(self, layers, readers, packed, L, tune: bool, choices) -> bool:
+        """Fuses the stem conv (op 0, on the fp32 input) into the
+        inverted-residual block after it when that block reads the stem's
+        output as its input and residual and nothing else does: recorded
+        choices fuse it where the block's label carries STEM_PREFIX; the
+        tuner times the stem + the chosen block against the fused launch at
+        the planner's and the WAVE_TILES tiles, resident and streamed
+        weights, the planner's or STEM_WAVES wavefronts, and keeps the
+        faster. The stem's output is then never stored."""
+        if self._stem_in is None or len(self.ops) < 2 or self.ops[1].kind != "ir_block":
+            return False
+        S, blk = layers[0], self.ops[1]
+        e, d, p = blk.layers
+        if e.src != S.name or p.res != S.name or readers.get(S.name, 0) != 2 or self.output == S.name:
+            return False
+        name = self._block_name(p)
+        y = self.tensors[p.name]
+        K, Wt = conv.IrKernel, conv.IrWeights
+        if choices is not None:
+            label = self.choices.get(name, ("", 0.0))[0]
+            if not label.startswith(self.STEM_PREFIX):
+                return False
+            _, tile, w, waves = self.parse_label(label)
+            sp = conv.StemIrBlockSpec(self._stem_in.spec,
+                                      dataclasses.replace(blk.spec, tile=tile, weights=w, kernel=K.WAVE, waves=waves))
+            if not sp.fusable():
+                raise conv.AihError(f"{name}: {label!r}: {conv.last_error()}")
+            self.ops[0:2] = [self._stem_block_op(blk, sp, packed, L, y)]
+            self.tensors.pop(S.name, None)
+            return True
+        if not tune:
+            return False
+        # time on a stand-in image (the stem's input slot is the caller's tensor)
+        xt = torch.zeros(self.n * self.ih * self.iw * self.cin, dtype=torch.float32, device=self.device)
+        a0 = self._stem_in.args
+        self._stem_in.args = (a0[0], xt.data_ptr()) + a0[2:]
+        best_us, best_label, best_op = self._time_ops([self._stem_in, blk]), None, None
+        seen = set()
+        for tile in [(0, 0)] + self.WAVE_TILES:
+            for w in (Wt.RESIDENT, Wt.STREAMED):
+                for waves in [0] + self.STEM_WAVES:
+                    sp = conv.StemIrBlockSpec(self._stem_in.spec, dataclasses.replace(
+                        blk.spec, tile=tile, weights=w, kernel=K.WAVE, waves=waves))
+                    if not sp.fusable():
+                        continue
+                    pl = sp.plan()
+                    if (pl.th, pl.tw, pl.resident, pl.waves) in seen:
+                        continue
+                    seen.add((pl.th, pl.tw, pl.resident, pl.waves))
+                    op = self._stem_block_op(blk, sp, packed, L, y, image=xt)
+                    us = self._time_ops([op])
+                    if us < best_us:
+                        best_us, best_op = us, op
+                        best_label = self.STEM_PREFIX + self.label_of(K.WAVE, pl.th, pl.tw, pl.resident, pl.waves)
+        self._stem_in.args = a0
+        self.tensors[p.name] = y
+        if best_op is None:
+            return False
+        a = best_op.args
+        best_op.args = a[:2] + (None,) + a[3:]
+        self.choices[name] = (best_label, best_us)
+        self.ops[0:2] = [best_op]
+        self.tensors.pop(S.name, None)
+        return True
+
     def _alloc(self, h: int, w: int, c: int) -> torch.Tensor:
         return torch.empty(self.n * h * w * (-(-c // 4)) * 4, dtype=_storage_torch(self.dt), device=self.device)
 
@@ -454,6 +551,9 @@ class Model:
         self._input_packed = False
         a = self._stem_in.args
         self._stem_in.args = (a[0], x.data_ptr()) + a[2:]
+        if self._stem_fused:
+            f = self.ops[0].args
+            self.ops[0].args = f[:2] + (x.data_ptr(),) + f[3:]
 
     def sync_input(self):
         """Fills tensors["input"] with the last upload when the stem read the
@@ -466,12 +566,16 @@ class Model:
 
     def _op(self, i: int) -> ModelOp:
         # op 0 reads the fp32 upload while it has not been packed into the
-        # input slot; otherwise (no upload yet, or the slot written) the slot
-        if i == 0 and self._stem_in is not None and not self._input_packed:
+        # input slot; otherwise (no upload yet, or the slot written) the slot.
+        # A stem fused into the block after it always reads the upload.
+        if i == 0 and self._stem_in is not None and (self._stem_fused or not self._input_packed):
+            if self._x_f32 is None:
+                raise conv.AihError("infer: the stem fused into the first block reads the fp32 upload: "
+                                    "call upload_input first")
             if self._x_f32._version != self._x_version:
                 raise conv.AihError("infer: the tensor given to upload_input was modified in place after the "
                                     "upload; call upload_input again")
-            return self._stem_in
+            return self.ops[0] if self._stem_fused else self._stem_in
         return self.ops[i]
 
     def infer(self, stream=None):
@@ -492,6 +596,8 @@ class Model:
         h, w, c = self.shapes[name]
         if name == "input":
             self.sync_input()
+        if name not in self.tensors:
+            raise conv.AihError(f"read_output: {name!r} is an intermediate of a fused launch and is not stored")
         a = self.tensors[name].detach().cpu().numpy()
         if a.dtype == np.int16:
             a = a.view(np.uint16)

@@ -166,7 +166,7 @@ def main() -> int:
         key = kernel_key(conv, op, n, DT[args.dtype], args.dtype)
         g = groups.setdefault(key, dict(launches=0, secs=0.0, flops=0, bytes=0, grids=[]))
         g["launches"] += 1
-        if op.kind == "ir_block":
+        if op.kind in ("ir_block", "stem_ir_block"):
             pl = op.spec.plan()
             # dispatch size in threads, as rocprofv3 lists it
             g["grids"].append(pl.grid * 64 * pl.waves)
@@ -368,6 +368,8 @@ def measured_traffic(key: str):
 def kernel_key(conv, op, n, dt, dtname) -> str:
     """Name of the kernel instantiation one model op launches (as the kernel
     trace names it for the fused block; descriptive for the conv kernels)."""
+    if op.kind == "stem_ir_block":
+        return f"ir_wave_stem_kernel<{int(dt)}>"
     if op.kind == "ir_block":
         p = op.spec.plan()
         if p.kernel in (conv.IrKernel.WAVE, conv.IrKernel.SPLIT):
@@ -579,7 +581,7 @@ def real_model(torch, conv, dev, stream) -> dict:
         out[key] = dict(us=round(t * 1e6, 1), frames_per_s=round(n / t, 1), tflops=round(2 * macs * n / t / 1e12, 2),
                         gflop_per_frame=round(2 * macs / 1e9, 3), ops=len(g["ops"]), launches=m.info.n_launches,
                         fused_blocks=[f"ops {f.first_op}-{f.first_op + f.n_ops - 1}: "
-                                      f"{f.plan if f.n_ops == 3 else f.dwpw}" for f in m.fused_blocks()])
+                                      f"{f.dwpw if f.n_ops == 2 else f.plan}" for f in m.fused_blocks()])
         log(f"real segm model {dt} b{n} {'fused' if fuse else 'unfused'}: {t * 1e3:.3f} ms {n / t:.0f} frames/s "
             f"({m.info.n_launches} launches)")
         m.close()

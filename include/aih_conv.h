@@ -358,6 +358,28 @@ int aih_pack_nhwc_device(const float *x, uint32_t n, uint32_t h, uint32_t w, uin
 int aih_conv_stem_f32in(const aih_igemm_desc *d, const float *x, const void *w, const void *bias,
                         const void *res, void *y, aih_stream stream);
 
+/* The stem conv fused into the inverted-residual block that reads its output
+ * as input and residual: one launch in place of aih_conv_stem_f32in followed
+ * by aih_ir_block (the reference dispatches the stem conv and the block's
+ * three convs separately, lowering.rs:122-168; no counterpart op). For each
+ * halo pixel of a block tile the launch computes the stem's output from the
+ * logical NHWC fp32 image with the stem kernel's operands, MFMA steps, bias,
+ * activation and rounding -- what aih_conv_stem_f32in would store, bit for
+ * bit -- and runs the block on it; the stem's output is never stored, so y
+ * equals the two calls' result bit for bit. stem: on aih_conv_stem_f32in's
+ * route with cin = 3, cout = 32, no residual, a clamp-type activation (none,
+ * ReLU, ReLU6, clamp01), image below 2 GiB; blk: 32 -> cexp -> 32 with a
+ * stride-1 depthwise, ReLU after the expand and the depthwise, residual = 1
+ * (the block's input: the stem's output), ih x iw = the stem's output size,
+ * the same n, dt = f16 or bf16 in both (weights in it), kernel AUTO or WAVE
+ * (the wave kernel runs it; tile_h / tile_w / weights / waves as for
+ * aih_ir_block, waves 2 / 4 / 8). */
+int aih_ir_block_stem_plan(const aih_igemm_desc *stem, const aih_ir_block_desc *blk, aih_ir_plan *out);
+int aih_ir_block_stem(const aih_igemm_desc *stem, const aih_ir_block_desc *blk, const float *image,
+                      const void *w_stem, const void *b_stem, const void *w_expand, const void *b_expand,
+                      const void *w_dw, const void *b_dw, const void *w_project, const void *b_project, void *y,
+                      aih_stream stream);
+
 /* ---- errors / info ---- */
 const char *aih_last_error(void);
 const char *aih_version(void);

@@ -126,6 +126,11 @@ aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt)
  * consecutive in the file's op order, whose two intermediate tensors no other
  * op, alias, graph output or state uses, and that aih_ir_block_plan accepts
  * (the plan's deterministic choice of kernel, tile and weight placement).
+ * A stem conv reading the graph's fp32 input (the route of
+ * aih_conv_stem_f32in) whose output only the next fused block reads, as its
+ * input and residual, joins that block's launch (aih_ir_block_stem, where it
+ * plans) when the input is uploaded (staged); an input written into its slot
+ * instead runs the stem and the block as two launches.
  * Elsewhere, a 3x3 depthwise and the 1x1 conv after it that alone reads its
  * output run as one aih_conv_dwpw launch when its plan has a tile for every
  * CU (weights in the activation dtype). The intermediates are then never stored:
@@ -135,8 +140,10 @@ aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt)
  * conv's arithmetic and rounding points. AIH_MODEL_NO_FUSE lowers every op on
  * its own. AIH_MODEL_TUNE times each fused inverted-residual block's launch
  * options at load (the plan's choice; the wave, split and tile kernels at a
- * set of forced tiles, weight placements and wavefront counts; a few
- * launches each on the model's own buffers) and keeps the fastest, as the
+ * set of forced tiles, weight placements and wavefront counts; for a stem
+ * joined to its block, the two launches against the joined one at those
+ * tiles; a few launches each on the model's own buffers) and keeps the
+ * fastest, as the
  * reference's Model::load does its per-model device work once
  * (model.rs:56-366); aih_model_fused_block reports the choice. */
 enum aih_model_flags { AIH_MODEL_NO_FUSE = 1, AIH_MODEL_TUNE = 2 };
@@ -178,7 +185,7 @@ int aih_model_tensor(const aih_model *m, const char *name, aih_tensor_info *out)
 
 typedef struct {
   uint32_t n_tensors, n_ops, n_inputs, n_outputs;
-  uint32_t n_launches; /* kernel launches of one aih_model_infer: ops, less n_ops - 1 per fused block */
+  uint32_t n_launches; /* kernel launches of one aih_model_infer from a staged upload: ops, less n_ops - 1 per fused block */
   uint32_t n_fused;    /* fused blocks (inverted-residual blocks and depthwise -> pointwise pairs) */
   int32_t dt, wdt;
   size_t device_bytes; /* weights + tensors + workspace */
@@ -187,8 +194,9 @@ int aih_model_get_info(const aih_model *m, aih_model_info *out);
 
 /* Fused block i (0 <= i < n_fused): its first op and op count (it covers
  * ops first_op .. first_op + n_ops - 1); for an inverted-residual block
- * (n_ops 3) the plan aih_ir_block runs it with, for a depthwise -> pointwise
- * pair (n_ops 2) the plan of aih_conv_dwpw. */
+ * (n_ops 3) the plan aih_ir_block runs it with, for the stem conv fused into
+ * the block after it (n_ops 4) the plan of aih_ir_block_stem, for a
+ * depthwise -> pointwise pair (n_ops 2) the plan of aih_conv_dwpw. */
 typedef struct {
   uint32_t first_op;
   uint32_t n_ops;

@@ -205,7 +205,7 @@ def _check_fused(m, fuse):
 
 def _launch_steps(m, graph):
     """(first op, last op + 1) of each launch the model makes: one op, or a
-    fused block's two or three."""
+    fused block's two, three or four."""
     firsts = {f.first_op: f.n_ops for f in m.fused_blocks()}
     k, out = 0, []
     while k < len(graph.g["ops"]):
@@ -477,10 +477,12 @@ def test_fusion_needs_single_readers(orc):
 def test_encoder_through_the_native_loader_tuned(dt):
     """The headline encoder written as the converter's .sw and loaded by
     aih_model_load_ex with AIH_MODEL_TUNE (each fused block's launch options
-    timed at load): all ten inverted-residual blocks fuse, the stem reads the
-    staged fp32 upload, and the output equals bit for bit that of the op-level
-    Model (ai_engine_amd.model) told to run the same kernels -- whose launches
-    the oracle checks in test_gpu_workloads / test_gpu_ir_tiles. Batch 8."""
+    timed at load): all ten inverted-residual blocks fuse, the first one with
+    the stem conv before it where the timing picks that (the stem reading the
+    staged fp32 upload either way), and the output equals bit for bit that of
+    the op-level Model (ai_engine_amd.model) told to run the same kernels --
+    whose launches the oracle checks in test_gpu_workloads / test_gpu_ir_tiles
+    / test_gpu_ir_stem. Batch 8."""
     from ai_engine_amd import workloads as W
     from ai_engine_amd.model import Model
 
@@ -491,8 +493,10 @@ def test_encoder_through_the_native_loader_tuned(dt):
     x = torch.from_numpy(rnd(91, n, meta["h"], meta["w"], 3)).cuda()
     m = sw.SwModel(data, n=n, dt=conv.DType(dt), tune=True)
     blocks = m.fused_blocks()
-    assert [f.n_ops for f in blocks] == [3] * 10 and m.info.n_launches == 12
-    choices = {f"b{i}": Model.label_of(f.plan.kernel, f.plan.th, f.plan.tw, bool(f.plan.resident), f.plan.waves)
+    ns = [f.n_ops for f in blocks]
+    assert ns[1:] == [3] * 9 and ns[0] in (3, 4) and m.info.n_launches == 15 - ns[0], (ns, m.info.n_launches)
+    choices = {f"b{i}": (Model.STEM_PREFIX if f.n_ops == 4 else "")
+               + Model.label_of(f.plan.kernel, f.plan.th, f.plan.tw, bool(f.plan.resident), f.plan.waves)
                for i, f in enumerate(blocks)}
     print(f"native tuned choices dt{dt}: {choices}", flush=True)
     m.upload_input("input", x)
