@@ -43,6 +43,14 @@ __host__ __device__ constexpr int stem_slot_tap(int h, int i) {
   return t[h][i];
 }
 
+// The accumulator of a 32x32 block starting at the bias: lane (pixel, half
+// lh) holds channels 8q + 4lh .. + 3 in elements 4q .. 4q + 3, b[q] those
+// channels' bias.
+__device__ __forceinline__ f32x16 stem_acc_init(const f32x4 (&b)[4]) {
+  return f32x16{b[0].x, b[0].y, b[0].z, b[0].w, b[1].x, b[1].y, b[1].z, b[1].w,
+                b[2].x, b[2].y, b[2].z, b[2].w, b[3].x, b[3].y, b[3].z, b[3].w};
+}
+
 // A operand of output channel o (lane row), lane half lh, step s: K =
 // s*16 + lh*8 + j, j < 4 the channels (ic 3 zero) of tap stem_slot_tap(lh,
 // 2s), j >= 4 those of stem_slot_tap(lh, 2s + 1), from the packed weights:

@@ -11,8 +11,9 @@
 // tap (the 4th channel zero), the two lane halves holding different taps, 3
 // MFMAs (K 16 each) per block and 5 input loads per lane instead of 9. The
 // weights sit in registers for the whole launch. The epilogue is
-// act(acc + bias) in the MFMA layout, then through LDS rows (+ residual) to
-// stores of whole pixel rows.
+// act(acc + bias) in the MFMA layout (16-bit: the bias is the MFMAs' first
+// accumulator), then through LDS rows (+ residual) to stores of whole pixel
+// rows.
 //
 // Every wavefront walks a contiguous run of 32-pixel blocks, the next two
 // blocks' input pixels in flight while the current one computes;
@@ -196,9 +197,16 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
       else asm volatile("" : "+v"(th[i])::"memory");
     }
     load_taps(blk + 2, raw);
+    // 16-bit: the bias is the MFMAs' first accumulator (as in the stem fused
+    // into the block after it, ir_wave_impl.h); fp32: added after the sum
     f32x16 acc[NOB];
 #pragma unroll
-    for (int ob = 0; ob < NOB; ++ob) acc[ob] = f32x16{};
+    for (int ob = 0; ob < NOB; ++ob) {
+      if constexpr (F32)
+        acc[ob] = f32x16{};
+      else
+        acc[ob] = stem_acc_init(bias[ob]);
+    }
     if constexpr (F32) {
       // lane half lh feeds K = 2s + lh: even K for lh = 0, odd for lh = 1
 #pragma unroll
@@ -234,7 +242,8 @@ __global__ __launch_bounds__(256) void conv_stem_kernel(StemArgs a) {
     for (int ob = 0; ob < NOB; ++ob) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const f32x4 o = f32x4{acc[ob][4 * q], acc[ob][4 * q + 1], acc[ob][4 * q + 2], acc[ob][4 * q + 3]} + bias[ob][q];
+        f32x4 o = f32x4{acc[ob][4 * q], acc[ob][4 * q + 1], acc[ob][4 * q + 2], acc[ob][4 * q + 3]};
+        if constexpr (F32) o += bias[ob][q];
         f32x4 r;
         if constexpr (CL)
           r = f32x4{act_clamp_any(actp, o.x), act_clamp_any(actp, o.y), act_clamp_any(actp, o.z), act_clamp_any(actp, o.w)};

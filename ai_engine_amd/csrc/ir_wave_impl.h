@@ -415,7 +415,7 @@ __device__ __forceinline__ void ir_wave_body(const IrWaveArgs &a) {
       } else {
         // the stem at block input pixel (iy, ix): its 5 input-pixel slots of
         // this lane half (zeros outside the image, or for a halo pixel
-        // outside the block's input), 3 MFMAs, act(acc + bias), rounded
+        // outside the block's input), 3 MFMAs from the bias, act, rounded
         const int32_t sy0 = iy * (int32_t)a.SS - a.SPT, sx0 = ix * (int32_t)a.SS - a.SPL;
         const uint32_t v0 = ((uint32_t)img * a.SIH + (uint32_t)sy0) * a.SIW + (uint32_t)sx0;
         u32x2 th[6];
@@ -431,7 +431,12 @@ __device__ __forceinline__ void ir_wave_body(const IrWaveArgs &a) {
           th[i] = pack4<DT>(f32x4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), 0.0f});
         }
         th[5] = u32x2{0u, 0u};
-        f32x16 sa = {};
+        // the accumulator starts at the bias, as in the stem kernel (the same
+        // fp32 sums)
+        const char *sbl = lds + a.lds_stem + 3 * 64 * 16 + lh * 16;
+        const f32x4 sbias[4] = {*reinterpret_cast<const f32x4 *>(sbl), *reinterpret_cast<const f32x4 *>(sbl + 32),
+                                *reinterpret_cast<const f32x4 *>(sbl + 64), *reinterpret_cast<const f32x4 *>(sbl + 96)};
+        f32x16 sa = stem_acc_init(sbias);
 #pragma unroll
         for (int s = 0; s < 3; ++s)
           sa = ir_mma<DT>(*reinterpret_cast<const u32x4 *>(lds + a.lds_stem + (s * 64 + lane) * 16),
@@ -440,8 +445,7 @@ __device__ __forceinline__ void ir_wave_body(const IrWaveArgs &a) {
         u32x2 h[4];
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-          const f32x4 o = f32x4{sa[4 * qq], sa[4 * qq + 1], sa[4 * qq + 2], sa[4 * qq + 3]} +
-                          *reinterpret_cast<const f32x4 *>(lds + a.lds_stem + 3 * 64 * 16 + (8 * qq + 4 * lh) * 4);
+          const f32x4 o = f32x4{sa[4 * qq], sa[4 * qq + 1], sa[4 * qq + 2], sa[4 * qq + 3]};
           const u32x2 p = pack4<DT>(f32x4{act_clamp_any(act_s, o.x), act_clamp_any(act_s, o.y),
                                           act_clamp_any(act_s, o.z), act_clamp_any(act_s, o.w)});
           h[qq] = in ? p : u32x2{0u, 0u};
