@@ -644,6 +644,7 @@ aih::IrWaveArgs wave_args(const aih_ir_block_desc *d, uint32_t oh, uint32_t ow, 
   a.lds_x = wp.lds_x;
   a.lds_stem = wp.lds_stem;
   a.lds_res = wp.lds_res;
+  a.lds_next = wp.lds_next;
   a.fd_hw = aih::make_fastdiv(wp.HW);
   a.fd_tw = aih::make_fastdiv(wp.TW);
   a.fd_tx = aih::make_fastdiv(wp.tiles_x);

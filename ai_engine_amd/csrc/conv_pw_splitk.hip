@@ -10,7 +10,8 @@
 // wavefronts split K: wave w runs K steps [w*spw, (w+1)*spw) on MFMA with
 // its operands loaded straight from memory into registers (16-byte loads),
 // then writes its 16x16 fp32 partial to LDS; after one barrier wavefront 0
-// sums the W partials in wave order (a fixed order: the result does not
+// (whose bias and residual loads went out with its K operands) sums the W
+// partials in wave order (a fixed order: the result does not
 // depend on timing) and applies act(acc + bias) (+ residual)
 // (common/epilogue.rs:13-30). 16x16 blocks rather than 32x32 give 4x more
 // workgroups, so a 180-pixel layer spreads over 120 CUs instead of 30.
@@ -49,6 +50,15 @@ __global__ __launch_bounds__(64 * W) void pw_splitk_kernel(PwSplitkArgs a) {
   const size_t xrow = (size_t)(pv ? p : 0) * a.KG;
   const uint32_t s0 = wave * a.spw;
   const uint32_t s1 = s0 + a.spw < a.steps ? s0 + a.spw : a.steps;
+  // the epilogue's operands (wavefront 0): loaded with the K operands, so the
+  // launch waits on memory once, not again after the reduction
+  const uint32_t c0 = nb * 16 + 4 * q;
+  const size_t vi = (size_t)p * (a.N4 / 4) + c0 / 4;
+  f32x4 bv = {0.0f, 0.0f, 0.0f, 0.0f}, rv = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (wave == 0) {
+    bv = Vec4IO<DT>::load(a.bias, c0 / 4);
+    if (a.has_res && pv) rv = Vec4IO<DT>::load(a.res, vi);
+  }
 
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   for (uint32_t sb = s0; sb < s1; sb += kSplitkBatch) {
@@ -102,11 +112,9 @@ __global__ __launch_bounds__(64 * W) void pw_splitk_kernel(PwSplitkArgs a) {
     for (int w = 1; w < W; ++w) acc += part[w][lane];
   }
   if (!pv) return;
-  const uint32_t c0 = nb * 16 + 4 * q;
-  f32x4 o = acc + Vec4IO<DT>::load(a.bias, c0 / 4);
+  f32x4 o = acc + bv;
   o = act4(act_params(a.act), o);
-  const size_t vi = (size_t)p * (a.N4 / 4) + c0 / 4;
-  if (a.has_res) o += Vec4IO<DT>::load(a.res, vi);
+  if (a.has_res) o += rv;
   Vec4IO<DT>::store(a.y, vi, o);
 }
 

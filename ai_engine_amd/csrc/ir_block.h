@@ -113,6 +113,7 @@ struct IrWaveArgs {
   uint32_t SIH, SIW, SS, sx_bytes; // image size, stem stride, bytes of sx
   int32_t SPT, SPL, act_s;         // stem padding (top, left), activation (clamp-type)
   uint32_t lds_stem, lds_res;      // LDS: stem A operands + fp32 bias; per-wavefront residual stashes
+  uint32_t lds_next;               // wave kernel, resident weights: the workgroup's next-tile counter (16 bytes)
 };
 
 // LDS of the stem-fused launch beyond the block's own: the stem's A operands
@@ -142,6 +143,7 @@ struct IrWavePlan {
   uint32_t tiles_y, tiles_x, ntiles;
   uint32_t lds_w, lds_bp, lds_xe, lds_red, lds_x, lds;  // LDS byte offsets and total
   uint32_t lds_stem, lds_res;           // stem-fused launch: stem tables, residual stashes
+  uint32_t lds_next;                    // wave kernel, resident weights: next-tile counter
   uint32_t occ, grid;                   // workgroups per CU, launched workgroups
 };
 

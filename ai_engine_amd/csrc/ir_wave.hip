@@ -171,6 +171,10 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
             p.lds_res = p.lds_stem + IRW_STEM_LDS;
             p.lds = p.lds_res + waves * IRW_RES_STASH;
           }
+          if (resident) {
+            p.lds_next = p.lds;
+            p.lds += 16;
+          }
           if (p.lds > 160u * 1024u) continue;
           p.occ = (uint32_t)irw_occupancy(stem ? 3 : 0, dt, ke, npi, nob, rl, waves, p.lds);
           if (p.occ == 0) continue;  // not resident at this size

@@ -366,13 +366,16 @@ __device__ __forceinline__ void ir_wave_body(const IrWaveArgs &a) {
       *reinterpret_cast<f32x4 *>(lds + a.lds_stem + 3 * 64 * 16 + g * 16) = Vec4IO<DT>::load(a.sb, g);
     }
   }
-  ir_dma_wait();
-  __syncthreads();
-
   // this workgroup's contiguous range of tiles (handed out XCD by XCD)
   const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x, a.nxcd);
   const uint32_t t_begin = (uint32_t)(((uint64_t)blk * a.ntiles) / gridDim.x);
   const uint32_t t_end = (uint32_t)(((uint64_t)(blk + 1) * a.ntiles) / gridDim.x);
+  // resident weights: after its first tile a wavefront claims the range's
+  // next unclaimed tile from this counter
+  uint32_t *next_tile = reinterpret_cast<uint32_t *>(lds + a.lds_next);
+  if (a.resident && tid == 0) *next_tile = t_begin + nwaves;
+  ir_dma_wait();
+  __syncthreads();
 
   const char *xg = reinterpret_cast<const char *>(a.x);
   const uint32_t img_bytes = a.IH * a.IW * C * ES;
@@ -526,11 +529,17 @@ __device__ __forceinline__ void ir_wave_body(const IrWaveArgs &a) {
   };
 
   if (a.resident) {
-    // every chunk in LDS: the wavefronts run their tiles independently
-    for (uint32_t T = t_begin + wave; T < t_end; T += nwaves) {
+    // every chunk in LDS: the wavefronts run their tiles independently, each
+    // claiming its next tile while it works on the current one, so the SIMDs
+    // whose wavefronts run ahead take more of the range (a fixed
+    // round-robin left one SIMD of a CU a tile more than the others)
+    for (uint32_t T = t_begin + wave; T < t_end;) {
+      uint32_t nx = 0;
+      if (lane == 0) nx = __hip_atomic_fetch_add(next_tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       begin_tile(T);
       for (uint32_t c = 0; c < nchunks; ++c) run_chunk(WL + c * SLOT);
       irdw_store<DT, NOG, STEM>(a, BpL, acc, ok, pix, q, act_p, ResL, l16);
+      T = __builtin_amdgcn_readfirstlane(nx);
     }
     return;
   }
