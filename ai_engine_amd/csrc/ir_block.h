@@ -149,8 +149,9 @@ struct IrWavePlan {
 
 // Split kernel LDS: the tile's halo (NPI x 32 rows of C channels + 16
 // bytes), per wavefront its expanded chunk and its two-slot ring of
-// depthwise taps and biases; partial sums: NOB blocks of 32 x 32 fp32 per
-// wavefront, over the rest once it is done with.
+// depthwise taps and biases; partial sums: NOB blocks of 32 x 32 fp32 for
+// each of up to four wavefronts (eight add theirs in pairs first), over the
+// rest once it is done with.
 constexpr uint32_t IRS_RING = 2 * IRW_SMB;
 constexpr uint32_t IRS_RED_BLOCK = 32 * 32 * 4;
 

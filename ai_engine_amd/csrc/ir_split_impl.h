@@ -26,9 +26,10 @@
 //     depthwise taps and biases into a private two-slot LDS ring (LDS-direct
 //     loads, completed by the wavefront's own wait);
 //   * each wavefront ends with projection partial sums over its chunks. They
-//     meet in LDS, and the wavefront that owns an output block adds the W
-//     partials in wavefront order (a fixed order: the result does not depend
-//     on timing) before the bias, activation, residual and store.
+//     meet in LDS (with eight wavefronts, 4 + w first added to w, so the
+//     region holds four), and the wavefront that owns an output block adds
+//     them in wavefront order (a fixed order: the result does not depend on
+//     timing) before the bias, activation, residual and store.
 //
 // Projection channels CO..COP (cout not a multiple of 32) read zero weights
 // through the buffer range check and are never stored.
@@ -307,18 +308,40 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
     }
   }
 
-  // ---- partial sums: wavefront w's unit (og, pg) at [w][og][pg][lane] (f32x4) ----
+  // ---- partial sums: slot s's unit (og, pg) at [s][og][pg][lane] (f32x4) ----
   // The region overlaps the halo, the wavefronts' XeL and rings: every
-  // wavefront must be done with them first.
+  // wavefront must be done with them first. At most four slots: with eight
+  // wavefronts, 4..7 first pass theirs to 0..3, which add them to their own
+  // (so the region holds four wavefronts' sums, not eight).
   __syncthreads();
   f32x4 *red = reinterpret_cast<f32x4 *>(lds + a.lds_red);
+  const uint32_t nslot = nw < 4 ? nw : 4;
+  if (nw > 4) {
+    if (wave >= 4) {
 #pragma unroll
-  for (int og = 0; og < NOG; ++og)
+      for (int og = 0; og < NOG; ++og)
 #pragma unroll
-    for (int pg = 0; pg < 2; ++pg) red[((wave * NOG + og) * 2 + pg) * 64 + lane] = acc[og][pg];
+        for (int pg = 0; pg < 2; ++pg) red[(((wave - 4) * NOG + og) * 2 + pg) * 64 + lane] = acc[og][pg];
+    }
+    __syncthreads();
+    if (wave < 4) {
+#pragma unroll
+      for (int og = 0; og < NOG; ++og)
+#pragma unroll
+        for (int pg = 0; pg < 2; ++pg) acc[og][pg] += red[((wave * NOG + og) * 2 + pg) * 64 + lane];
+    }
+    __syncthreads();
+  }
+  if (wave < nslot) {
+#pragma unroll
+    for (int og = 0; og < NOG; ++og)
+#pragma unroll
+      for (int pg = 0; pg < 2; ++pg) red[((wave * NOG + og) * 2 + pg) * 64 + lane] = acc[og][pg];
+  }
   __syncthreads();
-  // unit u = (og, pg) belongs to wavefront u % W: the sum over wavefronts
-  // 0..W-1 in order, then bias -> act -> (+ residual) -> store
+  // unit u = (og, pg) belongs to wavefront u % W: the sum over the slots in
+  // order (a fixed order: the result does not depend on timing), then bias ->
+  // act -> (+ residual) -> store
   for (uint32_t u = wave; u < (uint32_t)(2 * NOG); u += nw) {
     const uint32_t og = u >> 1, pg = u & 1;
     const uint32_t oc = og * 16 + 4 * q;
@@ -327,7 +350,7 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
     const uint32_t pixp = pg ? pix[1] : pix[0];
     if (og * 16 >= a.CO || !okp) continue;  // padding channels of the last block; pixels outside
     f32x4 v = red[((0 * NOG + og) * 2 + pg) * 64 + lane];
-    for (uint32_t w = 1; w < nw; ++w) v += red[((w * NOG + og) * 2 + pg) * 64 + lane];
+    for (uint32_t s = 1; s < nslot; ++s) v += red[((s * NOG + og) * 2 + pg) * 64 + lane];
     v += *reinterpret_cast<const f32x4 *>(BpL + oc);
     float t4[4] = {v.x, v.y, v.z, v.w};
     ir_act<true, 4>(act_p, t4);

@@ -212,7 +212,7 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
         p.lds_xe = p.lds_x + npi * 32 * (C * 2 + 16);
         p.lds_w = p.lds_xe + w * npi * 32 * IRW_XPIX;
         p.lds_red = p.lds_x;
-        p.lds = p.lds_x + std::max(p.lds_w + w * IRS_RING - p.lds_x, w * nob * IRS_RED_BLOCK);
+        p.lds = p.lds_x + std::max(p.lds_w + w * IRS_RING - p.lds_x, std::min(w, 4u) * nob * IRS_RED_BLOCK);
         if (p.lds > 160u * 1024u) continue;
         p.occ = (uint32_t)irw_occupancy(1, dt, ke, npi, nob, rl, w, p.lds);
         if (p.occ == 0) continue;  // not resident at this size
