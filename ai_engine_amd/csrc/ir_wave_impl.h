@@ -384,6 +384,7 @@ __device__ __forceinline__ void ir_wave_body(const IrWaveArgs &a) {
   const __amdgpu_buffer_rsrc_t rs_sx = STEM ? ir_rsrc(a.sx, a.sx_bytes) : ir_rsrc(a.we, 0);
   char *ResL = lds + a.lds_res + (uint32_t)wave * IRW_RES_STASH;
   const Act act_s = act_params(a.act_s);
+
   const uint32_t per_img = a.tiles_y * a.tiles_x;
   const uint32_t HPIX = a.HH * a.HW, TPIX = a.TH * a.TW;
   constexpr uint32_t ONE = DT == DT_F16 ? 0x3C00u : 0x3F80u;
@@ -420,19 +421,40 @@ __device__ __forceinline__ void ir_wave_body(const IrWaveArgs &a) {
         // this lane half (zeros outside the image, or for a halo pixel
         // outside the block's input), 3 MFMAs from the bias, act, rounded
         const int32_t sy0 = iy * (int32_t)a.SS - a.SPT, sx0 = ix * (int32_t)a.SS - a.SPL;
-        const uint32_t v0 = ((uint32_t)img * a.SIH + (uint32_t)sy0) * a.SIW + (uint32_t)sx0;
-        u32x2 th[6];
+        // taps inside the image, bit 3 dy + dx: rows times columns
+        const uint32_t rk = ((uint32_t)sy0 < a.SIH ? 07u : 0u) | ((uint32_t)(sy0 + 1) < a.SIH ? 070u : 0u) |
+                            ((uint32_t)(sy0 + 2) < a.SIH ? 0700u : 0u);
+        const uint32_t ck = ((uint32_t)sx0 < a.SIW ? 0111u : 0u) | ((uint32_t)(sx0 + 1) < a.SIW ? 0222u : 0u) |
+                            ((uint32_t)(sx0 + 2) < a.SIW ? 0444u : 0u);
+        const uint32_t m9 = in ? rk & ck : 0u;
+        // 3 x the pixel index of tap (0, 0) (modulo 2^32 where it lies
+        // outside the image; every tap read lies inside, below 2 GiB): a
+        // tap's byte offset is 4 x that + its wave-uniform offset, shifts and
+        // adds instead of a quarter-rate multiply per tap (the empty asm
+        // keeps the compiler from folding them back into one)
+        const uint32_t vp = ((uint32_t)img * a.SIH + (uint32_t)sy0) * a.SIW + (uint32_t)sx0;
+        uint32_t vp2 = vp << 1;
+        asm volatile("" : "+v"(vp2));
+        const uint32_t vp3 = vp2 + vp;
+        // the five loads go out together, converted after (the scheduler
+        // would otherwise wait for each before issuing the next)
+        typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+        u32x3 sv[5];
 #pragma unroll
         for (int i = 0; i < 5; ++i) {
+          // the slot's tap in either lane half (compile-time), its byte
+          // offset from tap (0, 0) (wave-uniform)
           const int t0 = stem_slot_tap(0, i), t1 = stem_slot_tap(1, i);
-          const int32_t dy = lh ? t1 / 3 : t0 / 3, dx = lh ? t1 % 3 : t0 % 3;
-          const bool tok = lh ? t1 < 9 : t0 < 9;
-          const bool sin = in && tok && (uint32_t)(sy0 + dy) < a.SIH && (uint32_t)(sx0 + dx) < a.SIW;
-          typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-          const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(
-              rs_sx, sin ? (v0 + (uint32_t)(dy * (int32_t)a.SIW + dx)) * 12u : IR_OOB, 0, 0);
-          th[i] = pack4<DT>(f32x4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), 0.0f});
+          const uint32_t so0 = ((uint32_t)(t0 / 3) * a.SIW + (uint32_t)(t0 % 3)) * 12u;
+          const uint32_t so1 = ((uint32_t)(t1 / 3) * a.SIW + (uint32_t)(t1 % 3)) * 12u;
+          const bool tin = lh ? (m9 >> t1) & 1u : (m9 >> t0) & 1u;  // bit 9 (no tap) is 0
+          sv[i] = __builtin_amdgcn_raw_buffer_load_b96(rs_sx, tin ? (vp3 << 2) + (lh ? so1 : so0) : IR_OOB, 0, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        u32x2 th[6];
+#pragma unroll
+        for (int i = 0; i < 5; ++i)
+          th[i] = pack4<DT>(f32x4{__uint_as_float(sv[i].x), __uint_as_float(sv[i].y), __uint_as_float(sv[i].z), 0.0f});
         th[5] = u32x2{0u, 0u};
         // the accumulator starts at the bias, as in the stem kernel (the same
         // fp32 sums)
