@@ -170,6 +170,7 @@ EXPORTS = (
     "aih_ir_block_plan", "aih_ir_block", "aih_last_error", "aih_version", "aih_conv_check", "aih_conv_plan",
     "aih_conv_noalloc", "aih_conv_stem_f32in", "aih_conv_dwpw_plan", "aih_conv_dwpw",
     "aih_ir_block_stem_plan", "aih_ir_block_stem",
+    "aih_ir_block_head_plan", "aih_ir_block_head",
 )
 
 _lib = None
@@ -206,6 +207,8 @@ def lib() -> C.CDLL:
         "aih_ir_block": (C.c_int, [C.POINTER(_IrDesc), P, P, P, P, P, P, P, P, P, P]),
         "aih_ir_block_stem_plan": (C.c_int, [C.POINTER(_IgemmDesc), C.POINTER(_IrDesc), C.POINTER(IrPlan)]),
         "aih_ir_block_stem": (C.c_int, [C.POINTER(_IgemmDesc), C.POINTER(_IrDesc)] + [P] * 11),
+        "aih_ir_block_head_plan": (C.c_int, [C.POINTER(_IrDesc), C.POINTER(_PwDesc), C.POINTER(IrPlan)]),
+        "aih_ir_block_head": (C.c_int, [C.POINTER(_IrDesc), C.POINTER(_PwDesc)] + [P] * 13),
         "aih_conv_dwpw_plan": (C.c_int, [C.POINTER(_DwPwDesc), C.POINTER(DwPwPlan)]),
         "aih_conv_dwpw": (C.c_int, [C.POINTER(_DwPwDesc), P, P, P, P, P, P, P, P]),
         "aih_last_error": (C.c_char_p, []),
@@ -531,6 +534,37 @@ class StemIrBlockSpec:
                                        _ptr(w_stem), _ptr(b_stem), _ptr(w_expand), _ptr(b_expand), _ptr(w_dw),
                                        _ptr(b_dw), _ptr(w_project), _ptr(b_project), _ptr(y), _stream(stream)))
         return y
+
+
+@dataclass
+class IrBlockHeadSpec:
+    """An inverted-residual block (an IrBlockSpec, on the split kernel) joined
+    to the pointwise conv with at most 4 outputs that reads its output -- a
+    GemmPwSpec on the narrow route, e.g. a segmentation head 128 -> 2
+    (aih_ir_block_head): one launch; its head output equals aih_ir_block
+    followed by aih_conv_pw bit for bit, and the block's own output is
+    stored only when y is given. The reference dispatches the block's convs
+    and the head separately (crates/ai-gpu-runtime/src/lowering.rs:122-168)."""
+
+    block: IrBlockSpec
+    head: GemmPwSpec
+
+    def plan(self) -> IrPlan:
+        p = IrPlan()
+        _check(lib().aih_ir_block_head_plan(C.byref(self.block.desc()), C.byref(self.head.desc()), C.byref(p)))
+        return p
+
+    def fusable(self) -> bool:
+        p = IrPlan()
+        return lib().aih_ir_block_head_plan(C.byref(self.block.desc()), C.byref(self.head.desc()), C.byref(p)) == 0
+
+    def run(self, x, w_expand, b_expand, w_dw, b_dw, w_project, b_project, res, y, w_head, b_head, y_head,
+            stream=None):
+        _check(lib().aih_ir_block_head(C.byref(self.block.desc()), C.byref(self.head.desc()), _ptr(x),
+                                       _ptr(w_expand), _ptr(b_expand), _ptr(w_dw), _ptr(b_dw), _ptr(w_project),
+                                       _ptr(b_project), _ptr(res), _ptr(y), _ptr(w_head), _ptr(b_head),
+                                       _ptr(y_head), _stream(stream)))
+        return y_head
 
 
 @dataclass

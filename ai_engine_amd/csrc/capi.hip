@@ -681,6 +681,30 @@ int plan_ir_stem(const aih_igemm_desc *sd, const aih_ir_block_desc *d, uint32_t 
   return stem_args(sd, soh, sow, sa);
 }
 
+// The head-joined block: the block on the split kernel and a pointwise conv
+// on the narrow route (<= 4 outputs, 16 lanes a pixel) reading its output
+// (aih_ir_block_head_plan / _head).
+int plan_ir_head(const aih_ir_block_desc *d, const aih_pw_desc *h, uint32_t *oh, uint32_t *ow, aih::IrWavePlan *wp) {
+  if (!d || !h) return fail("ir_block_head: null descriptor");
+  if (check_ir(d, oh, ow) || check_pw(h)) return AIH_ERR;
+  if (d->dt != AIH_F16 && d->dt != AIH_BF16) return fail("ir_block_head: the block must have f16 or bf16 storage");
+  if (h->dt != d->dt || h->wdt != d->dt) return fail("ir_block_head: the head's dt and wdt must be the block's");
+  if (h->n != d->n || h->m != *oh * *ow || h->kg != d->cout / 4 || h->ng != 1 || h->residual)
+    return fail("ir_block_head: the head must read the block's output (same n and pixels, kg = cout / 4) and "
+                "have at most 4 outputs (ng 1) and no residual");
+  if (pw_route(h) != PW_ROWS || aih::pw_narrow_group(h->kg) != 16)
+    return fail("ir_block_head: the head must be on the narrow route with 16 lanes a pixel (AUTO, splitk 0, "
+                "kg >= 16)");
+  if (d->kernel != AIH_IR_KERNEL_AUTO && d->kernel != AIH_IR_KERNEL_SPLIT)
+    return fail("ir_block_head: the head-joined block runs the split kernel");
+  if (d->ec && d->ec != 32) return fail("ir_block_head: the split kernel walks E in chunks of 32");
+  const char *why = aih::irw_plan(d->n, d->ih, d->iw, *oh, *ow, d->cin, d->cexp, d->cout, d->s, d->dt,
+                                  ir_clamp_acts(d), d->act_expand == AIH_ACT_RELU && d->act_dw == AIH_ACT_RELU,
+                                  d->tile_h, d->tile_w, d->weights, AIH_IR_KERNEL_SPLIT, d->waves, wp, false, true);
+  if (why) return fail(std::string("ir_block_head: ") + why);
+  return AIH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1368,6 +1392,55 @@ int aih_conv_stem_f32in(const aih_igemm_desc *d, const float *x, const void *w, 
     sa.y = y;
     const hipError_t e = aih::launch_conv_stem(sa, d->dt, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? AIH_OK : fail(std::string("conv stem launch: ") + hipGetErrorString(e));
+  });
+}
+
+int aih_ir_block_head_plan(const aih_ir_block_desc *blk, const aih_pw_desc *head, aih_ir_plan *out) {
+  return guarded([&] {
+    uint32_t oh, ow;
+    aih::IrWavePlan wp;
+    if (plan_ir_head(blk, head, &oh, &ow, &wp)) return AIH_ERR;
+    if (!out) return fail("null plan");
+    *out = aih_ir_plan{wp.TH, wp.TW, 32, blk->cexp / 32, wp.resident, wp.ntiles, wp.lds, wp.occ, wp.grid,
+                       AIH_IR_KERNEL_SPLIT, wp.waves, wp.deep};
+    return AIH_OK;
+  });
+}
+
+int aih_ir_block_head(const aih_ir_block_desc *blk, const aih_pw_desc *head, const void *x, const void *w_expand,
+                      const void *b_expand, const void *w_dw, const void *b_dw, const void *w_project,
+                      const void *b_project, const void *res, void *y, const void *w_head, const void *b_head,
+                      void *y_head, aih_stream stream) {
+  return guarded([&] {
+    uint32_t oh, ow;
+    aih::IrWavePlan wp;
+    if (plan_ir_head(blk, head, &oh, &ow, &wp)) return AIH_ERR;
+    if (!x || !w_expand || !b_expand || !w_dw || !b_dw || !w_project || !b_project || !w_head || !b_head || !y_head)
+      return fail("ir_block_head: null buffer");
+    if ((blk->residual != 0) != (res != nullptr)) return fail("ir_block_head: res must be given iff residual");
+    for (const void *p : {x, w_expand, w_dw, w_project, w_head, (const void *)y_head})
+      if (!aligned(p, 16)) return fail("ir_block_head: misaligned buffer (x, y, y_head and weights need 16 bytes)");
+    if (y && !aligned(y, 16)) return fail("ir_block_head: misaligned buffer (x, y, y_head and weights need 16 bytes)");
+    for (const void *p : {b_expand, b_dw, b_project, b_head})
+      if (!aligned(p, 8)) return fail("ir_block_head: misaligned bias (8 bytes)");
+    if (res && !aligned(res, 16)) return fail("ir_block_head: misaligned residual (16 bytes)");
+    aih::IrWaveArgs a = wave_args(blk, oh, ow, wp);
+    a.x = x;
+    a.we = w_expand;
+    a.be = b_expand;
+    a.wd = w_dw;
+    a.bd = b_dw;
+    a.wp = w_project;
+    a.bp = b_project;
+    a.res = res;
+    a.y = y;
+    a.hw = w_head;
+    a.hb = b_head;
+    a.hy = y_head;
+    a.act_h = head->act;
+    a.lds_head = wp.lds_head;
+    const hipError_t e = aih::launch_ir_wave(a, blk->dt, wp, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? AIH_OK : fail(std::string("ir_block_head launch: ") + hipGetErrorString(e));
   });
 }
 

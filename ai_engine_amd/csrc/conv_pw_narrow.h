@@ -4,7 +4,26 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "aih_device.h"
+
 namespace aih {
+
+// Weight vector vi of the packed narrow weights (one column group: vector
+// (kg, j) -- input channels 4kg..4kg+3 of output channel j -- at kg * 4 + j,
+// pack.rs:95) in fp32.
+template <int DTA, int DTW>
+__device__ __forceinline__ f32x4 narrow_w4(const void *w, size_t vi) {
+  if constexpr (DTW == DT_F32) return reinterpret_cast<const f32x4 *>(w)[vi];
+  else return unpack4<DTW>(reinterpret_cast<const u32x2 *>(w)[vi]);
+}
+
+// One input group's contribution to one output channel: the four products
+// as one fixed chain of fused multiply-adds. Shared by pw_narrow_kernel and
+// the head joined to an inverted-residual block (ir_split_impl.h), so both
+// sum the same products the same way.
+__device__ __forceinline__ float narrow_dot4(const f32x4 &x, const f32x4 &w) {
+  return __builtin_fmaf(x.w, w.w, __builtin_fmaf(x.z, w.z, __builtin_fmaf(x.y, w.y, x.x * w.x)));
+}
 
 struct PwNarrowArgs {
   const void *x, *w, *bias, *res;

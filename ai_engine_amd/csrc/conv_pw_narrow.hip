@@ -22,12 +22,6 @@
 namespace aih {
 namespace {
 
-template <int DTA, int DTW>
-__device__ __forceinline__ f32x4 ld_w4(const void *w, size_t vi) {
-  if constexpr (DTW == DT_F32) return reinterpret_cast<const f32x4 *>(w)[vi];
-  else return unpack4<DTW>(reinterpret_cast<const u32x2 *>(w)[vi]);
-}
-
 // Lanes per pixel G: 16 for at least 16 kg (a 128-channel head takes two
 // steps of 64 channels), 4 for 4-15 kg (24 channels: two steps, the second
 // half full), 1 below.
@@ -50,9 +44,9 @@ __global__ __launch_bounds__(256) void pw_narrow_kernel(PwNarrowArgs a) {
       const f32x4 xv = pv ? xl : f32x4{};
       f32x4 wv[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) wv[j] = ld_w4<DTA, DTW>(a.w, (size_t)kg * 4 + j);
+      for (int j = 0; j < 4; ++j) wv[j] = narrow_w4<DTA, DTW>(a.w, (size_t)kg * 4 + j);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] += xv.x * wv[j].x + xv.y * wv[j].y + xv.z * wv[j].z + xv.w * wv[j].w;
+      for (int j = 0; j < 4; ++j) acc[j] += narrow_dot4(xv, wv[j]);
     }
     // the group's partial sums, added by butterfly (every lane ends with the total)
 #pragma unroll

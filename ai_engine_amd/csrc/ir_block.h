@@ -114,7 +114,18 @@ struct IrWaveArgs {
   int32_t SPT, SPL, act_s;         // stem padding (top, left), activation (clamp-type)
   uint32_t lds_stem, lds_res;      // LDS: stem A operands + fp32 bias; per-wavefront residual stashes
   uint32_t lds_next;               // wave kernel, resident weights: the workgroup's next-tile counter (16 bytes)
+  // split kernel only: a pointwise conv with <= 4 output channels (one
+  // NHWC-C4 vector a pixel) reading the block's output -- the segmentation
+  // head -- joined to it; y may then be null (the block's output not stored)
+  const void *hw, *hb;             // head weights (packed, kg * 4 + j), bias [4]
+  void *hy;                        // head output [N][OH][OW][4], or null: no head
+  int32_t act_h;                   // head activation
+  uint32_t lds_head;               // LDS: the head's per-lane partial sums (IRW_HEAD_LDS bytes)
 };
+
+// LDS of the head joined to a split-kernel block: per 16-pixel group and
+// pixel, the 16 lanes' partial sums of pw_narrow_kernel (four fp32 each).
+constexpr uint32_t IRW_HEAD_LDS = 2 * 16 * 16 * 16;
 
 // LDS of the stem-fused launch beyond the block's own: the stem's A operands
 // (3 MFMA steps x 64 lanes x 16 bytes) and fp32 bias (32 channels), and per
@@ -144,6 +155,7 @@ struct IrWavePlan {
   uint32_t lds_w, lds_bp, lds_xe, lds_red, lds_x, lds;  // LDS byte offsets and total
   uint32_t lds_stem, lds_res;           // stem-fused launch: stem tables, residual stashes
   uint32_t lds_next;                    // wave kernel, resident weights: next-tile counter
+  uint32_t lds_head;                    // split kernel with a joined head: its partial sums
   uint32_t occ, grid;                   // workgroups per CU, launched workgroups
 };
 
@@ -166,10 +178,12 @@ constexpr uint32_t IRS_RED_BLOCK = 32 * 32 * 4;
 // instantiation whose register use bounds the occupancy). stem: the plan of
 // the stem-fused launch (ir_wave_stem_kernel: the wave kernel's 32 -> E -> 32
 // stride-1 shape with ReLU inside, its LDS grown by the stem tables and the
-// wavefronts' residual stashes).
+// wavefronts' residual stashes). head: the split kernel's plan with the
+// joined head's LDS (split plans only).
 const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
                      uint32_t CO, uint32_t S, int dt, bool cl, bool rl, uint32_t tile_h, uint32_t tile_w,
-                     int32_t weights, int32_t kernel, uint32_t waves, IrWavePlan *p, bool stem = false);
+                     int32_t weights, int32_t kernel, uint32_t waves, IrWavePlan *p, bool stem = false,
+                     bool head = false);
 
 hipError_t launch_ir_wave(const IrWaveArgs &a, int dt, const IrWavePlan &p, hipStream_t st);
 hipError_t launch_ir_wave_stem(const IrWaveArgs &a, int dt, const IrWavePlan &p, hipStream_t st);

@@ -35,6 +35,7 @@
 // through the buffer range check and are never stored.
 #pragma once
 
+#include "conv_pw_narrow.h"
 #include "ir_wave_impl.h"
 
 namespace aih {
@@ -62,6 +63,7 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
   const uint32_t c_begin = wave * nchunks / nw, c_end = (wave + 1) * nchunks / nw;
 
   float *BpL = reinterpret_cast<float *>(lds + a.lds_bp);
+  f32x4 *HeadL = reinterpret_cast<f32x4 *>(lds + a.lds_head);
   constexpr uint32_t RPX = C * ES + 16;  // halo row pitch: the pixel's C channels + 16 bytes
   const char *XL = lds + a.lds_x;
   constexpr uint32_t PLANE = NPI * 32 * 16;  // one 8-channel plane of the expanded chunk
@@ -357,7 +359,42 @@ __global__ __launch_bounds__(IRW_THREADS) void ir_split_kernel(IrWaveArgs a) {
     v = f32x4{t4[0], t4[1], t4[2], t4[3]};
     const size_t vi = (size_t)pixp * (a.CO / 4) + oc / 4;
     if (a.has_res) v += Vec4IO<DT>::load(a.res, vi);
-    Vec4IO<DT>::store(a.y, vi, v);
+    if (a.y) Vec4IO<DT>::store(a.y, vi, v);
+    if (a.hy) {
+      // the joined head: pw_narrow_kernel's lane g = kg % 16 of this pixel
+      // sums input groups g, g + 16, ... in that order, starting from 0; this
+      // unit holds group kg = oc / 4 (the same wavefront runs kg + 16 after
+      // kg, units u and u + 8), its four outputs added to lane g's slot. The
+      // inputs are the block's outputs as stored (rounded to DT).
+      const f32x4 xr = unpack4<DT>(pack4<DT>(v));
+      const uint32_t kg = oc / 4;
+      f32x4 *slot = HeadL + (pg * 16 + l16) * 16 + (kg & 15);
+      f32x4 d;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[j] = narrow_dot4(xr, narrow_w4<DT, DT>(a.hw, (size_t)kg * 4 + j));
+      *slot = (kg < 16 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : *slot) + d;
+    }
+  }
+  if (a.hy) {
+    // lane pg * 16 + p of wavefront 0 finishes pixel p of group pg: the
+    // 16 lanes' sums added as pw_narrow_kernel's butterfly leaves them in
+    // its lane 0 (xor 8, 4, 2, 1), then bias -> act -> store
+    __syncthreads();
+    if (wave == 0 && lane < 32) {
+      const uint32_t pg = (uint32_t)lane >> 4;
+      const bool okp = pg ? ok[1] : ok[0];
+      const uint32_t pixp = pg ? pix[1] : pix[0];
+      const f32x4 *P = HeadL + lane * 16;
+      f32x4 s8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s8[i] = P[i] + P[i + 8];
+      const f32x4 t0 = s8[0] + s8[4], t1 = s8[1] + s8[5], t2 = s8[2] + s8[6], t3 = s8[3] + s8[7];
+      const f32x4 acc_h = (t0 + t2) + (t1 + t3);
+      const f32x4 hb = Vec4IO<DT>::load(a.hb, 0);
+      float v[4] = {acc_h.x + hb.x, acc_h.y + hb.y, acc_h.z + hb.z, acc_h.w + hb.w};
+      act_array<4>(act_params(a.act_h), v);
+      if (okp) Vec4IO<DT>::store(a.hy, pixp, f32x4{v[0], v[1], v[2], v[3]});
+    }
   }
 }
 

@@ -63,7 +63,13 @@ double simd_eff(uint32_t n) { return n <= 1 ? 0.45 : n == 2 ? 0.7 : n == 3 ? 0.8
 
 const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t OW, uint32_t C, uint32_t E,
                      uint32_t CO, uint32_t S, int dt, bool cl, bool rl, uint32_t tile_h, uint32_t tile_w,
-                     int32_t weights, int32_t kernel, uint32_t waves_force, IrWavePlan *out, bool stem) {
+                     int32_t weights, int32_t kernel, uint32_t waves_force, IrWavePlan *out, bool stem,
+                     bool head) {
+  if (head) {
+    if (stem) return "a block joins the stem or the head, not both";
+    if (kernel != AIH_IR_KERNEL_AUTO && kernel != AIH_IR_KERNEL_SPLIT) return "the head joins the split kernel";
+    kernel = AIH_IR_KERNEL_SPLIT;
+  }
   if (stem) {
     if (C != 32 || CO != 32 || S != 1) return "the stem-fused block is 32 -> E -> 32 with a stride-1 depthwise";
     if (!rl) return "the stem-fused block takes ReLU after its expand and its depthwise";
@@ -96,13 +102,13 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = -1;
   struct Key {
-    uint32_t v[18];
+    uint32_t v[19];
     bool operator<(const Key &o) const { return std::memcmp(v, o.v, sizeof(v)) < 0; }
   };
   static std::mutex mu;
   static std::map<Key, IrWavePlan> cache;
   const Key key{{N, IH, IW, OH, OW, C, E, CO, S, (uint32_t)dt, tile_h, tile_w, (uint32_t)weights, (uint32_t)dev,
-                 rl ? 1u : 0u, (uint32_t)kernel, waves_force, stem ? 1u : 0u}};
+                 rl ? 1u : 0u, (uint32_t)kernel, waves_force, stem ? 1u : 0u, head ? 1u : 0u}};
   {
     std::lock_guard<std::mutex> lock(mu);
     auto it = cache.find(key);
@@ -213,6 +219,10 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
         p.lds_w = p.lds_xe + w * npi * 32 * IRW_XPIX;
         p.lds_red = p.lds_x;
         p.lds = p.lds_x + std::max(p.lds_w + w * IRS_RING - p.lds_x, std::min(w, 4u) * nob * IRS_RED_BLOCK);
+        if (head) {
+          p.lds_head = p.lds;
+          p.lds += IRW_HEAD_LDS;
+        }
         if (p.lds > 160u * 1024u) continue;
         p.occ = (uint32_t)irw_occupancy(1, dt, ke, npi, nob, rl, w, p.lds);
         if (p.occ == 0) continue;  // not resident at this size

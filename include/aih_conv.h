@@ -380,6 +380,26 @@ int aih_ir_block_stem(const aih_igemm_desc *stem, const aih_ir_block_desc *blk, 
                       const void *w_dw, const void *b_dw, const void *w_project, const void *b_project, void *y,
                       aih_stream stream);
 
+/* The inverted-residual block joined to the pointwise conv that reads its
+ * output when that conv has at most 4 outputs (a segmentation head, e.g.
+ * 128 -> 2): one launch in place of aih_ir_block followed by aih_conv_pw
+ * (the reference dispatches the block's three convs and the head
+ * separately, lowering.rs:122-168; no counterpart op). The block runs on the
+ * split kernel; each output block, as it is stored, also feeds the head's
+ * products, which are summed exactly as aih_conv_pw's narrow route sums them
+ * (the same fused multiply-adds per input group, each lane's groups in the
+ * same order, the lanes added in the same tree), so y_head equals the two
+ * calls' head output bit for bit. y: the block's output, or NULL to not store
+ * it (when nothing else reads it). blk: as for aih_ir_block, f16 or bf16,
+ * kernel AUTO or SPLIT (tile_h / tile_w / waves 1 / 2 / 4 / 8 as for
+ * aih_ir_block); head: n and m = the block's output, kg = cout / 4 >= 16,
+ * ng = 1, no residual, AIH_VAR_AUTO, splitk 0, dt = wdt = the block's dt. */
+int aih_ir_block_head_plan(const aih_ir_block_desc *blk, const aih_pw_desc *head, aih_ir_plan *out);
+int aih_ir_block_head(const aih_ir_block_desc *blk, const aih_pw_desc *head, const void *x, const void *w_expand,
+                      const void *b_expand, const void *w_dw, const void *b_dw, const void *w_project,
+                      const void *b_project, const void *res, void *y, const void *w_head, const void *b_head,
+                      void *y_head, aih_stream stream);
+
 /* ---- errors / info ---- */
 const char *aih_last_error(void);
 const char *aih_version(void);
