@@ -882,6 +882,141 @@ void fuse_stem_launch(aih_model *m) {
   m->internal[t] = (int32_t)k;
 }
 
+// The narrow head joined to the block before it (aih_ir_block_head): a 1x1
+// conv op k (no stride, pad, groups, residual or views; at most 4 outputs)
+// right after a three-op fused block (ops k - 3 .. k - 1) whose output t it
+// alone reads, t no graph output, state or alias. Runs after lower(): op
+// k - 3's launch becomes the joined one on the split kernel and op k's is
+// dropped; the block's record then covers the head (n_ops 4) and t counts as
+// its intermediate (never stored). Candidates: the block's own tile and
+// wavefronts where its plan is the split kernel, and with AIH_MODEL_TUNE the
+// split kernel at the tune tiles with 2 / 4 / 8 wavefronts, timed (two
+// passes) against the block's and the head's own launches, the fastest
+// kept; without tuning the joined launch where the block's own plan is the
+// split kernel. Not under AIH_MODEL_NO_FUSE.
+void fuse_head_launch(aih_model *m) {
+  if (m->flags & AIH_MODEL_NO_FUSE) return;
+  const auto &ops = m->g.ops;
+  const auto &T = m->g.tensors;
+  for (aih_model::Fused &f : m->fused) {
+    if (f.nops != 3) continue;
+    const size_t k = f.first + 3;
+    if (k >= ops.size() || m->block_of[k] >= 0) continue;
+    const sw::Op &A = ops[f.first], &B = ops[f.first + 1], &P = ops[f.first + 2], &H = ops[k];
+    const uint32_t t = P.out;
+    if (H.kind != sw::OP_CONV || H.in != t || !H.srcs.empty() || H.groups != 1 || H.kh != 1 || H.kw != 1 ||
+        H.sh != 1 || H.sw != 1 || H.pad[0] || H.pad[1] || H.pad[2] || H.pad[3] || H.res >= 0 || H.cout > 4 ||
+        T[t].alias_of >= 0 || !m->dense(t) || !m->dense(H.out))
+      continue;
+    bool keep = false;
+    for (uint32_t o : m->g.outputs) keep |= o == t;
+    for (const auto &st : m->g.states) keep |= st.first == t || st.second == t;
+    for (const auto &tt : T) keep |= tt.alias_of == (int64_t)t;
+    size_t nreads = 0;
+    for (const auto &op : ops)
+      for (uint32_t r : reads_of(op)) nreads += r == t;
+    if (keep || nreads != 1) continue;
+    aih_pw_desc hd{m->n, T[t].h * T[t].w, (H.cin + 3) / 4, 1, H.kg_pad, H.act, 0, m->dt, m->wdt, AIH_VAR_AUTO, 0};
+    // the candidates: the block's own split plan, then (tuning) the tune set
+    std::vector<aih_ir_block_desc> cands;
+    if (f.plan.kernel == AIH_IR_KERNEL_SPLIT) cands.push_back(f.d);
+    const bool tune = (m->flags & AIH_MODEL_TUNE) != 0;
+    if (tune)
+      for (const auto &tt : kTuneWaveTiles)
+        for (uint32_t wv : {2u, 4u, 8u}) {
+          aih_ir_block_desc d = f.d;
+          d.kernel = AIH_IR_KERNEL_SPLIT;
+          d.weights = AIH_IR_WEIGHTS_AUTO;
+          d.tile_h = tt[0];
+          d.tile_w = tt[1];
+          d.waves = wv;
+          cands.push_back(d);
+        }
+    std::set<std::array<uint32_t, 3>> seen;
+    std::vector<std::pair<aih_ir_block_desc, aih_ir_plan>> runs;
+    for (const auto &d : cands) {
+      aih_ir_plan plan;
+      if (aih_ir_block_head_plan(&d, &hd, &plan) != AIH_OK) continue;
+      if (!seen.insert({plan.th, plan.tw, plan.waves}).second) continue;
+      aih_ir_block_desc dd = d;
+      dd.kernel = AIH_IR_KERNEL_SPLIT;
+      dd.weights = AIH_IR_WEIGHTS_AUTO;
+      dd.tile_h = plan.th;
+      dd.tile_w = plan.tw;
+      dd.waves = plan.waves;
+      runs.emplace_back(dd, plan);
+    }
+    if (runs.empty()) continue;
+    const void *x = m->ptr(A.in), *we = m->wptr(A.w), *be = m->wptr(A.b), *wd = m->wptr(B.w), *bd = m->wptr(B.b),
+               *wp = m->wptr(P.w), *bp = m->wptr(P.b), *wh = m->wptr(H.w), *bh = m->wptr(H.b);
+    const void *res = P.res >= 0 ? m->ptr((uint32_t)P.res) : nullptr;
+    void *yh = m->ptr(H.out);
+    size_t best = 0;
+    if (tune) {
+      hipStream_t st = nullptr;
+      if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) throw std::runtime_error("tune: hipStreamCreate");
+      constexpr int R = kTuneReps;
+      hipEvent_t ev[2 * R];
+      for (auto &e : ev)
+        if (hipEventCreate(&e) != hipSuccess) throw std::runtime_error("tune: hipEventCreate");
+      struct Cleanup {
+        hipStream_t st;
+        hipEvent_t *ev;
+        ~Cleanup() {
+          for (int i = 0; i < 2 * R; ++i) (void)hipEventDestroy(ev[i]);
+          (void)hipStreamDestroy(st);
+        }
+      } cleanup{st, ev};
+      auto time = [&](const std::function<int(hipStream_t)> &fn) -> float {
+        for (int w = 0; w < 2; ++w)
+          if (fn(st) != AIH_OK) throw std::runtime_error(std::string("tune: ") + aih_last_error());
+        for (int r = 0; r < R; ++r)
+          if (hipEventRecord(ev[2 * r], st) != hipSuccess || fn(st) != AIH_OK ||
+              hipEventRecord(ev[2 * r + 1], st) != hipSuccess)
+            throw std::runtime_error("tune: launch");
+        if (hipEventSynchronize(ev[2 * R - 1]) != hipSuccess) throw std::runtime_error("tune: hipEventSynchronize");
+        float ts[R];
+        for (int r = 0; r < R; ++r)
+          if (hipEventElapsedTime(&ts[r], ev[2 * r], ev[2 * r + 1]) != hipSuccess) throw std::runtime_error("tune: elapsed");
+        std::sort(ts, ts + R);
+        return ts[R / 2];
+      };
+      const std::function<int(hipStream_t)> sep_blk = m->launches[f.first], sep_head = m->launches[k];
+      const auto sep = [&](hipStream_t s) { return sep_blk(s) != AIH_OK ? AIH_ERR : sep_head(s); };
+      auto joined = [&](const aih_ir_block_desc &dd) {
+        return [&, dd](hipStream_t s) {
+          return aih_ir_block_head(&dd, &hd, x, we, be, wd, bd, wp, bp, res, nullptr, wh, bh, yh, s);
+        };
+      };
+      // two passes (the two launches first), each keeping its faster median
+      float best_ms = time(sep);
+      std::vector<float> t1;
+      for (const auto &rp : runs) t1.push_back(time(joined(rp.first)));
+      best_ms = std::min(best_ms, time(sep));
+      best = runs.size();
+      for (size_t i = 0; i < runs.size(); ++i) {
+        const float ms = std::min(t1[i], time(joined(runs[i].first)));
+        if (ms < best_ms) {
+          best_ms = ms;
+          best = i;
+        }
+      }
+      if (hipStreamSynchronize(st) != hipSuccess) throw std::runtime_error("tune: hipStreamSynchronize");
+      if (best == runs.size()) continue;  // the two launches stay
+    }
+    const aih_ir_block_desc d = runs[best].first;
+    m->launches[f.first] = [d, hd, x, we, be, wd, bd, wp, bp, res, wh, bh, yh](hipStream_t s) {
+      return aih_ir_block_head(&d, &hd, x, we, be, wd, bd, wp, bp, res, nullptr, wh, bh, yh, s);
+    };
+    m->launches[k] = {};
+    f.nops = 4;
+    f.d = d;
+    f.plan = runs[best].second;
+    m->block_of[k] = m->block_of[f.first];
+    m->internal[t] = (int32_t)f.first;
+  }
+}
+
 void lower(aih_model *m) {
   const auto &T = m->g.tensors;
   for (size_t k = 0; k < m->g.ops.size(); ++k) {
@@ -1144,6 +1279,7 @@ aih_model *aih_model_load_ex(const void *bytes, size_t len, uint32_t n, int32_t 
     lower(m.get());
     if (m->ws_bytes) m->ws = m->dalloc(m->ws_bytes);
     fuse_stem_launch(m.get());
+    fuse_head_launch(m.get());
     out = m.release();
     return AIH_OK;
   });

@@ -68,8 +68,9 @@ def _to_device(a: np.ndarray, device) -> torch.Tensor:
 @dataclass
 class ModelOp:
     """One launch of the graph: a single conv ("conv"), a fused block
-    ("ir_block"), a fused depthwise + pointwise pair ("dw_pw") or the stem
-    conv fused into the block after it ("stem_ir_block")."""
+    ("ir_block"), a fused depthwise + pointwise pair ("dw_pw"), the stem
+    conv fused into the block after it ("stem_ir_block") or a block joined to
+    the narrow pointwise head after it ("ir_block_head")."""
 
     name: str
     kind: str
@@ -106,6 +107,18 @@ class ModelOp:
             w = (S.k * S.k * S.cin * S.cout + e.cin * e.cout + d.k * d.k * d.cout + p.cin * p.cout) * w_bytes
             b = (S.cout + e.cout + d.cout + p.cout) * act_bytes
             return x + y + w + b
+        if self.kind == "ir_block_head":
+            # the block's input (and a residual that is not it) in, the
+            # head's output out, weights once: the block's output (the head's
+            # input) is never stored
+            e, d, p, H = self.layers
+            oh, ow = p.out_hw()
+            x = n * e.ih * e.iw * c4(e.cin) * act_bytes
+            r = n * oh * ow * p.cout * act_bytes if p.res and p.res != e.src else 0
+            y = n * oh * ow * c4(H.cout) * act_bytes
+            w = (e.cin * e.cout + d.k * d.k * d.cout + p.cin * p.cout + H.cin * H.cout) * w_bytes
+            b = (e.cout + d.cout + p.cout + c4(H.cout)) * act_bytes
+            return x + r + y + w + b
         e, d, p = self.layers
         oh, ow = p.out_hw()
         x = n * e.ih * e.iw * c4(e.cin) * act_bytes
@@ -131,6 +144,10 @@ class Model:
     # launch (aih_ir_block_stem), the rest naming the block's wave-kernel plan
     STEM_PREFIX = "stem+"
     STEM_WAVES = [4, 8]
+    # a block's label with this suffix: the narrow pointwise head after it
+    # joined to its launch (aih_ir_block_head), the rest naming the block's
+    # split-kernel plan
+    HEAD_SUFFIX = "+head"
 
     def __init__(self, layers: list[Layer], weights: Weights, n: int, ih: int, iw: int, cin: int,
                  dt: conv.DType = conv.DType.F32, wdt: conv.DType | None = None, device="cuda:0",
@@ -190,6 +207,8 @@ class Model:
         self._stem_in = self._stem_input_op(layers, readers, packed, L)
         # the stem fused into the block after it: op 0 reads the fp32 upload
         self._stem_fused = self._fuse_stem(layers, readers, packed, L, tune, choices)
+        # the narrow head joined to the block before it
+        self._head_fused = self._fuse_head(readers, packed, L, tune, choices)
 
     # ------------------------------------------------------------ graph building
 
@@ -283,6 +302,8 @@ class Model:
             return None
         if label.startswith(Model.STEM_PREFIX):  # the block fused with the stem before it: the block's part
             label = label[len(Model.STEM_PREFIX):]
+        if label.endswith(Model.HEAD_SUFFIX):  # the block joined to the head after it: the block's part
+            label = label[:-len(Model.HEAD_SUFFIX)]
         m = re.fullmatch(r"dwpw (\d+)x(\d+) r([24])", label)
         if m:
             return "dwpw", (int(m.group(1)), int(m.group(2))), None, int(m.group(3))
@@ -326,7 +347,7 @@ class Model:
         planned = self.label_of(pl.kernel, pl.th, pl.tw, pl.resident, pl.waves)
         if kernel == conv.IrKernel.WAVE and not waves:
             planned = planned.rsplit(" w", 1)[0]  # a label without a count takes the plan's
-        if planned != label.removeprefix(self.STEM_PREFIX):
+        if planned != label.removeprefix(self.STEM_PREFIX).removesuffix(self.HEAD_SUFFIX):
             raise conv.AihError(f"{self._block_name(p)}: {label!r} planned as "
                                 f"{self.label_of(pl.kernel, pl.th, pl.tw, pl.resident, pl.waves)!r}")
         return [self._fused_op((e, d, p, sp), packed, L)]
@@ -530,6 +551,87 @@ class Model:
         self.choices[name] = (best_label, best_us)
         self.ops[0:2] = [best_op]
         self.tensors.pop(S.name, None)
+        return True
+
+    def _head_op(self, blk: ModelOp, hop: ModelOp, sp: conv.IrBlockHeadSpec, packed, L, y=None) -> ModelOp:
+        """The block blk and the narrow pointwise head hop after it as one
+        aih_ir_block_head launch; y: where the block's output goes, or None
+        (not stored)."""
+        e, d, p = blk.layers
+        H = hop.layers[0]
+        bd, hd = sp.block.desc(), sp.head.desc()
+        res = self.tensors[p.res] if p.res else None
+        yh = self.tensors[H.name]
+        args = (C.byref(bd), C.byref(hd), self.tensors[e.src].data_ptr()) + tuple(
+            packed[nm][k].data_ptr() for nm in (e.name, d.name, p.name) for k in (0, 1)) + (
+            res.data_ptr() if res is not None else None, y.data_ptr() if y is not None else None,
+            packed[H.name][0].data_ptr(), packed[H.name][1].data_ptr(), yh.data_ptr())
+        keep = [bd, hd] + [t for nm in (e.name, d.name, p.name, H.name) for t in packed[nm]]
+        return ModelOp(f"{blk.name}+{H.name}", "ir_block_head", [e, d, p, H], L.aih_ir_block_head, args, sp, keep)
+
+    def _fuse_head(self, readers, packed, L, tune: bool, choices) -> bool:
+        """Joins the last op, a 1x1 conv with at most 4 outputs (the
+        segmentation head) that alone reads the output of the fused block
+        before it, to that block's launch (aih_ir_block_head, the split
+        kernel): recorded choices join it where the block's label carries
+        HEAD_SUFFIX; the tuner times the block and the head against the
+        joined launch at the planner's and the WAVE_TILES tiles with each of
+        SPLIT_WAVES wavefronts (two passes) and keeps the faster. The block's
+        output is then never stored."""
+        if len(self.ops) < 2 or self.ops[-1].kind != "conv" or self.ops[-2].kind != "ir_block":
+            return False
+        blk, hop = self.ops[-2], self.ops[-1]
+        H = hop.layers[0]
+        e, d, p = blk.layers
+        if (H.depthwise or H.groups != 1 or H.k != 1 or H.s != 1 or H.res or H.cout > 4 or H.src != p.name
+                or readers.get(p.name, 0) != 1 or self.output != H.name or self.wdt != self.dt
+                or self.dt == conv.DType.F32):
+            return False
+        name = self._block_name(p)
+        oh, ow = p.out_hw()
+        hs = conv.GemmPwSpec(m=oh * ow, kg=p.cout // 4, ng=1, act=ACT[H.act], dt=self.dt, wdt=self.wdt, n=self.n)
+        K = conv.IrKernel
+        label0 = self.choices.get(name, ("", 0.0))[0]
+        if choices is not None:
+            if not label0.endswith(self.HEAD_SUFFIX):
+                return False
+            sp = conv.IrBlockHeadSpec(blk.spec, hs)
+            if not sp.fusable():
+                raise conv.AihError(f"{name}: {label0!r}: {conv.last_error()}")
+            self.ops[-2:] = [self._head_op(blk, hop, sp, packed, L)]
+            self.tensors.pop(p.name, None)
+            return True
+        if not tune:
+            return False
+        cands, seen = [], set()
+        for tile in [(0, 0)] + self.WAVE_TILES:
+            for waves in self.SPLIT_WAVES:
+                sp = conv.IrBlockHeadSpec(dataclasses.replace(blk.spec, tile=tile, kernel=K.SPLIT, waves=waves,
+                                                              weights=conv.IrWeights.AUTO), hs)
+                if not sp.fusable():
+                    continue
+                pl = sp.plan()
+                if (pl.th, pl.tw, pl.waves) in seen:
+                    continue
+                seen.add((pl.th, pl.tw, pl.waves))
+                sp = conv.IrBlockHeadSpec(dataclasses.replace(sp.block, tile=(pl.th, pl.tw), waves=pl.waves), hs)
+                cands.append((self.label_of(K.SPLIT, pl.th, pl.tw, False, pl.waves) + self.HEAD_SUFFIX,
+                              self._head_op(blk, hop, sp, packed, L)))
+        if not cands:
+            return False
+        # two passes, each candidate keeping its faster median (as _tuned_block)
+        best_us = min(self._time_ops([blk, hop]), self._time_ops([blk, hop]))
+        t1 = [self._time_ops([op]) for _, op in cands]
+        best_label, best_op = None, None
+        for a_, (label, op) in zip(t1, cands):
+            us = min(a_, self._time_ops([op]))
+            if us < best_us:
+                best_us, best_label, best_op = us, label, op
+        if best_op is None:
+            return False
+        self.choices[name] = (best_label, best_us)
+        self.ops[-2:] = [best_op]
+        self.tensors.pop(p.name, None)
         return True
 
     def _alloc(self, h: int, w: int, c: int) -> torch.Tensor:

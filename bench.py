@@ -166,7 +166,7 @@ def main() -> int:
         key = kernel_key(conv, op, n, DT[args.dtype], args.dtype)
         g = groups.setdefault(key, dict(launches=0, secs=0.0, flops=0, bytes=0, grids=[]))
         g["launches"] += 1
-        if op.kind in ("ir_block", "stem_ir_block"):
+        if op.kind in ("ir_block", "stem_ir_block", "ir_block_head"):
             pl = op.spec.plan()
             # dispatch size in threads, as rocprofv3 lists it
             g["grids"].append(pl.grid * 64 * pl.waves)
@@ -370,22 +370,24 @@ def kernel_key(conv, op, n, dt, dtname) -> str:
     trace names it for the fused block; descriptive for the conv kernels)."""
     if op.kind == "stem_ir_block":
         return f"ir_wave_stem_kernel<{int(dt)}>"
-    if op.kind == "ir_block":
+    if op.kind in ("ir_block", "ir_block_head"):
+        # the head joined to a block runs in the block's split kernel
         p = op.spec.plan()
+        bs = op.spec.block if op.kind == "ir_block_head" else op.spec
         if p.kernel in (conv.IrKernel.WAVE, conv.IrKernel.SPLIT):
-            s = op.spec.s
+            s = bs.s
             npi = 2 if ((p.th - 1) * s + 3) * ((p.tw - 1) * s + 3) <= 64 else 5
             A = conv.Activation
-            rl = "true" if int(op.spec.act_expand) == A.RELU and int(op.spec.act_dw) == A.RELU else "false"
-            head = f"<{int(dt)}, {op.spec.cin // 16}, {npi}, {-(-op.spec.cout // 32)}, {rl}"
+            rl = "true" if int(bs.act_expand) == A.RELU and int(bs.act_dw) == A.RELU else "false"
+            head = f"<{int(dt)}, {bs.cin // 16}, {npi}, {-(-bs.cout // 32)}, {rl}"
             if p.kernel == conv.IrKernel.WAVE:
                 return f"ir_wave_kernel{head}>"
             return f"ir_split_kernel{head}, {'true' if p.deep else 'false'}>"
         npw = -(-(-(-p.th * p.tw // 32)) // 4)
         A = conv.Activation
         clamp = all(int(x) in (A.NONE, A.RELU, A.RELU6, A.CLAMP01)
-                    for x in (op.spec.act_expand, op.spec.act_dw, op.spec.act_project))
-        return f"ir_block_kernel<{int(dt)}, {-(-op.spec.cout // 32)}, {npw}, {'true' if clamp else 'false'}>"
+                    for x in (bs.act_expand, bs.act_dw, bs.act_project))
+        return f"ir_block_kernel<{int(dt)}, {-(-bs.cout // 32)}, {npw}, {'true' if clamp else 'false'}>"
     Lr = op.layers[0]
     if Lr.depthwise:
         return f"conv_dw_strip_kernel<{dtname}>"

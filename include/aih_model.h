@@ -131,6 +131,10 @@ aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt)
  * input and residual, joins that block's launch (aih_ir_block_stem, where it
  * plans) when the input is uploaded (staged); an input written into its slot
  * instead runs the stem and the block as two launches.
+ * A 1x1 conv with at most 4 outputs (a segmentation head) right after a
+ * fused block whose output it alone reads joins that block's launch
+ * (aih_ir_block_head, the split kernel) where the block's plan is the split
+ * kernel, or where load-time tuning finds the joined launch faster.
  * Elsewhere, a 3x3 depthwise and the 1x1 conv after it that alone reads its
  * output run as one aih_conv_dwpw launch when its plan has a tile for every
  * CU (weights in the activation dtype). The intermediates are then never stored:
@@ -141,8 +145,8 @@ aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt)
  * its own. AIH_MODEL_TUNE times each fused inverted-residual block's launch
  * options at load (the plan's choice; the wave, split and tile kernels at a
  * set of forced tiles, weight placements and wavefront counts; for a stem
- * joined to its block, the two launches against the joined one at those
- * tiles; a few launches each on the model's own buffers) and keeps the
+ * or a head joined to its block, the two launches against the joined one at
+ * those tiles; a few launches each on the model's own buffers) and keeps the
  * fastest, as the
  * reference's Model::load does its per-model device work once
  * (model.rs:56-366); aih_model_fused_block reports the choice. */
@@ -195,7 +199,9 @@ int aih_model_get_info(const aih_model *m, aih_model_info *out);
 /* Fused block i (0 <= i < n_fused): its first op and op count (it covers
  * ops first_op .. first_op + n_ops - 1); for an inverted-residual block
  * (n_ops 3) the plan aih_ir_block runs it with, for the stem conv fused into
- * the block after it (n_ops 4) the plan of aih_ir_block_stem, for a
+ * the block after it (n_ops 4, first_op the stem's) the plan of
+ * aih_ir_block_stem, for a block joined to the head after it (n_ops 4,
+ * first_op the block's expand) the plan of aih_ir_block_head, for a
  * depthwise -> pointwise pair (n_ops 2) the plan of aih_conv_dwpw. */
 typedef struct {
   uint32_t first_op;

@@ -478,11 +478,12 @@ def test_encoder_through_the_native_loader_tuned(dt):
     """The headline encoder written as the converter's .sw and loaded by
     aih_model_load_ex with AIH_MODEL_TUNE (each fused block's launch options
     timed at load): all ten inverted-residual blocks fuse, the first one with
-    the stem conv before it where the timing picks that (the stem reading the
-    staged fp32 upload either way), and the output equals bit for bit that of
-    the op-level Model (ai_engine_amd.model) told to run the same kernels --
-    whose launches the oracle checks in test_gpu_workloads / test_gpu_ir_tiles
-    / test_gpu_ir_stem. Batch 8."""
+    the stem conv before it and the last one with the head after it where the
+    timing picks that (the stem reading the staged fp32 upload either way),
+    and the output equals bit for bit that of the op-level Model
+    (ai_engine_amd.model) told to run the same kernels -- whose launches the
+    oracle checks in test_gpu_workloads / test_gpu_ir_tiles / test_gpu_ir_stem
+    / test_gpu_ir_head. Batch 8."""
     from ai_engine_amd import workloads as W
     from ai_engine_amd.model import Model
 
@@ -494,9 +495,14 @@ def test_encoder_through_the_native_loader_tuned(dt):
     m = sw.SwModel(data, n=n, dt=conv.DType(dt), tune=True)
     blocks = m.fused_blocks()
     ns = [f.n_ops for f in blocks]
-    assert ns[1:] == [3] * 9 and ns[0] in (3, 4) and m.info.n_launches == 15 - ns[0], (ns, m.info.n_launches)
-    choices = {f"b{i}": (Model.STEM_PREFIX if f.n_ops == 4 else "")
+    # 32 ops: the stem, ten blocks of three, the head; 12 launches, one less
+    # for a joined stem (record from op 0) and for a joined head (from op 28)
+    assert len(ns) == 10 and ns[1:-1] == [3] * 8 and ns[0] in (3, 4) and ns[-1] in (3, 4), ns
+    assert blocks[0].first_op == (0 if ns[0] == 4 else 1) and blocks[-1].first_op == 28, blocks
+    assert m.info.n_launches == 12 - (ns[0] - 3) - (ns[-1] - 3), (ns, m.info.n_launches)
+    choices = {f"b{i}": (Model.STEM_PREFIX if f.n_ops == 4 and f.first_op == 0 else "")
                + Model.label_of(f.plan.kernel, f.plan.th, f.plan.tw, bool(f.plan.resident), f.plan.waves)
+               + (Model.HEAD_SUFFIX if f.n_ops == 4 and f.first_op != 0 else "")
                for i, f in enumerate(blocks)}
     print(f"native tuned choices dt{dt}: {choices}", flush=True)
     m.upload_input("input", x)
