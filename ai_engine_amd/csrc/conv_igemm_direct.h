@@ -52,10 +52,13 @@ inline uint32_t pw_lds_steps(uint32_t nj) {
 }
 
 // Output columns per wavefront (NOB blocks of 32) and column groups: N4 <=
-// 32 -> one block; <= 64 -> two; beyond (1x1 only, <= 256) -> groups of two
-// blocks, one group per work item.
-inline uint32_t ig_direct_nob(uint32_t N4) { return N4 <= 32 ? 1u : 2u; }
-inline uint32_t ig_direct_ncg(uint32_t N4) { return N4 <= 64 ? 1u : (N4 + 63) / 64; }
+// 32 -> one block; <= 64 -> two; beyond (1x1 only, <= 256) -> groups of four
+// blocks where N4 is a multiple of 128 (each activation load feeds twice the
+// MFMAs of a two-block group), else of two; one group per work item.
+inline uint32_t ig_direct_nob(uint32_t N4) { return N4 <= 32 ? 1u : N4 > 64 && N4 % 128 == 0 ? 4u : 2u; }
+inline uint32_t ig_direct_ncg(uint32_t N4) {
+  return N4 <= 64 ? 1u : (N4 + 32 * ig_direct_nob(N4) - 1) / (32 * ig_direct_nob(N4));
+}
 
 // LDS bytes of a launch: the weights as [taps][nj][2][ncg * NOB * 32]
 // 16-byte units, then the fp32 biases of those columns (nj: the

@@ -322,11 +322,11 @@ hipError_t launch_inst(const IgDirectArgs &a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int DT, int NOB>
+template <int DT, int NOB, bool PW_ONLY = false>
 hipError_t launch_nob(const IgDirectArgs &a, hipStream_t st) {
   // operand ring depth D (a divisor of 9 * NJ): 6 / 9 / 12 steps, measured
   // against 3 and 18 on the 16 -> 32 and 32 -> 32 / 64 shapes
-  if (a.taps == 1) {
+  if (PW_ONLY || a.taps == 1) {
     // 1x1: the steps run up to the instantiation's count (ring 8 / 12 deep)
     switch (pw_lds_steps(a.nj)) {
       case 8: return launch_inst<DT, NOB, 1, 8, 8>(a, st);
@@ -337,6 +337,7 @@ hipError_t launch_nob(const IgDirectArgs &a, hipStream_t st) {
       default: return hipErrorInvalidValue;
     }
   }
+  if constexpr (PW_ONLY) return hipErrorInvalidValue;
   switch (a.nj) {
     case 1: return launch_inst<DT, NOB, 9, 1, 9>(a, st);
     case 2: return launch_inst<DT, NOB, 9, 2, 6>(a, st);
@@ -354,7 +355,15 @@ hipError_t launch_nob(const IgDirectArgs &a, hipStream_t st) {
 
 template <int DT>
 hipError_t launch_dt(const IgDirectArgs &a, hipStream_t st) {
-  return a.N4 <= 32 ? launch_nob<DT, 1>(a, st) : launch_nob<DT, 2>(a, st);
+  switch (ig_direct_nob(a.N4)) {
+    case 1: return launch_nob<DT, 1>(a, st);
+    case 2: return launch_nob<DT, 2>(a, st);
+    default:
+      // four blocks: fp32 pointwise only (wider 16-bit and 3x3 calls are
+      // planned elsewhere)
+      if constexpr (DT == DT_F32) return launch_nob<DT, 4, true>(a, st);
+      return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
