@@ -318,6 +318,43 @@ def test_ir_block_rejects_unfusable_shapes():
     assert "res must be given" in conv.last_error()
 
 
+
+def test_ir_block_head_plan_and_rejections():
+    """The head joined to a block (aih_ir_block_head_plan): the block's split
+    plan at the same tile and wavefronts plus the head's 8 KB of LDS (per
+    16-pixel group and pixel, 16 lanes' four fp32 partial sums); what it
+    does not take fails with the reason, and a null buffer fails before any
+    launch."""
+    import dataclasses
+    F16 = conv.DType.F16
+    blk = conv.IrBlockSpec(ih=10, iw=18, cin=128, cexp=512, cout=128, s=1, residual=True, dt=F16, n=64,
+                           tile=(5, 6), waves=4, kernel=conv.IrKernel.SPLIT)
+    head = conv.GemmPwSpec(m=180, kg=32, ng=1, dt=F16, n=64)
+    assert head.plan().variant == conv.Variant.ROWS
+    j, b = conv.IrBlockHeadSpec(blk, head).plan(), blk.plan()
+    assert j.kernel == conv.IrKernel.SPLIT and (j.th, j.tw, j.waves, j.tiles) == (b.th, b.tw, b.waves, b.tiles)
+    assert j.lds_bytes == b.lds_bytes + 2 * 16 * 16 * 16 and j.lds_bytes <= 160 * 1024
+    # AUTO kernel: the head joins the split kernel
+    a = conv.IrBlockHeadSpec(dataclasses.replace(blk, kernel=conv.IrKernel.AUTO, tile=(0, 0), waves=0), head).plan()
+    assert a.kernel == conv.IrKernel.SPLIT
+    bad = [
+        (blk, dataclasses.replace(head, ng=2), "at most 4 outputs"),
+        (blk, dataclasses.replace(head, kg=16), "kg = cout / 4"),
+        (blk, dataclasses.replace(head, m=179), "same n and pixels"),
+        (blk, dataclasses.replace(head, residual=True), "no residual"),
+        (blk, dataclasses.replace(head, splitk=2), "narrow route"),
+        (blk, dataclasses.replace(head, dt=conv.DType.BF16), "dt and wdt"),
+        (dataclasses.replace(blk, kernel=conv.IrKernel.WAVE), head, "split kernel"),
+        (dataclasses.replace(blk, cout=32, cin=32, cexp=128), dataclasses.replace(head, kg=8), "16 lanes"),
+        (dataclasses.replace(blk, dt=conv.DType.F32), dataclasses.replace(head, dt=conv.DType.F32), "f16 or bf16"),
+    ]
+    for bb, hd, why in bad:
+        _expect_error(conv.IrBlockHeadSpec(bb, hd).plan, why)
+    L = conv.lib()
+    assert L.aih_ir_block_head(C.byref(blk.desc()), C.byref(head.desc()), 16, 16, 16, 16, 16, 16, 16, 16, None,
+                               16, 16, None, None) == -1
+    assert "null buffer" in conv.last_error()
+
 # ---------------------------------------------------------------- diagnostic overrides, forced placement
 
 def _plan_in_subprocess(env: dict, code: str) -> str:
