@@ -67,9 +67,10 @@ constexpr int IRW_THREADS = 512;              // the most threads a split-kernel
 // The most wavefronts a wave-kernel workgroup of a shape (KE = C / 16, NPI
 // halo blocks, NOB = COP / 32) has: 12 -- three per SIMD, one workgroup a
 // CU sharing one resident copy of the weights -- where the shape's registers
-// fit 168 VGPRs (the stride-1 tiles of 48- and 64-channel blocks), else 8.
+// fit 168 VGPRs (the stride-1 tiles of 32-, 48- and 64-channel blocks), else
+// 8.
 __host__ __device__ constexpr uint32_t irw_max_waves(uint32_t ke, uint32_t npi, uint32_t nob) {
-  return npi == 2 && nob == 2 && (ke == 3 || ke == 4) ? 12u : 8u;
+  return npi == 2 && ((nob == 2 && (ke == 3 || ke == 4)) || (nob == 1 && ke == 2)) ? 12u : 8u;
 }
 // A wavefront's expanded chunk in LDS: four planes of 8 channels (16 bytes a
 // halo pixel), plane h holding channels 8h .. 8h + 7 of every halo pixel in

@@ -267,7 +267,7 @@ const char *irw_plan(uint32_t N, uint32_t IH, uint32_t IW, uint32_t OH, uint32_t
 
 hipError_t launch_ir_wave_stem(const IrWaveArgs &a, int dt, const IrWavePlan &p, hipStream_t st) {
   if (p.lds > 160u * 1024u || p.grid == 0 || p.split || p.NPI != 2 || a.C != 32 || a.COP != 32 ||
-      (p.waves != 2 && p.waves != 4 && p.waves != 8))
+      (p.waves != 2 && p.waves != 4 && p.waves != 8 && p.waves != 12) || p.waves > irw_max_waves(2, 2, 1))
     return hipErrorInvalidValue;
   switch (dt) {
     case DT_F16: return launch_ir_wave_stem_f16(a, p.waves, p.lds, p.grid, st);

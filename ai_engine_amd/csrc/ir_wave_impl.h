@@ -255,11 +255,12 @@ __device__ __forceinline__ void irdw_store(const IrWaveArgs &a, const float *BpL
 // KE: expand K steps (C / 16); NPI: 32-pixel blocks of the halo tile; NOB:
 // projection blocks of 32 output channels; RL: the expand and depthwise
 // activations are both ReLU (applied to the packed 16-bit results).
-// Wavefronts per SIMD the register allocation aims for: four on the
-// narrowest shape (its operands fit 128 VGPRs), three where a workgroup may
-// have 12 wavefronts (168 VGPRs), else what the shape needs.
+// Wavefronts per SIMD the register allocation aims for: three where a
+// workgroup may have 12 wavefronts (168 VGPRs; the 32-channel shape, at four
+// wavefronts a SIMD within 128, spilled and ran slower), else what the shape
+// needs.
 __host__ __device__ constexpr int irw_waves_per_simd(int ke, int npi, int nob) {
-  return ke == 2 && npi == 2 && nob == 1 ? 4 : irw_max_waves(ke, npi, nob) == 12 ? 3 : 1;
+  return irw_max_waves(ke, npi, nob) == 12 ? 3 : 1;
 }
 
 // The kernel body. STEM: the block's input is computed, not read -- each halo

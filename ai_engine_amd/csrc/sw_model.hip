@@ -778,7 +778,7 @@ void fuse_stem_launch(aih_model *m) {
   if (tune)
     for (const auto &tt : kTuneWaveTiles)
       for (int32_t w : {AIH_IR_WEIGHTS_RESIDENT, AIH_IR_WEIGHTS_STREAMED})
-        for (uint32_t wv : {0u, 4u, 8u}) {
+        for (uint32_t wv : {0u, 4u, 8u, 12u}) {
           aih_ir_block_desc d = f.d;
           d.kernel = AIH_IR_KERNEL_WAVE;
           d.tile_h = tt[0];

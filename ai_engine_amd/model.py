@@ -143,7 +143,7 @@ class Model:
     # a block's label with this prefix: the stem conv before it fused into its
     # launch (aih_ir_block_stem), the rest naming the block's wave-kernel plan
     STEM_PREFIX = "stem+"
-    STEM_WAVES = [4, 8]
+    STEM_WAVES = [4, 8, 12]
     # a block's label with this suffix: the narrow pointwise head after it
     # joined to its launch (aih_ir_block_head), the rest naming the block's
     # split-kernel plan

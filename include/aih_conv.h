@@ -186,8 +186,8 @@ typedef struct {
   int32_t kernel;          /* enum aih_ir_kernel */
   uint32_t waves;          /* wavefronts per workgroup; 0 = chosen by the plan. The split kernel takes
                               1, 2, 4 or 8; the wave kernel 2, 4, 8, or 12 for the stride-1 tiles of
-                              48- and 64-channel blocks (three wavefronts per SIMD sharing one copy
-                              of the weights) */
+                              32-, 48- and 64-channel blocks (three wavefronts per SIMD sharing one
+                              copy of the weights) */
 } aih_ir_block_desc;
 
 /* Which fused kernel runs a block: chosen by the plan (the cheaper estimate
@@ -373,7 +373,7 @@ int aih_conv_stem_f32in(const aih_igemm_desc *d, const float *x, const void *w, 
  * (the block's input: the stem's output), ih x iw = the stem's output size,
  * the same n, dt = f16 or bf16 in both (weights in it), kernel AUTO or WAVE
  * (the wave kernel runs it; tile_h / tile_w / weights / waves as for
- * aih_ir_block, waves 2 / 4 / 8). */
+ * aih_ir_block, waves 2 / 4 / 8 / 12). */
 int aih_ir_block_stem_plan(const aih_igemm_desc *stem, const aih_ir_block_desc *blk, aih_ir_plan *out);
 int aih_ir_block_stem(const aih_igemm_desc *stem, const aih_ir_block_desc *blk, const float *image,
                       const void *w_stem, const void *b_stem, const void *w_expand, const void *b_expand,
