@@ -153,13 +153,15 @@ struct aih_model {
   uint32_t flags = 0;
   struct Fused {
     uint32_t first;  // ops first .. first + nops - 1
-    uint32_t nops;   // 3: inverted-residual block (d, plan); 2: depthwise -> pointwise pair (dp, dpp);
-                     // 4: the stem conv and the block after it (sd, d, plan: aih_ir_block_stem)
+    uint32_t nops;   // 3: inverted-residual block (d, plan); 2: depthwise -> pointwise pair (dp, dpp)
+                     // or a resize folded into the concat after it; 4: the stem conv and the block
+                     // after it (sd, d, plan: aih_ir_block_stem), or a block and the head after it
     aih_ir_block_desc d;
     aih_ir_plan plan;
     aih_dwpw_desc dp;
     aih_dwpw_plan dpp;
     aih_igemm_desc sd;
+    int32_t kind = AIH_FUSED_IR_BLOCK;  // enum aih_fused_kind
   };
   std::vector<Fused> fused;
   std::vector<int32_t> block_of;  // per op: its fused block, or -1
@@ -478,9 +480,66 @@ bool fuse_pair(aih_model *m, size_t k, const std::vector<uint32_t> &readers, con
   aih_dwpw_plan plan;
   if (aih_conv_dwpw_plan(&d, &plan) != AIH_OK || plan.tiles < aih::device_cus()) return false;
   const int32_t bi = (int32_t)m->fused.size();
-  m->fused.push_back(aih_model::Fused{(uint32_t)k, 2, aih_ir_block_desc{}, aih_ir_plan{}, d, plan});
+  m->fused.push_back(aih_model::Fused{(uint32_t)k, 2, aih_ir_block_desc{}, aih_ir_plan{}, d, plan,
+                                      aih_igemm_desc{}, AIH_FUSED_DWPW});
   m->block_of[k] = m->block_of[k + 1] = bi;
   m->internal[B.out] = (int32_t)k;
+  return true;
+}
+
+// The parts of the one aih_resize_concat launch that replaces a Resize (op
+// k) and the Concat after it (op k + 1): the concat's parts in order, the
+// resize's output replaced by the resize's own parts (its srcs, or its whole
+// input), each marked resized.
+struct FoldPart {
+  sw::Part part;
+  bool resized;
+};
+std::vector<FoldPart> fold_parts(const sw::Model &g, const sw::Op &R, const sw::Op &C) {
+  std::vector<FoldPart> out;
+  for (const sw::Part &p : C.srcs) {
+    if (p.tid != R.out) {
+      out.push_back(FoldPart{p, false});
+      continue;
+    }
+    if (R.srcs.empty())
+      out.push_back(FoldPart{sw::Part{R.in, g.tensors[R.in].c}, true});
+    else
+      for (const sw::Part &q : R.srcs) out.push_back(FoldPart{q, true});
+  }
+  return out;
+}
+
+// Ops k, k + 1 as one aih_resize_concat launch: a Resize whose output only
+// the Concat right after it reads (no alias, graph output or state), taken
+// whole as one of its parts, every part of the folded launch but the last
+// with a multiple of 4 channels, at most 8 parts, and a dense concat output.
+// The resize output is then never stored: at batch 64, f16, the real
+// segmentation model's 40x72x32 -> 80x144 resize and the 44-channel concat
+// after it write and read back 47 MB less.
+bool fold_resize_concat(aih_model *m, size_t k, const std::vector<uint32_t> &readers,
+                        const std::vector<bool> &pinned) {
+  const auto &ops = m->g.ops;
+  if (k + 1 >= ops.size()) return false;
+  const sw::Op &R = ops[k], &C = ops[k + 1];
+  if (R.kind != sw::OP_RESIZE || C.kind != sw::OP_CONCAT || readers[R.out] != 1 || pinned[R.out] ||
+      !dense_tid(m->g, C.out))
+    return false;
+  bool whole = false;
+  for (const sw::Part &p : C.srcs) whole = whole || (p.tid == R.out && p.c == m->g.tensors[R.out].c);
+  if (!whole) return false;
+  const std::vector<FoldPart> parts = fold_parts(m->g, R, C);
+  if (parts.size() > 8) return false;
+  for (size_t i = 0; i + 1 < parts.size(); ++i)
+    if (parts[i].part.c % 4) return false;
+  const int32_t bi = (int32_t)m->fused.size();
+  aih_model::Fused f{};
+  f.first = (uint32_t)k;
+  f.nops = 2;
+  f.kind = AIH_FUSED_RESIZE_CONCAT;
+  m->fused.push_back(f);
+  m->block_of[k] = m->block_of[k + 1] = bi;
+  m->internal[R.out] = (int32_t)k;
   return true;
 }
 
@@ -504,7 +563,7 @@ void find_fusions(aih_model *m) {
   const auto &T = m->g.tensors;
   m->block_of.assign(ops.size(), -1);
   m->internal.assign(T.size(), -1);
-  if ((m->flags & AIH_MODEL_NO_FUSE) || m->wdt != m->dt) return;
+  if (m->flags & AIH_MODEL_NO_FUSE) return;
   std::vector<uint32_t> readers(T.size(), 0);
   for (const sw::Op &op : ops)
     for (uint32_t t : reads_of(op)) ++readers[t];
@@ -513,6 +572,10 @@ void find_fusions(aih_model *m) {
   for (const auto &st : m->g.states) pinned[st.first] = pinned[st.second] = true;
   for (size_t i = 0; i < T.size(); ++i)
     if (T[i].alias_of >= 0) pinned[i] = pinned[(size_t)T[i].alias_of] = true;
+  // resize -> concat folds move no weights: any dtypes
+  for (size_t k = 0; k + 1 < ops.size(); ++k)
+    if (fold_resize_concat(m, k, readers, pinned)) ++k;
+  if (m->wdt != m->dt) return;
   auto aligned = [&](const sw::WRef &r, uintptr_t a) { return (reinterpret_cast<uintptr_t>(m->wptr(r)) % a) == 0; };
   for (size_t k = 0; k + 1 < ops.size();) {
     if (fuse_pair(m, k, readers, pinned)) {
@@ -546,7 +609,8 @@ void find_fusions(aih_model *m) {
       aih_ir_plan plan;
       if (aih_ir_block_plan(&d, &plan) == AIH_OK) {
         const int32_t bi = (int32_t)m->fused.size();
-        m->fused.push_back(aih_model::Fused{(uint32_t)k, 3, d, plan, aih_dwpw_desc{}, aih_dwpw_plan{}});
+        m->fused.push_back(aih_model::Fused{(uint32_t)k, 3, d, plan, aih_dwpw_desc{}, aih_dwpw_plan{},
+                                            aih_igemm_desc{}, AIH_FUSED_IR_BLOCK});
         m->block_of[k] = m->block_of[k + 1] = m->block_of[k + 2] = bi;
         m->internal[A.out] = m->internal[B.out] = (int32_t)k;
         k += 3;
@@ -875,6 +939,7 @@ void fuse_stem_launch(aih_model *m) {
   m->launches[k + 1] = {};
   f.first = (uint32_t)k;
   f.nops = 4;
+  f.kind = AIH_FUSED_STEM_BLOCK;
   f.sd = sd;
   f.d = best;
   f.plan = best_plan;
@@ -1010,6 +1075,7 @@ void fuse_head_launch(aih_model *m) {
     };
     m->launches[k] = {};
     f.nops = 4;
+    f.kind = AIH_FUSED_BLOCK_HEAD;
     f.d = d;
     f.plan = runs[best].second;
     m->block_of[k] = m->block_of[f.first];
@@ -1028,7 +1094,28 @@ void lower(aih_model *m) {
         m->launches.emplace_back();  // runs in the block's first op
         continue;
       }
-      if (f.nops == 2) {
+      if (f.kind == AIH_FUSED_RESIZE_CONCAT) {
+        const sw::Op &C = m->g.ops[k + 1];
+        const auto &I = T[op.in];
+        aih_resize_concat_desc d{};
+        d.n = m->n;
+        d.ih = I.h;
+        d.iw = I.w;
+        d.oh = T[C.out].h;
+        d.ow = T[C.out].w;
+        d.mode = op.coord;
+        d.dt = m->dt;
+        std::vector<const void *> ins;
+        for (const FoldPart &p : fold_parts(m->g, op, C)) {
+          d.resized |= (p.resized ? 1u : 0u) << d.nparts;
+          d.parts[d.nparts++] = m->src_of(p.part.tid, p.part.c);
+          ins.push_back(m->views[p.part.tid].base);
+        }
+        void *y = m->ptr(C.out);
+        m->launches.push_back([d, ins, y](hipStream_t s) { return aih_resize_concat(&d, ins.data(), y, s); });
+        continue;
+      }
+      if (f.kind == AIH_FUSED_DWPW) {
         const sw::Op &P = m->g.ops[k + 1];
         const aih_dwpw_desc d = f.dp;
         const void *x = m->ptr(op.in), *wd = m->wptr(op.w), *bd = m->wptr(op.b), *wp = m->wptr(P.w),
@@ -1481,7 +1568,7 @@ int aih_model_fused_block(const aih_model *m, uint32_t i, aih_model_fused_info *
     if (!m || !out) return api_fail("fused_block: null argument");
     if (i >= m->fused.size()) return api_fail("fused_block: no fused block " + std::to_string(i));
     const aih_model::Fused &f = m->fused[i];
-    *out = aih_model_fused_info{f.first, f.nops, f.plan, f.dpp};
+    *out = aih_model_fused_info{f.first, f.nops, f.plan, f.dpp, f.kind};
     return AIH_OK;
   });
 }

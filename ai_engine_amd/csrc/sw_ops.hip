@@ -7,6 +7,7 @@
 // host) so the index decomposition is 32-bit with precomputed divisors.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <string>
 
 #include "../../include/aih_model.h"
@@ -27,6 +28,7 @@ struct PartArg {
 struct Parts {
   PartArg v[kMaxParts];
   uint32_t n;
+  uint32_t resized;  // resize_kernel: bit p set = part p is bilinear-resized
 };
 
 template <int DT>
@@ -39,47 +41,102 @@ __device__ __forceinline__ float ld1(const void *base, size_t i) {
 // ---------------------------------------------------------------- resize
 
 // reference/resize.rs:13-43: src coordinate, taps clamped to the image,
-// weights clamped to [0, 1]; out = top*(1-ty) + bot*ty.
-__device__ __forceinline__ void resize_coord(uint32_t o, float scale, int mode, uint32_t in, uint32_t &i0,
-                                             uint32_t &i1, float &t) {
-  const float f = mode == AIH_COORD_HALF_PIXEL ? ((float)o + 0.5f) * scale - 0.5f : (float)o * scale;
+// weights clamped to [0, 1]; out = top*(1-ty) + bot*ty with top and bot the
+// same blend along x. Every product and sum is rounded on its own (no fused
+// multiply-add), as the reference's scalar code computes them, so fp32
+// results equal the reference's bit for bit. The scales (in / out, one fp32
+// division) come from the host, where IEEE division gives the same value.
+struct Coord {
+  uint32_t i0, i1;
+  float t, u;  // weight of i1, and 1 - t (the weight of i0)
+};
+
+__device__ __forceinline__ Coord resize_coord(uint32_t o, float scale, int mode, uint32_t in) {
+#pragma clang fp contract(off)
+  const float of = (float)o;  // exact: sizes are checked below 2^24
+  const float f = mode == AIH_COORD_HALF_PIXEL ? (of + 0.5f) * scale - 0.5f : of * scale;
   const float fl = floorf(f);
-  const int64_t b = (int64_t)fl;
-  const int64_t hi = (int64_t)in - 1;
-  i0 = (uint32_t)(b < 0 ? 0 : (b > hi ? hi : b));
-  i1 = (uint32_t)(b + 1 < 0 ? 0 : (b + 1 > hi ? hi : b + 1));
-  t = fminf(fmaxf(f - fl, 0.0f), 1.0f);
+  const int b = (int)fl;  // -1 <= b <= in: fits
+  const int hi = (int)in - 1;
+  Coord c;
+  c.i0 = (uint32_t)min(max(b, 0), hi);
+  c.i1 = (uint32_t)min(max(b + 1, 0), hi);
+  c.t = fminf(fmaxf(f - fl, 0.0f), 1.0f);
+  c.u = 1.0f - c.t;
+  return c;
 }
 
-template <int DT>
-__global__ __launch_bounds__(256) void resize_kernel(Parts parts, uint32_t total, uint32_t ih, uint32_t iw,
-                                                     uint32_t oh, uint32_t ow, int mode, uint32_t cg_out,
-                                                     FastDiv fd_cg, FastDiv fd_ow, FastDiv fd_oh, void *y) {
-  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;
-  const uint32_t pix = fdiv(i, fd_cg);
-  const uint32_t g = i - pix * cg_out;
-  const uint32_t t2 = fdiv(pix, fd_ow);
-  const uint32_t ox = pix - t2 * ow;
-  const uint32_t img = fdiv(t2, fd_oh);
-  const uint32_t oy = t2 - img * oh;
-  // the output vec4 lies in one part (all parts but the last hold a multiple of 4 channels)
-  uint32_t p = 0;
-  while (p + 1 < parts.n && g * 4 >= parts.v[p + 1].out_c0) ++p;
-  const PartArg &pa = parts.v[p];
-  const uint32_t k0 = g * 4 - pa.out_c0;
-  uint32_t y0, y1, x0, x1;
-  float ty, tx;
-  resize_coord(oy, (float)ih / (float)oh, mode, ih, y0, y1, ty);
-  resize_coord(ox, (float)iw / (float)ow, mode, iw, x0, x1, tx);
-  const uint32_t cgi = pa.stride_c / 4;
-  const size_t ibase = (size_t)img * ih * iw;
-  auto at = [&](uint32_t yy, uint32_t xx) {
-    return Vec4IO<DT>::load(pa.p, (ibase + yy * iw + xx) * cgi + (pa.c_off + k0) / 4);
-  };
-  const f32x4 top = at(y0, x0) * (1.0f - tx) + at(y0, x1) * tx;
-  const f32x4 bot = at(y1, x0) * (1.0f - tx) + at(y1, x1) * tx;
-  Vec4IO<DT>::store(y, i, top * (1.0f - ty) + bot * ty);
+__device__ __forceinline__ f32x4 lerp4(f32x4 a, f32x4 b, float t, float u) {
+#pragma clang fp contract(off)
+  return a * u + b * t;
+}
+
+// One workgroup per output row (image, oy): the row's source rows and y
+// weight are computed once, and the threads stride over the row's ow * cg
+// output vec4s (stores of consecutive threads are consecutive). Part p with
+// bit p of parts.resized set is read at ih x iw and blended from its four
+// taps; any other part is read at the output's own pixel (a plain concat
+// part). Lanes past a part's channels are stored as 0. The loop over parts
+// is uniform, so each part's fields sit in scalar registers; a lane takes
+// the one part its vec4 lies in.
+// Vec4 `idx` of a part: a 32-bit byte offset from the part's base when the
+// host found every part below 4 GiB (O32; the loads then take the base in
+// scalar registers and one 32-bit offset), else 64-bit indexing.
+template <int DT, bool O32>
+__device__ __forceinline__ f32x4 part_load(const void *base, size_t idx) {
+  if constexpr (O32)
+    return Vec4IO<DT>::load(static_cast<const char *>(base) + (uint32_t)idx * (DT == DT_F32 ? 16u : 8u), 0);
+  else
+    return Vec4IO<DT>::load(base, idx);
+}
+
+template <int DT, bool O32>
+__device__ __forceinline__ f32x4 resize_part(const PartArg &pa, bool resized, uint32_t k0, uint32_t ox,
+                                             size_t prow, size_t r0, size_t r1, const Coord &cy, float sx,
+                                             int mode, uint32_t iw) {
+  const uint32_t cgi = pa.stride_c / 4, q = (pa.c_off + k0) / 4;
+  f32x4 v;
+  if (resized) {
+    const Coord cx = resize_coord(ox, sx, mode, iw);
+    const f32x4 a = part_load<DT, O32>(pa.p, (r0 + cx.i0) * cgi + q);
+    const f32x4 b = part_load<DT, O32>(pa.p, (r0 + cx.i1) * cgi + q);
+    const f32x4 c = part_load<DT, O32>(pa.p, (r1 + cx.i0) * cgi + q);
+    const f32x4 d = part_load<DT, O32>(pa.p, (r1 + cx.i1) * cgi + q);
+    v = lerp4(lerp4(a, b, cx.t, cx.u), lerp4(c, d, cx.t, cx.u), cy.t, cy.u);
+  } else {
+    v = part_load<DT, O32>(pa.p, (prow + ox) * cgi + q);
+  }
+#pragma unroll
+  for (int l = 0; l < 4; ++l)
+    if (k0 + l >= pa.c) v[l] = 0.0f;
+  return v;
+}
+
+// Rows of up to 1024 vec4s take one thread per vec4 (the block rounded up
+// to whole wavefronts); longer rows 256 threads that stride over the row.
+template <int DT, bool O32>
+__global__ __launch_bounds__(1024) void resize_kernel(Parts parts, uint32_t ih, uint32_t iw, uint32_t oh,
+                                                      uint32_t ow, float sy, float sx, int mode, uint32_t cg_out,
+                                                      FastDiv fd_cg, FastDiv fd_oh, void *y) {
+  const uint32_t row = blockIdx.x;
+  const uint32_t img = fdiv(row, fd_oh);
+  const Coord cy = resize_coord(row - img * oh, sy, mode, ih);
+  const size_t r0 = ((size_t)img * ih + cy.i0) * iw, r1 = ((size_t)img * ih + cy.i1) * iw;
+  const size_t prow = (size_t)row * ow;
+  const uint32_t nrow = ow * cg_out;
+  for (uint32_t j = threadIdx.x; j < nrow; j += blockDim.x) {
+    const uint32_t ox = fdiv(j, fd_cg);
+    const uint32_t g4 = (j - ox * cg_out) * 4;
+    f32x4 v = {};
+    for (uint32_t p = 0; p < parts.n; ++p) {
+      const PartArg &pa = parts.v[p];
+      const uint32_t end = p + 1 < parts.n ? parts.v[p + 1].out_c0 : 0xffffffffu;
+      if (g4 >= pa.out_c0 && g4 < end)
+        v = resize_part<DT, O32>(pa, (parts.resized >> p) & 1u, g4 - pa.out_c0, ox, prow, r0, r1, cy, sx, mode,
+                                 iw);
+    }
+    Vec4IO<DT>::store(y, (size_t)row * nrow + j, v);
+  }
 }
 
 // ---------------------------------------------------------------- gpool
@@ -230,8 +287,57 @@ int fill_parts(const aih_src *src, uint32_t nsrc, const void *const *inputs, int
     c0 += s.c;
   }
   parts->n = nsrc;
+  parts->resized = 0;
   *out_c = c0;
   return AIH_OK;
+}
+
+// Shared by aih_resize (every part resized) and aih_resize_concat. `all`:
+// every part is resized; else bit i of `mask` picks part i. Sizes stay below
+// 2^24 so output coordinates convert to fp32 exactly.
+int launch_resize(const char *what, uint32_t n, uint32_t ih, uint32_t iw, uint32_t oh, uint32_t ow, int32_t mode,
+                  int32_t dt, const aih_src *srcs, uint32_t nsrcs, bool all, uint32_t mask,
+                  const void *const *inputs, void *y, aih_stream stream) {
+  const std::string w(what);
+  if (!dt_ok(dt)) return api_fail(w + ": unknown dtype");
+  if (!n || !ih || !iw || !oh || !ow) return api_fail(w + ": zero-sized dimension");
+  if (ih >= (1u << 24) || iw >= (1u << 24) || oh >= (1u << 24) || ow >= (1u << 24))
+    return api_fail(w + ": sizes must stay below 2^24");
+  if (mode != AIH_COORD_HALF_PIXEL && mode != AIH_COORD_ASYMMETRIC) return api_fail(w + ": unknown mode");
+  if (!y || !aligned(y, vec_bytes(dt))) return api_fail(w + ": null or misaligned output");
+  Parts parts;
+  uint32_t c = 0;
+  if (fill_parts(srcs, nsrcs, inputs, dt, true, &parts, &c)) return AIH_ERR;
+  if (!all && (mask >> nsrcs) != 0) return api_fail(w + ": resized bits past the parts");
+  parts.resized = all ? (1u << nsrcs) - 1u : mask;
+  const uint32_t cg = (c + 3) / 4;
+  const uint64_t rows = (uint64_t)n * oh;
+  const uint64_t total = rows * ow * cg;
+  if (total > 0xffffff00ull || rows > 0x7fffffffull) return api_fail(w + ": output too large");
+  const uint32_t nrow = ow * cg;
+  const uint32_t threads = nrow <= 1024 ? (nrow + 63) / 64 * 64 : 256u;
+  // every part's vec4s (its ih x iw or oh x ow pixels times stride_c / 4) below 4 GiB
+  bool o32 = true;
+  for (uint32_t i = 0; i < nsrcs; ++i) {
+    const bool rs = (parts.resized >> i) & 1u;
+    const uint64_t px = (uint64_t)n * (rs ? (uint64_t)ih * iw : (uint64_t)oh * ow);
+    o32 = o32 && px * srcs[i].stride_c / 4 * vec_bytes(dt) < (1ull << 32);
+  }
+  const float sy = (float)ih / (float)oh, sx = (float)iw / (float)ow;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)rows), block(threads);
+  const FastDiv fcg = make_fastdiv(cg), foh = make_fastdiv(oh);
+#define AIH_RESIZE_LAUNCH(D, O)                                                                                  \
+  hipLaunchKernelGGL((resize_kernel<D, O>), grid, block, 0, st, parts, ih, iw, oh, ow, sy, sx, (int)mode, cg, fcg, \
+                     foh, y)
+  switch (dt) {
+    case AIH_F32: if (o32) AIH_RESIZE_LAUNCH(DT_F32, true); else AIH_RESIZE_LAUNCH(DT_F32, false); break;
+    case AIH_F16: if (o32) AIH_RESIZE_LAUNCH(DT_F16, true); else AIH_RESIZE_LAUNCH(DT_F16, false); break;
+    default: if (o32) AIH_RESIZE_LAUNCH(DT_BF16, true); else AIH_RESIZE_LAUNCH(DT_BF16, false); break;
+  }
+#undef AIH_RESIZE_LAUNCH
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? AIH_OK : api_fail(w + " launch: " + hipGetErrorString(e));
 }
 
 }  // namespace
@@ -262,21 +368,16 @@ extern "C" {
 int aih_resize(const aih_resize_desc *d, const void *const *inputs, void *y, aih_stream stream) {
   return api_guarded([&] {
     if (!d) return api_fail("resize: null descriptor");
-    if (!dt_ok(d->dt)) return api_fail("resize: unknown dtype");
-    if (!d->n || !d->ih || !d->iw || !d->oh || !d->ow) return api_fail("resize: zero-sized dimension");
-    if (d->mode != AIH_COORD_HALF_PIXEL && d->mode != AIH_COORD_ASYMMETRIC) return api_fail("resize: unknown mode");
-    if (!y || !aligned(y, vec_bytes(d->dt))) return api_fail("resize: null or misaligned output");
-    Parts parts;
-    uint32_t c = 0;
-    if (fill_parts(d->srcs, d->nsrcs, inputs, d->dt, true, &parts, &c)) return AIH_ERR;
-    const uint32_t cg = (c + 3) / 4;
-    const uint64_t total = (uint64_t)d->n * d->oh * d->ow * cg;
-    if (total == 0 || total > 0xffffff00ull) return api_fail("resize: output too large");
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    AIH_LAUNCH_DT(resize_kernel, d->dt, grid_for(total), st, parts, (uint32_t)total, d->ih, d->iw, d->oh, d->ow,
-                  (int)d->mode, cg, make_fastdiv(cg), make_fastdiv(d->ow), make_fastdiv(d->oh), y);
-    const hipError_t e = hipGetLastError();
-    return e == hipSuccess ? AIH_OK : api_fail(std::string("resize launch: ") + hipGetErrorString(e));
+    return launch_resize("resize", d->n, d->ih, d->iw, d->oh, d->ow, d->mode, d->dt, d->srcs, d->nsrcs, true, 0,
+                         inputs, y, stream);
+  });
+}
+
+int aih_resize_concat(const aih_resize_concat_desc *d, const void *const *inputs, void *y, aih_stream stream) {
+  return api_guarded([&] {
+    if (!d) return api_fail("resize_concat: null descriptor");
+    return launch_resize("resize_concat", d->n, d->ih, d->iw, d->oh, d->ow, d->mode, d->dt, d->parts, d->nparts,
+                         false, d->resized, inputs, y, stream);
   });
 }
 

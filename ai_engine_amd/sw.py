@@ -43,6 +43,12 @@ class _Concat(C.Structure):
                 ("nparts", C.c_uint32), ("parts", conv._Src * 8)]
 
 
+class _ResizeConcat(C.Structure):
+    _fields_ = [("n", C.c_uint32), ("ih", C.c_uint32), ("iw", C.c_uint32), ("oh", C.c_uint32),
+                ("ow", C.c_uint32), ("mode", C.c_int32), ("dt", C.c_int32), ("nparts", C.c_uint32),
+                ("resized", C.c_uint32), ("parts", conv._Src * 8)]
+
+
 class TensorInfo(C.Structure):
     _fields_ = [("data", C.c_void_p), ("bytes", C.c_size_t), ("n", C.c_uint32), ("h", C.c_uint32),
                 ("w", C.c_uint32), ("c", C.c_uint32), ("stride_c", C.c_uint32), ("dt", C.c_int32)]
@@ -55,14 +61,19 @@ class ModelInfo(C.Structure):
 
 
 class FusedInfo(C.Structure):
-    _fields_ = [("first_op", C.c_uint32), ("n_ops", C.c_uint32), ("plan", conv.IrPlan), ("dwpw", conv.DwPwPlan)]
+    _fields_ = [("first_op", C.c_uint32), ("n_ops", C.c_uint32), ("plan", conv.IrPlan), ("dwpw", conv.DwPwPlan),
+                ("kind", C.c_int32)]
+
+
+# aih_fused_kind
+FUSED_IR_BLOCK, FUSED_DWPW, FUSED_STEM_BLOCK, FUSED_BLOCK_HEAD, FUSED_RESIZE_CONCAT = range(5)
 
 
 NO_FUSE, TUNE = 1, 2  # aih_model_flags
 
 
 EXPORTS = (
-    "aih_resize", "aih_gpool", "aih_binary", "aih_concat", "aih_model_load", "aih_model_load_ex", "aih_model_free",
+    "aih_resize", "aih_gpool", "aih_binary", "aih_concat", "aih_resize_concat", "aih_model_load", "aih_model_load_ex", "aih_model_free",
     "aih_model_upload_input", "aih_model_upload_input_device", "aih_model_infer", "aih_model_infer_range",
     "aih_model_read_output", "aih_model_write_tensor", "aih_model_reset", "aih_model_tensor", "aih_model_get_info", "aih_model_input_name", "aih_model_output_name",
     "aih_sw_describe", "aih_model_fused_block",
@@ -87,6 +98,7 @@ def lib() -> C.CDLL:
         "aih_gpool": (C.c_int, [C.POINTER(_Gpool), P, P, P]),
         "aih_binary": (C.c_int, [C.POINTER(_Binary), P, P, P, P]),
         "aih_concat": (C.c_int, [C.POINTER(_Concat), C.POINTER(P), P, P]),
+        "aih_resize_concat": (C.c_int, [C.POINTER(_ResizeConcat), C.POINTER(P), P, P]),
         "aih_model_load": (P, [C.c_char_p, sz, u32, i32]),
         "aih_model_load_ex": (P, [C.c_char_p, sz, u32, i32, u32]),
         "aih_model_fused_block": (C.c_int, [P, u32, C.POINTER(FusedInfo)]),
@@ -162,6 +174,17 @@ def concat(parts, n, h, w, dt, y, stream=None):
     """parts: [(tensor, c, stride_c, c_off)]."""
     d = _Concat(n, h, w, int(dt), len(parts), _srcs([(c, s, o) for _, c, s, o in parts]))
     conv._check(lib().aih_concat(C.byref(d), _ptrs([p[0] for p in parts]), conv._ptr(y), conv._stream(stream)))
+    return y
+
+
+def resize_concat(parts, n, ih, iw, oh, ow, mode, dt, y, stream=None):
+    """parts: [(tensor, c, stride_c, c_off, resized)]; a resized part is read at
+    ih x iw and resized to oh x ow, any other is copied at oh x ow."""
+    mask = sum(1 << i for i, p in enumerate(parts) if p[4])
+    d = _ResizeConcat(n, ih, iw, oh, ow, COORD[mode] if isinstance(mode, str) else mode, int(dt), len(parts), mask,
+                      _srcs([(c, s, o) for _, c, s, o, _ in parts]))
+    conv._check(lib().aih_resize_concat(C.byref(d), _ptrs([p[0] for p in parts]), conv._ptr(y),
+                                        conv._stream(stream)))
     return y
 
 

@@ -551,6 +551,13 @@ def kernel_table(torch, conv, W, Model, dev, stream, DT) -> dict:
     return res
 
 
+def fused_label(sw, f) -> str:
+    """What a native-runtime fused block runs: its kernel plan, or the fold."""
+    if f.kind == sw.FUSED_RESIZE_CONCAT:
+        return "resize folded into concat"
+    return str(f.dwpw if f.kind == sw.FUSED_DWPW else f.plan)
+
+
 def real_model(torch, conv, dev, stream) -> dict:
     """The reference converter's real segmentation model (tests/golden/
     segm_r11_160x288.sw: 36 convs + resize / gpool / binary / concat) through
@@ -582,8 +589,8 @@ def real_model(torch, conv, dev, stream) -> dict:
         key = f"segm_r11_real_160x288_b{n}_{dt}" + ("" if fuse else "_unfused")
         out[key] = dict(us=round(t * 1e6, 1), frames_per_s=round(n / t, 1), tflops=round(2 * macs * n / t / 1e12, 2),
                         gflop_per_frame=round(2 * macs / 1e9, 3), ops=len(g["ops"]), launches=m.info.n_launches,
-                        fused_blocks=[f"ops {f.first_op}-{f.first_op + f.n_ops - 1}: "
-                                      f"{f.dwpw if f.n_ops == 2 else f.plan}" for f in m.fused_blocks()])
+                        fused_blocks=[f"ops {f.first_op}-{f.first_op + f.n_ops - 1}: " + fused_label(sw, f)
+                                      for f in m.fused_blocks()])
         log(f"real segm model {dt} b{n} {'fused' if fuse else 'unfused'}: {t * 1e3:.3f} ms {n / t:.0f} frames/s "
             f"({m.info.n_launches} launches)")
         m.close()

@@ -19,6 +19,7 @@
  *   - aih_gpool   <- SwOp::Gpool (channel mean)
  *   - aih_binary  <- SwOp::Binary (add / sub / mul / prelu, six operand kinds) + act
  *   - aih_concat  <- SwOp::Concat (channel concat)
+ *   - aih_resize_concat <- a Resize folded into the Concat that alone reads it
  *
  * Supported .sw ops: Conv (all of lower_op's routes, concat parts, residual),
  * Binary, Gpool, Resize, Concat. Any other op kind makes aih_model_load fail
@@ -105,6 +106,24 @@ typedef struct {
 } aih_concat_desc;
 int aih_concat(const aih_concat_desc *d, const void *const *inputs, void *y, aih_stream stream);
 
+/* A Resize whose output only a Concat reads, folded into the concat: one
+ * launch writes the h x w concat, part i (parts[i] of inputs[i]) read at
+ * ih x iw and resized as aih_resize does when bit i of `resized` is set
+ * (the same coordinates, weights and arithmetic, so the same bits), and
+ * copied at oh x ow as aih_concat does otherwise. Every part but the last has
+ * a multiple of 4 channels. No counterpart in the reference, which runs the
+ * two ops as two dispatches (crates/ai-gpu-runtime/src/lowering.rs:335-388,
+ * the Resize and Concat arms); aih_model_load uses it for that pattern. */
+typedef struct {
+  uint32_t n, ih, iw, oh, ow;
+  int32_t mode; /* enum aih_coord */
+  int32_t dt;
+  uint32_t nparts;  /* 1..8 */
+  uint32_t resized; /* bit i: part i is resized from ih x iw */
+  aih_src parts[8];
+} aih_resize_concat_desc;
+int aih_resize_concat(const aih_resize_concat_desc *d, const void *const *inputs, void *y, aih_stream stream);
+
 /* ---- model ---- */
 
 typedef struct aih_model aih_model;
@@ -137,7 +156,10 @@ aih_model *aih_model_load(const void *bytes, size_t len, uint32_t n, int32_t dt)
  * kernel, or where load-time tuning finds the joined launch faster.
  * Elsewhere, a 3x3 depthwise and the 1x1 conv after it that alone reads its
  * output run as one aih_conv_dwpw launch when its plan has a tile for every
- * CU (weights in the activation dtype). The intermediates are then never stored:
+ * CU (weights in the activation dtype). A Resize whose output only the
+ * Concat right after it reads runs inside that concat's launch
+ * (aih_resize_concat) when every concat part but the last has a multiple of
+ * 4 channels (any dtypes). The intermediates are then never stored:
  * reading, writing or querying them fails, and aih_model_infer_range may not
  * split a fused block. The reference runtime dispatches the convs separately
  * (lowering.rs:122-152); this fusion has no counterpart there and keeps each
@@ -190,24 +212,33 @@ int aih_model_tensor(const aih_model *m, const char *name, aih_tensor_info *out)
 typedef struct {
   uint32_t n_tensors, n_ops, n_inputs, n_outputs;
   uint32_t n_launches; /* kernel launches of one aih_model_infer from a staged upload: ops, less n_ops - 1 per fused block */
-  uint32_t n_fused;    /* fused blocks (inverted-residual blocks and depthwise -> pointwise pairs) */
+  uint32_t n_fused;    /* fused blocks (every aih_fused_kind) */
   int32_t dt, wdt;
   size_t device_bytes; /* weights + tensors + workspace */
 } aih_model_info;
 int aih_model_get_info(const aih_model *m, aih_model_info *out);
 
-/* Fused block i (0 <= i < n_fused): its first op and op count (it covers
- * ops first_op .. first_op + n_ops - 1); for an inverted-residual block
- * (n_ops 3) the plan aih_ir_block runs it with, for the stem conv fused into
- * the block after it (n_ops 4, first_op the stem's) the plan of
+/* Fused block i (0 <= i < n_fused): its kind, first op and op count (it
+ * covers ops first_op .. first_op + n_ops - 1); for an inverted-residual
+ * block (n_ops 3) the plan aih_ir_block runs it with, for the stem conv fused
+ * into the block after it (n_ops 4, first_op the stem's) the plan of
  * aih_ir_block_stem, for a block joined to the head after it (n_ops 4,
  * first_op the block's expand) the plan of aih_ir_block_head, for a
- * depthwise -> pointwise pair (n_ops 2) the plan of aih_conv_dwpw. */
+ * depthwise -> pointwise pair (n_ops 2) the plan of aih_conv_dwpw; a resize
+ * folded into a concat (n_ops 2) has no plan (both zeroed). */
+enum aih_fused_kind {
+  AIH_FUSED_IR_BLOCK = 0,     /* aih_ir_block */
+  AIH_FUSED_DWPW = 1,         /* aih_conv_dwpw */
+  AIH_FUSED_STEM_BLOCK = 2,   /* aih_ir_block_stem */
+  AIH_FUSED_BLOCK_HEAD = 3,   /* aih_ir_block_head */
+  AIH_FUSED_RESIZE_CONCAT = 4 /* aih_resize_concat */
+};
 typedef struct {
   uint32_t first_op;
   uint32_t n_ops;
   aih_ir_plan plan;
   aih_dwpw_plan dwpw;
+  int32_t kind; /* enum aih_fused_kind */
 } aih_model_fused_info;
 int aih_model_fused_block(const aih_model *m, uint32_t i, aih_model_fused_info *out);
 /* Name of input / output i (valid while m lives). */

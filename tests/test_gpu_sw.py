@@ -63,25 +63,102 @@ def rnd(seed, *shape):
 
 # ---------------------------------------------------------------- ops
 
+def rdt(x, dt):
+    """x rounded to the storage dtype (round to nearest even), as fp32."""
+    n, h, w, c = x.shape
+    return orc.unpack_nhwc(orc.pack_nhwc(x.ravel(), n, h, w, c, dt), n, h, w, c, dt).reshape(x.shape)
+
+
+RESIZE_CASES = [(10, 18, 20, 36, "half_pixel"), (40, 72, 80, 144, "half_pixel"), (7, 9, 3, 4, "half_pixel"),
+                (5, 6, 10, 12, "asymmetric"), (80, 144, 160, 288, "half_pixel"), (3, 7, 10, 11, "half_pixel"),
+                (9, 5, 4, 13, "asymmetric")]
+
+
 @pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
-@pytest.mark.parametrize("case", [(10, 18, 20, 36, "half_pixel"), (40, 72, 80, 144, "half_pixel"),
-                                  (7, 9, 3, 4, "half_pixel"), (5, 6, 10, 12, "asymmetric"),
-                                  (80, 144, 160, 288, "half_pixel")],
-                         ids=lambda c: "x".join(map(str, c[:4])) + "_" + c[4])
+@pytest.mark.parametrize("case", RESIZE_CASES, ids=lambda c: "x".join(map(str, c[:4])) + "_" + c[4])
 def test_resize_matches_oracle(case, dt):
+    """Bit for bit: the kernel rounds every product and sum as the reference's
+    scalar code does (reference/resize.rs:36-38), so on inputs already in the
+    storage dtype its output is the oracle's fp32 result rounded to that
+    dtype. Up- and downscales at non-power-of-two ratios, both modes."""
     ih, iw, oh, ow, mode = case
     n = 2
     # two parts: 8 channels of a 12-channel tensor starting at channel 4 (a
     # view), then a 6-channel tensor -> 14 output channels
-    a = rnd(11, n, ih, iw, 12)
-    b = rnd(12, n, ih, iw, 6)
+    a = rdt(rnd(11, n, ih, iw, 12), dt)
+    b = rdt(rnd(12, n, ih, iw, 6), dt)
     y = G.poisoned(n * oh * ow * c4(14), dt)
     print(f"resize {case} dt{dt}", flush=True)
     sw.resize([(upload(a, dt), 8, 12, 4), (upload(b, dt), 6, 8, 0)], n, ih, iw, oh, ow, mode, dt, y)
     torch.cuda.synchronize()
     got = download(y, (n, oh, ow, 14), dt)
-    want = so.resize_bilinear(np.concatenate([a[..., 4:12], b], -1), oh, ow, mode)
-    assert G.rel_err(got, want) <= BAR[dt]
+    want = rdt(so.resize_bilinear(np.concatenate([a[..., 4:12], b], -1), oh, ow, mode), dt)
+    assert np.array_equal(got, want), G.rel_err(got, want)
+    raw = G.host(y, dt).reshape(n * oh * ow, c4(14))
+    assert not raw[:, 14:].any()  # padding lanes are zero
+
+
+# (channels, resized) per part; every part but the last a multiple of 4 channels
+RC_CASES = [[(32, True), (12, False)], [(12, False), (8, True), (5, True)], [(4, False), (8, False), (3, False)],
+            [(8, True)], [(16, True), (4, False), (8, True), (6, False)]]
+
+
+@pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("parts", RC_CASES, ids=lambda ps: "_".join(f"{c}{'r' if r else 'p'}" for c, r in ps))
+@pytest.mark.parametrize("geo", [(40, 72, 80, 144, "half_pixel"), (5, 7, 9, 4, "asymmetric")],
+                         ids=lambda g: "x".join(map(str, g[:4])) + "_" + g[4])
+def test_resize_concat_equals_resize_then_concat(geo, parts, dt):
+    """aih_resize_concat (a resize folded into the concat that reads it) is
+    bit for bit aih_resize of the resized parts followed by aih_concat, and
+    the oracle's resize and concatenation rounded to the storage dtype; the
+    resized parts are channel views (4 channels in, a 4-channel wider
+    buffer)."""
+    ih, iw, oh, ow, mode = geo
+    n = 2
+    xs, args, want = [], [], []
+    for i, (c, r) in enumerate(parts):
+        h, w = (ih, iw) if r else (oh, ow)
+        x = rdt(rnd(100 + i, n, h, w, c4(c) + 8), dt)  # the part is channels 4 .. 4 + c of a wider tensor
+        xs.append(x)
+        args.append((upload(x, dt), c, c4(c) + 8, 4, r))
+        want.append(so.resize_bilinear(x[..., 4:4 + c], oh, ow, mode) if r else x[..., 4:4 + c])
+    cout = sum(c for c, _ in parts)
+    y = G.poisoned(n * oh * ow * c4(cout), dt)
+    print(f"resize_concat {geo} {parts} dt{dt}", flush=True)
+    sw.resize_concat(args, n, ih, iw, oh, ow, mode, dt, y)
+    # the two launches: each resized part on its own, then the concat
+    tmp = []
+    for (t, c, st, off, r) in args:
+        if r:
+            z = G.poisoned(n * oh * ow * c4(c), dt)
+            sw.resize([(t, c, st, off)], n, ih, iw, oh, ow, mode, dt, z)
+            tmp.append((z, c, c4(c), 0))
+        else:
+            tmp.append((t, c, st, off))
+    y2 = G.poisoned(n * oh * ow * c4(cout), dt)
+    sw.concat(tmp, n, oh, ow, dt, y2)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(-1), y2.view(-1))
+    got = download(y, (n, oh, ow, cout), dt)
+    assert np.array_equal(got, rdt(np.concatenate(want, -1), dt))
+
+
+def test_resize_concat_rejects_bad_parts():
+    dt = F16
+    x = upload(rnd(5, 1, 4, 4, 8), dt)
+    y = G.poisoned(8 * 8 * 16, dt)
+    bad = [
+        ([(x, 8, 8, 0, True)], 2, "resized bits past the parts"),  # mask bit 1 without a part 1
+        ([(x, 6, 8, 0, True), (x, 8, 8, 0, False)], None, "multiple of 4"),
+        ([(x, 8, 8, 0, True)] * 9, None, "1 to 8 parts"),
+    ]
+    for parts, mask, why in bad:
+        d = sw._ResizeConcat(1, 4, 4, 8, 8, 0, dt, len(parts), mask if mask is not None else
+                             sum(1 << i for i, p in enumerate(parts) if p[4]),
+                             sw._srcs([(c, s, o) for _, c, s, o, _ in parts[:8]]))
+        rc = sw.lib().aih_resize_concat(sw.C.byref(d), sw._ptrs([p[0] for p in parts]), conv._ptr(y),
+                                        conv._stream(None))
+        assert rc != 0 and why in conv.last_error(), (why, conv.last_error())
 
 
 @pytest.mark.parametrize("dt", [F32, F16, BF16], ids=["f32", "f16", "bf16"])
@@ -188,18 +265,24 @@ def _op_inputs(op):
 
 SEGM_FUSED = [12, 15, 18, 21]  # first ops of the real model's inverted-residual blocks
 SEGM_PAIRS = {33, 40}  # depthwise -> pointwise pairs a load may fuse (when the batch gives every CU a tile)
+SEGM_RESIZE_CONCAT = [38]  # the 40x72 -> 80x144 resize folded into the concat after it
 
 
 def _check_fused(m, fuse):
-    """The model's fused launches: exactly the four inverted-residual blocks,
-    plus (fp32) depthwise -> pointwise pairs among SEGM_PAIRS only."""
+    """The model's fused launches: exactly the four inverted-residual blocks
+    and the resize folded into the concat, plus depthwise -> pointwise pairs
+    among SEGM_PAIRS only."""
     blocks = m.fused_blocks()
     if not fuse:
         assert blocks == []
         return []
-    assert [f.first_op for f in blocks if f.n_ops == 3] == SEGM_FUSED
-    pairs = [f.first_op for f in blocks if f.n_ops == 2]
+    assert [f.first_op for f in blocks if f.kind == sw.FUSED_IR_BLOCK] == SEGM_FUSED
+    assert [(f.first_op, f.n_ops) for f in blocks if f.kind == sw.FUSED_RESIZE_CONCAT] == [(k, 2) for k in
+                                                                                            SEGM_RESIZE_CONCAT]
+    pairs = [f.first_op for f in blocks if f.kind == sw.FUSED_DWPW]
+    assert all(f.n_ops == 2 for f in blocks if f.kind == sw.FUSED_DWPW)
     assert set(pairs) <= SEGM_PAIRS, pairs
+    assert len(blocks) == len(SEGM_FUSED) + len(SEGM_RESIZE_CONCAT) + len(pairs), [(f.first_op, f.kind) for f in blocks]
     return pairs
 
 
@@ -323,7 +406,8 @@ def _tile_batch(ref, reps):
 def test_real_model_batch64_every_launch(segm, dt):
     """The real model at batch 64 through aih_model_load, as the bench times
     it: fused as loaded by default -- also the depthwise -> pointwise pairs
-    that batch 64 fuses (ops 33-34 and 40-41; 34 launches) -- and every launch fed
+    that batch 64 fuses (ops 33-34 and 40-41) and the resize folded into the
+    concat (ops 38-39); 33 launches -- and every launch fed
     the oracle's values of its inputs against the oracle's output (fp32: 1e-4
     against the fp32 graph; f16: 2e-2 against the graph run with the same
     storage rounding). The batch is two oracle images repeated 32 times
@@ -334,9 +418,9 @@ def test_real_model_batch64_every_launch(segm, dt):
     x = np.concatenate([x2] * (n // base))
     m = sw.SwModel(data, n=n, dt=None if dt == F32 else conv.DType(dt))
     pairs = _check_fused(m, True)
-    assert sorted(pairs) == sorted(SEGM_PAIRS) and m.info.n_launches == 34, (pairs, m.info.n_launches)
+    assert sorted(pairs) == sorted(SEGM_PAIRS) and m.info.n_launches == 33, (pairs, m.info.n_launches)
     for f in m.fused_blocks():
-        if f.n_ops == 2:
+        if f.kind == sw.FUSED_DWPW:
             print(f"segm b64 dt{dt} pair ops {f.first_op}-{f.first_op + 1}: {f.dwpw}", flush=True)
     ref = graph if dt == F32 else so.SwGraph(data, round_dt=dt)
     want = _tile_batch(ref.run({"input_1": x2}, n=base, keep_all=True), n // base)
@@ -359,10 +443,10 @@ def test_tensor_storage_and_info(segm):
     assert t.bytes == 3 * 160 * 288 * 4 * 4 and t.data
     seg = m.tensor("segment")  # an alias of the last resize's output
     assert (seg.h, seg.w, seg.c, seg.stride_c) == (160, 288, 2, 4)
-    # four fused blocks (and at this batch fp32 depthwise -> pointwise pairs): 44 ops in 36 launches less one
-    # per pair
+    # four fused blocks, the resize folded into the concat (and at this batch fp32 depthwise -> pointwise
+    # pairs): 44 ops in 35 launches less one per pair
     npairs = len(_check_fused(m, True))
-    assert m.info.n_ops == 44 and m.info.n_fused == 4 + npairs and m.info.n_launches == 36 - npairs
+    assert m.info.n_ops == 44 and m.info.n_fused == 5 + npairs and m.info.n_launches == 35 - npairs
     assert m.info.device_bytes > 0
     # a fused block's intermediates are never stored; ranges keep blocks whole
     inner = graph.T[graph.g["ops"][12]["out"]]["name"]
