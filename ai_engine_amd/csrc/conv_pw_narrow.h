@@ -39,7 +39,7 @@ struct PwNarrowArgs {
 constexpr uint32_t kPwNarrowMaxKG = 2048;
 
 // Lanes per pixel for kg input channel groups: 16, 4 or 1.
-inline uint32_t pw_narrow_group(uint32_t kg) { return kg >= 16 ? 16u : kg >= 4 ? 4u : 1u; }
+inline uint32_t pw_narrow_group(uint32_t kg) { return kg >= 16 ? 16u : 1u; }
 
 hipError_t launch_pw_narrow(const PwNarrowArgs &a, int dta, int dtw, hipStream_t st);
 

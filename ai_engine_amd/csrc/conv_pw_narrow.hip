@@ -23,9 +23,14 @@ namespace aih {
 namespace {
 
 // Lanes per pixel G: 16 for at least 16 kg (a 128-channel head takes two
-// steps of 64 channels), 4 for 4-15 kg (24 channels: two steps, the second
-// half full), 1 below.
-template <int DTA, int DTW, int G>
+// steps of 64 channels), else 1: a lane owns a pixel and issues all of its
+// loads before the first product -- KGT (4, 8 or 16, at least kg) of them,
+// the ones past kg reading the last group again (cache hits, never summed),
+// so the loads need no predicate: a 24-channel head reads 48 contiguous bytes
+// a lane, 3 KB a wavefront in flight -- then sums them in channel order
+// against the weights, which the workgroup first copies to LDS in fp32 (a
+// wavefront-uniform address: broadcast reads).
+template <int DTA, int DTW, int G, int KGT>
 __global__ __launch_bounds__(256) void pw_narrow_kernel(PwNarrowArgs a) {
   // packed weights with one column group (NG = 1): vector (kg, j) -- input
   // channels 4kg..4kg+3 of output channel j -- at kg * 4 + j (pack.rs:95)
@@ -33,20 +38,42 @@ __global__ __launch_bounds__(256) void pw_narrow_kernel(PwNarrowArgs a) {
   const Act ap = act_params(a.act);
   const uint32_t g = threadIdx.x % G;
   const uint32_t per_block = 256 / G;
+  __shared__ f32x4 wl[G == 1 ? KGT * 4 : 1];
+  if constexpr (G == 1) {
+    for (uint32_t i = threadIdx.x; i < a.KG * 4; i += 256) wl[i] = narrow_w4<DTA, DTW>(a.w, i);
+    __syncthreads();
+  }
   for (uint32_t m0 = blockIdx.x * per_block; m0 < a.M; m0 += gridDim.x * per_block) {
     const uint32_t m = m0 + threadIdx.x / G;
     const bool pv = m < a.M;
     f32x4 acc = {};
     const size_t xrow = (size_t)(pv ? m : 0) * a.KGX;
+    if constexpr (G == 1) {
+      f32x4 xs[KGT];
+#pragma unroll
+      for (uint32_t kg = 0; kg < (uint32_t)KGT; ++kg) xs[kg] = Vec4IO<DTA>::load(a.x, xrow + min(kg, a.KG - 1));
+      // every load issued before the first product (the compiler would sink
+      // each load to its use behind the uniform exit below)
+#pragma unroll
+      for (int kg = 0; kg < KGT; ++kg) asm volatile("" : "+v"(xs[kg]));
+#pragma unroll
+      for (uint32_t kg = 0; kg < (uint32_t)KGT; ++kg) {
+        if (kg >= a.KG) break;
+        const f32x4 xv = pv ? xs[kg] : f32x4{};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] += narrow_dot4(xv, wl[kg * 4 + j]);
+      }
+    } else {
 #pragma unroll 2
-    for (uint32_t kg = g; kg < a.KG; kg += G) {
-      const f32x4 xl = Vec4IO<DTA>::load(a.x, xrow + kg);
-      const f32x4 xv = pv ? xl : f32x4{};
-      f32x4 wv[4];
+      for (uint32_t kg = g; kg < a.KG; kg += G) {
+        const f32x4 xl = Vec4IO<DTA>::load(a.x, xrow + kg);
+        const f32x4 xv = pv ? xl : f32x4{};
+        f32x4 wv[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) wv[j] = narrow_w4<DTA, DTW>(a.w, (size_t)kg * 4 + j);
+        for (int j = 0; j < 4; ++j) wv[j] = narrow_w4<DTA, DTW>(a.w, (size_t)kg * 4 + j);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] += narrow_dot4(xv, wv[j]);
+        for (int j = 0; j < 4; ++j) acc[j] += narrow_dot4(xv, wv[j]);
+      }
     }
     // the group's partial sums, added by butterfly (every lane ends with the total)
 #pragma unroll
@@ -63,20 +90,21 @@ __global__ __launch_bounds__(256) void pw_narrow_kernel(PwNarrowArgs a) {
   }
 }
 
-template <int DTA, int DTW, int G>
+template <int DTA, int DTW, int G, int KGT>
 hipError_t launch_g(const PwNarrowArgs &a, hipStream_t st) {
   const uint32_t per_block = 256 / G;
   const uint32_t blocks = (uint32_t)std::min<uint64_t>((a.M + per_block - 1) / per_block, 65535);
-  hipLaunchKernelGGL((pw_narrow_kernel<DTA, DTW, G>), dim3(blocks), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((pw_narrow_kernel<DTA, DTW, G, KGT>), dim3(blocks), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
 template <int DTA, int DTW>
 hipError_t launch_inst(const PwNarrowArgs &a, hipStream_t st) {
   const uint32_t g = pw_narrow_group(a.KG);
-  if (g == 16) return launch_g<DTA, DTW, 16>(a, st);
-  if (g == 4) return launch_g<DTA, DTW, 4>(a, st);
-  return launch_g<DTA, DTW, 1>(a, st);
+  if (g == 16) return launch_g<DTA, DTW, 16, 0>(a, st);
+  if (a.KG <= 4) return launch_g<DTA, DTW, 1, 4>(a, st);
+  if (a.KG <= 8) return launch_g<DTA, DTW, 1, 8>(a, st);
+  return launch_g<DTA, DTW, 1, 16>(a, st);
 }
 
 }  // namespace
