@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <string>
 
 #include "../../include/aih_model.h"
@@ -71,14 +72,6 @@ __device__ __forceinline__ f32x4 lerp4(f32x4 a, f32x4 b, float t, float u) {
   return a * u + b * t;
 }
 
-// One workgroup per output row (image, oy): the row's source rows and y
-// weight are computed once, and the threads stride over the row's ow * cg
-// output vec4s (stores of consecutive threads are consecutive). Part p with
-// bit p of parts.resized set is read at ih x iw and blended from its four
-// taps; any other part is read at the output's own pixel (a plain concat
-// part). Lanes past a part's channels are stored as 0. The loop over parts
-// is uniform, so each part's fields sit in scalar registers; a lane takes
-// the one part its vec4 lies in.
 // Vec4 `idx` of a part: a 32-bit byte offset from the part's base when the
 // host found every part below 4 GiB (O32; the loads then take the base in
 // scalar registers and one 32-bit offset), else 64-bit indexing.
@@ -90,26 +83,47 @@ __device__ __forceinline__ f32x4 part_load(const void *base, size_t idx) {
     return Vec4IO<DT>::load(base, idx);
 }
 
+// One workgroup per group of one or two consecutive output rows of an image
+// (`off` = 1: row 0 alone, then rows 2k - 1, 2k -- the pairs a 2x half-pixel
+// upsample maps to one source row pair; `off` = 0: rows 2k, 2k + 1). The
+// group's source rows and y weights are computed once, and the threads stride
+// over the row's ow * cg output vec4s (stores of consecutive threads are
+// consecutive). Part p with bit p of parts.resized set is read at ih x iw and
+// blended from its four taps -- when both rows of the group have the same
+// two source rows, their x blends (top, bot) are computed once and only the y
+// blend differs: the same operations on the same values as two separate rows
+// -- any other part is read at the output's own pixel (a plain concat part).
+// Lanes past a part's channels are stored as 0. The loop over parts is
+// uniform, so each part's fields sit in scalar registers; a lane takes the one
+// part its vec4 lies in.
 template <int DT, bool O32>
-__device__ __forceinline__ f32x4 resize_part(const PartArg &pa, bool resized, uint32_t k0, uint32_t ox,
-                                             size_t prow, size_t r0, size_t r1, const Coord &cy, float sx,
-                                             int mode, uint32_t iw) {
+__device__ __forceinline__ void resize_vec(const PartArg &pa, bool resized, uint32_t k0, uint32_t ox, size_t pa_row,
+                                           size_t pb_row, bool two, bool shared, size_t a0, size_t a1, size_t b0,
+                                           size_t b1, const Coord &ca, const Coord &cb, float sx, int mode,
+                                           uint32_t iw, f32x4 &va, f32x4 &vb) {
   const uint32_t cgi = pa.stride_c / 4, q = (pa.c_off + k0) / 4;
-  f32x4 v;
   if (resized) {
     const Coord cx = resize_coord(ox, sx, mode, iw);
-    const f32x4 a = part_load<DT, O32>(pa.p, (r0 + cx.i0) * cgi + q);
-    const f32x4 b = part_load<DT, O32>(pa.p, (r0 + cx.i1) * cgi + q);
-    const f32x4 c = part_load<DT, O32>(pa.p, (r1 + cx.i0) * cgi + q);
-    const f32x4 d = part_load<DT, O32>(pa.p, (r1 + cx.i1) * cgi + q);
-    v = lerp4(lerp4(a, b, cx.t, cx.u), lerp4(c, d, cx.t, cx.u), cy.t, cy.u);
+    auto blend_x = [&](size_t r) {
+      const f32x4 l = part_load<DT, O32>(pa.p, (r + cx.i0) * cgi + q);
+      const f32x4 h = part_load<DT, O32>(pa.p, (r + cx.i1) * cgi + q);
+      return lerp4(l, h, cx.t, cx.u);
+    };
+    const f32x4 top = blend_x(a0), bot = blend_x(a1);
+    va = lerp4(top, bot, ca.t, ca.u);
+    if (shared) {
+      vb = lerp4(top, bot, cb.t, cb.u);
+    } else if (two) {
+      const f32x4 top_b = blend_x(b0), bot_b = blend_x(b1);
+      vb = lerp4(top_b, bot_b, cb.t, cb.u);
+    }
   } else {
-    v = part_load<DT, O32>(pa.p, (prow + ox) * cgi + q);
+    va = part_load<DT, O32>(pa.p, (pa_row + ox) * cgi + q);
+    if (two) vb = part_load<DT, O32>(pa.p, (pb_row + ox) * cgi + q);
   }
 #pragma unroll
   for (int l = 0; l < 4; ++l)
-    if (k0 + l >= pa.c) v[l] = 0.0f;
-  return v;
+    if (k0 + l >= pa.c) va[l] = vb[l] = 0.0f;
 }
 
 // Rows of up to 1024 vec4s take one thread per vec4 (the block rounded up
@@ -117,25 +131,32 @@ __device__ __forceinline__ f32x4 resize_part(const PartArg &pa, bool resized, ui
 template <int DT, bool O32>
 __global__ __launch_bounds__(1024) void resize_kernel(Parts parts, uint32_t ih, uint32_t iw, uint32_t oh,
                                                       uint32_t ow, float sy, float sx, int mode, uint32_t cg_out,
-                                                      FastDiv fd_cg, FastDiv fd_oh, void *y) {
-  const uint32_t row = blockIdx.x;
-  const uint32_t img = fdiv(row, fd_oh);
-  const Coord cy = resize_coord(row - img * oh, sy, mode, ih);
-  const size_t r0 = ((size_t)img * ih + cy.i0) * iw, r1 = ((size_t)img * ih + cy.i1) * iw;
-  const size_t prow = (size_t)row * ow;
+                                                      FastDiv fd_cg, uint32_t groups, FastDiv fd_groups,
+                                                      uint32_t off, void *y) {
+  const uint32_t img = fdiv(blockIdx.x, fd_groups);
+  const uint32_t k = blockIdx.x - img * groups;
+  const uint32_t ra = off ? (k == 0 ? 0u : 2 * k - 1) : 2 * k;
+  const bool two = !(off && k == 0) && ra + 1 < oh;
+  const Coord ca = resize_coord(ra, sy, mode, ih);
+  const Coord cb = resize_coord(two ? ra + 1 : ra, sy, mode, ih);
+  const bool shared = two && ca.i0 == cb.i0 && ca.i1 == cb.i1;
+  const size_t ib = (size_t)img * ih;
+  const size_t a0 = (ib + ca.i0) * iw, a1 = (ib + ca.i1) * iw, b0 = (ib + cb.i0) * iw, b1 = (ib + cb.i1) * iw;
+  const size_t row_a = (size_t)img * oh + ra;  // output (and plain part) rows
   const uint32_t nrow = ow * cg_out;
   for (uint32_t j = threadIdx.x; j < nrow; j += blockDim.x) {
     const uint32_t ox = fdiv(j, fd_cg);
     const uint32_t g4 = (j - ox * cg_out) * 4;
-    f32x4 v = {};
+    f32x4 va = {}, vb = {};
     for (uint32_t p = 0; p < parts.n; ++p) {
       const PartArg &pa = parts.v[p];
       const uint32_t end = p + 1 < parts.n ? parts.v[p + 1].out_c0 : 0xffffffffu;
       if (g4 >= pa.out_c0 && g4 < end)
-        v = resize_part<DT, O32>(pa, (parts.resized >> p) & 1u, g4 - pa.out_c0, ox, prow, r0, r1, cy, sx, mode,
-                                 iw);
+        resize_vec<DT, O32>(pa, (parts.resized >> p) & 1u, g4 - pa.out_c0, ox, row_a * ow, (row_a + 1) * ow, two,
+                            shared, a0, a1, b0, b1, ca, cb, sx, mode, iw, va, vb);
     }
-    Vec4IO<DT>::store(y, (size_t)row * nrow + j, v);
+    Vec4IO<DT>::store(y, row_a * nrow + j, va);
+    if (two) Vec4IO<DT>::store(y, (row_a + 1) * nrow + j, vb);
   }
 }
 
@@ -324,12 +345,24 @@ int launch_resize(const char *what, uint32_t n, uint32_t ih, uint32_t iw, uint32
     o32 = o32 && px * srcs[i].stride_c / 4 * vec_bytes(dt) < (1ull << 32);
   }
   const float sy = (float)ih / (float)oh, sx = (float)iw / (float)ow;
+  // row groups: pairs from row 1 where that pairs rows of the same source
+  // rows more often than pairs from row 0 (a 2x upsample); only the speed
+  // depends on it, the kernel checks each pair
+  auto src_row = [&](uint32_t o) {
+    const float f = mode == AIH_COORD_HALF_PIXEL ? ((float)o + 0.5f) * sy - 0.5f : (float)o * sy;
+    return (int64_t)std::floor(f);
+  };
+  uint32_t share[2] = {0, 0};
+  for (uint32_t o = 0; o + 1 < oh && o < 64; ++o)
+    if (src_row(o) == src_row(o + 1)) ++share[o & 1];
+  const uint32_t off = share[1] > share[0] ? 1u : 0u;
+  const uint32_t groups = off ? 1 + oh / 2 : (oh + 1) / 2;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)rows), block(threads);
-  const FastDiv fcg = make_fastdiv(cg), foh = make_fastdiv(oh);
+  const dim3 grid((unsigned)(n * groups)), block(threads);
+  const FastDiv fcg = make_fastdiv(cg), fgr = make_fastdiv(groups);
 #define AIH_RESIZE_LAUNCH(D, O)                                                                                  \
   hipLaunchKernelGGL((resize_kernel<D, O>), grid, block, 0, st, parts, ih, iw, oh, ow, sy, sx, (int)mode, cg, fcg, \
-                     foh, y)
+                     groups, fgr, off, y)
   switch (dt) {
     case AIH_F32: if (o32) AIH_RESIZE_LAUNCH(DT_F32, true); else AIH_RESIZE_LAUNCH(DT_F32, false); break;
     case AIH_F16: if (o32) AIH_RESIZE_LAUNCH(DT_F16, true); else AIH_RESIZE_LAUNCH(DT_F16, false); break;
