@@ -563,8 +563,8 @@ def real_model(torch, conv, dev, stream) -> dict:
     segm_r11_160x288.sw: 36 convs + resize / gpool / binary / concat) through
     the native .sw runtime, batch 64, fp32 as converted and with 16-bit
     storage converted at load, as loaded by default (its four inverted-
-    residual blocks fused) and op by op; one step = device upload + the whole
-    graph."""
+    residual blocks fused), f16 also with load-time tuning (AIH_MODEL_TUNE),
+    and op by op; one step = device upload + the whole graph."""
     from ai_engine_amd import sw
 
     data = open(os.path.join(ROOT, "tests", "golden", "segm_r11_160x288.sw"), "rb").read()
@@ -578,20 +578,22 @@ def real_model(torch, conv, dev, stream) -> dict:
     n = 64
     x = (torch.rand(n, 160, 288, 3, device=dev) * 2 - 1).contiguous()
     out = {}
-    for dt, fuse in (("f32", True), ("f16", True), ("f32", False), ("f16", False)):
-        m = sw.SwModel(data, n=n, dt=None if dt == "f32" else conv.DType.F16, fuse=fuse)
+    for dt, fuse, tune in (("f32", True, False), ("f16", True, False), ("f16", True, True), ("f32", False, False),
+                           ("f16", False, False)):
+        m = sw.SwModel(data, n=n, dt=None if dt == "f32" else conv.DType.F16, fuse=fuse, tune=tune)
 
         def step(_):
             m.upload_input("input_1", x, stream)
             m.infer(stream)
 
         t = time_launches(torch, stream, step, 10)
-        key = f"segm_r11_real_160x288_b{n}_{dt}" + ("" if fuse else "_unfused")
+        key = f"segm_r11_real_160x288_b{n}_{dt}" + ("" if fuse else "_unfused") + ("_tuned" if tune else "")
         out[key] = dict(us=round(t * 1e6, 1), frames_per_s=round(n / t, 1), tflops=round(2 * macs * n / t / 1e12, 2),
                         gflop_per_frame=round(2 * macs / 1e9, 3), ops=len(g["ops"]), launches=m.info.n_launches,
                         fused_blocks=[f"ops {f.first_op}-{f.first_op + f.n_ops - 1}: " + fused_label(sw, f)
                                       for f in m.fused_blocks()])
-        log(f"real segm model {dt} b{n} {'fused' if fuse else 'unfused'}: {t * 1e3:.3f} ms {n / t:.0f} frames/s "
+        log(f"real segm model {dt} b{n} {'fused' if fuse else 'unfused'}{' tuned at load' if tune else ''}: "
+            f"{t * 1e3:.3f} ms {n / t:.0f} frames/s "
             f"({m.info.n_launches} launches)")
         m.close()
     return out
