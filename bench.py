@@ -293,6 +293,7 @@ PROFILE_CONFIGS = {
     "igemm3x3s1_32to64_relu_80x144_b32": ("ig", 32, 80, 144, 32, 64, 1, "RELU"),
     "ir_block_chain_4x_64c_40x72_b64": ("chain",),
     "encoder_160x288_b64": ("encoder",),
+    "segm_r11_real_160x288_b64": ("segm",),  # the real model through the native runtime, --dtype storage
     "copy_1gib": ("copy",),  # calibration: reads and writes 1 GiB
 }
 
@@ -332,6 +333,15 @@ def profile_config(args, torch, conv, W, Model, dev, DT) -> int:
         m4.tensors["input"].uniform_(-1, 1)
         for _ in range(reps):
             m4.infer()
+    elif cfg[0] == "segm":
+        from ai_engine_amd import sw
+
+        data = open(os.path.join(ROOT, "tests", "golden", "segm_r11_160x288.sw"), "rb").read()
+        m = sw.SwModel(data, n=64, dt=DT[args.dtype])
+        x = (torch.rand(64, 160, 288, 3, device=dev) * 2 - 1).contiguous()
+        m.upload_input("input_1", x)
+        for _ in range(reps):
+            m.infer()
     elif cfg[0] == "copy":
         src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
