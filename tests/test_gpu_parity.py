@@ -277,6 +277,11 @@ def test_dw_16bit(dt):
     check("dw16 a", res, dt)
     res = G.run_dw(36, 64, 96, 5, 2, "none", False, dt, 5102)
     check("dw16 b", res, dt)
+    # the real segmentation model's small 5x5 layers (one-pixel strips of 4-channel vectors), a batch of 4
+    res = G.run_dw(20, 36, 32, 5, 1, "none", True, dt, 5103, n=4)
+    check("dw16 c", res, dt)
+    res = G.run_dw(20, 36, 96, 5, 2, "relu", False, dt, 5104, n=4)
+    check("dw16 d", res, dt)
 
 
 def test_dw_batch():
