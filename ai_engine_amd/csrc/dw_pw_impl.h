@@ -187,6 +187,11 @@ __global__ __launch_bounds__(512) void dw_pw_kernel(DwPwArgs a) {
 #pragma unroll
         for (int o = 0; o < NO; ++o)
           aw[o] = *reinterpret_cast<const f32x4 *>(W + (NWD + U + u * COP + 16 * o + p16) * 16);
+        // the projection MFMAs at raised priority: a wavefront that has
+        // finished its depthwise issues them ahead of the SIMD's others still
+        // in theirs (C4 chain, fp32: 800 -> 770 us on one box; the 16-bit
+        // branch below measured no gain from it)
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -194,6 +199,7 @@ __global__ __launch_bounds__(512) void dw_pw_kernel(DwPwArgs a) {
 #pragma unroll
             for (int o = 0; o < NO; ++o)
               acc[b][o] = __builtin_amdgcn_mfma_f32_16x16x4f32(aw[o][j], d[b][j], acc[b][o], 0, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
       } else {
         // 16-bit storage: the depthwise in fp32 from the widened taps (sum
         // from the bias, taps in (ky, kx) order), act, rounded to DT where
