@@ -1,10 +1,13 @@
 // sw_ops.hip -- the non-conv ops of a segmentation graph (include/aih_model.h):
-// bilinear resize with concat parts, global average pool, binary elementwise
-// with the six SwOperand kinds, channel concat. All are HBM-bound streaming
-// kernels over NHWC-C4 (one thread per output vec4, fp32 arithmetic on the
-// storage dtype); the grids cover the output exactly and every index is
-// checked against it. Output vec4 counts are kept below 2^32 (checked on the
-// host) so the index decomposition is 32-bit with precomputed divisors.
+// bilinear resize with concat parts (and a resize folded into the concat that
+// reads it), global average pool, binary elementwise with the six SwOperand
+// kinds, channel concat. All are streaming kernels over NHWC-C4 with fp32
+// arithmetic on the storage dtype: one thread per output vec4 (gpool: a
+// workgroup per image and channel group; resize: a workgroup per pair of
+// output rows, its threads over the rows' vec4s); the grids cover the output
+// exactly and every index is checked against it. Output vec4 counts are kept
+// below 2^32 (checked on the host) so the index decomposition is 32-bit with
+// precomputed divisors.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
