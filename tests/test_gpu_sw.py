@@ -457,6 +457,13 @@ def test_tensor_storage_and_info(segm):
     for a, b in [(13, 15), (12, 13), (0, 14)]:
         with pytest.raises(conv.AihError, match="inside the fused block"):
             m.infer_range(a, b)
+    # the resize folded into the concat after it: its output is never stored either
+    rs = graph.T[graph.g["ops"][38]["out"]]["name"]
+    with pytest.raises(conv.AihError, match="stays inside the fused block of ops 38..39"):
+        m.read_output(rs)
+    with pytest.raises(conv.AihError, match="inside the fused block"):
+        m.infer_range(38, 39)
+    m.infer_range(38, 40)  # the whole fold runs
     unfused = sw.SwModel(data, n=3, fuse=False)
     assert unfused.info.n_fused == 0 and unfused.info.n_launches == 44
     assert unfused.tensor(inner).c == 96
