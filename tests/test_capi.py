@@ -204,6 +204,32 @@ def _expect_error(fn, fragment):
     assert fragment in str(e.value)
 
 
+def test_resize_rejects_bad_descriptors_before_the_device():
+    """aih_resize / aih_resize_concat check the descriptor on the host; every
+    call here passes no buffers at all, so none can reach a launch."""
+    from ai_engine_amd import sw
+
+    L = sw.lib()
+    assert L.aih_resize_concat(None, None, None, None) == -1 and "null descriptor" in conv.last_error()
+    assert L.aih_resize(None, None, None, None) == -1 and "null descriptor" in conv.last_error()
+
+    def rc(**kw):
+        f = dict(n=1, ih=4, iw=4, oh=8, ow=8, mode=0, dt=1, nparts=1, resized=1)
+        f.update(kw)
+        d = sw._ResizeConcat(f["n"], f["ih"], f["iw"], f["oh"], f["ow"], f["mode"], f["dt"], f["nparts"],
+                             f["resized"], sw._srcs([(8, 8, 0)]))
+        assert L.aih_resize_concat(C.byref(d), None, None, None) == -1
+        return conv.last_error()
+
+    assert "unknown dtype" in rc(dt=7)
+    assert "zero-sized dimension" in rc(n=0)
+    assert "below 2^24" in rc(ow=1 << 24)
+    assert "unknown mode" in rc(mode=3)
+    assert "null or misaligned output" in rc()
+    d = sw._Resize(1, 4, 4, 8, 8, 0, 1, 1, sw._srcs([(8, 8, 0)]))
+    assert L.aih_resize(C.byref(d), None, None, None) == -1 and "resize: null or misaligned output" in conv.last_error()
+
+
 def test_invalid_descriptors_fail_cleanly():
     L = conv.lib()
     assert L.aih_conv_pw(None, None, None, None, None, None, None, 0, None) == -1
